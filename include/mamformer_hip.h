@@ -1,0 +1,159 @@
+/*
+ * mamformer_hip.h -- C ABI of libmamformer_hip.so, the MI355X (gfx950) scan path.
+ *
+ * The reference (Find-Vulnerabilities/Mamformer) has no FFI: its boundary is the
+ * Python function API of the scan path.  Each entry point below replaces one of
+ * those functions; the Python module mamformer_amd.ops binds them through
+ * ctypes and keeps the reference names, argument order and layouts.
+ * Paths are relative to "mamformer 671b/" in the reference tree.
+ *
+ * Conventions
+ *  - All tensor pointers are device pointers owned by the caller; the library
+ *    never allocates device memory and never synchronises the stream.
+ *  - Strides are in elements.  The innermost dimension of every tensor is
+ *    contiguous; 16-byte vector access requires 16-byte aligned base pointers
+ *    and row strides that are multiples of 16 bytes (checked).
+ *  - `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *  - Every call returns MH_OK (0) or a negative MH_ERR_* code; the detail of
+ *    the last failure on the calling thread is returned by mh_last_error().
+ *    Argument checks happen before any HIP call, so a rejected call has no
+ *    side effect.
+ */
+#ifndef MAMFORMER_HIP_H
+#define MAMFORMER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MH_ABI_VERSION 1
+
+/* element types of x / B / C / y / q / k / v / o */
+enum { MH_F32 = 0, MH_BF16 = 1 };
+
+/* status codes */
+enum {
+  MH_OK = 0,
+  MH_ERR_NULL = -1,        /* required pointer is NULL */
+  MH_ERR_SHAPE = -2,       /* non-positive or inconsistent sizes */
+  MH_ERR_DTYPE = -3,       /* unknown element type */
+  MH_ERR_STRIDE = -4,      /* innermost dimension not contiguous / bad stride */
+  MH_ERR_ALIGN = -5,       /* pointer or row stride not 16-byte aligned */
+  MH_ERR_UNSUPPORTED = -6, /* size outside what the kernels implement */
+  MH_ERR_WORKSPACE = -7,   /* workspace missing or too small */
+  MH_ERR_HIP = -8          /* HIP launch error (message in mh_last_error) */
+};
+
+/* flags shared by the SSD entry points */
+enum {
+  MH_DT_SOFTPLUS = 1,      /* dt <- softplus(dt + dt_bias)   (mamba2.py:293, 304) */
+  MH_DT_LIMIT = 2,         /* dt <- clamp(dt, dt_min, dt_max) after softplus */
+  MH_D_PER_CHANNEL = 4     /* D has nheads*headdim entries instead of nheads */
+};
+
+/* ------------------------------------------------------------------------
+ * SSD chunked-scan prefill.
+ * Replaces selective_scan / _selective_scan_impl
+ *   (mamformer/layers/mamba2.py:31-67, 70-130) and triton_ssd_scan
+ *   (mamformer/kernels/triton_ssd.py:508-564), in the per-head SSD convention:
+ *   x (b, L, H, P), dt (b, L, H) fp32, A (H,) fp32 (A <= 0), B/C (b, L, G, N),
+ *   D (H,) or (H*P,) fp32 or NULL, initial_state / final_state (b, H, P, N) fp32.
+ *   y (b, L, H, P) in the dtype of x.  Supported: P = 64, N in {64, 128},
+ *   H % G == 0.  chunk_len = state-passing chunk (multiple of 64; 0 = auto).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int64_t batch, seqlen, nheads, headdim, dstate, ngroups;
+  int64_t chunk_len;
+  int32_t dtype;
+  int32_t flags;
+  float dt_min, dt_max;
+  const void* x;   int64_t x_stride_b, x_stride_l, x_stride_h;
+  const float* dt; int64_t dt_stride_b, dt_stride_l;
+  const float* A;
+  const void* B;   int64_t B_stride_b, B_stride_l;
+  const void* C;   int64_t C_stride_b, C_stride_l;
+  const float* D;
+  const float* dt_bias;
+  const float* initial_state;
+  void* y;         int64_t y_stride_b, y_stride_l, y_stride_h;
+  float* final_state;
+  void* workspace; size_t workspace_bytes;
+} mh_ssd_args;
+
+/* Bytes of workspace mh_ssd_chunk_scan_fwd needs for these sizes. */
+int mh_ssd_workspace_bytes(const mh_ssd_args* a, size_t* bytes);
+/* Resolved chunk_len (auto choice when a->chunk_len == 0). */
+int mh_ssd_chunk_len(const mh_ssd_args* a, int64_t* chunk_len);
+int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Single-token selective state update (decode step).
+ * Replaces Mamba2Block._recurrent_step (mamformer/layers/mamba2.py:407-458):
+ *   state (b, H, P, N) fp32 read from state_in and written to state_out (the
+ *   two may alias: in-place update), x (b, H, P), dt (b, H) fp32 raw (bias,
+ *   softplus and clamp applied per flags), A (H,), B/C (b, G, N), D, y (b, H, P).
+ *   Supported: N in {16, 32, 64, 128, 256}, H % G == 0.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int64_t batch, nheads, headdim, dstate, ngroups;
+  int32_t dtype;
+  int32_t flags;
+  float dt_min, dt_max;
+  const float* state_in;
+  float* state_out;
+  const void* x;   int64_t x_stride_b;
+  const float* dt; int64_t dt_stride_b;
+  const float* A;
+  const void* B;   int64_t B_stride_b;
+  const void* C;   int64_t C_stride_b;
+  const float* D;
+  const float* dt_bias;
+  void* y;         int64_t y_stride_b;
+} mh_ssu_args;
+
+int mh_ssd_state_update(const mh_ssu_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * KDA linear-attention chunked scan, layout (B, H, S, D) contiguous.
+ * mode MH_KDA_GATED: S_t = diag(exp(g_t)) S_{t-1} + k_t^T v_t,
+ *                    o_t = q1_t S_t - lam q2_t S_t   (benchmark operator; no
+ *                    reference function).  g (B,H,S,dk) fp32 or NULL (= 0).
+ * mode MH_KDA_REFERENCE: the reference's phi(x) = elu(x)+1 normalised scan,
+ *   replacing triton_linear_attn_scan (mamformer/kernels/triton_ssd.py:260-350)
+ *   and LinearDiffAttention._linear_attention_scan
+ *   (mamformer/layers/kda_diff.py:357-478): writes o1 and o2 separately.
+ * initial_state / final_state (B,H,dk,dv) fp32 may be NULL.
+ * Supported: dk = dv = 128.
+ * ---------------------------------------------------------------------- */
+enum { MH_KDA_GATED = 0, MH_KDA_REFERENCE = 1 };
+
+typedef struct {
+  int64_t batch, nheads, seqlen, dk, dv;
+  int32_t dtype;
+  int32_t mode;
+  int32_t kernel_dim;
+  float lam;
+  const float* lam_per_head;
+  const void* q1; const void* q2; const void* k; const void* v;
+  const float* g;
+  const float* initial_state;
+  const float* initial_z;
+  float* final_state;
+  float* final_z;
+  void* o;
+  void* o2;
+} mh_kda_args;
+
+int mh_kda_chunk_scan_fwd(const mh_kda_args* a, void* stream);
+
+/* ------------------------------------------------------------------------ */
+int mh_abi_version(void);
+const char* mh_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MAMFORMER_HIP_H */

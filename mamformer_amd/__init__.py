@@ -1,0 +1,11 @@
+"""mamformer_amd -- MI355X (gfx950) implementation of Mamformer's Mamba-2 SSD / KDA scan path.
+
+Public ops (``mamformer_amd.ops``): ``selective_scan`` (SSD chunked-scan
+prefill), ``selective_state_update`` / ``recurrent_step`` (decode step) and
+``linear_attn_scan`` (KDA gated scan).  They run hand-written HIP kernels from
+``libmamformer_hip.so`` (build with ``python -m mamformer_amd.build``).
+"""
+
+from .ops import linear_attn_scan, recurrent_step, selective_scan, selective_state_update, ssd_chunk_len
+
+__all__ = ["selective_scan", "selective_state_update", "recurrent_step", "linear_attn_scan", "ssd_chunk_len"]

@@ -1,0 +1,131 @@
+"""ctypes binding of libmamformer_hip.so (C ABI in include/mamformer_hip.h).
+
+The library is loaded lazily on first use and there is no fallback: if the
+shared library is missing or fails to load, every op raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as ct
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
+
+ABI_VERSION = 1
+
+MH_F32, MH_BF16 = 0, 1
+MH_DT_SOFTPLUS, MH_DT_LIMIT, MH_D_PER_CHANNEL = 1, 2, 4
+MH_KDA_GATED, MH_KDA_REFERENCE = 0, 1
+
+ERRORS = {
+    -1: "MH_ERR_NULL", -2: "MH_ERR_SHAPE", -3: "MH_ERR_DTYPE", -4: "MH_ERR_STRIDE",
+    -5: "MH_ERR_ALIGN", -6: "MH_ERR_UNSUPPORTED", -7: "MH_ERR_WORKSPACE", -8: "MH_ERR_HIP",
+}
+
+_i64, _i32, _f32, _vp, _sz = ct.c_int64, ct.c_int32, ct.c_float, ct.c_void_p, ct.c_size_t
+
+
+class SsdArgs(ct.Structure):
+    _fields_ = [
+        ("batch", _i64), ("seqlen", _i64), ("nheads", _i64), ("headdim", _i64), ("dstate", _i64),
+        ("ngroups", _i64), ("chunk_len", _i64),
+        ("dtype", _i32), ("flags", _i32), ("dt_min", _f32), ("dt_max", _f32),
+        ("x", _vp), ("x_stride_b", _i64), ("x_stride_l", _i64), ("x_stride_h", _i64),
+        ("dt", _vp), ("dt_stride_b", _i64), ("dt_stride_l", _i64),
+        ("A", _vp),
+        ("B", _vp), ("B_stride_b", _i64), ("B_stride_l", _i64),
+        ("C", _vp), ("C_stride_b", _i64), ("C_stride_l", _i64),
+        ("D", _vp), ("dt_bias", _vp), ("initial_state", _vp),
+        ("y", _vp), ("y_stride_b", _i64), ("y_stride_l", _i64), ("y_stride_h", _i64),
+        ("final_state", _vp),
+        ("workspace", _vp), ("workspace_bytes", _sz),
+    ]
+
+
+class SsuArgs(ct.Structure):
+    _fields_ = [
+        ("batch", _i64), ("nheads", _i64), ("headdim", _i64), ("dstate", _i64), ("ngroups", _i64),
+        ("dtype", _i32), ("flags", _i32), ("dt_min", _f32), ("dt_max", _f32),
+        ("state_in", _vp), ("state_out", _vp),
+        ("x", _vp), ("x_stride_b", _i64),
+        ("dt", _vp), ("dt_stride_b", _i64),
+        ("A", _vp),
+        ("B", _vp), ("B_stride_b", _i64),
+        ("C", _vp), ("C_stride_b", _i64),
+        ("D", _vp), ("dt_bias", _vp),
+        ("y", _vp), ("y_stride_b", _i64),
+    ]
+
+
+class KdaArgs(ct.Structure):
+    _fields_ = [
+        ("batch", _i64), ("nheads", _i64), ("seqlen", _i64), ("dk", _i64), ("dv", _i64),
+        ("dtype", _i32), ("mode", _i32), ("kernel_dim", _i32), ("lam", _f32),
+        ("lam_per_head", _vp),
+        ("q1", _vp), ("q2", _vp), ("k", _vp), ("v", _vp),
+        ("g", _vp),
+        ("initial_state", _vp), ("initial_z", _vp),
+        ("final_state", _vp), ("final_z", _vp),
+        ("o", _vp), ("o2", _vp),
+    ]
+
+
+# every symbol include/mamformer_hip.h declares
+EXPORTS = (
+    "mh_abi_version", "mh_last_error",
+    "mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
+    "mh_ssd_state_update",
+    "mh_kda_chunk_scan_fwd",
+)
+
+_lock = threading.Lock()
+_lib = None
+
+
+class MHError(RuntimeError):
+    """A C-ABI call returned a nonzero status."""
+
+    def __init__(self, fn, code, msg):
+        super().__init__(f"{fn}: {ERRORS.get(code, code)}: {msg}")
+        self.code = code
+
+
+def lib():
+    """Load (once) and return the ctypes handle; raises if the library is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH.name} is not built; run `python -m mamformer_amd.build` "
+                    "(there is no CPU fallback for the scan ops)")
+            h = ct.CDLL(str(LIB_PATH))
+            h.mh_abi_version.restype = ct.c_int
+            h.mh_last_error.restype = ct.c_char_p
+            h.mh_ssd_workspace_bytes.argtypes = [ct.POINTER(SsdArgs), ct.POINTER(_sz)]
+            h.mh_ssd_chunk_len.argtypes = [ct.POINTER(SsdArgs), ct.POINTER(_i64)]
+            h.mh_ssd_chunk_scan_fwd.argtypes = [ct.POINTER(SsdArgs), _vp]
+            h.mh_ssd_state_update.argtypes = [ct.POINTER(SsuArgs), _vp]
+            h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
+            for name in ("mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
+                         "mh_ssd_state_update", "mh_kda_chunk_scan_fwd"):
+                getattr(h, name).restype = ct.c_int
+            ver = h.mh_abi_version()
+            if ver != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH.name} ABI version {ver} != expected {ABI_VERSION}; rebuild")
+            _lib = h
+    return _lib
+
+
+def check(fn: str, rc: int):
+    if rc != 0:
+        msg = lib().mh_last_error().decode(errors="replace")
+        raise MHError(fn, rc, msg)
+
+
+def call(fn: str, *args):
+    rc = getattr(lib(), fn)(*args)
+    check(fn, rc)

@@ -1,0 +1,246 @@
+// extern "C" entry points of libmamformer_hip.so (declared in include/mamformer_hip.h).
+// Every entry point validates its argument block completely before the first
+// HIP call, records a message for mh_last_error() on failure, then fills the
+// internal parameter block and launches on the caller's stream.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/mamformer_hip.h"
+#include "launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int elem_size(int32_t dtype) { return dtype == MH_F32 ? 4 : (dtype == MH_BF16 ? 2 : 0); }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+bool stride_ok(int64_t s, int es) { return s >= 0 && ((s * es) % 16) == 0; }
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MH_OK;
+  return fail(MH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// ------------------------------------------------------------------ SSD prefill
+constexpr int64_t kMaxDim = (int64_t)1 << 30;
+
+int ssd_heads_per_wg(const mh_ssd_args* a) {
+  const int64_t hpg = a->nheads / a->ngroups;
+  int hg = 4;
+  if (a->dtype == MH_F32 && a->dstate == 128) hg = 2;
+  while (hg > 1 && (hpg % hg) != 0) hg >>= 1;
+  return hg;
+}
+
+int64_t ssd_auto_chunk(const mh_ssd_args* a) {
+  const int64_t hg = ssd_heads_per_wg(a);
+  const int64_t units = a->batch * (a->nheads / hg);           // workgroups per chunk index
+  const int64_t target = 512;                                   // ~2 workgroups per CU on 256 CUs
+  int64_t want = (a->seqlen * units + target - 1) / target;     // tokens per workgroup
+  want = ((want + 63) / 64) * 64;
+  if (want < 256) want = 256;
+  if (want > 4096) want = 4096;
+  return want;
+}
+
+int ssd_validate(const mh_ssd_args* a, int64_t* chunk_len_out) {
+  if (!a) return fail(MH_ERR_NULL, "ssd: args is NULL");
+  if (a->batch <= 0 || a->seqlen < 0 || a->nheads <= 0 || a->headdim <= 0 || a->dstate <= 0 || a->ngroups <= 0)
+    return fail(MH_ERR_SHAPE, "ssd: sizes must be positive (batch=%lld seqlen=%lld nheads=%lld headdim=%lld dstate=%lld ngroups=%lld)",
+                (long long)a->batch, (long long)a->seqlen, (long long)a->nheads, (long long)a->headdim,
+                (long long)a->dstate, (long long)a->ngroups);
+  if (a->batch > kMaxDim || a->seqlen > kMaxDim || a->nheads > 65535)
+    return fail(MH_ERR_SHAPE, "ssd: sizes out of range");
+  if (a->nheads % a->ngroups)
+    return fail(MH_ERR_SHAPE, "ssd: nheads (%lld) must be a multiple of ngroups (%lld)", (long long)a->nheads,
+                (long long)a->ngroups);
+  const int es = elem_size(a->dtype);
+  if (!es) return fail(MH_ERR_DTYPE, "ssd: unknown dtype %d", a->dtype);
+  if (a->headdim != 64) return fail(MH_ERR_UNSUPPORTED, "ssd: headdim %lld not supported (64)", (long long)a->headdim);
+  if (a->dstate != 64 && a->dstate != 128)
+    return fail(MH_ERR_UNSUPPORTED, "ssd: dstate %lld not supported (64, 128)", (long long)a->dstate);
+  int64_t cl = a->chunk_len;
+  if (cl == 0) cl = ssd_auto_chunk(a);
+  if (cl < 64 || cl % 64 || cl > (1 << 20))
+    return fail(MH_ERR_SHAPE, "ssd: chunk_len %lld must be a positive multiple of 64", (long long)a->chunk_len);
+  if ((a->flags & MH_DT_LIMIT) && !(a->dt_min <= a->dt_max))
+    return fail(MH_ERR_SHAPE, "ssd: dt_min > dt_max");
+  if (!a->x || !a->dt || !a->A || !a->B || !a->C || !a->y) return fail(MH_ERR_NULL, "ssd: x, dt, A, B, C, y are required");
+  if (!aligned16(a->x) || !aligned16(a->B) || !aligned16(a->C) || !aligned16(a->y))
+    return fail(MH_ERR_ALIGN, "ssd: x, B, C, y must be 16-byte aligned");
+  if (!stride_ok(a->x_stride_b, es) || !stride_ok(a->x_stride_l, es) || !stride_ok(a->x_stride_h, es) ||
+      !stride_ok(a->y_stride_b, es) || !stride_ok(a->y_stride_l, es) || !stride_ok(a->y_stride_h, es) ||
+      !stride_ok(a->B_stride_b, es) || !stride_ok(a->B_stride_l, es) || !stride_ok(a->C_stride_b, es) ||
+      !stride_ok(a->C_stride_l, es))
+    return fail(MH_ERR_ALIGN, "ssd: strides of x, y, B, C must be multiples of 16 bytes");
+  if (a->dt_stride_b < 0 || a->dt_stride_l < 0) return fail(MH_ERR_STRIDE, "ssd: negative dt stride");
+  if (a->x_stride_h < a->headdim || a->y_stride_h < a->headdim)
+    return fail(MH_ERR_STRIDE, "ssd: x/y head stride smaller than headdim (headdim must be contiguous)");
+  if (a->B_stride_l < a->ngroups * a->dstate || a->C_stride_l < a->ngroups * a->dstate)
+    return fail(MH_ERR_STRIDE, "ssd: B/C token stride smaller than ngroups*dstate ((g, n) must be contiguous)");
+  const int64_t nchunks = (a->seqlen + cl - 1) / cl;
+  if (nchunks > 65535) return fail(MH_ERR_SHAPE, "ssd: too many chunks (%lld)", (long long)nchunks);
+  if (chunk_len_out) *chunk_len_out = cl;
+  return MH_OK;
+}
+
+// ------------------------------------------------------------------ decode
+int ssu_validate(const mh_ssu_args* a) {
+  if (!a) return fail(MH_ERR_NULL, "state_update: args is NULL");
+  if (a->batch <= 0 || a->nheads <= 0 || a->headdim <= 0 || a->dstate <= 0 || a->ngroups <= 0)
+    return fail(MH_ERR_SHAPE, "state_update: sizes must be positive");
+  if (a->batch * a->nheads > 0x7fffffffLL || a->headdim > 4096)
+    return fail(MH_ERR_SHAPE, "state_update: sizes out of range");
+  if (a->nheads % a->ngroups) return fail(MH_ERR_SHAPE, "state_update: nheads must be a multiple of ngroups");
+  const int es = elem_size(a->dtype);
+  if (!es) return fail(MH_ERR_DTYPE, "state_update: unknown dtype %d", a->dtype);
+  switch (a->dstate) {
+    case 16: case 32: case 64: case 128: case 256: break;
+    default: return fail(MH_ERR_UNSUPPORTED, "state_update: dstate %lld not supported (16..256, power of two)",
+                         (long long)a->dstate);
+  }
+  if ((a->flags & MH_DT_LIMIT) && !(a->dt_min <= a->dt_max)) return fail(MH_ERR_SHAPE, "state_update: dt_min > dt_max");
+  if (!a->state_in || !a->state_out || !a->x || !a->dt || !a->A || !a->B || !a->C || !a->y)
+    return fail(MH_ERR_NULL, "state_update: state_in, state_out, x, dt, A, B, C, y are required");
+  if (!aligned16(a->state_in) || !aligned16(a->state_out))
+    return fail(MH_ERR_ALIGN, "state_update: state must be 16-byte aligned");
+  if (a->x_stride_b < a->nheads * a->headdim || a->y_stride_b < a->nheads * a->headdim ||
+      a->B_stride_b < a->ngroups * a->dstate || a->C_stride_b < a->ngroups * a->dstate || a->dt_stride_b < a->nheads)
+    return fail(MH_ERR_STRIDE, "state_update: batch stride smaller than a row ((h, p) / (g, n) / h contiguous)");
+  if (a->state_in != a->state_out) {
+    const uintptr_t bytes = (uintptr_t)(a->batch * a->nheads * a->headdim * a->dstate * 4);
+    const uintptr_t i0 = (uintptr_t)a->state_in, o0 = (uintptr_t)a->state_out;
+    if (i0 < o0 + bytes && o0 < i0 + bytes)
+      return fail(MH_ERR_STRIDE, "state_update: state_in and state_out overlap without being identical");
+  }
+  return MH_OK;
+}
+
+// ------------------------------------------------------------------ KDA
+int kda_validate(const mh_kda_args* a) {
+  if (!a) return fail(MH_ERR_NULL, "kda: args is NULL");
+  if (a->batch <= 0 || a->nheads <= 0 || a->seqlen < 0 || a->dk <= 0 || a->dv <= 0)
+    return fail(MH_ERR_SHAPE, "kda: sizes must be positive");
+  if (a->batch * a->nheads > 0x7fffffffLL || a->seqlen > kMaxDim) return fail(MH_ERR_SHAPE, "kda: sizes out of range");
+  if (!elem_size(a->dtype)) return fail(MH_ERR_DTYPE, "kda: unknown dtype %d", a->dtype);
+  if (a->dtype != MH_BF16) return fail(MH_ERR_UNSUPPORTED, "kda: only bf16 q/k/v/o are supported");
+  if (a->mode != MH_KDA_GATED) return fail(MH_ERR_UNSUPPORTED, "kda: reference mode is not built yet");
+  if (a->mode != MH_KDA_GATED && a->mode != MH_KDA_REFERENCE) return fail(MH_ERR_UNSUPPORTED, "kda: unknown mode %d", a->mode);
+  if (a->dk != 128 || a->dv != 128)
+    return fail(MH_ERR_UNSUPPORTED, "kda: dk=%lld dv=%lld not supported (128, 128)", (long long)a->dk, (long long)a->dv);
+  if (!a->q1 || !a->k || !a->v || !a->o) return fail(MH_ERR_NULL, "kda: q1, k, v, o are required");
+  if (!a->q2 && a->mode == MH_KDA_REFERENCE) return fail(MH_ERR_NULL, "kda: reference mode needs q2");
+  if (a->mode == MH_KDA_REFERENCE) {
+    if (!a->o2) return fail(MH_ERR_NULL, "kda: reference mode writes o1 and o2");
+    if (a->kernel_dim <= 0) return fail(MH_ERR_SHAPE, "kda: kernel_dim must be positive");
+  }
+  if (!aligned16(a->q1) || (a->q2 && !aligned16(a->q2)) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o) ||
+      (a->o2 && !aligned16(a->o2)) || (a->g && !aligned16(a->g)))
+    return fail(MH_ERR_ALIGN, "kda: tensors must be 16-byte aligned");
+  return MH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mh_abi_version(void) { return MH_ABI_VERSION; }
+const char* mh_last_error(void) { return g_err; }
+
+int mh_ssd_chunk_len(const mh_ssd_args* a, int64_t* chunk_len) {
+  if (!chunk_len) return fail(MH_ERR_NULL, "ssd: chunk_len output is NULL");
+  return ssd_validate(a, chunk_len);
+}
+
+int mh_ssd_workspace_bytes(const mh_ssd_args* a, size_t* bytes) {
+  if (!bytes) return fail(MH_ERR_NULL, "ssd: bytes output is NULL");
+  int64_t cl = 0;
+  int rc = ssd_validate(a, &cl);
+  if (rc) return rc;
+  const int64_t nchunks = (a->seqlen + cl - 1) / cl;
+  *bytes = mh::ssd_workspace_bytes((int)a->batch, (int)nchunks, (int)a->nheads, (int)a->headdim, (int)a->dstate);
+  return MH_OK;
+}
+
+int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream) {
+  int64_t cl = 0;
+  int rc = ssd_validate(a, &cl);
+  if (rc) return rc;
+  const int64_t nchunks = (a->seqlen + cl - 1) / cl;
+  const size_t need = mh::ssd_workspace_bytes((int)a->batch, (int)nchunks, (int)a->nheads, (int)a->headdim, (int)a->dstate);
+  if (nchunks > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+    return fail(MH_ERR_WORKSPACE, "ssd: workspace of %zu bytes (16-byte aligned) required, got %zu", need, a->workspace_bytes);
+  mh::SsdParams p;
+  memset(&p, 0, sizeof(p));
+  p.batch = (int)a->batch; p.seqlen = (int)a->seqlen; p.nheads = (int)a->nheads; p.headdim = (int)a->headdim;
+  p.dstate = (int)a->dstate; p.ngroups = (int)a->ngroups; p.dtype = a->dtype;
+  p.chunk_len = (int)cl; p.nchunks = (int)nchunks; p.heads_per_wg = ssd_heads_per_wg(a);
+  p.dt_softplus = (a->flags & MH_DT_SOFTPLUS) != 0;
+  p.has_dt_limit = (a->flags & MH_DT_LIMIT) != 0;
+  p.D_per_channel = (a->flags & MH_D_PER_CHANNEL) != 0;
+  p.dt_min = a->dt_min; p.dt_max = a->dt_max;
+  p.x = a->x; p.x_sb = a->x_stride_b; p.x_sl = a->x_stride_l; p.x_sh = a->x_stride_h;
+  p.dt = a->dt; p.dt_sb = a->dt_stride_b; p.dt_sl = a->dt_stride_l;
+  p.A = a->A;
+  p.B = a->B; p.B_sb = a->B_stride_b; p.B_sl = a->B_stride_l;
+  p.C = a->C; p.C_sb = a->C_stride_b; p.C_sl = a->C_stride_l;
+  p.D = a->D; p.dt_bias = a->dt_bias; p.init_state = a->initial_state;
+  p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l; p.y_sh = a->y_stride_h;
+  p.final_state = a->final_state;
+  if (nchunks > 0) {
+    const size_t states = (size_t)a->batch * nchunks * a->nheads * a->headdim * a->dstate * sizeof(float);
+    p.chunk_states = reinterpret_cast<float*>(a->workspace);
+    p.chunk_decay = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + ((states + 255) / 256) * 256);
+  }
+  return hip_status(mh::launch_ssd(p, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_fwd");
+}
+
+int mh_ssd_state_update(const mh_ssu_args* a, void* stream) {
+  int rc = ssu_validate(a);
+  if (rc) return rc;
+  mh::SsuParams p;
+  memset(&p, 0, sizeof(p));
+  p.batch = (int)a->batch; p.nheads = (int)a->nheads; p.headdim = (int)a->headdim; p.dstate = (int)a->dstate;
+  p.ngroups = (int)a->ngroups; p.dtype = a->dtype;
+  p.dt_softplus = (a->flags & MH_DT_SOFTPLUS) != 0;
+  p.has_dt_limit = (a->flags & MH_DT_LIMIT) != 0;
+  p.D_per_channel = (a->flags & MH_D_PER_CHANNEL) != 0;
+  p.dt_min = a->dt_min; p.dt_max = a->dt_max;
+  p.state_in = a->state_in; p.state_out = a->state_out;
+  p.x = a->x; p.x_stride_b = a->x_stride_b;
+  p.dt = a->dt; p.dt_stride_b = a->dt_stride_b;
+  p.A = a->A;
+  p.B = a->B; p.B_stride_b = a->B_stride_b;
+  p.C = a->C; p.C_stride_b = a->C_stride_b;
+  p.D = a->D; p.dt_bias = a->dt_bias;
+  p.y = a->y; p.y_stride_b = a->y_stride_b;
+  return hip_status(mh::launch_ssu(p, reinterpret_cast<hipStream_t>(stream)), "ssd_state_update");
+}
+
+int mh_kda_chunk_scan_fwd(const mh_kda_args* a, void* stream) {
+  int rc = kda_validate(a);
+  if (rc) return rc;
+  mh::KdaParams p;
+  memset(&p, 0, sizeof(p));
+  p.batch = (int)a->batch; p.nheads = (int)a->nheads; p.seqlen = (int)a->seqlen; p.dk = (int)a->dk;
+  p.dv = (int)a->dv; p.dtype = a->dtype; p.mode = a->mode;
+  p.kernel_dim = a->kernel_dim < (int32_t)a->dk ? a->kernel_dim : (int32_t)a->dk;
+  p.lam = a->lam; p.lam_h = a->lam_per_head;
+  p.q1 = a->q1; p.q2 = a->q2; p.k = a->k; p.v = a->v; p.g = a->g;
+  p.init_state = a->initial_state; p.init_z = a->initial_z;
+  p.final_state = a->final_state; p.final_z = a->final_z;
+  p.o = a->o; p.o2 = a->o2;
+  return hip_status(mh::launch_kda(p, reinterpret_cast<hipStream_t>(stream)), "kda_chunk_scan_fwd");
+}
+
+}  // extern "C"

@@ -1,0 +1,130 @@
+// Shared device helpers for the gfx950 scan kernels: element conversion,
+// 32x32 MFMA tiles (bf16 and fp32 operand flavours) and wave primitives.
+//
+// Register layout of one 32x32 fp32 accumulator tile (f32x16 per lane), as the
+// CDNA3/CDNA4 32x32 MFMA family writes it:
+//     lane l, element r  ->  row = 8*(r/4) + 4*(l/32) + (r%4),  col = l%32
+// Operand fragments (8 values per lane, one 32x32x16 step):
+//     A[row][k]: lane l holds row l%32,  B[k][col]: lane l holds col l%32,
+// and the 8 k-values a lane holds are addressed by (half = l/32, j = 0..7).
+// The contraction runs over (half, j) identically for A and B, so any
+// bijection (half, j) -> k is a valid "k-set" as long as both operands use
+// it.  The kernels use the *accumulator-derived* k-set
+//     KSET(half, j) = (j < 4) ? 4*half + j : 8 + 4*half + (j - 4)     (within a 16-wide k-step)
+// which is exactly the set of rows an accumulator tile gives a lane for one
+// 16-row half of the tile.  That lets an fp32 accumulator tile be fed back as
+// an MFMA operand (after conversion) with no data movement.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mh {
+
+typedef __bf16 bf16;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
+
+// KSET position of element j of a fragment held by lane-half `half`.
+__device__ __forceinline__ int kset(int half, int j) {
+  return (j < 4) ? (4 * half + j) : (8 + 4 * half + (j - 4));
+}
+
+// ---------------------------------------------------------------- MFMA tiles
+// Fragment of 8 operand values in MFMA input precision.
+template <typename TM> struct Frag;
+template <> struct Frag<bf16> {
+  bf16x8 v;
+  __device__ __forceinline__ void set(int j, float x) { v[j] = (bf16)x; }
+  __device__ __forceinline__ float get(int j) const { return (float)v[j]; }
+};
+template <> struct Frag<float> {
+  float v[8];
+  __device__ __forceinline__ void set(int j, float x) { v[j] = x; }
+  __device__ __forceinline__ float get(int j) const { return v[j]; }
+};
+
+// acc += A(32x16) * B(16x32) for one k-step.
+__device__ __forceinline__ f32x16 mma(const Frag<bf16>& a, const Frag<bf16>& b, f32x16 acc) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+// fp32 operands: eight 32x32x2 steps, step j consuming element j of each half.
+__device__ __forceinline__ f32x16 mma(const Frag<float>& a, const Frag<float>& b, f32x16 acc) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.v[j], b.v[j], acc, 0, 0, 0);
+  return acc;
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// Row of accumulator element r for lane-half `half` (see header comment).
+__device__ __forceinline__ int acc_row(int half, int r) { return 8 * (r >> 2) + 4 * half + (r & 3); }
+
+// Operand fragment for k-step `c` (0 or 1) taken from an accumulator tile:
+// element j of the fragment is accumulator row 16*c + KSET(half, j).
+template <typename TM>
+__device__ __forceinline__ Frag<TM> acc_to_frag(const f32x16& acc, int c) {
+  Frag<TM> f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f.set(j, acc[8 * c + j]);
+  return f;
+}
+// Same with a per-element scale.
+template <typename TM>
+__device__ __forceinline__ Frag<TM> acc_to_frag_scaled(const f32x16& acc, int c, float s) {
+  Frag<TM> f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f.set(j, acc[8 * c + j] * s);
+  return f;
+}
+
+// ---------------------------------------------------------------- wave helpers
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_incl_scan(float v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    float o = __shfl_up(v, off, 64);
+    if (l >= off) v += o;
+  }
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// softplus with PyTorch's default threshold (x > 20 -> x).
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+
+}  // namespace mh

@@ -1,0 +1,320 @@
+// KDA decay-gated linear-attention chunked scan for gfx950.
+//
+//   S_t = diag(exp(g_t)) S_{t-1} + k_t^T v_t          (S: dk x dv, fp32)
+//   o_t = (q1_t - lam q2_t) S_t                          (inclusive of token t)
+// The differential form is linear in q, so q_e = q1 - lam q2 is formed once.
+// With g = 0 this is the un-normalised causal linear attention whose
+// normalised phi(x)=elu(x)+1 form is the reference's LinearDiffAttention scan
+// (mamformer/layers/kda_diff.py:357-478, mamformer/kernels/triton_ssd.py:121-181).
+//
+// One workgroup of 4 waves per (b, h, V-half) walks the sequence in segments
+// of <= 64 tokens.  Per segment, with G = in-segment inclusive cumsum of g
+// (per channel k) and m = its midpoint:
+//     A^T[s][t] = sum_k (k_s e^{m-G_s})[k] (q_e,t e^{G_t-m})[k]   (s <= t)   MFMA, K = dk
+//     o^T[v][t] = sum_s v^T[v][s] A^T[s][t]                                    MFMA
+//               + sum_k S[k][v] (q_e,t e^{G_t})[k]                             MFMA (state read-out)
+//     S[k][v]  <- e^{G_end[k]} S[k][v] + sum_s (k_s e^{G_end-G_s})[k] v_s[v]   MFMA
+// The state lives in MFMA accumulator registers: wave w owns the 32-wide v-tile
+// (w & 1) and the k-half (w >> 1); the two k-halves' read-out partials are
+// summed through LDS.  Segments are cut so that the spread of G within a
+// segment never exceeds RANGE, which keeps every factor finite.
+#include "common.h"
+#include "launch.h"
+
+namespace mh {
+
+namespace {
+
+constexpr int SEGK = 64;          // tokens per segment (max)
+constexpr int DK = 128;
+constexpr int DVH = 64;           // v columns per workgroup
+constexpr float KRANGE = 50.f;    // max spread of G per channel within a segment
+
+template <typename T>
+struct KdaSmem {
+  static constexpr int PK = DK + 16 / (int)sizeof(T);
+  static constexpr int PV = DVH + 16 / (int)sizeof(T);
+  T Qt[SEGK * PK];          // q_e e^{G - m}
+  T Qh[SEGK * PK];          // q_e e^{G}
+  T Kt[SEGK * PK];          // k e^{m - G}   (zero rows beyond the segment)
+  T V[SEGK * PV];           // v[:, V-half]  (zero rows beyond the segment)
+  float G[SEGK][DK];        // in-segment inclusive cumsum of g
+  float tot[2][DK], gmax[2][DK], gmin[2][DK];
+  float m[DK], em[DK], ek[DK], eg[DK];
+  f32x16 red[2][2][64];     // read-out partials of the k-half 1 waves: vt, tt, lane
+  int len;
+};
+
+template <typename TM>
+struct KdaFrags {
+  Frag<TM> A[3][2][64];     // masked A^T tiles as B-operand fragments
+};
+
+}  // namespace
+
+template <typename T, typename TM>
+__global__ __launch_bounds__(256) void kda_gated_kernel(KdaParams p) {
+  __shared__ KdaSmem<T> sm;
+  __shared__ KdaFrags<TM> sf;
+  using SM = KdaSmem<T>;
+  const int nbh = p.batch * p.nheads;
+  int bh, vh;
+  const int L = blockIdx.x;
+  if ((nbh & 7) == 0) {               // keep both V-halves of a (b, h) on one XCD (ids congruent mod 8)
+    bh = (L & 7) | ((L >> 4) << 3);
+    vh = (L >> 3) & 1;
+  } else {
+    bh = L >> 1;
+    vh = L & 1;
+  }
+  const int h = bh % p.nheads;
+  const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
+  const int vt = w & 1, kh = w >> 1;
+  const int tid = threadIdx.x;
+  const int S = p.seqlen;
+  const float lam = p.lam_h ? p.lam_h[h] : p.lam;
+  const int64_t rowbase = (int64_t)bh * S;          // token row index base in (B,H,S,*) tensors
+  const T* q1 = reinterpret_cast<const T*>(p.q1);
+  const T* q2 = reinterpret_cast<const T*>(p.q2);
+  const T* kk = reinterpret_cast<const T*>(p.k);
+  const T* vv = reinterpret_cast<const T*>(p.v);
+  T* oo = reinterpret_cast<T*>(p.o);
+  const int v0 = vh * DVH;
+
+  // state tiles S[k][v] for kt = 2*kh + i, v-tile vt of this V-half
+  f32x16 St[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    St[i] = zero16();
+    if (p.init_state) {
+      const float* s0 = p.init_state + (int64_t)bh * DK * 128;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 32 * (2 * kh + i) + acc_row(half, r);
+        St[i][r] = s0[kr * 128 + v0 + 32 * vt + l32];
+      }
+    }
+  }
+
+  const int kc = tid & 127, th = tid >> 7;
+  for (int pos = 0; pos < S;) {
+    // ---- phase A: per-channel cumulative log-decay, admissible segment length
+    if (tid == 0) sm.len = SEGK;
+    float gl[32];
+    float run = 0.f, lmax = -INFINITY, lmin = INFINITY;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int t = th * 32 + i;
+      float gv = 0.f;
+      if (p.g && pos + t < S) gv = p.g[(rowbase + pos + t) * DK + kc];
+      run += gv;
+      gl[i] = run;
+      lmax = fmaxf(lmax, run);
+      lmin = fminf(lmin, run);
+    }
+    sm.tot[th][kc] = run;
+    sm.gmax[th][kc] = lmax;
+    sm.gmin[th][kc] = lmin;
+    __syncthreads();
+    const float off = th ? sm.tot[0][kc] : 0.f;
+    float pmax = th ? sm.gmax[0][kc] : -INFINITY;
+    float pmin = th ? sm.gmin[0][kc] : INFINITY;
+    int bad = SEGK;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int t = th * 32 + i;
+      const float G = gl[i] + off;
+      sm.G[t][kc] = G;
+      pmax = fmaxf(pmax, G);
+      pmin = fminf(pmin, G);
+      if ((pmax - pmin > KRANGE || pos + t >= S) && bad == SEGK) bad = t;
+    }
+    atomicMin(&sm.len, bad);
+    __syncthreads();
+    const int len = sm.len;
+    if (tid < DK) {
+      const float g0 = sm.G[0][tid], ge = sm.G[len - 1][tid];
+      const float m = 0.5f * (g0 + ge);
+      sm.m[tid] = m;
+      sm.em[tid] = __expf(m);
+      sm.ek[tid] = __expf(ge - m);
+      sm.eg[tid] = __expf(ge);
+    }
+    __syncthreads();
+
+    // ---- phase B: operand tiles
+    for (int e = tid; e < SEGK * (DK / 8); e += 256) {
+      const int t = e >> 4, k0 = (e & 15) * 8;
+      const bool in = t < len;
+      float qv1[8], qv2[8], kv[8];
+      if (in) {
+        const int64_t r = (rowbase + pos + t) * DK + k0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          qv1[j] = to_f32(q1[r + j]);
+          qv2[j] = p.q2 ? to_f32(q2[r + j]) : 0.f;
+          kv[j] = to_f32(kk[r + j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float qt = 0.f, qh = 0.f, kt = 0.f;
+        if (in) {
+          const float G = sm.G[t][k0 + j], m = sm.m[k0 + j];
+          const float e1 = __expf(G - m);
+          const float qe = qv1[j] - lam * qv2[j];
+          qt = qe * e1;
+          qh = qt * sm.em[k0 + j];
+          kt = kv[j] * __expf(m - G);
+        }
+        sm.Qt[t * SM::PK + k0 + j] = from_f32<T>(qt);
+        sm.Qh[t * SM::PK + k0 + j] = from_f32<T>(qh);
+        sm.Kt[t * SM::PK + k0 + j] = from_f32<T>(kt);
+      }
+    }
+    for (int e = tid; e < SEGK * (DVH / 8); e += 256) {
+      const int t = e >> 3, c0 = (e & 7) * 8;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (t < len) {
+        if (sizeof(T) == 2) {
+          val = *reinterpret_cast<const uint4*>(vv + (rowbase + pos + t) * 128 + v0 + c0);
+        }
+      }
+      if (sizeof(T) == 2) {
+        *reinterpret_cast<uint4*>(&sm.V[t * SM::PV + c0]) = val;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          sm.V[t * SM::PV + c0 + j] = (t < len) ? vv[(rowbase + pos + t) * 128 + v0 + c0 + j] : from_f32<T>(0.f);
+      }
+    }
+    __syncthreads();
+
+    // ---- phase C: masked A^T tiles (s-tile, t-tile) in {(0,0),(0,1),(1,1)}
+    if (w < 3) {
+      const int st = (w == 2) ? 1 : 0, tt = (w == 0) ? 0 : 1;
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int c = 0; c < DK / 16; ++c) {
+        Frag<TM> a, bb;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          a.set(j, to_f32(sm.Kt[(32 * st + l32) * SM::PK + 16 * c + 8 * half + j]));
+          bb.set(j, to_f32(sm.Qt[(32 * tt + l32) * SM::PK + 16 * c + 8 * half + j]));
+        }
+        acc = mma(a, bb, acc);
+      }
+      const int tl = 32 * tt + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int s = 32 * st + acc_row(half, r);
+        if (!(s <= tl && s < len)) acc[r] = 0.f;
+      }
+      sf.A[w][0][l] = acc_to_frag<TM>(acc, 0);
+      sf.A[w][1][l] = acc_to_frag<TM>(acc, 1);
+    }
+    __syncthreads();
+
+    // ---- phase D: per wave (v-tile vt, k-half kh)
+    Frag<TM> vf[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vf[c].set(j, to_f32(sm.V[(16 * c + kset(half, j)) * SM::PV + 32 * vt + l32]));
+
+    f32x16 o[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int kt = 2 * kh + i;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const Frag<TM> sa = acc_to_frag<TM>(St[i], c);
+          Frag<TM> qb;
+          const T* row = sm.Qh + (32 * tt + l32) * SM::PK + 32 * kt + 16 * c;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            qb.set(j, to_f32(row[4 * half + j]));
+            qb.set(4 + j, to_f32(row[8 + 4 * half + j]));
+          }
+          acc = mma(sa, qb, acc);
+        }
+      }
+      o[tt] = acc;
+    }
+    if (kh == 0) {
+      o[0] = mma(vf[0], sf.A[0][0][l], o[0]);
+      o[0] = mma(vf[1], sf.A[0][1][l], o[0]);
+    } else {
+      o[1] = mma(vf[0], sf.A[1][0][l], o[1]);
+      o[1] = mma(vf[1], sf.A[1][1][l], o[1]);
+      o[1] = mma(vf[2], sf.A[2][0][l], o[1]);
+      o[1] = mma(vf[3], sf.A[2][1][l], o[1]);
+      sm.red[vt][0][l] = o[0];
+      sm.red[vt][1][l] = o[1];
+    }
+    // state update (uses sm.Kt, sm.V, sm.eg, sm.ek only)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int kt = 2 * kh + i;
+      const int krow = 32 * kt + l32;           // A-operand row of this lane
+      const float ekr = sm.ek[krow];
+      f32x16 acc = St[i];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] *= sm.eg[32 * kt + acc_row(half, r)];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        Frag<TM> kf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) kf.set(j, ekr * to_f32(sm.Kt[(16 * c + kset(half, j)) * SM::PK + krow]));
+        acc = mma(kf, vf[c], acc);
+      }
+      St[i] = acc;
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int tl = 32 * tt + l32;
+        const f32x16 other = sm.red[vt][tt][l];
+        if (tl < len) {
+          T* orow = oo + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = from_f32<T>(o[tt][r] + other[r]);
+        }
+      }
+    }
+    __syncthreads();
+    pos += len;
+  }
+
+  if (p.final_state) {
+    float* sf_out = p.final_state + (int64_t)bh * DK * 128;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 32 * (2 * kh + i) + acc_row(half, r);
+        sf_out[kr * 128 + v0 + 32 * vt + l32] = St[i][r];
+      }
+  }
+}
+
+hipError_t launch_kda(const KdaParams& p, hipStream_t st) {
+  if (p.mode != 0) return hipErrorInvalidValue;   // reference mode: not built yet
+  const int nbh = p.batch * p.nheads;
+  if (p.seqlen == 0) {
+    if (!p.final_state) return hipSuccess;
+    const size_t bytes = (size_t)nbh * DK * 128 * sizeof(float);
+    if (p.init_state) return hipMemcpyAsync(p.final_state, p.init_state, bytes, hipMemcpyDeviceToDevice, st);
+    return hipMemsetAsync(p.final_state, 0, bytes, st);
+  }
+  if (p.dtype != DT_BF16) return hipErrorInvalidValue;
+  dim3 grid((unsigned)(2 * nbh)), block(256);
+  hipLaunchKernelGGL((kda_gated_kernel<bf16, bf16>), grid, block, 0, st, p);
+  return hipGetLastError();
+}
+
+}  // namespace mh

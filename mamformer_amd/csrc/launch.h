@@ -1,0 +1,72 @@
+// Internal (not exported) kernel parameter blocks and launchers.  The C ABI in
+// capi.hip validates the public argument structs, fills these and launches.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mh {
+
+enum { DT_F32 = 0, DT_BF16 = 1 };
+
+// ------------------------------------------------------------- decode
+struct SsuParams {
+  int batch, nheads, headdim, dstate, ngroups, dtype;
+  int dt_softplus, has_dt_limit, D_per_channel;
+  float dt_min, dt_max;
+  const float* state_in;
+  float* state_out;
+  const void* x; int64_t x_stride_b;
+  const float* dt; int64_t dt_stride_b;
+  const float* A;
+  const void* B; int64_t B_stride_b;
+  const void* C; int64_t C_stride_b;
+  const float* D;
+  const float* dt_bias;
+  void* y; int64_t y_stride_b;
+};
+hipError_t launch_ssu(const SsuParams& p, hipStream_t st);
+
+// ------------------------------------------------------------- SSD prefill
+struct SsdParams {
+  int batch, seqlen, nheads, headdim, dstate, ngroups, dtype;
+  int chunk_len;       // state-passing chunk length (multiple of 64)
+  int nchunks;         // ceil(seqlen / chunk_len)
+  int heads_per_wg;    // heads handled by one workgroup (one wave per head)
+  int dt_softplus, has_dt_limit, D_per_channel;
+  float dt_min, dt_max;
+  const void* x; int64_t x_sb, x_sl, x_sh;
+  const float* dt; int64_t dt_sb, dt_sl;
+  const float* A;
+  const void* B; int64_t B_sb, B_sl;
+  const void* C; int64_t C_sb, C_sl;
+  const float* D;
+  const float* dt_bias;
+  const float* init_state;
+  void* y; int64_t y_sb, y_sl, y_sh;
+  float* final_state;
+  float* chunk_states;   // workspace: [batch][nchunks][nheads][headdim][dstate]
+  float* chunk_decay;    // workspace: [batch][nheads][nchunks]  (sum of A*dt over the chunk)
+};
+hipError_t launch_ssd(const SsdParams& p, hipStream_t st);
+size_t ssd_workspace_bytes(int batch, int nchunks, int nheads, int headdim, int dstate);
+
+// ------------------------------------------------------------- KDA
+struct KdaParams {
+  int batch, nheads, seqlen, dk, dv, dtype;
+  int mode;            // 0 gated, 1 reference (phi + normaliser)
+  int kernel_dim;      // reference mode: phi applied to the first kernel_dim channels
+  float lam;           // gated mode: scalar lambda
+  const float* lam_h;  // per-head lambda (overrides lam when set)
+  const void* q1; const void* q2; const void* k; const void* v;
+  const float* g;      // gated mode: per-channel log decay (B,H,S,dk) fp32, may be null (no decay)
+  const float* init_state;   // (B,H,dk,dv) fp32 or null
+  const float* init_z;       // reference mode: (B,H,dk) fp32 or null
+  float* final_state;        // (B,H,dk,dv) fp32 or null
+  float* final_z;            // reference mode: (B,H,dk) or null
+  void* o;                   // gated: o; reference: o1
+  void* o2;                  // reference: o2
+};
+hipError_t launch_kda(const KdaParams& p, hipStream_t st);
+
+}  // namespace mh

@@ -1,0 +1,105 @@
+// Single-token selective state update (the decode step of a Mamba-2 layer).
+//
+// Per (b, h):  dt' = clamp(softplus(dt + dt_bias)),  a = exp(A_h dt')
+//              s[p, n] <- a * s[p, n] + dt' * x[p] * B[g, n]          (fp32, read-modify-write)
+//              y[p]     = sum_n C[g, n] * s[p, n] + D * x[p]
+// Reference semantics: Mamba2Block._recurrent_step, mamformer/layers/mamba2.py:431-458
+// (with A_log, dt, D in the per-head SSD convention; see the oracle's bridge).
+//
+// Bandwidth-bound: the fp32 state is read once and written once; everything
+// else is a few KB.  One workgroup of 256 threads per (b, h): each thread owns
+// a 16-byte column slice (4 states) of N/4-thread rows and walks P/(1024/N)
+// rows with all loads issued before any arithmetic so that up to eight
+// 16-byte loads per thread are in flight.  The dot product over N is a
+// shuffle reduction inside the N/4 lanes that share a row.
+#include "common.h"
+#include "launch.h"
+
+namespace mh {
+
+template <int N, typename T>
+__global__ __launch_bounds__(256) void ssu_kernel(SsuParams p) {
+  constexpr int TPR = N / 4;        // threads per state row
+  constexpr int RP = 256 / TPR;     // rows per pass
+  constexpr int UNROLL = 8;
+  const int bh = blockIdx.x;
+  const int b = bh / p.nheads;
+  const int h = bh - b * p.nheads;
+  const int g = h / (p.nheads / p.ngroups);
+  const int ln = threadIdx.x % TPR;
+  const int row0 = threadIdx.x / TPR;
+
+  float dt = p.dt[(int64_t)b * p.dt_stride_b + h];
+  if (p.dt_bias) dt += p.dt_bias[h];
+  if (p.dt_softplus) dt = softplus_f(dt);
+  if (p.has_dt_limit) dt = fminf(fmaxf(dt, p.dt_min), p.dt_max);
+  const float a = __expf(p.A[h] * dt);
+
+  const T* Bp = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_stride_b + (int64_t)g * N + ln * 4;
+  const T* Cp = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_stride_b + (int64_t)g * N + ln * 4;
+  float Bv[4], Cv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    Bv[i] = to_f32(Bp[i]) * dt;
+    Cv[i] = to_f32(Cp[i]);
+  }
+  const T* xp = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_stride_b + (int64_t)h * p.headdim;
+  T* yp = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_stride_b + (int64_t)h * p.headdim;
+  const int64_t sbase = ((int64_t)b * p.nheads + h) * p.headdim * N;
+  const f32x4* sin = reinterpret_cast<const f32x4*>(p.state_in + sbase);
+  f32x4* sout = reinterpret_cast<f32x4*>(p.state_out + sbase);
+  const float Dh = p.D ? (p.D_per_channel ? 0.f : p.D[h]) : 0.f;
+
+  for (int pbase = row0; pbase < p.headdim; pbase += RP * UNROLL) {
+    f32x4 s[UNROLL];
+    float xv[UNROLL];
+#pragma unroll
+    for (int i = 0; i < UNROLL; ++i) {
+      const int pr = pbase + i * RP;
+      if (pr < p.headdim) {
+        s[i] = __builtin_nontemporal_load(&sin[pr * TPR + ln]);
+        xv[i] = to_f32(xp[pr]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < UNROLL; ++i) {
+      const int pr = pbase + i * RP;
+      if (pr < p.headdim) {  // uniform within a row group
+        f32x4 v = s[i];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = a * v[c] + xv[i] * Bv[c];
+        __builtin_nontemporal_store(v, &sout[pr * TPR + ln]);
+        float part = v[0] * Cv[0] + v[1] * Cv[1] + v[2] * Cv[2] + v[3] * Cv[3];
+#pragma unroll
+        for (int off = TPR / 2; off > 0; off >>= 1) part += __shfl_xor(part, off, TPR);
+        if (ln == 0) {
+          const float dd = p.D ? (p.D_per_channel ? p.D[h * p.headdim + pr] : Dh) : 0.f;
+          yp[pr] = from_f32<T>(part + dd * xv[i]);
+        }
+      }
+    }
+  }
+}
+
+template <int N>
+static hipError_t launch_ssu_n(const SsuParams& p, hipStream_t st) {
+  dim3 grid((unsigned)(p.batch * p.nheads)), block(256);
+  if (p.dtype == DT_BF16)
+    hipLaunchKernelGGL((ssu_kernel<N, bf16>), grid, block, 0, st, p);
+  else
+    hipLaunchKernelGGL((ssu_kernel<N, float>), grid, block, 0, st, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_ssu(const SsuParams& p, hipStream_t st) {
+  switch (p.dstate) {
+    case 16: return launch_ssu_n<16>(p, st);
+    case 32: return launch_ssu_n<32>(p, st);
+    case 64: return launch_ssu_n<64>(p, st);
+    case 128: return launch_ssu_n<128>(p, st);
+    case 256: return launch_ssu_n<256>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace mh

@@ -1,0 +1,341 @@
+"""Scan-path operators with the reference's names, argument order and layouts.
+
+Every op launches hand-written gfx950 HIP kernels through the C ABI
+(``libmamformer_hip.so``) on the current torch stream.  There is no CPU or
+PyTorch fallback: non-CUDA tensors or a missing library raise.
+
+Reference functions replaced (``R`` = ``mamformer 671b/``):
+
+=====================================  ====================================================================
+``selective_scan``                      R/mamformer/layers/mamba2.py:31-67 (``_selective_scan_impl`` :70-130)
+``recurrent_step``                      R/mamformer/layers/mamba2.py:407-458 (``Mamba2Block._recurrent_step``)
+``selective_state_update``              in-place form of the same decode step (the state is updated in HBM)
+``linear_attn_scan``                    gated KDA scan of the benchmark configuration (no reference function)
+=====================================  ====================================================================
+
+SSD convention.  The reference's scan uses a per-channel dt and a per-state
+A_log (decay exp(-exp(A_log[n]) dt[c])); the kernels implement the Mamba-2
+per-head form (decay exp(A_h dt_h), A_h < 0).  The two meet exactly through
+the reparameterisation A_log = 0, dt_ref = -A_h dt_h, x_ref = x / -A_h,
+D_ref = -A_h D_h (see ``oracle.ssd``).  Channel ``c = h * headdim + p`` so
+``x (b, L, d_inner)`` and ``final_state (b, d_inner, N)`` keep the reference
+memory layout.
+"""
+
+from __future__ import annotations
+
+import ctypes as ct
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import SsdArgs, SsuArgs, KdaArgs
+
+__all__ = ["selective_scan", "selective_state_update", "recurrent_step", "linear_attn_scan",
+           "ssd_chunk_len"]
+
+_DT = {torch.float32: _lib.MH_F32, torch.bfloat16: _lib.MH_BF16}
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ct.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device):
+    return ct.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _require_cuda(name, *ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"{name}: HIP op needs device tensors (got {t.device}); no CPU path exists")
+    devs = {t.device for t in ts if t is not None}
+    if len(devs) > 1:
+        raise RuntimeError(f"{name}: tensors on different devices {devs}")
+
+
+def _f32c(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    return t.to(torch.float32).contiguous()
+
+
+def _inner_contig(t: torch.Tensor, ndim_inner: int = 1) -> torch.Tensor:
+    """Make the innermost `ndim_inner` dims contiguous and 16-byte aligned rows (copy if needed)."""
+    es = t.element_size()
+    ok = t.stride(-1) == 1 and (ndim_inner == 1 or t.stride(-2) == t.shape[-1])
+    ok = ok and t.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in t.stride()[:-ndim_inner])
+    return t if ok else t.contiguous()
+
+
+def _ssd_args(x4, dt, A, B4, C4, D, dt_bias, dt_softplus, dt_limit, initial_state, y4, final_state, chunk_size):
+    b, L, H, P = x4.shape
+    G, N = B4.shape[2], B4.shape[3]
+    a = SsdArgs()
+    a.batch, a.seqlen, a.nheads, a.headdim, a.dstate, a.ngroups = b, L, H, P, N, G
+    a.chunk_len = int(chunk_size or 0)
+    a.dtype = _DT[x4.dtype]
+    flags = 0
+    if dt_softplus:
+        flags |= _lib.MH_DT_SOFTPLUS
+    if dt_limit is not None:
+        flags |= _lib.MH_DT_LIMIT
+        a.dt_min, a.dt_max = float(dt_limit[0]), float(dt_limit[1])
+    if D is not None and D.numel() == H * P and H * P != H:
+        flags |= _lib.MH_D_PER_CHANNEL
+    a.flags = flags
+    a.x, a.x_stride_b, a.x_stride_l, a.x_stride_h = _ptr(x4), x4.stride(0), x4.stride(1), x4.stride(2)
+    a.dt, a.dt_stride_b, a.dt_stride_l = _ptr(dt), dt.stride(0), dt.stride(1)
+    a.A = _ptr(A)
+    a.B, a.B_stride_b, a.B_stride_l = _ptr(B4), B4.stride(0), B4.stride(1)
+    a.C, a.C_stride_b, a.C_stride_l = _ptr(C4), C4.stride(0), C4.stride(1)
+    a.D, a.dt_bias, a.initial_state = _ptr(D), _ptr(dt_bias), _ptr(initial_state)
+    a.y, a.y_stride_b, a.y_stride_l, a.y_stride_h = _ptr(y4), y4.stride(0), y4.stride(1), y4.stride(2)
+    a.final_state = _ptr(final_state)
+    return a
+
+
+def ssd_chunk_len(batch, seqlen, nheads, headdim, dstate, ngroups, dtype=torch.bfloat16, chunk_size=None):
+    """State-passing chunk length the kernels will use for these sizes (auto when chunk_size is None)."""
+    a = SsdArgs()
+    a.batch, a.seqlen, a.nheads, a.headdim, a.dstate, a.ngroups = batch, seqlen, nheads, headdim, dstate, ngroups
+    a.chunk_len = int(chunk_size or 0)
+    a.dtype = _DT[dtype]
+    # dummy, aligned, non-null pointers and consistent strides (validation only)
+    fake = ct.c_void_p(256)
+    a.x = a.B = a.C = a.y = a.dt = a.A = fake
+    a.x_stride_h = a.y_stride_h = headdim
+    a.x_stride_l = a.y_stride_l = nheads * headdim
+    a.x_stride_b = a.y_stride_b = seqlen * nheads * headdim
+    a.B_stride_l = a.C_stride_l = ngroups * dstate
+    a.B_stride_b = a.C_stride_b = seqlen * ngroups * dstate
+    out = ct.c_int64()
+    _lib.call("mh_ssd_chunk_len", ct.byref(a), ct.byref(out))
+    return out.value
+
+
+def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=False, *,
+                   chunk_size=None, initial_state=None, dt_bias=None, dt_softplus=False, dt_limit=None):
+    """Mamba-2 SSD chunked-scan prefill.  Drop-in for ``selective_scan`` (R/mamformer/layers/mamba2.py:31-67).
+
+    Args (SSD convention; see module docstring):
+        x: (b, L, H*P) like the reference, or (b, L, H, P); fp32 or bf16.
+        dt: (b, L, H) per-head step sizes (positive unless ``dt_softplus``).
+        A: (H,) per-head decay rates, A <= 0.
+        B, C: (b, L, N) (one group, as the reference) or (b, L, G, N); dtype of x.
+        D: (H,), (H*P,) or None.
+        return_h_states: not supported by the HIP path yet (raises).
+        return_final_state: also return the state after the last token,
+            shaped (b, H*P, N) for 3-D x (the reference's (b, d_inner, d_state)) or (b, H, P, N).
+        chunk_size: state-passing chunk length (multiple of 64); None picks it from the shape.
+        initial_state: (b, H*P, N) / (b, H, P, N) fp32 state before the first token (prefill of a cached
+            sequence); the reference scan always starts from zero (mamba2.py:101).
+        dt_bias, dt_softplus, dt_limit: dt <- clamp(softplus(dt + dt_bias), *dt_limit) inside the kernel.
+    Returns y (like x), or (y, final_state) in the reference's tuple order (mamba2.py:121-130).
+    """
+    if return_h_states:
+        raise NotImplementedError("selective_scan: return_h_states is not implemented by the HIP path")
+    _require_cuda("selective_scan", x, dt, A, B, C, D, initial_state, dt_bias)
+    if x.dtype not in _DT:
+        raise TypeError(f"selective_scan: x dtype {x.dtype} not supported (float32, bfloat16)")
+    if B.dtype != x.dtype or C.dtype != x.dtype:
+        raise TypeError("selective_scan: B and C must have the dtype of x")
+    if dt.dim() != 3:
+        raise ValueError(f"selective_scan: dt must be (b, L, H), got {tuple(dt.shape)}")
+    b, L, H = dt.shape
+    if x.dim() == 3:
+        if x.shape[0] != b or x.shape[1] != L or x.shape[2] % H:
+            raise ValueError(f"selective_scan: x {tuple(x.shape)} incompatible with dt {tuple(dt.shape)}")
+        P = x.shape[2] // H
+        x4 = x.view(b, L, H, P) if x.stride(-1) == 1 else x.contiguous().view(b, L, H, P)
+    elif x.dim() == 4:
+        P = x.shape[3]
+        if tuple(x.shape[:3]) != (b, L, H):
+            raise ValueError(f"selective_scan: x {tuple(x.shape)} incompatible with dt {tuple(dt.shape)}")
+        x4 = x
+    else:
+        raise ValueError("selective_scan: x must be (b, L, H*P) or (b, L, H, P)")
+    B4 = B.unsqueeze(2) if B.dim() == 3 else B
+    C4 = C.unsqueeze(2) if C.dim() == 3 else C
+    if B4.shape[:2] != (b, L) or C4.shape != B4.shape:
+        raise ValueError(f"selective_scan: B {tuple(B.shape)} / C {tuple(C.shape)} incompatible with dt")
+    G, N = B4.shape[2], B4.shape[3]
+    if A.shape != (H,):
+        raise ValueError(f"selective_scan: A must be (H,) = ({H},), got {tuple(A.shape)}")
+    if D is not None and D.numel() not in (H, H * P):
+        raise ValueError(f"selective_scan: D must have H or H*P entries, got {tuple(D.shape)}")
+    x4 = _inner_contig(x4)
+    B4 = _inner_contig(B4, 2)
+    C4 = _inner_contig(C4, 2)
+    dt32 = dt.to(torch.float32)
+    if dt32.stride(-1) != 1:
+        dt32 = dt32.contiguous()
+    if dt_bias is not None and dt_bias.numel() != H:
+        raise ValueError(f"selective_scan: dt_bias must have H = {H} entries")
+    A32, D32, bias32 = _f32c(A), _f32c(D.reshape(-1) if D is not None else None), _f32c(dt_bias)
+    h0 = None
+    if initial_state is not None:
+        if initial_state.numel() != b * H * P * N:
+            raise ValueError(f"selective_scan: initial_state must hold b*H*P*N = {b * H * P * N} values")
+        h0 = initial_state.reshape(b, H, P, N).to(torch.float32).contiguous()
+    y4 = torch.empty((b, L, H, P), device=x.device, dtype=x.dtype)
+    fin = torch.empty((b, H, P, N), device=x.device, dtype=torch.float32) if return_final_state else None
+    args = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, y4, fin, chunk_size)
+    nbytes = ct.c_size_t()
+    _lib.call("mh_ssd_workspace_bytes", ct.byref(args), ct.byref(nbytes))
+    ws = torch.empty(max(int(nbytes.value), 16), device=x.device, dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = _ptr(ws), nbytes.value
+    _lib.call("mh_ssd_chunk_scan_fwd", ct.byref(args), _stream(x.device))
+    y = y4.view(x.shape) if x.dim() == 3 else y4
+    if not return_final_state:
+        return y
+    return y, (fin.view(b, H * P, N) if x.dim() == 3 else fin)
+
+
+def selective_state_update(state, x, dt, A, B, C, D=None, *, dt_bias=None, dt_softplus=True, dt_limit=None,
+                           out_state=None):
+    """One-token SSD state update on the GPU, in place by default.
+
+    state (b, H, P, N) fp32 (updated in place unless ``out_state`` is given);
+    x (b, H, P); dt (b, H) raw (``dt_softplus``/``dt_bias``/``dt_limit`` applied
+    in the kernel, as the decode path of mamba2.py:293 does before the step);
+    A (H,); B, C (b, N) or (b, G, N); D (H,), (H, P) or None.  Returns y (b, H, P).
+    Semantics of ``Mamba2Block._recurrent_step`` (R/mamformer/layers/mamba2.py:431-458).
+    """
+    _require_cuda("selective_state_update", state, x, dt, A, B, C, D, dt_bias, out_state)
+    if state.dim() != 4 or state.dtype != torch.float32:
+        raise ValueError("selective_state_update: state must be (b, H, P, N) float32")
+    b, H, P, N = state.shape
+    if x.shape != (b, H, P):
+        raise ValueError(f"selective_state_update: x must be {(b, H, P)}, got {tuple(x.shape)}")
+    if x.dtype not in _DT or B.dtype != x.dtype or C.dtype != x.dtype:
+        raise TypeError("selective_state_update: x, B, C must share a dtype in (float32, bfloat16)")
+    B3 = B.unsqueeze(1) if B.dim() == 2 else B
+    C3 = C.unsqueeze(1) if C.dim() == 2 else C
+    if B3.shape[0] != b or B3.shape[2] != N or C3.shape != B3.shape:
+        raise ValueError("selective_state_update: B/C must be (b, N) or (b, G, N)")
+    G = B3.shape[1]
+    if dt.shape != (b, H):
+        raise ValueError(f"selective_state_update: dt must be {(b, H)}")
+    if not state.is_contiguous():
+        raise ValueError("selective_state_update: state must be contiguous (it is updated in place)")
+    xs = x if (x.stride(-1) == 1 and x.stride(-2) == P) else x.contiguous()
+    Bs = B3 if (B3.stride(-1) == 1 and B3.stride(-2) == N) else B3.contiguous()
+    Cs = C3 if (C3.stride(-1) == 1 and C3.stride(-2) == N) else C3.contiguous()
+    if A.numel() != H:
+        raise ValueError(f"selective_state_update: A must have H = {H} entries")
+    if D is not None and D.numel() not in (H, H * P):
+        raise ValueError("selective_state_update: D must have H or H*P entries")
+    if dt_bias is not None and dt_bias.numel() != H:
+        raise ValueError(f"selective_state_update: dt_bias must have H = {H} entries")
+    if H % G:
+        raise ValueError("selective_state_update: nheads must be a multiple of ngroups")
+    dt32 = dt.to(torch.float32)
+    if dt32.stride(-1) != 1:
+        dt32 = dt32.contiguous()
+    A32, D32, bias32 = _f32c(A), _f32c(D.reshape(-1) if D is not None else None), _f32c(dt_bias)
+    dst = state if out_state is None else out_state
+    if dst is not state and (dst.shape != state.shape or dst.dtype != torch.float32 or not dst.is_contiguous()):
+        raise ValueError("selective_state_update: out_state must match state")
+    y = torch.empty((b, H, P), device=x.device, dtype=x.dtype)
+    a = SsuArgs()
+    a.batch, a.nheads, a.headdim, a.dstate, a.ngroups = b, H, P, N, G
+    a.dtype = _DT[x.dtype]
+    flags = _lib.MH_DT_SOFTPLUS if dt_softplus else 0
+    if dt_limit is not None:
+        flags |= _lib.MH_DT_LIMIT
+        a.dt_min, a.dt_max = float(dt_limit[0]), float(dt_limit[1])
+    if D32 is not None and D32.numel() == H * P and P != 1:
+        flags |= _lib.MH_D_PER_CHANNEL
+    a.flags = flags
+    a.state_in, a.state_out = _ptr(state), _ptr(dst)
+    a.x, a.x_stride_b = _ptr(xs), xs.stride(0)
+    a.dt, a.dt_stride_b = _ptr(dt32), dt32.stride(0)
+    a.A = _ptr(A32)
+    a.B, a.B_stride_b = _ptr(Bs), Bs.stride(0)
+    a.C, a.C_stride_b = _ptr(Cs), Cs.stride(0)
+    a.D, a.dt_bias = _ptr(D32), _ptr(bias32)
+    a.y, a.y_stride_b = _ptr(y), y.stride(0)
+    _lib.call("mh_ssd_state_update", ct.byref(a), _stream(x.device))
+    return y
+
+
+def recurrent_step(x, dt, B, C, h_prev, A, D, *, dt_bias=None, dt_softplus=False, dt_limit=None):
+    """``Mamba2Block._recurrent_step`` counterpart (R/mamformer/layers/mamba2.py:407-458), per-head form.
+
+    x (b, seqlen, H*P) -- only the last token is used (:435-438); dt (b, seqlen, H)
+    (already softplus'ed, as at mamba2.py:293, unless ``dt_softplus``); B, C (b, seqlen, N)
+    or (b, seqlen, G, N); h_prev (b, H*P, N) or None (zeros, :448-449); A (H,); D (H,) or (H*P,).
+    Returns (y_t (b, 1, H*P), h_t (b, H*P, N)) -- a new state tensor, as the reference returns.
+    """
+    b, _, d_inner = x.shape
+    H = dt.shape[-1]
+    P = d_inner // H
+    Bl = B[:, -1]
+    Cl = C[:, -1]
+    N = Bl.shape[-1]
+    if h_prev is None:
+        state = torch.zeros((b, H, P, N), device=x.device, dtype=torch.float32)
+    else:
+        state = h_prev.reshape(b, H, P, N).to(torch.float32)
+    out = torch.empty((b, H, P, N), device=x.device, dtype=torch.float32)
+    y = selective_state_update(state.contiguous(), x[:, -1].reshape(b, H, P), dt[:, -1], A, Bl, Cl, D,
+                               dt_bias=dt_bias, dt_softplus=dt_softplus, dt_limit=dt_limit, out_state=out)
+    return y.reshape(b, 1, d_inner), out.view(b, d_inner, N)
+
+
+def linear_attn_scan(q1, q2, k, v, *, g=None, lam=0.8, mode="gated", kernel_dim=None, initial_state=None,
+                     return_final_state=False, chunk_size=64):
+    """KDA linear-attention chunked scan on the GPU, layout (B, H, S, D) as the reference (kda_diff.py:270-273).
+
+    mode="gated": S_t = diag(exp(g_t)) S_{t-1} + k_t^T v_t, o_t = q1_t S_t - lam q2_t S_t
+        (g (B, H, S, dk) fp32 per-channel log-decay, or None for no decay; lam a float or (H,) tensor;
+        q2 may be None for a single query).  Returns o, or (o, final_state (B, H, dk, dv) fp32).
+    chunk_size: accepted for API compatibility; the kernel walks segments of <= 64 tokens.
+    """
+    if mode != "gated":
+        raise NotImplementedError(f"linear_attn_scan: mode {mode!r} is not implemented by the HIP path yet")
+    _require_cuda("linear_attn_scan", q1, q2, k, v, g, initial_state)
+    if q1.dim() != 4:
+        raise ValueError("linear_attn_scan: q1 must be (B, H, S, dk)")
+    Bb, H, S, dk = q1.shape
+    dv = v.shape[-1]
+    if k.shape != q1.shape or (q2 is not None and q2.shape != q1.shape) or v.shape[:3] != (Bb, H, S):
+        raise ValueError("linear_attn_scan: q1/q2/k must be (B, H, S, dk) and v (B, H, S, dv)")
+    if q1.dtype not in _DT or any(t is not None and t.dtype != q1.dtype for t in (q2, k, v)):
+        raise TypeError("linear_attn_scan: q1, q2, k, v must share a dtype")
+    q1c, kc, vc = q1.contiguous(), k.contiguous(), v.contiguous()
+    q2c = q2.contiguous() if q2 is not None else None
+    gc = None
+    if g is not None:
+        if g.shape != (Bb, H, S, dk):
+            raise ValueError("linear_attn_scan: g must be (B, H, S, dk)")
+        gc = g.to(torch.float32).contiguous()
+    lam_h = None
+    if torch.is_tensor(lam):
+        lam_h = lam.to(device=q1.device, dtype=torch.float32).reshape(-1).contiguous()
+        if lam_h.numel() != H:
+            raise ValueError("linear_attn_scan: per-head lam must have H entries")
+        lam_f = 0.0
+    else:
+        lam_f = float(lam)
+    s0 = None
+    if initial_state is not None:
+        if initial_state.numel() != Bb * H * dk * dv:
+            raise ValueError("linear_attn_scan: initial_state must be (B, H, dk, dv)")
+        s0 = initial_state.reshape(Bb, H, dk, dv).to(torch.float32).contiguous()
+    o = torch.empty((Bb, H, S, dv), device=q1.device, dtype=q1.dtype)
+    fin = torch.empty((Bb, H, dk, dv), device=q1.device, dtype=torch.float32) if return_final_state else None
+    a = KdaArgs()
+    a.batch, a.nheads, a.seqlen, a.dk, a.dv = Bb, H, S, dk, dv
+    a.dtype = _DT[q1.dtype]
+    a.mode = _lib.MH_KDA_GATED
+    a.kernel_dim = dk
+    a.lam = lam_f
+    a.lam_per_head = _ptr(lam_h)
+    a.q1, a.q2, a.k, a.v, a.g = _ptr(q1c), _ptr(q2c), _ptr(kc), _ptr(vc), _ptr(gc)
+    a.initial_state, a.final_state = _ptr(s0), _ptr(fin)
+    a.o = _ptr(o)
+    _lib.call("mh_kda_chunk_scan_fwd", ct.byref(a), _stream(q1.device))
+    return (o, fin) if return_final_state else o

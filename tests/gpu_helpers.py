@@ -1,0 +1,41 @@
+"""Shared helpers of the GPU parity tests (not collected by pytest)."""
+
+import sys
+
+import numpy as np
+import torch
+
+TOL = {torch.bfloat16: 1e-2, torch.float32: 1e-4}
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(a, dtype=torch.float32):
+    if a is None:
+        return None
+    t = torch.as_tensor(np.asarray(a)) if not torch.is_tensor(a) else a
+    return t.to(device="cuda", dtype=dtype)
+
+
+def host(t):
+    return t.detach().to(torch.float64).cpu().numpy()
+
+
+def rel_l2(out, ref):
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.linalg.norm(ref.ravel())
+    return np.linalg.norm((out - ref).ravel()) / den if den > 0 else np.linalg.norm(out.ravel())
+
+
+def check(name, out, ref, tol):
+    out = host(out) if torch.is_tensor(out) else np.asarray(out)
+    assert np.isfinite(out).all(), f"{name}: non-finite output"
+    e = rel_l2(out, ref)
+    m = np.abs(out - np.asarray(ref)).max() if out.size else 0.0
+    say(f"{name}: rel_l2={e:.3e} max_abs={m:.3e} tol={tol:.0e}")
+    assert e <= tol, f"{name}: rel_l2 {e:.3e} > {tol:.0e}"
+    return e

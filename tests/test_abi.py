@@ -1,0 +1,145 @@
+"""C ABI of libmamformer_hip.so on the CPU host: loads, exports every declared symbol,
+and rejects bad arguments before any HIP call (no compute is launched here)."""
+
+import ctypes as ct
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import mamformer_amd
+from mamformer_amd import _lib
+from mamformer_amd._lib import KdaArgs, SsdArgs, SsuArgs
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "mamformer_hip.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*|size_t)\s+(mh_\w+)\s*\(", text, re.M)))
+
+
+def test_library_loads_and_exports_every_header_symbol():
+    h = _lib.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 7
+    for s in syms:
+        assert hasattr(h, s), s
+    assert set(syms) == set(_lib.EXPORTS)
+    assert h.mh_abi_version() == _lib.ABI_VERSION
+
+
+def _good_ssd():
+    a = SsdArgs()
+    b, L, H, P, N, G = 2, 300, 8, 64, 128, 2
+    a.batch, a.seqlen, a.nheads, a.headdim, a.dstate, a.ngroups = b, L, H, P, N, G
+    a.dtype = _lib.MH_BF16
+    fake = ct.c_void_p(4096)
+    a.x = a.B = a.C = a.y = a.dt = a.A = fake
+    a.x_stride_h = a.y_stride_h = P
+    a.x_stride_l = a.y_stride_l = H * P
+    a.x_stride_b = a.y_stride_b = L * H * P
+    a.B_stride_l = a.C_stride_l = G * N
+    a.B_stride_b = a.C_stride_b = L * G * N
+    a.dt_stride_l, a.dt_stride_b = H, L * H
+    return a
+
+
+def _rc(fn, *args):
+    return getattr(_lib.lib(), fn)(*args)
+
+
+def test_ssd_workspace_and_chunk_len():
+    a = _good_ssd()
+    n = ct.c_size_t()
+    assert _rc("mh_ssd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+    cl = ct.c_int64()
+    assert _rc("mh_ssd_chunk_len", ct.byref(a), ct.byref(cl)) == 0
+    nch = -(-300 // cl.value)
+    assert n.value >= 2 * nch * 8 * 64 * 128 * 4 + 2 * 8 * nch * 4
+    a.chunk_len = 128
+    assert _rc("mh_ssd_chunk_len", ct.byref(a), ct.byref(cl)) == 0 and cl.value == 128
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("headdim", 32, -6), ("dstate", 96, -6), ("dtype", 7, -3), ("ngroups", 3, -2), ("batch", 0, -2),
+    ("chunk_len", 100, -2), ("x_stride_l", 8 * 64 + 1, -5), ("B_stride_l", 64, -4),
+])
+def test_ssd_rejects_bad_arguments(field, value, code):
+    a = _good_ssd()
+    setattr(a, field, value)
+    n = ct.c_size_t()
+    assert _rc("mh_ssd_workspace_bytes", ct.byref(a), ct.byref(n)) == code
+    assert _lib.lib().mh_last_error()
+
+
+def test_ssd_rejects_null_and_misaligned_pointers_and_small_workspace():
+    a = _good_ssd()
+    a.C = None
+    assert _rc("mh_ssd_chunk_scan_fwd", ct.byref(a), None) == -1
+    a = _good_ssd()
+    a.y = ct.c_void_p(4096 + 2)
+    assert _rc("mh_ssd_chunk_scan_fwd", ct.byref(a), None) == -5
+    a = _good_ssd()
+    a.workspace, a.workspace_bytes = ct.c_void_p(8192), 16
+    assert _rc("mh_ssd_chunk_scan_fwd", ct.byref(a), None) == -7
+    assert b"workspace" in _lib.lib().mh_last_error()
+    assert _rc("mh_ssd_chunk_scan_fwd", None, None) == -1
+
+
+def _good_ssu():
+    a = SsuArgs()
+    a.batch, a.nheads, a.headdim, a.dstate, a.ngroups = 4, 8, 64, 128, 1
+    a.dtype = _lib.MH_BF16
+    a.state_in = a.state_out = ct.c_void_p(1 << 20)
+    a.x = a.dt = a.A = a.B = a.C = a.y = ct.c_void_p(4096)
+    a.x_stride_b = a.y_stride_b = 8 * 64
+    a.B_stride_b = a.C_stride_b = 128
+    a.dt_stride_b = 8
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("dstate", 48, -6), ("ngroups", 3, -2), ("dtype", 5, -3), ("x_stride_b", 10, -4), ("nheads", 0, -2),
+])
+def test_state_update_rejects_bad_arguments(field, value, code):
+    a = _good_ssu()
+    setattr(a, field, value)
+    assert _rc("mh_ssd_state_update", ct.byref(a), None) == code
+
+
+def test_state_update_rejects_partial_overlap():
+    a = _good_ssu()
+    a.state_out = ct.c_void_p((1 << 20) + 4096)
+    assert _rc("mh_ssd_state_update", ct.byref(a), None) == -4
+
+
+def test_kda_rejects_bad_arguments():
+    a = KdaArgs()
+    a.batch, a.nheads, a.seqlen, a.dk, a.dv = 1, 2, 10, 128, 128
+    a.dtype = _lib.MH_BF16
+    a.q1 = a.q2 = a.k = a.v = a.o = ct.c_void_p(4096)
+    a.dk = 64
+    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -6
+    a.dk = 128
+    a.v = None
+    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -1
+    a.v = ct.c_void_p(4096)
+    a.dtype = _lib.MH_F32
+    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -6
+
+
+def test_ops_refuse_cpu_tensors():
+    x = torch.zeros(1, 64, 64)
+    dt = torch.zeros(1, 64, 1)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        mamformer_amd.selective_scan(x, dt, torch.zeros(1), torch.zeros(1, 64, 64), torch.zeros(1, 64, 64), None)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        mamformer_amd.linear_attn_scan(*(torch.zeros(1, 1, 4, 128) for _ in range(4)))
+
+
+def test_chunk_len_auto_choice():
+    assert mamformer_amd.ssd_chunk_len(2, 4096, 64, 64, 128, 1) % 64 == 0
+    assert mamformer_amd.ssd_chunk_len(1, 131072, 128, 64, 128, 8) == 4096
+    assert mamformer_amd.ssd_chunk_len(1, 512, 8, 64, 64, 1, chunk_size=128) == 128
