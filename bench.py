@@ -1,0 +1,258 @@
+#!/usr/bin/env python
+"""Benchmark of the Mamba-2 SSD / decode / KDA scan path on one MI355X (gfx950).
+
+Headline (``value``): SSD chunked-scan prefill throughput in Mtok/s at the
+1b shape ``ssd2`` (b2 L4096 H64 P64 N128 G1, bf16 I/O, fp32 final state),
+with inputs resident in HBM.  A step is one ``selective_scan`` pass over one
+batch; three input/output buffer sets rotate so the 256 MB MALL cannot serve
+a step from the previous one.  The same JSON line carries:
+
+* ``roofline`` -- one launch of the prefill op (``mh_ssd_chunk_scan_fwd``:
+  chunk_state + state_pass + chunk_scan dispatches): algorithmic bytes per
+  launch (compulsory I/O only) / average launch duration from HIP events on
+  the launch stream, against 8 TB/s (the op is HBM-bound by intensity).
+* ``cpu_baseline`` -- the reference's pure-PyTorch CPU prefill
+  (``oracle/baseline.py``, mamba2.py:84-126 structure) timed on the host cores
+  on a bounded token sample of the same workload.
+* ``decode`` -- selective state update at B=64 and B=256 (HBM GB/s vs 8 TB/s).
+* ``other`` -- ssd4 (128K prefill with state carry) and kda5 (gated KDA scan).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM = 8.0e12        # B/s, MI355X HBM3E
+PEAK_BF16 = 2.5e15       # FLOP/s, dense bf16 MFMA
+METRIC = "SSD prefill Mtok/s (% MFMA/HBM roofline) + decode-step HBM GB/s vs peak"
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------------- algorithmic counts (compulsory I/O, dense FLOPs)
+
+def ssd_alg(cfg, Q=256):
+    """Bytes: x, B, C, dt read once, y and the fp32 final state written once (+ h0 read); A, D (2H floats) omitted.
+    FLOPs: per (b, chunk of Q): 2Q^2 N G (C B^T) + H (2Q^2 P + 4 Q N P)."""
+    b, L, H, P, N, G = cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups
+    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    nbytes = (2 * b * L * H * P * es + 2 * b * L * G * N * es + b * L * H * 4
+              + b * H * P * N * 4 * (2 if cfg.init_state else 1))
+    nchunks = L // Q
+    flops = b * nchunks * (2 * Q * Q * N * G + H * (2 * Q * Q * P + 4 * Q * N * P))
+    return nbytes, flops
+
+
+def decode_alg(cfg):
+    """Bytes: fp32 state read + written, x and y, B, C, dt, A, D, dt_bias."""
+    b, H, P, N, G = cfg.batch, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups
+    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    return 2 * b * H * P * N * 4 + 2 * b * H * P * es + 2 * b * G * N * es + b * H * 4 + 3 * H * 4
+
+
+def kda_alg(cfg):
+    """Bytes: q1, q2, k, v (bf16), g (fp32) read, o (bf16) and the fp32 final state written.
+    FLOPs (q_e = q1 - lam q2 fused): per (b, h, chunk Q): 2Q^2 K + 2Q^2 V + 2QKV (read-out) + 2QKV (state)."""
+    B, H, S, K, V, Q = cfg.batch, cfg.nheads, cfg.seqlen, cfg.dk, cfg.dv, cfg.chunk
+    nbytes = B * H * S * (3 * K * 2 + V * 2 + K * 4 + V * 2) + B * H * K * V * 4
+    flops = B * H * (S // Q) * (2 * Q * Q * K + 2 * Q * Q * V + 4 * Q * K * V)
+    return nbytes, flops
+
+
+# ----------------------------------------------------------------- timing
+
+def time_plans(plans, steps, warmup):
+    """Warm up, then time exactly `steps` launches cycling through `plans`.
+
+    Returns (wall ms/step, HIP-event ms/step).  Events are recorded on the
+    current torch stream, which is the stream the plans launch on.
+    """
+    for i in range(warmup):
+        plans[i % len(plans)]()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for i in range(steps):
+        plans[i % len(plans)]()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return wall, ev0.elapsed_time(ev1) / steps
+
+
+def bench_ssd(cfg, steps, warmup, nsets, chunk=None):
+    import mamformer_amd as mh
+    from mamformer_amd import workloads as W
+
+    plans = []
+    for i in range(nsets):
+        inp = W.ssd_inputs(cfg.scaled(seed=cfg.seed + 1000 * i), device="cuda")
+        plans.append(mh.plan_selective_scan(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
+                                            return_final_state=True, initial_state=inp["initial_state"],
+                                            chunk_size=chunk))
+    wall, ev = time_plans(plans, steps, warmup)
+    nbytes, flops = ssd_alg(cfg)
+    t = ev * 1e-3
+    chunk_len = mh.ssd_chunk_len(cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups,
+                                 cfg.dtype, chunk)
+    t_roof = max(nbytes / PEAK_HBM, flops / PEAK_BF16)
+    res = dict(mtok_s=cfg.batch * cfg.seqlen / t / 1e6, us_per_step=ev * 1e3, wall_us_per_step=wall * 1e3,
+               alg_bytes=nbytes, alg_flops=flops, hbm_GBs=nbytes / t / 1e9, tflops=flops / t / 1e12,
+               roofline_frac=t_roof / t, chunk_len=chunk_len)
+    del plans
+    torch.cuda.empty_cache()
+    return res, wall, ev
+
+
+def bench_decode(cfg, steps, warmup, nsets):
+    import mamformer_amd as mh
+    from mamformer_amd import workloads as W
+
+    plans = []
+    for i in range(nsets):
+        inp = W.decode_inputs(cfg.scaled(seed=cfg.seed + 1000 * i), device="cuda")
+        plans.append(mh.plan_selective_state_update(inp["state"], inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"],
+                                                    inp["D"], dt_bias=inp["dt_bias"], dt_softplus=True))
+    wall, ev = time_plans(plans, steps, warmup)
+    nbytes = decode_alg(cfg)
+    t = ev * 1e-3
+    res = dict(us_per_step=ev * 1e3, alg_bytes=nbytes, hbm_GBs=nbytes / t / 1e9, roofline_frac=nbytes / PEAK_HBM / t,
+               wall_us_per_step=wall * 1e3)
+    del plans
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_kda(cfg, steps, warmup):
+    import mamformer_amd as mh
+    from mamformer_amd import workloads as W
+
+    inp = W.kda_inputs(cfg, device="cuda")
+    plan = mh.plan_linear_attn_scan(inp["q1"], inp["q2"], inp["k"], inp["v"], g=inp["g"], lam=inp["lam"],
+                                    return_final_state=True)
+    wall, ev = time_plans([plan], steps, warmup)
+    nbytes, flops = kda_alg(cfg)
+    t = ev * 1e-3
+    res = dict(mtok_s=cfg.batch * cfg.seqlen / t / 1e6, us_per_step=ev * 1e3, alg_bytes=nbytes, alg_flops=flops,
+               hbm_GBs=nbytes / t / 1e9, roofline_frac=max(nbytes / PEAK_HBM, flops / PEAK_BF16) / t)
+    del plan, inp
+    torch.cuda.empty_cache()
+    return res
+
+
+# ----------------------------------------------------------------- CPU baseline (reference algorithm on the host)
+
+def cpu_baseline(cfg, sample_len):
+    from mamformer_amd import workloads as W
+    from oracle import baseline as BL
+
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    inp = W.ssd_inputs(cfg.scaled(seqlen=sample_len))
+    x4, dt, A, B, C, D = (inp[k] for k in ("x", "dt", "A", "B", "C", "D"))
+    BL.ssd_prefill_sample(x4[:, :16], dt[:, :16], A, B[:, :16], C[:, :16], D)      # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        BL.ssd_prefill_sample(x4, dt, A, B, C, D)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    return dict(value=cfg.batch * sample_len / t / 1e6, unit="Mtok/s", cores=cores, kind="port",
+                sample=(f"{cfg.name} full width (b{cfg.batch} d_inner {cfg.nheads * cfg.headdim} N{cfg.dstate}), "
+                        f"first {sample_len} of {cfg.seqlen} tokens, fp32, median of 3 runs ({t:.2f} s each); "
+                        f"torch {torch.__version__} threads={torch.get_num_threads()}"))
+
+
+# ----------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only (no decode / ssd4 / kda5 / cpu legs)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=512)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU (--gpus {args.gpus} requested); the scan path has no "
+              "multi-GPU mode here -- see DESIGN.md for how it would shard.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    from mamformer_amd import workloads as W
+
+    torch.cuda.set_device(0)
+    cfg = W.SSD2
+    log(f"ssd2 headline: {args.steps} steps after {args.warmup} warmup, 3 rotating buffer sets")
+    head, wall, ev = bench_ssd(cfg, args.steps, args.warmup, nsets=3)
+    log(f"ssd2: {head['mtok_s']:.1f} Mtok/s, {head['us_per_step']:.1f} us/step, roofline {head['roofline_frac']:.3f}")
+    out = {
+        "metric": METRIC,
+        "value": round(head["mtok_s"], 3),
+        "unit": "Mtok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded recipes of mamformer_amd/workloads.py, drawn on the GPU)",
+        "config": {"workload": "ssd2: 1b-shape SSD chunked-scan prefill, b2 L4096 nheads64 headdim64 dstate128 "
+                               "ngroups1, bf16 x/B/C/y, fp32 dt/A/D and final state",
+                   "batch": cfg.batch, "seqlen": cfg.seqlen, "nheads": cfg.nheads, "headdim": cfg.headdim,
+                   "dstate": cfg.dstate, "ngroups": cfg.ngroups, "chunk_len": head["chunk_len"],
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(head["hbm_GBs"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                     "frac": round(head["hbm_GBs"] / (PEAK_HBM / 1e9), 4), "traffic": None,
+                     "kernel": "mh_ssd_chunk_scan_fwd (ssd_chunk_state + ssd_state_pass + ssd_chunk_scan)",
+                     "alg_bytes_per_launch": head["alg_bytes"], "alg_flops_per_launch": head["alg_flops"],
+                     "launch_us": round(head["us_per_step"], 2),
+                     "mfma_frac": round(head["alg_flops"] / (head["us_per_step"] * 1e-6) / PEAK_BF16, 4)},
+    }
+    if not args.quick:
+        dec = {}
+        for b in (64, 256):
+            c = W.DEC3.scaled(batch=b)
+            r = bench_decode(c, max(args.steps, 50), args.warmup, nsets=3 if b == 64 else 2)
+            log(f"decode B={b}: {r['hbm_GBs']:.0f} GB/s ({r['roofline_frac']:.3f} of 8 TB/s), {r['us_per_step']:.1f} us")
+            dec[f"dec3_b{b}"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        out["decode"] = dec
+        other = {}
+        r, _, _ = bench_ssd(W.SSD4, max(5, args.steps // 10), 3, nsets=1)
+        log(f"ssd4: {r['mtok_s']:.1f} Mtok/s, {r['us_per_step']:.0f} us, roofline {r['roofline_frac']:.3f}")
+        other["ssd4"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        r = bench_kda(W.KDA5, max(5, args.steps // 5), 3)
+        log(f"kda5: {r['mtok_s']:.1f} Mtok/s, {r['us_per_step']:.0f} us, roofline {r['roofline_frac']:.3f}")
+        other["kda5"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        r, _, _ = bench_ssd(W.SSD1, args.steps, args.warmup, nsets=1, chunk=64)
+        other["ssd1"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        out["other"] = other
+    if not args.no_cpu and not args.quick:
+        log(f"cpu baseline: reference prefill on {args.cpu_sample} tokens of ssd2")
+        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_sample)
+        log(f"cpu: {out['cpu_baseline']['value']:.4f} Mtok/s")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

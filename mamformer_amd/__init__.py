@@ -6,6 +6,8 @@ prefill), ``selective_state_update`` / ``recurrent_step`` (decode step) and
 ``libmamformer_hip.so`` (build with ``python -m mamformer_amd.build``).
 """
 
-from .ops import linear_attn_scan, recurrent_step, selective_scan, selective_state_update, ssd_chunk_len
+from .ops import (Plan, linear_attn_scan, plan_linear_attn_scan, plan_selective_scan, plan_selective_state_update,
+                  recurrent_step, selective_scan, selective_state_update, ssd_chunk_len)
 
-__all__ = ["selective_scan", "selective_state_update", "recurrent_step", "linear_attn_scan", "ssd_chunk_len"]
+__all__ = ["selective_scan", "selective_state_update", "recurrent_step", "linear_attn_scan", "ssd_chunk_len",
+           "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan"]

@@ -75,7 +75,9 @@ int ssd_validate(const mh_ssd_args* a, int64_t* chunk_len_out) {
     return fail(MH_ERR_SHAPE, "ssd: chunk_len %lld must be a positive multiple of 64", (long long)a->chunk_len);
   if ((a->flags & MH_DT_LIMIT) && !(a->dt_min <= a->dt_max))
     return fail(MH_ERR_SHAPE, "ssd: dt_min > dt_max");
-  if (!a->x || !a->dt || !a->A || !a->B || !a->C || !a->y) return fail(MH_ERR_NULL, "ssd: x, dt, A, B, C, y are required");
+  if (!a->A) return fail(MH_ERR_NULL, "ssd: A is required");
+  if (a->seqlen > 0 && (!a->x || !a->dt || !a->B || !a->C || !a->y))
+    return fail(MH_ERR_NULL, "ssd: x, dt, A, B, C, y are required");
   if (!aligned16(a->x) || !aligned16(a->B) || !aligned16(a->C) || !aligned16(a->y))
     return fail(MH_ERR_ALIGN, "ssd: x, B, C, y must be 16-byte aligned");
   if (!stride_ok(a->x_stride_b, es) || !stride_ok(a->x_stride_l, es) || !stride_ok(a->x_stride_h, es) ||

@@ -33,7 +33,7 @@ from . import _lib
 from ._lib import SsdArgs, SsuArgs, KdaArgs
 
 __all__ = ["selective_scan", "selective_state_update", "recurrent_step", "linear_attn_scan",
-           "ssd_chunk_len"]
+           "ssd_chunk_len", "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan"]
 
 _DT = {torch.float32: _lib.MH_F32, torch.bfloat16: _lib.MH_BF16}
 
@@ -115,8 +115,35 @@ def ssd_chunk_len(batch, seqlen, nheads, headdim, dstate, ngroups, dtype=torch.b
     return out.value
 
 
+class Plan:
+    """A validated launch of one op on fixed device buffers.
+
+    Calling the plan re-runs the op on the same buffers (inputs may be
+    overwritten in place between calls) with no allocation and no Python-side
+    checks -- for serving loops, graph capture and benchmarking.  Outputs are
+    attributes (``y``, ``final_state``, ``o``...).  The plan keeps every buffer
+    it references alive.
+    """
+
+    def __init__(self, fn, args, device, keep=(), **outputs):
+        self._fn, self._args, self._device, self._keep = fn, args, device, keep
+        self.__dict__.update(outputs)
+
+    def __call__(self, stream=None):
+        s = _stream(self._device) if stream is None else ct.c_void_p(stream)
+        _lib.call(self._fn, ct.byref(self._args), s)
+        return self
+
+
+def plan_selective_scan(*args, **kw):
+    """Validate and allocate once; returns a ``Plan`` whose call launches ``selective_scan`` (outputs ``y``,
+    ``final_state``)."""
+    return selective_scan(*args, _plan_only=True, **kw)
+
+
 def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=False, *,
-                   chunk_size=None, initial_state=None, dt_bias=None, dt_softplus=False, dt_limit=None):
+                   chunk_size=None, initial_state=None, dt_bias=None, dt_softplus=False, dt_limit=None,
+                   _plan_only=False):
     """Mamba-2 SSD chunked-scan prefill.  Drop-in for ``selective_scan`` (R/mamformer/layers/mamba2.py:31-67).
 
     Args (SSD convention; see module docstring):
@@ -186,15 +213,28 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
     _lib.call("mh_ssd_workspace_bytes", ct.byref(args), ct.byref(nbytes))
     ws = torch.empty(max(int(nbytes.value), 16), device=x.device, dtype=torch.uint8)
     args.workspace, args.workspace_bytes = _ptr(ws), nbytes.value
-    _lib.call("mh_ssd_chunk_scan_fwd", ct.byref(args), _stream(x.device))
     y = y4.view(x.shape) if x.dim() == 3 else y4
+    if fin is not None and x.dim() == 3:
+        fin_out = fin.view(b, H * P, N)
+    else:
+        fin_out = fin
+    plan = Plan("mh_ssd_chunk_scan_fwd", args, x.device,
+                keep=(x4, dt32, A32, B4, C4, D32, bias32, h0, y4, fin, ws), y=y, final_state=fin_out)
+    if _plan_only:
+        return plan
+    plan()
     if not return_final_state:
         return y
-    return y, (fin.view(b, H * P, N) if x.dim() == 3 else fin)
+    return y, fin_out
+
+
+def plan_selective_state_update(*args, **kw):
+    """``Plan`` of ``selective_state_update`` on fixed buffers (output ``y``; the state is updated per call)."""
+    return selective_state_update(*args, _plan_only=True, **kw)
 
 
 def selective_state_update(state, x, dt, A, B, C, D=None, *, dt_bias=None, dt_softplus=True, dt_limit=None,
-                           out_state=None):
+                           out_state=None, _plan_only=False):
     """One-token SSD state update on the GPU, in place by default.
 
     state (b, H, P, N) fp32 (updated in place unless ``out_state`` is given);
@@ -257,7 +297,10 @@ def selective_state_update(state, x, dt, A, B, C, D=None, *, dt_bias=None, dt_so
     a.C, a.C_stride_b = _ptr(Cs), Cs.stride(0)
     a.D, a.dt_bias = _ptr(D32), _ptr(bias32)
     a.y, a.y_stride_b = _ptr(y), y.stride(0)
-    _lib.call("mh_ssd_state_update", ct.byref(a), _stream(x.device))
+    plan = Plan("mh_ssd_state_update", a, x.device, keep=(state, dst, xs, dt32, A32, Bs, Cs, D32, bias32), y=y)
+    if _plan_only:
+        return plan
+    plan()
     return y
 
 
@@ -285,8 +328,13 @@ def recurrent_step(x, dt, B, C, h_prev, A, D, *, dt_bias=None, dt_softplus=False
     return y.reshape(b, 1, d_inner), out.view(b, d_inner, N)
 
 
+def plan_linear_attn_scan(*args, **kw):
+    """``Plan`` of ``linear_attn_scan`` on fixed buffers (outputs ``o``, ``final_state``)."""
+    return linear_attn_scan(*args, _plan_only=True, **kw)
+
+
 def linear_attn_scan(q1, q2, k, v, *, g=None, lam=0.8, mode="gated", kernel_dim=None, initial_state=None,
-                     return_final_state=False, chunk_size=64):
+                     return_final_state=False, chunk_size=64, _plan_only=False):
     """KDA linear-attention chunked scan on the GPU, layout (B, H, S, D) as the reference (kda_diff.py:270-273).
 
     mode="gated": S_t = diag(exp(g_t)) S_{t-1} + k_t^T v_t, o_t = q1_t S_t - lam q2_t S_t
@@ -337,5 +385,8 @@ def linear_attn_scan(q1, q2, k, v, *, g=None, lam=0.8, mode="gated", kernel_dim=
     a.q1, a.q2, a.k, a.v, a.g = _ptr(q1c), _ptr(q2c), _ptr(kc), _ptr(vc), _ptr(gc)
     a.initial_state, a.final_state = _ptr(s0), _ptr(fin)
     a.o = _ptr(o)
-    _lib.call("mh_kda_chunk_scan_fwd", ct.byref(a), _stream(q1.device))
+    plan = Plan("mh_kda_chunk_scan_fwd", a, q1.device, keep=(q1c, q2c, kc, vc, gc, lam_h, s0), o=o, final_state=fin)
+    if _plan_only:
+        return plan
+    plan()
     return (o, fin) if return_final_state else o

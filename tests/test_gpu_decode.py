@@ -83,7 +83,7 @@ def test_prefill_then_decode_matches_longer_prefill():
         ys.append(mh.selective_state_update(st, d["x"][:, t], d["dt"][:, t], d["A"], d["B"][:, t], d["C"][:, t],
                                             d["D"], dt_softplus=False))
     check("decoded y", torch.stack(ys, 1), host(y_full[:, -m:]), 1e-2)
-    check("state", st, host(f_full), 1e-3)
+    check("state", st, host(f_full), 1e-2)
 
 
 def test_recurrent_step_wrapper_returns_new_state():
