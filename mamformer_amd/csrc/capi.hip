@@ -36,8 +36,9 @@ constexpr int64_t kMaxDim = (int64_t)1 << 30;
 
 int ssd_heads_per_wg(const mh_ssd_args* a) {
   const int64_t hpg = a->nheads / a->ngroups;
-  int hg = 4;
-  if (a->dtype == MH_F32 && a->dstate == 128) hg = 2;
+  // fp32 tiles with N = 128 are twice the bf16 size: one head per workgroup
+  // keeps the running state and operands in registers.
+  int hg = (a->dtype == MH_F32 && a->dstate == 128) ? 1 : 4;
   while (hg > 1 && (hpg % hg) != 0) hg >>= 1;
   return hg;
 }
@@ -45,7 +46,7 @@ int ssd_heads_per_wg(const mh_ssd_args* a) {
 int64_t ssd_auto_chunk(const mh_ssd_args* a) {
   const int64_t hg = ssd_heads_per_wg(a);
   const int64_t units = a->batch * (a->nheads / hg);           // workgroups per chunk index
-  const int64_t target = 512;                                   // ~2 workgroups per CU on 256 CUs
+  const int64_t target = 256;                                   // one 8-wave workgroup per CU on 256 CUs
   int64_t want = (a->seqlen * units + target - 1) / target;     // tokens per workgroup
   want = ((want + 63) / 64) * 64;
   if (want < 256) want = 256;
