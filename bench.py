@@ -17,7 +17,8 @@ a step from the previous one.  The same JSON line carries:
 * ``decode`` -- selective state update at B=64 and B=256 (HBM GB/s vs 8 TB/s).
 * ``other`` -- ssd4 (128K prefill with state carry) and kda5 (gated KDA scan).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu] [--only LEGS]
+                       [--copy-calibration BYTES]
 """
 
 from __future__ import annotations
@@ -178,7 +179,41 @@ def cpu_baseline(cfg, sample_len):
                         f"torch {torch.__version__} threads={torch.get_num_threads()}"))
 
 
+# ----------------------------------------------------------------- HBM traffic calibration
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def copy_calibration(nbytes, reps=5):
+    """A plain device copy of `nbytes` (read nbytes + write nbytes), run `reps` times.
+
+    Run under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` next to the scan
+    kernels, its counters give the KiB-per-byte scale used to turn the scan
+    kernels' counter readings into HBM bytes.
+    """
+    n = nbytes // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: {reps} x {nbytes} bytes")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline op from the committed PMC summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t.get("ssd2")
+    except (OSError, ValueError):
+        return None
+
+
 # ----------------------------------------------------------------- main
+
+LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd1", "cpu")
+
 
 def main():
     ap = argparse.ArgumentParser()
@@ -187,31 +222,44 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only (no decode / ssd4 / kda5 / cpu legs)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None,
+                    help=f"comma-separated legs to run, of {','.join(LEGS)} (profiling); the JSON line then carries "
+                         "only those")
     ap.add_argument("--cpu-sample", type=int, default=512)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="first run a plain device copy of BYTES (HBM counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (--gpus {args.gpus} requested); the scan path has no "
-              "multi-GPU mode here -- see DESIGN.md for how it would shard.", file=sys.stderr)
+              "multi-GPU mode here (each GPU would take its own share of heads or batch).", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.only:
+        legs = set(args.only.split(","))
+        bad = legs - set(LEGS)
+        if bad:
+            ap.error(f"unknown legs {sorted(bad)}")
+    elif args.quick:
+        legs = {"ssd2"}
+    else:
+        legs = set(LEGS) - ({"cpu"} if args.no_cpu else set())
 
     from mamformer_amd import workloads as W
 
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
     cfg = W.SSD2
-    log(f"ssd2 headline: {args.steps} steps after {args.warmup} warmup, 3 rotating buffer sets")
-    head, wall, ev = bench_ssd(cfg, args.steps, args.warmup, nsets=3)
-    log(f"ssd2: {head['mtok_s']:.1f} Mtok/s, {head['us_per_step']:.1f} us/step, roofline {head['roofline_frac']:.3f}")
     out = {
         "metric": METRIC,
-        "value": round(head["mtok_s"], 3),
+        "value": None,
         "unit": "Mtok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall, 5),
+        "ms_per_step": None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -220,16 +268,29 @@ def main():
         "config": {"workload": "ssd2: 1b-shape SSD chunked-scan prefill, b2 L4096 nheads64 headdim64 dstate128 "
                                "ngroups1, bf16 x/B/C/y, fp32 dt/A/D and final state",
                    "batch": cfg.batch, "seqlen": cfg.seqlen, "nheads": cfg.nheads, "headdim": cfg.headdim,
-                   "dstate": cfg.dstate, "ngroups": cfg.ngroups, "chunk_len": head["chunk_len"],
-                   "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(head["hbm_GBs"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                     "frac": round(head["hbm_GBs"] / (PEAK_HBM / 1e9), 4), "traffic": None,
-                     "kernel": "mh_ssd_chunk_scan_fwd (ssd_chunk_state + ssd_state_pass + ssd_chunk_scan)",
-                     "alg_bytes_per_launch": head["alg_bytes"], "alg_flops_per_launch": head["alg_flops"],
-                     "launch_us": round(head["us_per_step"], 2),
-                     "mfma_frac": round(head["alg_flops"] / (head["us_per_step"] * 1e-6) / PEAK_BF16, 4)},
+                   "dstate": cfg.dstate, "ngroups": cfg.ngroups, "parallelism": "single GPU"},
     }
-    if not args.quick:
+    if "ssd2" in legs:
+        log(f"ssd2 headline: {args.steps} steps after {args.warmup} warmup, 3 rotating buffer sets")
+        head, wall, ev = bench_ssd(cfg, args.steps, args.warmup, nsets=3)
+        log(f"ssd2: {head['mtok_s']:.1f} Mtok/s, {head['us_per_step']:.1f} us/step, "
+            f"roofline {head['roofline_frac']:.3f}")
+        out["value"] = round(head["mtok_s"], 3)
+        out["ms_per_step"] = round(wall, 5)
+        out["config"]["chunk_len"] = head["chunk_len"]
+        tr = measured_traffic()
+        out["roofline"] = {
+            "bound": "hbm", "achieved": round(head["hbm_GBs"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+            "frac": round(head["hbm_GBs"] / (PEAK_HBM / 1e9), 4),
+            "traffic": None if tr is None else tr["bytes_per_launch"],
+            "kernel": "mh_ssd_chunk_scan_fwd (ssd_chunk_state + ssd_state_pass + ssd_chunk_scan)",
+            "alg_bytes_per_launch": head["alg_bytes"], "alg_flops_per_launch": head["alg_flops"],
+            "launch_us": round(head["us_per_step"], 2),
+            "mfma_frac": round(head["alg_flops"] / (head["us_per_step"] * 1e-6) / PEAK_BF16, 4),
+        }
+        if tr is not None:
+            out["roofline"]["traffic_source"] = tr.get("source")
+    if "decode" in legs:
         dec = {}
         for b in (64, 256):
             c = W.DEC3.scaled(batch=b)
@@ -237,17 +298,21 @@ def main():
             log(f"decode B={b}: {r['hbm_GBs']:.0f} GB/s ({r['roofline_frac']:.3f} of 8 TB/s), {r['us_per_step']:.1f} us")
             dec[f"dec3_b{b}"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
         out["decode"] = dec
-        other = {}
+    other = {}
+    if "ssd4" in legs:
         r, _, _ = bench_ssd(W.SSD4, max(5, args.steps // 10), 3, nsets=1)
         log(f"ssd4: {r['mtok_s']:.1f} Mtok/s, {r['us_per_step']:.0f} us, roofline {r['roofline_frac']:.3f}")
         other["ssd4"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+    if "kda5" in legs:
         r = bench_kda(W.KDA5, max(5, args.steps // 5), 3)
         log(f"kda5: {r['mtok_s']:.1f} Mtok/s, {r['us_per_step']:.0f} us, roofline {r['roofline_frac']:.3f}")
         other["kda5"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+    if "ssd1" in legs:
         r, _, _ = bench_ssd(W.SSD1, args.steps, args.warmup, nsets=1, chunk=64)
         other["ssd1"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+    if other:
         out["other"] = other
-    if not args.no_cpu and not args.quick:
+    if "cpu" in legs:
         log(f"cpu baseline: reference prefill on {args.cpu_sample} tokens of ssd2")
         out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_sample)
         log(f"cpu: {out['cpu_baseline']['value']:.4f} Mtok/s")
