@@ -76,11 +76,19 @@ def kda_alg(cfg):
 # ----------------------------------------------------------------- timing
 
 def time_plans(plans, steps, warmup):
-    """Warm up, then time exactly `steps` launches cycling through `plans`.
+    """Spin up the clocks, warm up `warmup` launches, then time exactly `steps` launches cycling through `plans`.
 
     Returns (wall ms/step, HIP-event ms/step).  Events are recorded on the
     current torch stream, which is the stream the plans launch on.
     """
+    # bring the GPU to its working clocks first (about 0.3 s of the same launches), then the W warmup steps
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < 0.3:
+        plans[i % len(plans)]()
+        i += 1
+        if i % 16 == 0:
+            torch.cuda.synchronize()
     for i in range(warmup):
         plans[i % len(plans)]()
     torch.cuda.synchronize()

@@ -7,64 +7,77 @@
 // (with A_log, dt, D in the per-head SSD convention; see the oracle's bridge).
 //
 // Bandwidth-bound: the fp32 state is read once and written once; everything
-// else is a few KB.  One workgroup of 256 threads per (b, h): each thread owns
-// a 16-byte column slice (4 states) of N/4-thread rows and walks P/(1024/N)
-// rows with all loads issued before any arithmetic so that up to eight
-// 16-byte loads per thread are in flight.  The dot product over N is a
-// shuffle reduction inside the N/4 lanes that share a row.
+// else is a few KB.  One workgroup per (b, h) of up to 1024 threads: each
+// thread owns a 16-byte column slice (4 states) of ROWS state rows spaced
+// blockDim/(N/4) rows apart.  The state loads are issued first (nontemporal:
+// the state is touched once per step), the small per-head operands (dt, B, C,
+// x) after them so their latency hides under the state traffic.  The dot
+// product over N is a shuffle reduction inside the N/4 lanes that share a row.
 #include "common.h"
 #include "launch.h"
 
 namespace mh {
 
+constexpr int SSU_ROWS = 2;   // state rows per thread per pass
+
 template <int N, typename T>
-__global__ __launch_bounds__(256) void ssu_kernel(SsuParams p) {
+__global__ __launch_bounds__(1024) void ssu_kernel(SsuParams p) {
   constexpr int TPR = N / 4;        // threads per state row
-  constexpr int RP = 256 / TPR;     // rows per pass
-  constexpr int UNROLL = 8;
+  const int rp = blockDim.x / TPR;  // rows per pass
   const int bh = blockIdx.x;
   const int b = bh / p.nheads;
   const int h = bh - b * p.nheads;
   const int g = h / (p.nheads / p.ngroups);
   const int ln = threadIdx.x % TPR;
   const int row0 = threadIdx.x / TPR;
+  const int P = p.headdim;
+
+  const int64_t sbase = ((int64_t)b * p.nheads + h) * P * N;
+  const f32x4* sin = reinterpret_cast<const f32x4*>(p.state_in + sbase);
+  f32x4* sout = reinterpret_cast<f32x4*>(p.state_out + sbase);
+  const T* xp = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_stride_b + (int64_t)h * P;
+  T* yp = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_stride_b + (int64_t)h * P;
+
+  // Loads use row indices clamped into [0, P) so they are straight-line code
+  // (no per-row branches, hence no early waits); only the stores are guarded.
+  f32x4 s[SSU_ROWS];
+  float xv[SSU_ROWS], dv[SSU_ROWS];
+  const float* Dc = (p.D && p.D_per_channel) ? p.D + (int64_t)h * P : nullptr;
+  auto load = [&](int pbase) {
+#pragma unroll
+    for (int i = 0; i < SSU_ROWS; ++i) s[i] = __builtin_nontemporal_load(&sin[min(pbase + i * rp, P - 1) * TPR + ln]);
+#pragma unroll
+    for (int i = 0; i < SSU_ROWS; ++i) xv[i] = to_f32(xp[min(pbase + i * rp, P - 1)]);
+    if (Dc) {
+#pragma unroll
+      for (int i = 0; i < SSU_ROWS; ++i) dv[i] = Dc[min(pbase + i * rp, P - 1)];
+    }
+  };
+  load(row0);
 
   float dt = p.dt[(int64_t)b * p.dt_stride_b + h];
-  if (p.dt_bias) dt += p.dt_bias[h];
-  if (p.dt_softplus) dt = softplus_f(dt);
-  if (p.has_dt_limit) dt = fminf(fmaxf(dt, p.dt_min), p.dt_max);
-  const float a = __expf(p.A[h] * dt);
-
   const T* Bp = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_stride_b + (int64_t)g * N + ln * 4;
   const T* Cp = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_stride_b + (int64_t)g * N + ln * 4;
   float Bv[4], Cv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    Bv[i] = to_f32(Bp[i]) * dt;
+    Bv[i] = to_f32(Bp[i]);
     Cv[i] = to_f32(Cp[i]);
   }
-  const T* xp = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_stride_b + (int64_t)h * p.headdim;
-  T* yp = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_stride_b + (int64_t)h * p.headdim;
-  const int64_t sbase = ((int64_t)b * p.nheads + h) * p.headdim * N;
-  const f32x4* sin = reinterpret_cast<const f32x4*>(p.state_in + sbase);
-  f32x4* sout = reinterpret_cast<f32x4*>(p.state_out + sbase);
-  const float Dh = p.D ? (p.D_per_channel ? 0.f : p.D[h]) : 0.f;
+  if (p.dt_bias) dt += p.dt_bias[h];
+  if (p.dt_softplus) dt = softplus_f(dt);
+  if (p.has_dt_limit) dt = fminf(fmaxf(dt, p.dt_min), p.dt_max);
+  const float a = __expf(p.A[h] * dt);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) Bv[i] *= dt;
+  const float Dh = (p.D && !p.D_per_channel) ? p.D[h] : 0.f;
 
-  for (int pbase = row0; pbase < p.headdim; pbase += RP * UNROLL) {
-    f32x4 s[UNROLL];
-    float xv[UNROLL];
+  for (int pbase = row0; pbase < P; pbase += rp * SSU_ROWS) {
+    if (pbase != row0) load(pbase);
 #pragma unroll
-    for (int i = 0; i < UNROLL; ++i) {
-      const int pr = pbase + i * RP;
-      if (pr < p.headdim) {
-        s[i] = __builtin_nontemporal_load(&sin[pr * TPR + ln]);
-        xv[i] = to_f32(xp[pr]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < UNROLL; ++i) {
-      const int pr = pbase + i * RP;
-      if (pr < p.headdim) {  // uniform within a row group
+    for (int i = 0; i < SSU_ROWS; ++i) {
+      const int pr = pbase + i * rp;
+      if (pr < P) {  // uniform within a row group
         f32x4 v = s[i];
 #pragma unroll
         for (int c = 0; c < 4; ++c) v[c] = a * v[c] + xv[i] * Bv[c];
@@ -72,10 +85,7 @@ __global__ __launch_bounds__(256) void ssu_kernel(SsuParams p) {
         float part = v[0] * Cv[0] + v[1] * Cv[1] + v[2] * Cv[2] + v[3] * Cv[3];
 #pragma unroll
         for (int off = TPR / 2; off > 0; off >>= 1) part += __shfl_xor(part, off, TPR);
-        if (ln == 0) {
-          const float dd = p.D ? (p.D_per_channel ? p.D[h * p.headdim + pr] : Dh) : 0.f;
-          yp[pr] = from_f32<T>(part + dd * xv[i]);
-        }
+        if (ln == 0) yp[pr] = from_f32<T>(part + (Dc ? dv[i] : Dh) * xv[i]);
       }
     }
   }
@@ -83,7 +93,12 @@ __global__ __launch_bounds__(256) void ssu_kernel(SsuParams p) {
 
 template <int N>
 static hipError_t launch_ssu_n(const SsuParams& p, hipStream_t st) {
-  dim3 grid((unsigned)(p.batch * p.nheads)), block(256);
+  constexpr int TPR = N / 4;
+  // rows per pass: enough to cover P in SSU_ROWS rows per thread, capped at 1024 threads
+  int rows = (p.headdim + SSU_ROWS - 1) / SSU_ROWS;
+  if (rows * TPR > 1024) rows = 1024 / TPR;
+  const int threads = ((rows * TPR + 63) / 64) * 64;   // whole waves; extra lanes fall past P
+  dim3 grid((unsigned)(p.batch * p.nheads)), block((unsigned)threads);
   if (p.dtype == DT_BF16)
     hipLaunchKernelGGL((ssu_kernel<N, bf16>), grid, block, 0, st, p);
   else
