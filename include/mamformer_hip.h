@@ -149,6 +149,37 @@ typedef struct {
 
 int mh_kda_chunk_scan_fwd(const mh_kda_args* a, void* stream);
 
+/* ------------------------------------------------------------------------
+ * One-token step of the reference-mode scan (KDA decode).
+ * Replaces LinearDiffAttention._linear_attention_recurrent
+ *   (mamformer/layers/kda_diff.py:564-605) together with the cache update of
+ *   a one-token forward (kda_diff.py:329-338):
+ *   S += phi(k)^T v, z += phi(k)  (state (B,H,dk,dv) fp32 and z (B,H,dk) fp32, in place),
+ *   o_i = phi(q_i) S / (phi(q_i) z + 1e-8);  o = (o1 - lam o2) / (1 - lam + 1e-8) when o2 is NULL
+ *   and q2 is given, else o = o1 (and o2 = o2 when given).
+ *   q1/q2/k (B,H,dk), v/o/o2 (B,H,dv), contiguous.  flags: MH_KDA_PHI applies
+ *   phi(x) = elu(x)+1 to the first kernel_dim channels of q/k (0 beyond); without
+ *   it q/k are taken as already feature-mapped (the reference's calling form).
+ *   Supported: dv in {64, 128, 256}, dk <= 16384 / dv.
+ * ---------------------------------------------------------------------- */
+enum { MH_KDA_PHI = 1 };
+
+typedef struct {
+  int64_t batch, nheads, dk, dv;
+  int32_t dtype;
+  int32_t flags;
+  int32_t kernel_dim;
+  float lam;
+  const float* lam_per_head;
+  const void* q1; const void* q2; const void* k; const void* v;
+  float* state;
+  float* z;
+  void* o;
+  void* o2;
+} mh_kda_step_args;
+
+int mh_kda_recurrent_step(const mh_kda_step_args* a, void* stream);
+
 /* ------------------------------------------------------------------------ */
 int mh_abi_version(void);
 const char* mh_last_error(void);

@@ -6,8 +6,13 @@ prefill), ``selective_state_update`` / ``recurrent_step`` (decode step) and
 ``libmamformer_hip.so`` (build with ``python -m mamformer_amd.build``).
 """
 
-from .ops import (Plan, linear_attn_scan, plan_linear_attn_scan, plan_selective_scan, plan_selective_state_update,
-                  recurrent_step, selective_scan, selective_state_update, ssd_chunk_len)
+from .ops import (Plan, diff_lambda, linear_attention_recurrent, linear_attention_scan, linear_attn_scan,
+                  linear_attn_scan_pair, linear_attn_scan_single, linear_attn_step, plan_linear_attn_scan,
+                  plan_linear_attn_step, plan_selective_scan, plan_selective_state_update, recurrent_step,
+                  selective_scan, selective_state_update, ssd_chunk_len)
 
-__all__ = ["selective_scan", "selective_state_update", "recurrent_step", "linear_attn_scan", "ssd_chunk_len",
-           "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan"]
+__all__ = ["selective_scan", "selective_state_update", "recurrent_step", "linear_attn_scan",
+           "linear_attn_scan_pair", "linear_attn_scan_single", "linear_attention_scan", "diff_lambda",
+           "linear_attn_step", "linear_attention_recurrent",
+           "ssd_chunk_len", "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan",
+           "plan_linear_attn_step"]

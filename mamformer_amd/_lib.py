@@ -17,6 +17,7 @@ ABI_VERSION = 1
 MH_F32, MH_BF16 = 0, 1
 MH_DT_SOFTPLUS, MH_DT_LIMIT, MH_D_PER_CHANNEL = 1, 2, 4
 MH_KDA_GATED, MH_KDA_REFERENCE = 0, 1
+MH_KDA_PHI = 1
 
 ERRORS = {
     -1: "MH_ERR_NULL", -2: "MH_ERR_SHAPE", -3: "MH_ERR_DTYPE", -4: "MH_ERR_STRIDE",
@@ -71,12 +72,23 @@ class KdaArgs(ct.Structure):
     ]
 
 
+class KdaStepArgs(ct.Structure):
+    _fields_ = [
+        ("batch", _i64), ("nheads", _i64), ("dk", _i64), ("dv", _i64),
+        ("dtype", _i32), ("flags", _i32), ("kernel_dim", _i32), ("lam", _f32),
+        ("lam_per_head", _vp),
+        ("q1", _vp), ("q2", _vp), ("k", _vp), ("v", _vp),
+        ("state", _vp), ("z", _vp), ("o", _vp), ("o2", _vp),
+    ]
+
+
 # every symbol include/mamformer_hip.h declares
 EXPORTS = (
     "mh_abi_version", "mh_last_error",
     "mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
     "mh_ssd_state_update",
     "mh_kda_chunk_scan_fwd",
+    "mh_kda_recurrent_step",
 )
 
 _lock = threading.Lock()
@@ -110,8 +122,9 @@ def lib():
             h.mh_ssd_chunk_scan_fwd.argtypes = [ct.POINTER(SsdArgs), _vp]
             h.mh_ssd_state_update.argtypes = [ct.POINTER(SsuArgs), _vp]
             h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
+            h.mh_kda_recurrent_step.argtypes = [ct.POINTER(KdaStepArgs), _vp]
             for name in ("mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
-                         "mh_ssd_state_update", "mh_kda_chunk_scan_fwd"):
+                         "mh_ssd_state_update", "mh_kda_chunk_scan_fwd", "mh_kda_recurrent_step"):
                 getattr(h, name).restype = ct.c_int
             ver = h.mh_abi_version()
             if ver != ABI_VERSION:

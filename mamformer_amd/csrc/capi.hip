@@ -137,19 +137,36 @@ int kda_validate(const mh_kda_args* a) {
   if (a->batch * a->nheads > 0x7fffffffLL || a->seqlen > kMaxDim) return fail(MH_ERR_SHAPE, "kda: sizes out of range");
   if (!elem_size(a->dtype)) return fail(MH_ERR_DTYPE, "kda: unknown dtype %d", a->dtype);
   if (a->dtype != MH_BF16) return fail(MH_ERR_UNSUPPORTED, "kda: only bf16 q/k/v/o are supported");
-  if (a->mode != MH_KDA_GATED) return fail(MH_ERR_UNSUPPORTED, "kda: reference mode is not built yet");
   if (a->mode != MH_KDA_GATED && a->mode != MH_KDA_REFERENCE) return fail(MH_ERR_UNSUPPORTED, "kda: unknown mode %d", a->mode);
   if (a->dk != 128 || a->dv != 128)
     return fail(MH_ERR_UNSUPPORTED, "kda: dk=%lld dv=%lld not supported (128, 128)", (long long)a->dk, (long long)a->dv);
   if (!a->q1 || !a->k || !a->v || !a->o) return fail(MH_ERR_NULL, "kda: q1, k, v, o are required");
-  if (!a->q2 && a->mode == MH_KDA_REFERENCE) return fail(MH_ERR_NULL, "kda: reference mode needs q2");
   if (a->mode == MH_KDA_REFERENCE) {
-    if (!a->o2) return fail(MH_ERR_NULL, "kda: reference mode writes o1 and o2");
     if (a->kernel_dim <= 0) return fail(MH_ERR_SHAPE, "kda: kernel_dim must be positive");
+    if (a->g) return fail(MH_ERR_SHAPE, "kda: reference mode takes no gate g");
+    if (!a->q2 && a->o2) return fail(MH_ERR_NULL, "kda: o2 given without q2");
+  } else {
+    if (a->o2 || a->initial_z || a->final_z) return fail(MH_ERR_SHAPE, "kda: o2 / initial_z / final_z are reference-mode outputs");
   }
   if (!aligned16(a->q1) || (a->q2 && !aligned16(a->q2)) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o) ||
       (a->o2 && !aligned16(a->o2)) || (a->g && !aligned16(a->g)))
     return fail(MH_ERR_ALIGN, "kda: tensors must be 16-byte aligned");
+  return MH_OK;
+}
+
+int kda_step_validate(const mh_kda_step_args* a) {
+  if (!a) return fail(MH_ERR_NULL, "kda_step: args is NULL");
+  if (a->batch <= 0 || a->nheads <= 0 || a->dk <= 0 || a->dv <= 0) return fail(MH_ERR_SHAPE, "kda_step: sizes must be positive");
+  if (a->batch * a->nheads > 0x7fffffffLL) return fail(MH_ERR_SHAPE, "kda_step: sizes out of range");
+  if (!elem_size(a->dtype)) return fail(MH_ERR_DTYPE, "kda_step: unknown dtype %d", a->dtype);
+  if (a->dv != 64 && a->dv != 128 && a->dv != 256)
+    return fail(MH_ERR_UNSUPPORTED, "kda_step: dv %lld not supported (64, 128, 256)", (long long)a->dv);
+  if (a->dk > 16384 / a->dv) return fail(MH_ERR_UNSUPPORTED, "kda_step: dk %lld > %lld", (long long)a->dk, (long long)(16384 / a->dv));
+  if ((a->flags & MH_KDA_PHI) && a->kernel_dim <= 0) return fail(MH_ERR_SHAPE, "kda_step: kernel_dim must be positive");
+  if (!a->q1 || !a->k || !a->v || !a->state || !a->z || !a->o)
+    return fail(MH_ERR_NULL, "kda_step: q1, k, v, state, z, o are required");
+  if (!a->q2 && a->o2) return fail(MH_ERR_NULL, "kda_step: o2 given without q2");
+  if (!aligned16(a->state)) return fail(MH_ERR_ALIGN, "kda_step: state must be 16-byte aligned");
   return MH_OK;
 }
 
@@ -244,6 +261,20 @@ int mh_kda_chunk_scan_fwd(const mh_kda_args* a, void* stream) {
   p.final_state = a->final_state; p.final_z = a->final_z;
   p.o = a->o; p.o2 = a->o2;
   return hip_status(mh::launch_kda(p, reinterpret_cast<hipStream_t>(stream)), "kda_chunk_scan_fwd");
+}
+
+int mh_kda_recurrent_step(const mh_kda_step_args* a, void* stream) {
+  int rc = kda_step_validate(a);
+  if (rc) return rc;
+  mh::KdaStepParams p;
+  memset(&p, 0, sizeof(p));
+  p.batch = (int)a->batch; p.nheads = (int)a->nheads; p.dk = (int)a->dk; p.dv = (int)a->dv; p.dtype = a->dtype;
+  p.apply_phi = (a->flags & MH_KDA_PHI) != 0;
+  p.kernel_dim = p.apply_phi ? (a->kernel_dim < (int32_t)a->dk ? a->kernel_dim : (int32_t)a->dk) : (int)a->dk;
+  p.lam = a->lam; p.lam_h = a->lam_per_head;
+  p.q1 = a->q1; p.q2 = a->q2; p.k = a->k; p.v = a->v;
+  p.state = a->state; p.z = a->z; p.o = a->o; p.o2 = a->o2;
+  return hip_status(mh::launch_kda_step(p, reinterpret_cast<hipStream_t>(stream)), "kda_recurrent_step");
 }
 
 }  // extern "C"

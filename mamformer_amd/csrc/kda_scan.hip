@@ -1,4 +1,6 @@
-// KDA decay-gated linear-attention chunked scan for gfx950.
+// KDA linear-attention chunked scans for gfx950: the decay-gated operator
+// (kda_gated_kernel) and the reference's normalised phi-kernel scan
+// (kda_ref_kernel, further below).
 //
 //   S_t = diag(exp(g_t)) S_{t-1} + k_t^T v_t          (S: dk x dv, fp32)
 //   o_t = (q1_t - lam q2_t) S_t                          (inclusive of token t)
@@ -302,18 +304,319 @@ __global__ __launch_bounds__(256) void kda_gated_kernel(KdaParams p) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Reference mode: the reference's normalised linear-attention scan
+// (LinearDiffAttention._linear_attention_scan, kda_diff.py:357-478, and the
+// Triton kernel it dispatches to, triton_ssd.py:121-181):
+//     phi(x) = elu(x) + 1 on the first kernel_dim channels (0 beyond, kda_diff.py:67-89)
+//     S_t = S_{t-1} + phi(k_t)^T v_t,   z_t = z_{t-1} + phi(k_t)            (inclusive of t)
+//     o_i,t = phi(q_i,t) S_t / (phi(q_i,t) z_t + 1e-8)                     (i = 1, 2)
+// Outputs: the pair (o1, o2); or, with o2 == NULL and two queries, the fused
+// differential combination (o1 - lam o2) / (1 - lam + 1e-8) (kda_diff.py:534-538);
+// or, with q2 == NULL, the single-query o1 (triton_ssd.py:184-257).
+// Same segment walk and wave split as the gated kernel with g = 0; the
+// normaliser is the row sum of the masked phi(q) phi(k)^T tile plus
+// phi(q) . z_prev, with z (fp32) kept in LDS.
+// ---------------------------------------------------------------------------
+namespace {
+
+__device__ __forceinline__ float phi1(float x) { return x > 0.f ? x + 1.f : __expf(x); }
+
+template <int NQ>
+struct KdaRefSmem {
+  static constexpr int PK = DK + 8;      // bf16 row pitch
+  static constexpr int PV = DVH + 8;
+  bf16 Q[NQ][SEGK * PK];                 // phi(q_i)
+  bf16 Kt[SEGK * PK];                    // phi(k), zero rows beyond the segment
+  bf16 V[SEGK * PV];                     // v[:, V-half], zero rows beyond the segment
+  float z[DK];                           // running sum of phi(k) before this segment
+  float zq[NQ][SEGK];                    // phi(q_i,t) . z
+  float nrm[NQ][3][32];                  // row sums of the masked A tiles
+  f32x16 red[2][NQ][2][64];              // k-half 1 read-out partials: vt, query, t-tile, lane
+  Frag<bf16> A[3 * NQ][2][64];           // masked A^T tiles as B-operand fragments (bf16 high part)
+  Frag<bf16> Alo[3 * NQ][2][64];         // ... and the bf16 rounding remainder (A = A + Alo to ~2^-17)
+};
+
+}  // namespace
+
+template <int NQ>
+__global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
+  __shared__ KdaRefSmem<NQ> sm;
+  using SM = KdaRefSmem<NQ>;
+  using TM = bf16;
+  const int nbh = p.batch * p.nheads;
+  int bh, vh;
+  const int L = blockIdx.x;
+  if ((nbh & 7) == 0) {               // keep both V-halves of a (b, h) on one XCD (ids congruent mod 8)
+    bh = (L & 7) | ((L >> 4) << 3);
+    vh = (L >> 3) & 1;
+  } else {
+    bh = L >> 1;
+    vh = L & 1;
+  }
+  const int h = bh % p.nheads;
+  const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
+  const int vt = w & 1, kh = w >> 1;
+  const int tid = threadIdx.x;
+  const int S = p.seqlen;
+  const int kd = p.kernel_dim;
+  const bool fuse_diff = (NQ == 2) && (p.o2 == nullptr);
+  const float lam = p.lam_h ? p.lam_h[h] : p.lam;
+  const float inv_1ml = 1.f / (1.f - lam + 1e-8f);
+  const int64_t rowbase = (int64_t)bh * S;
+  const bf16* qp[2] = {reinterpret_cast<const bf16*>(p.q1), reinterpret_cast<const bf16*>(p.q2)};
+  const bf16* kk = reinterpret_cast<const bf16*>(p.k);
+  const bf16* vv = reinterpret_cast<const bf16*>(p.v);
+  bf16* op[2] = {reinterpret_cast<bf16*>(p.o), reinterpret_cast<bf16*>(p.o2)};
+  const int v0 = vh * DVH;
+
+  f32x16 St[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    St[i] = zero16();
+    if (p.init_state) {
+      const float* s0 = p.init_state + (int64_t)bh * DK * 128;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 32 * (2 * kh + i) + acc_row(half, r);
+        St[i][r] = s0[kr * 128 + v0 + 32 * vt + l32];
+      }
+    }
+  }
+  if (tid < DK) sm.z[tid] = p.init_z ? p.init_z[(int64_t)bh * DK + tid] : 0.f;
+
+  for (int pos = 0; pos < S; pos += SEGK) {
+    const int len = min(SEGK, S - pos);
+    // ---- phase B: phi(q_i), phi(k), v tiles
+    for (int e = tid; e < SEGK * (DK / 8); e += 256) {
+      const int t = e >> 4, k0 = (e & 15) * 8;
+      const bool in = t < len;
+      const int64_t r = (rowbase + pos + min(t, len - 1)) * DK + k0;
+      const bf16x8 kv8 = *reinterpret_cast<const bf16x8*>(kk + r);
+      bf16x8 qv8[NQ];
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) qv8[i] = *reinterpret_cast<const bf16x8*>(qp[i] + r);
+      bf16x8 ko;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ko[j] = (bf16)((in && k0 + j < kd) ? phi1((float)kv8[j]) : 0.f);
+      *reinterpret_cast<bf16x8*>(&sm.Kt[t * SM::PK + k0]) = ko;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) {
+        bf16x8 qo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qo[j] = (bf16)((in && k0 + j < kd) ? phi1((float)qv8[i][j]) : 0.f);
+        *reinterpret_cast<bf16x8*>(&sm.Q[i][t * SM::PK + k0]) = qo;
+      }
+    }
+    for (int e = tid; e < SEGK * (DVH / 8); e += 256) {
+      const int t = e >> 3, c0 = (e & 7) * 8;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (t < len) val = *reinterpret_cast<const uint4*>(vv + (rowbase + pos + t) * 128 + v0 + c0);
+      *reinterpret_cast<uint4*>(&sm.V[t * SM::PV + c0]) = val;
+    }
+    __syncthreads();
+
+    // ---- phase B2: phi(q_i,t) . z_prev  (4 adjacent lanes per (query, token), 32 channels each)
+    for (int it = tid; it < NQ * SEGK * 4; it += 256) {
+      const int i = it / (SEGK * 4), t = (it >> 2) % SEGK, qq = it & 3;
+      const bf16* row = &sm.Q[i][t * SM::PK + 32 * qq];
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < 32; c += 8) {
+        const bf16x8 q8 = *reinterpret_cast<const bf16x8*>(row + c);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += (float)q8[j] * sm.z[32 * qq + c + j];
+      }
+      acc += __shfl_xor(acc, 1, 64);
+      acc += __shfl_xor(acc, 2, 64);
+      if (qq == 0) sm.zq[i][t] = acc;
+    }
+
+    // ---- phase C: masked A^T tiles (query, s-tile, t-tile) and their row sums
+    for (int ti = w; ti < 3 * NQ; ti += 4) {
+      const int qi = ti / 3, tile = ti - 3 * qi;
+      const int st = (tile == 2) ? 1 : 0, tt = (tile == 0) ? 0 : 1;
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int c = 0; c < DK / 16; ++c) {
+        Frag<TM> a, bb;
+        a.v = *reinterpret_cast<const bf16x8*>(&sm.Kt[(32 * st + l32) * SM::PK + 16 * c + 8 * half]);
+        bb.v = *reinterpret_cast<const bf16x8*>(&sm.Q[qi][(32 * tt + l32) * SM::PK + 16 * c + 8 * half]);
+        acc = mma(a, bb, acc);
+      }
+      const int tl = 32 * tt + l32;
+      float rs = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int s_ = 32 * st + acc_row(half, r);
+        if (!(s_ <= tl && s_ < len)) acc[r] = 0.f;
+        rs += acc[r];
+      }
+      rs += __shfl_xor(rs, 32, 64);
+      if (half == 0) sm.nrm[qi][tile][l32] = rs;
+      // The normaliser uses the fp32 row sums, so the weights that multiply v must carry
+      // more than bf16 precision or their rounding (independent per entry) does not cancel
+      // against it; the differential combination can amplify that by 1/(1 - lam) <= 100.
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        Frag<TM> hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float x = acc[8 * c + j];
+          hi.v[j] = (bf16)x;
+          lo.v[j] = (bf16)(x - (float)hi.v[j]);
+        }
+        sm.A[ti][c][l] = hi;
+        sm.Alo[ti][c][l] = lo;
+      }
+    }
+    __syncthreads();
+
+    // ---- z update (z_prev was consumed by phase B2 before the barrier)
+    {
+      const int kc = tid & 127, th = tid >> 7;
+      float zs = 0.f;
+      for (int t = th * 32; t < th * 32 + 32; ++t) zs += (float)sm.Kt[t * SM::PK + kc];
+      atomicAdd(&sm.z[kc], zs);
+    }
+
+    // ---- phase D: per wave (v-tile vt, k-half kh)
+    Frag<TM> vf[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vf[c].set(j, (float)sm.V[(16 * c + kset(half, j)) * SM::PV + 32 * vt + l32]);
+
+    f32x16 o[NQ][2];
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int kt = 2 * kh + i;
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const Frag<TM> sa = acc_to_frag<TM>(St[i], c);
+            Frag<TM> qb;
+            const bf16* row = &sm.Q[qi][(32 * tt + l32) * SM::PK + 32 * kt + 16 * c];
+            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + 4 * half);
+            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 8 + 4 * half);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { qb.v[j] = lo[j]; qb.v[4 + j] = hi[j]; }
+            acc = mma(sa, qb, acc);
+          }
+        }
+        o[qi][tt] = acc;
+      }
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) {
+      if (kh == 0) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          o[qi][0] = mma(vf[c], sm.A[3 * qi + 0][c][l], o[qi][0]);
+          o[qi][0] = mma(vf[c], sm.Alo[3 * qi + 0][c][l], o[qi][0]);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          o[qi][1] = mma(vf[c], sm.A[3 * qi + 1][c][l], o[qi][1]);
+          o[qi][1] = mma(vf[c], sm.Alo[3 * qi + 1][c][l], o[qi][1]);
+          o[qi][1] = mma(vf[2 + c], sm.A[3 * qi + 2][c][l], o[qi][1]);
+          o[qi][1] = mma(vf[2 + c], sm.Alo[3 * qi + 2][c][l], o[qi][1]);
+        }
+        sm.red[vt][qi][0][l] = o[qi][0];
+        sm.red[vt][qi][1][l] = o[qi][1];
+      }
+    }
+    // state update (no decay): S[k][v] += sum_s phi(k_s)[k] v_s[v]
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int kt = 2 * kh + i;
+      const int krow = 32 * kt + l32;
+      f32x16 acc = St[i];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        Frag<TM> kf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) kf.v[j] = sm.Kt[(16 * c + kset(half, j)) * SM::PK + krow];
+        acc = mma(kf, vf[c], acc);
+      }
+      St[i] = acc;
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int tl = 32 * tt + l32;
+        if (tl < len) {
+          float res[NQ][16];
+#pragma unroll
+          for (int qi = 0; qi < NQ; ++qi) {
+            const float nr = sm.zq[qi][tl] + (tt == 0 ? sm.nrm[qi][0][l32] : sm.nrm[qi][1][l32] + sm.nrm[qi][2][l32]);
+            const float inv = 1.f / (nr + 1e-8f);
+            const f32x16 other = sm.red[vt][qi][tt][l];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) res[qi][r] = (o[qi][tt][r] + other[r]) * inv;
+          }
+          if (fuse_diff) {
+            bf16* orow = op[0] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = (bf16)((res[0][r] - lam * res[NQ - 1][r]) * inv_1ml);
+          } else {
+#pragma unroll
+            for (int qi = 0; qi < NQ; ++qi) {
+              bf16* orow = op[qi] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
+#pragma unroll
+              for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = (bf16)res[qi][r];
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if (p.final_state) {
+    float* sf_out = p.final_state + (int64_t)bh * DK * 128;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 32 * (2 * kh + i) + acc_row(half, r);
+        sf_out[kr * 128 + v0 + 32 * vt + l32] = St[i][r];
+      }
+  }
+  if (p.final_z && vh == 0 && tid < DK) p.final_z[(int64_t)bh * DK + tid] = sm.z[tid];
+}
+
 hipError_t launch_kda(const KdaParams& p, hipStream_t st) {
-  if (p.mode != 0) return hipErrorInvalidValue;   // reference mode: not built yet
   const int nbh = p.batch * p.nheads;
   if (p.seqlen == 0) {
-    if (!p.final_state) return hipSuccess;
-    const size_t bytes = (size_t)nbh * DK * 128 * sizeof(float);
-    if (p.init_state) return hipMemcpyAsync(p.final_state, p.init_state, bytes, hipMemcpyDeviceToDevice, st);
-    return hipMemsetAsync(p.final_state, 0, bytes, st);
+    if (p.final_state) {
+      const size_t bytes = (size_t)nbh * DK * 128 * sizeof(float);
+      hipError_t e = p.init_state ? hipMemcpyAsync(p.final_state, p.init_state, bytes, hipMemcpyDeviceToDevice, st)
+                                  : hipMemsetAsync(p.final_state, 0, bytes, st);
+      if (e != hipSuccess) return e;
+    }
+    if (p.final_z) {
+      const size_t bytes = (size_t)nbh * DK * sizeof(float);
+      return p.init_z ? hipMemcpyAsync(p.final_z, p.init_z, bytes, hipMemcpyDeviceToDevice, st)
+                      : hipMemsetAsync(p.final_z, 0, bytes, st);
+    }
+    return hipSuccess;
   }
   if (p.dtype != DT_BF16) return hipErrorInvalidValue;
   dim3 grid((unsigned)(2 * nbh)), block(256);
-  hipLaunchKernelGGL((kda_gated_kernel<bf16, bf16>), grid, block, 0, st, p);
+  if (p.mode == 0) {
+    hipLaunchKernelGGL((kda_gated_kernel<bf16, bf16>), grid, block, 0, st, p);
+  } else if (p.q2) {
+    hipLaunchKernelGGL(kda_ref_kernel<2>, grid, block, 0, st, p);
+  } else {
+    hipLaunchKernelGGL(kda_ref_kernel<1>, grid, block, 0, st, p);
+  }
   return hipGetLastError();
 }
 

@@ -69,4 +69,19 @@ struct KdaParams {
 };
 hipError_t launch_kda(const KdaParams& p, hipStream_t st);
 
+// ------------------------------------------------------------- KDA one-token step
+struct KdaStepParams {
+  int batch, nheads, dk, dv, dtype;
+  int kernel_dim;            // phi applied to the first kernel_dim channels (apply_phi)
+  int apply_phi;             // 1: q/k are raw, apply phi in the kernel; 0: already feature-mapped
+  float lam;
+  const float* lam_h;
+  const void* q1; const void* q2; const void* k; const void* v;   // (B,H,dk) / (B,H,dv) contiguous
+  float* state;              // (B,H,dk,dv) fp32, in place
+  float* z;                  // (B,H,dk) fp32, in place
+  void* o;                   // (B,H,dv): fused diff output, or o1
+  void* o2;                  // optional o2 (pair)
+};
+hipError_t launch_kda_step(const KdaStepParams& p, hipStream_t st);
+
 }  // namespace mh

@@ -10,7 +10,13 @@ Reference functions replaced (``R`` = ``mamformer 671b/``):
 ``selective_scan``                      R/mamformer/layers/mamba2.py:31-67 (``_selective_scan_impl`` :70-130)
 ``recurrent_step``                      R/mamformer/layers/mamba2.py:407-458 (``Mamba2Block._recurrent_step``)
 ``selective_state_update``              in-place form of the same decode step (the state is updated in HBM)
-``linear_attn_scan``                    gated KDA scan of the benchmark configuration (no reference function)
+``linear_attn_scan``                    gated KDA scan of the benchmark configuration (no reference function);
+                                        ``mode="reference"``: the normalised phi-kernel scan below
+``linear_attn_scan_pair``               R/mamformer/kernels/triton_ssd.py:260-350 (``triton_linear_attn_scan``)
+``linear_attn_scan_single``             R/mamformer/kernels/triton_ssd.py:353-400 (``triton_linear_attn_scan_single``)
+``linear_attention_scan``               R/mamformer/layers/kda_diff.py:357-478 (``_linear_attention_scan``)
+``linear_attention_recurrent``          R/mamformer/layers/kda_diff.py:564-605 (``_linear_attention_recurrent``)
+``linear_attn_step``                    in-place form of the same step (fp32 state and z updated in HBM)
 =====================================  ====================================================================
 
 SSD convention.  The reference's scan uses a per-channel dt and a per-state
@@ -33,7 +39,10 @@ from . import _lib
 from ._lib import SsdArgs, SsuArgs, KdaArgs
 
 __all__ = ["selective_scan", "selective_state_update", "recurrent_step", "linear_attn_scan",
-           "ssd_chunk_len", "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan"]
+           "linear_attn_scan_pair", "linear_attn_scan_single", "linear_attention_scan", "diff_lambda",
+           "linear_attn_step", "linear_attention_recurrent",
+           "ssd_chunk_len", "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan",
+           "plan_linear_attn_step"]
 
 _DT = {torch.float32: _lib.MH_F32, torch.bfloat16: _lib.MH_BF16}
 
@@ -329,22 +338,37 @@ def recurrent_step(x, dt, B, C, h_prev, A, D, *, dt_bias=None, dt_softplus=False
 
 
 def plan_linear_attn_scan(*args, **kw):
-    """``Plan`` of ``linear_attn_scan`` on fixed buffers (outputs ``o``, ``final_state``)."""
+    """``Plan`` of ``linear_attn_scan`` on fixed buffers (outputs ``o``, ``o2``, ``final_state``, ``final_z``)."""
     return linear_attn_scan(*args, _plan_only=True, **kw)
 
 
+def diff_lambda(lambda_raw):
+    """lambda = min(sigmoid(lambda_raw), 0.99) per head (R/mamformer/layers/kda_diff.py:473-474)."""
+    return torch.clamp(torch.sigmoid(lambda_raw.to(torch.float32)), max=0.99)
+
+
 def linear_attn_scan(q1, q2, k, v, *, g=None, lam=0.8, mode="gated", kernel_dim=None, initial_state=None,
-                     return_final_state=False, chunk_size=64, _plan_only=False):
+                     initial_z=None, return_final_state=False, pair=False, chunk_size=64, _plan_only=False):
     """KDA linear-attention chunked scan on the GPU, layout (B, H, S, D) as the reference (kda_diff.py:270-273).
 
-    mode="gated": S_t = diag(exp(g_t)) S_{t-1} + k_t^T v_t, o_t = q1_t S_t - lam q2_t S_t
-        (g (B, H, S, dk) fp32 per-channel log-decay, or None for no decay; lam a float or (H,) tensor;
-        q2 may be None for a single query).  Returns o, or (o, final_state (B, H, dk, dv) fp32).
-    chunk_size: accepted for API compatibility; the kernel walks segments of <= 64 tokens.
+    mode="gated" (benchmark operator, no reference function):
+        S_t = diag(exp(g_t)) S_{t-1} + k_t^T v_t,  o_t = q1_t S_t - lam q2_t S_t
+        g (B, H, S, dk) fp32 per-channel log-decay or None (no decay); lam a float or (H,) tensor;
+        q2 may be None (single query).  Returns o, or (o, final_state (B, H, dk, dv) fp32).
+    mode="reference" (the reference's normalised scan, triton_ssd.py:121-181 / kda_diff.py:357-478):
+        phi(x) = elu(x) + 1 on the first ``kernel_dim`` channels;  S_t = S_{t-1} + phi(k_t)^T v_t,
+        z_t = z_{t-1} + phi(k_t),  o_i,t = phi(q_i,t) S_t / (phi(q_i,t) z_t + 1e-8).
+        ``pair=True`` returns (o1, o2) like ``triton_linear_attn_scan``; otherwise the differential
+        combination (o1 - lam o2) / (1 - lam + 1e-8) is fused into the kernel and returned as one tensor
+        (q2=None: the single-query o1).  ``initial_state`` (B, H, dk, dv) / ``initial_z`` (B, H, dk) seed the
+        accumulators (the reference always starts at zero); with ``return_final_state`` the result gains
+        (final_state, final_z).
+    chunk_size: accepted for API compatibility; the kernels walk segments of <= 64 tokens.
     """
-    if mode != "gated":
-        raise NotImplementedError(f"linear_attn_scan: mode {mode!r} is not implemented by the HIP path yet")
-    _require_cuda("linear_attn_scan", q1, q2, k, v, g, initial_state)
+    if mode not in ("gated", "reference"):
+        raise ValueError(f"linear_attn_scan: unknown mode {mode!r} (gated, reference)")
+    ref_mode = mode == "reference"
+    _require_cuda("linear_attn_scan", q1, q2, k, v, g, initial_state, initial_z)
     if q1.dim() != 4:
         raise ValueError("linear_attn_scan: q1 must be (B, H, S, dk)")
     Bb, H, S, dk = q1.shape
@@ -353,6 +377,10 @@ def linear_attn_scan(q1, q2, k, v, *, g=None, lam=0.8, mode="gated", kernel_dim=
         raise ValueError("linear_attn_scan: q1/q2/k must be (B, H, S, dk) and v (B, H, S, dv)")
     if q1.dtype not in _DT or any(t is not None and t.dtype != q1.dtype for t in (q2, k, v)):
         raise TypeError("linear_attn_scan: q1, q2, k, v must share a dtype")
+    if ref_mode and g is not None:
+        raise ValueError("linear_attn_scan: reference mode has no gate g")
+    if pair and (not ref_mode or q2 is None):
+        raise ValueError("linear_attn_scan: pair=True needs mode='reference' and two queries")
     q1c, kc, vc = q1.contiguous(), k.contiguous(), v.contiguous()
     q2c = q2.contiguous() if q2 is not None else None
     gc = None
@@ -368,25 +396,132 @@ def linear_attn_scan(q1, q2, k, v, *, g=None, lam=0.8, mode="gated", kernel_dim=
         lam_f = 0.0
     else:
         lam_f = float(lam)
-    s0 = None
+    s0 = z0 = None
     if initial_state is not None:
         if initial_state.numel() != Bb * H * dk * dv:
             raise ValueError("linear_attn_scan: initial_state must be (B, H, dk, dv)")
         s0 = initial_state.reshape(Bb, H, dk, dv).to(torch.float32).contiguous()
+    if initial_z is not None:
+        if not ref_mode or initial_z.numel() != Bb * H * dk:
+            raise ValueError("linear_attn_scan: initial_z (B, H, dk) is a reference-mode input")
+        z0 = initial_z.reshape(Bb, H, dk).to(torch.float32).contiguous()
     o = torch.empty((Bb, H, S, dv), device=q1.device, dtype=q1.dtype)
+    o2 = torch.empty((Bb, H, S, dv), device=q1.device, dtype=q1.dtype) if pair else None
     fin = torch.empty((Bb, H, dk, dv), device=q1.device, dtype=torch.float32) if return_final_state else None
+    finz = (torch.empty((Bb, H, dk), device=q1.device, dtype=torch.float32)
+            if (return_final_state and ref_mode) else None)
     a = KdaArgs()
     a.batch, a.nheads, a.seqlen, a.dk, a.dv = Bb, H, S, dk, dv
     a.dtype = _DT[q1.dtype]
-    a.mode = _lib.MH_KDA_GATED
-    a.kernel_dim = dk
+    a.mode = _lib.MH_KDA_REFERENCE if ref_mode else _lib.MH_KDA_GATED
+    a.kernel_dim = int(kernel_dim) if (ref_mode and kernel_dim is not None) else dk
     a.lam = lam_f
     a.lam_per_head = _ptr(lam_h)
     a.q1, a.q2, a.k, a.v, a.g = _ptr(q1c), _ptr(q2c), _ptr(kc), _ptr(vc), _ptr(gc)
     a.initial_state, a.final_state = _ptr(s0), _ptr(fin)
-    a.o = _ptr(o)
-    plan = Plan("mh_kda_chunk_scan_fwd", a, q1.device, keep=(q1c, q2c, kc, vc, gc, lam_h, s0), o=o, final_state=fin)
+    a.initial_z, a.final_z = _ptr(z0), _ptr(finz)
+    a.o, a.o2 = _ptr(o), _ptr(o2)
+    plan = Plan("mh_kda_chunk_scan_fwd", a, q1.device, keep=(q1c, q2c, kc, vc, gc, lam_h, s0, z0),
+                o=o, o2=o2, final_state=fin, final_z=finz)
     if _plan_only:
         return plan
     plan()
-    return (o, fin) if return_final_state else o
+    out = (o, o2) if pair else (o,)
+    if return_final_state:
+        out = out + ((fin, finz) if ref_mode else (fin,))
+    return out if len(out) > 1 else out[0]
+
+
+def linear_attn_scan_pair(q1, q2, k, v, kernel_dim, block_k=128, block_d=128, group_h=0):
+    """``triton_linear_attn_scan`` counterpart (R/mamformer/kernels/triton_ssd.py:260-350): raw q1, q2, k, v
+    (B, H, S, D) -> (o1, o2) of the phi(x)=elu(x)+1 normalised scan.  ``block_k``/``block_d``/``group_h`` are the
+    Triton tiling knobs, accepted and ignored (the HIP kernel's tiling is fixed)."""
+    return linear_attn_scan(q1, q2, k, v, mode="reference", kernel_dim=kernel_dim, pair=True)
+
+
+def linear_attn_scan_single(q, k, v, kernel_dim, block_k=128, block_d=128):
+    """``triton_linear_attn_scan_single`` counterpart (triton_ssd.py:353-400): one query stream -> o."""
+    return linear_attn_scan(q, None, k, v, mode="reference", kernel_dim=kernel_dim)
+
+
+def linear_attention_scan(q1, q2, k, v, kernel_dim, lambda_raw):
+    """``LinearDiffAttention._linear_attention_scan`` counterpart (R/mamformer/layers/kda_diff.py:357-478):
+    the normalised scan of both queries with the differential combination
+    (o1 - lam o2) / (1 - lam + 1e-8), lam = min(sigmoid(lambda_raw), 0.99) per head, fused into the kernel.
+    Starts from a zero state, as the reference does."""
+    return linear_attn_scan(q1, q2, k, v, mode="reference", kernel_dim=kernel_dim, lam=diff_lambda(lambda_raw))
+
+
+def plan_linear_attn_step(*args, **kw):
+    """``Plan`` of ``linear_attn_step`` on fixed buffers (output ``o``; state and z are updated per call)."""
+    return linear_attn_step(*args, _plan_only=True, **kw)
+
+
+def linear_attn_step(state, z, q1, q2, k, v, *, lam=0.8, kernel_dim=None, apply_phi=True, pair=False,
+                     _plan_only=False):
+    """One-token step of the reference-mode scan, updating ``state`` and ``z`` in place (KDA decode).
+
+    state (B, H, dk, dv) fp32 contiguous; z (B, H, dk) or (B, H, dk, 1) fp32 contiguous; q1, q2, k
+    (B, H, dk) or (B, H, 1, dk); v (B, H, dv) or (B, H, 1, dv).  ``apply_phi``: q/k are raw and
+    phi(x) = elu(x)+1 is applied to their first ``kernel_dim`` channels in the kernel (else they are already
+    feature-mapped).  Returns the differential output (o1 - lam o2) / (1 - lam + 1e-8) shaped like v
+    (q2=None: o1; ``pair=True``: (o1, o2)).  Semantics of ``_linear_attention_recurrent``
+    (R/mamformer/layers/kda_diff.py:564-605) with the cache update of kda_diff.py:329-338.
+    """
+    _require_cuda("linear_attn_step", state, z, q1, q2, k, v)
+    if state.dim() != 4 or state.dtype != torch.float32 or not state.is_contiguous():
+        raise ValueError("linear_attn_step: state must be a contiguous (B, H, dk, dv) float32 tensor")
+    Bb, H, dk, dv = state.shape
+    if z.dtype != torch.float32 or not z.is_contiguous() or z.numel() != Bb * H * dk:
+        raise ValueError("linear_attn_step: z must be a contiguous float32 (B, H, dk[, 1]) tensor")
+    if pair and q2 is None:
+        raise ValueError("linear_attn_step: pair=True needs q2")
+    if q1.dtype not in _DT or any(t is not None and t.dtype != q1.dtype for t in (q2, k, v)):
+        raise TypeError("linear_attn_step: q1, q2, k, v must share a dtype")
+
+    def rows(t, d, name):
+        if t is None:
+            return None
+        if t.numel() != Bb * H * d:
+            raise ValueError(f"linear_attn_step: {name} must hold B*H*{d} values (one token)")
+        return t.reshape(Bb, H, d).contiguous()
+
+    q1c, q2c, kc, vc = rows(q1, dk, "q1"), rows(q2, dk, "q2"), rows(k, dk, "k"), rows(v, dv, "v")
+    lam_h = None
+    if torch.is_tensor(lam):
+        lam_h = lam.to(device=state.device, dtype=torch.float32).reshape(-1).contiguous()
+        if lam_h.numel() != H:
+            raise ValueError("linear_attn_step: per-head lam must have H entries")
+        lam_f = 0.0
+    else:
+        lam_f = float(lam)
+    o = torch.empty((Bb, H, dv), device=state.device, dtype=q1.dtype)
+    o2 = torch.empty((Bb, H, dv), device=state.device, dtype=q1.dtype) if pair else None
+    a = _lib.KdaStepArgs()
+    a.batch, a.nheads, a.dk, a.dv = Bb, H, dk, dv
+    a.dtype = _DT[q1.dtype]
+    a.flags = _lib.MH_KDA_PHI if apply_phi else 0
+    a.kernel_dim = int(kernel_dim) if kernel_dim is not None else dk
+    a.lam = lam_f
+    a.lam_per_head = _ptr(lam_h)
+    a.q1, a.q2, a.k, a.v = _ptr(q1c), _ptr(q2c), _ptr(kc), _ptr(vc)
+    a.state, a.z = _ptr(state), _ptr(z)
+    a.o, a.o2 = _ptr(o), _ptr(o2)
+    plan = Plan("mh_kda_recurrent_step", a, state.device, keep=(state, z, q1c, q2c, kc, vc, lam_h), o=o, o2=o2)
+    if _plan_only:
+        return plan
+    plan()
+    shape = v.shape
+    return (o.view(shape), o2.view(shape)) if pair else o.view(shape)
+
+
+def linear_attention_recurrent(q1_phi, q2_phi, k_phi, v, S, z, lambda_raw):
+    """``LinearDiffAttention._linear_attention_recurrent`` counterpart (R/mamformer/layers/kda_diff.py:564-605).
+
+    q1_phi, q2_phi, k_phi (B, H, 1, K) already feature-mapped; v (B, H, 1, D); S (B, H, K, D); z (B, H, K, 1).
+    Returns the differential output (B, H, 1, D).  As in the reference, S and z are not modified (the step
+    runs on float32 copies); ``linear_attn_step`` is the in-place form for a float32 cache.
+    """
+    S32 = S.to(torch.float32).clone(memory_format=torch.contiguous_format)
+    z32 = z.to(torch.float32).clone(memory_format=torch.contiguous_format)
+    return linear_attn_step(S32, z32, q1_phi, q2_phi, k_phi, v, lam=diff_lambda(lambda_raw), apply_phi=False)

@@ -143,3 +143,55 @@ def test_chunk_len_auto_choice():
     assert mamformer_amd.ssd_chunk_len(2, 4096, 64, 64, 128, 1) % 64 == 0
     assert mamformer_amd.ssd_chunk_len(1, 131072, 128, 64, 128, 8) == 4096
     assert mamformer_amd.ssd_chunk_len(1, 512, 8, 64, 64, 1, chunk_size=128) == 128
+
+
+def test_kda_reference_mode_validation():
+    a = KdaArgs()
+    a.batch, a.nheads, a.seqlen, a.dk, a.dv = 1, 2, 10, 128, 128
+    a.dtype = _lib.MH_BF16
+    a.mode = _lib.MH_KDA_REFERENCE
+    a.q1 = a.k = a.v = a.o = ct.c_void_p(4096)
+    a.kernel_dim = 0
+    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -2          # kernel_dim must be positive
+    a.kernel_dim = 128
+    a.g = ct.c_void_p(4096)
+    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -2          # no gate in reference mode
+    a.g = None
+    a.o2 = ct.c_void_p(4096)
+    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -1          # o2 without q2
+    a.mode = 7
+    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -6
+    g = KdaArgs()
+    g.batch, g.nheads, g.seqlen, g.dk, g.dv = 1, 2, 10, 128, 128
+    g.dtype = _lib.MH_BF16
+    g.q1 = g.k = g.v = g.o = ct.c_void_p(4096)
+    g.final_z = ct.c_void_p(4096)
+    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(g), None) == -2          # z outputs belong to reference mode
+
+
+def _good_step():
+    a = _lib.KdaStepArgs()
+    a.batch, a.nheads, a.dk, a.dv = 2, 4, 128, 128
+    a.dtype = _lib.MH_BF16
+    a.flags = _lib.MH_KDA_PHI
+    a.kernel_dim = 128
+    a.q1 = a.q2 = a.k = a.v = a.o = ct.c_void_p(4096)
+    a.state = a.z = ct.c_void_p(8192)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("dv", 96, -6), ("dk", 256, -6), ("kernel_dim", 0, -2), ("dtype", 5, -3), ("batch", 0, -2),
+    ("state", None, -1), ("z", None, -1), ("q1", None, -1), ("state", 8196, -5),
+])
+def test_kda_step_rejects_bad_arguments(field, value, code):
+    a = _good_step()
+    setattr(a, field, ct.c_void_p(value) if field in ("state", "z", "q1") and value is not None else value)
+    assert _rc("mh_kda_recurrent_step", ct.byref(a), None) == code
+
+
+def test_kda_step_o2_needs_q2():
+    a = _good_step()
+    a.q2 = None
+    a.o2 = ct.c_void_p(4096)
+    assert _rc("mh_kda_recurrent_step", ct.byref(a), None) == -1
