@@ -8,25 +8,23 @@
 // cached sequence) and the final state returned for the decode cache.
 //
 // Decomposition (three launches on the caller's stream):
-//   1. ssd_chunk_state  grid (nchunks, H/HG, b): for each state chunk of
-//      `chunk_len` tokens the chunk-local final state
+//   1. ssd_chunk_state  grid (nchunks, H/HG, b): the chunk-local final state
 //          S_k[p, n] = sum_{s in k} exp(sum_{s<tau in k} A dt_tau) dt_s x_s[p] B_s[n]
-//      as an MFMA reduction over tokens, plus the chunk's total log-decay.
+//      and the chunk's total log-decay T_k, walking the chunk forwards in
+//      64-token segments with S in MFMA accumulators.
 //   2. ssd_state_pass   elementwise over (b, h, P*N): H_0 = h0, H_{k+1} = e^{T_k} H_k + S_k.
 //      Writes the *entering* state H_k over S_k and the final state.
-//   3. ssd_chunk_scan   grid (nchunks, H/HG, b): each head's state chunk is
-//      walked in segments of <= 64 tokens with the running state in MFMA
-//      accumulator registers, kept as H = e^kappa * Hs (Hs fp32, kappa a scalar).
-//      With cs the in-segment cumulative log-decay counted from just after the
-//      segment's first token (cs_0 = 0, first-token decay folded into kappa):
-//          xs_s = e^{-kappa - cs_s} dt_s x_s                      (one bf16 operand per token)
-//          Y    = [C B^T o causal mask] xs + C Hs^T                (MFMA; no per-segment state rescale)
-//          y_t  = e^{cs_t + kappa} Y_t + D x_t
-//          Hs  += B^T xs ;  kappa += cs_end
-//      exp(cs_t - cs_s) = e^{cs_t + kappa} e^{-kappa - cs_s} is exact; segments
-//      are cut so the spread of cs stays <= RANGE, and Hs is renormalised
-//      (Hs *= e^kappa, kappa = 0) whenever a factor would leave e^{+-RANGE}, so
-//      every intermediate stays finite for any decay.
+//   3. ssd_chunk_scan   grid (nchunks, H/HG, b): walks the chunk in 64-token
+//      segments with the running state H in MFMA accumulators.  With cs_t the
+//      in-segment inclusive cumulative log-decay (cs_t <= 0, non-increasing):
+//          y_t  = e^{cs_t} C_t H^T + sum_{s<=t} e^{cs_t - cs_s} (C_t . B_s) dt_s x_s + D x_t
+//          H   <- e^{cs_end} H + sum_s e^{cs_end - cs_s} dt_s x_s B_s^T
+//      Every factor of the state update is <= 1.  The intra-segment term is
+//      factorised as e^{cs_t - m} * e^{m - cs_s} around the midpoint m of the
+//      segment's log-decay range when that range is <= FACT_RANGE (both factors
+//      within e^{+-30}), so the masked C B^T tile is shared by all heads of a
+//      group; a segment with a wider range (very strong decay) takes an
+//      exact per-element e^{cs_t - cs_s} path instead (wave-uniform branch).
 // Work split: a workgroup owns HG heads of one group with two waves per head;
 // wave w handles head w / 2 and the 32 state columns p of half w % 2, so each
 // wave's state is N/32 accumulator tiles.  C B^T (three 32x32 tiles) and the
@@ -36,49 +34,23 @@
 // accumulator layout that the next MFMA consumes.
 // Memory: tiles of the next segment are fetched straight into a second LDS
 // buffer (global_load_lds_dwordx4, no register staging) while the current one
-// is computed; LDS tiles are XOR-swizzled per row for conflict-free fragment
-// reads; y is staged in LDS and written with 16-byte stores; the chunk-state
-// workspace is kept in MFMA fragment order (64 contiguous bytes per lane).
+// is computed.  Each wave owns the 32-column half of its head's x tile that it
+// reads, so it stages its y columns in place of x and writes them to HBM one
+// segment later, after the next segment's fetch has been issued: no wave ever
+// waits for its own y stores.  LDS tiles are XOR-swizzled per row for
+// conflict-free fragment reads; the chunk-state workspace is kept in MFMA
+// fragment order (64 contiguous bytes per lane).
 // bf16 I/O uses 32x32x16 bf16 MFMAs, fp32 I/O 32x32x2 fp32 MFMAs; accumulation is fp32.
 #include "common.h"
 #include "launch.h"
 
 namespace mh {
 
-constexpr int SEG = 64;          // tokens per segment (max)
-constexpr int HD = 64;           // headdim handled by these kernels
-constexpr float RANGE = 40.f;    // max spread of in-segment cumulative log-decay; renormalisation threshold
+constexpr int SEG = 64;              // tokens per segment
+constexpr int HD = 64;               // headdim handled by these kernels
+constexpr float FACT_RANGE = 60.f;   // max in-segment log-decay range of the factorised intra-segment path
 
-// ------------------------------------------------------------------ wave helpers
-
-// Reverse inclusive prefix sum over the 64 lanes: r_l = sum_{i >= l} v_i.
-__device__ __forceinline__ float wave_incl_rscan(float v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    float o = __shfl_down(v, off, 64);
-    if (l + off < 64) v += o;
-  }
-  return v;
-}
-__device__ __forceinline__ float wave_prefix_max(float v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    float o = __shfl_up(v, off, 64);
-    if (l >= off) v = fmaxf(v, o);
-  }
-  return v;
-}
-__device__ __forceinline__ float wave_prefix_min(float v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    float o = __shfl_up(v, off, 64);
-    if (l >= off) v = fminf(v, o);
-  }
-  return v;
-}
+// ------------------------------------------------------------------ helpers
 
 __device__ __forceinline__ float process_dt(const SsdParams& p, float dt, int h) {
   if (p.dt_bias) dt += p.dt_bias[h];
@@ -88,12 +60,16 @@ __device__ __forceinline__ float process_dt(const SsdParams& p, float dt, int h)
 }
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
 
 // ------------------------------------------------------------------ LDS tiles
 
-// Rows of W elements, unpadded, 16-byte chunks XOR-swizzled by row (chunk c of
-// row r lives at chunk c ^ (r & MASK)) so the lanes of one LDS access phase,
-// reading the same column of consecutive rows, hit distinct banks.
+// B / C tiles: SEG rows of W elements, unpadded, 16-byte chunks XOR-swizzled by
+// row (chunk c of row r lives at chunk c ^ (r & MASK)) so the lanes of one LDS
+// access phase, reading the same column of consecutive rows, hit distinct banks.
 template <typename T, int W>
 struct Tile {
   static constexpr int EPC = 16 / (int)sizeof(T);   // elements per 16-byte chunk
@@ -104,12 +80,27 @@ struct Tile {
   __device__ static __forceinline__ int chunk(int r, int c) { return r * W + (c ^ (r & MASK)) * EPC; }
 };
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
+// One wave's half of a head's x tile: SEG token rows x 32 columns.  Rows of 64
+// bytes (bf16) are swizzled with ((r >> 1) ^ (r >> 3)) & 3, which spreads the
+// 16-byte reads of 16 consecutive rows over all banks whether the LDS serves
+// 8 or 16 lanes of a 128-bit read per cycle; 128-byte rows (fp32) use r & 7.
+template <typename T>
+struct XHalf {
+  static constexpr int W = 32;
+  static constexpr int EPC = 16 / (int)sizeof(T);
+  static constexpr int CPR = W / EPC;               // 4 (bf16) / 8 (fp32)
+  static constexpr int RPB = 64 / CPR;              // 16 / 8 rows per 1 KB block
+  static constexpr int NBLK = SEG / RPB;            // 4 / 8 blocks
+  __device__ static __forceinline__ int swz(int r) {
+    if constexpr (CPR == 4) return ((r >> 1) ^ (r >> 3)) & 3;
+    else return r & 7;
+  }
+  __device__ static __forceinline__ int chunk(int r, int c) { return r * W + (c ^ swz(r)) * EPC; }
+};
 
 // Direct global -> LDS fetch of 1 KB blocks [blk0, blk0 + nblk) of a swizzled
-// tile: lane i of the wave writes LDS bytes [16 i, 16 i + 16) of the block, so
-// it fetches the logical chunk that the swizzle places there.  Rows past
+// B/C tile: lane i of the wave writes LDS bytes [16 i, 16 i + 16) of the block,
+// so it fetches the logical chunk that the swizzle places there.  Rows past
 // `last_tok` (end of the sequence) re-read the last valid row; their values
 // are finite and every consumer masks them.
 template <typename T, int W>
@@ -128,6 +119,42 @@ __device__ __forceinline__ void fetch_tile(T* dst, const T* src, int64_t row_str
   }
 }
 
+// Direct fetch of a wave's x half tile (src points at column 0 of the half).
+template <typename T>
+__device__ __forceinline__ void fetch_xhalf(T* dst, const T* src, int64_t row_stride, int tok0, int last_tok,
+                                            int lane) {
+  using X = XHalf<T>;
+  const int rr = lane / X::CPR, phys = lane % X::CPR;
+#pragma unroll
+  for (int blk = 0; blk < X::NBLK; ++blk) {
+    const int r = blk * X::RPB + rr;
+    const int c = phys ^ X::swz(r);
+    const int tok = min(tok0 + r, last_tok);
+    const T* g = src + (int64_t)tok * row_stride + c * X::EPC;
+    T* d = dst + blk * (1024 / (int)sizeof(T));
+    __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)d, 16, 0, 0);
+  }
+}
+
+// Write the y rows [0, len) staged in a wave's x half tile to HBM (16-byte stores).
+template <typename T>
+__device__ __forceinline__ void store_yhalf(T* dst, int64_t row_stride, const T* tile, int len, int lane) {
+  using X = XHalf<T>;
+  uint4 v[X::NBLK];
+#pragma unroll
+  for (int i = 0; i < X::NBLK; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = *reinterpret_cast<const uint4*>(tile + X::chunk(e / X::CPR, e % X::CPR));
+  }
+#pragma unroll
+  for (int i = 0; i < X::NBLK; ++i) {
+    const int e = lane + 64 * i;
+    const int r = e / X::CPR, c = e % X::CPR;
+    if (r < len) *reinterpret_cast<uint4*>(dst + (int64_t)r * row_stride + c * X::EPC) = v[i];
+  }
+  wait_lds();   // the staged rows have been read: the buffer may be refilled
+}
+
 // 8 consecutive elements of row r starting at column e0 (e0 % 8 == 0) as an MFMA fragment.
 template <typename TM, typename T, int W>
 __device__ __forceinline__ Frag<TM> row_frag(const T* tile, int r, int e0) {
@@ -137,6 +164,20 @@ __device__ __forceinline__ Frag<TM> row_frag(const T* tile, int r, int e0) {
   } else {
     const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + Tile<T, W>::chunk(r, e0 / 4));
     const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + Tile<T, W>::chunk(r, e0 / 4 + 1));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { f.v[j] = lo[j]; f.v[4 + j] = hi[j]; }
+  }
+  return f;
+}
+template <typename TM, typename T>
+__device__ __forceinline__ Frag<TM> xrow_frag(const T* tile, int r, int e0) {
+  using X = XHalf<T>;
+  Frag<TM> f;
+  if constexpr (sizeof(T) == 2) {
+    f.v = *reinterpret_cast<const bf16x8*>(tile + X::chunk(r, e0 / 8));
+  } else {
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + X::chunk(r, e0 / 4));
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + X::chunk(r, e0 / 4 + 1));
 #pragma unroll
     for (int j = 0; j < 4; ++j) { f.v[j] = lo[j]; f.v[4 + j] = hi[j]; }
   }
@@ -160,9 +201,9 @@ __device__ __forceinline__ Frag<TM> kset_frag(const T* tile, int r, int base, in
   return f;
 }
 
-// Per-token scale factors of the 8 tokens a KSET fragment covers (k-step c):
+// Values of a per-token array at the 8 tokens a KSET fragment covers (k-step c):
 // tokens 16c+4*half+{0..3} and 16c+8+4*half+{0..3}, read as two float4.
-__device__ __forceinline__ void kset_scales(const float* v, int c, int half, float (&s)[8]) {
+__device__ __forceinline__ void kset_vals(const float* v, int c, int half, float (&s)[8]) {
   const f32x4 lo = *reinterpret_cast<const f32x4*>(v + 16 * c + 4 * half);
   const f32x4 hi = *reinterpret_cast<const f32x4*>(v + 16 * c + 8 + 4 * half);
 #pragma unroll
@@ -179,7 +220,7 @@ __device__ __forceinline__ Frag<TM> ident_frag(int c, int half, int l32) {
   return f;
 }
 
-// Transpose a 32x32 block of a row-major LDS tile through the MFMA unit:
+// Transpose a 32x32 block of a row-major B tile through the MFMA unit:
 // returns the accumulator tile D[r][q] = tile[r0 + r][q0 + q] (r, q < 32), whose
 // lane l holds column q0 + (l % 32) and rows r0 + acc_row(half, i).
 template <typename TM, typename T, int W>
@@ -191,19 +232,27 @@ __device__ __forceinline__ f32x16 mfma_transpose(const T* tile, int r0, int q0, 
   return acc;
 }
 
-// x~^T fragments of one 32-column p-tile: lane = p, elements = tokens (KSET), each token scaled.
-template <typename TM, typename T>
-__device__ __forceinline__ void scaled_xt_frags(const T* xtile, int pt, const float* scale, const Frag<TM> (&id)[2],
-                                                int half, int l32, Frag<TM> (&xf)[4]) {
+// x^T of a wave's x half tile (lane = p, tokens on the k axis, KSET order) as
+// two sets of 4 fragments: xa scaled per token by sa[], xb scaled by sb[].
+template <typename TM, typename T, bool TWO>
+__device__ __forceinline__ void xt_frags(const T* xtile, const float* sa, const float* sb, const Frag<TM> (&id)[2],
+                                         int half, int l32, Frag<TM> (&xa)[4], Frag<TM> (&xb)[4]) {
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
-    const f32x16 xt = mfma_transpose<TM, T, HD>(xtile, 32 * st, 32 * pt, id, half, l32);
+    f32x16 xt = zero16();
+#pragma unroll
+    for (int c = 0; c < 2; ++c) xt = mma(xrow_frag<TM, T>(xtile, 32 * st + l32, 16 * c + 8 * half), id[c], xt);
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      float sc[8];
-      kset_scales(scale, 2 * st + c, half, sc);
+      float s[8];
+      kset_vals(sa, 2 * st + c, half, s);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) xf[2 * st + c].set(j, xt[8 * c + j] * sc[j]);
+      for (int j = 0; j < 8; ++j) xa[2 * st + c].set(j, xt[8 * c + j] * s[j]);
+      if constexpr (TWO) {
+        kset_vals(sb, 2 * st + c, half, s);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xb[2 * st + c].set(j, xt[8 * c + j] * s[j]);
+      }
     }
   }
 }
@@ -211,85 +260,75 @@ __device__ __forceinline__ void scaled_xt_frags(const T* xtile, int pt, const fl
 // Shared per-segment MFMA work of a workgroup of NW waves: the three C B^T
 // tiles (N/16 MFMAs each, k-reductions, one wave each) and the 2 * N/32 B^T
 // blocks (2 MFMAs each), spread so the busiest wave does one C B^T tile.
-template <int NW, int N>
+template <int NW, int N, bool CB>
 struct SharedWork {
   static constexpr int NBLK = 2 * (N / 32);
-  static constexpr int CBW = NW < 3 ? NW : 3;                   // waves that own C B^T tiles
-  static constexpr int BTW = NW > 3 ? NW - 3 : NW;              // waves that own B^T blocks
-  static constexpr int BTPER = (NBLK + BTW - 1) / BTW;
-  static constexpr int CBPER = (3 + CBW - 1) / CBW;
+  static constexpr int NCB = CB ? 3 : 0;
+  static constexpr int CBW = !CB ? 0 : (NW < 3 ? NW : 3);          // waves that own C B^T tiles
+  static constexpr int BTW = (NW > CBW) ? NW - CBW : NW;          // waves that own B^T blocks
+  static constexpr int BTP = (NBLK + BTW - 1) / BTW;
+  static constexpr int CBPER = CB ? (3 + CBW - 1) / CBW : 0;
   __device__ static __forceinline__ int cb_tile(int w, int i) { return (w < CBW) ? w + i * CBW : 99; }
   __device__ static __forceinline__ int bt_block(int w, int i) {
-    if (NW > 3) return (w >= 3) ? (w - 3) + i * BTW : 99;
+    if (NW > CBW) return (w >= CBW) ? (w - CBW) + i * BTW : 99;
     return w + i * NW;
   }
 };
 
-// B^T A-operand fragments (row n, k = token via KSET) of the B tile, computed
-// by the waves SharedWork assigns, in registers until the caller's barrier.
-template <typename T, typename TM, int N, int NW>
-struct BtWork {
-  using SW = SharedWork<NW, N>;
-  f32x16 acc[SW::BTPER];
-  __device__ __forceinline__ void compute(const T* Bs, int w, const Frag<TM> (&id)[2], int half, int l32) {
-#pragma unroll
-    for (int i = 0; i < SW::BTPER; ++i) {
-      const int blk = SW::bt_block(w, i);
-      if (blk < SW::NBLK) acc[i] = mfma_transpose<TM, T, N>(Bs, 32 * (blk & 1), 32 * (blk >> 1), id, half, l32);
-    }
-  }
-  __device__ __forceinline__ void store(Frag<TM> (*Bt)[4][64], int w, int l) const {
-#pragma unroll
-    for (int i = 0; i < SW::BTPER; ++i) {
-      const int blk = SW::bt_block(w, i);
-      if (blk < SW::NBLK) {
-        Bt[blk >> 1][2 * (blk & 1)][l] = acc_to_frag<TM>(acc[i], 0);
-        Bt[blk >> 1][2 * (blk & 1) + 1][l] = acc_to_frag<TM>(acc[i], 1);
-      }
-    }
-  }
+// B^T A-operand fragments (row n, k = token via KSET) of one segment, in LDS.
+template <typename TM, int N>
+struct BtFrags {
+  Frag<TM> f[N / 32][4][64];   // n-tile, k-step (16 tokens), lane
 };
 
-// One buffer of segment tiles.  The B tile is overwritten by its B^T fragments
-// once both have been read (same size: 64 x N elements).
-template <typename T, typename TM, int N, int HG>
-struct SegTiles {
-  union {
-    T B[SEG * N];
-    Frag<TM> Bt[N / 32][4][64];
-  };
+// Compute the B^T blocks a wave owns and store them as fragments.
+template <typename T, typename TM, int N, int NW, bool CB>
+__device__ __forceinline__ void bt_work(const T* Bs, BtFrags<TM, N>& bt, int w, const Frag<TM> (&id)[2], int half,
+                                        int l32, int l) {
+  using SW = SharedWork<NW, N, CB>;
+#pragma unroll
+  for (int i = 0; i < SW::BTP; ++i) {
+    const int blk = SW::bt_block(w, i);
+    if (blk < SW::NBLK) {
+      const f32x16 acc = mfma_transpose<TM, T, N>(Bs, 32 * (blk & 1), 32 * (blk >> 1), id, half, l32);
+      bt.f[blk >> 1][2 * (blk & 1)][l] = acc_to_frag<TM>(acc, 0);
+      bt.f[blk >> 1][2 * (blk & 1) + 1][l] = acc_to_frag<TM>(acc, 1);
+    }
+  }
+}
+
+// Per-stage tiles.
+template <typename T, int N, int HG>
+struct ScanStage {
+  T B[SEG * N];
   T C[SEG * N];
-  T X[HG][SEG * HD];
+  T X[2 * HG][SEG * 32];      // per wave: its half of its head's x tile (y staged in place)
 };
-template <typename T, typename TM, int N, int HG>
-struct StateTiles {
-  union {
-    T B[SEG * N];
-    Frag<TM> Bt[N / 32][4][64];
-  };
-  T X[HG][SEG * HD];
+template <typename T, int N, int HG>
+struct StateStage {
+  T B[SEG * N];
+  T X[2 * HG][SEG * 32];
 };
-static_assert(sizeof(Frag<bf16>) * (128 / 32) * 4 * 64 == sizeof(bf16) * SEG * 128, "Bt must alias B exactly");
-static_assert(sizeof(Frag<float>) * (128 / 32) * 4 * 64 == sizeof(float) * SEG * 128, "Bt must alias B exactly");
 
 template <typename T, typename TM, int N, int HG, int NBUF>
 struct ScanSmem {
-  SegTiles<T, TM, N, HG> buf[NBUF];
-  Frag<TM> CB[3][2][64];          // masked (C B^T)^T tiles as B-operand fragments: tile, k-step, lane
-  float cs[HG][SEG];              // log of the output row scale
-  float sa[HG][SEG];              // per-token operand scale
-  float dcol[HG][HD];             // D per column of each head (per-head D broadcast)
-  int len[HG];
+  ScanStage<T, N, HG> st[NBUF];
+  BtFrags<TM, N> bt;
+  Frag<TM> CB[3][2][64];      // masked (C B^T)^T tiles as B-operand fragments: tile, k-step, lane
+  float sa[2 * HG][SEG];      // per wave: operand scale of the intra-segment term
+  float sb[2 * HG][SEG];      // per wave: decay to the segment end, e^{cs_end - cs_s} (exact path)
+  float cs[2 * HG][SEG];      // per wave: in-segment cumulative log-decay
+  float dcol[HG][HD];         // D per column of each head
 };
 template <typename T, typename TM, int N, int HG, int NBUF>
 struct StateSmem {
-  StateTiles<T, TM, N, HG> buf[NBUF];
-  float w[HG][SEG];
+  StateStage<T, N, HG> st[NBUF];
+  BtFrags<TM, N> bt;
+  float sb[2 * HG][SEG];
 };
 
 // Tiles are double-buffered (the next segment fetched during this one's
-// compute) where two buffers fit in the 160 KB of LDS, else single-buffered
-// (fetched between segments).
+// compute) where two buffers fit in the 160 KB of LDS, else single-buffered.
 constexpr size_t LDS_BYTES = 160 * 1024;
 template <typename T, typename TM, int N, int HG>
 constexpr int scan_nbuf = sizeof(ScanSmem<T, TM, N, HG, 2>) <= LDS_BYTES ? 2 : 1;
@@ -299,20 +338,36 @@ constexpr int state_nbuf = sizeof(StateSmem<T, TM, N, HG, 2>) <= LDS_BYTES ? 2 :
 // Offset (floats) of state tile (nt, pt) element block of lane l in the fragment-native workspace order.
 __device__ __forceinline__ int frag_off(int nt, int pt, int l) { return ((nt * 2 + pt) * 64 + l) * 16; }
 
-// Fetch the B (and optionally C) tiles shared by the workgroup and the x tile
-// of each head (by that head's two waves) for the segment starting at tok0.
-template <typename T, int N, int NW>
-__device__ __forceinline__ void fetch_segment(T* Bs, T* Cs, T* Xs, const T* Bg, int64_t B_sl, const T* Cg,
-                                              int64_t C_sl, const T* xg, int64_t x_sl, int tok0, int last_tok,
-                                              int w, int ph, int l) {
-  using TB = Tile<T, N>;
-  using TX = Tile<T, HD>;
-  constexpr int BPW = (TB::NBLK + NW - 1) / NW;             // B/C blocks per wave
-  const int b0 = w * BPW, nb = max(0, min(BPW, TB::NBLK - b0));
-  fetch_tile<T, N>(Bs, Bg, B_sl, tok0, last_tok, b0, nb, l);
-  if (Cs) fetch_tile<T, N>(Cs, Cg, C_sl, tok0, last_tok, b0, nb, l);
-  constexpr int XPW = TX::NBLK / 2;                         // x blocks per wave (two waves per head)
-  fetch_tile<T, HD>(Xs, xg, x_sl, tok0, last_tok, ph * XPW, XPW, l);
+// In-segment decay of one head (lane = token of the segment starting at pos,
+// tokens at or past c1 have dt = 0): returns cs_t (inclusive cumulative log-decay).
+__device__ __forceinline__ float seg_decay(const SsdParams& p, float dtraw, int h, float Ah, int t, int c1,
+                                           float& dtv) {
+  dtv = (t < c1) ? process_dt(p, dtraw, h) : 0.f;
+  return wave_incl_scan(Ah * dtv);
+}
+
+// State read-out of one wave for one 32-token t-tile (rows tl of the C tile):
+// Y^T[p][t] += sum_n H[p][n] C^T[n][t], H as A operand straight from the accumulators.
+template <typename TM, typename T, int N>
+__device__ __forceinline__ void readout(const f32x16 (&H)[N / 32], const T* Cs, int tl, int half, f32x16& Y) {
+#pragma unroll
+  for (int nt = 0; nt < N / 32; ++nt)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) Y = mma(acc_to_frag<TM>(H[nt], c), kset_frag<TM, T, N>(Cs, tl, 32 * nt + 16 * c, half), Y);
+}
+
+// H[n][p] += sum_s B^T[n][s] xf[s][p] over the segment's 64 tokens.
+template <typename TM, int N>
+__device__ __forceinline__ void state_update(f32x16 (&H)[N / 32], const BtFrags<TM, N>& bt, const Frag<TM> (&xf)[4],
+                                             int l) {
+#pragma unroll
+  for (int nt = 0; nt < N / 32; ++nt) {
+    Frag<TM> btf[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) btf[c] = bt.f[nt][c][l];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) H[nt] = mma(btf[c], xf[c], H[nt]);
+  }
 }
 
 // ------------------------------------------------------------------ kernel 1
@@ -323,6 +378,8 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_state_kernel(SsdParams p) 
   using SM = StateSmem<T, TM, N, HG, NBUF>;
   __shared__ SM sm;
   constexpr int NT = N / 32, NW = 2 * HG;
+  using TB = Tile<T, N>;
+  constexpr int BPW = (TB::NBLK + NW - 1) / NW;            // B blocks fetched per wave
   const int k = blockIdx.x, b = blockIdx.z;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
   const int j = w >> 1, ph = w & 1;
@@ -330,74 +387,64 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_state_kernel(SsdParams p) 
   const int g = h / (p.nheads / p.ngroups);
   const int c0 = k * p.chunk_len;
   const int c1 = min(p.seqlen, c0 + p.chunk_len);
+  const int last = p.seqlen - 1;
   const float Ah = p.A[h];
-  const T* xg = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh;
+  const T* xg = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + 32 * ph;
   const T* Bg = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)g * N;
   const float* dtg = p.dt + (int64_t)b * p.dt_sb + h;
+  const int b0 = w * BPW, nb = max(0, min(BPW, TB::NBLK - b0));
   Frag<TM> id[2];
   id[0] = ident_frag<TM>(0, half, l32);
   id[1] = ident_frag<TM>(1, half, l32);
 
-  f32x16 acc[NT];
+  f32x16 S[NT];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) acc[nt] = zero16();
+  for (int nt = 0; nt < NT; ++nt) S[nt] = zero16();
+  float total = 0.f;
 
-  // Walk the chunk backwards so the decay to the chunk end is a running suffix
-  // sum; the previous segment's tiles are fetched while this one is reduced.
-  float suffix = 0.f;
   const int nseg = (c1 - c0 + SEG - 1) / SEG;
-  int cur = 0;
-  float dtraw = 0.f;
-  {
-    const int pos = c0 + (nseg - 1) * SEG;
-    fetch_segment<T, N, NW>(sm.buf[0].B, nullptr, sm.buf[0].X[j], Bg, p.B_sl, nullptr, 0, xg, p.x_sl, pos, c1 - 1,
-                            w, ph, l);
-    if (pos + l < c1) dtraw = dtg[(int64_t)(pos + l) * p.dt_sl];
-    wait_vmem();
-    __syncthreads();
-  }
-  for (int si = nseg - 1; si >= 0; --si) {
-    auto& bf = sm.buf[cur];
+  float dtraw = (c0 + l < c1) ? dtg[(int64_t)(c0 + l) * p.dt_sl] : 0.f;
+  fetch_tile<T, N>(sm.st[0].B, Bg, p.B_sl, c0, last, b0, nb, l);
+  fetch_xhalf<T>(sm.st[0].X[w], xg, p.x_sl, c0, last, l);
+  for (int si = 0; si < nseg; ++si) {
+    int lq = l;
+    asm volatile("" : "+v"(lq));
+    const int ll = lq, halfq = lq >> 5, l32q = lq & 31;
     const int pos = c0 + si * SEG;
-    const int t = pos + l;
-    const float dtv = (t < c1) ? process_dt(p, dtraw, h) : 0.f;
-    const float a = Ah * dtv;
-    const float rs = wave_incl_rscan(a);                 // sum_{i >= l} a_i within segment
-    float ex = __shfl_down(rs, 1, 64);                    // sum_{i > l}
-    if (l == 63) ex = 0.f;
-    if (ph == 0) sm.w[j][l] = __expf(ex + suffix) * dtv;
-    suffix += __shfl(rs, 0, 64);
-    if (si > 0) {                                          // fetch the previous segment
-      const int pp = pos - SEG;
-      if constexpr (NBUF == 2)
-        fetch_segment<T, N, NW>(sm.buf[cur ^ 1].B, nullptr, sm.buf[cur ^ 1].X[j], Bg, p.B_sl, nullptr, 0, xg,
-                                p.x_sl, pp, c1 - 1, w, ph, l);
-      dtraw = dtg[(int64_t)(pp + l) * p.dt_sl];
-    }
-    BtWork<T, TM, N, NW> bt;
-    bt.compute(bf.B, w, id, half, l32);
-    __syncthreads();
-    bt.store(bf.Bt, w, l);
-    __syncthreads();
-    Frag<TM> xf[4];
-    scaled_xt_frags<TM, T>(bf.X[j], ph, sm.w[j], id, half, l32, xf);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      Frag<TM> btf[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) btf[c] = bf.Bt[nt][c][l];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) acc[nt] = mma(btf[c], xf[c], acc[nt]);
-    }
+    const int cur = (NBUF == 2) ? (si & 1) : 0;
+    auto& sg = sm.st[cur];
     if constexpr (NBUF == 1) {
-      __syncthreads();
-      if (si > 0)
-        fetch_segment<T, N, NW>(sm.buf[0].B, nullptr, sm.buf[0].X[j], Bg, p.B_sl, nullptr, 0, xg, p.x_sl, pos - SEG,
-                                c1 - 1, w, ph, l);
+      if (si > 0) {
+        __syncthreads();                                   // every wave is done with the previous tiles
+        fetch_tile<T, N>(sg.B, Bg, p.B_sl, pos, last, b0, nb, ll);
+        fetch_xhalf<T>(sg.X[w], xg, p.x_sl, pos, last, ll);
+      }
     }
     wait_vmem();
-    __syncthreads();
-    cur ^= NBUF - 1;
+    __syncthreads();                                       // tiles of this segment are in LDS
+    float dtn = 0.f;
+    if constexpr (NBUF == 2) {
+      if (si + 1 < nseg) {                                 // fetch the next segment into the other buffer
+        auto& ng = sm.st[cur ^ 1];
+        fetch_tile<T, N>(ng.B, Bg, p.B_sl, pos + SEG, last, b0, nb, ll);
+        fetch_xhalf<T>(ng.X[w], xg, p.x_sl, pos + SEG, last, ll);
+      }
+    }
+    if (si + 1 < nseg && pos + SEG + l < c1) dtn = dtg[(int64_t)(pos + SEG + l) * p.dt_sl];
+    float dtv;
+    const float cs = seg_decay(p, dtraw, h, Ah, pos + l, c1, dtv);
+    const float cse = __shfl(cs, 63, 64);
+    sm.sb[w][ll] = __expf(cse - cs) * dtv;
+    bt_work<T, TM, N, NW, false>(sg.B, sm.bt, w, id, halfq, l32q, ll);
+    __syncthreads();                                       // B^T fragments and scales visible
+    Frag<TM> xw[4];
+    xt_frags<TM, T, false>(sg.X[w], sm.sb[w], nullptr, id, halfq, l32q, xw, xw);
+    const float e = __expf(cse);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) S[nt] *= e;
+    state_update<TM, N>(S, sm.bt, xw, ll);
+    total += cse;
+    dtraw = dtn;
   }
 
   float* out = p.chunk_states + (((int64_t)b * p.nchunks + k) * p.nheads + h) * (HD * N);
@@ -407,11 +454,11 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_state_kernel(SsdParams p) 
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       f32x4 v;
-      v[0] = acc[nt][4 * q]; v[1] = acc[nt][4 * q + 1]; v[2] = acc[nt][4 * q + 2]; v[3] = acc[nt][4 * q + 3];
+      v[0] = S[nt][4 * q]; v[1] = S[nt][4 * q + 1]; v[2] = S[nt][4 * q + 2]; v[3] = S[nt][4 * q + 3];
       o4[q] = v;
     }
   }
-  if (l == 0 && ph == 0) p.chunk_decay[((int64_t)b * p.nheads + h) * p.nchunks + k] = suffix;
+  if (l == 0 && ph == 0) p.chunk_decay[((int64_t)b * p.nheads + h) * p.nchunks + k] = total;
 }
 
 // ------------------------------------------------------------------ kernel 2
@@ -451,10 +498,12 @@ template <typename T, typename TM, int N, int HG>
 __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
   constexpr int NBUF = scan_nbuf<T, TM, N, HG>;
   using SM = ScanSmem<T, TM, N, HG, NBUF>;
-  using SW = SharedWork<2 * HG, N>;
-  using TX = Tile<T, HD>;
-  __shared__ SM sm;
   constexpr int NT = N / 32, NW = 2 * HG;
+  using SW = SharedWork<NW, N, true>;
+  using TB = Tile<T, N>;
+  using TX = XHalf<T>;
+  constexpr int BPW = (TB::NBLK + NW - 1) / NW;            // B and C blocks fetched per wave
+  __shared__ SM sm;
   const int k = blockIdx.x, b = blockIdx.z;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
   const int j = w >> 1, ph = w & 1;                       // head of the workgroup, 32-column half of P
@@ -464,19 +513,19 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
   const int c1 = min(p.seqlen, c0 + p.chunk_len);
   const int last = p.seqlen - 1;
   const float Ah = p.A[h];
-  const T* xg = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh;
+  const T* xg = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + 32 * ph;
   const T* Bg = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)g * N;
   const T* Cg = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb + (int64_t)g * N;
   const float* dtg = p.dt + (int64_t)b * p.dt_sb + h;
-  T* yg = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_sb + (int64_t)h * p.y_sh;
+  T* yg = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_sb + (int64_t)h * p.y_sh + 32 * ph;
+  const int b0 = w * BPW, nb = max(0, min(BPW, TB::NBLK - b0));
   Frag<TM> id[2];
   id[0] = ident_frag<TM>(0, half, l32);
   id[1] = ident_frag<TM>(1, half, l32);
   if (ph == 0) sm.dcol[j][l] = p.D ? (p.D_per_channel ? p.D[h * HD + l] : p.D[h]) : 0.f;
 
-  // Entering state H_k (fragment-native workspace order), columns of this wave's P-half;
-  // H = e^kappa * Hs with kappa = 0.
-  f32x16 Hs[NT];
+  // Entering state H_k (fragment-native workspace order), columns of this wave's P-half.
+  f32x16 H[NT];
   {
     const float* hk = p.chunk_states + (((int64_t)b * p.nchunks + k) * p.nheads + h) * (HD * N);
 #pragma unroll
@@ -485,177 +534,182 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const f32x4 v = h4[q];
-        Hs[nt][4 * q] = v[0]; Hs[nt][4 * q + 1] = v[1]; Hs[nt][4 * q + 2] = v[2]; Hs[nt][4 * q + 3] = v[3];
+        H[nt][4 * q] = v[0]; H[nt][4 * q + 1] = v[1]; H[nt][4 * q + 2] = v[2]; H[nt][4 * q + 3] = v[3];
       }
     }
   }
-  float kappa = 0.f;
 
-  int cur = 0;
+  const int nseg = (c1 - c0 + SEG - 1) / SEG;
   float dtraw = (c0 + l < c1) ? dtg[(int64_t)(c0 + l) * p.dt_sl] : 0.f;
-  fetch_segment<T, N, NW>(sm.buf[0].B, sm.buf[0].C, sm.buf[0].X[j], Bg, p.B_sl, Cg, p.C_sl, xg, p.x_sl, c0, last,
-                          w, ph, l);
-  wait_vmem();
-  __syncthreads();
+  fetch_tile<T, N>(sm.st[0].B, Bg, p.B_sl, c0, last, b0, nb, l);
+  fetch_tile<T, N>(sm.st[0].C, Cg, p.C_sl, c0, last, b0, nb, l);
+  fetch_xhalf<T>(sm.st[0].X[w], xg, p.x_sl, c0, last, l);
 
-  for (int pos = c0; pos < c1;) {
-    auto& bf = sm.buf[cur];
-    // ---- dt, in-segment cumulative log-decay, longest admissible prefix (both waves of a head agree)
-    const int t = pos + l;
-    const float dtv = (t < c1) ? process_dt(p, dtraw, h) : 0.f;
-    const float csa = wave_incl_scan(Ah * dtv);            // includes token 0's own decay
-    const float pmax = wave_prefix_max(csa), pmin = wave_prefix_min(csa);
-    const bool ok = (pmax - pmin <= RANGE) && (t < c1);
-    const uint64_t bal = __ballot(ok);
-    const int len_w = (~bal == 0ull) ? 64 : __builtin_ctzll(~bal);
-    if (l == 0 && ph == 0) sm.len[j] = len_w;
-    __syncthreads();
-
-    int len = sm.len[0];
-#pragma unroll
-    for (int i = 1; i < HG; ++i) len = min(len, sm.len[i]);
-    const int next = pos + len;
-    if (next < c1) {                                       // fetch the next segment into the other buffer
-      if constexpr (NBUF == 2) {
-        auto& nb = sm.buf[cur ^ 1];
-        fetch_segment<T, N, NW>(nb.B, nb.C, nb.X[j], Bg, p.B_sl, Cg, p.C_sl, xg, p.x_sl, next, last, w, ph, l);
+  for (int si = 0; si < nseg; ++si) {
+    // Lane-dependent LDS addresses are recomputed each segment (cheap VALU) instead of
+    // being hoisted out of the loop, where they would all stay live and spill.
+    int lq = l;
+    asm volatile("" : "+v"(lq));
+    const int ll = lq, halfq = lq >> 5, l32q = lq & 31;
+    const int pos = c0 + si * SEG;
+    const int cur = (NBUF == 2) ? (si & 1) : 0;
+    auto& sg = sm.st[cur];
+    T* xt = sg.X[w];
+    if constexpr (NBUF == 1) {
+      if (si > 0) {
+        store_yhalf<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, xt, SEG, ll);   // y of the previous segment
+        __syncthreads();                                   // every wave is done with the previous tiles
+        fetch_tile<T, N>(sg.B, Bg, p.B_sl, pos, last, b0, nb, ll);
+        fetch_tile<T, N>(sg.C, Cg, p.C_sl, pos, last, b0, nb, ll);
+        fetch_xhalf<T>(xt, xg, p.x_sl, pos, last, ll);
       }
-      dtraw = (next + l < c1) ? dtg[(int64_t)(next + l) * p.dt_sl] : 0.f;
     }
-    const float a0 = __shfl(csa, 0, 64);
-    const float cs = csa - a0;                             // cs_0 = 0
-    const float csmax = __shfl(pmax, len - 1, 64) - a0, csmin = __shfl(pmin, len - 1, 64) - a0;
-    float ke = kappa + a0;                                 // kappa with token 0's decay applied
-    if (ke + csmin < -RANGE || ke + csmax > RANGE) {       // renormalise Hs (wave-uniform)
-      const float s = __expf(ke);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) Hs[nt] *= s;
-      ke = 0.f;
+    wait_vmem();
+    __syncthreads();                                       // tiles of this segment are in LDS
+    float dtn = 0.f;
+    if constexpr (NBUF == 2) {
+      auto& og = sm.st[cur ^ 1];
+      // y of the previous segment (staged in place of its x), then the next segment's fetch into the same buffer
+      if (si > 0) store_yhalf<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, og.X[w], SEG, ll);
+      if (si + 1 < nseg) {
+        fetch_tile<T, N>(og.B, Bg, p.B_sl, pos + SEG, last, b0, nb, ll);
+        fetch_tile<T, N>(og.C, Cg, p.C_sl, pos + SEG, last, b0, nb, ll);
+        fetch_xhalf<T>(og.X[w], xg, p.x_sl, pos + SEG, last, ll);
+      }
     }
-    if (ph == 0) {
-      sm.cs[j][l] = cs + ke;
-      sm.sa[j][l] = (l < len) ? __expf(-ke - cs) * dtv : 0.f;
-    }
+    if (si + 1 < nseg && pos + SEG + l < c1) dtn = dtg[(int64_t)(pos + SEG + l) * p.dt_sl];
 
-    // ---- shared: C B^T tiles (s-tile, t-tile) in {(0,0), (0,1), (1,1)} and B^T fragments;
-    //      both read the B tile, which the B^T fragments overwrite after the barrier
-    f32x16 cbacc[SW::CBPER];
+    // ---- this head's in-segment decay (lane = token); the factorised path when the range is small
+    const int len = min(SEG, c1 - pos);
+    float dtv;
+    const float cs = seg_decay(p, dtraw, h, Ah, pos + l, c1, dtv);
+    const float cse = __shfl(cs, 63, 64);
+    const bool fact = (-cse <= FACT_RANGE);               // wave-uniform
+    const float m = fact ? 0.5f * cse : 0.f;
+    sm.sa[w][ll] = (fact ? __expf(m - cs) : 1.f) * dtv;
+    sm.sb[w][ll] = __expf(cse - cs);
+    sm.cs[w][ll] = cs;
+
+    // ---- shared: C B^T tiles (s-tile, t-tile) in {(0,0), (0,1), (1,1)} and B^T fragments
 #pragma unroll
     for (int i = 0; i < SW::CBPER; ++i) {
       const int ti = SW::cb_tile(w, i);
-      cbacc[i] = zero16();
       if (ti < 3) {
         const int st = (ti == 2) ? 1 : 0, tt = (ti == 0) ? 0 : 1;
+        f32x16 acc = zero16();
 #pragma unroll
         for (int c = 0; c < N / 16; ++c)
-          cbacc[i] = mma(row_frag<TM, T, N>(bf.B, 32 * st + l32, 16 * c + 8 * half),
-                         row_frag<TM, T, N>(bf.C, 32 * tt + l32, 16 * c + 8 * half), cbacc[i]);
-      }
-    }
-    BtWork<T, TM, N, NW> bt;
-    bt.compute(bf.B, w, id, half, l32);
-    __syncthreads();
-    bt.store(bf.Bt, w, l);
-#pragma unroll
-    for (int i = 0; i < SW::CBPER; ++i) {
-      const int ti = SW::cb_tile(w, i);
-      if (ti < 3) {
-        const int st = (ti == 2) ? 1 : 0, tt = (ti == 0) ? 0 : 1;
-        const int tl = 32 * tt + l32;
+          acc = mma(row_frag<TM, T, N>(sg.B, 32 * st + l32q, 16 * c + 8 * halfq),
+                    row_frag<TM, T, N>(sg.C, 32 * tt + l32q, 16 * c + 8 * halfq), acc);
+        const int tl = 32 * tt + l32q;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int s = 32 * st + acc_row(half, r);
-          if (!(s <= tl && s < len)) cbacc[i][r] = 0.f;
+          const int s = 32 * st + acc_row(halfq, r);
+          if (!(s <= tl && s < len)) acc[r] = 0.f;
         }
-        sm.CB[ti][0][l] = acc_to_frag<TM>(cbacc[i], 0);
-        sm.CB[ti][1][l] = acc_to_frag<TM>(cbacc[i], 1);
+        sm.CB[ti][0][ll] = acc_to_frag<TM>(acc, 0);
+        sm.CB[ti][1][ll] = acc_to_frag<TM>(acc, 1);
       }
     }
-    __syncthreads();
+    bt_work<T, TM, N, NW, true>(sg.B, sm.bt, w, id, halfq, l32q, ll);
+    __syncthreads();                                       // C B^T, B^T fragments and scales visible
 
-    // ---- per wave: head j, p-tile ph
-    Frag<TM> xf[4];
-    scaled_xt_frags<TM, T>(bf.X[j], ph, sm.sa[j], id, half, l32, xf);
-    // Y^T[p][t] = sum_s xs^T[p][s] M^T[s][t] + sum_n Hs[p][n] C^T[n][t]
-    f32x16 Y0 = zero16(), Y1 = zero16();
-    Y0 = mma(xf[0], sm.CB[0][0][l], Y0);
-    Y0 = mma(xf[1], sm.CB[0][1][l], Y0);
-    Y1 = mma(xf[0], sm.CB[1][0][l], Y1);
-    Y1 = mma(xf[1], sm.CB[1][1][l], Y1);
-    Y1 = mma(xf[2], sm.CB[2][0][l], Y1);
-    Y1 = mma(xf[3], sm.CB[2][1][l], Y1);
+    // ---- per wave: head j, p-tile ph.  Y^T[p][t] = sum_n H[p][n] C^T[n][t] + sum_s xa^T[p][s] M^T[s][t],
+    // one 32-token t-tile at a time (its y staged in place of x before the next).
+    // Factorised path: H is carried at the segment midpoint, Hm = e^m H, with xa_s = e^{m - cs_s} dt_s x_s:
+    //   y_t = e^{cs_t - m} (C_t Hm^T + sum_s M[t][s] xa_s),   H_end = e^{cse - m} (Hm + B^T xa).
+    // Exact path (range above FACT_RANGE): xa_s = dt_s x_s, each masked C B^T entry decayed by
+    // e^{cs_t - cs_s} (s <= t), the state term weighted by e^{cs_t}; H_end = e^{cse} H + B^T (e^{cse - cs} xa).
+    Frag<TM> xa[4];
+    xt_frags<TM, T, false>(xt, sm.sa[w], nullptr, id, halfq, l32q, xa, xa);
+    if (fact) {
+      const float em = __expf(m);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const Frag<TM> hf = acc_to_frag<TM>(Hs[nt], c);
-        Y0 = mma(hf, kset_frag<TM, T, N>(bf.C, l32, 32 * nt + 16 * c, half), Y0);
-        Y1 = mma(hf, kset_frag<TM, T, N>(bf.C, 32 + l32, 32 * nt + 16 * c, half), Y1);
-      }
-    // y[t][p] = e^{cs_t + kappa} Y + D x, staged in place of x (this wave's 32 columns only)
+      for (int nt = 0; nt < NT; ++nt) H[nt] *= em;
+    }
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const int tl = 32 * tt + l32;
-      const float rsc = __expf(sm.cs[j][tl]);
+      const int tl = 32 * tt + l32q;
+      const float cst = sm.cs[w][tl];
+      f32x16 Y = zero16();
+      readout<TM, T, N>(H, sg.C, tl, halfq, Y);
+      float rsc = 1.f;
+      if (fact) {
+        if (tt == 0) {
+          Y = mma(xa[0], sm.CB[0][0][ll], Y);
+          Y = mma(xa[1], sm.CB[0][1][ll], Y);
+        } else {
+          Y = mma(xa[0], sm.CB[1][0][ll], Y);
+          Y = mma(xa[1], sm.CB[1][1][ll], Y);
+          Y = mma(xa[2], sm.CB[2][0][ll], Y);
+          Y = mma(xa[3], sm.CB[2][1][ll], Y);
+        }
+        rsc = __expf(cst - m);
+      } else {
+        Y *= __expf(cst);
+#pragma unroll
+        for (int ti = tt; ti < 2 * tt + 1; ++ti) {         // tiles (s-tile, tt): tt = 0 -> {0}, tt = 1 -> {1, 2}
+          const int st = (ti == 2) ? 1 : 0;
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            float css[8];
+            kset_vals(sm.cs[w] + 32 * st, c, halfq, css);
+            const Frag<TM> cb = sm.CB[ti][c][ll];
+            Frag<TM> md;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) md.set(e, cb.get(e) * __expf(fminf(cst - css[e], 0.f)));
+            Y = mma(xa[2 * st + c], md, Y);
+          }
+        }
+      }
+      // y[t][p] = rsc Y + D x, staged in place of x
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int p0 = 32 * ph + 8 * q + 4 * half;       // 4 consecutive columns, inside one 16-byte chunk
-        T* xp = bf.X[j] + TX::chunk(tl, p0 / TX::EPC) + (p0 % TX::EPC);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sm.dcol[j][p0]);
-        const float y0 = (tt ? Y1[4 * q] : Y0[4 * q]), y1 = (tt ? Y1[4 * q + 1] : Y0[4 * q + 1]);
-        const float y2 = (tt ? Y1[4 * q + 2] : Y0[4 * q + 2]), y3 = (tt ? Y1[4 * q + 3] : Y0[4 * q + 3]);
+        const int p0 = 8 * q + 4 * halfq;                // 4 consecutive columns of the half, inside one chunk
+        T* xp = xt + TX::chunk(tl, (unsigned)p0 / TX::EPC) + ((unsigned)p0 % TX::EPC);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sm.dcol[j][32 * ph + p0]);
         if constexpr (sizeof(T) == 2) {
           const bf16x4 xv = *reinterpret_cast<const bf16x4*>(xp);
           bf16x4 yv;
-          yv[0] = (bf16)(rsc * y0 + d4[0] * (float)xv[0]);
-          yv[1] = (bf16)(rsc * y1 + d4[1] * (float)xv[1]);
-          yv[2] = (bf16)(rsc * y2 + d4[2] * (float)xv[2]);
-          yv[3] = (bf16)(rsc * y3 + d4[3] * (float)xv[3]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) yv[i] = (bf16)(rsc * Y[4 * q + i] + d4[i] * (float)xv[i]);
           *reinterpret_cast<bf16x4*>(xp) = yv;
         } else {
           const f32x4 xv = *reinterpret_cast<const f32x4*>(xp);
           f32x4 yv;
-          yv[0] = rsc * y0 + d4[0] * xv[0];
-          yv[1] = rsc * y1 + d4[1] * xv[1];
-          yv[2] = rsc * y2 + d4[2] * xv[2];
-          yv[3] = rsc * y3 + d4[3] * xv[3];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) yv[i] = rsc * Y[4 * q + i] + d4[i] * xv[i];
           *reinterpret_cast<f32x4*>(xp) = yv;
         }
       }
     }
-    // ---- coalesced store of this wave's staged y columns for rows t < len
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    constexpr int HCPR = TX::CPR / 2;                       // 16-byte chunks per row in a 32-column half
+    // ---- state update
+    if (fact) {
+      state_update<TM, N>(H, sm.bt, xa, ll);
+      const float eo = __expf(cse - m);
 #pragma unroll
-    for (int i = 0; i < SEG * HCPR / 64; ++i) {
-      const int e = l + 64 * i;
-      const int r = e / HCPR, c = ph * HCPR + (e - r * HCPR);
-      if (r < len)
-        *reinterpret_cast<uint4*>(yg + (int64_t)(pos + r) * p.y_sl + c * TX::EPC) =
-            *reinterpret_cast<const uint4*>(bf.X[j] + TX::chunk(r, c));
+      for (int nt = 0; nt < NT; ++nt) H[nt] *= eo;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {                        // xa <- e^{cse - cs_s} xa
+        float f[8];
+        kset_vals(sm.sb[w], c, halfq, f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xa[c].set(e, xa[c].get(e) * f[e]);
+      }
+      const float e = __expf(cse);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) H[nt] *= e;
+      state_update<TM, N>(H, sm.bt, xa, ll);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // ---- state: Hs += B^T xs
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      Frag<TM> btf[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) btf[c] = bf.Bt[nt][c][l];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) Hs[nt] = mma(btf[c], xf[c], Hs[nt]);
-    }
-    kappa = ke + __shfl(cs, len - 1, 64);
-    if constexpr (NBUF == 1) {
-      __syncthreads();
-      if (next < c1)
-        fetch_segment<T, N, NW>(bf.B, bf.C, bf.X[j], Bg, p.B_sl, Cg, p.C_sl, xg, p.x_sl, next, last, w, ph, l);
-    }
-    wait_vmem();
-    __syncthreads();
-    cur ^= NBUF - 1;
-    pos = next;
+    dtraw = dtn;
+  }
+  // y of the last segment
+  {
+    const int si = nseg - 1;
+    const int cur = (NBUF == 2) ? (si & 1) : 0;
+    const int pos = c0 + si * SEG;
+    store_yhalf<T>(yg + (int64_t)pos * p.y_sl, p.y_sl, sm.st[cur].X[w], c1 - pos, l);
   }
 }
 
@@ -682,11 +736,18 @@ static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <typename T, typename TM, int N, int HG>
+constexpr bool ssd_fits = sizeof(ScanSmem<T, TM, N, HG, 1>) <= LDS_BYTES && sizeof(StateSmem<T, TM, N, HG, 1>) <= LDS_BYTES;
+
 template <typename T, typename TM, int N>
 static hipError_t launch_ssd_n(const SsdParams& p, hipStream_t st) {
   switch (p.heads_per_wg) {
-    case 4: return launch_ssd_t<T, TM, N, 4>(p, st);
-    case 2: return launch_ssd_t<T, TM, N, 2>(p, st);
+    case 4:
+      if constexpr (ssd_fits<T, TM, N, 4>) return launch_ssd_t<T, TM, N, 4>(p, st);
+      return hipErrorInvalidValue;
+    case 2:
+      if constexpr (ssd_fits<T, TM, N, 2>) return launch_ssd_t<T, TM, N, 2>(p, st);
+      return hipErrorInvalidValue;
     case 1: return launch_ssd_t<T, TM, N, 1>(p, st);
     default: return hipErrorInvalidValue;
   }
