@@ -180,6 +180,32 @@ typedef struct {
 
 int mh_kda_recurrent_step(const mh_kda_step_args* a, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Causal depthwise conv1d (+ optional SiLU), the Mamba layer prologue.
+ * Replaces Mamba2Block._causal_conv1d (mamformer/layers/mamba2.py:370-405)
+ *   and the SiLU that follows it (mamba2.py:282-283):
+ *   y[b,t,d] = act(bias[d] + sum_{j<width} weight[d,j] * xin[b, t-(width-1)+j, d])
+ *   with xin = x for t >= 0, the last conv_state_len rows of conv_state
+ *   (the cached raw inputs, mamba2.py:355-359) before that, and 0 beyond.
+ *   x, conv_state, y (b, L, D) channels-last in one dtype, innermost
+ *   contiguous; weight (D, width) fp32; bias (D,) fp32 or NULL.
+ *   Supported: width 1..8, D % 8 == 0, conv_state_len <= width - 1.
+ * ---------------------------------------------------------------------- */
+enum { MH_CONV_SILU = 1 };
+
+typedef struct {
+  int64_t batch, seqlen, dim, width;
+  int32_t dtype;
+  int32_t flags;
+  const void* x; int64_t x_stride_b, x_stride_l;
+  const float* weight;
+  const float* bias;
+  const void* conv_state; int64_t conv_state_len, conv_state_stride_b, conv_state_stride_l;
+  void* y; int64_t y_stride_b, y_stride_l;
+} mh_conv1d_args;
+
+int mh_causal_conv1d_fwd(const mh_conv1d_args* a, void* stream);
+
 /* ------------------------------------------------------------------------ */
 int mh_abi_version(void);
 const char* mh_last_error(void);

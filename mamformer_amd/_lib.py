@@ -82,6 +82,19 @@ class KdaStepArgs(ct.Structure):
     ]
 
 
+class Conv1dArgs(ct.Structure):
+    _fields_ = [
+        ("batch", _i64), ("seqlen", _i64), ("dim", _i64), ("width", _i64),
+        ("dtype", _i32), ("flags", _i32),
+        ("x", _vp), ("x_stride_b", _i64), ("x_stride_l", _i64),
+        ("weight", _vp), ("bias", _vp),
+        ("conv_state", _vp), ("conv_state_len", _i64), ("conv_state_stride_b", _i64), ("conv_state_stride_l", _i64),
+        ("y", _vp), ("y_stride_b", _i64), ("y_stride_l", _i64),
+    ]
+
+
+MH_CONV_SILU = 1
+
 # every symbol include/mamformer_hip.h declares
 EXPORTS = (
     "mh_abi_version", "mh_last_error",
@@ -89,6 +102,7 @@ EXPORTS = (
     "mh_ssd_state_update",
     "mh_kda_chunk_scan_fwd",
     "mh_kda_recurrent_step",
+    "mh_causal_conv1d_fwd",
 )
 
 _lock = threading.Lock()
@@ -123,8 +137,10 @@ def lib():
             h.mh_ssd_state_update.argtypes = [ct.POINTER(SsuArgs), _vp]
             h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
             h.mh_kda_recurrent_step.argtypes = [ct.POINTER(KdaStepArgs), _vp]
+            h.mh_causal_conv1d_fwd.argtypes = [ct.POINTER(Conv1dArgs), _vp]
             for name in ("mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
-                         "mh_ssd_state_update", "mh_kda_chunk_scan_fwd", "mh_kda_recurrent_step"):
+                         "mh_ssd_state_update", "mh_kda_chunk_scan_fwd", "mh_kda_recurrent_step",
+                         "mh_causal_conv1d_fwd"):
                 getattr(h, name).restype = ct.c_int
             ver = h.mh_abi_version()
             if ver != ABI_VERSION:

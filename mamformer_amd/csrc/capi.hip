@@ -89,8 +89,9 @@ int ssd_validate(const mh_ssd_args* a, int64_t* chunk_len_out) {
   if (a->dt_stride_b < 0 || a->dt_stride_l < 0) return fail(MH_ERR_STRIDE, "ssd: negative dt stride");
   if (a->x_stride_h < a->headdim || a->y_stride_h < a->headdim)
     return fail(MH_ERR_STRIDE, "ssd: x/y head stride smaller than headdim (headdim must be contiguous)");
-  if (a->B_stride_l < a->ngroups * a->dstate || a->C_stride_l < a->ngroups * a->dstate)
-    return fail(MH_ERR_STRIDE, "ssd: B/C token stride smaller than ngroups*dstate ((g, n) must be contiguous)");
+  if ((a->B_stride_l != 0 && a->B_stride_l < a->ngroups * a->dstate) ||
+      (a->C_stride_l != 0 && a->C_stride_l < a->ngroups * a->dstate))
+    return fail(MH_ERR_STRIDE, "ssd: B/C token stride smaller than ngroups*dstate ((g, n) must be contiguous; 0 broadcasts)");
   const int64_t nchunks = (a->seqlen + cl - 1) / cl;
   if (nchunks > 65535) return fail(MH_ERR_SHAPE, "ssd: too many chunks (%lld)", (long long)nchunks);
   if (chunk_len_out) *chunk_len_out = cl;
@@ -167,6 +168,31 @@ int kda_step_validate(const mh_kda_step_args* a) {
     return fail(MH_ERR_NULL, "kda_step: q1, k, v, state, z, o are required");
   if (!a->q2 && a->o2) return fail(MH_ERR_NULL, "kda_step: o2 given without q2");
   if (!aligned16(a->state)) return fail(MH_ERR_ALIGN, "kda_step: state must be 16-byte aligned");
+  return MH_OK;
+}
+
+int conv_validate(const mh_conv1d_args* a) {
+  if (!a) return fail(MH_ERR_NULL, "conv1d: args is NULL");
+  if (a->batch <= 0 || a->seqlen < 0 || a->dim <= 0 || a->width <= 0)
+    return fail(MH_ERR_SHAPE, "conv1d: sizes must be positive");
+  if (a->batch > 65535 || a->seqlen > kMaxDim || a->dim > kMaxDim) return fail(MH_ERR_SHAPE, "conv1d: sizes out of range");
+  if (a->width > 8) return fail(MH_ERR_UNSUPPORTED, "conv1d: width %lld not supported (1..8)", (long long)a->width);
+  if (a->dim % 8) return fail(MH_ERR_UNSUPPORTED, "conv1d: dim %lld must be a multiple of 8", (long long)a->dim);
+  const int es = elem_size(a->dtype);
+  if (!es) return fail(MH_ERR_DTYPE, "conv1d: unknown dtype %d", a->dtype);
+  if (!a->weight) return fail(MH_ERR_NULL, "conv1d: weight is required");
+  if (a->seqlen > 0 && (!a->x || !a->y)) return fail(MH_ERR_NULL, "conv1d: x and y are required");
+  if (a->conv_state_len < 0 || a->conv_state_len > a->width - 1)
+    return fail(MH_ERR_SHAPE, "conv1d: conv_state_len %lld outside [0, width-1]", (long long)a->conv_state_len);
+  if (a->conv_state_len > 0 && !a->conv_state) return fail(MH_ERR_NULL, "conv1d: conv_state is NULL");
+  if (!aligned16(a->x) || !aligned16(a->y) || (a->conv_state && !aligned16(a->conv_state)))
+    return fail(MH_ERR_ALIGN, "conv1d: x, y, conv_state must be 16-byte aligned");
+  if (!stride_ok(a->x_stride_b, es) || !stride_ok(a->x_stride_l, es) || !stride_ok(a->y_stride_b, es) ||
+      !stride_ok(a->y_stride_l, es) ||
+      (a->conv_state && (!stride_ok(a->conv_state_stride_b, es) || !stride_ok(a->conv_state_stride_l, es))))
+    return fail(MH_ERR_ALIGN, "conv1d: strides must be multiples of 16 bytes");
+  if (a->x_stride_l < a->dim || a->y_stride_l < a->dim)
+    return fail(MH_ERR_STRIDE, "conv1d: token stride smaller than dim (channels must be contiguous)");
   return MH_OK;
 }
 
@@ -275,6 +301,22 @@ int mh_kda_recurrent_step(const mh_kda_step_args* a, void* stream) {
   p.q1 = a->q1; p.q2 = a->q2; p.k = a->k; p.v = a->v;
   p.state = a->state; p.z = a->z; p.o = a->o; p.o2 = a->o2;
   return hip_status(mh::launch_kda_step(p, reinterpret_cast<hipStream_t>(stream)), "kda_recurrent_step");
+}
+
+int mh_causal_conv1d_fwd(const mh_conv1d_args* a, void* stream) {
+  int rc = conv_validate(a);
+  if (rc) return rc;
+  mh::Conv1dParams p;
+  memset(&p, 0, sizeof(p));
+  p.batch = (int)a->batch; p.seqlen = (int)a->seqlen; p.dim = (int)a->dim; p.width = (int)a->width;
+  p.dtype = a->dtype; p.silu = (a->flags & MH_CONV_SILU) != 0;
+  p.cs_len = (int)a->conv_state_len;
+  p.x = a->x; p.x_sb = a->x_stride_b; p.x_sl = a->x_stride_l;
+  p.weight = a->weight; p.bias = a->bias;
+  p.conv_state = a->conv_state_len > 0 ? a->conv_state : nullptr;
+  p.cs_sb = a->conv_state_stride_b; p.cs_sl = a->conv_state_stride_l;
+  p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l;
+  return hip_status(mh::launch_conv1d(p, reinterpret_cast<hipStream_t>(stream)), "causal_conv1d_fwd");
 }
 
 }  // extern "C"

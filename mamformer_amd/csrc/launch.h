@@ -84,4 +84,16 @@ struct KdaStepParams {
 };
 hipError_t launch_kda_step(const KdaStepParams& p, hipStream_t st);
 
+// ------------------------------------------------------------- causal conv1d
+struct Conv1dParams {
+  int batch, seqlen, dim, width, dtype, silu;
+  int cs_len;                  // rows of conv_state (0 .. width-1)
+  const void* x; int64_t x_sb, x_sl;
+  const float* weight;         // (dim, width) fp32
+  const float* bias;           // (dim,) fp32 or null
+  const void* conv_state; int64_t cs_sb, cs_sl;
+  void* y; int64_t y_sb, y_sl;
+};
+hipError_t launch_conv1d(const Conv1dParams& p, hipStream_t st);
+
 }  // namespace mh

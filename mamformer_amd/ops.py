@@ -17,6 +17,8 @@ Reference functions replaced (``R`` = ``mamformer 671b/``):
 ``linear_attention_scan``               R/mamformer/layers/kda_diff.py:357-478 (``_linear_attention_scan``)
 ``linear_attention_recurrent``          R/mamformer/layers/kda_diff.py:564-605 (``_linear_attention_recurrent``)
 ``linear_attn_step``                    in-place form of the same step (fp32 state and z updated in HBM)
+``causal_conv1d``                       R/mamformer/layers/mamba2.py:370-405 (``Mamba2Block._causal_conv1d``)
+                                        with the SiLU of mamba2.py:282-283 optionally fused
 =====================================  ====================================================================
 
 SSD convention.  The reference's scan uses a per-channel dt and a per-state
@@ -36,13 +38,13 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import SsdArgs, SsuArgs, KdaArgs
+from ._lib import SsdArgs, SsuArgs, KdaArgs, Conv1dArgs
 
 __all__ = ["selective_scan", "selective_state_update", "recurrent_step", "linear_attn_scan",
            "linear_attn_scan_pair", "linear_attn_scan_single", "linear_attention_scan", "diff_lambda",
            "linear_attn_step", "linear_attention_recurrent",
            "ssd_chunk_len", "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan",
-           "plan_linear_attn_step"]
+           "plan_linear_attn_step", "causal_conv1d"]
 
 _DT = {torch.float32: _lib.MH_F32, torch.bfloat16: _lib.MH_BF16}
 
@@ -161,17 +163,18 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
         A: (H,) per-head decay rates, A <= 0.
         B, C: (b, L, N) (one group, as the reference) or (b, L, G, N); dtype of x.
         D: (H,), (H*P,) or None.
-        return_h_states: not supported by the HIP path yet (raises).
+        return_h_states: also return h_states (b, L, N), the per-token mean of the state over the
+            H*P channels (mamba2.py:114-116); computed by a second run of the same kernels (see below).
         return_final_state: also return the state after the last token,
             shaped (b, H*P, N) for 3-D x (the reference's (b, d_inner, d_state)) or (b, H, P, N).
         chunk_size: state-passing chunk length (multiple of 64); None picks it from the shape.
         initial_state: (b, H*P, N) / (b, H, P, N) fp32 state before the first token (prefill of a cached
             sequence); the reference scan always starts from zero (mamba2.py:101).
         dt_bias, dt_softplus, dt_limit: dt <- clamp(softplus(dt + dt_bias), *dt_limit) inside the kernel.
-    Returns y (like x), or (y, final_state) in the reference's tuple order (mamba2.py:121-130).
+    Returns y (like x), or a tuple in the reference's order (y, h_states, final_state) (mamba2.py:121-130).
     """
-    if return_h_states:
-        raise NotImplementedError("selective_scan: return_h_states is not implemented by the HIP path")
+    if return_h_states and _plan_only:
+        raise ValueError("plan_selective_scan: return_h_states is not planned (call selective_scan)")
     _require_cuda("selective_scan", x, dt, A, B, C, D, initial_state, dt_bias)
     if x.dtype not in _DT:
         raise TypeError(f"selective_scan: x dtype {x.dtype} not supported (float32, bfloat16)")
@@ -232,9 +235,88 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
     if _plan_only:
         return plan
     plan()
-    if not return_final_state:
-        return y
-    return y, fin_out
+    out = [y]
+    if return_h_states:
+        out.append(_h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size))
+    if return_final_state:
+        out.append(fin_out)
+    return out[0] if len(out) == 1 else tuple(out)
+
+
+def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size):
+    """h_states[b, t, n] = mean over (h, p) of the state h_t[h, p, n] (mamba2.py:114-116).
+
+    The channel sum of the state is itself an SSD output once the roles of x and B are swapped: with
+    heads h' = (h, q) over the two 64-wide halves q of the state dimension n, headdim' = 64 (n' = n - 64q),
+    x'_t[h', n'] = B_t[g(h), 64q + n'], one group per original head with B'_t[h, p] = x_t[h, p]
+    (dstate' = P), C' = 1, D' = 0, and the same dt and A per head, the recurrence gives
+    h'_t[h', n', p] = h_t[h, p, 64q + n'], so y'_t[h', n'] = sum_p h_t[h, p, 64q + n'].  The same kernels
+    compute it; the mean over heads is a reduction over the head axis.
+    """
+    b, L, H, P = x4.shape
+    G, N = B4.shape[2], B4.shape[3]
+    if P != 64 or N % 64:
+        raise NotImplementedError("selective_scan: return_h_states needs headdim 64 and dstate a multiple of 64")
+    Q = N // 64
+    gidx = torch.arange(H, device=x4.device) // (H // G)
+    xs = B4[:, :, gidx, :].reshape(b, L, H * Q, 64).contiguous()                # x'
+    Bs = x4 if (x4.stride(-1) == 1 and x4.stride(-2) == P) else x4.contiguous()  # B' (g' = h, n' = p)
+    Cs = torch.ones((1, 1, H, P), device=x4.device, dtype=x4.dtype).expand(b, L, H, P)
+    dts = dt32.repeat_interleave(Q, dim=-1)
+    As = A32.repeat_interleave(Q)
+    bias_s = bias32.repeat_interleave(Q) if bias32 is not None else None
+    h0s = None
+    if h0 is not None:
+        h0s = h0.view(b, H, P, Q, 64).permute(0, 1, 3, 4, 2).reshape(b, H * Q, 64, P).contiguous()
+    ys = torch.empty((b, L, H * Q, 64), device=x4.device, dtype=x4.dtype)
+    args = _ssd_args(xs, dts, As, Bs, Cs, None, bias_s, dt_softplus, dt_limit, h0s, ys, None, chunk_size)
+    nbytes = ct.c_size_t()
+    _lib.call("mh_ssd_workspace_bytes", ct.byref(args), ct.byref(nbytes))
+    ws = torch.empty(max(int(nbytes.value), 16), device=x4.device, dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = _ptr(ws), nbytes.value
+    _lib.call("mh_ssd_chunk_scan_fwd", ct.byref(args), _stream(x4.device))
+    hs = ys.view(b, L, H, N).to(torch.float32).sum(dim=2) / float(H * P)
+    return hs.to(x4.dtype)
+
+
+def causal_conv1d(x, weight, bias=None, conv_state=None, *, silu=False):
+    """Causal depthwise conv1d over channels-last x (b, L, D) on the GPU (+ SiLU when ``silu``).
+
+    ``Mamba2Block._causal_conv1d`` counterpart (R/mamformer/layers/mamba2.py:370-405): weight (D, 1, K) or
+    (D, K) as ``nn.Conv1d(D, D, K, groups=D)`` holds it, optional bias (D,); ``conv_state`` (b, S_c, D) with
+    S_c <= K-1 are the cached raw inputs prepended on the incremental path (:388-390).  Returns y (b, L, D)
+    in the dtype of x (fp32 accumulation).
+    """
+    _require_cuda("causal_conv1d", x, weight, bias, conv_state)
+    if x.dim() != 3:
+        raise ValueError("causal_conv1d: x must be (b, L, D)")
+    if x.dtype not in _DT:
+        raise TypeError(f"causal_conv1d: x dtype {x.dtype} not supported (float32, bfloat16)")
+    b, L, Dm = x.shape
+    w = weight.reshape(Dm, -1).to(torch.float32).contiguous()
+    K = w.shape[1]
+    xc = _inner_contig(x)
+    bc = _f32c(bias.reshape(-1)) if bias is not None else None
+    cs = None
+    if conv_state is not None and conv_state.shape[1] > 0:
+        if conv_state.dim() != 3 or conv_state.shape[0] != b or conv_state.shape[2] != Dm:
+            raise ValueError("causal_conv1d: conv_state must be (b, S_c, D)")
+        if conv_state.shape[1] > K - 1:
+            conv_state = conv_state[:, -(K - 1):] if K > 1 else conv_state[:, :0]
+        cs = _inner_contig(conv_state.to(x.dtype))
+    y = torch.empty((b, L, Dm), device=x.device, dtype=x.dtype)
+    a = Conv1dArgs()
+    a.batch, a.seqlen, a.dim, a.width = b, L, Dm, K
+    a.dtype = _DT[x.dtype]
+    a.flags = _lib.MH_CONV_SILU if silu else 0
+    a.x, a.x_stride_b, a.x_stride_l = _ptr(xc), xc.stride(0), xc.stride(1)
+    a.weight, a.bias = _ptr(w), _ptr(bc)
+    if cs is not None and cs.shape[1] > 0:
+        a.conv_state, a.conv_state_len = _ptr(cs), cs.shape[1]
+        a.conv_state_stride_b, a.conv_state_stride_l = cs.stride(0), cs.stride(1)
+    a.y, a.y_stride_b, a.y_stride_l = _ptr(y), y.stride(0), y.stride(1)
+    _lib.call("mh_causal_conv1d_fwd", ct.byref(a), _stream(x.device))
+    return y
 
 
 def plan_selective_state_update(*args, **kw):

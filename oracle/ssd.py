@@ -7,6 +7,7 @@ Reference algorithm (``R`` = ``/root/reference/mamformer 671b/``):
 * ``ref_selective_scan``  restates ``_selective_scan_impl``  R/mamformer/layers/mamba2.py:70-130
 * ``ref_recurrent_step``  restates ``Mamba2Block._recurrent_step`` R/mamformer/layers/mamba2.py:407-458
 * ``softplus``            restates ``F.softplus`` (beta=1, threshold=20) as used at mamba2.py:293/304
+* ``ref_causal_conv1d``   restates ``Mamba2Block._causal_conv1d`` R/mamformer/layers/mamba2.py:370-405
 
 SSD (Mamba-2) convention -- nheads H, headdim P, scalar A_h < 0 per head, dt per
 head, ngroups G sharing B/C -- is reduced to the reference formula by the exact
@@ -32,6 +33,8 @@ __all__ = [
     "softplus",
     "ref_selective_scan",
     "ref_recurrent_step",
+    "ref_causal_conv1d",
+    "ssd_h_states",
     "process_dt",
     "ssd_via_reference",
     "ssd_direct",
@@ -118,6 +121,29 @@ def ref_recurrent_step(x, dt, B, C, h_prev, A_log, D):
     return y_t[:, None, :], h_t
 
 
+def ref_causal_conv1d(x, weight, bias=None, conv_state=None):
+    """Restates ``Mamba2Block._causal_conv1d`` (R/mamformer/layers/mamba2.py:370-405) in float64.
+
+    x (b, L, D); weight (D, 1, K) or (D, K) (depthwise ``nn.Conv1d``); bias (D,) or None; conv_state
+    (b, S_c, D) cached raw inputs or None.  With a cache the input is cat(conv_state, x) (:388-390); the
+    sequence is left-padded with K-1 zeros (:393), cross-correlated with the per-channel kernel
+    (``F.conv1d``, :397) and, with a cache, only the last L outputs are kept (:401-402).
+    """
+    x = np.asarray(x, np.float64)
+    w = np.asarray(weight, np.float64).reshape(x.shape[2], -1)
+    K = w.shape[1]
+    L = x.shape[1]
+    xin = x if conv_state is None else np.concatenate([np.asarray(conv_state, np.float64), x], axis=1)
+    pad = np.concatenate([np.zeros((x.shape[0], K - 1, x.shape[2])), xin], axis=1)
+    n_out = xin.shape[1]
+    out = np.zeros((x.shape[0], n_out, x.shape[2]))
+    for j in range(K):
+        out += w[None, None, :, j] * pad[:, j:j + n_out, :]
+    if bias is not None:
+        out += np.asarray(bias, np.float64)[None, None, :]
+    return out[:, -L:] if L else out[:, :0]
+
+
 # ---------------------------------------------------------------------------
 # SSD convention helpers
 # ---------------------------------------------------------------------------
@@ -159,12 +185,14 @@ def _expand_D(D, H, P):
     return D.reshape(H, P)
 
 
-def ssd_via_reference(x, dt, A, B, C, D=None, initial_state=None):
+def ssd_via_reference(x, dt, A, B, C, D=None, initial_state=None, return_h_states=False):
     """SSD-convention scan computed *by the reference algorithm* through the bridge.
 
     x (b,L,H,P); dt (b,L,H) already processed (positive); A (H,) with A < 0;
     B, C (b,L,N) or (b,L,G,N); D None, (H,) or (H,P); initial_state (b,H,P,N) or None.
-    Returns (y (b,L,H,P), final_state (b,H,P,N)), float64.
+    Returns (y (b,L,H,P), final_state (b,H,P,N)), float64; with ``return_h_states`` (zero initial
+    state) also h_states (b,L,N) = the reference's per-token mean of the state over all H*P channels
+    (mamba2.py:114-116), combined over the per-group calls weighted by their channel counts.
 
     Zero initial state: one ``ref_selective_scan`` call per group (heads
     h with h // (H//G) == g share B[:,:,g], C[:,:,g]).  Nonzero initial state:
@@ -186,6 +214,9 @@ def ssd_via_reference(x, dt, A, B, C, D=None, initial_state=None):
     hpg = H // G
     y = np.zeros((b, L, H, P))
     final = np.zeros((b, H, P, N))
+    if return_h_states and initial_state is not None:
+        raise ValueError("ssd_via_reference: h_states through the bridge needs a zero initial state")
+    hs_all = np.zeros((b, L, N)) if return_h_states else None
     for g in range(G):
         hs = slice(g * hpg, (g + 1) * hpg)
         ag = a[hs]                                               # (hpg,)
@@ -195,7 +226,11 @@ def ssd_via_reference(x, dt, A, B, C, D=None, initial_state=None):
         dt_ref = dt_ref.reshape(b, L, hpg * P)
         x_ref = x_ref.reshape(b, L, hpg * P)
         A_log = np.zeros(N)
-        if initial_state is None:
+        if initial_state is None and return_h_states:
+            yg, hsg, hg = ref_selective_scan(x_ref, dt_ref, A_log, Bg[:, :, g], Cg[:, :, g], D_ref,
+                                             return_h_states=True, return_final_state=True)
+            hs_all += hsg * (hpg * P) / (H * P)
+        elif initial_state is None:
             yg, hg = ref_selective_scan(x_ref, dt_ref, A_log, Bg[:, :, g], Cg[:, :, g], D_ref,
                                         return_final_state=True)
         else:
@@ -208,7 +243,29 @@ def ssd_via_reference(x, dt, A, B, C, D=None, initial_state=None):
             hg = h
         y[:, :, hs, :] = yg.reshape(b, L, hpg, P)
         final[:, hs] = hg.reshape(b, hpg, P, N)
+    if return_h_states:
+        return y, final, hs_all
     return y, final
+
+
+def ssd_h_states(x, dt, A, B, C=None, initial_state=None):
+    """h_states[b,t,n] = mean over (h, p) of the SSD state after token t, in direct SSD form (any initial
+    state); the quantity ``selective_scan(..., return_h_states=True)`` returns (mamba2.py:114-116)."""
+    x = np.asarray(x, np.float64)
+    dt = np.asarray(dt, np.float64)
+    A = np.asarray(A, np.float64)
+    b, L, H, P = x.shape
+    Bg, G = _groups_of(B, H)
+    N = Bg.shape[-1]
+    gidx = np.arange(H) // (H // G)
+    h = np.zeros((b, H, P, N)) if initial_state is None else np.array(initial_state, np.float64)
+    hs = np.zeros((b, L, N))
+    for t in range(L):
+        dA = np.exp(A[None, :] * dt[:, t, :])
+        Bt = Bg[:, t][:, gidx]
+        h = dA[:, :, None, None] * h + (dt[:, t, :, None, None] * x[:, t, :, :, None]) * Bt[:, :, None, :]
+        hs[:, t] = h.mean(axis=(1, 2))
+    return hs
 
 
 def ssd_direct(x, dt, A, B, C, D=None, initial_state=None):

@@ -10,7 +10,7 @@ import torch
 
 import mamformer_amd
 from mamformer_amd import _lib
-from mamformer_amd._lib import KdaArgs, SsdArgs, SsuArgs
+from mamformer_amd._lib import Conv1dArgs, KdaArgs, SsdArgs, SsuArgs
 
 ROOT = Path(__file__).resolve().parent.parent
 
@@ -195,3 +195,31 @@ def test_kda_step_o2_needs_q2():
     a.q2 = None
     a.o2 = ct.c_void_p(4096)
     assert _rc("mh_kda_recurrent_step", ct.byref(a), None) == -1
+
+
+def _good_conv():
+    a = Conv1dArgs()
+    a.batch, a.seqlen, a.dim, a.width = 2, 50, 256, 4
+    a.dtype = _lib.MH_BF16
+    fake = ct.c_void_p(4096)
+    a.x = a.y = a.weight = fake
+    a.x_stride_l = a.y_stride_l = 256
+    a.x_stride_b = a.y_stride_b = 50 * 256
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("width", 9, -6), ("dim", 12, -6), ("dtype", 5, -3), ("batch", 0, -2), ("conv_state_len", 4, -2),
+    ("x_stride_l", 100, -5), ("y_stride_l", 128, -4),
+])
+def test_conv1d_rejects_bad_arguments(field, value, code):
+    a = _good_conv()
+    setattr(a, field, value)
+    assert _rc("mh_causal_conv1d_fwd", ct.byref(a), None) == code
+    assert _lib.lib().mh_last_error()
+
+
+def test_conv1d_rejects_missing_conv_state():
+    a = _good_conv()
+    a.conv_state_len = 2
+    assert _rc("mh_causal_conv1d_fwd", ct.byref(a), None) == -1

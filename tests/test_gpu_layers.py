@@ -1,0 +1,202 @@
+"""GPU parity of the layer-level pieces around the scans against the float64 oracle.
+
+* ``causal_conv1d`` (HIP) vs ``oracle.ssd.ref_causal_conv1d`` (mamba2.py:370-405), with and without the
+  cached raw rows, bias and fused SiLU;
+* ``selective_scan(return_h_states=True)`` vs ``oracle.ssd.ssd_h_states`` (mamba2.py:114-116);
+* ``Mamba2Layer`` (A3 dispatch and cache, mamba2.py:249-364) vs the same layer composed in float64 from the
+  oracle pieces, and prefill + one incremental step vs one longer prefill;
+* ``kda_linear_attention`` (A13 state semantics, kda_diff.py:286-338) vs the reference-mode KDA oracle.
+Tolerances: relative L2 <= 1e-4 for fp32 I/O, <= 1e-2 for bf16 I/O.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import mamformer_amd as mh
+from mamformer_amd.layers import Mamba2Layer, kda_linear_attention
+from oracle import kda as okda
+from oracle import ssd as ref
+from tests.gpu_helpers import TOL, check, dev, host, say
+
+pytestmark = pytest.mark.gpu
+
+
+# ----------------------------------------------------------------- conv1d
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("L,D,K,cs_len", [(1, 8, 4, 0), (5, 64, 4, 3), (70, 256, 4, 2), (1000, 512, 3, 0),
+                                          (33, 4096, 2, 1)])
+def test_conv1d_vs_oracle(dtype, L, D, K, cs_len):
+    g = torch.Generator().manual_seed(L * 7 + D)
+    b = 2
+    x = torch.randn(b, L, D, generator=g)
+    w = torch.randn(D, 1, K, generator=g) * 0.5
+    bias = torch.randn(D, generator=g)
+    cs = torch.randn(b, cs_len, D, generator=g) if cs_len else None
+    xd, csd = dev(x, dtype), (dev(cs, dtype) if cs is not None else None)
+    for silu in (False, True):
+        say(f"conv1d L={L} D={D} K={K} cs={cs_len} silu={silu} {dtype}")
+        y = mh.causal_conv1d(xd, dev(w), dev(bias), csd, silu=silu)
+        torch.cuda.synchronize()
+        r = ref.ref_causal_conv1d(host(xd), w.numpy(), bias.numpy(), host(csd) if csd is not None else None)
+        if silu:
+            r = r / (1.0 + np.exp(-r))
+        check("conv1d y", y, r, TOL[dtype])
+
+
+# ----------------------------------------------------------------- h_states
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("G,N,h0", [(1, 64, False), (2, 128, True)])
+def test_h_states_vs_oracle(dtype, G, N, h0):
+    g = torch.Generator().manual_seed(5 + N)
+    b, L, H, P = 2, 150, 4, 64
+    x = torch.randn(b, L, H, P, generator=g)
+    B = torch.randn(b, L, G, N, generator=g)
+    C = torch.randn(b, L, G, N, generator=g)
+    dt = F.softplus(torch.randn(b, L, H, generator=g) - 2.0)
+    A = -torch.exp(torch.rand(H, generator=g) * 2.5)
+    s0 = 0.1 * torch.randn(b, H, P, N, generator=g) if h0 else None
+    say(f"h_states G={G} N={N} h0={h0} {dtype}")
+    xd, Bd, Cd = dev(x, dtype), dev(B, dtype), dev(C, dtype)
+    y, hs, fin = mh.selective_scan(xd, dev(dt), dev(A), Bd, Cd, None, return_h_states=True, return_final_state=True,
+                                   initial_state=dev(s0) if h0 else None)
+    torch.cuda.synchronize()
+    assert hs.shape == (b, L, N) and hs.dtype == dtype
+    r = ref.ssd_h_states(host(xd), dt.double().numpy(), A.double().numpy(), host(Bd),
+                         initial_state=s0.double().numpy() if h0 else None)
+    check("h_states", hs, r, TOL[dtype])
+    check("h_states last row = mean of final state", hs[:, -1], host(fin).mean(axis=(1, 2)), TOL[dtype])
+
+
+# ----------------------------------------------------------------- Mamba2Layer
+
+def _layer_ref(layer, u, use_cache_state=None):
+    """Float64 composition of the layer from the oracle pieces (no cache)."""
+    P64 = {k: v.detach().double().cpu().numpy() for k, v in layer.named_parameters()}
+    un = u.detach().double().cpu().numpy()
+    xz = un @ P64["in_proj.weight"].T
+    x, z = np.split(xz, 2, axis=-1)
+    xc = ref.ref_causal_conv1d(x, P64["conv_weight"])
+    xa = xc / (1.0 + np.exp(-xc))
+    dt_raw = (xa @ P64["dt_proj.0.weight"].T) @ P64["dt_proj.1.weight"].T
+    Bm = xa @ P64["B_proj.weight"].T
+    Cm = xa @ P64["C_proj.weight"].T
+    b, L, _ = un.shape
+    H, Pd, G, N = layer.nheads, layer.headdim, layer.ngroups, layer.d_state
+    dt = ref.softplus(dt_raw + P64["dt_bias"])
+    A = -np.exp(P64["A_log"])
+    y, fin = ref.ssd_direct(xa.reshape(b, L, H, Pd), dt, A, Bm.reshape(b, L, G, N), Cm.reshape(b, L, G, N),
+                            P64["D"])
+    hs = ref.ssd_h_states(xa.reshape(b, L, H, Pd), dt, A, Bm.reshape(b, L, G, N))
+    y = y.reshape(b, L, H * Pd) * (z / (1.0 + np.exp(-z)))
+    out = y @ P64["out_proj.weight"].T
+    return out, fin.reshape(b, H * Pd, N), hs, x
+
+
+@pytest.mark.parametrize("G,N", [(1, 64), (2, 128)])
+def test_mamba2_layer_forward_vs_oracle(G, N):
+    torch.manual_seed(11)
+    layer = Mamba2Layer(256, d_state=N, expand=1, headdim=64, ngroups=G, device="cuda", dtype=torch.float32)
+    with torch.no_grad():   # larger dt projections than the default init so the scan dominates the output
+        for lin in layer.dt_proj:
+            lin.weight.normal_(std=0.05)
+    u = torch.randn(2, 97, 256, device="cuda")
+    say(f"Mamba2Layer forward G={G} N={N}")
+    with torch.no_grad():
+        out, cache = layer(u)
+        out2, cache2, hs = layer(u, use_cache=True, return_h_states=True)
+    torch.cuda.synchronize()
+    assert cache is None
+    r_out, r_fin, r_hs, r_x = _layer_ref(layer, u)
+    check("layer out", out, r_out, 1e-4)
+    check("layer out (cache path)", out2, r_out, 1e-4)
+    check("layer h_states", hs, r_hs, 1e-4)
+    check("layer ssm_state", cache2["ssm_state"], r_fin, 1e-4)
+    assert cache2["ssm_state"].shape == (2, 256, N)
+    assert torch.equal(cache2["conv_state"], layer.in_proj(u)[:, -3:, :256])
+
+
+def test_mamba2_layer_prefill_then_step_equals_longer_prefill():
+    torch.manual_seed(12)
+    layer = Mamba2Layer(256, d_state=128, expand=2, headdim=64, ngroups=1, device="cuda", dtype=torch.float32)
+    u = torch.randn(2, 65, 256, device="cuda")
+    say("Mamba2Layer prefill 64 + step vs prefill 65")
+    with torch.no_grad():
+        full, cfull = layer(u, use_cache=True)
+        pre, c = layer(u[:, :64], use_cache=True)
+        step, c2 = layer(u[:, 64:], use_cache=True, cache=c)
+        step2, c3 = layer(u[:, 64:], use_cache=True, cache=c2)   # a second step keeps going
+    torch.cuda.synchronize()
+    check("prefill prefix", pre, host(full[:, :64]), 1e-4)
+    check("step output", step, host(full[:, 64:]), 1e-4)
+    check("step ssm_state", c2["ssm_state"], host(cfull["ssm_state"]), 1e-4)
+    # raw x rows come from in_proj GEMMs of different sizes: equal to fp32 rounding, not bit for bit
+    check("step conv_state", c2["conv_state"], host(cfull["conv_state"]), 1e-5)
+    assert step2.shape == (2, 1, 256) and torch.isfinite(step2).all()
+
+
+def test_mamba2_layer_bf16_runs_the_hip_path():
+    torch.manual_seed(13)
+    layer = Mamba2Layer(512, d_state=128, expand=2, headdim=64, device="cuda", dtype=torch.bfloat16)
+    u = torch.randn(1, 300, 512, device="cuda", dtype=torch.bfloat16)
+    say("Mamba2Layer bf16")
+    with torch.no_grad():
+        out, cache = layer(u, use_cache=True)
+        lay32 = Mamba2Layer(512, d_state=128, expand=2, headdim=64, device="cuda", dtype=torch.float32)
+        lay32.load_state_dict({k: v.float() for k, v in layer.state_dict().items()})
+        out32, _ = lay32(u.float(), use_cache=True)
+    torch.cuda.synchronize()
+    check("bf16 layer vs fp32 layer", out, host(out32), 2e-2)
+    assert cache["ssm_state"].dtype == torch.float32
+
+
+# ----------------------------------------------------------------- KDA state semantics
+
+def _kda_inputs(seed, B=2, H=2, S=40, D=128):
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda: (torch.randn(B, H, S, D, generator=g) / D ** 0.5).to(torch.bfloat16)
+    return mk(), mk(), mk(), mk(), torch.randn(H, generator=g)
+
+
+@pytest.mark.parametrize("K", [128, 64])
+def test_kda_linear_attention_cache_semantics(K):
+    q1, q2, k, v, lr = _kda_inputs(3 + K)
+    B, H, S, D = q1.shape
+    a = {n: t.double().numpy() for n, t in dict(q1=q1, q2=q2, k=k, v=v).items()}
+    say(f"kda_linear_attention K={K}")
+    # no cache: the normalised scan from zero
+    out, c = kda_linear_attention(dev(q1, torch.bfloat16), dev(q2, torch.bfloat16), dev(k, torch.bfloat16),
+                                  dev(v, torch.bfloat16), dev(lr), K)
+    torch.cuda.synchronize()
+    r = okda.ref_attention_scan(a["q1"], a["q2"], a["k"], a["v"], K, lr.double().numpy())
+    check("no-cache output", out, r, 1e-2)
+    assert c is None
+    # multi-token with a cache: outputs ignore S_prev, the cache accumulates it (kda_diff.py:287-338)
+    gs = torch.Generator().manual_seed(99)
+    S_prev = torch.rand(B, H, K, D, generator=gs)
+    z_prev = torch.rand(B, H, K, 1, generator=gs) + 1.0
+    cache = {"S": dev(S_prev), "z": dev(z_prev), "attn_type": "linear"}
+    out2, c2 = kda_linear_attention(dev(q1, torch.bfloat16), dev(q2, torch.bfloat16), dev(k, torch.bfloat16),
+                                    dev(v, torch.bfloat16), dev(lr), K, use_cache=True, cache=cache)
+    torch.cuda.synchronize()
+    check("cached multi-token output", out2, r, 1e-2)
+    _, _, S_sum, z_sum = okda.ref_scan_pair(a["q1"], a["q2"], a["k"], a["v"], K)
+    # bf16 I/O: the scan's MFMAs take phi(k) and v as bf16 operands, so the state is within the bf16 bound
+    check("cache S", c2["S"], S_prev.double().numpy() + S_sum, 1e-2)
+    check("cache z", c2["z"], z_prev.double().numpy() + z_sum[..., None], 1e-2)
+    # one-token step from that cache
+    t1 = lambda x: x[:, :, :1]
+    out3, c3 = kda_linear_attention(dev(t1(q1), torch.bfloat16), dev(t1(q2), torch.bfloat16),
+                                    dev(t1(k), torch.bfloat16), dev(t1(v), torch.bfloat16), dev(lr), K,
+                                    use_cache=True, cache=c2)
+    torch.cuda.synchronize()
+    fm = lambda x: okda.feature_map(x[:, :, :1], K)
+    r3, S3, z3 = okda.ref_attention_recurrent(fm(a["q1"]), fm(a["q2"]), fm(a["k"]), a["v"][:, :, :1],
+                                              host(c2["S"]), host(c2["z"]), lr.double().numpy())
+    check("one-token output", out3, r3, 1e-2)
+    check("one-token cache S", c3["S"], S3, 1e-4)
+    check("one-token cache z", c3["z"], z3, 1e-4)
+    assert c3["attn_type"] == "linear" and c3["S"].shape == (B, H, K, D) and c3["z"].shape == (B, H, K, 1)

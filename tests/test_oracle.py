@@ -289,3 +289,48 @@ def test_feature_map_is_elu_plus_one():
 def test_diff_lambda_clamp():
     lam = kda.diff_lambda(np.array([-10.0, 0.0, 10.0]))
     assert np.allclose(lam, [1 / (1 + np.exp(10)), 0.5, 0.99])
+
+
+# ----------------------------------------------------------------- conv1d and h_states
+
+@pytest.mark.parametrize("K", [1, 2, 4])
+def test_causal_conv1d_matches_numpy_convolve(rng, K):
+    """Causal depthwise conv == per-channel np.convolve with the flipped kernel (cross-correlation), truncated."""
+    x = rng.standard_normal((2, 11, 6))
+    w = rng.standard_normal((6, 1, K))
+    bias = rng.standard_normal(6)
+    out = ssd.ref_causal_conv1d(x, w, bias)
+    exp = np.stack([np.stack([np.convolve(x[b, :, d], w[d, 0, ::-1])[:11] + bias[d] for d in range(6)], -1)
+                    for b in range(2)])
+    assert np.abs(out - exp).max() < 1e-12
+
+
+def test_causal_conv1d_cache_equals_longer_sequence(rng):
+    """With the cached raw rows prepended, the outputs equal the tail of the conv over the whole sequence;
+    a cache shorter than K-1 rows behaves as a zero-padded one (mamba2.py:355, :388-402)."""
+    x = rng.standard_normal((2, 9, 4))
+    w = rng.standard_normal((4, 1, 4))
+    full = ssd.ref_causal_conv1d(x, w)
+    tail = ssd.ref_causal_conv1d(x[:, 6:], w, conv_state=x[:, 3:6])
+    assert np.abs(tail - full[:, 6:]).max() < 1e-12
+    short = ssd.ref_causal_conv1d(x[:, 2:], w, conv_state=x[:, :2])
+    assert np.abs(short - full[:, 2:]).max() < 1e-12
+
+
+def test_planted_unflipped_conv_kernel_is_caught(rng):
+    x = rng.standard_normal((1, 8, 3))
+    w = rng.standard_normal((3, 1, 3))
+    good = ssd.ref_causal_conv1d(x, w)
+    bad = ssd.ref_causal_conv1d(x, w[:, :, ::-1])
+    assert rel_l2(bad, good) > 1e-2
+
+
+@pytest.mark.parametrize("G", [1, 2])
+def test_h_states_bridge_matches_direct(rng, G):
+    """h_states through the reference recurrence (bridge, mean over each group's channels, combined) equals
+    the direct per-token mean of the SSD state; the last row is the mean of the final state."""
+    x, dt, A, B, C, D, _ = ssd_case(rng, G=G)
+    y, fin, hs = ssd.ssd_via_reference(x, dt, A, B, C, D, return_h_states=True)
+    hs2 = ssd.ssd_h_states(x, dt, A, B)
+    assert rel_l2(hs, hs2) < 1e-12
+    assert np.abs(hs[:, -1] - fin.mean(axis=(1, 2))).max() < 1e-12
