@@ -214,7 +214,8 @@ int mh_ssd_workspace_bytes(const mh_ssd_args* a, size_t* bytes) {
   int rc = ssd_validate(a, &cl);
   if (rc) return rc;
   const int64_t nchunks = (a->seqlen + cl - 1) / cl;
-  *bytes = mh::ssd_workspace_bytes((int)a->batch, (int)nchunks, (int)a->nheads, (int)a->headdim, (int)a->dstate);
+  *bytes = mh::ssd_workspace_bytes((int)a->batch, (int)a->seqlen, (int)nchunks, (int)a->nheads, (int)a->headdim,
+                                   (int)a->dstate, (int)a->ngroups, a->dtype);
   return MH_OK;
 }
 
@@ -223,7 +224,8 @@ int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream) {
   int rc = ssd_validate(a, &cl);
   if (rc) return rc;
   const int64_t nchunks = (a->seqlen + cl - 1) / cl;
-  const size_t need = mh::ssd_workspace_bytes((int)a->batch, (int)nchunks, (int)a->nheads, (int)a->headdim, (int)a->dstate);
+  const size_t need = mh::ssd_workspace_bytes((int)a->batch, (int)a->seqlen, (int)nchunks, (int)a->nheads,
+                                              (int)a->headdim, (int)a->dstate, (int)a->ngroups, a->dtype);
   if (nchunks > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
     return fail(MH_ERR_WORKSPACE, "ssd: workspace of %zu bytes (16-byte aligned) required, got %zu", need, a->workspace_bytes);
   mh::SsdParams p;
@@ -243,10 +245,16 @@ int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream) {
   p.D = a->D; p.dt_bias = a->dt_bias; p.init_state = a->initial_state;
   p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l; p.y_sh = a->y_stride_h;
   p.final_state = a->final_state;
+  p.nseg = (int)((a->seqlen + 63) / 64);
   if (nchunks > 0) {
     const size_t states = (size_t)a->batch * nchunks * a->nheads * a->headdim * a->dstate * sizeof(float);
-    p.chunk_states = reinterpret_cast<float*>(a->workspace);
-    p.chunk_decay = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + ((states + 255) / 256) * 256);
+    const size_t decay = (size_t)a->batch * a->nheads * nchunks * sizeof(float);
+    char* ws = reinterpret_cast<char*>(a->workspace);
+    p.chunk_states = reinterpret_cast<float*>(ws);
+    p.chunk_decay = reinterpret_cast<float*>(ws + ((states + 255) / 256) * 256);
+    p.seg_frags = ws + ((states + 255) / 256) * 256 + ((decay + 255) / 256) * 256;
+    const size_t frags = (size_t)a->batch * a->ngroups * p.nseg * mh::ssd_frag_bytes(a->dtype, (int)a->dstate);
+    p.entering = reinterpret_cast<char*>(p.seg_frags) + ((frags + 255) / 256) * 256;
   }
   return hip_status(mh::launch_ssd(p, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_fwd");
 }

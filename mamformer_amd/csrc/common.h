@@ -108,6 +108,26 @@ __device__ __forceinline__ float wave_incl_scan(float v) {
   }
   return v;
 }
+// Same scan on the DPP crossbar (row shifts within 16-lane rows, then the row
+// broadcasts of lanes 15 and 31): six dependent VALU ops instead of six LDS
+// permutes.
+__device__ __forceinline__ float wave_incl_scan_dpp(float v) {
+  int iv;
+  iv = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, false);   // row_shr:1
+  v += __int_as_float(iv);
+  iv = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xf, 0xf, false);   // row_shr:2
+  v += __int_as_float(iv);
+  iv = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xf, false);   // row_shr:4
+  v += __int_as_float(iv);
+  iv = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xf, 0xf, false);   // row_shr:8
+  v += __int_as_float(iv);
+  iv = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false);   // row_bcast:15 -> rows 1, 3
+  v += __int_as_float(iv);
+  iv = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, false);   // row_bcast:31 -> rows 2, 3
+  v += __int_as_float(iv);
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -122,6 +142,15 @@ __device__ __forceinline__ float wave_min(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
   return v;
+}
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations,
+// then s_barrier.  __syncthreads() also carries a workgroup release fence, which
+// on gfx950 waits for every outstanding global load and store (vmcnt(0)) --
+// including asynchronous prefetches meant to overlap the compute that follows.
+// Callers that need prefetched data (global_load_lds) wait for vmcnt themselves.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // softplus with PyTorch's default threshold (x > 20 -> x).

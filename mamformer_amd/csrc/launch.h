@@ -47,9 +47,14 @@ struct SsdParams {
   float* final_state;
   float* chunk_states;   // workspace: [batch][nchunks][nheads][headdim][dstate]
   float* chunk_decay;    // workspace: [batch][nheads][nchunks]  (sum of A*dt over the chunk)
+  void* seg_frags;       // workspace: [batch][ngroups][nseg] shared MFMA fragments of each 64-token segment
+  void* entering;        // workspace (bf16 I/O): bf16 entering states, chunk_states order
+  int nseg;              // ceil(seqlen / 64)
 };
 hipError_t launch_ssd(const SsdParams& p, hipStream_t st);
-size_t ssd_workspace_bytes(int batch, int nchunks, int nheads, int headdim, int dstate);
+size_t ssd_frag_bytes(int dtype, int dstate);
+size_t ssd_workspace_bytes(int batch, int seqlen, int nchunks, int nheads, int headdim, int dstate, int ngroups,
+                           int dtype);
 
 // ------------------------------------------------------------- KDA
 struct KdaParams {

@@ -7,37 +7,40 @@
 // per-head SSD parameterisation, with an optional initial state (prefill of a
 // cached sequence) and the final state returned for the decode cache.
 //
-// Decomposition (three launches on the caller's stream):
+// Decomposition (four launches on the caller's stream):
+//   0. ssd_seg_frags    grid (nseg, G, b): per 64-token segment of each group, the
+//      MFMA operand fragments every head of the group shares -- B^T (n x token)
+//      and the causally masked (C B^T)^T tile -- written once to the workspace.
 //   1. ssd_chunk_state  grid (nchunks, H/HG, b): the chunk-local final state
 //          S_k[p, n] = sum_{s in k} exp(sum_{s<tau in k} A dt_tau) dt_s x_s[p] B_s[n]
-//      and the chunk's total log-decay T_k, walking the chunk forwards in
-//      64-token segments with S in MFMA accumulators.
+//      and the chunk's total log-decay T_k, walking the chunk in 64-token segments
+//      with S in MFMA accumulators.
 //   2. ssd_state_pass   elementwise over (b, h, P*N): H_0 = h0, H_{k+1} = e^{T_k} H_k + S_k.
 //      Writes the *entering* state H_k over S_k and the final state.
 //   3. ssd_chunk_scan   grid (nchunks, H/HG, b): walks the chunk in 64-token
-//      segments with the running state H in MFMA accumulators.  With cs_t the
+//      segments with the running state in MFMA accumulators.  With cs_t the
 //      in-segment inclusive cumulative log-decay (cs_t <= 0, non-increasing):
 //          y_t  = e^{cs_t} C_t H^T + sum_{s<=t} e^{cs_t - cs_s} (C_t . B_s) dt_s x_s + D x_t
 //          H   <- e^{cs_end} H + sum_s e^{cs_end - cs_s} dt_s x_s B_s^T
-//      Every factor of the state update is <= 1.  The intra-segment term is
-//      factorised as e^{cs_t - m} * e^{m - cs_s} around the midpoint m of the
-//      segment's log-decay range when that range is <= FACT_RANGE (both factors
-//      within e^{+-30}), so the masked C B^T tile is shared by all heads of a
-//      group; a segment with a wider range (very strong decay) takes an
-//      exact per-element e^{cs_t - cs_s} path instead (wave-uniform branch).
+//      The state is carried lazily as H_true = e^kappa H, so a segment needs one
+//      scaled operand xs_s = e^{-kappa - cs_s} dt_s x_s for both terms:
+//          y_t = e^{kappa + cs_t} (C_t H^T + sum_{s<=t} M[t][s] xs_s),  H += B^T xs,  kappa += cs_end
+//      and H is rescaled only when a factor would pass e^{FACT_RANGE}.  A segment
+//      whose own decay range exceeds FACT_RANGE takes an exact path with the
+//      per-element factor e^{cs_t - cs_s} (wave-uniform branch).
 // Work split: a workgroup owns HG heads of one group with two waves per head;
 // wave w handles head w / 2 and the 32 state columns p of half w % 2, so each
-// wave's state is N/32 accumulator tiles.  C B^T (three 32x32 tiles) and the
-// B^T fragments are computed once per segment and shared by all waves.
-// Transposes needed by the token-contracted MFMAs (B^T, x^T) are done on the
-// MFMA unit itself: a row-loaded tile times an identity fragment lands in the
-// accumulator layout that the next MFMA consumes.
-// Memory: tiles of the next segment are fetched straight into a second LDS
-// buffer (global_load_lds_dwordx4, no register staging) while the current one
-// is computed.  Each wave owns the 32-column half of its head's x tile that it
-// reads, so it stages its y columns in place of x and writes them to HBM one
-// segment later, after the next segment's fetch has been issued: no wave ever
-// waits for its own y stores.  LDS tiles are XOR-swizzled per row for
+// wave's state is N/32 accumulator tiles.  Transposes needed by the
+// token-contracted MFMAs (B^T, x^T) are done on the MFMA unit itself: a
+// row-loaded tile times an identity fragment lands in the accumulator layout
+// that the next MFMA consumes.
+// Memory: every segment's inputs (shared fragments, C tile, x tile, dt) are
+// fetched straight into LDS (global_load_lds, no register staging) one or two
+// segments ahead of their use, and waited for with vmcnt only where consumed;
+// barriers inside the loops order LDS traffic only (no memory fence, which
+// would also wait for the prefetch).  Each wave owns the 32-column half of its
+// head's x tile, so it stages its y columns in place of x and writes them to
+// HBM one segment later.  LDS tiles are XOR-swizzled per row for
 // conflict-free fragment reads; the chunk-state workspace is kept in MFMA
 // fragment order (64 contiguous bytes per lane).
 // bf16 I/O uses 32x32x16 bf16 MFMAs, fp32 I/O 32x32x2 fp32 MFMAs; accumulation is fp32.
@@ -48,18 +51,26 @@ namespace mh {
 
 constexpr int SEG = 64;              // tokens per segment
 constexpr int HD = 64;               // headdim handled by these kernels
-constexpr float FACT_RANGE = 60.f;   // max in-segment log-decay range of the factorised intra-segment path
+constexpr float FACT_RANGE = 60.f;   // max exponent of an operand scale factor
 
 // ------------------------------------------------------------------ helpers
 
-__device__ __forceinline__ float process_dt(const SsdParams& p, float dt, int h) {
-  if (p.dt_bias) dt += p.dt_bias[h];
+__device__ __forceinline__ float process_dt(const SsdParams& p, float dt, float bias) {
+  dt += bias;
   if (p.dt_softplus) dt = softplus_f(dt);
   if (p.has_dt_limit) dt = fminf(fmaxf(dt, p.dt_min), p.dt_max);
   return dt;
 }
 
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// vmcnt(n) through the builtin (vmcnt n, expcnt 7, lgkmcnt 15), so the compiler's own wait tracking
+// knows the counter state.  Loads complete in issue order: vmcnt(n) waits for all but the n most recent.
+template <int n>
+__device__ __forceinline__ void wait_vmem_n() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00);
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void wait_vmem() { wait_vmem_n<0>(); }
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -134,6 +145,20 @@ __device__ __forceinline__ void fetch_xhalf(T* dst, const T* src, int64_t row_st
     T* d = dst + blk * (1024 / (int)sizeof(T));
     __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)d, 16, 0, 0);
   }
+}
+
+// Direct fetch of the raw dt of 64 tokens (lane = token, rows past the end clamped) into LDS.
+__device__ __forceinline__ void fetch_dt(float* dst, const float* src, int64_t stride, int tok0, int last_tok,
+                                         int lane) {
+  __builtin_amdgcn_global_load_lds((glb_void_t*)(src + (int64_t)min(tok0 + lane, last_tok) * stride),
+                                   (lds_void_t*)dst, 4, 0, 0);
+}
+
+// Direct copy of nb contiguous 1 KB blocks starting at block b0 (precomputed fragments).
+__device__ __forceinline__ void fetch_blocks(char* dst, const char* src, int b0, int nb, int lane) {
+  for (int q = 0; q < nb; ++q)
+    __builtin_amdgcn_global_load_lds((glb_void_t*)(src + (b0 + q) * 1024 + 16 * lane),
+                                     (lds_void_t*)(dst + (b0 + q) * 1024), 16, 0, 0);
 }
 
 // Write the y rows [0, len) staged in a wave's x half tile to HBM (16-byte stores).
@@ -233,10 +258,10 @@ __device__ __forceinline__ f32x16 mfma_transpose(const T* tile, int r0, int q0, 
 }
 
 // x^T of a wave's x half tile (lane = p, tokens on the k axis, KSET order) as
-// two sets of 4 fragments: xa scaled per token by sa[], xb scaled by sb[].
-template <typename TM, typename T, bool TWO>
-__device__ __forceinline__ void xt_frags(const T* xtile, const float* sa, const float* sb, const Frag<TM> (&id)[2],
-                                         int half, int l32, Frag<TM> (&xa)[4], Frag<TM> (&xb)[4]) {
+// 4 fragments, each token scaled by sa[token].
+template <typename TM, typename T>
+__device__ __forceinline__ void xt_frags(const T* xtile, const float* sa, const Frag<TM> (&id)[2], int half, int l32,
+                                         Frag<TM> (&xa)[4]) {
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
     f32x16 xt = zero16();
@@ -248,125 +273,154 @@ __device__ __forceinline__ void xt_frags(const T* xtile, const float* sa, const 
       kset_vals(sa, 2 * st + c, half, s);
 #pragma unroll
       for (int j = 0; j < 8; ++j) xa[2 * st + c].set(j, xt[8 * c + j] * s[j]);
-      if constexpr (TWO) {
-        kset_vals(sb, 2 * st + c, half, s);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xb[2 * st + c].set(j, xt[8 * c + j] * s[j]);
-      }
     }
   }
 }
 
-// Shared per-segment MFMA work of a workgroup of NW waves: the three C B^T
-// tiles (N/16 MFMAs each, k-reductions, one wave each) and the 2 * N/32 B^T
-// blocks (2 MFMAs each), spread so the busiest wave does one C B^T tile.
-template <int NW, int N, bool CB>
-struct SharedWork {
-  static constexpr int NBLK = 2 * (N / 32);
-  static constexpr int NCB = CB ? 3 : 0;
-  static constexpr int CBW = !CB ? 0 : (NW < 3 ? NW : 3);          // waves that own C B^T tiles
-  static constexpr int BTW = (NW > CBW) ? NW - CBW : NW;          // waves that own B^T blocks
-  static constexpr int BTP = (NBLK + BTW - 1) / BTW;
-  static constexpr int CBPER = CB ? (3 + CBW - 1) / CBW : 0;
-  __device__ static __forceinline__ int cb_tile(int w, int i) { return (w < CBW) ? w + i * CBW : 99; }
-  __device__ static __forceinline__ int bt_block(int w, int i) {
-    if (NW > CBW) return (w >= CBW) ? (w - CBW) + i * BTW : 99;
-    return w + i * NW;
-  }
-};
-
-// B^T A-operand fragments (row n, k = token via KSET) of one segment, in LDS.
+// Operand fragments one segment of a group shares among all its heads, in the
+// layout written by ssd_seg_frags and copied verbatim (1 KB blocks) into LDS:
+//   bt[nt][c][lane]  B^T A-operand fragment (row n = 32 nt + lane % 32, k = token 16 c + KSET)
+//   cb[ti][c][lane]  masked (C B^T)^T tile ti in {(s 0, t 0), (s 0, t 1), (s 1, t 1)} as a
+//                    B-operand fragment (column t, k = token s 16 c + KSET within the s-tile)
 template <typename TM, int N>
-struct BtFrags {
-  Frag<TM> f[N / 32][4][64];   // n-tile, k-step (16 tokens), lane
+struct SegFrags {
+  Frag<TM> bt[N / 32][4][64];
+  Frag<TM> cb[3][2][64];
 };
-
-// Compute the B^T blocks a wave owns and store them as fragments.
-template <typename T, typename TM, int N, int NW, bool CB>
-__device__ __forceinline__ void bt_work(const T* Bs, BtFrags<TM, N>& bt, int w, const Frag<TM> (&id)[2], int half,
-                                        int l32, int l) {
-  using SW = SharedWork<NW, N, CB>;
-#pragma unroll
-  for (int i = 0; i < SW::BTP; ++i) {
-    const int blk = SW::bt_block(w, i);
-    if (blk < SW::NBLK) {
-      const f32x16 acc = mfma_transpose<TM, T, N>(Bs, 32 * (blk & 1), 32 * (blk >> 1), id, half, l32);
-      bt.f[blk >> 1][2 * (blk & 1)][l] = acc_to_frag<TM>(acc, 0);
-      bt.f[blk >> 1][2 * (blk & 1) + 1][l] = acc_to_frag<TM>(acc, 1);
-    }
-  }
-}
+template <typename TM, int N>
+constexpr int frag_blocks = (int)(sizeof(SegFrags<TM, N>) / 1024);
+template <typename TM, int N>
+constexpr int bt_blocks = (int)(sizeof(Frag<TM>) * (N / 32) * 4 * 64 / 1024);
+static_assert(sizeof(SegFrags<bf16, 128>) % 1024 == 0 && sizeof(SegFrags<float, 64>) % 1024 == 0, "1 KB blocks");
 
 // Per-stage tiles.
-template <typename T, int N, int HG>
+template <typename T, typename TM, int N, int HG>
 struct ScanStage {
-  T B[SEG * N];
+  SegFrags<TM, N> fr;
   T C[SEG * N];
   T X[2 * HG][SEG * 32];      // per wave: its half of its head's x tile (y staged in place)
+  float dt[2 * HG][SEG];      // per wave: raw dt of its head for the segment's tokens
 };
-template <typename T, int N, int HG>
+template <typename T, typename TM, int N, int HG>
 struct StateStage {
-  T B[SEG * N];
+  Frag<TM> bt[N / 32][4][64];
   T X[2 * HG][SEG * 32];
+  float dt[2 * HG][SEG];
 };
 
 template <typename T, typename TM, int N, int HG, int NBUF>
 struct ScanSmem {
-  ScanStage<T, N, HG> st[NBUF];
-  BtFrags<TM, N> bt;
-  Frag<TM> CB[3][2][64];      // masked (C B^T)^T tiles as B-operand fragments: tile, k-step, lane
-  float sa[2 * HG][SEG];      // per wave: operand scale of the intra-segment term
-  float sb[2 * HG][SEG];      // per wave: decay to the segment end, e^{cs_end - cs_s} (exact path)
+  ScanStage<T, TM, N, HG> st[NBUF];
+  float sa[2 * HG][SEG];      // per wave: per-token operand scale
   float cs[2 * HG][SEG];      // per wave: in-segment cumulative log-decay
   float dcol[HG][HD];         // D per column of each head
 };
 template <typename T, typename TM, int N, int HG, int NBUF>
 struct StateSmem {
-  StateStage<T, N, HG> st[NBUF];
-  BtFrags<TM, N> bt;
+  StateStage<T, TM, N, HG> st[NBUF];
   float sb[2 * HG][SEG];
 };
 
-// Tiles are double-buffered (the next segment fetched during this one's
-// compute) where two buffers fit in the 160 KB of LDS, else single-buffered.
+// Tiles are fetched ahead into as many stages as fit in the 160 KB of LDS.
 constexpr size_t LDS_BYTES = 160 * 1024;
 template <typename T, typename TM, int N, int HG>
 constexpr int scan_nbuf = sizeof(ScanSmem<T, TM, N, HG, 2>) <= LDS_BYTES ? 2 : 1;
 template <typename T, typename TM, int N, int HG>
-constexpr int state_nbuf = sizeof(StateSmem<T, TM, N, HG, 2>) <= LDS_BYTES ? 2 : 1;
+constexpr int state_nbuf = sizeof(StateSmem<T, TM, N, HG, 3>) <= LDS_BYTES ? 3
+                           : (sizeof(StateSmem<T, TM, N, HG, 2>) <= LDS_BYTES ? 2 : 1);
 
 // Offset (floats) of state tile (nt, pt) element block of lane l in the fragment-native workspace order.
 __device__ __forceinline__ int frag_off(int nt, int pt, int l) { return ((nt * 2 + pt) * 64 + l) * 16; }
 
-// In-segment decay of one head (lane = token of the segment starting at pos,
-// tokens at or past c1 have dt = 0): returns cs_t (inclusive cumulative log-decay).
-__device__ __forceinline__ float seg_decay(const SsdParams& p, float dtraw, int h, float Ah, int t, int c1,
+// In-segment decay of one head (lane = token; tokens at or past c1 have dt = 0):
+// returns cs_t, the inclusive cumulative log-decay.
+__device__ __forceinline__ float seg_decay(const SsdParams& p, float dtraw, float bias, float Ah, int t, int c1,
                                            float& dtv) {
-  dtv = (t < c1) ? process_dt(p, dtraw, h) : 0.f;
-  return wave_incl_scan(Ah * dtv);
+  dtv = (t < c1) ? process_dt(p, dtraw, bias) : 0.f;
+  return wave_incl_scan_dpp(Ah * dtv);
 }
 
-// State read-out of one wave for one 32-token t-tile (rows tl of the C tile):
-// Y^T[p][t] += sum_n H[p][n] C^T[n][t], H as A operand straight from the accumulators.
+// State read-out of one wave: Y^T[p][t] += sum_n H[p][n] C^T[n][t] for the two 32-token t-tiles of the
+// segment (H as A operand straight from the accumulators, converted once for both).
 template <typename TM, typename T, int N>
-__device__ __forceinline__ void readout(const f32x16 (&H)[N / 32], const T* Cs, int tl, int half, f32x16& Y) {
+__device__ __forceinline__ void readout(const f32x16 (&H)[N / 32], const T* Cs, int l32, int half, f32x16& Y0,
+                                        f32x16& Y1) {
 #pragma unroll
   for (int nt = 0; nt < N / 32; ++nt)
 #pragma unroll
-    for (int c = 0; c < 2; ++c) Y = mma(acc_to_frag<TM>(H[nt], c), kset_frag<TM, T, N>(Cs, tl, 32 * nt + 16 * c, half), Y);
+    for (int c = 0; c < 2; ++c) {
+      const Frag<TM> hf = acc_to_frag<TM>(H[nt], c);
+      Y0 = mma(hf, kset_frag<TM, T, N>(Cs, l32, 32 * nt + 16 * c, half), Y0);
+      Y1 = mma(hf, kset_frag<TM, T, N>(Cs, 32 + l32, 32 * nt + 16 * c, half), Y1);
+    }
 }
 
 // H[n][p] += sum_s B^T[n][s] xf[s][p] over the segment's 64 tokens.
 template <typename TM, int N>
-__device__ __forceinline__ void state_update(f32x16 (&H)[N / 32], const BtFrags<TM, N>& bt, const Frag<TM> (&xf)[4],
-                                             int l) {
+__device__ __forceinline__ void state_update(f32x16 (&H)[N / 32], const Frag<TM> (&bt)[N / 32][4][64],
+                                             const Frag<TM> (&xf)[4], int l) {
 #pragma unroll
   for (int nt = 0; nt < N / 32; ++nt) {
     Frag<TM> btf[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) btf[c] = bt.f[nt][c][l];
+    for (int c = 0; c < 4; ++c) btf[c] = bt[nt][c][l];
 #pragma unroll
     for (int c = 0; c < 4; ++c) H[nt] = mma(btf[c], xf[c], H[nt]);
+  }
+}
+
+// Workspace layout: [chunk states][chunk log-decays][segment fragments], each 256-byte aligned.
+__host__ __device__ __forceinline__ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// ------------------------------------------------------------------ kernel 0
+
+// One workgroup of 8 waves per (segment, group, batch): 3 + 2 N/32 work items
+// (the C B^T tiles and the B^T blocks), wave w taking items w and w + 8.
+template <typename T, typename TM, int N>
+__global__ __launch_bounds__(512) void ssd_seg_frags_kernel(SsdParams p) {
+  using TB = Tile<T, N>;
+  static_assert(TB::NBLK % 8 == 0, "B and C tiles split evenly over 8 waves");
+  __shared__ T Bs[SEG * N];
+  __shared__ T Cs[SEG * N];
+  const int sgi = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
+  const int tok0 = sgi * SEG;
+  const int len = min(SEG, p.seqlen - tok0);
+  const int last = p.seqlen - 1;
+  const T* Bg = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)g * N;
+  const T* Cg = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb + (int64_t)g * N;
+  constexpr int BPW = TB::NBLK / 8;
+  fetch_tile<T, N>(Bs, Bg, p.B_sl, tok0, last, w * BPW, BPW, l);
+  fetch_tile<T, N>(Cs, Cg, p.C_sl, tok0, last, w * BPW, BPW, l);
+  wait_vmem();
+  lds_barrier();
+  Frag<TM> id[2];
+  id[0] = ident_frag<TM>(0, half, l32);
+  id[1] = ident_frag<TM>(1, half, l32);
+  auto* out = reinterpret_cast<SegFrags<TM, N>*>(p.seg_frags) + ((int64_t)b * p.ngroups + g) * p.nseg + sgi;
+  constexpr int NBT = 2 * (N / 32);
+  for (int it = w; it < 3 + NBT; it += 8) {
+    if (it < 3) {
+      const int st = (it == 2) ? 1 : 0, tt = (it == 0) ? 0 : 1;
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int c = 0; c < N / 16; ++c)
+        acc = mma(row_frag<TM, T, N>(Bs, 32 * st + l32, 16 * c + 8 * half),
+                  row_frag<TM, T, N>(Cs, 32 * tt + l32, 16 * c + 8 * half), acc);
+      const int tl = 32 * tt + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int s = 32 * st + acc_row(half, r);
+        if (!(s <= tl && s < len)) acc[r] = 0.f;
+      }
+      out->cb[it][0][l] = acc_to_frag<TM>(acc, 0);
+      out->cb[it][1][l] = acc_to_frag<TM>(acc, 1);
+    } else {
+      const int blk = it - 3;
+      const f32x16 acc = mfma_transpose<TM, T, N>(Bs, 32 * (blk & 1), 32 * (blk >> 1), id, half, l32);
+      out->bt[blk >> 1][2 * (blk & 1)][l] = acc_to_frag<TM>(acc, 0);
+      out->bt[blk >> 1][2 * (blk & 1) + 1][l] = acc_to_frag<TM>(acc, 1);
+    }
   }
 }
 
@@ -375,11 +429,15 @@ __device__ __forceinline__ void state_update(f32x16 (&H)[N / 32], const BtFrags<
 template <typename T, typename TM, int N, int HG>
 __global__ __launch_bounds__(128 * HG) void ssd_chunk_state_kernel(SsdParams p) {
   constexpr int NBUF = state_nbuf<T, TM, N, HG>;
+  constexpr int DIST = NBUF - 1;                           // segments fetched ahead (0: fetch-then-wait)
   using SM = StateSmem<T, TM, N, HG, NBUF>;
   __shared__ SM sm;
   constexpr int NT = N / 32, NW = 2 * HG;
-  using TB = Tile<T, N>;
-  constexpr int BPW = (TB::NBLK + NW - 1) / NW;            // B blocks fetched per wave
+  using TX = XHalf<T>;
+  constexpr int FB = bt_blocks<TM, N>;
+  static_assert(FB % NW == 0, "every wave fetches the same number of fragment blocks");
+  constexpr int BPW = FB / NW;
+  constexpr int LOADS = BPW + TX::NBLK + 1;                // loads one wave issues per segment
   const int k = blockIdx.x, b = blockIdx.z;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
   const int j = w >> 1, ph = w & 1;
@@ -389,62 +447,88 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_state_kernel(SsdParams p) 
   const int c1 = min(p.seqlen, c0 + p.chunk_len);
   const int last = p.seqlen - 1;
   const float Ah = p.A[h];
+  const float dtb = p.dt_bias ? p.dt_bias[h] : 0.f;
   const T* xg = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + 32 * ph;
-  const T* Bg = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)g * N;
   const float* dtg = p.dt + (int64_t)b * p.dt_sb + h;
-  const int b0 = w * BPW, nb = max(0, min(BPW, TB::NBLK - b0));
+  const char* fg = reinterpret_cast<const char*>(reinterpret_cast<const SegFrags<TM, N>*>(p.seg_frags) +
+                                                 ((int64_t)b * p.ngroups + g) * p.nseg + c0 / SEG);
   Frag<TM> id[2];
   id[0] = ident_frag<TM>(0, half, l32);
   id[1] = ident_frag<TM>(1, half, l32);
 
+  // S_true = e^kappa * S (kappa <= 0 carried lazily; S is rescaled only when a factor would
+  // pass e^{FACT_RANGE}), so a segment adds B^T (e^{-kappa - cs_s} dt_s x_s) without touching S.
   f32x16 S[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) S[nt] = zero16();
-  float total = 0.f;
+  float kappa = 0.f, total = 0.f;
 
   const int nseg = (c1 - c0 + SEG - 1) / SEG;
-  float dtraw = (c0 + l < c1) ? dtg[(int64_t)(c0 + l) * p.dt_sl] : 0.f;
-  fetch_tile<T, N>(sm.st[0].B, Bg, p.B_sl, c0, last, b0, nb, l);
-  fetch_xhalf<T>(sm.st[0].X[w], xg, p.x_sl, c0, last, l);
+  // every wave issues exactly LOADS loads per segment (rows past the end are clamped), so vmcnt counts them
+  // (issued in two parts so the x half can be spread into the compute of the current segment)
+  auto fetch_a = [&](int seg) {
+    auto& sg = sm.st[seg % NBUF];
+    fetch_blocks(reinterpret_cast<char*>(sg.bt), fg + (size_t)seg * sizeof(SegFrags<TM, N>), w * BPW, BPW, l);
+    fetch_dt(sg.dt[w], dtg, p.dt_sl, c0 + seg * SEG, last, l);
+  };
+  auto fetch_b = [&](int seg) { fetch_xhalf<T>(sm.st[seg % NBUF].X[w], xg, p.x_sl, c0 + seg * SEG, last, l); };
+  auto fetch = [&](int seg) { fetch_a(seg); fetch_b(seg); };
+#pragma unroll
+  for (int d = 0; d < (DIST > 0 ? DIST : 1); ++d)          // segments 0 .. DIST-1 in flight before the loop
+    if (d < nseg) fetch(d);
+
   for (int si = 0; si < nseg; ++si) {
+    // lane-dependent LDS addresses are recomputed each segment instead of hoisted (and spilled)
     int lq = l;
     asm volatile("" : "+v"(lq));
     const int ll = lq, halfq = lq >> 5, l32q = lq & 31;
     const int pos = c0 + si * SEG;
-    const int cur = (NBUF == 2) ? (si & 1) : 0;
-    auto& sg = sm.st[cur];
-    if constexpr (NBUF == 1) {
+    auto& sg = sm.st[si % NBUF];
+    if constexpr (DIST == 0) {
       if (si > 0) {
-        __syncthreads();                                   // every wave is done with the previous tiles
-        fetch_tile<T, N>(sg.B, Bg, p.B_sl, pos, last, b0, nb, ll);
-        fetch_xhalf<T>(sg.X[w], xg, p.x_sl, pos, last, ll);
+        lds_barrier();                                     // every wave is done with the previous tiles
+        fetch(si);
       }
     }
-    wait_vmem();
-    __syncthreads();                                       // tiles of this segment are in LDS
-    float dtn = 0.f;
-    if constexpr (NBUF == 2) {
-      if (si + 1 < nseg) {                                 // fetch the next segment into the other buffer
-        auto& ng = sm.st[cur ^ 1];
-        fetch_tile<T, N>(ng.B, Bg, p.B_sl, pos + SEG, last, b0, nb, ll);
-        fetch_xhalf<T>(ng.X[w], xg, p.x_sl, pos + SEG, last, ll);
-      }
+    if (DIST == 2 && si + 1 < nseg) wait_vmem_n<LOADS>();  // this segment's loads; the next one's may fly
+    else wait_vmem();
+    lds_barrier();                                         // this segment's tiles are in LDS
+    if constexpr (DIST > 0) {
+      if (si + DIST < nseg) fetch_a(si + DIST);
     }
-    if (si + 1 < nseg && pos + SEG + l < c1) dtn = dtg[(int64_t)(pos + SEG + l) * p.dt_sl];
     float dtv;
-    const float cs = seg_decay(p, dtraw, h, Ah, pos + l, c1, dtv);
+    const float cs = seg_decay(p, sg.dt[w][ll], dtb, Ah, pos + l, c1, dtv);
     const float cse = __shfl(cs, 63, 64);
-    sm.sb[w][ll] = __expf(cse - cs) * dtv;
-    bt_work<T, TM, N, NW, false>(sg.B, sm.bt, w, id, halfq, l32q, ll);
-    __syncthreads();                                       // B^T fragments and scales visible
+    float wsc;                                             // per-token operand scale (wave-uniform choice)
+    if (-cse > FACT_RANGE) {                               // very strong decay: carry S exactly through it
+      const float e = __expf(kappa + cse);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) S[nt] *= e;
+      kappa = 0.f;
+      wsc = __expf(cse - cs);
+    } else {
+      if (-(kappa + cse) > FACT_RANGE) {                   // renormalise: S_true = e^kappa S
+        const float e = __expf(kappa);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) S[nt] *= e;
+        kappa = 0.f;
+      }
+      wsc = __expf(-kappa - cs);
+      kappa += cse;
+    }
+    sm.sb[w][ll] = wsc * dtv;                              // wave-private: read back by this wave only
     Frag<TM> xw[4];
-    xt_frags<TM, T, false>(sg.X[w], sm.sb[w], nullptr, id, halfq, l32q, xw, xw);
-    const float e = __expf(cse);
+    xt_frags<TM, T>(sg.X[w], sm.sb[w], id, halfq, l32q, xw);
+    if constexpr (DIST > 0) {
+      if (si + DIST < nseg) fetch_b(si + DIST);
+    }
+    state_update<TM, N>(S, sg.bt, xw, ll);
+    total += cse;
+  }
+  {
+    const float e = __expf(kappa);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) S[nt] *= e;
-    state_update<TM, N>(S, sm.bt, xw, ll);
-    total += cse;
-    dtraw = dtn;
   }
 
   float* out = p.chunk_states + (((int64_t)b * p.nchunks + k) * p.nheads + h) * (HD * N);
@@ -470,6 +554,9 @@ __device__ __forceinline__ int canon_index(int e, int N) {
   return (32 * pt + (lane & 31)) * N + 32 * nt + acc_row(lane >> 5, r);
 }
 
+// Entering states for the scan kernel: fp32 in place of S_k, or (bf16 I/O, where the scan consumes
+// the state as bf16 MFMA operands) bf16 in a separate array of the same fragment order.
+template <typename TE>
 __global__ __launch_bounds__(256) void ssd_state_pass_kernel(SsdParams p) {
   const int bh = blockIdx.y;
   const int b = bh / p.nheads, h = bh - b * p.nheads;
@@ -482,9 +569,17 @@ __global__ __launch_bounds__(256) void ssd_state_pass_kernel(SsdParams p) {
   if (p.init_state) H = *reinterpret_cast<const f32x4*>(p.init_state + (int64_t)bh * per + ci);
   const float* dec = p.chunk_decay + (int64_t)bh * p.nchunks;
   for (int k = 0; k < p.nchunks; ++k) {
-    float* sp = p.chunk_states + (((int64_t)b * p.nchunks + k) * p.nheads + h) * per + e4;
+    const int64_t idx = (((int64_t)b * p.nchunks + k) * p.nheads + h) * per + e4;
+    float* sp = p.chunk_states + idx;
     const f32x4 S = *reinterpret_cast<const f32x4*>(sp);
-    *reinterpret_cast<f32x4*>(sp) = H;
+    if constexpr (sizeof(TE) == 4) {
+      *reinterpret_cast<f32x4*>(sp) = H;
+    } else {
+      bf16x4 hb;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hb[i] = (bf16)H[i];
+      *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(p.entering) + idx) = hb;
+    }
     const float a = __expf(dec[k]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) H[i] = a * H[i] + S[i];
@@ -498,11 +593,14 @@ template <typename T, typename TM, int N, int HG>
 __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
   constexpr int NBUF = scan_nbuf<T, TM, N, HG>;
   using SM = ScanSmem<T, TM, N, HG, NBUF>;
+  using Stage = ScanStage<T, TM, N, HG>;
   constexpr int NT = N / 32, NW = 2 * HG;
-  using SW = SharedWork<NW, N, true>;
   using TB = Tile<T, N>;
   using TX = XHalf<T>;
-  constexpr int BPW = (TB::NBLK + NW - 1) / NW;            // B and C blocks fetched per wave
+  constexpr int FB = frag_blocks<TM, N>;
+  constexpr int FPW = (FB + NW - 1) / NW;                  // fragment blocks fetched per wave (the last ones fewer)
+  static_assert(TB::NBLK % NW == 0, "C blocks split evenly over the waves");
+  constexpr int CPW = TB::NBLK / NW;
   __shared__ SM sm;
   const int k = blockIdx.x, b = blockIdx.z;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
@@ -513,12 +611,14 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
   const int c1 = min(p.seqlen, c0 + p.chunk_len);
   const int last = p.seqlen - 1;
   const float Ah = p.A[h];
+  const float dtb = p.dt_bias ? p.dt_bias[h] : 0.f;
   const T* xg = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + 32 * ph;
-  const T* Bg = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)g * N;
   const T* Cg = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb + (int64_t)g * N;
   const float* dtg = p.dt + (int64_t)b * p.dt_sb + h;
+  const char* fg = reinterpret_cast<const char*>(reinterpret_cast<const SegFrags<TM, N>*>(p.seg_frags) +
+                                                 ((int64_t)b * p.ngroups + g) * p.nseg + c0 / SEG);
   T* yg = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_sb + (int64_t)h * p.y_sh + 32 * ph;
-  const int b0 = w * BPW, nb = max(0, min(BPW, TB::NBLK - b0));
+  const int f0 = w * FPW, fn = max(0, min(FPW, FB - f0));
   Frag<TM> id[2];
   id[0] = ident_frag<TM>(0, half, l32);
   id[1] = ident_frag<TM>(1, half, l32);
@@ -527,27 +627,47 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
   // Entering state H_k (fragment-native workspace order), columns of this wave's P-half.
   f32x16 H[NT];
   {
-    const float* hk = p.chunk_states + (((int64_t)b * p.nchunks + k) * p.nheads + h) * (HD * N);
+    const int64_t hidx = (((int64_t)b * p.nchunks + k) * p.nheads + h) * (HD * N);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const f32x4* h4 = reinterpret_cast<const f32x4*>(hk + frag_off(nt, ph, l));
+      if constexpr (sizeof(T) == 2) {
+        const bf16x8* h8 = reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.entering) + hidx +
+                                                           frag_off(nt, ph, l));
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 v = h4[q];
-        H[nt][4 * q] = v[0]; H[nt][4 * q + 1] = v[1]; H[nt][4 * q + 2] = v[2]; H[nt][4 * q + 3] = v[3];
+        for (int q = 0; q < 2; ++q) {
+          const bf16x8 v = h8[q];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) H[nt][8 * q + i] = (float)v[i];
+        }
+      } else {
+        const f32x4* h4 = reinterpret_cast<const f32x4*>(p.chunk_states + hidx + frag_off(nt, ph, l));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 v = h4[q];
+          H[nt][4 * q] = v[0]; H[nt][4 * q + 1] = v[1]; H[nt][4 * q + 2] = v[2]; H[nt][4 * q + 3] = v[3];
+        }
       }
     }
   }
-
+  float kappa = 0.f;
   const int nseg = (c1 - c0 + SEG - 1) / SEG;
-  float dtraw = (c0 + l < c1) ? dtg[(int64_t)(c0 + l) * p.dt_sl] : 0.f;
-  fetch_tile<T, N>(sm.st[0].B, Bg, p.B_sl, c0, last, b0, nb, l);
-  fetch_tile<T, N>(sm.st[0].C, Cg, p.C_sl, c0, last, b0, nb, l);
-  fetch_xhalf<T>(sm.st[0].X[w], xg, p.x_sl, c0, last, l);
+  // a segment's fetch in two parts (shared tiles, then this wave's x and dt) so its issue can be spread
+  // through the compute of the current segment
+  auto fetch_shared = [&](int seg, Stage& sg) {
+    const int pos = c0 + seg * SEG;
+    fetch_blocks(reinterpret_cast<char*>(&sg.fr), fg + (size_t)seg * sizeof(SegFrags<TM, N>), f0, fn, l);
+    fetch_tile<T, N>(sg.C, Cg, p.C_sl, pos, last, w * CPW, CPW, l);
+  };
+  auto fetch_own = [&](int seg, Stage& sg) {
+    const int pos = c0 + seg * SEG;
+    fetch_xhalf<T>(sg.X[w], xg, p.x_sl, pos, last, l);
+    fetch_dt(sg.dt[w], dtg, p.dt_sl, pos, last, l);
+  };
+  fetch_shared(0, sm.st[0]);
+  fetch_own(0, sm.st[0]);
 
   for (int si = 0; si < nseg; ++si) {
-    // Lane-dependent LDS addresses are recomputed each segment (cheap VALU) instead of
-    // being hoisted out of the loop, where they would all stay live and spill.
+    // lane-dependent LDS addresses are recomputed each segment instead of hoisted (and spilled)
     int lq = l;
     asm volatile("" : "+v"(lq));
     const int ll = lq, halfq = lq >> 5, l32q = lq & 31;
@@ -558,111 +678,94 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
     if constexpr (NBUF == 1) {
       if (si > 0) {
         store_yhalf<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, xt, SEG, ll);   // y of the previous segment
-        __syncthreads();                                   // every wave is done with the previous tiles
-        fetch_tile<T, N>(sg.B, Bg, p.B_sl, pos, last, b0, nb, ll);
-        fetch_tile<T, N>(sg.C, Cg, p.C_sl, pos, last, b0, nb, ll);
-        fetch_xhalf<T>(xt, xg, p.x_sl, pos, last, ll);
+        lds_barrier();                                     // every wave is done with the previous tiles
+        fetch_shared(si, sg);
+        fetch_own(si, sg);
       }
     }
     wait_vmem();
-    __syncthreads();                                       // tiles of this segment are in LDS
-    float dtn = 0.f;
+    lds_barrier();                                         // this segment's tiles are in LDS
     if constexpr (NBUF == 2) {
-      auto& og = sm.st[cur ^ 1];
-      // y of the previous segment (staged in place of its x), then the next segment's fetch into the same buffer
-      if (si > 0) store_yhalf<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, og.X[w], SEG, ll);
-      if (si + 1 < nseg) {
-        fetch_tile<T, N>(og.B, Bg, p.B_sl, pos + SEG, last, b0, nb, ll);
-        fetch_tile<T, N>(og.C, Cg, p.C_sl, pos + SEG, last, b0, nb, ll);
-        fetch_xhalf<T>(og.X[w], xg, p.x_sl, pos + SEG, last, ll);
-      }
+      if (si + 1 < nseg) fetch_shared(si + 1, sm.st[cur ^ 1]);
     }
-    if (si + 1 < nseg && pos + SEG + l < c1) dtn = dtg[(int64_t)(pos + SEG + l) * p.dt_sl];
 
-    // ---- this head's in-segment decay (lane = token); the factorised path when the range is small
-    const int len = min(SEG, c1 - pos);
+    // ---- this head's in-segment decay (lane = token).  H_true = e^kappa H (kappa <= 0 carried lazily).
     float dtv;
-    const float cs = seg_decay(p, dtraw, h, Ah, pos + l, c1, dtv);
+    const float cs = seg_decay(p, sg.dt[w][ll], dtb, Ah, pos + l, c1, dtv);
     const float cse = __shfl(cs, 63, 64);
     const bool fact = (-cse <= FACT_RANGE);               // wave-uniform
-    const float m = fact ? 0.5f * cse : 0.f;
-    sm.sa[w][ll] = (fact ? __expf(m - cs) : 1.f) * dtv;
-    sm.sb[w][ll] = __expf(cse - cs);
+    if (!fact || -(kappa + cse) > FACT_RANGE) {
+      const float e = __expf(kappa);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) H[nt] *= e;
+      kappa = 0.f;
+    }
+    sm.sa[w][ll] = (fact ? __expf(-kappa - cs) : 1.f) * dtv;   // wave-private scratch
     sm.cs[w][ll] = cs;
 
-    // ---- shared: C B^T tiles (s-tile, t-tile) in {(0,0), (0,1), (1,1)} and B^T fragments
-#pragma unroll
-    for (int i = 0; i < SW::CBPER; ++i) {
-      const int ti = SW::cb_tile(w, i);
-      if (ti < 3) {
-        const int st = (ti == 2) ? 1 : 0, tt = (ti == 0) ? 0 : 1;
-        f32x16 acc = zero16();
-#pragma unroll
-        for (int c = 0; c < N / 16; ++c)
-          acc = mma(row_frag<TM, T, N>(sg.B, 32 * st + l32q, 16 * c + 8 * halfq),
-                    row_frag<TM, T, N>(sg.C, 32 * tt + l32q, 16 * c + 8 * halfq), acc);
-        const int tl = 32 * tt + l32q;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int s = 32 * st + acc_row(halfq, r);
-          if (!(s <= tl && s < len)) acc[r] = 0.f;
-        }
-        sm.CB[ti][0][ll] = acc_to_frag<TM>(acc, 0);
-        sm.CB[ti][1][ll] = acc_to_frag<TM>(acc, 1);
-      }
-    }
-    bt_work<T, TM, N, NW, true>(sg.B, sm.bt, w, id, halfq, l32q, ll);
-    __syncthreads();                                       // C B^T, B^T fragments and scales visible
-
-    // ---- per wave: head j, p-tile ph.  Y^T[p][t] = sum_n H[p][n] C^T[n][t] + sum_s xa^T[p][s] M^T[s][t],
-    // one 32-token t-tile at a time (its y staged in place of x before the next).
-    // Factorised path: H is carried at the segment midpoint, Hm = e^m H, with xa_s = e^{m - cs_s} dt_s x_s:
-    //   y_t = e^{cs_t - m} (C_t Hm^T + sum_s M[t][s] xa_s),   H_end = e^{cse - m} (Hm + B^T xa).
-    // Exact path (range above FACT_RANGE): xa_s = dt_s x_s, each masked C B^T entry decayed by
-    // e^{cs_t - cs_s} (s <= t), the state term weighted by e^{cs_t}; H_end = e^{cse} H + B^T (e^{cse - cs} xa).
+    // ---- per wave: head j, p-tile ph.  Y^T[p][t] = sum_n H[p][n] C^T[n][t] + sum_s xa^T[p][s] M^T[s][t]
     Frag<TM> xa[4];
-    xt_frags<TM, T, false>(xt, sm.sa[w], nullptr, id, halfq, l32q, xa, xa);
-    if (fact) {
-      const float em = __expf(m);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) H[nt] *= em;
+    xt_frags<TM, T>(xt, sm.sa[w], id, halfq, l32q, xa);
+    if constexpr (NBUF == 2) {
+      // y of the previous segment (staged in place of its x), then the next x and dt into the same buffer
+      auto& og = sm.st[cur ^ 1];
+      if (si > 0) store_yhalf<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, og.X[w], SEG, ll);
+      if (si + 1 < nseg) fetch_own(si + 1, og);
     }
+    const float cs0 = sm.cs[w][l32q], cs1 = sm.cs[w][32 + l32q];
+    f32x16 Y0 = zero16(), Y1 = zero16();
+    readout<TM, T, N>(H, sg.C, l32q, halfq, Y0, Y1);
+    float rs0, rs1;
+    if (fact) {
+      Y0 = mma(xa[0], sg.fr.cb[0][0][ll], Y0);
+      Y0 = mma(xa[1], sg.fr.cb[0][1][ll], Y0);
+      Y1 = mma(xa[0], sg.fr.cb[1][0][ll], Y1);
+      Y1 = mma(xa[1], sg.fr.cb[1][1][ll], Y1);
+      Y1 = mma(xa[2], sg.fr.cb[2][0][ll], Y1);
+      Y1 = mma(xa[3], sg.fr.cb[2][1][ll], Y1);
+      state_update<TM, N>(H, sg.fr.bt, xa, ll);
+      rs0 = __expf(kappa + cs0);
+      rs1 = __expf(kappa + cs1);
+      kappa += cse;
+    } else {
+      // exact path (kappa = 0 here): xa_s = dt_s x_s, each masked C B^T entry decayed by e^{cs_t - cs_s}
+      // (s <= t), the state term weighted by e^{cs_t};  H <- e^{cse} H + B^T (e^{cse - cs} xa)
+      Y0 *= __expf(cs0);
+      Y1 *= __expf(cs1);
+#pragma unroll
+      for (int ti = 0; ti < 3; ++ti) {
+        const int st = (ti == 2) ? 1 : 0;
+        const float cst = (ti == 0) ? cs0 : cs1;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          float css[8];
+          kset_vals(sm.cs[w] + 32 * st, c, halfq, css);
+          const Frag<TM> cb = sg.fr.cb[ti][c][ll];
+          Frag<TM> md;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) md.set(e, cb.get(e) * __expf(fminf(cst - css[e], 0.f)));
+          if (ti == 0) Y0 = mma(xa[2 * st + c], md, Y0);
+          else Y1 = mma(xa[2 * st + c], md, Y1);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float f[8];
+        kset_vals(sm.cs[w], c, halfq, f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xa[c].set(e, xa[c].get(e) * __expf(cse - f[e]));
+      }
+      const float e = __expf(cse);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) H[nt] *= e;
+      state_update<TM, N>(H, sg.fr.bt, xa, ll);
+      rs0 = rs1 = 1.f;
+    }
+    // y[t][p] = rs_t Y + D x, staged in place of x
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       const int tl = 32 * tt + l32q;
-      const float cst = sm.cs[w][tl];
-      f32x16 Y = zero16();
-      readout<TM, T, N>(H, sg.C, tl, halfq, Y);
-      float rsc = 1.f;
-      if (fact) {
-        if (tt == 0) {
-          Y = mma(xa[0], sm.CB[0][0][ll], Y);
-          Y = mma(xa[1], sm.CB[0][1][ll], Y);
-        } else {
-          Y = mma(xa[0], sm.CB[1][0][ll], Y);
-          Y = mma(xa[1], sm.CB[1][1][ll], Y);
-          Y = mma(xa[2], sm.CB[2][0][ll], Y);
-          Y = mma(xa[3], sm.CB[2][1][ll], Y);
-        }
-        rsc = __expf(cst - m);
-      } else {
-        Y *= __expf(cst);
-#pragma unroll
-        for (int ti = tt; ti < 2 * tt + 1; ++ti) {         // tiles (s-tile, tt): tt = 0 -> {0}, tt = 1 -> {1, 2}
-          const int st = (ti == 2) ? 1 : 0;
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            float css[8];
-            kset_vals(sm.cs[w] + 32 * st, c, halfq, css);
-            const Frag<TM> cb = sm.CB[ti][c][ll];
-            Frag<TM> md;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) md.set(e, cb.get(e) * __expf(fminf(cst - css[e], 0.f)));
-            Y = mma(xa[2 * st + c], md, Y);
-          }
-        }
-      }
-      // y[t][p] = rsc Y + D x, staged in place of x
+      const float rsc = tt ? rs1 : rs0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int p0 = 8 * q + 4 * halfq;                // 4 consecutive columns of the half, inside one chunk
@@ -672,37 +775,17 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
           const bf16x4 xv = *reinterpret_cast<const bf16x4*>(xp);
           bf16x4 yv;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) yv[i] = (bf16)(rsc * Y[4 * q + i] + d4[i] * (float)xv[i]);
+          for (int i = 0; i < 4; ++i) yv[i] = (bf16)(rsc * (tt ? Y1[4 * q + i] : Y0[4 * q + i]) + d4[i] * (float)xv[i]);
           *reinterpret_cast<bf16x4*>(xp) = yv;
         } else {
           const f32x4 xv = *reinterpret_cast<const f32x4*>(xp);
           f32x4 yv;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) yv[i] = rsc * Y[4 * q + i] + d4[i] * xv[i];
+          for (int i = 0; i < 4; ++i) yv[i] = rsc * (tt ? Y1[4 * q + i] : Y0[4 * q + i]) + d4[i] * xv[i];
           *reinterpret_cast<f32x4*>(xp) = yv;
         }
       }
     }
-    // ---- state update
-    if (fact) {
-      state_update<TM, N>(H, sm.bt, xa, ll);
-      const float eo = __expf(cse - m);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) H[nt] *= eo;
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {                        // xa <- e^{cse - cs_s} xa
-        float f[8];
-        kset_vals(sm.sb[w], c, halfq, f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xa[c].set(e, xa[c].get(e) * f[e]);
-      }
-      const float e = __expf(cse);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) H[nt] *= e;
-      state_update<TM, N>(H, sm.bt, xa, ll);
-    }
-    dtraw = dtn;
   }
   // y of the last segment
   {
@@ -715,21 +798,34 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
 
 // ------------------------------------------------------------------ launch
 
-size_t ssd_workspace_bytes(int batch, int nchunks, int nheads, int headdim, int dstate) {
+size_t ssd_frag_bytes(int dtype, int dstate) {
+  return dtype == DT_BF16 ? (dstate == 128 ? sizeof(SegFrags<bf16, 128>) : sizeof(SegFrags<bf16, 64>))
+                          : (dstate == 128 ? sizeof(SegFrags<float, 128>) : sizeof(SegFrags<float, 64>));
+}
+
+size_t ssd_workspace_bytes(int batch, int seqlen, int nchunks, int nheads, int headdim, int dstate, int ngroups,
+                           int dtype) {
   const size_t states = (size_t)batch * nchunks * nheads * headdim * dstate * sizeof(float);
   const size_t decay = (size_t)batch * nheads * nchunks * sizeof(float);
-  return ((states + 255) / 256) * 256 + ((decay + 255) / 256) * 256;
+  const size_t nseg = (size_t)(seqlen + SEG - 1) / SEG;
+  const size_t entering = dtype == DT_BF16 ? states / 2 : 0;      // bf16 copy of the entering states
+  return align256(states) + align256(decay) + align256((size_t)batch * ngroups * nseg * ssd_frag_bytes(dtype, dstate)) +
+         align256(entering);
 }
 
 template <typename T, typename TM, int N, int HG>
 static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st) {
+  hipLaunchKernelGGL((ssd_seg_frags_kernel<T, TM, N>), dim3((unsigned)p.nseg, (unsigned)p.ngroups, (unsigned)p.batch),
+                     dim3(512), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   dim3 grid((unsigned)p.nchunks, (unsigned)(p.nheads / HG), (unsigned)p.batch);
   hipLaunchKernelGGL((ssd_chunk_state_kernel<T, TM, N, HG>), grid, dim3(128 * HG), 0, st, p);
-  hipError_t e = hipGetLastError();
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int per4 = HD * N / 4;
   dim3 g2((unsigned)((per4 + 255) / 256), (unsigned)(p.batch * p.nheads));
-  hipLaunchKernelGGL(ssd_state_pass_kernel, g2, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((ssd_state_pass_kernel<T>), g2, dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_chunk_scan_kernel<T, TM, N, HG>), grid, dim3(128 * HG), 0, st, p);
@@ -737,7 +833,8 @@ static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st) {
 }
 
 template <typename T, typename TM, int N, int HG>
-constexpr bool ssd_fits = sizeof(ScanSmem<T, TM, N, HG, 1>) <= LDS_BYTES && sizeof(StateSmem<T, TM, N, HG, 1>) <= LDS_BYTES;
+constexpr bool ssd_fits = sizeof(ScanSmem<T, TM, N, HG, 1>) <= LDS_BYTES && sizeof(StateSmem<T, TM, N, HG, 1>) <= LDS_BYTES &&
+                          bt_blocks<TM, N> % (2 * HG) == 0 && Tile<T, N>::NBLK % (2 * HG) == 0;
 
 template <typename T, typename TM, int N>
 static hipError_t launch_ssd_n(const SsdParams& p, hipStream_t st) {
@@ -748,18 +845,27 @@ static hipError_t launch_ssd_n(const SsdParams& p, hipStream_t st) {
     case 2:
       if constexpr (ssd_fits<T, TM, N, 2>) return launch_ssd_t<T, TM, N, 2>(p, st);
       return hipErrorInvalidValue;
-    case 1: return launch_ssd_t<T, TM, N, 1>(p, st);
+    case 1:
+      if constexpr (ssd_fits<T, TM, N, 1>) return launch_ssd_t<T, TM, N, 1>(p, st);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
 
+// Empty sequence: the final state is the initial state (or zero) -- a plain kernel rather than a memset or
+// copy node, so the launch behaves the same inside a captured graph.
+__global__ __launch_bounds__(256) void ssd_empty_kernel(const float* __restrict__ h0, float* __restrict__ fin, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) fin[i] = h0 ? h0[i] : 0.f;
+}
+
 hipError_t launch_ssd(const SsdParams& p, hipStream_t st) {
   if (p.nchunks == 0) {
-    // Empty sequence: the final state is the initial state.
     if (!p.final_state) return hipSuccess;
-    const size_t bytes = (size_t)p.batch * p.nheads * HD * p.dstate * sizeof(float);
-    if (p.init_state) return hipMemcpyAsync(p.final_state, p.init_state, bytes, hipMemcpyDeviceToDevice, st);
-    return hipMemsetAsync(p.final_state, 0, bytes, st);
+    const size_t n = (size_t)p.batch * p.nheads * HD * p.dstate;
+    hipLaunchKernelGGL(ssd_empty_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p.init_state,
+                       p.final_state, n);
+    return hipGetLastError();
   }
   if (p.dtype == DT_BF16) {
     if (p.dstate == 128) return launch_ssd_n<bf16, bf16, 128>(p, st);
