@@ -153,7 +153,23 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// softplus with PyTorch's default threshold (x > 20 -> x).
-__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+// softplus with PyTorch's default threshold (x > 20 -> x): log(1 + e^x).  For e = e^x < 1/16 the
+// log1p series e - e^2/2 + ... + e^7/7 (truncation below e^8/8, i.e. < 4e-10 relative); above, 1 + e
+// is formed with relative rounding error 6e-8 against a logarithm >= 0.06.
+__device__ __forceinline__ float softplus_f(float x) {
+  if (x > 20.f) return x;
+  const float e = __expf(x);
+  if (e < 0.0625f) {
+    float s = 1.f / 7.f;
+    s = 1.f / 6.f - e * s;
+    s = 1.f / 5.f - e * s;
+    s = 1.f / 4.f - e * s;
+    s = 1.f / 3.f - e * s;
+    s = 1.f / 2.f - e * s;
+    s = 1.f - e * s;
+    return e * s;
+  }
+  return __logf(1.f + e);
+}
 
 }  // namespace mh

@@ -161,16 +161,33 @@ __device__ __forceinline__ void fetch_blocks(char* dst, const char* src, int b0,
                                      (lds_void_t*)(dst + (b0 + q) * 1024), 16, 0, 0);
 }
 
-// Write the y rows [0, len) staged in a wave's x half tile to HBM (16-byte stores).
+// y rows staged in a wave's x half tile: lane-held 16-byte chunks (read), then written to HBM.
 template <typename T>
-__device__ __forceinline__ void store_yhalf(T* dst, int64_t row_stride, const T* tile, int len, int lane) {
+__device__ __forceinline__ void load_yhalf(const T* tile, int lane, uint4 (&v)[XHalf<T>::NBLK]) {
   using X = XHalf<T>;
-  uint4 v[X::NBLK];
 #pragma unroll
   for (int i = 0; i < X::NBLK; ++i) {
     const int e = lane + 64 * i;
     v[i] = *reinterpret_cast<const uint4*>(tile + X::chunk(e / X::CPR, e % X::CPR));
   }
+}
+// All SEG rows (a full segment): exactly NBLK store instructions per wave, whatever the lane.
+template <typename T>
+__device__ __forceinline__ void store_yhalf_full(T* dst, int64_t row_stride, const uint4 (&v)[XHalf<T>::NBLK],
+                                                 int lane) {
+  using X = XHalf<T>;
+#pragma unroll
+  for (int i = 0; i < X::NBLK; ++i) {
+    const int e = lane + 64 * i;
+    *reinterpret_cast<uint4*>(dst + (int64_t)(e / X::CPR) * row_stride + (e % X::CPR) * X::EPC) = v[i];
+  }
+}
+// Rows [0, len) only.
+template <typename T>
+__device__ __forceinline__ void store_yhalf(T* dst, int64_t row_stride, const T* tile, int len, int lane) {
+  using X = XHalf<T>;
+  uint4 v[X::NBLK];
+  load_yhalf<T>(tile, lane, v);
 #pragma unroll
   for (int i = 0; i < X::NBLK; ++i) {
     const int e = lane + 64 * i;
@@ -651,8 +668,7 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
   }
   float kappa = 0.f;
   const int nseg = (c1 - c0 + SEG - 1) / SEG;
-  // a segment's fetch in two parts (shared tiles, then this wave's x and dt) so its issue can be spread
-  // through the compute of the current segment
+  // a segment's fetch: the tiles all heads share, and this wave's x half and dt
   auto fetch_shared = [&](int seg, Stage& sg) {
     const int pos = c0 + seg * SEG;
     fetch_blocks(reinterpret_cast<char*>(&sg.fr), fg + (size_t)seg * sizeof(SegFrags<TM, N>), f0, fn, l);
@@ -683,10 +699,25 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
         fetch_own(si, sg);
       }
     }
-    wait_vmem();
-    lds_barrier();                                         // this segment's tiles are in LDS
     if constexpr (NBUF == 2) {
-      if (si + 1 < nseg) fetch_shared(si + 1, sm.st[cur ^ 1]);
+      wait_vmem();                                         // this segment's tiles (and the last y stores)
+      auto& og = sm.st[cur ^ 1];
+      if (si > 0) {
+        // y of the previous segment (a full one: only a chunk's last segment is partial), staged by this
+        // wave in place of its x in the other stage: read out and stored before the stage is refilled,
+        // with no fetch in flight (an LDS read behind a pending direct-to-LDS load would wait for it).
+        uint4 yv[TX::NBLK];
+        load_yhalf<T>(og.X[w], ll, yv);
+        store_yhalf_full<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, yv, ll);
+      }
+      lds_barrier();                                       // this segment's tiles are in LDS; the other stage is free
+      if (si + 1 < nseg) {
+        fetch_shared(si + 1, og);
+        fetch_own(si + 1, og);
+      }
+    } else {
+      wait_vmem();
+      lds_barrier();                                       // this segment's tiles are in LDS
     }
 
     // ---- this head's in-segment decay (lane = token).  H_true = e^kappa H (kappa <= 0 carried lazily).
@@ -706,12 +737,6 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
     // ---- per wave: head j, p-tile ph.  Y^T[p][t] = sum_n H[p][n] C^T[n][t] + sum_s xa^T[p][s] M^T[s][t]
     Frag<TM> xa[4];
     xt_frags<TM, T>(xt, sm.sa[w], id, halfq, l32q, xa);
-    if constexpr (NBUF == 2) {
-      // y of the previous segment (staged in place of its x), then the next x and dt into the same buffer
-      auto& og = sm.st[cur ^ 1];
-      if (si > 0) store_yhalf<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, og.X[w], SEG, ll);
-      if (si + 1 < nseg) fetch_own(si + 1, og);
-    }
     const float cs0 = sm.cs[w][l32q], cs1 = sm.cs[w][32 + l32q];
     f32x16 Y0 = zero16(), Y1 = zero16();
     readout<TM, T, N>(H, sg.C, l32q, halfq, Y0, Y1);
