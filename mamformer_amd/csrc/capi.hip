@@ -87,6 +87,11 @@ int ssd_validate(const mh_ssd_args* a, int64_t* chunk_len_out) {
       !stride_ok(a->C_stride_l, es))
     return fail(MH_ERR_ALIGN, "ssd: strides of x, y, B, C must be multiples of 16 bytes");
   if (a->dt_stride_b < 0 || a->dt_stride_l < 0) return fail(MH_ERR_STRIDE, "ssd: negative dt stride");
+  // the kernels address one 64-token segment of x / y / B / C / dt with 32-bit offsets
+  constexpr int64_t kSpan = (int64_t)1 << 31;
+  if (a->x_stride_l * es * 64 >= kSpan || a->y_stride_l * es * 64 >= kSpan || a->B_stride_l * es * 64 >= kSpan ||
+      a->C_stride_l * es * 64 >= kSpan || a->dt_stride_l * 4 * 64 >= kSpan)
+    return fail(MH_ERR_STRIDE, "ssd: token stride too large (64 tokens must span less than 2 GiB)");
   if (a->x_stride_h < a->headdim || a->y_stride_h < a->headdim)
     return fail(MH_ERR_STRIDE, "ssd: x/y head stride smaller than headdim (headdim must be contiguous)");
   if ((a->B_stride_l != 0 && a->B_stride_l < a->ngroups * a->dstate) ||

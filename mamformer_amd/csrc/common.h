@@ -96,7 +96,8 @@ __device__ __forceinline__ Frag<TM> acc_to_frag_scaled(const f32x16& acc, int c,
 
 // ---------------------------------------------------------------- wave helpers
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+// Wave index within the workgroup, in a scalar register (wave-uniform for the compiler).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ float wave_incl_scan(float v) {

@@ -109,6 +109,17 @@ struct XHalf {
   __device__ static __forceinline__ int chunk(int r, int c) { return r * W + (c ^ swz(r)) * EPC; }
 };
 
+// Direct global -> LDS load of `bytes` (16 or 4) per lane from a wave-uniform base plus a 32-bit lane
+// offset (scalar-base addressing: no 64-bit per-lane address arithmetic).  Token strides are validated on
+// the host so that a segment's span (SEG rows) stays below 2 GiB.
+template <int bytes>
+__device__ __forceinline__ void dma_lds(const void* base, uint32_t off, void* lds) {
+  static_assert(bytes == 16 || bytes == 4, "direct-to-LDS load size");
+  glb_void_t* g = (glb_void_t*)(reinterpret_cast<const char*>(base) + off);
+  if constexpr (bytes == 16) __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
+  else __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 4, 0, 0);
+}
+
 // Direct global -> LDS fetch of 1 KB blocks [blk0, blk0 + nblk) of a swizzled
 // B/C tile: lane i of the wave writes LDS bytes [16 i, 16 i + 16) of the block,
 // so it fetches the logical chunk that the swizzle places there.  Rows past
@@ -119,14 +130,14 @@ __device__ __forceinline__ void fetch_tile(T* dst, const T* src, int64_t row_str
                                            int blk0, int nblk, int lane) {
   using TL = Tile<T, W>;
   const int rr = lane / TL::CPR, phys = lane % TL::CPR;
+  const T* base = src + (int64_t)tok0 * row_stride;       // wave-uniform
+  const int rmax = last_tok - tok0;                        // >= 0; rows beyond it are clamped
   for (int q = 0; q < nblk; ++q) {
     const int blk = blk0 + q;
     const int r = blk * TL::RPB + rr;
     const int c = phys ^ (r & TL::MASK);
-    const int tok = min(tok0 + r, last_tok);
-    const T* g = src + (int64_t)tok * row_stride + c * TL::EPC;
-    T* d = dst + blk * (1024 / (int)sizeof(T));
-    __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)d, 16, 0, 0);
+    const uint32_t off = (uint32_t)(min(r, rmax) * (int)row_stride + c * TL::EPC) * (uint32_t)sizeof(T);
+    dma_lds<16>(base, off, dst + blk * (1024 / (int)sizeof(T)));
   }
 }
 
@@ -136,29 +147,27 @@ __device__ __forceinline__ void fetch_xhalf(T* dst, const T* src, int64_t row_st
                                             int lane) {
   using X = XHalf<T>;
   const int rr = lane / X::CPR, phys = lane % X::CPR;
+  const T* base = src + (int64_t)tok0 * row_stride;
+  const int rmax = last_tok - tok0;
 #pragma unroll
   for (int blk = 0; blk < X::NBLK; ++blk) {
     const int r = blk * X::RPB + rr;
     const int c = phys ^ X::swz(r);
-    const int tok = min(tok0 + r, last_tok);
-    const T* g = src + (int64_t)tok * row_stride + c * X::EPC;
-    T* d = dst + blk * (1024 / (int)sizeof(T));
-    __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)d, 16, 0, 0);
+    const uint32_t off = (uint32_t)(min(r, rmax) * (int)row_stride + c * X::EPC) * (uint32_t)sizeof(T);
+    dma_lds<16>(base, off, dst + blk * (1024 / (int)sizeof(T)));
   }
 }
 
 // Direct fetch of the raw dt of 64 tokens (lane = token, rows past the end clamped) into LDS.
 __device__ __forceinline__ void fetch_dt(float* dst, const float* src, int64_t stride, int tok0, int last_tok,
                                          int lane) {
-  __builtin_amdgcn_global_load_lds((glb_void_t*)(src + (int64_t)min(tok0 + lane, last_tok) * stride),
-                                   (lds_void_t*)dst, 4, 0, 0);
+  const float* base = src + (int64_t)tok0 * stride;
+  dma_lds<4>(base, (uint32_t)(min(lane, last_tok - tok0) * (int)stride) * 4u, dst);
 }
 
 // Direct copy of nb contiguous 1 KB blocks starting at block b0 (precomputed fragments).
 __device__ __forceinline__ void fetch_blocks(char* dst, const char* src, int b0, int nb, int lane) {
-  for (int q = 0; q < nb; ++q)
-    __builtin_amdgcn_global_load_lds((glb_void_t*)(src + (b0 + q) * 1024 + 16 * lane),
-                                     (lds_void_t*)(dst + (b0 + q) * 1024), 16, 0, 0);
+  for (int q = 0; q < nb; ++q) dma_lds<16>(src + (b0 + q) * 1024, 16u * lane, dst + (b0 + q) * 1024);
 }
 
 // y rows staged in a wave's x half tile: lane-held 16-byte chunks (read), then written to HBM.
@@ -299,10 +308,13 @@ __device__ __forceinline__ void xt_frags(const T* xtile, const float* sa, const 
 //   bt[nt][c][lane]  B^T A-operand fragment (row n = 32 nt + lane % 32, k = token 16 c + KSET)
 //   cb[ti][c][lane]  masked (C B^T)^T tile ti in {(s 0, t 0), (s 0, t 1), (s 1, t 1)} as a
 //                    B-operand fragment (column t, k = token s 16 c + KSET within the s-tile)
+//   ct[nt][c][tt][lane]  C^T as a B-operand fragment (column t = 32 tt + lane % 32,
+//                    k = state n = 32 nt + 16 c + KSET) for the state read-out
 template <typename TM, int N>
 struct SegFrags {
   Frag<TM> bt[N / 32][4][64];
   Frag<TM> cb[3][2][64];
+  Frag<TM> ct[N / 32][2][2][64];
 };
 template <typename TM, int N>
 constexpr int frag_blocks = (int)(sizeof(SegFrags<TM, N>) / 1024);
@@ -314,7 +326,6 @@ static_assert(sizeof(SegFrags<bf16, 128>) % 1024 == 0 && sizeof(SegFrags<float, 
 template <typename T, typename TM, int N, int HG>
 struct ScanStage {
   SegFrags<TM, N> fr;
-  T C[SEG * N];
   T X[2 * HG][SEG * 32];      // per wave: its half of its head's x tile (y staged in place)
   float dt[2 * HG][SEG];      // per wave: raw dt of its head for the segment's tokens
 };
@@ -358,17 +369,18 @@ __device__ __forceinline__ float seg_decay(const SsdParams& p, float dtraw, floa
 }
 
 // State read-out of one wave: Y^T[p][t] += sum_n H[p][n] C^T[n][t] for the two 32-token t-tiles of the
-// segment (H as A operand straight from the accumulators, converted once for both).
-template <typename TM, typename T, int N>
-__device__ __forceinline__ void readout(const f32x16 (&H)[N / 32], const T* Cs, int l32, int half, f32x16& Y0,
-                                        f32x16& Y1) {
+// segment (H as A operand straight from the accumulators, converted once for both; C^T fragments
+// precomputed per segment).
+template <typename TM, int N>
+__device__ __forceinline__ void readout(const f32x16 (&H)[N / 32], const Frag<TM> (&ct)[N / 32][2][2][64], int l,
+                                        f32x16& Y0, f32x16& Y1) {
 #pragma unroll
   for (int nt = 0; nt < N / 32; ++nt)
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const Frag<TM> hf = acc_to_frag<TM>(H[nt], c);
-      Y0 = mma(hf, kset_frag<TM, T, N>(Cs, l32, 32 * nt + 16 * c, half), Y0);
-      Y1 = mma(hf, kset_frag<TM, T, N>(Cs, 32 + l32, 32 * nt + 16 * c, half), Y1);
+      Y0 = mma(hf, ct[nt][c][0][l], Y0);
+      Y1 = mma(hf, ct[nt][c][1][l], Y1);
     }
 }
 
@@ -392,7 +404,8 @@ __host__ __device__ __forceinline__ size_t align256(size_t n) { return (n + 255)
 // ------------------------------------------------------------------ kernel 0
 
 // One workgroup of 8 waves per (segment, group, batch): 3 + 2 N/32 work items
-// (the C B^T tiles and the B^T blocks), wave w taking items w and w + 8.
+// (the C B^T tiles and the B^T blocks), wave w taking items w and w + 8, then
+// the C^T fragments, read straight out of the C tile.
 template <typename T, typename TM, int N>
 __global__ __launch_bounds__(512) void ssd_seg_frags_kernel(SsdParams p) {
   using TB = Tile<T, N>;
@@ -438,6 +451,11 @@ __global__ __launch_bounds__(512) void ssd_seg_frags_kernel(SsdParams p) {
       out->bt[blk >> 1][2 * (blk & 1)][l] = acc_to_frag<TM>(acc, 0);
       out->bt[blk >> 1][2 * (blk & 1) + 1][l] = acc_to_frag<TM>(acc, 1);
     }
+  }
+  // C^T read-out fragments: (nt, c, tt) = f, two per wave
+  for (int f = w; f < (N / 32) * 4; f += 8) {
+    const int nt = f >> 2, c = (f >> 1) & 1, tt = f & 1;
+    out->ct[nt][c][tt][l] = kset_frag<TM, T, N>(Cs, 32 * tt + l32, 32 * nt + 16 * c, half);
   }
 }
 
@@ -612,12 +630,9 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
   using SM = ScanSmem<T, TM, N, HG, NBUF>;
   using Stage = ScanStage<T, TM, N, HG>;
   constexpr int NT = N / 32, NW = 2 * HG;
-  using TB = Tile<T, N>;
   using TX = XHalf<T>;
   constexpr int FB = frag_blocks<TM, N>;
   constexpr int FPW = (FB + NW - 1) / NW;                  // fragment blocks fetched per wave (the last ones fewer)
-  static_assert(TB::NBLK % NW == 0, "C blocks split evenly over the waves");
-  constexpr int CPW = TB::NBLK / NW;
   __shared__ SM sm;
   const int k = blockIdx.x, b = blockIdx.z;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
@@ -630,7 +645,6 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
   const float Ah = p.A[h];
   const float dtb = p.dt_bias ? p.dt_bias[h] : 0.f;
   const T* xg = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + 32 * ph;
-  const T* Cg = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb + (int64_t)g * N;
   const float* dtg = p.dt + (int64_t)b * p.dt_sb + h;
   const char* fg = reinterpret_cast<const char*>(reinterpret_cast<const SegFrags<TM, N>*>(p.seg_frags) +
                                                  ((int64_t)b * p.ngroups + g) * p.nseg + c0 / SEG);
@@ -670,9 +684,7 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
   const int nseg = (c1 - c0 + SEG - 1) / SEG;
   // a segment's fetch: the tiles all heads share, and this wave's x half and dt
   auto fetch_shared = [&](int seg, Stage& sg) {
-    const int pos = c0 + seg * SEG;
     fetch_blocks(reinterpret_cast<char*>(&sg.fr), fg + (size_t)seg * sizeof(SegFrags<TM, N>), f0, fn, l);
-    fetch_tile<T, N>(sg.C, Cg, p.C_sl, pos, last, w * CPW, CPW, l);
   };
   auto fetch_own = [&](int seg, Stage& sg) {
     const int pos = c0 + seg * SEG;
@@ -739,7 +751,7 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
     xt_frags<TM, T>(xt, sm.sa[w], id, halfq, l32q, xa);
     const float cs0 = sm.cs[w][l32q], cs1 = sm.cs[w][32 + l32q];
     f32x16 Y0 = zero16(), Y1 = zero16();
-    readout<TM, T, N>(H, sg.C, l32q, halfq, Y0, Y1);
+    readout<TM, N>(H, sg.fr.ct, ll, Y0, Y1);
     float rs0, rs1;
     if (fact) {
       Y0 = mma(xa[0], sg.fr.cb[0][0][ll], Y0);
