@@ -9,19 +9,18 @@
 // normalised phi(x)=elu(x)+1 form is the reference's LinearDiffAttention scan
 // (mamformer/layers/kda_diff.py:357-478, mamformer/kernels/triton_ssd.py:121-181).
 //
-// One workgroup of 4 waves per (b, h, V-half) walks the sequence in segments
-// of <= 64 tokens.  Per segment, with G = in-segment inclusive cumsum of g
-// (per channel k) and m = its midpoint:
+// Per window of tokens (a 64-token tile, or a piece of one), with G the
+// in-tile inclusive cumsum of g (per channel k), base / end its values just
+// before / at the window's last token and m the midpoint of its range:
 //     A^T[s][t] = sum_k (k_s e^{m-G_s})[k] (q_e,t e^{G_t-m})[k]   (s <= t)   MFMA, K = dk
 //     o^T[v][t] = sum_s v^T[v][s] A^T[s][t]                                    MFMA
-//               + sum_k S[k][v] (q_e,t e^{G_t})[k]                             MFMA (state read-out)
-//     S[k][v]  <- e^{G_end[k]} S[k][v] + sum_s (k_s e^{G_end-G_s})[k] v_s[v]   MFMA
-// The state lives in MFMA accumulator registers: wave w owns the 32-wide v-tile
-// (w & 1) and the k-half (w >> 1); the two k-halves' read-out partials are
-// summed through LDS.  Segments are cut so that the spread of G within a
-// segment never exceeds RANGE, which keeps every factor finite.
+//               + sum_k (S[k][v] e^{m-base}) (q_e,t e^{G_t-m})[k]              MFMA (state read-out)
+//     S[k][v]  <- e^{end-base} S[k][v] + sum_s (e^{end-m} k_s e^{m-G_s})[k] v_s[v]   MFMA
+// Windows are cut so that the spread of G within one never exceeds KRANGE,
+// which keeps every factor finite.
 #include "common.h"
 #include "launch.h"
+#include "tiles.h"
 
 namespace mh {
 
@@ -32,33 +31,44 @@ constexpr int DK = 128;
 constexpr int DVH = 64;           // v columns per workgroup
 constexpr float KRANGE = 50.f;    // max spread of G per channel within a segment
 
-template <typename T>
-struct KdaSmem {
-  static constexpr int PK = DK + 16 / (int)sizeof(T);
-  static constexpr int PV = DVH + 16 / (int)sizeof(T);
-  T Qt[SEGK * PK];          // q_e e^{G - m}
-  T Qh[SEGK * PK];          // q_e e^{G}
-  T Kt[SEGK * PK];          // k e^{m - G}   (zero rows beyond the segment)
-  T V[SEGK * PV];           // v[:, V-half]  (zero rows beyond the segment)
-  float G[SEGK][DK];        // in-segment inclusive cumsum of g
-  float tot[2][DK], gmax[2][DK], gmin[2][DK];
-  float m[DK], em[DK], ek[DK], eg[DK];
-  f32x16 red[2][2][64];     // read-out partials of the k-half 1 waves: vt, tt, lane
-  int len;
+// ----------------------------------------------------------------- gated mode
+// One workgroup of 8 waves per (b, h, V-half) walks the sequence in 64-token
+// tiles.  The next tile's q1, q2, k, v are loaded into registers (and its g
+// straight into LDS) while the current tile computes, so the walk streams at
+// memory speed.  Wave w owns v-tile vt = w & 1, t-tile tt = (w >> 1) & 1 and
+// k-half kh = w >> 2: it keeps the state tiles S[kh][vt] (replicated over tt),
+// computes the read-out partial of (vt, tt) over its k-half, and the kh = 1
+// partials are summed through LDS.  Waves 5..7 also form the three masked
+// A^T tiles.  Token-contracted operands (k^T, v^T) are transposed on the MFMA
+// unit.  A tile is one factorisation window unless the spread of G within it
+// exceeds KRANGE for some channel; it is then cut into shorter windows.
+constexpr int KW = 8;                 // waves per workgroup
+
+struct KdaGatedSmem {
+  float G[SEG][DK];                   // raw g of the tile (direct loads), then its in-tile inclusive cumsum
+  bf16 Qt[SEG * DK];                  // q_e e^{G - m}   (Tile<bf16, DK>, zero rows outside the window)
+  bf16 Kt[SEG * DK];                  // k e^{m - G}     (zero rows outside the window)
+  bf16 V[SEG * DVH];                  // v[:, V-half]    (Tile<bf16, DVH>)
+  Frag<bf16> A[3][2][64];             // masked A^T tiles (s0,t0), (s0,t1), (s1,t1) as B-operand fragments
+  f32x16 red[2][2][64];               // read-out partials of the kh = 1 waves: vt, tt, lane
+  bf16 O[4][32 * 32];                 // o blocks (vt, tt) staged for coalesced stores (XHalf rows 0..31)
+  float qtot[4][DK], qmin[4][DK], qmax[4][DK];   // per token-quarter cumsum statistics
+  float mm[DK], em[DK], ek[DK], eg[DK];          // window midpoint m, e^{m - base}, e^{end - m}, e^{end - base}
+  int wend, cut;
 };
 
-template <typename TM>
-struct KdaFrags {
-  Frag<TM> A[3][2][64];     // masked A^T tiles as B-operand fragments
+// Register-staged q1, q2, k (two 16-byte chunks each per thread) and v (one) of a tile.
+struct KdaStage {
+  uint4 q1[2], q2[2], k[2], v;
 };
 
 }  // namespace
 
-template <typename T, typename TM>
-__global__ __launch_bounds__(256) void kda_gated_kernel(KdaParams p) {
-  __shared__ KdaSmem<T> sm;
-  __shared__ KdaFrags<TM> sf;
-  using SM = KdaSmem<T>;
+__global__ __launch_bounds__(64 * KW) void kda_gated_kernel(KdaParams p) {
+  __shared__ KdaGatedSmem sm;
+  using TQ = Tile<bf16, DK>;
+  using TV = Tile<bf16, DVH>;
+  using XO = XHalf<bf16>;
   const int nbh = p.batch * p.nheads;
   int bh, vh;
   const int L = blockIdx.x;
@@ -71,19 +81,23 @@ __global__ __launch_bounds__(256) void kda_gated_kernel(KdaParams p) {
   }
   const int h = bh % p.nheads;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
-  const int vt = w & 1, kh = w >> 1;
+  const int vt = w & 1, tt = (w >> 1) & 1, kh = w >> 2;
   const int tid = threadIdx.x;
   const int S = p.seqlen;
   const float lam = p.lam_h ? p.lam_h[h] : p.lam;
   const int64_t rowbase = (int64_t)bh * S;          // token row index base in (B,H,S,*) tensors
-  const T* q1 = reinterpret_cast<const T*>(p.q1);
-  const T* q2 = reinterpret_cast<const T*>(p.q2);
-  const T* kk = reinterpret_cast<const T*>(p.k);
-  const T* vv = reinterpret_cast<const T*>(p.v);
-  T* oo = reinterpret_cast<T*>(p.o);
+  const bf16* q1g = reinterpret_cast<const bf16*>(p.q1);
+  const bf16* q2g = reinterpret_cast<const bf16*>(p.q2);
+  const bf16* kg = reinterpret_cast<const bf16*>(p.k);
+  const bf16* vg = reinterpret_cast<const bf16*>(p.v);
+  bf16* og = reinterpret_cast<bf16*>(p.o);
   const int v0 = vh * DVH;
+  const bool has_q2 = p.q2 != nullptr, has_g = p.g != nullptr;
+  Frag<bf16> id[2];
+  id[0] = ident_frag<bf16>(0, half, l32);
+  id[1] = ident_frag<bf16>(1, half, l32);
 
-  // state tiles S[k][v] for kt = 2*kh + i, v-tile vt of this V-half
+  // state tiles S[k][v] for k-tile 2 kh + i, v-tile vt of this V-half
   f32x16 St[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -98,201 +112,262 @@ __global__ __launch_bounds__(256) void kda_gated_kernel(KdaParams p) {
     }
   }
 
-  const int kc = tid & 127, th = tid >> 7;
-  for (int pos = 0; pos < S;) {
-    // ---- phase A: per-channel cumulative log-decay, admissible segment length
-    if (tid == 0) sm.len = SEGK;
-    float gl[32];
-    float run = 0.f, lmax = -INFINITY, lmin = INFINITY;
+  // tile loads: q1 / q2 / k chunks e = tid + 512 i -> row e >> 4, columns 8 (e & 15); v chunk tid -> row
+  // tid >> 3, columns v0 + 8 (tid & 7); g rows straight into LDS (wave w: 1 KB blocks 4 w .. 4 w + 3)
+  KdaStage stg;
+  auto load_tile = [&](int pos) {
+    const int last = S - 1;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const int t = th * 32 + i;
-      float gv = 0.f;
-      if (p.g && pos + t < S) gv = p.g[(rowbase + pos + t) * DK + kc];
-      run += gv;
-      gl[i] = run;
-      lmax = fmaxf(lmax, run);
-      lmin = fminf(lmin, run);
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 512 * i;
+      const int64_t off = (rowbase + min(pos + (e >> 4), last)) * DK + 8 * (e & 15);
+      stg.q1[i] = *reinterpret_cast<const uint4*>(q1g + off);
+      if (has_q2) stg.q2[i] = *reinterpret_cast<const uint4*>(q2g + off);
+      stg.k[i] = *reinterpret_cast<const uint4*>(kg + off);
     }
-    sm.tot[th][kc] = run;
-    sm.gmax[th][kc] = lmax;
-    sm.gmin[th][kc] = lmin;
-    __syncthreads();
-    const float off = th ? sm.tot[0][kc] : 0.f;
-    float pmax = th ? sm.gmax[0][kc] : -INFINITY;
-    float pmin = th ? sm.gmin[0][kc] : INFINITY;
-    int bad = SEGK;
+    stg.v = *reinterpret_cast<const uint4*>(vg + (rowbase + min(pos + (tid >> 3), last)) * 128 + v0 + 8 * (tid & 7));
+    if (has_g) {
+      const float* gb = p.g + (rowbase + pos) * DK;      // wave-uniform
+      const int rmax = last - pos;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const int t = th * 32 + i;
-      const float G = gl[i] + off;
-      sm.G[t][kc] = G;
-      pmax = fmaxf(pmax, G);
-      pmin = fminf(pmin, G);
-      if ((pmax - pmin > KRANGE || pos + t >= S) && bad == SEGK) bad = t;
+      for (int q = 0; q < 4; ++q) {
+        const int blk = 4 * w + q;                       // rows 2 blk, 2 blk + 1
+        const int r = 2 * blk + (l >> 5);
+        dma_lds<16>(gb, (uint32_t)(min(r, rmax) * DK + 4 * (l & 31)) * 4u, &sm.G[2 * blk][0]);
+      }
     }
-    atomicMin(&sm.len, bad);
-    __syncthreads();
-    const int len = sm.len;
-    if (tid < DK) {
-      const float g0 = sm.G[0][tid], ge = sm.G[len - 1][tid];
-      const float m = 0.5f * (g0 + ge);
-      sm.m[tid] = m;
-      sm.em[tid] = __expf(m);
-      sm.ek[tid] = __expf(ge - m);
-      sm.eg[tid] = __expf(ge);
-    }
-    __syncthreads();
+  };
+  load_tile(0);
 
-    // ---- phase B: operand tiles
-    for (int e = tid; e < SEGK * (DK / 8); e += 256) {
-      const int t = e >> 4, k0 = (e & 15) * 8;
-      const bool in = t < len;
-      float qv1[8], qv2[8], kv[8];
-      if (in) {
-        const int64_t r = (rowbase + pos + t) * DK + k0;
+  for (int pos = 0; pos < S; pos += SEG) {
+    const int len = min(SEG, S - pos);
+    wait_vmem();                                         // this tile's registers and g rows
+    *reinterpret_cast<uint4*>(&sm.V[TV::chunk(tid >> 3, tid & 7)]) = stg.v;
+    lds_barrier();                                       // B1: g rows of every wave are in LDS
+
+    // ---- in-tile cumsum of g per channel: thread (channel kc, token quarter qq)
+    {
+      const int kc = tid & (DK - 1), qq = tid >> 7;
+      float loc[16];
+      float run = 0.f, lmin = INFINITY, lmax = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          qv1[j] = to_f32(q1[r + j]);
-          qv2[j] = p.q2 ? to_f32(q2[r + j]) : 0.f;
-          kv[j] = to_f32(kk[r + j]);
-        }
+      for (int i = 0; i < 16; ++i) {
+        const int t = 16 * qq + i;
+        const float gv = (has_g && t < len) ? sm.G[t][kc] : 0.f;   // g = 0 past the end: G stays flat
+        run += gv;
+        loc[i] = run;
+        lmin = fminf(lmin, run);
+        lmax = fmaxf(lmax, run);
+      }
+      sm.qtot[qq][kc] = run;
+      sm.qmin[qq][kc] = lmin;
+      sm.qmax[qq][kc] = lmax;
+      if (tid == 0) sm.cut = 0;                          // set below (after B2), read after B3
+      lds_barrier();                                     // B2
+      float off = 0.f, end = 0.f, gmin = INFINITY, gmax = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float tq = sm.qtot[q][kc];
+        gmin = fminf(gmin, end + sm.qmin[q][kc]);
+        gmax = fmaxf(gmax, end + sm.qmax[q][kc]);
+        if (q < qq) off += tq;
+        end += tq;
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float qt = 0.f, qh = 0.f, kt = 0.f;
-        if (in) {
-          const float G = sm.G[t][k0 + j], m = sm.m[k0 + j];
-          const float e1 = __expf(G - m);
-          const float qe = qv1[j] - lam * qv2[j];
-          qt = qe * e1;
-          qh = qt * sm.em[k0 + j];
-          kt = kv[j] * __expf(m - G);
-        }
-        sm.Qt[t * SM::PK + k0 + j] = from_f32<T>(qt);
-        sm.Qh[t * SM::PK + k0 + j] = from_f32<T>(qh);
-        sm.Kt[t * SM::PK + k0 + j] = from_f32<T>(kt);
+      for (int i = 0; i < 16; ++i) sm.G[16 * qq + i][kc] = loc[i] + off;
+      if (qq == 0) {
+        // window [0, len): base G_{-1} = 0, end = G_{len-1}, m = midpoint of the G range
+        const float m = 0.5f * (gmin + gmax);
+        sm.mm[kc] = m;
+        sm.em[kc] = __expf(m);
+        sm.ek[kc] = __expf(end - m);
+        sm.eg[kc] = __expf(end);
+        if (gmax - gmin > KRANGE) sm.cut = 1;            // benign race: every writer stores 1
       }
     }
-    for (int e = tid; e < SEGK * (DVH / 8); e += 256) {
-      const int t = e >> 3, c0 = (e & 7) * 8;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (t < len) {
-        if (sizeof(T) == 2) {
-          val = *reinterpret_cast<const uint4*>(vv + (rowbase + pos + t) * 128 + v0 + c0);
+    lds_barrier();                                       // B3: G, window parameters, cut flag
+    const bool cut = sm.cut != 0;
+
+    // ---- factorisation windows [a, b) of this tile
+    for (int a = 0; a < len;) {
+      // lane-dependent LDS addresses are recomputed per window instead of hoisted (and spilled)
+      int lq = l;
+      asm volatile("" : "+v"(lq));
+      const int halfq = lq >> 5, l32q = lq & 31;
+      int b = len;
+      if (cut) {
+        // longest window from a whose per-channel G spread stays within KRANGE (at least one token)
+        if (tid == 0) sm.wend = len;
+        lds_barrier();
+        if (tid < DK) {
+          float mn = INFINITY, mx = -INFINITY;
+          int bad = len;
+          for (int t = a; t < len; ++t) {
+            const float gv = sm.G[t][tid];
+            mn = fminf(mn, gv);
+            mx = fmaxf(mx, gv);
+            if (mx - mn > KRANGE) { bad = t; break; }
+          }
+          atomicMin(&sm.wend, bad);
         }
-      }
-      if (sizeof(T) == 2) {
-        *reinterpret_cast<uint4*>(&sm.V[t * SM::PV + c0]) = val;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          sm.V[t * SM::PV + c0 + j] = (t < len) ? vv[(rowbase + pos + t) * 128 + v0 + c0 + j] : from_f32<T>(0.f);
-      }
-    }
-    __syncthreads();
-
-    // ---- phase C: masked A^T tiles (s-tile, t-tile) in {(0,0),(0,1),(1,1)}
-    if (w < 3) {
-      const int st = (w == 2) ? 1 : 0, tt = (w == 0) ? 0 : 1;
-      f32x16 acc = zero16();
-#pragma unroll
-      for (int c = 0; c < DK / 16; ++c) {
-        Frag<TM> a, bb;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          a.set(j, to_f32(sm.Kt[(32 * st + l32) * SM::PK + 16 * c + 8 * half + j]));
-          bb.set(j, to_f32(sm.Qt[(32 * tt + l32) * SM::PK + 16 * c + 8 * half + j]));
+        lds_barrier();
+        b = max(sm.wend, a + 1);
+        if (tid < DK) {
+          float mn = INFINITY, mx = -INFINITY;
+          for (int t = a; t < b; ++t) {
+            const float gv = sm.G[t][tid];
+            mn = fminf(mn, gv);
+            mx = fmaxf(mx, gv);
+          }
+          const float base = a ? sm.G[a - 1][tid] : 0.f, end = sm.G[b - 1][tid];
+          const float m = 0.5f * (mn + mx);
+          sm.mm[tid] = m;
+          sm.em[tid] = __expf(m - base);
+          sm.ek[tid] = __expf(end - m);
+          sm.eg[tid] = __expf(end - base);
         }
-        acc = mma(a, bb, acc);
+        lds_barrier();
       }
-      const int tl = 32 * tt + l32;
+      const bool last_window = (b == len);
+
+      // Qt = q_e e^{G - m}, Kt = k e^{m - G} on rows [a, b), zero elsewhere
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int s = 32 * st + acc_row(half, r);
-        if (!(s <= tl && s < len)) acc[r] = 0.f;
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + 512 * i;
+        const int r = e >> 4, c8 = e & 15;
+        bf16x8 qo, ko;
+        if (r >= a && r < b) {
+          const bf16x8 x1 = __builtin_bit_cast(bf16x8, stg.q1[i]);
+          const bf16x8 x2 = __builtin_bit_cast(bf16x8, stg.q2[i]);
+          const bf16x8 xk = __builtin_bit_cast(bf16x8, stg.k[i]);
+          const f32x4 g0 = *reinterpret_cast<const f32x4*>(&sm.G[r][8 * c8]);
+          const f32x4 g1 = *reinterpret_cast<const f32x4*>(&sm.G[r][8 * c8 + 4]);
+          const f32x4 m0 = *reinterpret_cast<const f32x4*>(&sm.mm[8 * c8]);
+          const f32x4 m1 = *reinterpret_cast<const f32x4*>(&sm.mm[8 * c8 + 4]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float d = (j < 4 ? g0[j] : g1[j - 4]) - (j < 4 ? m0[j] : m1[j - 4]);   // G - m
+            const float qe = has_q2 ? (float)x1[j] - lam * (float)x2[j] : (float)x1[j];
+            qo[j] = (bf16)(qe * __expf(d));
+            ko[j] = (bf16)((float)xk[j] * __expf(-d));
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) qo[j] = ko[j] = (bf16)0.f;
+        }
+        *reinterpret_cast<bf16x8*>(&sm.Qt[TQ::chunk(r, c8)]) = qo;
+        *reinterpret_cast<bf16x8*>(&sm.Kt[TQ::chunk(r, c8)]) = ko;
       }
-      sf.A[w][0][l] = acc_to_frag<TM>(acc, 0);
-      sf.A[w][1][l] = acc_to_frag<TM>(acc, 1);
-    }
-    __syncthreads();
+      lds_barrier();                                     // Qt, Kt ready; G no longer read
+      if (last_window && pos + SEG < S) load_tile(pos + SEG);   // next tile streams in behind the MFMAs
 
-    // ---- phase D: per wave (v-tile vt, k-half kh)
-    Frag<TM> vf[4];
+      // ---- phase 1: A^T tiles (waves 5..7), operand transposes, read-out partial
+      if (w >= 5) {
+        const int it = w - 5;
+        const int st = (it == 2) ? 1 : 0, ttA = (it == 0) ? 0 : 1;
+        f32x16 acc = zero16();
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < DK / 16; ++c)
+          acc = mma(row_frag<bf16, bf16, DK>(sm.Kt, 32 * st + l32q, 16 * c + 8 * halfq),
+                    row_frag<bf16, bf16, DK>(sm.Qt, 32 * ttA + l32q, 16 * c + 8 * halfq), acc);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) vf[c].set(j, to_f32(sm.V[(16 * c + kset(half, j)) * SM::PV + 32 * vt + l32]));
-
-    f32x16 o[2];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      f32x16 acc = zero16();
+        for (int r = 0; r < 16; ++r)
+          if (32 * st + acc_row(halfq, r) > 32 * ttA + l32q) acc[r] = 0.f;
+        sm.A[it][0][lq] = acc_to_frag<bf16>(acc, 0);
+        sm.A[it][1][lq] = acc_to_frag<bf16>(acc, 1);
+      }
+      // o^T[v][t] = sum_k (S[k][v] e^{m_k - base_k}) Qt[t][k] over this wave's k-half, t-tile tt
+      f32x16 o = zero16();
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int kt = 2 * kh + i;
+        f32x16 sv = St[i];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const Frag<TM> sa = acc_to_frag<TM>(St[i], c);
-          Frag<TM> qb;
-          const T* row = sm.Qh + (32 * tt + l32) * SM::PK + 32 * kt + 16 * c;
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 e4 = *reinterpret_cast<const f32x4*>(&sm.em[32 * kt + 8 * q + 4 * halfq]);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            qb.set(j, to_f32(row[4 * half + j]));
-            qb.set(4 + j, to_f32(row[8 + 4 * half + j]));
-          }
-          acc = mma(sa, qb, acc);
+          for (int j = 0; j < 4; ++j) sv[4 * q + j] *= e4[j];
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          o = mma(acc_to_frag<bf16>(sv, c), kset_frag<bf16, bf16, DK>(sm.Qt, 32 * tt + l32q, 32 * kt + 16 * c, halfq), o);
+      }
+      lds_barrier();                                     // A^T fragments ready
+
+      // ---- phase 2: intra-window term (kh = 0), partial exchange, state update
+      // v^T fragments (lane = v, k = token)
+      Frag<bf16> vf[4];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const f32x16 d = mfma_transpose<bf16, bf16, DVH>(sm.V, 32 * st, 32 * vt, id, halfq, l32q);
+        vf[2 * st] = acc_to_frag<bf16>(d, 0);
+        vf[2 * st + 1] = acc_to_frag<bf16>(d, 1);
+      }
+      if (kh == 0) {
+        if (tt == 0) {
+          o = mma(vf[0], sm.A[0][0][lq], o);
+          o = mma(vf[1], sm.A[0][1][lq], o);
+        } else {
+          o = mma(vf[0], sm.A[1][0][lq], o);
+          o = mma(vf[1], sm.A[1][1][lq], o);
+          o = mma(vf[2], sm.A[2][0][lq], o);
+          o = mma(vf[3], sm.A[2][1][lq], o);
+        }
+      } else {
+        sm.red[vt][tt][lq] = o;
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int kt = 2 * kh + i;
+        // e^{end - m}-scaled k^T fragments (lane = channel, k = token)
+        const float ekl = sm.ek[32 * kt + l32q];
+        Frag<bf16> kf[4];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const f32x16 d = mfma_transpose<bf16, bf16, DK>(sm.Kt, 32 * st, 32 * kt, id, halfq, l32q);
+          kf[2 * st] = acc_to_frag_scaled<bf16>(d, 0, ekl);
+          kf[2 * st + 1] = acc_to_frag_scaled<bf16>(d, 1, ekl);
+        }
+        f32x16 acc = St[i];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 e4 = *reinterpret_cast<const f32x4*>(&sm.eg[32 * kt + 8 * q + 4 * halfq]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[4 * q + j] *= e4[j];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc = mma(kf[c], vf[c], acc);
+        St[i] = acc;
+      }
+      lds_barrier();                                     // partials in LDS; Kt, V, A^T no longer read
+
+      // ---- output rows [a, b) of block (vt, tt): staged, then 16-byte stores
+      if (kh == 0) {
+        const f32x16 other = sm.red[vt][tt][lq];
+        bf16* ob = sm.O[2 * vt + tt];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c0 = 8 * q + 4 * halfq;              // 4 consecutive v columns inside one 16-byte chunk
+          bf16x4 yv;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) yv[j] = (bf16)(o[4 * q + j] + other[4 * q + j]);
+          *reinterpret_cast<bf16x4*>(ob + XO::chunk(l32q, c0 >> 3) + (c0 & 7)) = yv;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int e = lq + 64 * i;
+          const int r = e >> 2, c = e & 3;               // row t of the block, 16-byte chunk
+          const uint4 val = *reinterpret_cast<const uint4*>(ob + XO::chunk(r, c));
+          const int t = 32 * tt + r;
+          if (t >= a && t < b)
+            *reinterpret_cast<uint4*>(og + (rowbase + pos + t) * 128 + v0 + 32 * vt + 8 * c) = val;
         }
       }
-      o[tt] = acc;
+      a = b;
     }
-    if (kh == 0) {
-      o[0] = mma(vf[0], sf.A[0][0][l], o[0]);
-      o[0] = mma(vf[1], sf.A[0][1][l], o[0]);
-    } else {
-      o[1] = mma(vf[0], sf.A[1][0][l], o[1]);
-      o[1] = mma(vf[1], sf.A[1][1][l], o[1]);
-      o[1] = mma(vf[2], sf.A[2][0][l], o[1]);
-      o[1] = mma(vf[3], sf.A[2][1][l], o[1]);
-      sm.red[vt][0][l] = o[0];
-      sm.red[vt][1][l] = o[1];
-    }
-    // state update (uses sm.Kt, sm.V, sm.eg, sm.ek only)
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int kt = 2 * kh + i;
-      const int krow = 32 * kt + l32;           // A-operand row of this lane
-      const float ekr = sm.ek[krow];
-      f32x16 acc = St[i];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] *= sm.eg[32 * kt + acc_row(half, r)];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        Frag<TM> kf;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) kf.set(j, ekr * to_f32(sm.Kt[(16 * c + kset(half, j)) * SM::PK + krow]));
-        acc = mma(kf, vf[c], acc);
-      }
-      St[i] = acc;
-    }
-    __syncthreads();
-    if (kh == 0) {
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int tl = 32 * tt + l32;
-        const f32x16 other = sm.red[vt][tt][l];
-        if (tl < len) {
-          T* orow = oo + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = from_f32<T>(o[tt][r] + other[r]);
-        }
-      }
-    }
-    __syncthreads();
-    pos += len;
   }
 
-  if (p.final_state) {
+  if (p.final_state && tt == 0) {
     float* sf_out = p.final_state + (int64_t)bh * DK * 128;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -304,6 +379,14 @@ __global__ __launch_bounds__(256) void kda_gated_kernel(KdaParams p) {
   }
 }
 
+// Empty sequence: final state (and z) = initial (or zero), written by a plain kernel (no copy or memset
+// node, so a captured launch behaves the same).
+__global__ __launch_bounds__(256) void kda_empty_kernel(const float* __restrict__ s0, float* __restrict__ sf, size_t ns,
+                                                       const float* __restrict__ z0, float* __restrict__ zf, size_t nz) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (sf && i < ns) sf[i] = s0 ? s0[i] : 0.f;
+  if (zf && i < nz) zf[i] = z0 ? z0[i] : 0.f;
+}
 
 // ---------------------------------------------------------------------------
 // Reference mode: the reference's normalised linear-attention scan
@@ -595,27 +678,20 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
 hipError_t launch_kda(const KdaParams& p, hipStream_t st) {
   const int nbh = p.batch * p.nheads;
   if (p.seqlen == 0) {
-    if (p.final_state) {
-      const size_t bytes = (size_t)nbh * DK * 128 * sizeof(float);
-      hipError_t e = p.init_state ? hipMemcpyAsync(p.final_state, p.init_state, bytes, hipMemcpyDeviceToDevice, st)
-                                  : hipMemsetAsync(p.final_state, 0, bytes, st);
-      if (e != hipSuccess) return e;
-    }
-    if (p.final_z) {
-      const size_t bytes = (size_t)nbh * DK * sizeof(float);
-      return p.init_z ? hipMemcpyAsync(p.final_z, p.init_z, bytes, hipMemcpyDeviceToDevice, st)
-                      : hipMemsetAsync(p.final_z, 0, bytes, st);
-    }
-    return hipSuccess;
+    const size_t ns = p.final_state ? (size_t)nbh * DK * 128 : 0, nz = p.final_z ? (size_t)nbh * DK : 0;
+    const size_t n = ns > nz ? ns : nz;
+    if (n) hipLaunchKernelGGL(kda_empty_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p.init_state,
+                              p.final_state, ns, p.init_z, p.final_z, nz);
+    return hipGetLastError();
   }
   if (p.dtype != DT_BF16) return hipErrorInvalidValue;
-  dim3 grid((unsigned)(2 * nbh)), block(256);
+  const dim3 grid((unsigned)(2 * nbh));
   if (p.mode == 0) {
-    hipLaunchKernelGGL((kda_gated_kernel<bf16, bf16>), grid, block, 0, st, p);
+    hipLaunchKernelGGL(kda_gated_kernel, grid, dim3(64 * KW), 0, st, p);
   } else if (p.q2) {
-    hipLaunchKernelGGL(kda_ref_kernel<2>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(kda_ref_kernel<2>, grid, dim3(256), 0, st, p);
   } else {
-    hipLaunchKernelGGL(kda_ref_kernel<1>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(kda_ref_kernel<1>, grid, dim3(256), 0, st, p);
   }
   return hipGetLastError();
 }

@@ -46,10 +46,10 @@
 // bf16 I/O uses 32x32x16 bf16 MFMAs, fp32 I/O 32x32x2 fp32 MFMAs; accumulation is fp32.
 #include "common.h"
 #include "launch.h"
+#include "tiles.h"
 
 namespace mh {
 
-constexpr int SEG = 64;              // tokens per segment
 constexpr int HD = 64;               // headdim handled by these kernels
 constexpr float FACT_RANGE = 60.f;   // max exponent of an operand scale factor
 
@@ -60,227 +60,6 @@ __device__ __forceinline__ float process_dt(const SsdParams& p, float dt, float 
   if (p.dt_softplus) dt = softplus_f(dt);
   if (p.has_dt_limit) dt = fminf(fmaxf(dt, p.dt_min), p.dt_max);
   return dt;
-}
-
-// vmcnt(n) through the builtin (vmcnt n, expcnt 7, lgkmcnt 15), so the compiler's own wait tracking
-// knows the counter state.  Loads complete in issue order: vmcnt(n) waits for all but the n most recent.
-template <int n>
-__device__ __forceinline__ void wait_vmem_n() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00);
-  asm volatile("" ::: "memory");
-}
-__device__ __forceinline__ void wait_vmem() { wait_vmem_n<0>(); }
-__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
-
-// ------------------------------------------------------------------ LDS tiles
-
-// B / C tiles: SEG rows of W elements, unpadded, 16-byte chunks XOR-swizzled by
-// row (chunk c of row r lives at chunk c ^ (r & MASK)) so the lanes of one LDS
-// access phase, reading the same column of consecutive rows, hit distinct banks.
-template <typename T, int W>
-struct Tile {
-  static constexpr int EPC = 16 / (int)sizeof(T);   // elements per 16-byte chunk
-  static constexpr int CPR = W / EPC;               // chunks per row (power of two)
-  static constexpr int MASK = (CPR < 16 ? CPR : 16) - 1;
-  static constexpr int RPB = 64 / CPR;              // rows per 1 KB block (one wave-wide direct load)
-  static constexpr int NBLK = SEG / RPB;            // 1 KB blocks per tile
-  __device__ static __forceinline__ int chunk(int r, int c) { return r * W + (c ^ (r & MASK)) * EPC; }
-};
-
-// One wave's half of a head's x tile: SEG token rows x 32 columns.  Rows of 64
-// bytes (bf16) are swizzled with ((r >> 1) ^ (r >> 3)) & 3, which spreads the
-// 16-byte reads of 16 consecutive rows over all banks whether the LDS serves
-// 8 or 16 lanes of a 128-bit read per cycle; 128-byte rows (fp32) use r & 7.
-template <typename T>
-struct XHalf {
-  static constexpr int W = 32;
-  static constexpr int EPC = 16 / (int)sizeof(T);
-  static constexpr int CPR = W / EPC;               // 4 (bf16) / 8 (fp32)
-  static constexpr int RPB = 64 / CPR;              // 16 / 8 rows per 1 KB block
-  static constexpr int NBLK = SEG / RPB;            // 4 / 8 blocks
-  __device__ static __forceinline__ int swz(int r) {
-    if constexpr (CPR == 4) return ((r >> 1) ^ (r >> 3)) & 3;
-    else return r & 7;
-  }
-  __device__ static __forceinline__ int chunk(int r, int c) { return r * W + (c ^ swz(r)) * EPC; }
-};
-
-// Direct global -> LDS load of `bytes` (16 or 4) per lane from a wave-uniform base plus a 32-bit lane
-// offset (scalar-base addressing: no 64-bit per-lane address arithmetic).  Token strides are validated on
-// the host so that a segment's span (SEG rows) stays below 2 GiB.
-template <int bytes>
-__device__ __forceinline__ void dma_lds(const void* base, uint32_t off, void* lds) {
-  static_assert(bytes == 16 || bytes == 4, "direct-to-LDS load size");
-  glb_void_t* g = (glb_void_t*)(reinterpret_cast<const char*>(base) + off);
-  if constexpr (bytes == 16) __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 16, 0, 0);
-  else __builtin_amdgcn_global_load_lds(g, (lds_void_t*)lds, 4, 0, 0);
-}
-
-// Direct global -> LDS fetch of 1 KB blocks [blk0, blk0 + nblk) of a swizzled
-// B/C tile: lane i of the wave writes LDS bytes [16 i, 16 i + 16) of the block,
-// so it fetches the logical chunk that the swizzle places there.  Rows past
-// `last_tok` (end of the sequence) re-read the last valid row; their values
-// are finite and every consumer masks them.
-template <typename T, int W>
-__device__ __forceinline__ void fetch_tile(T* dst, const T* src, int64_t row_stride, int tok0, int last_tok,
-                                           int blk0, int nblk, int lane) {
-  using TL = Tile<T, W>;
-  const int rr = lane / TL::CPR, phys = lane % TL::CPR;
-  const T* base = src + (int64_t)tok0 * row_stride;       // wave-uniform
-  const int rmax = last_tok - tok0;                        // >= 0; rows beyond it are clamped
-  for (int q = 0; q < nblk; ++q) {
-    const int blk = blk0 + q;
-    const int r = blk * TL::RPB + rr;
-    const int c = phys ^ (r & TL::MASK);
-    const uint32_t off = (uint32_t)(min(r, rmax) * (int)row_stride + c * TL::EPC) * (uint32_t)sizeof(T);
-    dma_lds<16>(base, off, dst + blk * (1024 / (int)sizeof(T)));
-  }
-}
-
-// Direct fetch of a wave's x half tile (src points at column 0 of the half).
-template <typename T>
-__device__ __forceinline__ void fetch_xhalf(T* dst, const T* src, int64_t row_stride, int tok0, int last_tok,
-                                            int lane) {
-  using X = XHalf<T>;
-  const int rr = lane / X::CPR, phys = lane % X::CPR;
-  const T* base = src + (int64_t)tok0 * row_stride;
-  const int rmax = last_tok - tok0;
-#pragma unroll
-  for (int blk = 0; blk < X::NBLK; ++blk) {
-    const int r = blk * X::RPB + rr;
-    const int c = phys ^ X::swz(r);
-    const uint32_t off = (uint32_t)(min(r, rmax) * (int)row_stride + c * X::EPC) * (uint32_t)sizeof(T);
-    dma_lds<16>(base, off, dst + blk * (1024 / (int)sizeof(T)));
-  }
-}
-
-// Direct fetch of the raw dt of 64 tokens (lane = token, rows past the end clamped) into LDS.
-__device__ __forceinline__ void fetch_dt(float* dst, const float* src, int64_t stride, int tok0, int last_tok,
-                                         int lane) {
-  const float* base = src + (int64_t)tok0 * stride;
-  dma_lds<4>(base, (uint32_t)(min(lane, last_tok - tok0) * (int)stride) * 4u, dst);
-}
-
-// Direct copy of nb contiguous 1 KB blocks starting at block b0 (precomputed fragments).
-__device__ __forceinline__ void fetch_blocks(char* dst, const char* src, int b0, int nb, int lane) {
-  for (int q = 0; q < nb; ++q) dma_lds<16>(src + (b0 + q) * 1024, 16u * lane, dst + (b0 + q) * 1024);
-}
-
-// y rows staged in a wave's x half tile: lane-held 16-byte chunks (read), then written to HBM.
-template <typename T>
-__device__ __forceinline__ void load_yhalf(const T* tile, int lane, uint4 (&v)[XHalf<T>::NBLK]) {
-  using X = XHalf<T>;
-#pragma unroll
-  for (int i = 0; i < X::NBLK; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = *reinterpret_cast<const uint4*>(tile + X::chunk(e / X::CPR, e % X::CPR));
-  }
-}
-// All SEG rows (a full segment): exactly NBLK store instructions per wave, whatever the lane.
-template <typename T>
-__device__ __forceinline__ void store_yhalf_full(T* dst, int64_t row_stride, const uint4 (&v)[XHalf<T>::NBLK],
-                                                 int lane) {
-  using X = XHalf<T>;
-#pragma unroll
-  for (int i = 0; i < X::NBLK; ++i) {
-    const int e = lane + 64 * i;
-    *reinterpret_cast<uint4*>(dst + (int64_t)(e / X::CPR) * row_stride + (e % X::CPR) * X::EPC) = v[i];
-  }
-}
-// Rows [0, len) only.
-template <typename T>
-__device__ __forceinline__ void store_yhalf(T* dst, int64_t row_stride, const T* tile, int len, int lane) {
-  using X = XHalf<T>;
-  uint4 v[X::NBLK];
-  load_yhalf<T>(tile, lane, v);
-#pragma unroll
-  for (int i = 0; i < X::NBLK; ++i) {
-    const int e = lane + 64 * i;
-    const int r = e / X::CPR, c = e % X::CPR;
-    if (r < len) *reinterpret_cast<uint4*>(dst + (int64_t)r * row_stride + c * X::EPC) = v[i];
-  }
-  wait_lds();   // the staged rows have been read: the buffer may be refilled
-}
-
-// 8 consecutive elements of row r starting at column e0 (e0 % 8 == 0) as an MFMA fragment.
-template <typename TM, typename T, int W>
-__device__ __forceinline__ Frag<TM> row_frag(const T* tile, int r, int e0) {
-  Frag<TM> f;
-  if constexpr (sizeof(T) == 2) {
-    f.v = *reinterpret_cast<const bf16x8*>(tile + Tile<T, W>::chunk(r, e0 / 8));
-  } else {
-    const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + Tile<T, W>::chunk(r, e0 / 4));
-    const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + Tile<T, W>::chunk(r, e0 / 4 + 1));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) { f.v[j] = lo[j]; f.v[4 + j] = hi[j]; }
-  }
-  return f;
-}
-template <typename TM, typename T>
-__device__ __forceinline__ Frag<TM> xrow_frag(const T* tile, int r, int e0) {
-  using X = XHalf<T>;
-  Frag<TM> f;
-  if constexpr (sizeof(T) == 2) {
-    f.v = *reinterpret_cast<const bf16x8*>(tile + X::chunk(r, e0 / 8));
-  } else {
-    const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + X::chunk(r, e0 / 4));
-    const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + X::chunk(r, e0 / 4 + 1));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) { f.v[j] = lo[j]; f.v[4 + j] = hi[j]; }
-  }
-  return f;
-}
-// KSET fragment of row r (base % 16 == 0): columns base+4*half+{0..3} and base+8+4*half+{0..3}.
-template <typename TM, typename T, int W>
-__device__ __forceinline__ Frag<TM> kset_frag(const T* tile, int r, int base, int half) {
-  Frag<TM> f;
-  if constexpr (sizeof(T) == 2) {
-    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(tile + Tile<T, W>::chunk(r, base / 8) + 4 * half);
-    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(tile + Tile<T, W>::chunk(r, base / 8 + 1) + 4 * half);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) { f.v[j] = lo[j]; f.v[4 + j] = hi[j]; }
-  } else {
-    const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + Tile<T, W>::chunk(r, base / 4 + half));
-    const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + Tile<T, W>::chunk(r, base / 4 + 2 + half));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) { f.v[j] = lo[j]; f.v[4 + j] = hi[j]; }
-  }
-  return f;
-}
-
-// Values of a per-token array at the 8 tokens a KSET fragment covers (k-step c):
-// tokens 16c+4*half+{0..3} and 16c+8+4*half+{0..3}, read as two float4.
-__device__ __forceinline__ void kset_vals(const float* v, int c, int half, float (&s)[8]) {
-  const f32x4 lo = *reinterpret_cast<const f32x4*>(v + 16 * c + 4 * half);
-  const f32x4 hi = *reinterpret_cast<const f32x4*>(v + 16 * c + 8 + 4 * half);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) { s[j] = lo[j]; s[4 + j] = hi[j]; }
-}
-
-// Identity B-operand fragment for k-step c of a 32-wide block: element j has
-// k = 16c + 8*half + j, the lane's column is l32.
-template <typename TM>
-__device__ __forceinline__ Frag<TM> ident_frag(int c, int half, int l32) {
-  Frag<TM> f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) f.set(j, (16 * c + 8 * half + j == l32) ? 1.f : 0.f);
-  return f;
-}
-
-// Transpose a 32x32 block of a row-major B tile through the MFMA unit:
-// returns the accumulator tile D[r][q] = tile[r0 + r][q0 + q] (r, q < 32), whose
-// lane l holds column q0 + (l % 32) and rows r0 + acc_row(half, i).
-template <typename TM, typename T, int W>
-__device__ __forceinline__ f32x16 mfma_transpose(const T* tile, int r0, int q0, const Frag<TM> (&id)[2], int half,
-                                                 int l32) {
-  f32x16 acc = zero16();
-#pragma unroll
-  for (int c = 0; c < 2; ++c) acc = mma(row_frag<TM, T, W>(tile, r0 + l32, q0 + 16 * c + 8 * half), id[c], acc);
-  return acc;
 }
 
 // x^T of a wave's x half tile (lane = p, tokens on the k axis, KSET order) as
