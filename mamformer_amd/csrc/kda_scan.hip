@@ -33,14 +33,13 @@ constexpr float KRANGE = 50.f;    // max spread of G per channel within a segmen
 
 // ----------------------------------------------------------------- gated mode
 // One workgroup of 8 waves per (b, h, V-half) walks the sequence in 64-token
-// tiles.  The next tile's q1, q2, k, v are loaded into registers (and its g
-// straight into LDS) while the current tile computes, so the walk streams at
-// memory speed.  Wave w owns v-tile vt = w & 1, t-tile tt = (w >> 1) & 1 and
+// tiles.  The next tile's q1, q2, k, v and g are loaded into registers while
+// the current tile computes, so the walk streams at memory speed.  Wave w owns v-tile vt = w & 1, t-tile tt = (w >> 1) & 1 and
 // k-half kh = w >> 2: it keeps the state tiles S[kh][vt] (replicated over tt),
 // computes the read-out partial of (vt, tt) over its k-half, and the kh = 1
 // partials are summed through LDS.  Waves 5..7 also form the three masked
-// A^T tiles.  Token-contracted operands (k^T, v^T) are transposed on the MFMA
-// unit.  A tile is one factorisation window unless the spread of G within it
+// A^T tiles while waves 0..4 transpose the token-contracted operands (k^T,
+// v^T) on the MFMA unit, each transpose once per tile, shared through LDS.  A tile is one factorisation window unless the spread of G within it
 // exceeds KRANGE for some channel; it is then cut into shorter windows.
 constexpr int KW = 8;                 // waves per workgroup
 
@@ -50,6 +49,8 @@ struct KdaGatedSmem {
   bf16 Kt[SEG * DK];                  // k e^{m - G}     (zero rows outside the window)
   bf16 V[SEG * DVH];                  // v[:, V-half]    (Tile<bf16, DVH>)
   Frag<bf16> A[3][2][64];             // masked A^T tiles (s0,t0), (s0,t1), (s1,t1) as B-operand fragments
+  Frag<bf16> VF[2][4][64];            // v^T fragments per v-tile (lane = v, k = token 16 c + KSET)
+  Frag<bf16> KF[4][4][64];            // e^{end - m}-scaled k^T fragments per k-tile (lane = channel)
   f32x16 red[2][2][64];               // read-out partials of the kh = 1 waves: vt, tt, lane
   bf16 O[4][32 * 32];                 // o blocks (vt, tt) staged for coalesced stores (XHalf rows 0..31)
   float qtot[4][DK], qmin[4][DK], qmax[4][DK];   // per token-quarter cumsum statistics
@@ -57,9 +58,10 @@ struct KdaGatedSmem {
   int wend, cut;
 };
 
-// Register-staged q1, q2, k (two 16-byte chunks each per thread) and v (one) of a tile.
+// Register-staged q1, q2, k (two 16-byte chunks each per thread), v (one) and g (four) of a tile.
 struct KdaStage {
   uint4 q1[2], q2[2], k[2], v;
+  f32x4 g[4];
 };
 
 }  // namespace
@@ -112,10 +114,11 @@ __global__ __launch_bounds__(64 * KW) void kda_gated_kernel(KdaParams p) {
     }
   }
 
-  // tile loads: q1 / q2 / k chunks e = tid + 512 i -> row e >> 4, columns 8 (e & 15); v chunk tid -> row
-  // tid >> 3, columns v0 + 8 (tid & 7); g rows straight into LDS (wave w: 1 KB blocks 4 w .. 4 w + 3)
+  // tile loads into registers (plain loads: a direct-to-LDS load in flight would make every later LDS
+  // access of the tile wait for it): q1 / q2 / k chunks e = tid + 512 i -> row e >> 4, columns 8 (e & 15);
+  // v chunk tid -> row tid >> 3, columns v0 + 8 (tid & 7); g chunks e = tid + 512 i -> row e >> 5, columns 4 (e & 31)
   KdaStage stg;
-  auto load_tile = [&](int pos) {
+  auto load_qk = [&](int pos) {
     const int last = S - 1;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -125,25 +128,33 @@ __global__ __launch_bounds__(64 * KW) void kda_gated_kernel(KdaParams p) {
       if (has_q2) stg.q2[i] = *reinterpret_cast<const uint4*>(q2g + off);
       stg.k[i] = *reinterpret_cast<const uint4*>(kg + off);
     }
+  };
+  auto load_gv = [&](int pos) {
+    const int last = S - 1;
     stg.v = *reinterpret_cast<const uint4*>(vg + (rowbase + min(pos + (tid >> 3), last)) * 128 + v0 + 8 * (tid & 7));
     if (has_g) {
-      const float* gb = p.g + (rowbase + pos) * DK;      // wave-uniform
-      const int rmax = last - pos;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int blk = 4 * w + q;                       // rows 2 blk, 2 blk + 1
-        const int r = 2 * blk + (l >> 5);
-        dma_lds<16>(gb, (uint32_t)(min(r, rmax) * DK + 4 * (l & 31)) * 4u, &sm.G[2 * blk][0]);
+      for (int i = 0; i < 4; ++i) {
+        const int e = tid + 512 * i;                     // row e >> 5, columns 4 (e & 31)
+        stg.g[i] = *reinterpret_cast<const f32x4*>(p.g + (rowbase + min(pos + (e >> 5), last)) * DK + 4 * (e & 31));
       }
     }
   };
-  load_tile(0);
+  load_gv(0);
+  load_qk(0);
 
   for (int pos = 0; pos < S; pos += SEG) {
     const int len = min(SEG, S - pos);
-    wait_vmem();                                         // this tile's registers and g rows
+    wait_vmem();                                         // this tile's registers
     *reinterpret_cast<uint4*>(&sm.V[TV::chunk(tid >> 3, tid & 7)]) = stg.v;
-    lds_barrier();                                       // B1: g rows of every wave are in LDS
+    if (has_g) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = tid + 512 * i;
+        *reinterpret_cast<f32x4*>(&sm.G[e >> 5][4 * (e & 31)]) = stg.g[i];
+      }
+    }
+    lds_barrier();                                       // B1: g and v rows are in LDS
 
     // ---- in-tile cumsum of g per channel: thread (channel kc, token quarter qq)
     {
@@ -259,10 +270,27 @@ __global__ __launch_bounds__(64 * KW) void kda_gated_kernel(KdaParams p) {
         *reinterpret_cast<bf16x8*>(&sm.Kt[TQ::chunk(r, c8)]) = ko;
       }
       lds_barrier();                                     // Qt, Kt ready; G no longer read
-      if (last_window && pos + SEG < S) load_tile(pos + SEG);   // next tile streams in behind the MFMAs
+      const bool prefetch = last_window && pos + SEG < S;
+      if (prefetch) load_gv(pos + SEG);                  // the next tile streams in behind the MFMAs
 
-      // ---- phase 1: A^T tiles (waves 5..7), operand transposes, read-out partial
-      if (w >= 5) {
+      // ---- phase 1: A^T tiles (waves 5..7), the 12 operand transposes (waves 0..4), read-out partials
+      if (w < 5) {
+        // jobs 0..3: v^T of (v-tile j >> 1, token tile j & 1); 4..11: k^T of (k-tile (j-4) >> 1, token tile)
+        for (int j = w; j < 12; j += 5) {
+          if (j < 4) {
+            const int vtj = j >> 1, st = j & 1;
+            const f32x16 d = mfma_transpose<bf16, bf16, DVH>(sm.V, 32 * st, 32 * vtj, id, halfq, l32q);
+            sm.VF[vtj][2 * st][lq] = acc_to_frag<bf16>(d, 0);
+            sm.VF[vtj][2 * st + 1][lq] = acc_to_frag<bf16>(d, 1);
+          } else {
+            const int kt = (j - 4) >> 1, st = (j - 4) & 1;
+            const float ekl = sm.ek[32 * kt + l32q];
+            const f32x16 d = mfma_transpose<bf16, bf16, DK>(sm.Kt, 32 * st, 32 * kt, id, halfq, l32q);
+            sm.KF[kt][2 * st][lq] = acc_to_frag_scaled<bf16>(d, 0, ekl);
+            sm.KF[kt][2 * st + 1][lq] = acc_to_frag_scaled<bf16>(d, 1, ekl);
+          }
+        }
+      } else {
         const int it = w - 5;
         const int st = (it == 2) ? 1 : 0, ttA = (it == 0) ? 0 : 1;
         f32x16 acc = zero16();
@@ -292,17 +320,13 @@ __global__ __launch_bounds__(64 * KW) void kda_gated_kernel(KdaParams p) {
         for (int c = 0; c < 2; ++c)
           o = mma(acc_to_frag<bf16>(sv, c), kset_frag<bf16, bf16, DK>(sm.Qt, 32 * tt + l32q, 32 * kt + 16 * c, halfq), o);
       }
-      lds_barrier();                                     // A^T fragments ready
+      lds_barrier();                                     // A^T, v^T, k^T fragments ready
+      if (prefetch) load_qk(pos + SEG);
 
       // ---- phase 2: intra-window term (kh = 0), partial exchange, state update
-      // v^T fragments (lane = v, k = token)
       Frag<bf16> vf[4];
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const f32x16 d = mfma_transpose<bf16, bf16, DVH>(sm.V, 32 * st, 32 * vt, id, halfq, l32q);
-        vf[2 * st] = acc_to_frag<bf16>(d, 0);
-        vf[2 * st + 1] = acc_to_frag<bf16>(d, 1);
-      }
+      for (int c = 0; c < 4; ++c) vf[c] = sm.VF[vt][c][lq];
       if (kh == 0) {
         if (tt == 0) {
           o = mma(vf[0], sm.A[0][0][lq], o);
@@ -319,15 +343,9 @@ __global__ __launch_bounds__(64 * KW) void kda_gated_kernel(KdaParams p) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int kt = 2 * kh + i;
-        // e^{end - m}-scaled k^T fragments (lane = channel, k = token)
-        const float ekl = sm.ek[32 * kt + l32q];
         Frag<bf16> kf[4];
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          const f32x16 d = mfma_transpose<bf16, bf16, DK>(sm.Kt, 32 * st, 32 * kt, id, halfq, l32q);
-          kf[2 * st] = acc_to_frag_scaled<bf16>(d, 0, ekl);
-          kf[2 * st + 1] = acc_to_frag_scaled<bf16>(d, 1, ekl);
-        }
+        for (int c = 0; c < 4; ++c) kf[c] = sm.KF[kt][c][lq];
         f32x16 acc = St[i];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -339,7 +357,7 @@ __global__ __launch_bounds__(64 * KW) void kda_gated_kernel(KdaParams p) {
         for (int c = 0; c < 4; ++c) acc = mma(kf[c], vf[c], acc);
         St[i] = acc;
       }
-      lds_barrier();                                     // partials in LDS; Kt, V, A^T no longer read
+      lds_barrier();                                     // partials in LDS; tile fragments no longer read
 
       // ---- output rows [a, b) of block (vt, tt): staged, then 16-byte stores
       if (kh == 0) {
