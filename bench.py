@@ -8,7 +8,7 @@ batch; three input/output buffer sets rotate so the 256 MB MALL cannot serve
 a step from the previous one.  The same JSON line carries:
 
 * ``roofline`` -- one launch of the prefill op (``mh_ssd_chunk_scan_fwd``:
-  chunk_state + state_pass + chunk_scan dispatches): algorithmic bytes per
+  seg_frags + chunk_state + state_pass + chunk_scan dispatches): algorithmic bytes per
   launch (compulsory I/O only) / average launch duration from HIP events on
   the launch stream, against 8 TB/s (the op is HBM-bound by intensity).
 * ``cpu_baseline`` -- the reference's pure-PyTorch CPU prefill
@@ -208,12 +208,12 @@ def copy_calibration(nbytes, reps=5):
     log(f"copy calibration: {reps} x {nbytes} bytes")
 
 
-def measured_traffic():
-    """HBM bytes per launch of the headline op from the committed PMC summary, or None."""
+def measured_traffic(workload="ssd2"):
+    """HBM bytes per launch of a workload's op from the committed PMC summary, or None."""
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
-        return t.get("ssd2")
+        return t.get(workload)
     except (OSError, ValueError):
         return None
 
@@ -233,7 +233,8 @@ def main():
     ap.add_argument("--only", default=None,
                     help=f"comma-separated legs to run, of {','.join(LEGS)} (profiling); the JSON line then carries "
                          "only those")
-    ap.add_argument("--cpu-sample", type=int, default=512)
+    ap.add_argument("--cpu-sample", type=int, default=4096,
+                    help="tokens per sequence of the CPU baseline sample (ssd2 has 4096: the whole workload)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="first run a plain device copy of BYTES (HBM counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -291,7 +292,7 @@ def main():
             "bound": "hbm", "achieved": round(head["hbm_GBs"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "frac": round(head["hbm_GBs"] / (PEAK_HBM / 1e9), 4),
             "traffic": None if tr is None else tr["bytes_per_launch"],
-            "kernel": "mh_ssd_chunk_scan_fwd (ssd_chunk_state + ssd_state_pass + ssd_chunk_scan)",
+            "kernel": "mh_ssd_chunk_scan_fwd (ssd_seg_frags + ssd_chunk_state + ssd_state_pass + ssd_chunk_scan)",
             "alg_bytes_per_launch": head["alg_bytes"], "alg_flops_per_launch": head["alg_flops"],
             "launch_us": round(head["us_per_step"], 2),
             "mfma_frac": round(head["alg_flops"] / (head["us_per_step"] * 1e-6) / PEAK_BF16, 4),
@@ -315,6 +316,9 @@ def main():
         r = bench_kda(W.KDA5, max(5, args.steps // 5), 3)
         log(f"kda5: {r['mtok_s']:.1f} Mtok/s, {r['us_per_step']:.0f} us, roofline {r['roofline_frac']:.3f}")
         other["kda5"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        tr = measured_traffic("kda5")
+        if tr is not None:
+            other["kda5"]["traffic"] = tr["bytes_per_launch"]
     if "ssd1" in legs:
         r, _, _ = bench_ssd(W.SSD1, args.steps, args.warmup, nsets=1, chunk=64)
         other["ssd1"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
