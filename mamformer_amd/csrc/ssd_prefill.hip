@@ -490,22 +490,19 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
         fetch_own(si, sg);
       }
     }
+    auto& og = sm.st[cur ^ 1];
+    uint4 yv[TX::NBLK];
     if constexpr (NBUF == 2) {
       wait_vmem();                                         // this segment's tiles (and the last y stores)
-      auto& og = sm.st[cur ^ 1];
+      // y of the previous segment (a full one: only a chunk's last segment is partial), staged by this wave in
+      // place of its x in the other stage: read out before that stage is refilled, with no fetch in flight (an
+      // LDS read behind a pending direct-to-LDS load would wait for it).
       if (si > 0) {
-        // y of the previous segment (a full one: only a chunk's last segment is partial), staged by this
-        // wave in place of its x in the other stage: read out and stored before the stage is refilled,
-        // with no fetch in flight (an LDS read behind a pending direct-to-LDS load would wait for it).
-        uint4 yv[TX::NBLK];
         load_yhalf<T>(og.X[w], ll, yv);
         store_yhalf_full<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, yv, ll);
       }
       lds_barrier();                                       // this segment's tiles are in LDS; the other stage is free
-      if (si + 1 < nseg) {
-        fetch_shared(si + 1, og);
-        fetch_own(si + 1, og);
-      }
+      if (si + 1 < nseg) fetch_shared(si + 1, og);
     } else {
       wait_vmem();
       lds_barrier();                                       // this segment's tiles are in LDS
@@ -528,10 +525,39 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
     // ---- per wave: head j, p-tile ph.  Y^T[p][t] = sum_n H[p][n] C^T[n][t] + sum_s xa^T[p][s] M^T[s][t]
     Frag<TM> xa[4];
     xt_frags<TM, T>(xt, sm.sa[w], id, halfq, l32q, xa);
+    if constexpr (NBUF == 2) {
+      if (si + 1 < nseg) fetch_own(si + 1, og);          // the next segment's own tiles, issued apart from the rest
+    }
     const float cs0 = sm.cs[w][l32q], cs1 = sm.cs[w][32 + l32q];
     f32x16 Y0 = zero16(), Y1 = zero16();
+    // y[t][p] = rs_t Y + D x, staged in place of x
+    auto epilogue = [&](float rs0, float rs1) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int tl = 32 * tt + l32q;
+        const float rsc = tt ? rs1 : rs0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int p0 = 8 * q + 4 * halfq;                // 4 consecutive columns of the half, inside one chunk
+          T* xp = xt + TX::chunk(tl, (unsigned)p0 / TX::EPC) + ((unsigned)p0 % TX::EPC);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sm.dcol[j][32 * ph + p0]);
+          if constexpr (sizeof(T) == 2) {
+            const bf16x4 xv = *reinterpret_cast<const bf16x4*>(xp);
+            bf16x4 yo;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) yo[i] = (bf16)(rsc * (tt ? Y1[4 * q + i] : Y0[4 * q + i]) + d4[i] * (float)xv[i]);
+            *reinterpret_cast<bf16x4*>(xp) = yo;
+          } else {
+            const f32x4 xv = *reinterpret_cast<const f32x4*>(xp);
+            f32x4 yo;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) yo[i] = rsc * (tt ? Y1[4 * q + i] : Y0[4 * q + i]) + d4[i] * xv[i];
+            *reinterpret_cast<f32x4*>(xp) = yo;
+          }
+        }
+      }
+    };
     readout<TM, N>(H, sg.fr.ct, ll, Y0, Y1);
-    float rs0, rs1;
     if (fact) {
       Y0 = mma(xa[0], sg.fr.cb[0][0][ll], Y0);
       Y0 = mma(xa[1], sg.fr.cb[0][1][ll], Y0);
@@ -540,8 +566,7 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
       Y1 = mma(xa[2], sg.fr.cb[2][0][ll], Y1);
       Y1 = mma(xa[3], sg.fr.cb[2][1][ll], Y1);
       state_update<TM, N>(H, sg.fr.bt, xa, ll);
-      rs0 = __expf(kappa + cs0);
-      rs1 = __expf(kappa + cs1);
+      epilogue(__expf(kappa + cs0), __expf(kappa + cs1));
       kappa += cse;
     } else {
       // exact path (kappa = 0 here): xa_s = dt_s x_s, each masked C B^T entry decayed by e^{cs_t - cs_s}
@@ -575,32 +600,7 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) H[nt] *= e;
       state_update<TM, N>(H, sg.fr.bt, xa, ll);
-      rs0 = rs1 = 1.f;
-    }
-    // y[t][p] = rs_t Y + D x, staged in place of x
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int tl = 32 * tt + l32q;
-      const float rsc = tt ? rs1 : rs0;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int p0 = 8 * q + 4 * halfq;                // 4 consecutive columns of the half, inside one chunk
-        T* xp = xt + TX::chunk(tl, (unsigned)p0 / TX::EPC) + ((unsigned)p0 % TX::EPC);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sm.dcol[j][32 * ph + p0]);
-        if constexpr (sizeof(T) == 2) {
-          const bf16x4 xv = *reinterpret_cast<const bf16x4*>(xp);
-          bf16x4 yv;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) yv[i] = (bf16)(rsc * (tt ? Y1[4 * q + i] : Y0[4 * q + i]) + d4[i] * (float)xv[i]);
-          *reinterpret_cast<bf16x4*>(xp) = yv;
-        } else {
-          const f32x4 xv = *reinterpret_cast<const f32x4*>(xp);
-          f32x4 yv;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) yv[i] = rsc * (tt ? Y1[4 * q + i] : Y0[4 * q + i]) + d4[i] * xv[i];
-          *reinterpret_cast<f32x4*>(xp) = yv;
-        }
-      }
+      epilogue(1.f, 1.f);
     }
   }
   // y of the last segment
