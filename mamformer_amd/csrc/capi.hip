@@ -251,16 +251,7 @@ int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream) {
   p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l; p.y_sh = a->y_stride_h;
   p.final_state = a->final_state;
   p.nseg = (int)((a->seqlen + 63) / 64);
-  if (nchunks > 0) {
-    const size_t states = (size_t)a->batch * nchunks * a->nheads * a->headdim * a->dstate * sizeof(float);
-    const size_t decay = (size_t)a->batch * a->nheads * nchunks * sizeof(float);
-    char* ws = reinterpret_cast<char*>(a->workspace);
-    p.chunk_states = reinterpret_cast<float*>(ws);
-    p.chunk_decay = reinterpret_cast<float*>(ws + ((states + 255) / 256) * 256);
-    p.seg_frags = ws + ((states + 255) / 256) * 256 + ((decay + 255) / 256) * 256;
-    const size_t frags = (size_t)a->batch * a->ngroups * p.nseg * mh::ssd_frag_bytes(a->dtype, (int)a->dstate);
-    p.entering = reinterpret_cast<char*>(p.seg_frags) + ((frags + 255) / 256) * 256;
-  }
+  if (nchunks > 0) mh::ssd_workspace_layout(p, a->workspace);
   return hip_status(mh::launch_ssd(p, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_fwd");
 }
 

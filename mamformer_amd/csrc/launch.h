@@ -45,7 +45,7 @@ struct SsdParams {
   const float* init_state;
   void* y; int64_t y_sb, y_sl, y_sh;
   float* final_state;
-  float* chunk_states;   // workspace: [batch][nchunks][nheads][headdim][dstate]
+  float* chunk_states;   // workspace: [batch][nchunks][nheads][headdim][dstate] (bf16 elements for bf16 I/O)
   float* chunk_decay;    // workspace: [batch][nheads][nchunks]  (sum of A*dt over the chunk)
   void* seg_frags;       // workspace: [batch][ngroups][nseg] shared MFMA fragments of each 64-token segment
   void* entering;        // workspace (bf16 I/O): bf16 entering states, chunk_states order
@@ -55,6 +55,8 @@ hipError_t launch_ssd(const SsdParams& p, hipStream_t st);
 size_t ssd_frag_bytes(int dtype, int dstate);
 size_t ssd_workspace_bytes(int batch, int seqlen, int nchunks, int nheads, int headdim, int dstate, int ngroups,
                            int dtype);
+// Point p's workspace parts into `workspace` (ssd_workspace_bytes of p's sizes).
+void ssd_workspace_layout(SsdParams& p, void* workspace);
 
 // ------------------------------------------------------------- KDA
 struct KdaParams {

@@ -345,15 +345,28 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_state_kernel(SsdParams p) 
     for (int nt = 0; nt < NT; ++nt) S[nt] *= e;
   }
 
-  float* out = p.chunk_states + (((int64_t)b * p.nchunks + k) * p.nheads + h) * (HD * N);
+  // chunk-local state in fragment order: bf16 for bf16 I/O (the scan consumes the entering state as bf16
+  // MFMA operands anyway), fp32 otherwise
+  const int64_t obase = (((int64_t)b * p.nchunks + k) * p.nheads + h) * (HD * N);
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    f32x4* o4 = reinterpret_cast<f32x4*>(out + frag_off(nt, ph, l));
+    if constexpr (sizeof(T) == 2) {
+      bf16x8* o8 = reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(p.chunk_states) + obase + frag_off(nt, ph, l));
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      f32x4 v;
-      v[0] = S[nt][4 * q]; v[1] = S[nt][4 * q + 1]; v[2] = S[nt][4 * q + 2]; v[3] = S[nt][4 * q + 3];
-      o4[q] = v;
+      for (int q = 0; q < 2; ++q) {
+        bf16x8 v;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (bf16)S[nt][8 * q + i];
+        o8[q] = v;
+      }
+    } else {
+      f32x4* o4 = reinterpret_cast<f32x4*>(p.chunk_states + obase + frag_off(nt, ph, l));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4 v;
+        v[0] = S[nt][4 * q]; v[1] = S[nt][4 * q + 1]; v[2] = S[nt][4 * q + 2]; v[3] = S[nt][4 * q + 3];
+        o4[q] = v;
+      }
     }
   }
   if (l == 0 && ph == 0) p.chunk_decay[((int64_t)b * p.nheads + h) * p.nchunks + k] = total;
@@ -368,8 +381,9 @@ __device__ __forceinline__ int canon_index(int e, int N) {
   return (32 * pt + (lane & 31)) * N + 32 * nt + acc_row(lane >> 5, r);
 }
 
-// Entering states for the scan kernel: fp32 in place of S_k, or (bf16 I/O, where the scan consumes
-// the state as bf16 MFMA operands) bf16 in a separate array of the same fragment order.
+// Entering states for the scan kernel: fp32 in place of fp32 S_k, or (bf16 I/O, where the chunk states
+// are bf16 and the scan consumes the state as bf16 MFMA operands) bf16 in a separate array of the same
+// fragment order.  The running sum and the final state are fp32.
 template <typename TE>
 __global__ __launch_bounds__(256) void ssd_state_pass_kernel(SsdParams p) {
   const int bh = blockIdx.y;
@@ -384,11 +398,15 @@ __global__ __launch_bounds__(256) void ssd_state_pass_kernel(SsdParams p) {
   const float* dec = p.chunk_decay + (int64_t)bh * p.nchunks;
   for (int k = 0; k < p.nchunks; ++k) {
     const int64_t idx = (((int64_t)b * p.nchunks + k) * p.nheads + h) * per + e4;
-    float* sp = p.chunk_states + idx;
-    const f32x4 S = *reinterpret_cast<const f32x4*>(sp);
+    f32x4 S;
     if constexpr (sizeof(TE) == 4) {
+      float* sp = p.chunk_states + idx;
+      S = *reinterpret_cast<const f32x4*>(sp);
       *reinterpret_cast<f32x4*>(sp) = H;
     } else {
+      const bf16x4 sb = *reinterpret_cast<const bf16x4*>(reinterpret_cast<const bf16*>(p.chunk_states) + idx);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S[i] = (float)sb[i];
       bf16x4 hb;
 #pragma unroll
       for (int i = 0; i < 4; ++i) hb[i] = (bf16)H[i];
@@ -622,14 +640,40 @@ size_t ssd_frag_bytes(int dtype, int dstate) {
                           : (dstate == 128 ? sizeof(SegFrags<float, 128>) : sizeof(SegFrags<float, 64>));
 }
 
+// Workspace parts, each 256-byte aligned: chunk-local states (bf16 for bf16 I/O, fp32 otherwise), chunk
+// log-decays, per-segment shared fragments, bf16 entering states (bf16 I/O only).
+struct SsdWorkspace {
+  size_t states, decay, frags, entering;
+  size_t total() const { return align256(states) + align256(decay) + align256(frags) + align256(entering); }
+};
+static SsdWorkspace ssd_workspace(int batch, int seqlen, int nchunks, int nheads, int headdim, int dstate,
+                                  int ngroups, int dtype) {
+  const size_t nstate = (size_t)batch * nchunks * nheads * headdim * dstate;
+  const size_t nseg = (size_t)(seqlen + SEG - 1) / SEG;
+  SsdWorkspace w;
+  w.states = nstate * (dtype == DT_BF16 ? sizeof(bf16) : sizeof(float));
+  w.decay = (size_t)batch * nheads * nchunks * sizeof(float);
+  w.frags = (size_t)batch * ngroups * nseg * ssd_frag_bytes(dtype, dstate);
+  w.entering = dtype == DT_BF16 ? nstate * sizeof(bf16) : 0;
+  return w;
+}
+
 size_t ssd_workspace_bytes(int batch, int seqlen, int nchunks, int nheads, int headdim, int dstate, int ngroups,
                            int dtype) {
-  const size_t states = (size_t)batch * nchunks * nheads * headdim * dstate * sizeof(float);
-  const size_t decay = (size_t)batch * nheads * nchunks * sizeof(float);
-  const size_t nseg = (size_t)(seqlen + SEG - 1) / SEG;
-  const size_t entering = dtype == DT_BF16 ? states / 2 : 0;      // bf16 copy of the entering states
-  return align256(states) + align256(decay) + align256((size_t)batch * ngroups * nseg * ssd_frag_bytes(dtype, dstate)) +
-         align256(entering);
+  return ssd_workspace(batch, seqlen, nchunks, nheads, headdim, dstate, ngroups, dtype).total();
+}
+
+void ssd_workspace_layout(SsdParams& p, void* workspace) {
+  const SsdWorkspace w = ssd_workspace(p.batch, p.seqlen, p.nchunks, p.nheads, p.headdim, p.dstate, p.ngroups,
+                                       p.dtype);
+  char* c = reinterpret_cast<char*>(workspace);
+  p.chunk_states = reinterpret_cast<float*>(c);
+  c += align256(w.states);
+  p.chunk_decay = reinterpret_cast<float*>(c);
+  c += align256(w.decay);
+  p.seg_frags = c;
+  c += align256(w.frags);
+  p.entering = c;
 }
 
 template <typename T, typename TM, int N, int HG>
