@@ -153,27 +153,57 @@ __device__ __forceinline__ float seg_decay(const SsdParams& p, float dtraw, floa
 template <typename TM, int N>
 __device__ __forceinline__ void readout(const f32x16 (&H)[N / 32], const Frag<TM> (&ct)[N / 32][2][2][64], int l,
                                         f32x16& Y0, f32x16& Y1) {
+  // C^T fragments of state tile nt + 1 are read from LDS while the MFMAs of tile nt run
+  Frag<TM> cur[2][2], nxt[2][2];
 #pragma unroll
-  for (int nt = 0; nt < N / 32; ++nt)
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) cur[c][tt] = ct[0][c][tt][l];
+#pragma unroll
+  for (int nt = 0; nt < N / 32; ++nt) {
+    if (nt + 1 < N / 32) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) nxt[c][tt] = ct[nt + 1][c][tt][l];
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const Frag<TM> hf = acc_to_frag<TM>(H[nt], c);
-      Y0 = mma(hf, ct[nt][c][0][l], Y0);
-      Y1 = mma(hf, ct[nt][c][1][l], Y1);
+      Y0 = mma(hf, cur[c][0], Y0);
+      Y1 = mma(hf, cur[c][1], Y1);
     }
+    if (nt + 1 < N / 32) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) cur[c][tt] = nxt[c][tt];
+    }
+  }
 }
 
 // H[n][p] += sum_s B^T[n][s] xf[s][p] over the segment's 64 tokens.
 template <typename TM, int N>
 __device__ __forceinline__ void state_update(f32x16 (&H)[N / 32], const Frag<TM> (&bt)[N / 32][4][64],
                                              const Frag<TM> (&xf)[4], int l) {
+  // B^T fragments of state tile nt + 1 are read from LDS while the MFMAs of tile nt run
+  Frag<TM> cur[4], nxt[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) cur[c] = bt[0][c][l];
 #pragma unroll
   for (int nt = 0; nt < N / 32; ++nt) {
-    Frag<TM> btf[4];
+    if (nt + 1 < N / 32) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) btf[c] = bt[nt][c][l];
+      for (int c = 0; c < 4; ++c) nxt[c] = bt[nt + 1][c][l];
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) H[nt] = mma(btf[c], xf[c], H[nt]);
+    for (int c = 0; c < 4; ++c) H[nt] = mma(cur[c], xf[c], H[nt]);
+    if (nt + 1 < N / 32) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) cur[c] = nxt[c];
+    }
   }
 }
 
