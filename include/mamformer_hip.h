@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MH_ABI_VERSION 1
+#define MH_ABI_VERSION 2
 
 /* element types of x / B / C / y / q / k / v / o */
 enum { MH_F32 = 0, MH_BF16 = 1 };
@@ -81,6 +81,9 @@ typedef struct {
   void* y;         int64_t y_stride_b, y_stride_l, y_stride_h;
   float* final_state;
   void* workspace; size_t workspace_bytes;
+  /* optional output gate (NULL: none): y <- y * silu(z), z laid out like y in the dtype of x -- the
+     z-gate that Mamba2Block.forward applies right after the scan (mamformer/layers/mamba2.py:337-338) */
+  const void* z;   int64_t z_stride_b, z_stride_l, z_stride_h;
 } mh_ssd_args;
 
 /* Bytes of workspace mh_ssd_chunk_scan_fwd needs for these sizes. */
@@ -112,6 +115,9 @@ typedef struct {
   const float* D;
   const float* dt_bias;
   void* y;         int64_t y_stride_b;
+  /* optional output gate (NULL: none): y <- y * silu(z), z (b, H, P) in the dtype of x
+     (mamformer/layers/mamba2.py:337-338 on the one-token path) */
+  const void* z;   int64_t z_stride_b;
 } mh_ssu_args;
 
 int mh_ssd_state_update(const mh_ssu_args* a, void* stream);

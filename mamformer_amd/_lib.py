@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MH_F32, MH_BF16 = 0, 1
 MH_DT_SOFTPLUS, MH_DT_LIMIT, MH_D_PER_CHANNEL = 1, 2, 4
@@ -41,6 +41,7 @@ class SsdArgs(ct.Structure):
         ("y", _vp), ("y_stride_b", _i64), ("y_stride_l", _i64), ("y_stride_h", _i64),
         ("final_state", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
+        ("z", _vp), ("z_stride_b", _i64), ("z_stride_l", _i64), ("z_stride_h", _i64),
     ]
 
 
@@ -56,6 +57,7 @@ class SsuArgs(ct.Structure):
         ("C", _vp), ("C_stride_b", _i64),
         ("D", _vp), ("dt_bias", _vp),
         ("y", _vp), ("y_stride_b", _i64),
+        ("z", _vp), ("z_stride_b", _i64),
     ]
 
 

@@ -94,6 +94,15 @@ int ssd_validate(const mh_ssd_args* a, int64_t* chunk_len_out) {
     return fail(MH_ERR_STRIDE, "ssd: token stride too large (64 tokens must span less than 2 GiB)");
   if (a->x_stride_h < a->headdim || a->y_stride_h < a->headdim)
     return fail(MH_ERR_STRIDE, "ssd: x/y head stride smaller than headdim (headdim must be contiguous)");
+  if (a->z) {
+    if (!aligned16(a->z)) return fail(MH_ERR_ALIGN, "ssd: z must be 16-byte aligned");
+    if (!stride_ok(a->z_stride_b, es) || !stride_ok(a->z_stride_l, es) || !stride_ok(a->z_stride_h, es))
+      return fail(MH_ERR_ALIGN, "ssd: strides of z must be multiples of 16 bytes");
+    if (a->z_stride_h < a->headdim)
+      return fail(MH_ERR_STRIDE, "ssd: z head stride smaller than headdim (headdim must be contiguous)");
+    if (a->z_stride_l * es * 64 >= ((int64_t)1 << 31))
+      return fail(MH_ERR_STRIDE, "ssd: z token stride too large (64 tokens must span less than 2 GiB)");
+  }
   if ((a->B_stride_l != 0 && a->B_stride_l < a->ngroups * a->dstate) ||
       (a->C_stride_l != 0 && a->C_stride_l < a->ngroups * a->dstate))
     return fail(MH_ERR_STRIDE, "ssd: B/C token stride smaller than ngroups*dstate ((g, n) must be contiguous; 0 broadcasts)");
@@ -123,6 +132,8 @@ int ssu_validate(const mh_ssu_args* a) {
     return fail(MH_ERR_NULL, "state_update: state_in, state_out, x, dt, A, B, C, y are required");
   if (!aligned16(a->state_in) || !aligned16(a->state_out))
     return fail(MH_ERR_ALIGN, "state_update: state must be 16-byte aligned");
+  if (a->z && a->z_stride_b < a->nheads * a->headdim)
+    return fail(MH_ERR_STRIDE, "state_update: z batch stride smaller than a row ((h, p) contiguous)");
   if (a->x_stride_b < a->nheads * a->headdim || a->y_stride_b < a->nheads * a->headdim ||
       a->B_stride_b < a->ngroups * a->dstate || a->C_stride_b < a->ngroups * a->dstate || a->dt_stride_b < a->nheads)
     return fail(MH_ERR_STRIDE, "state_update: batch stride smaller than a row ((h, p) / (g, n) / h contiguous)");
@@ -250,6 +261,7 @@ int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream) {
   p.D = a->D; p.dt_bias = a->dt_bias; p.init_state = a->initial_state;
   p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l; p.y_sh = a->y_stride_h;
   p.final_state = a->final_state;
+  p.z = a->z; p.z_sb = a->z_stride_b; p.z_sl = a->z_stride_l; p.z_sh = a->z_stride_h;
   p.nseg = (int)((a->seqlen + 63) / 64);
   if (nchunks > 0) mh::ssd_workspace_layout(p, a->workspace);
   return hip_status(mh::launch_ssd(p, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_fwd");
@@ -274,6 +286,7 @@ int mh_ssd_state_update(const mh_ssu_args* a, void* stream) {
   p.C = a->C; p.C_stride_b = a->C_stride_b;
   p.D = a->D; p.dt_bias = a->dt_bias;
   p.y = a->y; p.y_stride_b = a->y_stride_b;
+  p.z = a->z; p.z_stride_b = a->z_stride_b;
   return hip_status(mh::launch_ssu(p, reinterpret_cast<hipStream_t>(stream)), "ssd_state_update");
 }
 

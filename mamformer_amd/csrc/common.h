@@ -173,4 +173,7 @@ __device__ __forceinline__ float softplus_f(float x) {
   return __logf(1.f + e);
 }
 
+// silu(x) = x / (1 + e^{-x}); e^{-x} overflowing to +inf gives -0 (the limit) for very negative x.
+__device__ __forceinline__ float silu_f(float x) { return __fdividef(x, 1.f + __expf(-x)); }
+
 }  // namespace mh

@@ -24,6 +24,7 @@ struct SsuParams {
   const float* D;
   const float* dt_bias;
   void* y; int64_t y_stride_b;
+  const void* z; int64_t z_stride_b;       // optional gate: y <- y * silu(z)
 };
 hipError_t launch_ssu(const SsuParams& p, hipStream_t st);
 
@@ -44,6 +45,7 @@ struct SsdParams {
   const float* dt_bias;
   const float* init_state;
   void* y; int64_t y_sb, y_sl, y_sh;
+  const void* z; int64_t z_sb, z_sl, z_sh; // optional gate: y <- y * silu(z)
   float* final_state;
   float* chunk_states;   // workspace: [batch][nchunks][nheads][headdim][dstate] (bf16 elements for bf16 I/O)
   float* chunk_decay;    // workspace: [batch][nheads][nchunks]  (sum of A*dt over the chunk)

@@ -2,8 +2,9 @@
 //
 // Per (b, h):  dt' = clamp(softplus(dt + dt_bias)),  a = exp(A_h dt')
 //              s[p, n] <- a * s[p, n] + dt' * x[p] * B[g, n]          (fp32, read-modify-write)
-//              y[p]     = sum_n C[g, n] * s[p, n] + D * x[p]
-// Reference semantics: Mamba2Block._recurrent_step, mamformer/layers/mamba2.py:431-458
+//              y[p]     = sum_n C[g, n] * s[p, n] + D * x[p]     (times silu(z[p]) when a gate is given)
+// Reference semantics: Mamba2Block._recurrent_step, mamformer/layers/mamba2.py:431-458, and the
+// z-gate applied after it (:337-338)
 // (with A_log, dt, D in the per-head SSD convention; see the oracle's bridge).
 //
 // Bandwidth-bound: the fp32 state is read once and written once; everything
@@ -37,11 +38,12 @@ __global__ __launch_bounds__(1024) void ssu_kernel(SsuParams p) {
   f32x4* sout = reinterpret_cast<f32x4*>(p.state_out + sbase);
   const T* xp = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_stride_b + (int64_t)h * P;
   T* yp = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_stride_b + (int64_t)h * P;
+  const T* zp = p.z ? reinterpret_cast<const T*>(p.z) + (int64_t)b * p.z_stride_b + (int64_t)h * P : nullptr;
 
   // Loads use row indices clamped into [0, P) so they are straight-line code
   // (no per-row branches, hence no early waits); only the stores are guarded.
   f32x4 s[SSU_ROWS];
-  float xv[SSU_ROWS], dv[SSU_ROWS];
+  float xv[SSU_ROWS], dv[SSU_ROWS], zv[SSU_ROWS];
   const float* Dc = (p.D && p.D_per_channel) ? p.D + (int64_t)h * P : nullptr;
   auto load = [&](int pbase) {
 #pragma unroll
@@ -51,6 +53,10 @@ __global__ __launch_bounds__(1024) void ssu_kernel(SsuParams p) {
     if (Dc) {
 #pragma unroll
       for (int i = 0; i < SSU_ROWS; ++i) dv[i] = Dc[min(pbase + i * rp, P - 1)];
+    }
+    if (zp) {
+#pragma unroll
+      for (int i = 0; i < SSU_ROWS; ++i) zv[i] = to_f32(zp[min(pbase + i * rp, P - 1)]);
     }
   };
   load(row0);
@@ -85,7 +91,11 @@ __global__ __launch_bounds__(1024) void ssu_kernel(SsuParams p) {
         float part = v[0] * Cv[0] + v[1] * Cv[1] + v[2] * Cv[2] + v[3] * Cv[3];
 #pragma unroll
         for (int off = TPR / 2; off > 0; off >>= 1) part += __shfl_xor(part, off, TPR);
-        if (ln == 0) yp[pr] = from_f32<T>(part + (Dc ? dv[i] : Dh) * xv[i]);
+        if (ln == 0) {
+          float yv = part + (Dc ? dv[i] : Dh) * xv[i];
+          if (zp) yv *= silu_f(zv[i]);                 // z-gate of mamba2.py:337-338
+          yp[pr] = from_f32<T>(yv);
+        }
       }
     }
   }

@@ -476,6 +476,12 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
   const char* fg = reinterpret_cast<const char*>(reinterpret_cast<const SegFrags<TM, N>*>(p.seg_frags) +
                                                  ((int64_t)b * p.ngroups + g) * p.nseg + c0 / SEG);
   T* yg = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_sb + (int64_t)h * p.y_sh + 32 * ph;
+  // optional output gate y <- y * silu(z): the z rows of a segment are loaded one segment before its y is
+  // stored (bf16: into registers right after the tiles barrier; fp32: at the store)
+  const T* zg = p.z ? reinterpret_cast<const T*>(p.z) + (int64_t)b * p.z_sb + (int64_t)h * p.z_sh + 32 * ph
+                    : nullptr;
+  constexpr bool ZPRE = sizeof(T) == 2;
+  uint4 zv[TX::NBLK];
   const int f0 = w * FPW, fn = max(0, min(FPW, FB - f0));
   Frag<TM> id[2];
   id[0] = ident_frag<TM>(0, half, l32);
@@ -532,7 +538,9 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
     T* xt = sg.X[w];
     if constexpr (NBUF == 1) {
       if (si > 0) {
-        store_yhalf<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, xt, SEG, ll);   // y of the previous segment
+        if (zg && !ZPRE) load_zhalf<T>(zg + (int64_t)(pos - SEG) * p.z_sl, p.z_sl, SEG - 1, ll, zv);
+        store_yhalf<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, xt, SEG, ll,   // y of the previous segment
+                       zg != nullptr, zv);
         lds_barrier();                                     // every wave is done with the previous tiles
         fetch_shared(si, sg);
         fetch_own(si, sg);
@@ -546,7 +554,9 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
       // place of its x in the other stage: read out before that stage is refilled, with no fetch in flight (an
       // LDS read behind a pending direct-to-LDS load would wait for it).
       if (si > 0) {
+        if (zg && !ZPRE) load_zhalf<T>(zg + (int64_t)(pos - SEG) * p.z_sl, p.z_sl, SEG - 1, ll, zv);
         load_yhalf<T>(og.X[w], ll, yv);
+        if (zg) gate_chunks<T>(yv, zv);
         store_yhalf_full<T>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, yv, ll);
       }
       lds_barrier();                                       // this segment's tiles are in LDS; the other stage is free
@@ -555,6 +565,7 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
       wait_vmem();
       lds_barrier();                                       // this segment's tiles are in LDS
     }
+    if (ZPRE && zg) load_zhalf<T>(zg + (int64_t)pos * p.z_sl, p.z_sl, c1 - 1 - pos, ll, zv);   // for its y store
 
     // ---- this head's in-segment decay (lane = token).  H_true = e^kappa H (kappa <= 0 carried lazily).
     float dtv;
@@ -659,7 +670,8 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
     const int si = nseg - 1;
     const int cur = (NBUF == 2) ? (si & 1) : 0;
     const int pos = c0 + si * SEG;
-    store_yhalf<T>(yg + (int64_t)pos * p.y_sl, p.y_sl, sm.st[cur].X[w], c1 - pos, l);
+    if (zg && !ZPRE) load_zhalf<T>(zg + (int64_t)pos * p.z_sl, p.z_sl, c1 - 1 - pos, l, zv);
+    store_yhalf<T>(yg + (int64_t)pos * p.y_sl, p.y_sl, sm.st[cur].X[w], c1 - pos, l, zg != nullptr, zv);
   }
 }
 
@@ -726,7 +738,8 @@ static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st) {
 }
 
 template <typename T, typename TM, int N, int HG>
-constexpr bool ssd_fits = sizeof(ScanSmem<T, TM, N, HG, 1>) <= LDS_BYTES && sizeof(StateSmem<T, TM, N, HG, 1>) <= LDS_BYTES &&
+constexpr bool ssd_fits = !(sizeof(T) == 4 && N == 128 && HG > 1) &&   // fp32 N=128 runs one head per workgroup
+                          sizeof(ScanSmem<T, TM, N, HG, 1>) <= LDS_BYTES && sizeof(StateSmem<T, TM, N, HG, 1>) <= LDS_BYTES &&
                           bt_blocks<TM, N> % (2 * HG) == 0 && Tile<T, N>::NBLK % (2 * HG) == 0;
 
 template <typename T, typename TM, int N>

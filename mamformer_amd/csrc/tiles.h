@@ -141,12 +141,48 @@ __device__ __forceinline__ void store_yhalf_full(T* dst, int64_t row_stride, con
     *reinterpret_cast<uint4*>(dst + (int64_t)(e / X::CPR) * row_stride + (e % X::CPR) * X::EPC) = v[i];
   }
 }
-// Rows [0, len) only.
+// Output gate on the staged y chunks: y <- y * silu(z), z chunks in the same lane order.
 template <typename T>
-__device__ __forceinline__ void store_yhalf(T* dst, int64_t row_stride, const T* tile, int len, int lane) {
+__device__ __forceinline__ void gate_chunks(uint4 (&v)[XHalf<T>::NBLK], const uint4 (&z)[XHalf<T>::NBLK]) {
+#pragma unroll
+  for (int i = 0; i < XHalf<T>::NBLK; ++i) {
+    if constexpr (sizeof(T) == 2) {
+      bf16x8 y = __builtin_bit_cast(bf16x8, v[i]);
+      const bf16x8 g = __builtin_bit_cast(bf16x8, z[i]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = (bf16)((float)y[j] * silu_f((float)g[j]));
+      v[i] = __builtin_bit_cast(uint4, y);
+    } else {
+      f32x4 y = __builtin_bit_cast(f32x4, v[i]);
+      const f32x4 g = __builtin_bit_cast(f32x4, z[i]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[j] *= silu_f(g[j]);
+      v[i] = __builtin_bit_cast(uint4, y);
+    }
+  }
+}
+
+// Gate chunks z of a wave's 32-column half, rows [0, SEG) of src (rows past rmax re-read row rmax), in
+// the lane order of load_yhalf.
+template <typename T>
+__device__ __forceinline__ void load_zhalf(const T* src, int64_t row_stride, int rmax, int lane,
+                                           uint4 (&v)[XHalf<T>::NBLK]) {
+  using X = XHalf<T>;
+#pragma unroll
+  for (int i = 0; i < X::NBLK; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = *reinterpret_cast<const uint4*>(src + (int64_t)min(e / X::CPR, rmax) * row_stride + (e % X::CPR) * X::EPC);
+  }
+}
+
+// Rows [0, len) only; with `gate`, y <- y * silu(z) on the z chunks loaded with load_zhalf.
+template <typename T>
+__device__ __forceinline__ void store_yhalf(T* dst, int64_t row_stride, const T* tile, int len, int lane, bool gate,
+                                            const uint4 (&zv)[XHalf<T>::NBLK]) {
   using X = XHalf<T>;
   uint4 v[X::NBLK];
   load_yhalf<T>(tile, lane, v);
+  if (gate) gate_chunks<T>(v, zv);
 #pragma unroll
   for (int i = 0; i < X::NBLK; ++i) {
     const int e = lane + 64 * i;

@@ -4,8 +4,9 @@
 SSD scan: in_proj -> causal depthwise conv1d -> SiLU -> dt/B/C projections -> scan (full
 prefill, or the one-token recurrent step when a cache holds an SSM state) -> SiLU(z) gate
 -> out_proj, with the reference's cache dict ``{"conv_state", "ssm_state"}``.  The conv,
-SiLU, scan and decode step run the HIP kernels of ``mamformer_amd.ops``; the projections
-are plain library GEMMs.
+SiLU, scan, z-gate and decode step run the HIP kernels of ``mamformer_amd.ops`` (conv and
+SiLU fused; the gate applied by the scan / step kernels as y is stored); the projections are
+plain library GEMMs.
 
 Recorded deviation (per-head SSD convention): the reference parameterises dt per channel
 (``dt_proj: d_inner -> d_inner``) and A per state (``A_log (d_state,)``), which is a
@@ -25,7 +26,6 @@ from typing import Optional
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import ops
 
@@ -95,17 +95,17 @@ class Mamba2Layer(nn.Module):
         A = -torch.exp(self.A_log.float())
         D = self.D.float()
         h_states = None
+        # the z-gate y * silu(z) (:337-338) is applied by the kernels as y is stored
         if incremental:
             y, final = ops.recurrent_step(x_act, dt, Bm, Cm, cache["ssm_state"], A, D,
-                                          dt_bias=self.dt_bias, dt_softplus=True)
+                                          dt_bias=self.dt_bias, dt_softplus=True, z=z)
         else:
             res = ops.selective_scan(x_act, dt, A, Bm, Cm, D, return_h_states=return_h_states,
-                                     return_final_state=use_cache, dt_bias=self.dt_bias, dt_softplus=True)
+                                     return_final_state=use_cache, dt_bias=self.dt_bias, dt_softplus=True, z=z)
             res = res if isinstance(res, tuple) else (res,)
             y = res[0]
             h_states = res[1] if return_h_states else None
             final = res[-1] if use_cache else None
-        y = y * F.silu(z)                                        # :337-338 (broadcasts on the one-token path)
         out = self.out_proj(y)
         new_cache = None
         if use_cache:

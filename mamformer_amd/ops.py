@@ -80,7 +80,8 @@ def _inner_contig(t: torch.Tensor, ndim_inner: int = 1) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
-def _ssd_args(x4, dt, A, B4, C4, D, dt_bias, dt_softplus, dt_limit, initial_state, y4, final_state, chunk_size):
+def _ssd_args(x4, dt, A, B4, C4, D, dt_bias, dt_softplus, dt_limit, initial_state, y4, final_state, chunk_size,
+              z4=None):
     b, L, H, P = x4.shape
     G, N = B4.shape[2], B4.shape[3]
     a = SsdArgs()
@@ -104,6 +105,8 @@ def _ssd_args(x4, dt, A, B4, C4, D, dt_bias, dt_softplus, dt_limit, initial_stat
     a.D, a.dt_bias, a.initial_state = _ptr(D), _ptr(dt_bias), _ptr(initial_state)
     a.y, a.y_stride_b, a.y_stride_l, a.y_stride_h = _ptr(y4), y4.stride(0), y4.stride(1), y4.stride(2)
     a.final_state = _ptr(final_state)
+    if z4 is not None:
+        a.z, a.z_stride_b, a.z_stride_l, a.z_stride_h = _ptr(z4), z4.stride(0), z4.stride(1), z4.stride(2)
     return a
 
 
@@ -153,7 +156,7 @@ def plan_selective_scan(*args, **kw):
 
 
 def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=False, *,
-                   chunk_size=None, initial_state=None, dt_bias=None, dt_softplus=False, dt_limit=None,
+                   chunk_size=None, initial_state=None, dt_bias=None, dt_softplus=False, dt_limit=None, z=None,
                    _plan_only=False):
     """Mamba-2 SSD chunked-scan prefill.  Drop-in for ``selective_scan`` (R/mamformer/layers/mamba2.py:31-67).
 
@@ -171,11 +174,14 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
         initial_state: (b, H*P, N) / (b, H, P, N) fp32 state before the first token (prefill of a cached
             sequence); the reference scan always starts from zero (mamba2.py:101).
         dt_bias, dt_softplus, dt_limit: dt <- clamp(softplus(dt + dt_bias), *dt_limit) inside the kernel.
+        z: optional gate shaped like x: y <- y * silu(z) applied as y is stored -- the z-gate that
+            ``Mamba2Block.forward`` applies right after the scan (mamba2.py:337-338).  h_states and the
+            final state are not gated.
     Returns y (like x), or a tuple in the reference's order (y, h_states, final_state) (mamba2.py:121-130).
     """
     if return_h_states and _plan_only:
         raise ValueError("plan_selective_scan: return_h_states is not planned (call selective_scan)")
-    _require_cuda("selective_scan", x, dt, A, B, C, D, initial_state, dt_bias)
+    _require_cuda("selective_scan", x, dt, A, B, C, D, initial_state, dt_bias, z)
     if x.dtype not in _DT:
         raise TypeError(f"selective_scan: x dtype {x.dtype} not supported (float32, bfloat16)")
     if B.dtype != x.dtype or C.dtype != x.dtype:
@@ -218,9 +224,18 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
         if initial_state.numel() != b * H * P * N:
             raise ValueError(f"selective_scan: initial_state must hold b*H*P*N = {b * H * P * N} values")
         h0 = initial_state.reshape(b, H, P, N).to(torch.float32).contiguous()
+    z4 = None
+    if z is not None:
+        if z.shape != x.shape or z.dtype != x.dtype:
+            raise ValueError(f"selective_scan: z must have the shape and dtype of x, got {tuple(z.shape)} {z.dtype}")
+        if z.dim() == 3:
+            z4 = z.view(b, L, H, P) if z.stride(-1) == 1 else z.contiguous().view(b, L, H, P)
+        else:
+            z4 = z
+        z4 = _inner_contig(z4)
     y4 = torch.empty((b, L, H, P), device=x.device, dtype=x.dtype)
     fin = torch.empty((b, H, P, N), device=x.device, dtype=torch.float32) if return_final_state else None
-    args = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, y4, fin, chunk_size)
+    args = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, y4, fin, chunk_size, z4)
     nbytes = ct.c_size_t()
     _lib.call("mh_ssd_workspace_bytes", ct.byref(args), ct.byref(nbytes))
     ws = torch.empty(max(int(nbytes.value), 16), device=x.device, dtype=torch.uint8)
@@ -231,7 +246,7 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
     else:
         fin_out = fin
     plan = Plan("mh_ssd_chunk_scan_fwd", args, x.device,
-                keep=(x4, dt32, A32, B4, C4, D32, bias32, h0, y4, fin, ws), y=y, final_state=fin_out)
+                keep=(x4, dt32, A32, B4, C4, D32, bias32, h0, y4, fin, ws, z4), y=y, final_state=fin_out)
     if _plan_only:
         return plan
     plan()
@@ -325,16 +340,17 @@ def plan_selective_state_update(*args, **kw):
 
 
 def selective_state_update(state, x, dt, A, B, C, D=None, *, dt_bias=None, dt_softplus=True, dt_limit=None,
-                           out_state=None, _plan_only=False):
+                           out_state=None, z=None, _plan_only=False):
     """One-token SSD state update on the GPU, in place by default.
 
     state (b, H, P, N) fp32 (updated in place unless ``out_state`` is given);
     x (b, H, P); dt (b, H) raw (``dt_softplus``/``dt_bias``/``dt_limit`` applied
     in the kernel, as the decode path of mamba2.py:293 does before the step);
-    A (H,); B, C (b, N) or (b, G, N); D (H,), (H, P) or None.  Returns y (b, H, P).
+    A (H,); B, C (b, N) or (b, G, N); D (H,), (H, P) or None; optional gate z (b, H, P) like x:
+    y <- y * silu(z) (mamba2.py:337-338).  Returns y (b, H, P).
     Semantics of ``Mamba2Block._recurrent_step`` (R/mamformer/layers/mamba2.py:431-458).
     """
-    _require_cuda("selective_state_update", state, x, dt, A, B, C, D, dt_bias, out_state)
+    _require_cuda("selective_state_update", state, x, dt, A, B, C, D, dt_bias, out_state, z)
     if state.dim() != 4 or state.dtype != torch.float32:
         raise ValueError("selective_state_update: state must be (b, H, P, N) float32")
     b, H, P, N = state.shape
@@ -369,6 +385,11 @@ def selective_state_update(state, x, dt, A, B, C, D=None, *, dt_bias=None, dt_so
     dst = state if out_state is None else out_state
     if dst is not state and (dst.shape != state.shape or dst.dtype != torch.float32 or not dst.is_contiguous()):
         raise ValueError("selective_state_update: out_state must match state")
+    zs = None
+    if z is not None:
+        if z.shape != (b, H, P) or z.dtype != x.dtype:
+            raise ValueError(f"selective_state_update: z must be {(b, H, P)} in the dtype of x")
+        zs = z if (z.stride(-1) == 1 and z.stride(-2) == P) else z.contiguous()
     y = torch.empty((b, H, P), device=x.device, dtype=x.dtype)
     a = SsuArgs()
     a.batch, a.nheads, a.headdim, a.dstate, a.ngroups = b, H, P, N, G
@@ -388,19 +409,22 @@ def selective_state_update(state, x, dt, A, B, C, D=None, *, dt_bias=None, dt_so
     a.C, a.C_stride_b = _ptr(Cs), Cs.stride(0)
     a.D, a.dt_bias = _ptr(D32), _ptr(bias32)
     a.y, a.y_stride_b = _ptr(y), y.stride(0)
-    plan = Plan("mh_ssd_state_update", a, x.device, keep=(state, dst, xs, dt32, A32, Bs, Cs, D32, bias32), y=y)
+    if zs is not None:
+        a.z, a.z_stride_b = _ptr(zs), zs.stride(0)
+    plan = Plan("mh_ssd_state_update", a, x.device, keep=(state, dst, xs, dt32, A32, Bs, Cs, D32, bias32, zs), y=y)
     if _plan_only:
         return plan
     plan()
     return y
 
 
-def recurrent_step(x, dt, B, C, h_prev, A, D, *, dt_bias=None, dt_softplus=False, dt_limit=None):
+def recurrent_step(x, dt, B, C, h_prev, A, D, *, dt_bias=None, dt_softplus=False, dt_limit=None, z=None):
     """``Mamba2Block._recurrent_step`` counterpart (R/mamformer/layers/mamba2.py:407-458), per-head form.
 
     x (b, seqlen, H*P) -- only the last token is used (:435-438); dt (b, seqlen, H)
     (already softplus'ed, as at mamba2.py:293, unless ``dt_softplus``); B, C (b, seqlen, N)
     or (b, seqlen, G, N); h_prev (b, H*P, N) or None (zeros, :448-449); A (H,); D (H,) or (H*P,).
+    Optional gate z (b, seqlen, H*P) (last token used): y_t <- y_t * silu(z_t) (mamba2.py:337-338).
     Returns (y_t (b, 1, H*P), h_t (b, H*P, N)) -- a new state tensor, as the reference returns.
     """
     b, _, d_inner = x.shape
@@ -414,8 +438,9 @@ def recurrent_step(x, dt, B, C, h_prev, A, D, *, dt_bias=None, dt_softplus=False
     else:
         state = h_prev.reshape(b, H, P, N).to(torch.float32)
     out = torch.empty((b, H, P, N), device=x.device, dtype=torch.float32)
+    zl = z[:, -1].reshape(b, H, P) if z is not None else None
     y = selective_state_update(state.contiguous(), x[:, -1].reshape(b, H, P), dt[:, -1], A, Bl, Cl, D,
-                               dt_bias=dt_bias, dt_softplus=dt_softplus, dt_limit=dt_limit, out_state=out)
+                               dt_bias=dt_bias, dt_softplus=dt_softplus, dt_limit=dt_limit, out_state=out, z=zl)
     return y.reshape(b, 1, d_inner), out.view(b, d_inner, N)
 
 

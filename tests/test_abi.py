@@ -88,6 +88,24 @@ def test_ssd_rejects_null_and_misaligned_pointers_and_small_workspace():
     assert _rc("mh_ssd_chunk_scan_fwd", None, None) == -1
 
 
+def test_ssd_and_state_update_validate_the_output_gate():
+    a = _good_ssd()
+    a.z, a.z_stride_b, a.z_stride_l, a.z_stride_h = ct.c_void_p(4096), a.y_stride_b, a.y_stride_l, a.y_stride_h
+    n = ct.c_size_t()
+    assert _rc("mh_ssd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+    a.z = ct.c_void_p(4096 + 8)
+    assert _rc("mh_ssd_workspace_bytes", ct.byref(a), ct.byref(n)) == -5
+    a.z = ct.c_void_p(4096)
+    a.z_stride_h = 32
+    assert _rc("mh_ssd_workspace_bytes", ct.byref(a), ct.byref(n)) == -4
+    a.z_stride_h, a.z_stride_l = 64, 8 * 64 + 4
+    assert _rc("mh_ssd_workspace_bytes", ct.byref(a), ct.byref(n)) == -5
+    u = _good_ssu()
+    u.z, u.z_stride_b = ct.c_void_p(4096), 8 * 64 - 1
+    assert _rc("mh_ssd_state_update", ct.byref(u), None) == -4
+    assert b"z" in _lib.lib().mh_last_error()
+
+
 def _good_ssu():
     a = SsuArgs()
     a.batch, a.nheads, a.headdim, a.dstate, a.ngroups = 4, 8, 64, 128, 1

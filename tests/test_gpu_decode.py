@@ -50,6 +50,30 @@ def test_decode_all_dstates(N, dtype):
     check("state", out, s_ref, 1e-4)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_output_gate(dtype):
+    """Fused z-gate on the one-token path: y * silu(z) (mamba2.py:337-338); the state is not gated."""
+    g = torch.Generator().manual_seed(5)
+    b, H, P, N = 3, 8, 64, 128
+    s0 = torch.randn(b, H, P, N, generator=g) * 0.1
+    x = torch.randn(b, H, P, generator=g).to(dtype)
+    z = (torch.randn(b, H, P, generator=g) * 3).to(dtype)
+    B = torch.randn(b, 1, N, generator=g).to(dtype)
+    C = torch.randn(b, 1, N, generator=g).to(dtype)
+    dt = torch.randn(b, H, generator=g)
+    A = -torch.exp(torch.rand(H, generator=g) * 2.7)
+    D = torch.randn(H, generator=g)
+    say(f"decode gate {dtype}")
+    out = torch.empty(b, H, P, N, device="cuda")
+    y = mh.selective_state_update(dev(s0), dev(x, dtype), dev(dt), dev(A), dev(B, dtype), dev(C, dtype), dev(D),
+                                  dt_softplus=True, out_state=out, z=dev(z, dtype))
+    y_ref, s_ref = ref.state_update_direct(s0.double().numpy(), x.double().numpy(), dt.numpy(), A.numpy(),
+                                           B.double().numpy(), C.double().numpy(), D.numpy(), dt_softplus=True)
+    zr = z.double().numpy()
+    check("gated y", y, y_ref * (zr / (1.0 + np.exp(-zr))), 1e-2 if dtype == torch.bfloat16 else 1e-4)
+    check("state", out, s_ref, 1e-4)
+
+
 @pytest.mark.parametrize("batch", [64, 256])
 def test_decode_benchmark_shape(batch):
     inp = W.decode_inputs(W.DEC3.scaled(batch=batch))

@@ -126,6 +126,36 @@ def test_ssd_extreme_decay_cuts_segments():
     check("final", fin, f_ref, 1e-4)
 
 
+@pytest.mark.parametrize("dtype,L,H,N,chunk", [(torch.bfloat16, 1000, 8, 128, 256), (torch.float32, 333, 4, 64, None),
+                                               (torch.float32, 200, 2, 128, 64)])
+def test_ssd_output_gate_vs_oracle(dtype, L, H, N, chunk):
+    """Fused z-gate y * silu(z) (mamba2.py:337-338), z a strided slice of a wider buffer as in_proj gives it;
+    partial last segments, several chunks, both the prefetched (bf16) and the at-store (fp32) gate loads."""
+    g = torch.Generator().manual_seed(L + H)
+    b, P = 2, 64
+    d_inner = H * P
+    x = torch.randn(b, L, H, P, generator=g).to(dtype)
+    xz = torch.randn(b, L, 2 * d_inner, generator=g).to(dtype)      # [x' | z]: z is the second half
+    B = torch.randn(b, L, 1, N, generator=g).to(dtype)
+    C = torch.randn(b, L, 1, N, generator=g).to(dtype)
+    dt = torch.rand(b, L, H, generator=g) * 0.2 + 0.01
+    A = -torch.exp(torch.rand(H, generator=g) * 2.0)
+    D = torch.randn(H, generator=g)
+    zd = dev(xz, dtype)[..., d_inner:]
+    say(f"output gate {dtype} L={L} H={H} N={N} chunk={chunk}")
+    y, fin = mh.selective_scan(dev(x, dtype), dev(dt), dev(A), dev(B, dtype), dev(C, dtype), dev(D),
+                               return_final_state=True, chunk_size=chunk, z=zd.reshape(b, L, H, P))
+    y3 = mh.selective_scan(dev(x, dtype).reshape(b, L, d_inner), dev(dt), dev(A), dev(B, dtype), dev(C, dtype),
+                           dev(D), chunk_size=chunk, z=zd)
+    torch.cuda.synchronize()
+    y_ref, f_ref = ref.ssd_direct(x.double().numpy(), dt.double().numpy(), A.double().numpy(), B.double().numpy(),
+                                  C.double().numpy(), D.double().numpy())
+    zr = xz[..., d_inner:].double().numpy().reshape(b, L, H, P)
+    check("gated y", y, y_ref * (zr / (1.0 + np.exp(-zr))), TOL[dtype])
+    check("final (not gated)", fin, f_ref, TOL[dtype])
+    assert torch.equal(y3.view(b, L, H, P), y)
+
+
 def test_ssd_empty_sequence():
     h0 = torch.randn(1, 4, 64, 64, device="cuda")
     x = torch.zeros(1, 0, 4, 64, device="cuda")
