@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MH_ABI_VERSION 2
+#define MH_ABI_VERSION 3
 
 /* element types of x / B / C / y / q / k / v / o */
 enum { MH_F32 = 0, MH_BF16 = 1 };
@@ -91,6 +91,38 @@ int mh_ssd_workspace_bytes(const mh_ssd_args* a, size_t* bytes);
 /* Resolved chunk_len (auto choice when a->chunk_len == 0). */
 int mh_ssd_chunk_len(const mh_ssd_args* a, int64_t* chunk_len);
 int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * SSD chunked-scan prefill backward.
+ * Replaces the autograd backward of selective_scan / _selective_scan_impl
+ *   (mamformer/layers/mamba2.py:70-130; trained through in tests/test_mamba2.py:56-71):
+ *   gradients of <dy, y> + <d_final_state, final_state> for the forward call described by `fwd`
+ *   (its x, dt, A, B, C, D, dt_bias, initial_state, flags, strides; fwd.y, fwd.final_state,
+ *   fwd.workspace and fwd.chunk_len are ignored, fwd.z must be NULL and B/C may not broadcast).
+ *   dy, dx (b, L, H, P) in the dtype of x; d_final_state, d_initial_state (b, H, P, N) fp32
+ *   (NULL: zero / not wanted); ddt (b, L, H) fp32, the gradient w.r.t. the raw dt (through
+ *   dt_bias, softplus and the clamp per fwd.flags); dA (H,) fp32; dB, dC (b, L, G, N) in the dtype
+ *   of x; dD like D (NULL when D is NULL); d_dt_bias (H,) fp32 or NULL.  Every output is
+ *   overwritten.  Same supported sizes as the forward.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  mh_ssd_args fwd;
+  const void* dy;  int64_t dy_stride_b, dy_stride_l, dy_stride_h;
+  const float* d_final_state;
+  void* dx;        int64_t dx_stride_b, dx_stride_l, dx_stride_h;
+  float* ddt;      int64_t ddt_stride_b, ddt_stride_l;
+  float* dA;
+  void* dB;        int64_t dB_stride_b, dB_stride_l;
+  void* dC;        int64_t dC_stride_b, dC_stride_l;
+  float* dD;
+  float* d_dt_bias;
+  float* d_initial_state;
+  void* workspace; size_t workspace_bytes;
+} mh_ssd_bwd_args;
+
+/* Bytes of workspace mh_ssd_chunk_scan_bwd needs for these sizes. */
+int mh_ssd_bwd_workspace_bytes(const mh_ssd_bwd_args* a, size_t* bytes);
+int mh_ssd_chunk_scan_bwd(const mh_ssd_bwd_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
  * Single-token selective state update (decode step).

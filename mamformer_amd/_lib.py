@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MH_F32, MH_BF16 = 0, 1
 MH_DT_SOFTPLUS, MH_DT_LIMIT, MH_D_PER_CHANNEL = 1, 2, 4
@@ -42,6 +42,21 @@ class SsdArgs(ct.Structure):
         ("final_state", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
         ("z", _vp), ("z_stride_b", _i64), ("z_stride_l", _i64), ("z_stride_h", _i64),
+    ]
+
+
+class SsdBwdArgs(ct.Structure):
+    _fields_ = [
+        ("fwd", SsdArgs),
+        ("dy", _vp), ("dy_stride_b", _i64), ("dy_stride_l", _i64), ("dy_stride_h", _i64),
+        ("d_final_state", _vp),
+        ("dx", _vp), ("dx_stride_b", _i64), ("dx_stride_l", _i64), ("dx_stride_h", _i64),
+        ("ddt", _vp), ("ddt_stride_b", _i64), ("ddt_stride_l", _i64),
+        ("dA", _vp),
+        ("dB", _vp), ("dB_stride_b", _i64), ("dB_stride_l", _i64),
+        ("dC", _vp), ("dC_stride_b", _i64), ("dC_stride_l", _i64),
+        ("dD", _vp), ("d_dt_bias", _vp), ("d_initial_state", _vp),
+        ("workspace", _vp), ("workspace_bytes", _sz),
     ]
 
 
@@ -101,6 +116,7 @@ MH_CONV_SILU = 1
 EXPORTS = (
     "mh_abi_version", "mh_last_error",
     "mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
+    "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",
     "mh_ssd_state_update",
     "mh_kda_chunk_scan_fwd",
     "mh_kda_recurrent_step",
@@ -136,6 +152,8 @@ def lib():
             h.mh_ssd_workspace_bytes.argtypes = [ct.POINTER(SsdArgs), ct.POINTER(_sz)]
             h.mh_ssd_chunk_len.argtypes = [ct.POINTER(SsdArgs), ct.POINTER(_i64)]
             h.mh_ssd_chunk_scan_fwd.argtypes = [ct.POINTER(SsdArgs), _vp]
+            h.mh_ssd_bwd_workspace_bytes.argtypes = [ct.POINTER(SsdBwdArgs), ct.POINTER(_sz)]
+            h.mh_ssd_chunk_scan_bwd.argtypes = [ct.POINTER(SsdBwdArgs), _vp]
             h.mh_ssd_state_update.argtypes = [ct.POINTER(SsuArgs), _vp]
             h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
             h.mh_kda_recurrent_step.argtypes = [ct.POINTER(KdaStepArgs), _vp]

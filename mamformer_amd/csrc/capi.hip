@@ -212,6 +212,72 @@ int conv_validate(const mh_conv1d_args* a) {
   return MH_OK;
 }
 
+// Forward parameter block from a validated argument struct (workspace not laid out).
+void ssd_fill(const mh_ssd_args* a, int64_t cl, int64_t nchunks, mh::SsdParams& p) {
+  memset(&p, 0, sizeof(p));
+  p.batch = (int)a->batch; p.seqlen = (int)a->seqlen; p.nheads = (int)a->nheads; p.headdim = (int)a->headdim;
+  p.dstate = (int)a->dstate; p.ngroups = (int)a->ngroups; p.dtype = a->dtype;
+  p.chunk_len = (int)cl; p.nchunks = (int)nchunks; p.heads_per_wg = ssd_heads_per_wg(a);
+  p.dt_softplus = (a->flags & MH_DT_SOFTPLUS) != 0;
+  p.has_dt_limit = (a->flags & MH_DT_LIMIT) != 0;
+  p.D_per_channel = (a->flags & MH_D_PER_CHANNEL) != 0;
+  p.dt_min = a->dt_min; p.dt_max = a->dt_max;
+  p.x = a->x; p.x_sb = a->x_stride_b; p.x_sl = a->x_stride_l; p.x_sh = a->x_stride_h;
+  p.dt = a->dt; p.dt_sb = a->dt_stride_b; p.dt_sl = a->dt_stride_l;
+  p.A = a->A;
+  p.B = a->B; p.B_sb = a->B_stride_b; p.B_sl = a->B_stride_l;
+  p.C = a->C; p.C_sb = a->C_stride_b; p.C_sl = a->C_stride_l;
+  p.D = a->D; p.dt_bias = a->dt_bias; p.init_state = a->initial_state;
+  p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l; p.y_sh = a->y_stride_h;
+  p.final_state = a->final_state;
+  p.z = a->z; p.z_sb = a->z_stride_b; p.z_sl = a->z_stride_l; p.z_sh = a->z_stride_h;
+  p.nseg = (int)((a->seqlen + 63) / 64);
+}
+
+int ssd_bwd_validate(const mh_ssd_bwd_args* a) {
+  if (!a) return fail(MH_ERR_NULL, "ssd_bwd: args is NULL");
+  const mh_ssd_args* f = &a->fwd;
+  if (f->z) return fail(MH_ERR_UNSUPPORTED, "ssd_bwd: the output gate is not differentiated here (fwd.z must be NULL)");
+  // the forward's checks, with the outputs the backward does not touch taken from x and 64-token chunks
+  mh_ssd_args g = *f;
+  g.y = const_cast<void*>(g.x); g.y_stride_b = g.x_stride_b; g.y_stride_l = g.x_stride_l; g.y_stride_h = g.x_stride_h;
+  g.chunk_len = 64;
+  int rc = ssd_validate(&g, nullptr);
+  if (rc) return rc;
+  const int es = elem_size(f->dtype);
+  if (f->seqlen > 0 && (f->B_stride_l == 0 || f->C_stride_l == 0))
+    return fail(MH_ERR_UNSUPPORTED, "ssd_bwd: broadcast B/C (token stride 0) not supported");
+  if (f->seqlen > 0 && (!a->dy || !a->dx || !a->ddt || !a->dB || !a->dC))
+    return fail(MH_ERR_NULL, "ssd_bwd: dy, dx, ddt, dB, dC are required");
+  if (!a->dA) return fail(MH_ERR_NULL, "ssd_bwd: dA is required");
+  if (f->D && !a->dD) return fail(MH_ERR_NULL, "ssd_bwd: dD is required when D is given");
+  if (!aligned16(a->dy) || !aligned16(a->dx) || !aligned16(a->dB) || !aligned16(a->dC) ||
+      !aligned16(a->d_final_state) || !aligned16(a->d_initial_state))
+    return fail(MH_ERR_ALIGN, "ssd_bwd: dy, dx, dB, dC, d_final_state, d_initial_state must be 16-byte aligned");
+  if (!stride_ok(a->dy_stride_b, es) || !stride_ok(a->dy_stride_l, es) || !stride_ok(a->dy_stride_h, es) ||
+      !stride_ok(a->dx_stride_b, es) || !stride_ok(a->dx_stride_l, es) || !stride_ok(a->dx_stride_h, es) ||
+      !stride_ok(a->dB_stride_b, es) || !stride_ok(a->dB_stride_l, es) || !stride_ok(a->dC_stride_b, es) ||
+      !stride_ok(a->dC_stride_l, es))
+    return fail(MH_ERR_ALIGN, "ssd_bwd: strides of dy, dx, dB, dC must be multiples of 16 bytes");
+  if (a->dy_stride_h < f->headdim || a->dx_stride_h < f->headdim)
+    return fail(MH_ERR_STRIDE, "ssd_bwd: dy/dx head stride smaller than headdim (headdim must be contiguous)");
+  if (a->dB_stride_l < f->ngroups * f->dstate || a->dC_stride_l < f->ngroups * f->dstate)
+    return fail(MH_ERR_STRIDE, "ssd_bwd: dB/dC token stride smaller than ngroups*dstate");
+  if (a->ddt_stride_b < 0 || a->ddt_stride_l < 0) return fail(MH_ERR_STRIDE, "ssd_bwd: negative ddt stride");
+  constexpr int64_t kSpan = (int64_t)1 << 31;
+  if (a->dy_stride_l * es * 64 >= kSpan)
+    return fail(MH_ERR_STRIDE, "ssd_bwd: dy token stride too large (64 tokens must span less than 2 GiB)");
+  return MH_OK;
+}
+
+// Heads of one group per workgroup of the gradient kernel: the largest of 8, 4, 2, 1 dividing H / G.
+int ssd_bwd_heads_per_wg(const mh_ssd_args* f) {
+  const int64_t hpg = f->nheads / f->ngroups;
+  int hb = 8;
+  while (hb > 1 && hpg % hb) hb >>= 1;
+  return hb;
+}
+
 }  // namespace
 
 extern "C" {
@@ -245,24 +311,7 @@ int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream) {
   if (nchunks > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
     return fail(MH_ERR_WORKSPACE, "ssd: workspace of %zu bytes (16-byte aligned) required, got %zu", need, a->workspace_bytes);
   mh::SsdParams p;
-  memset(&p, 0, sizeof(p));
-  p.batch = (int)a->batch; p.seqlen = (int)a->seqlen; p.nheads = (int)a->nheads; p.headdim = (int)a->headdim;
-  p.dstate = (int)a->dstate; p.ngroups = (int)a->ngroups; p.dtype = a->dtype;
-  p.chunk_len = (int)cl; p.nchunks = (int)nchunks; p.heads_per_wg = ssd_heads_per_wg(a);
-  p.dt_softplus = (a->flags & MH_DT_SOFTPLUS) != 0;
-  p.has_dt_limit = (a->flags & MH_DT_LIMIT) != 0;
-  p.D_per_channel = (a->flags & MH_D_PER_CHANNEL) != 0;
-  p.dt_min = a->dt_min; p.dt_max = a->dt_max;
-  p.x = a->x; p.x_sb = a->x_stride_b; p.x_sl = a->x_stride_l; p.x_sh = a->x_stride_h;
-  p.dt = a->dt; p.dt_sb = a->dt_stride_b; p.dt_sl = a->dt_stride_l;
-  p.A = a->A;
-  p.B = a->B; p.B_sb = a->B_stride_b; p.B_sl = a->B_stride_l;
-  p.C = a->C; p.C_sb = a->C_stride_b; p.C_sl = a->C_stride_l;
-  p.D = a->D; p.dt_bias = a->dt_bias; p.init_state = a->initial_state;
-  p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l; p.y_sh = a->y_stride_h;
-  p.final_state = a->final_state;
-  p.z = a->z; p.z_sb = a->z_stride_b; p.z_sl = a->z_stride_l; p.z_sh = a->z_stride_h;
-  p.nseg = (int)((a->seqlen + 63) / 64);
+  ssd_fill(a, cl, nchunks, p);
   if (nchunks > 0) mh::ssd_workspace_layout(p, a->workspace);
   return hip_status(mh::launch_ssd(p, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_fwd");
 }
@@ -334,6 +383,44 @@ int mh_causal_conv1d_fwd(const mh_conv1d_args* a, void* stream) {
   p.cs_sb = a->conv_state_stride_b; p.cs_sl = a->conv_state_stride_l;
   p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l;
   return hip_status(mh::launch_conv1d(p, reinterpret_cast<hipStream_t>(stream)), "causal_conv1d_fwd");
+}
+
+int mh_ssd_bwd_workspace_bytes(const mh_ssd_bwd_args* a, size_t* bytes) {
+  if (!bytes) return fail(MH_ERR_NULL, "ssd_bwd: bytes output is NULL");
+  int rc = ssd_bwd_validate(a);
+  if (rc) return rc;
+  const mh_ssd_args* f = &a->fwd;
+  *bytes = mh::ssd_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->headdim,
+                                       (int)f->dstate, (int)f->ngroups, f->dtype);
+  return MH_OK;
+}
+
+int mh_ssd_chunk_scan_bwd(const mh_ssd_bwd_args* a, void* stream) {
+  int rc = ssd_bwd_validate(a);
+  if (rc) return rc;
+  const mh_ssd_args* f = &a->fwd;
+  const size_t need = mh::ssd_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->headdim,
+                                                  (int)f->dstate, (int)f->ngroups, f->dtype);
+  if (f->seqlen > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+    return fail(MH_ERR_WORKSPACE, "ssd_bwd: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
+                a->workspace_bytes);
+  mh::SsdBwdParams q;
+  memset(&q, 0, sizeof(q));
+  const int64_t nseg = (f->seqlen + 63) / 64;
+  ssd_fill(f, 64, nseg, q.f);          // entering states per 64-token segment
+  q.f.y = nullptr;
+  q.f.final_state = nullptr;
+  q.f.z = nullptr;
+  q.dy = a->dy; q.dy_sb = a->dy_stride_b; q.dy_sl = a->dy_stride_l; q.dy_sh = a->dy_stride_h;
+  q.d_final = a->d_final_state;
+  q.dx = a->dx; q.dx_sb = a->dx_stride_b; q.dx_sl = a->dx_stride_l; q.dx_sh = a->dx_stride_h;
+  q.ddt = a->ddt; q.ddt_sb = a->ddt_stride_b; q.ddt_sl = a->ddt_stride_l;
+  q.dA = a->dA; q.dD = f->D ? a->dD : nullptr; q.dbias = a->d_dt_bias; q.dh0 = a->d_initial_state;
+  q.dB = a->dB; q.dB_sb = a->dB_stride_b; q.dB_sl = a->dB_stride_l;
+  q.dC = a->dC; q.dC_sb = a->dC_stride_b; q.dC_sl = a->dC_stride_l;
+  q.heads_per_wg = ssd_bwd_heads_per_wg(f);
+  if (nseg > 0) mh::ssd_bwd_workspace_layout(q, a->workspace);
+  return hip_status(mh::launch_ssd_bwd(q, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_bwd");
 }
 
 }  // extern "C"

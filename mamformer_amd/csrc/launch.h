@@ -59,6 +59,31 @@ size_t ssd_workspace_bytes(int batch, int seqlen, int nchunks, int nheads, int h
                            int dtype);
 // Point p's workspace parts into `workspace` (ssd_workspace_bytes of p's sizes).
 void ssd_workspace_layout(SsdParams& p, void* workspace);
+// Kernels 0-2 of the prefill only: the entering state of every chunk, left in the workspace
+// (p.entering for bf16 I/O, p.chunk_states in place for fp32 I/O).
+hipError_t launch_ssd_states(const SsdParams& p, hipStream_t st);
+
+// ------------------------------------------------------------- SSD prefill backward
+struct SsdBwdParams {
+  SsdParams f;               // forward sizes and inputs; chunk_len = 64 (one segment per chunk), workspace laid out
+  const void* dy; int64_t dy_sb, dy_sl, dy_sh;
+  const float* d_final;      // (b, H, P, N) fp32 or null
+  void* dx; int64_t dx_sb, dx_sl, dx_sh;
+  float* ddt; int64_t ddt_sb, ddt_sl;     // gradient w.r.t. the raw dt
+  float* dA;                 // (H,)
+  float* dD;                 // (H,) or (H*P,) or null
+  float* dbias;              // (H,) or null
+  float* dh0;                // (b, H, P, N) or null
+  void* dB; int64_t dB_sb, dB_sl;
+  void* dC; int64_t dC_sb, dC_sl;
+  float* dB_acc;             // workspace: (b, L, G, N) fp32 sums over the heads of a group
+  float* dC_acc;
+  void* lam;                 // workspace: per-segment adjoint of the state leaving the segment, states' order
+  int heads_per_wg;          // heads of one group handled by a workgroup of the gradient kernel
+};
+hipError_t launch_ssd_bwd(const SsdBwdParams& p, hipStream_t st);
+size_t ssd_bwd_workspace_bytes(int batch, int seqlen, int nheads, int headdim, int dstate, int ngroups, int dtype);
+void ssd_bwd_workspace_layout(SsdBwdParams& p, void* workspace);
 
 // ------------------------------------------------------------- KDA
 struct KdaParams {

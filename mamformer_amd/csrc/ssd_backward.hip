@@ -1,0 +1,824 @@
+// Backward of the Mamba-2 SSD chunked-scan prefill for gfx950: gradients of
+//     L = <dy, y> + <d_final, h_L>,   y, h_L = scan(x, dt, A, B, C, D, h0)
+// with respect to x, the raw dt (through bias / softplus / clamp), A, B, C, D, dt_bias and h0 -- what
+// PyTorch autograd computes through the reference's selective_scan (mamformer/layers/mamba2.py:70-130,
+// trained through in tests/test_mamba2.py:56-71), in the per-head SSD parameterisation.
+//
+// Per head, with a_t = exp(A dt_t), the adjoint of the state h_t is
+//     lam_t = a_{t+1} lam_{t+1} + dy_t C_t^T,        lam_{L-1} = dy_{L-1} C_{L-1}^T + d_final
+// and, per 64-token segment with in-segment inclusive log-decay c_t (c_t <= 0, non-increasing), entering
+// state h_in and lam_out the adjoint of the state leaving the segment (the next segment's entering adjoint):
+//     dx_s  = dt_s [ sum_{t>=s} M[t][s] dy_t + e^{c_end - c_s} lam_out B_s ] + D dy_s
+//     dB_s  = sum_h dt_s [ sum_{t>=s} C_t L[t][s] XD[t][s] + e^{c_end - c_s} lam_out^T x_s ]
+//     dC_t  = sum_h [ sum_{s<=t} B_s L[t][s] XD[t][s] dt_s + e^{c_t} h_in^T dy_t ]
+// where L[t][s] = e^{c_t - c_s} (s <= t), CB[t][s] = C_t.B_s, M = L o CB, XD[t][s] = dy_t.x_s.
+// The decay gradient per token comes from per-token sums: with
+//     colG_s = sum_t (M o XD)[t][s],             bint_s = B_s . (dB_s inter part / dt_s),
+//     rowG_t = sum_s (M o XD)[t][s] dt_s,        u_t = C_t . (dC_t inter part),
+// dL/dc_t = rowG_t - dt_t colG_t + u_t inside the segment, and the state terms give
+//     da_tau = sum_{t>=tau} dL/dc_t + e^{c_end} <lam_out, h_in> + sum_{s<tau} dt_s bint_s
+//     ddt_tau = colG_tau + bint_tau + A da_tau,    dA = sum_tau dt_tau da_tau,    dD = sum dy . x.
+//
+// Launches (caller's stream):
+//   0. ssd_bwd_zero      clears the fp32 accumulators (a kernel, not a memset node).
+//   1. prefill kernels 0-2 at chunk length 64: the entering state h_in of every segment (workspace).
+//   2. ssd_bwd_lambda    grid (2, H, b): one workgroup per (b, h, 32-column half of P) walks the segments
+//      from last to first with lam in MFMA accumulators, stores lam_out of every segment (workspace, the
+//      entering states' fragment order) and finally dh0.  lam <- e^{c_end} lam + sum_t e^{c_t} C_t^T dy_t.
+//   3. ssd_bwd_grad      grid (nseg, H / HB, b): one workgroup per (segment, block of HB heads of a group),
+//      fully parallel; dx and ddt stored directly, dB / dC summed over the block's heads in registers and
+//      added to fp32 accumulators with hardware float atomics, dA / dD / dt_bias likewise.
+//   4. ssd_bwd_convert   accumulators -> dB, dC in the I/O dtype and the caller's strides.
+// Token-contracted products take their transposed operands from the MFMA unit (identity products), as in
+// the forward; all accumulation is fp32.
+#include "common.h"
+#include "launch.h"
+#include "ssd_shared.h"
+#include "tiles.h"
+
+namespace mh {
+
+// ------------------------------------------------------------------ helpers
+
+// KSET-ordered identity B operand for k-step c: element j of lane (column l32) is 1 where
+// 16 c + kset(half, j) == l32.
+template <typename TM>
+__device__ __forceinline__ Frag<TM> ident_kset(int c, int half, int l32) {
+  Frag<TM> f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f.set(j, (16 * c + kset(half, j) == l32) ? 1.f : 0.f);
+  return f;
+}
+
+// One 32x32 block of a state in fragment-native order (16 values per lane, element i = row acc_row(half, i)
+// of column l32).
+template <typename T> struct StateBlk;
+template <> struct StateBlk<bf16> {
+  bf16x8 v[2];
+  __device__ __forceinline__ float at(int i) const { return (float)v[i >> 3][i & 7]; }
+  __device__ __forceinline__ Frag<bf16> frag(int c) const { Frag<bf16> f; f.v = v[c]; return f; }
+};
+template <> struct StateBlk<float> {
+  f32x4 v[4];
+  __device__ __forceinline__ float at(int i) const { return v[i >> 2][i & 3]; }
+  __device__ __forceinline__ Frag<float> frag(int c) const {
+    Frag<float> f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.v[j] = v[2 * c + (j >> 2)][j & 3];
+    return f;
+  }
+};
+template <typename T>
+__device__ __forceinline__ StateBlk<T> load_state_blk(const T* base, int nt, int pt, int l) {
+  StateBlk<T> s;
+  const T* q = base + frag_off(nt, pt, l);
+  if constexpr (sizeof(T) == 2) {
+    s.v[0] = *reinterpret_cast<const bf16x8*>(q);
+    s.v[1] = *reinterpret_cast<const bf16x8*>(q + 8);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s.v[i] = *reinterpret_cast<const f32x4*>(q + 4 * i);
+  }
+  return s;
+}
+template <typename T>
+__device__ __forceinline__ void store_state_blk(T* base, int nt, int pt, int l, const f32x16& a) {
+  T* q = base + frag_off(nt, pt, l);
+  if constexpr (sizeof(T) == 2) {
+    bf16x8 lo, hi;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { lo[i] = (bf16)a[i]; hi[i] = (bf16)a[8 + i]; }
+    *reinterpret_cast<bf16x8*>(q) = lo;
+    *reinterpret_cast<bf16x8*>(q + 8) = hi;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 v;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = a[4 * i + k];
+      *reinterpret_cast<f32x4*>(q + 4 * i) = v;
+    }
+  }
+}
+
+// Transposed fragments of a state block X (rows n, columns p): out[c] has lane = row n, k = p = 16 c + KSET --
+// two products with the KSET identity turn the column-per-lane block into a row-per-lane accumulator.
+template <typename T>
+__device__ __forceinline__ void blk_transpose(const StateBlk<T>& s, const Frag<T> (&idk)[2], Frag<T> (&out)[2]) {
+  f32x16 e = zero16();
+  e = mma(s.frag(0), idk[0], e);
+  e = mma(s.frag(1), idk[1], e);
+  out[0] = acc_to_frag<T>(e, 0);
+  out[1] = acc_to_frag<T>(e, 1);
+}
+
+// Row `row` of a swizzled Tile<T, W> at the 16 columns col0 + acc_row(half, i) -- the values an
+// accumulator tile whose lane column is `row` holds (col0 % 32 == 0).
+template <typename T, int W>
+__device__ __forceinline__ void acc_cols(const T* tile, int row, int col0, int half, float (&v)[16]) {
+  using TL = Tile<T, W>;
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int c = col0 + 8 * jj + 4 * half;
+    if constexpr (sizeof(T) == 2) {
+      const bf16x4 q = *reinterpret_cast<const bf16x4*>(tile + TL::chunk(row, c / 8) + (c & 7));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * jj + k] = (float)q[k];
+    } else {
+      const f32x4 q = *reinterpret_cast<const f32x4*>(tile + TL::chunk(row, c / 4));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * jj + k] = q[k];
+    }
+  }
+}
+
+// 16 values of a per-token LDS array at the rows r0 + acc_row(half, i).
+__device__ __forceinline__ void acc_rows(const float* a, int r0, int half, float (&v)[16]) {
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const f32x4 q = *reinterpret_cast<const f32x4*>(a + r0 + 8 * jj + 4 * half);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[4 * jj + k] = q[k];
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ Frag<T> scaled(Frag<T> f, float s) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f.set(j, f.get(j) * s);
+  return f;
+}
+
+// x^T-style transpose of a 32-column half tile (XHalf layout): D[r][q] = tile[r0 + r][q], lane = column q.
+template <typename T>
+__device__ __forceinline__ f32x16 xhalf_transpose(const T* tile, int r0, const Frag<T> (&id)[2], int half, int l32) {
+  f32x16 acc = zero16();
+#pragma unroll
+  for (int c = 0; c < 2; ++c) acc = mma(xrow_frag<T, T>(tile, r0 + l32, 16 * c + 8 * half), id[c], acc);
+  return acc;
+}
+
+// d(processed dt) / d(raw dt): sigmoid below softplus' threshold (identity above), times the clamp's pass mask.
+__device__ __forceinline__ float dt_chain(const SsdParams& p, float raw, float bias) {
+  const float u = raw + bias;
+  float g = 1.f, v = u;
+  if (p.dt_softplus) {
+    if (u <= 20.f) g = 1.f / (1.f + __expf(-u));
+    v = softplus_f(u);
+  }
+  if (p.has_dt_limit && !(v >= p.dt_min && v <= p.dt_max)) g = 0.f;
+  return g;
+}
+
+// ------------------------------------------------------------------ kernel 0: clear accumulators
+
+struct ZeroRanges {
+  float* p[5];
+  int64_t n[5];
+};
+__global__ __launch_bounds__(256) void ssd_bwd_zero_kernel(ZeroRanges z) {
+  const int r = blockIdx.y;
+  float* p = z.p[r];
+  if (!p) return;
+  const int64_t n = z.n[r];
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0.f;
+}
+
+// dh0 of an empty sequence: d_final itself (or zero).
+__global__ __launch_bounds__(256) void ssd_bwd_copy_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                           size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = src ? src[i] : 0.f;
+}
+
+// ------------------------------------------------------------------ kernel 2: adjoint sweep
+
+template <typename T, int N>
+struct LamStage {
+  T C[SEG * N];             // Tile<T, N>
+  T DY[SEG * 32];           // XHalf<T>: the workgroup's 32 columns of dy
+  float dtraw[SEG];
+};
+template <typename T, int N>
+struct LamSmem {
+  LamStage<T, N> st[2];
+  float ec[N / 32][SEG];    // per wave: e^{c_t} (0 past the end)
+};
+
+template <typename T, int N>
+__global__ __launch_bounds__(64 * (N / 32)) void ssd_bwd_lambda_kernel(SsdBwdParams q) {
+  constexpr int NB = N / 32;
+  __shared__ LamSmem<T, N> sm;
+  const SsdParams& p = q.f;
+  const int pt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int g = h / (p.nheads / p.ngroups);
+  const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
+  const int nt = w;
+  const float Ah = p.A[h], bias = p.dt_bias ? p.dt_bias[h] : 0.f;
+  Frag<T> id[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) id[c] = ident_frag<T>(c, half, l32);
+  const int64_t per = (int64_t)HD * N;
+  // lam leaving the last segment = d_final, canonical (p, n) -> block (nt, pt)
+  f32x16 lam = zero16();
+  if (q.d_final) {
+    const float* src = q.d_final + ((int64_t)b * p.nheads + h) * per + (32 * pt + l32) * N + 32 * nt;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(src + 8 * jj + 4 * half);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lam[4 * jj + k] = v[k];
+    }
+  }
+  const T* Cb = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb + g * N;
+  const T* dyb = reinterpret_cast<const T*>(q.dy) + (int64_t)b * q.dy_sb + (int64_t)h * q.dy_sh + 32 * pt;
+  const float* dtb = p.dt + (int64_t)b * p.dt_sb + h;
+  auto issue = [&](int k, int s) {
+    const int t0 = k * SEG, lst = min(t0 + SEG, p.seqlen) - 1;
+    constexpr int nblk = Tile<T, N>::NBLK / NB;
+    fetch_tile<T, N>(sm.st[s].C, Cb, p.C_sl, t0, lst, w * nblk, nblk, l);
+    if (w == 0) {
+      fetch_xhalf<T>(sm.st[s].DY, dyb, q.dy_sl, t0, lst, l);
+      fetch_dt(sm.st[s].dtraw, dtb, p.dt_sl, t0, lst, l);
+    }
+  };
+  T* lam_ws = reinterpret_cast<T*>(q.lam);
+  const int nseg = p.nseg;
+  issue(nseg - 1, (nseg - 1) & 1);
+  for (int k = nseg - 1; k >= 0; --k) {
+    const int s = k & 1;
+    wait_vmem();
+    lds_barrier();
+    if (k > 0) issue(k - 1, s ^ 1);
+    store_state_blk<T>(lam_ws + (((int64_t)b * nseg + k) * p.nheads + h) * per, nt, pt, l, lam);
+    const int len = min(SEG, p.seqlen - k * SEG);
+    float dtv;
+    const float cs = seg_decay(p, sm.st[s].dtraw[l], bias, Ah, l, len, dtv);
+    const float cend = __shfl(cs, 63);
+    sm.ec[w][l] = (l < len) ? __expf(cs) : 0.f;
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      const f32x16 ct = mfma_transpose<T, T, N>(sm.st[s].C, 32 * tb, 32 * nt, id, half, l32);   // [t][n]
+      const f32x16 dt_ = xhalf_transpose<T>(sm.st[s].DY, 32 * tb, id, half, l32);              // [t][p]
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float e[8];
+        kset_vals(sm.ec[w], 2 * tb + c, half, e);
+        Frag<T> a;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a.set(j, ct[8 * c + j] * e[j]);
+        acc = mma(a, acc_to_frag<T>(dt_, c), acc);       // [n][p] += sum_t C[t][n] e^{c_t} dy[t][p]
+      }
+    }
+    const float dec = __expf(cend);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lam[i] = dec * lam[i] + acc[i];
+  }
+  if (q.dh0) {
+    float* dst = q.dh0 + ((int64_t)b * p.nheads + h) * per + (32 * pt + l32) * N + 32 * nt;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      f32x4 v;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = lam[4 * jj + k];
+      *reinterpret_cast<f32x4*>(dst + 8 * jj + 4 * half) = v;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ kernel 3: gradients per segment
+
+template <typename T, int N>
+struct GradSmem {
+  T B[SEG * N];             // Tile<T, N>
+  T C[SEG * N];
+  T X[SEG * HD];            // Tile<T, HD> of the current head
+  T DY[SEG * HD];
+  float dtraw[SEG];
+  float cs[2 * (N / 32)][SEG];   // per wave: c_t of the current head
+  float dtp[2 * (N / 32)][SEG];  // per wave: processed dt
+  float red[2][N / 32][SEG];     // per n-block partial dots: bint, u
+  float colg[SEG];               // sum_t (M o XD)[t][s], from fp32 tiles
+  float rowg[SEG];               // sum_s (M o XD)[t][s] dt_s, from fp32 tiles
+  float lh[N / 32];              // <lam_out, h_in> per n-block
+  float dd[2];                   // trace of dy x^T per diagonal 32-block
+  float ddp[HD];                 // per-channel dD partial
+  float cb[3][64 * 16];          // CB[t][s] tiles (t-block, s-block) = (0,0), (1,0), (1,1), accumulator order
+  float cbt[3][64 * 16];         // CB^T[s][t] tiles (s-block, t-block) = (0,0), (0,1), (1,1)
+};
+
+// Work split (NW = 2 N/32 waves): wave w owns n-block nb = w % (N/32) and token block r = w / (N/32) of the
+// dB^T [n][s] and dC^T [n][t] tiles; waves 0-3 also own the dx^T [p][s] tile (p-block w & 1, s-block w >> 1).
+template <typename T, int N>
+__global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdParams q) {
+  constexpr int NB = N / 32, NW = 2 * NB;
+  using TB = Tile<T, N>;
+  using TX = Tile<T, HD>;
+  __shared__ GradSmem<T, N> sm;
+  const SsdParams& p = q.f;
+  const int si = blockIdx.x, b = blockIdx.z;
+  const int HB = q.heads_per_wg;
+  const int hfirst = blockIdx.y * HB;
+  const int g = hfirst / (p.nheads / p.ngroups);
+  const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
+  const int nb = w % NB, r = w / NB;
+  const bool dxw = w < 4;
+  const int pb = w & 1, sbx = (w >> 1) & 1;
+  const int tok0 = si * SEG;
+  const int len = min(SEG, p.seqlen - tok0);
+  const int last = tok0 + len - 1;
+  const int s_l = 32 * r + l32;             // token column of this lane in the dB / dC tiles
+  const int s_x = 32 * sbx + l32;           // token column of this lane in the dx tile
+  const int64_t per = (int64_t)HD * N;
+
+  const T* xb = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb;
+  const T* dyb = reinterpret_cast<const T*>(q.dy) + (int64_t)b * q.dy_sb;
+  const float* dtb = p.dt + (int64_t)b * p.dt_sb;
+  {
+    constexpr int nblk = TB::NBLK / NW;
+    fetch_tile<T, N>(sm.B, reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + g * N, p.B_sl, tok0, last,
+                     w * nblk, nblk, l);
+    fetch_tile<T, N>(sm.C, reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb + g * N, p.C_sl, tok0, last,
+                     w * nblk, nblk, l);
+  }
+  auto fetch_head = [&](int h) {
+    constexpr int nblk = TX::NBLK / NW;
+    fetch_tile<T, HD>(sm.X, xb + (int64_t)h * p.x_sh, p.x_sl, tok0, last, w * nblk, nblk, l);
+    fetch_tile<T, HD>(sm.DY, dyb + (int64_t)h * q.dy_sh, q.dy_sl, tok0, last, w * nblk, nblk, l);
+    if (w == 0) fetch_dt(sm.dtraw, dtb + h, p.dt_sl, tok0, last, l);
+  };
+  fetch_head(hfirst);
+  if (w == 0) sm.ddp[l] = 0.f;
+
+  const T* hin_ws = reinterpret_cast<const T*>(p.dtype == DT_BF16 ? p.entering : (void*)p.chunk_states);
+  const T* lam_ws = reinterpret_cast<const T*>(q.lam);
+  f32x16 dBacc = zero16(), dCacc = zero16();
+
+  wait_vmem();                      // B / C tiles (and the first head's tiles) in LDS
+  lds_barrier();
+  if (dxw && pb == 1) {
+    // CB^T[s][t] = B_s . C_t for the tiles (sb, sbx), sb <= sbx (t-block sbx)
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      if (sb <= sbx) {
+        f32x16 a = zero16();
+#pragma unroll
+        for (int k = 0; k < N / 16; ++k)
+          a = mma(row_frag<T, T, N>(sm.B, 32 * sb + l32, 16 * k + 8 * half),
+                  row_frag<T, T, N>(sm.C, s_x, 16 * k + 8 * half), a);
+        float* o = sm.cbt[sb + sbx] + 16 * l;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f32x4 v;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[k] = a[4 * i + k];
+          *reinterpret_cast<f32x4*>(o + 4 * i) = v;
+        }
+      }
+    }
+  }
+  if (dxw && pb == 0) {
+    // CB[t][s] = C_t . B_s for the tiles (tb, sbx), tb >= sbx, parked in LDS for every head of the block
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      if (tb >= sbx) {
+        f32x16 a = zero16();
+#pragma unroll
+        for (int k = 0; k < N / 16; ++k)
+          a = mma(row_frag<T, T, N>(sm.C, 32 * tb + l32, 16 * k + 8 * half),
+                  row_frag<T, T, N>(sm.B, s_x, 16 * k + 8 * half), a);
+        float* o = sm.cb[tb + sbx] + 16 * l;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f32x4 v;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[k] = a[4 * i + k];
+          *reinterpret_cast<f32x4*>(o + 4 * i) = v;
+        }
+      }
+    }
+  }
+  for (int j = 0; j < HB; ++j) {
+    // Lane-derived values are recomputed per head from a laundered lane id (and length): otherwise the
+    // compiler keeps dozens of loop-invariant row indices and masks in registers across the head loop.
+    int lq = l, lenq = len;
+    asm volatile("" : "+v"(lq), "+s"(lenq));
+    const int l = lq, len = lenq;
+    const int half = l >> 5, l32 = l & 31;
+    const int s_l = 32 * r + l32, s_x = 32 * sbx + l32;
+    Frag<T> id[2], idk[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      id[c] = ident_frag<T>(c, half, l32);
+      idk[c] = ident_kset<T>(c, half, l32);
+    }
+    const int h = hfirst + j;
+    const int64_t sidx = (((int64_t)b * p.nseg + si) * p.nheads + h) * per;
+    StateBlk<T> Lb[2], Hb[2];
+#pragma unroll
+    for (int pt = 0; pt < 2; ++pt) {
+      Lb[pt] = load_state_blk<T>(lam_ws + sidx, nb, pt, l);
+      Hb[pt] = load_state_blk<T>(hin_ws + sidx, nb, pt, l);
+    }
+    wait_vmem();
+    lds_barrier();
+    // ---- decay of this head (lane = token), wave-private copies for per-row reads
+    const float Ah = p.A[h];
+    const float bias = p.dt_bias ? p.dt_bias[h] : 0.f;
+    const float raw = sm.dtraw[l];
+    float dtv;
+    const float cs = seg_decay(p, raw, bias, Ah, l, len, dtv);
+    const float cend = __shfl(cs, 63);
+    sm.cs[w][l] = cs;
+    sm.dtp[w][l] = dtv;
+    const float cs_l = __shfl(cs, s_l), dt_l = __shfl(dtv, s_l);
+
+    // ---- XD[t][s] = dy_t . x_s (tiles tb >= r, column block r), masked and decayed (L o XD), as
+    //      B-operand fragments (column s, k = t)
+    // The per-token sums of M o XD that the decay gradient needs (colG here, rowG below) are taken from
+    // these fp32 tiles, not from the bf16-operand products: the two sums cancel pairwise in da, and only
+    // identically rounded copies cancel.
+    Frag<T> XDf[2][2];
+    float colg = 0.f;
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      f32x16 a = zero16();
+      if (tb >= r) {
+#pragma unroll
+        for (int k = 0; k < HD / 16; ++k)
+          a = mma(row_frag<T, T, HD>(sm.DY, 32 * tb + l32, 16 * k + 8 * half),
+                  row_frag<T, T, HD>(sm.X, s_l, 16 * k + 8 * half), a);
+        float ct[16];
+        acc_rows(sm.cs[w], 32 * tb, half, ct);
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int t = 32 * tb + acc_row(half, i);
+          a[i] = (t < len && t >= s_l) ? a[i] * __expf(ct[i] - cs_l) : 0.f;
+          d += (t == s_l) ? a[i] : 0.f;
+        }
+        if (nb == 0) {
+          // trace of dy x^T (per-head D): the diagonal block (r, r)
+          if (tb == r) {
+            d = wave_sum(d);
+            if (l == 0) sm.dd[r] = d;
+          }
+          const float* cbp = sm.cb[tb + r] + 16 * l;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) colg += v[k] * a[4 * i + k];
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) XDf[tb][c] = acc_to_frag<T>(a, c);
+    }
+    if (nb == 0) {
+      colg += __shfl_xor(colg, 32);
+      if (half == 0) sm.colg[s_l] = colg;
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep the phases apart: bounded register lifetimes
+    // ---- dB^T tile (n-block nb, s-block r): inter part from lam_out, intra part from C^T (L o XD)
+    {
+      Frag<T> lamT[2][2];
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt) blk_transpose<T>(Lb[pt], idk, lamT[pt]);
+      const float wend_l = __expf(cend - cs_l);
+      f32x16 ai = zero16(), aa = zero16();
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          ai = mma(lamT[pt][c], scaled<T>(kset_frag<T, T, HD>(sm.X, s_l, 32 * pt + 16 * c, half), wend_l), ai);
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        if (tb >= r) {
+          const f32x16 ct = mfma_transpose<T, T, N>(sm.C, 32 * tb, 32 * nb, id, half, l32);   // [t][n]
+#pragma unroll
+          for (int c = 0; c < 2; ++c) aa = mma(acc_to_frag<T>(ct, c), XDf[tb][c], aa);
+        }
+      }
+      float Bv[16];
+      acc_cols<T, N>(sm.B, s_l, 32 * nb, half, Bv);
+      float sI = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        sI += ai[i] * Bv[i];
+        dBacc[i] += dt_l * (ai[i] + aa[i]);
+      }
+      sI += __shfl_xor(sI, 32);
+      if (half == 0) sm.red[0][nb][s_l] = sI;
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep the phases apart: bounded register lifetimes
+    // ---- XD^T[s][t] (tiles sb <= r, column block r), masked, decayed, scaled by dt_s: (column t, k = s)
+    Frag<T> XTf[2][2];
+    float rowg = 0.f;
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      f32x16 a = zero16();
+      if (sb <= r) {
+#pragma unroll
+        for (int k = 0; k < HD / 16; ++k)
+          a = mma(row_frag<T, T, HD>(sm.X, 32 * sb + l32, 16 * k + 8 * half),
+                  row_frag<T, T, HD>(sm.DY, s_l, 16 * k + 8 * half), a);
+        float cr[16], dr[16];
+        acc_rows(sm.cs[w], 32 * sb, half, cr);
+        acc_rows(sm.dtp[w], 32 * sb, half, dr);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int s = 32 * sb + acc_row(half, i);
+          a[i] = (s_l < len && s <= s_l) ? a[i] * __expf(cs_l - cr[i]) * dr[i] : 0.f;
+        }
+        if (nb == 0) {
+          const float* cbp = sm.cbt[sb + r] + 16 * l;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) rowg += v[k] * a[4 * i + k];
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) XTf[sb][c] = acc_to_frag<T>(a, c);
+    }
+    if (nb == 0) {
+      rowg += __shfl_xor(rowg, 32);
+      if (half == 0) sm.rowg[s_l] = rowg;
+    }
+
+    // <lam_out, h_in> over the blocks of n-block nb (one wave per n-block)
+    if (r == 0) {
+      float d = 0.f;
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d += Lb[pt].at(i) * Hb[pt].at(i);
+      d = wave_sum(d);
+      if (l == 0) sm.lh[nb] = d;
+    }
+
+    // ---- dC^T tile (n-block nb, t-block r): inter part from h_in, intra part from B^T (L o XD o dt)^T
+    {
+      Frag<T> hT[2][2];
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt) blk_transpose<T>(Hb[pt], idk, hT[pt]);
+      const float ec_l = __expf(cs_l);
+      f32x16 ah = zero16(), ac = zero16();
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          ah = mma(hT[pt][c], scaled<T>(kset_frag<T, T, HD>(sm.DY, s_l, 32 * pt + 16 * c, half), ec_l), ah);
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        if (sb <= r) {
+          const f32x16 bt = mfma_transpose<T, T, N>(sm.B, 32 * sb, 32 * nb, id, half, l32);   // [s][n]
+#pragma unroll
+          for (int c = 0; c < 2; ++c) ac = mma(acc_to_frag<T>(bt, c), XTf[sb][c], ac);
+        }
+      }
+      float Cv[16];
+      acc_cols<T, N>(sm.C, s_l, 32 * nb, half, Cv);
+      float sU = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        sU += ah[i] * Cv[i];
+        dCacc[i] += ah[i] + ac[i];
+      }
+      sU += __shfl_xor(sU, 32);
+      if (half == 0) sm.red[1][nb][s_l] = sU;
+    }
+
+    __builtin_amdgcn_sched_barrier(0);   // keep the phases apart: bounded register lifetimes
+    // ---- dx^T tile (p-block pb, s-block sbx)
+    if (dxw) {
+      const float csx = __shfl(cs, s_x), dtx = __shfl(dtv, s_x), wx = __expf(cend - csx);
+      f32x16 ax = zero16();
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        if (tb >= sbx) {
+          f32x16 m;
+          const float* cbp = sm.cb[tb + sbx] + 16 * l;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) m[4 * i + k] = v[k];
+          }
+          float ct[16];
+          acc_rows(sm.cs[w], 32 * tb, half, ct);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int t = 32 * tb + acc_row(half, i);
+            m[i] = (t < len && t >= s_x) ? m[i] * __expf(ct[i] - csx) : 0.f;
+          }
+          const f32x16 dyt = mfma_transpose<T, T, HD>(sm.DY, 32 * tb, 32 * pb, id, half, l32);   // [t][p]
+#pragma unroll
+          for (int c = 0; c < 2; ++c) ax = mma(acc_to_frag<T>(dyt, c), acc_to_frag<T>(m, c), ax);
+        }
+      }
+#pragma unroll
+      for (int nt = 0; nt < NB; ++nt) {
+        const StateBlk<T> lx = load_state_blk<T>(lam_ws + sidx, nt, pb, l);
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          ax = mma(lx.frag(c), scaled<T>(kset_frag<T, T, N>(sm.B, s_x, 32 * nt + 16 * c, half), wx), ax);
+      }
+      float dyv[16];
+      acc_cols<T, HD>(sm.DY, s_x, 32 * pb, half, dyv);
+      float Dv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        Dv[i] = p.D ? (p.D_per_channel ? p.D[h * HD + 32 * pb + acc_row(half, i)] : p.D[h]) : 0.f;
+      if (s_x < len) {
+        T* o = reinterpret_cast<T*>(q.dx) + (int64_t)b * q.dx_sb + (int64_t)(tok0 + s_x) * q.dx_sl +
+               (int64_t)h * q.dx_sh + 32 * pb + 4 * half;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          if constexpr (sizeof(T) == 2) {
+            bf16x4 v;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = (bf16)(dtx * ax[4 * jj + k] + Dv[4 * jj + k] * dyv[4 * jj + k]);
+            *reinterpret_cast<bf16x4*>(o + 8 * jj) = v;
+          } else {
+            f32x4 v;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = dtx * ax[4 * jj + k] + Dv[4 * jj + k] * dyv[4 * jj + k];
+            *reinterpret_cast<f32x4*>(o + 8 * jj) = v;
+          }
+        }
+      }
+      if (p.D_per_channel && q.dD && s_x < len) {
+        float xv[16];
+        acc_cols<T, HD>(sm.X, s_x, 32 * pb, half, xv);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) atomicAdd(&sm.ddp[32 * pb + acc_row(half, i)], xv[i] * dyv[i]);
+      }
+    }
+
+    lds_barrier();                     // partial dots complete; X / DY / dt free for the next head
+    if (j + 1 < HB) fetch_head(h + 1);
+    if (w == 0) {
+      const float colG = sm.colg[l], rowG = sm.rowg[l];
+      float bint = 0.f, u = 0.f, lh = 0.f;
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        bint += sm.red[0][k][l];
+        u += sm.red[1][k][l];
+        lh += sm.lh[k];
+      }
+      const bool valid = l < len;
+      const float qv = valid ? rowG - dtv * colG + u : 0.f;
+      const float vv = dtv * bint;
+      const float qi = wave_incl_scan_dpp(qv);
+      const float qtot = __shfl(qi, 63);
+      const float vi = wave_incl_scan_dpp(vv);
+      const float da = (qtot - qi + qv) + __expf(cend) * lh + (vi - vv);
+      const float ddr = valid ? (colG + bint + Ah * da) * dt_chain(p, raw, bias) : 0.f;
+      if (valid) q.ddt[(int64_t)b * q.ddt_sb + (int64_t)(tok0 + l) * q.ddt_sl + h] = ddr;
+      const float sdA = wave_sum(valid ? dtv * da : 0.f);
+      const float sdb = wave_sum(ddr);
+      if (l == 0) {
+        unsafeAtomicAdd(&q.dA[h], sdA);
+        if (q.dbias) unsafeAtomicAdd(&q.dbias[h], sdb);
+        if (q.dD && !p.D_per_channel) unsafeAtomicAdd(&q.dD[h], sm.dd[0] + sm.dd[1]);
+      }
+      if (q.dD && p.D_per_channel) {
+        unsafeAtomicAdd(&q.dD[h * HD + l], sm.ddp[l]);
+        sm.ddp[l] = 0.f;
+      }
+    }
+  }
+  // group sums of this block's heads -> fp32 accumulators (b, L, G, N)
+  if (s_l < len) {
+    const int64_t row = (((int64_t)b * p.seqlen + tok0 + s_l) * p.ngroups + g) * N + 32 * nb;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      unsafeAtomicAdd(q.dB_acc + row + acc_row(half, i), dBacc[i]);
+      unsafeAtomicAdd(q.dC_acc + row + acc_row(half, i), dCacc[i]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ kernel 4: accumulators -> dB, dC
+
+template <typename T>
+__global__ __launch_bounds__(256) void ssd_bwd_convert_kernel(const float* __restrict__ acc, void* out, int64_t sb,
+                                                              int64_t sl, int L, int GN, int64_t n4) {
+  const int64_t i4 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i4 >= n4) return;
+  const int64_t e = i4 * 4;
+  const int64_t row = e / GN;
+  const int col = (int)(e - row * GN);
+  const int64_t bb = row / L, t = row - bb * L;
+  const f32x4 v = *reinterpret_cast<const f32x4*>(acc + e);
+  T* o = reinterpret_cast<T*>(out) + bb * sb + t * sl + col;
+  if constexpr (sizeof(T) == 2) {
+    bf16x4 u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) u[k] = (bf16)v[k];
+    *reinterpret_cast<bf16x4*>(o) = u;
+  } else {
+    *reinterpret_cast<f32x4*>(o) = v;
+  }
+}
+
+// ------------------------------------------------------------------ host side
+
+struct BwdWorkspace {
+  size_t fwd, lam, acc;
+  size_t total() const { return align256(fwd) + align256(lam) + 2 * align256(acc); }
+};
+static BwdWorkspace bwd_workspace(int batch, int seqlen, int nheads, int headdim, int dstate, int ngroups, int dtype) {
+  const int nseg = (seqlen + SEG - 1) / SEG;
+  BwdWorkspace w;
+  w.fwd = ssd_workspace_bytes(batch, seqlen, nseg, nheads, headdim, dstate, ngroups, dtype);
+  w.lam = (size_t)batch * nseg * nheads * headdim * dstate * (dtype == DT_BF16 ? sizeof(bf16) : sizeof(float));
+  w.acc = (size_t)batch * seqlen * ngroups * dstate * sizeof(float);
+  return w;
+}
+
+size_t ssd_bwd_workspace_bytes(int batch, int seqlen, int nheads, int headdim, int dstate, int ngroups, int dtype) {
+  return bwd_workspace(batch, seqlen, nheads, headdim, dstate, ngroups, dtype).total();
+}
+
+void ssd_bwd_workspace_layout(SsdBwdParams& q, void* workspace) {
+  SsdParams& p = q.f;
+  const BwdWorkspace w = bwd_workspace(p.batch, p.seqlen, p.nheads, p.headdim, p.dstate, p.ngroups, p.dtype);
+  char* c = reinterpret_cast<char*>(workspace);
+  ssd_workspace_layout(p, c);
+  c += align256(w.fwd);
+  q.lam = c;
+  c += align256(w.lam);
+  q.dB_acc = reinterpret_cast<float*>(c);
+  c += align256(w.acc);
+  q.dC_acc = reinterpret_cast<float*>(c);
+}
+
+template <typename T, int N>
+static hipError_t launch_bwd_t(const SsdBwdParams& q, hipStream_t st) {
+  const SsdParams& p = q.f;
+  constexpr int NB = N / 32;
+  hipLaunchKernelGGL((ssd_bwd_lambda_kernel<T, N>), dim3(2, (unsigned)p.nheads, (unsigned)p.batch), dim3(64 * NB), 0,
+                     st, q);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_bwd_grad_kernel<T, N>),
+                     dim3((unsigned)p.nseg, (unsigned)(p.nheads / q.heads_per_wg), (unsigned)p.batch),
+                     dim3(128 * NB), 0, st, q);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int GN = p.ngroups * N;
+  const int64_t n4 = (int64_t)p.batch * p.seqlen * GN / 4;
+  const unsigned nblk = (unsigned)((n4 + 255) / 256);
+  hipLaunchKernelGGL((ssd_bwd_convert_kernel<T>), dim3(nblk), dim3(256), 0, st, q.dB_acc, q.dB, q.dB_sb, q.dB_sl,
+                     p.seqlen, GN, n4);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((ssd_bwd_convert_kernel<T>), dim3(nblk), dim3(256), 0, st, q.dC_acc, q.dC, q.dC_sb, q.dC_sl,
+                     p.seqlen, GN, n4);
+  return hipGetLastError();
+}
+
+hipError_t launch_ssd_bwd(const SsdBwdParams& q, hipStream_t st) {
+  const SsdParams& p = q.f;
+  ZeroRanges z;
+  z.p[0] = q.dB_acc;  z.n[0] = (int64_t)p.batch * p.seqlen * p.ngroups * p.dstate;
+  z.p[1] = q.dC_acc;  z.n[1] = z.n[0];
+  z.p[2] = q.dA;      z.n[2] = p.nheads;
+  z.p[3] = q.dD;      z.n[3] = p.D_per_channel ? (int64_t)p.nheads * HD : p.nheads;
+  z.p[4] = q.dbias;   z.n[4] = p.nheads;
+  if (p.nseg == 0) { z.p[0] = nullptr; z.p[1] = nullptr; }
+  int64_t most = 0;
+  for (int i = 0; i < 5; ++i)
+    if (z.p[i] && z.n[i] > most) most = z.n[i];
+  if (most > 0) {
+    const int64_t nb256 = (most + 255) / 256;
+    const unsigned gx = (unsigned)(nb256 < 4096 ? nb256 : 4096);
+    hipLaunchKernelGGL(ssd_bwd_zero_kernel, dim3(gx, 5), dim3(256), 0, st, z);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (p.nseg == 0) {
+    if (!q.dh0) return hipSuccess;
+    const size_t n = (size_t)p.batch * p.nheads * HD * p.dstate;
+    hipLaunchKernelGGL(ssd_bwd_copy_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, q.d_final, q.dh0, n);
+    return hipGetLastError();
+  }
+  hipError_t e = launch_ssd_states(p, st);
+  if (e != hipSuccess) return e;
+  if (p.dtype == DT_BF16) {
+    if (p.dstate == 128) return launch_bwd_t<bf16, 128>(q, st);
+    if (p.dstate == 64) return launch_bwd_t<bf16, 64>(q, st);
+  } else {
+    if (p.dstate == 128) return launch_bwd_t<float, 128>(q, st);
+    if (p.dstate == 64) return launch_bwd_t<float, 64>(q, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace mh

@@ -46,21 +46,14 @@
 // bf16 I/O uses 32x32x16 bf16 MFMAs, fp32 I/O 32x32x2 fp32 MFMAs; accumulation is fp32.
 #include "common.h"
 #include "launch.h"
+#include "ssd_shared.h"
 #include "tiles.h"
 
 namespace mh {
 
-constexpr int HD = 64;               // headdim handled by these kernels
 constexpr float FACT_RANGE = 60.f;   // max exponent of an operand scale factor
 
 // ------------------------------------------------------------------ helpers
-
-__device__ __forceinline__ float process_dt(const SsdParams& p, float dt, float bias) {
-  dt += bias;
-  if (p.dt_softplus) dt = softplus_f(dt);
-  if (p.has_dt_limit) dt = fminf(fmaxf(dt, p.dt_min), p.dt_max);
-  return dt;
-}
 
 // x^T of a wave's x half tile (lane = p, tokens on the k axis, KSET order) as
 // 4 fragments, each token scaled by sa[token].
@@ -136,17 +129,6 @@ template <typename T, typename TM, int N, int HG>
 constexpr int state_nbuf = sizeof(StateSmem<T, TM, N, HG, 3>) <= LDS_BYTES ? 3
                            : (sizeof(StateSmem<T, TM, N, HG, 2>) <= LDS_BYTES ? 2 : 1);
 
-// Offset (floats) of state tile (nt, pt) element block of lane l in the fragment-native workspace order.
-__device__ __forceinline__ int frag_off(int nt, int pt, int l) { return ((nt * 2 + pt) * 64 + l) * 16; }
-
-// In-segment decay of one head (lane = token; tokens at or past c1 have dt = 0):
-// returns cs_t, the inclusive cumulative log-decay.
-__device__ __forceinline__ float seg_decay(const SsdParams& p, float dtraw, float bias, float Ah, int t, int c1,
-                                           float& dtv) {
-  dtv = (t < c1) ? process_dt(p, dtraw, bias) : 0.f;
-  return wave_incl_scan_dpp(Ah * dtv);
-}
-
 // State read-out of one wave: Y^T[p][t] += sum_n H[p][n] C^T[n][t] for the two 32-token t-tiles of the
 // segment (H as A operand straight from the accumulators, converted once for both; C^T fragments
 // precomputed per segment).
@@ -208,8 +190,6 @@ __device__ __forceinline__ void state_update(f32x16 (&H)[N / 32], const Frag<TM>
 }
 
 // Workspace layout: [chunk states][chunk log-decays][segment fragments], each 256-byte aligned.
-__host__ __device__ __forceinline__ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
-
 // ------------------------------------------------------------------ kernel 0
 
 // One workgroup of 8 waves per (segment, group, batch): 3 + 2 N/32 work items
@@ -403,13 +383,6 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_state_kernel(SsdParams p) 
 }
 
 // ------------------------------------------------------------------ kernel 2
-
-// Workspace element e (fragment-native order) <-> canonical state index p * N + n.
-__device__ __forceinline__ int canon_index(int e, int N) {
-  const int r = e & 15, lane = (e >> 4) & 63, tile = e >> 10;
-  const int pt = tile & 1, nt = tile >> 1;
-  return (32 * pt + (lane & 31)) * N + 32 * nt + acc_row(lane >> 5, r);
-}
 
 // Entering states for the scan kernel: fp32 in place of fp32 S_k, or (bf16 I/O, where the chunk states
 // are bf16 and the scan consumes the state as bf16 MFMA operands) bf16 in a separate array of the same
@@ -719,7 +692,7 @@ void ssd_workspace_layout(SsdParams& p, void* workspace) {
 }
 
 template <typename T, typename TM, int N, int HG>
-static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st) {
+static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st, bool scan) {
   hipLaunchKernelGGL((ssd_seg_frags_kernel<T, TM, N>), dim3((unsigned)p.nseg, (unsigned)p.ngroups, (unsigned)p.batch),
                      dim3(512), 0, st, p);
   hipError_t e = hipGetLastError();
@@ -732,7 +705,7 @@ static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st) {
   dim3 g2((unsigned)((per4 + 255) / 256), (unsigned)(p.batch * p.nheads));
   hipLaunchKernelGGL((ssd_state_pass_kernel<T>), g2, dim3(256), 0, st, p);
   e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || !scan) return e;
   hipLaunchKernelGGL((ssd_chunk_scan_kernel<T, TM, N, HG>), grid, dim3(128 * HG), 0, st, p);
   return hipGetLastError();
 }
@@ -743,16 +716,16 @@ constexpr bool ssd_fits = !(sizeof(T) == 4 && N == 128 && HG > 1) &&   // fp32 N
                           bt_blocks<TM, N> % (2 * HG) == 0 && Tile<T, N>::NBLK % (2 * HG) == 0;
 
 template <typename T, typename TM, int N>
-static hipError_t launch_ssd_n(const SsdParams& p, hipStream_t st) {
+static hipError_t launch_ssd_n(const SsdParams& p, hipStream_t st, bool scan) {
   switch (p.heads_per_wg) {
     case 4:
-      if constexpr (ssd_fits<T, TM, N, 4>) return launch_ssd_t<T, TM, N, 4>(p, st);
+      if constexpr (ssd_fits<T, TM, N, 4>) return launch_ssd_t<T, TM, N, 4>(p, st, scan);
       return hipErrorInvalidValue;
     case 2:
-      if constexpr (ssd_fits<T, TM, N, 2>) return launch_ssd_t<T, TM, N, 2>(p, st);
+      if constexpr (ssd_fits<T, TM, N, 2>) return launch_ssd_t<T, TM, N, 2>(p, st, scan);
       return hipErrorInvalidValue;
     case 1:
-      if constexpr (ssd_fits<T, TM, N, 1>) return launch_ssd_t<T, TM, N, 1>(p, st);
+      if constexpr (ssd_fits<T, TM, N, 1>) return launch_ssd_t<T, TM, N, 1>(p, st, scan);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
@@ -765,22 +738,27 @@ __global__ __launch_bounds__(256) void ssd_empty_kernel(const float* __restrict_
   if (i < n) fin[i] = h0 ? h0[i] : 0.f;
 }
 
-hipError_t launch_ssd(const SsdParams& p, hipStream_t st) {
+static hipError_t launch_ssd_impl(const SsdParams& p, hipStream_t st, bool scan) {
   if (p.nchunks == 0) {
-    if (!p.final_state) return hipSuccess;
+    if (!p.final_state || !scan) return hipSuccess;
     const size_t n = (size_t)p.batch * p.nheads * HD * p.dstate;
     hipLaunchKernelGGL(ssd_empty_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p.init_state,
                        p.final_state, n);
     return hipGetLastError();
   }
   if (p.dtype == DT_BF16) {
-    if (p.dstate == 128) return launch_ssd_n<bf16, bf16, 128>(p, st);
-    if (p.dstate == 64) return launch_ssd_n<bf16, bf16, 64>(p, st);
+    if (p.dstate == 128) return launch_ssd_n<bf16, bf16, 128>(p, st, scan);
+    if (p.dstate == 64) return launch_ssd_n<bf16, bf16, 64>(p, st, scan);
   } else {
-    if (p.dstate == 128) return launch_ssd_n<float, float, 128>(p, st);
-    if (p.dstate == 64) return launch_ssd_n<float, float, 64>(p, st);
+    if (p.dstate == 128) return launch_ssd_n<float, float, 128>(p, st, scan);
+    if (p.dstate == 64) return launch_ssd_n<float, float, 64>(p, st, scan);
   }
   return hipErrorInvalidValue;
 }
+
+hipError_t launch_ssd(const SsdParams& p, hipStream_t st) { return launch_ssd_impl(p, st, true); }
+
+// Kernels 0-2 only: the entering state of every chunk (workspace), for the backward pass.
+hipError_t launch_ssd_states(const SsdParams& p, hipStream_t st) { return launch_ssd_impl(p, st, false); }
 
 }  // namespace mh

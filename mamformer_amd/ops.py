@@ -7,7 +7,10 @@ PyTorch fallback: non-CUDA tensors or a missing library raise.
 Reference functions replaced (``R`` = ``mamformer 671b/``):
 
 =====================================  ====================================================================
-``selective_scan``                      R/mamformer/layers/mamba2.py:31-67 (``_selective_scan_impl`` :70-130)
+``selective_scan``                      R/mamformer/layers/mamba2.py:31-67 (``_selective_scan_impl`` :70-130);
+                                        differentiable (autograd through ``selective_scan_bwd``)
+``selective_scan_bwd``                  the autograd backward of the same scan (trained through in
+                                        R/tests/test_mamba2.py:56-71), as one explicit op
 ``recurrent_step``                      R/mamformer/layers/mamba2.py:407-458 (``Mamba2Block._recurrent_step``)
 ``selective_state_update``              in-place form of the same decode step (the state is updated in HBM)
 ``linear_attn_scan``                    gated KDA scan of the benchmark configuration (no reference function);
@@ -38,9 +41,9 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import SsdArgs, SsuArgs, KdaArgs, Conv1dArgs
+from ._lib import SsdArgs, SsdBwdArgs, SsuArgs, KdaArgs, Conv1dArgs
 
-__all__ = ["selective_scan", "selective_state_update", "recurrent_step", "linear_attn_scan",
+__all__ = ["selective_scan", "selective_scan_bwd", "selective_state_update", "recurrent_step", "linear_attn_scan",
            "linear_attn_scan_pair", "linear_attn_scan_single", "linear_attention_scan", "diff_lambda",
            "linear_attn_step", "linear_attention_recurrent",
            "ssd_chunk_len", "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan",
@@ -233,6 +236,18 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
         else:
             z4 = z
         z4 = _inner_contig(z4)
+    if not _plan_only and torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (x4, dt32, A32, B4, C4, D32, bias32, h0, z4)):
+        if return_h_states:
+            raise NotImplementedError("selective_scan: return_h_states is not differentiable")
+        y4, fin = _SelectiveScanFn.apply(x4, dt32, A32, B4, C4, D32, h0, bias32,
+                                         (dt_softplus, dt_limit, chunk_size))
+        if z4 is not None:
+            y4 = y4 * torch.nn.functional.silu(z4)
+        y = y4.reshape(x.shape) if x.dim() == 3 else y4
+        if not return_final_state:
+            return y
+        return y, (fin.reshape(b, H * P, N) if x.dim() == 3 else fin)
     y4 = torch.empty((b, L, H, P), device=x.device, dtype=x.dtype)
     fin = torch.empty((b, H, P, N), device=x.device, dtype=torch.float32) if return_final_state else None
     args = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, y4, fin, chunk_size, z4)
@@ -256,6 +271,124 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
     if return_final_state:
         out.append(fin_out)
     return out[0] if len(out) == 1 else tuple(out)
+
+
+def _scan_fwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg):
+    dt_softplus, dt_limit, chunk_size = cfg
+    b, L, H, P = x4.shape
+    N = B4.shape[3]
+    y4 = torch.empty((b, L, H, P), device=x4.device, dtype=x4.dtype)
+    fin = torch.empty((b, H, P, N), device=x4.device, dtype=torch.float32)
+    args = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, y4, fin, chunk_size)
+    nbytes = ct.c_size_t()
+    _lib.call("mh_ssd_workspace_bytes", ct.byref(args), ct.byref(nbytes))
+    ws = torch.empty(max(int(nbytes.value), 16), device=x4.device, dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = _ptr(ws), nbytes.value
+    _lib.call("mh_ssd_chunk_scan_fwd", ct.byref(args), _stream(x4.device))
+    return y4, fin
+
+
+def _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4, dfin, need_dh0):
+    dt_softplus, dt_limit, _ = cfg
+    b, L, H, P = x4.shape
+    G, N = B4.shape[2], B4.shape[3]
+    dev = x4.device
+    if dy4 is None:
+        dy4 = torch.zeros((b, L, H, P), device=dev, dtype=x4.dtype)
+    dy4 = _inner_contig(dy4.to(x4.dtype))
+    dfin = None if dfin is None else dfin.reshape(b, H, P, N).to(torch.float32).contiguous()
+    dx = torch.empty((b, L, H, P), device=dev, dtype=x4.dtype)
+    ddt = torch.empty((b, L, H), device=dev, dtype=torch.float32)
+    dA = torch.empty((H,), device=dev, dtype=torch.float32)
+    dB = torch.empty((b, L, G, N), device=dev, dtype=x4.dtype)
+    dC = torch.empty((b, L, G, N), device=dev, dtype=x4.dtype)
+    dD = torch.empty_like(D32) if D32 is not None else None
+    dbias = torch.empty((H,), device=dev, dtype=torch.float32) if bias32 is not None else None
+    dh0 = torch.empty((b, H, P, N), device=dev, dtype=torch.float32) if need_dh0 else None
+    a = SsdBwdArgs()
+    a.fwd = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, x4, None, 64)
+    a.fwd.y = None
+    a.dy, a.dy_stride_b, a.dy_stride_l, a.dy_stride_h = _ptr(dy4), dy4.stride(0), dy4.stride(1), dy4.stride(2)
+    a.d_final_state = _ptr(dfin)
+    a.dx, a.dx_stride_b, a.dx_stride_l, a.dx_stride_h = _ptr(dx), dx.stride(0), dx.stride(1), dx.stride(2)
+    a.ddt, a.ddt_stride_b, a.ddt_stride_l = _ptr(ddt), ddt.stride(0), ddt.stride(1)
+    a.dA = _ptr(dA)
+    a.dB, a.dB_stride_b, a.dB_stride_l = _ptr(dB), dB.stride(0), dB.stride(1)
+    a.dC, a.dC_stride_b, a.dC_stride_l = _ptr(dC), dC.stride(0), dC.stride(1)
+    a.dD, a.d_dt_bias, a.d_initial_state = _ptr(dD), _ptr(dbias), _ptr(dh0)
+    nbytes = ct.c_size_t()
+    _lib.call("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(nbytes))
+    ws = torch.empty(max(int(nbytes.value), 16), device=dev, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = _ptr(ws), nbytes.value
+    _lib.call("mh_ssd_chunk_scan_bwd", ct.byref(a), _stream(dev))
+    return dx, ddt, dA, dB, dC, dD, dh0, dbias
+
+
+class _SelectiveScanFn(torch.autograd.Function):
+    """Autograd node of the HIP scan: forward = the prefill kernels, backward = ``mh_ssd_chunk_scan_bwd``."""
+
+    @staticmethod
+    def forward(ctx, x4, dt32, A32, B4, C4, D32, h0, bias32, cfg):
+        y4, fin = _scan_fwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg)
+        ctx.save_for_backward(x4, dt32, A32, B4, C4, D32, h0, bias32)
+        ctx.cfg = cfg
+        return y4, fin
+
+    @staticmethod
+    def backward(ctx, dy4, dfin):
+        x4, dt32, A32, B4, C4, D32, h0, bias32 = ctx.saved_tensors
+        need_dh0 = h0 is not None and ctx.needs_input_grad[6]
+        dx, ddt, dA, dB, dC, dD, dh0, dbias = _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, ctx.cfg, dy4,
+                                                        dfin, need_dh0)
+        return dx, ddt, dA, dB, dC, dD, dh0, dbias, None
+
+
+def selective_scan_bwd(dy, x, dt, A, B, C, D=None, *, d_final_state=None, initial_state=None, dt_bias=None,
+                       dt_softplus=False, dt_limit=None):
+    """Gradients of ``<dy, y> + <d_final_state, final_state>`` for ``y, final_state = selective_scan(x, dt, A, B,
+    C, D, initial_state=..., dt_bias=..., dt_softplus=..., dt_limit=...)`` -- the backward PyTorch autograd runs
+    through the reference's scan (mamba2.py:70-130; R/tests/test_mamba2.py:56-71), on the GPU.
+
+    Shapes as ``selective_scan`` (x and dy (b, L, H*P) or (b, L, H, P)); ``dy`` None means zero.
+    Returns a dict with dx (like x), ddt (b, L, H) fp32 w.r.t. the raw dt (through bias / softplus / clamp),
+    dA (H,), dB, dC (like B, C), dD (like D, when D is given), d_dt_bias (H,) when dt_bias is given and
+    d_initial_state (like initial_state, or (b, H, P, N) when none was given: the gradient w.r.t. a zero one).
+    """
+    _require_cuda("selective_scan_bwd", dy, x, dt, A, B, C, D, d_final_state, initial_state, dt_bias)
+    if x.dtype not in _DT or B.dtype != x.dtype or C.dtype != x.dtype:
+        raise TypeError("selective_scan_bwd: x, B, C must share one dtype (float32 or bfloat16)")
+    b, L, H = dt.shape
+    if x.dim() == 3:
+        P = x.shape[2] // H
+        x4 = x.reshape(b, L, H, P)
+    else:
+        P = x.shape[3]
+        x4 = x
+    B4 = B.unsqueeze(2) if B.dim() == 3 else B
+    C4 = C.unsqueeze(2) if C.dim() == 3 else C
+    N = B4.shape[3]
+    if A.shape != (H,):
+        raise ValueError(f"selective_scan_bwd: A must be (H,) = ({H},), got {tuple(A.shape)}")
+    if D is not None and D.numel() not in (H, H * P):
+        raise ValueError(f"selective_scan_bwd: D must have H or H*P entries, got {tuple(D.shape)}")
+    x4 = _inner_contig(x4)
+    B4, C4 = _inner_contig(B4, 2), _inner_contig(C4, 2)
+    dt32 = dt.to(torch.float32)
+    if dt32.stride(-1) != 1:
+        dt32 = dt32.contiguous()
+    A32, D32, bias32 = _f32c(A), _f32c(D.reshape(-1) if D is not None else None), _f32c(dt_bias)
+    h0 = None if initial_state is None else initial_state.reshape(b, H, P, N).to(torch.float32).contiguous()
+    dy4 = None if dy is None else dy.reshape(b, L, H, P)
+    with torch.no_grad():
+        dx, ddt, dA, dB, dC, dD, dh0, dbias = _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32,
+                                                        (dt_softplus, dt_limit, None), dy4, d_final_state, True)
+    out = {"dx": dx.reshape(x.shape), "ddt": ddt, "dA": dA, "dB": dB.reshape(B.shape), "dC": dC.reshape(C.shape),
+           "d_initial_state": dh0 if initial_state is None else dh0.reshape(initial_state.shape)}
+    if D is not None:
+        out["dD"] = dD.reshape(D.shape)
+    if dt_bias is not None:
+        out["d_dt_bias"] = dbias.reshape(dt_bias.shape)
+    return out
 
 
 def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size):

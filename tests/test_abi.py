@@ -10,7 +10,7 @@ import torch
 
 import mamformer_amd
 from mamformer_amd import _lib
-from mamformer_amd._lib import Conv1dArgs, KdaArgs, SsdArgs, SsuArgs
+from mamformer_amd._lib import SsdBwdArgs, Conv1dArgs, KdaArgs, SsdArgs, SsuArgs
 
 ROOT = Path(__file__).resolve().parent.parent
 
@@ -241,3 +241,59 @@ def test_conv1d_rejects_missing_conv_state():
     a = _good_conv()
     a.conv_state_len = 2
     assert _rc("mh_causal_conv1d_fwd", ct.byref(a), None) == -1
+
+
+def _good_bwd():
+    a = SsdBwdArgs()
+    a.fwd = _good_ssd()
+    f = a.fwd
+    P, H, L, G, N = 64, f.nheads, f.seqlen, f.ngroups, f.dstate
+    fake = ct.c_void_p(8192)
+    a.dy = a.dx = a.ddt = a.dA = a.dB = a.dC = fake
+    a.dy_stride_h = a.dx_stride_h = P
+    a.dy_stride_l = a.dx_stride_l = H * P
+    a.dy_stride_b = a.dx_stride_b = L * H * P
+    a.ddt_stride_l, a.ddt_stride_b = H, L * H
+    a.dB_stride_l = a.dC_stride_l = G * N
+    a.dB_stride_b = a.dC_stride_b = L * G * N
+    return a
+
+
+def test_ssd_bwd_workspace_and_validation():
+    a = _good_bwd()
+    n = ct.c_size_t()
+    assert _rc("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+    nseg = -(-300 // 64)
+    # forward states (bf16 chunk-local + entering) and lam per segment, plus two fp32 (b, L, G, N) accumulators
+    assert n.value >= 3 * 2 * nseg * 8 * 64 * 128 * 2 + 2 * 2 * 300 * 2 * 128 * 4
+    a.fwd.y = None                                       # the forward output is not needed
+    assert _rc("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+    a.fwd.chunk_len = 100                                # ignored: the backward uses 64-token segments
+    assert _rc("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+
+
+@pytest.mark.parametrize("mutate,code,word", [
+    (lambda a: setattr(a.fwd, "z", ct.c_void_p(4096)), -6, b"gate"),
+    (lambda a: setattr(a.fwd, "B_stride_l", 0), -6, b"broadcast"),
+    (lambda a: setattr(a, "dy", None), -1, b"dy"),
+    (lambda a: setattr(a, "dA", None), -1, b"dA"),
+    (lambda a: setattr(a.fwd, "D", ct.c_void_p(4096)), -1, b"dD"),
+    (lambda a: setattr(a, "dB", ct.c_void_p(8192 + 4)), -5, b"aligned"),
+    (lambda a: setattr(a, "dx_stride_h", 32), -4, b"head stride"),
+    (lambda a: setattr(a, "dC_stride_l", 64), -4, b"token stride"),
+    (lambda a: setattr(a.fwd, "dstate", 96), -6, b"dstate"),
+])
+def test_ssd_bwd_rejects_bad_arguments(mutate, code, word):
+    a = _good_bwd()
+    mutate(a)
+    n = ct.c_size_t()
+    assert _rc("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == code
+    assert word in _lib.lib().mh_last_error()
+    assert _rc("mh_ssd_chunk_scan_bwd", ct.byref(a), None) == code
+
+
+def test_ssd_bwd_rejects_small_workspace():
+    a = _good_bwd()
+    a.workspace, a.workspace_bytes = ct.c_void_p(8192), 64
+    assert _rc("mh_ssd_chunk_scan_bwd", ct.byref(a), None) == -7
+    assert _rc("mh_ssd_chunk_scan_bwd", None, None) == -1
