@@ -15,7 +15,8 @@ a step from the previous one.  The same JSON line carries:
   (``oracle/baseline.py``, mamba2.py:84-126 structure) timed on the host cores
   on a bounded token sample of the same workload.
 * ``decode`` -- selective state update at B=64 and B=256 (HBM GB/s vs 8 TB/s).
-* ``other`` -- ssd4 (128K prefill with state carry) and kda5 (gated KDA scan).
+* ``other`` -- ssd4 (128K prefill with state carry), kda5 (gated KDA scan) and ssd2_bwd (the backward of
+  the ssd2 prefill: all input gradients from dy and d_final).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu] [--only LEGS]
                        [--copy-calibration BYTES]
@@ -54,6 +55,20 @@ def ssd_alg(cfg, Q=256):
               + b * H * P * N * 4 * (2 if cfg.init_state else 1))
     nchunks = L // Q
     flops = b * nchunks * (2 * Q * Q * N * G + H * (2 * Q * Q * P + 4 * Q * N * P))
+    return nbytes, flops
+
+
+def ssd_bwd_alg(cfg, Q=64):
+    """Backward of the prefill.  Bytes: x, dy, B, C, dt and d_final read once; dx, dB, dC, ddt and the fp32 dh0
+    written once (+ h0 read).  FLOPs per (b, 64-token segment): 2 Q^2 N G (C B^T) + H (4 Q^2 P + 4 Q^2 N +
+    10 Q P N): dy x^T, the dx / dB / dC token-pair products, their four state products, the adjoint update and the
+    forward state recompute."""
+    b, L, H, P, N, G = cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups
+    es = 2 if cfg.dtype == torch.bfloat16 else 4
+    nbytes = (3 * b * L * H * P * es + 4 * b * L * G * N * es + 2 * b * L * H * 4
+              + b * H * P * N * 4 * (3 if cfg.init_state else 2))
+    nseg = -(-L // Q)
+    flops = b * nseg * (2 * Q * Q * N * G + H * (4 * Q * Q * P + 4 * Q * Q * N + 10 * Q * P * N))
     return nbytes, flops
 
 
@@ -126,6 +141,31 @@ def bench_ssd(cfg, steps, warmup, nsets, chunk=None):
     del plans
     torch.cuda.empty_cache()
     return res, wall, ev
+
+
+def bench_ssd_bwd(cfg, steps, warmup, nsets):
+    import mamformer_amd as mh
+    from mamformer_amd import workloads as W
+
+    plans = []
+    for i in range(nsets):
+        c = cfg.scaled(seed=cfg.seed + 1000 * i)
+        inp = W.ssd_inputs(c, device="cuda")
+        g = torch.Generator(device="cuda").manual_seed(c.seed + 7)
+        dy = torch.randn(inp["x"].shape, device="cuda", generator=g).to(inp["x"].dtype)
+        dfin = 0.1 * torch.randn((c.batch, c.nheads, c.headdim, c.dstate), device="cuda", generator=g)
+        plans.append(mh.plan_selective_scan_bwd(dy, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
+                                                d_final_state=dfin, initial_state=inp["initial_state"]))
+    wall, ev = time_plans(plans, steps, warmup)
+    nbytes, flops = ssd_bwd_alg(cfg)
+    t = ev * 1e-3
+    t_roof = max(nbytes / PEAK_HBM, flops / PEAK_BF16)
+    res = dict(mtok_s=cfg.batch * cfg.seqlen / t / 1e6, us_per_step=ev * 1e3, wall_us_per_step=wall * 1e3,
+               alg_bytes=nbytes, alg_flops=flops, hbm_GBs=nbytes / t / 1e9, tflops=flops / t / 1e12,
+               roofline_frac=t_roof / t)
+    del plans
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_decode(cfg, steps, warmup, nsets):
@@ -220,7 +260,7 @@ def measured_traffic(workload="ssd2"):
 
 # ----------------------------------------------------------------- main
 
-LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd1", "cpu")
+LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd2_bwd", "ssd1", "cpu")
 
 
 def main():
@@ -319,6 +359,10 @@ def main():
         tr = measured_traffic("kda5")
         if tr is not None:
             other["kda5"]["traffic"] = tr["bytes_per_launch"]
+    if "ssd2_bwd" in legs:
+        r = bench_ssd_bwd(cfg, max(10, args.steps // 2), 5, nsets=3)
+        log(f"ssd2 backward: {r['us_per_step']:.1f} us, {r['tflops']:.0f} TFLOP/s, roofline {r['roofline_frac']:.3f}")
+        other["ssd2_bwd"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
     if "ssd1" in legs:
         r, _, _ = bench_ssd(W.SSD1, args.steps, args.warmup, nsets=1, chunk=64)
         other["ssd1"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}

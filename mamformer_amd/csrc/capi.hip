@@ -270,10 +270,10 @@ int ssd_bwd_validate(const mh_ssd_bwd_args* a) {
   return MH_OK;
 }
 
-// Heads of one group per workgroup of the gradient kernel: the largest of 8, 4, 2, 1 dividing H / G.
+// Heads of one group per workgroup of the gradient kernel: the largest of 16, 8, 4, 2, 1 dividing H / G.
 int ssd_bwd_heads_per_wg(const mh_ssd_args* f) {
   const int64_t hpg = f->nheads / f->ngroups;
-  int hb = 8;
+  int hb = 16;
   while (hb > 1 && hpg % hb) hb >>= 1;
   return hb;
 }
@@ -390,8 +390,8 @@ int mh_ssd_bwd_workspace_bytes(const mh_ssd_bwd_args* a, size_t* bytes) {
   int rc = ssd_bwd_validate(a);
   if (rc) return rc;
   const mh_ssd_args* f = &a->fwd;
-  *bytes = mh::ssd_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->headdim,
-                                       (int)f->dstate, (int)f->ngroups, f->dtype);
+  *bytes = mh::ssd_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate,
+                                       (int)f->ngroups, f->dtype, ssd_bwd_heads_per_wg(f));
   return MH_OK;
 }
 
@@ -399,15 +399,15 @@ int mh_ssd_chunk_scan_bwd(const mh_ssd_bwd_args* a, void* stream) {
   int rc = ssd_bwd_validate(a);
   if (rc) return rc;
   const mh_ssd_args* f = &a->fwd;
-  const size_t need = mh::ssd_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->headdim,
-                                                  (int)f->dstate, (int)f->ngroups, f->dtype);
+  const size_t need = mh::ssd_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate,
+                                                  (int)f->ngroups, f->dtype, ssd_bwd_heads_per_wg(f));
   if (f->seqlen > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
     return fail(MH_ERR_WORKSPACE, "ssd_bwd: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
                 a->workspace_bytes);
   mh::SsdBwdParams q;
   memset(&q, 0, sizeof(q));
   const int64_t nseg = (f->seqlen + 63) / 64;
-  ssd_fill(f, 64, nseg, q.f);          // entering states per 64-token segment
+  ssd_fill(f, 64, nseg, q.f);
   q.f.y = nullptr;
   q.f.final_state = nullptr;
   q.f.z = nullptr;

@@ -65,7 +65,7 @@ hipError_t launch_ssd_states(const SsdParams& p, hipStream_t st);
 
 // ------------------------------------------------------------- SSD prefill backward
 struct SsdBwdParams {
-  SsdParams f;               // forward sizes and inputs; chunk_len = 64 (one segment per chunk), workspace laid out
+  SsdParams f;               // forward sizes and inputs (no forward workspace)
   const void* dy; int64_t dy_sb, dy_sl, dy_sh;
   const float* d_final;      // (b, H, P, N) fp32 or null
   void* dx; int64_t dx_sb, dx_sl, dx_sh;
@@ -76,13 +76,15 @@ struct SsdBwdParams {
   float* dh0;                // (b, H, P, N) or null
   void* dB; int64_t dB_sb, dB_sl;
   void* dC; int64_t dC_sb, dC_sl;
-  float* dB_acc;             // workspace: (b, L, G, N) fp32 sums over the heads of a group
-  float* dC_acc;
-  void* lam;                 // workspace: per-segment adjoint of the state leaving the segment, states' order
-  int heads_per_wg;          // heads of one group handled by a workgroup of the gradient kernel
+  float* dB_part;            // workspace: per head block of a group, (b, L, G, N) fp32 sums over its heads
+  float* dC_part;
+  void* hin;                 // workspace: state entering every 64-token segment, (b, nseg, H) x fragment order
+  void* lam;                 // workspace: adjoint of the state leaving every segment, same layout
+  int heads_per_wg;          // heads of one group handled by a workgroup of the gradient kernel (HB)
 };
 hipError_t launch_ssd_bwd(const SsdBwdParams& p, hipStream_t st);
-size_t ssd_bwd_workspace_bytes(int batch, int seqlen, int nheads, int headdim, int dstate, int ngroups, int dtype);
+size_t ssd_bwd_workspace_bytes(int batch, int seqlen, int nheads, int dstate, int ngroups, int dtype,
+                               int heads_per_wg);
 void ssd_bwd_workspace_layout(SsdBwdParams& p, void* workspace);
 
 // ------------------------------------------------------------- KDA

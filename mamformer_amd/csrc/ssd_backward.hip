@@ -20,17 +20,19 @@
 //     ddt_tau = colG_tau + bint_tau + A da_tau,    dA = sum_tau dt_tau da_tau,    dD = sum dy . x.
 //
 // Launches (caller's stream):
-//   0. ssd_bwd_zero      clears the fp32 accumulators (a kernel, not a memset node).
-//   1. prefill kernels 0-2 at chunk length 64: the entering state h_in of every segment (workspace).
-//   2. ssd_bwd_lambda    grid (2, H, b): one workgroup per (b, h, 32-column half of P) walks the segments
-//      from last to first with lam in MFMA accumulators, stores lam_out of every segment (workspace, the
-//      entering states' fragment order) and finally dh0.  lam <- e^{c_end} lam + sum_t e^{c_t} C_t^T dy_t.
-//   3. ssd_bwd_grad      grid (nseg, H / HB, b): one workgroup per (segment, block of HB heads of a group),
+//   0. ssd_bwd_zero      clears dA, dD, d_dt_bias (a kernel, not a memset node).
+//   1. ssd_bwd_sweep     grid (2 directions x 2 halves of P, H, b): the forward direction walks the segments
+//      first to last and stores the entering state h_in of every 64-token segment; the adjoint direction walks
+//      them last to first, stores lam_out of every segment and finally dh0
+//      (lam <- e^{c_end} lam + sum_t e^{c_t} C_t^T dy_t).  Both into the workspace, fragment-native order.
+//   2. ssd_bwd_grad      grid (nseg, H / HB, b): one workgroup per (segment, block of HB heads of a group),
 //      fully parallel; dx and ddt stored directly, dB / dC summed over the block's heads in registers and
-//      added to fp32 accumulators with hardware float atomics, dA / dD / dt_bias likewise.
-//   4. ssd_bwd_convert   accumulators -> dB, dC in the I/O dtype and the caller's strides.
+//      stored as one fp32 partial per head block; dA / dD / dt_bias with float atomics.
+//   3. ssd_bwd_reduce    partials -> dB, dC (fixed summation order) in the I/O dtype and the caller's strides.
 // Token-contracted products take their transposed operands from the MFMA unit (identity products), as in
 // the forward; all accumulation is fp32.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 #include "ssd_shared.h"
@@ -176,6 +178,7 @@ struct ZeroRanges {
   float* p[5];
   int64_t n[5];
 };
+// (dA, dD and d_dt_bias are sums of float atomics over the segment workgroups)
 __global__ __launch_bounds__(256) void ssd_bwd_zero_kernel(ZeroRanges z) {
   const int r = blockIdx.y;
   float* p = z.p[r];
@@ -191,97 +194,123 @@ __global__ __launch_bounds__(256) void ssd_bwd_copy_kernel(const float* __restri
   if (i < n) dst[i] = src ? src[i] : 0.f;
 }
 
-// ------------------------------------------------------------------ kernel 2: adjoint sweep
+// ------------------------------------------------------------------ kernel 1: state sweeps
 
 template <typename T, int N>
-struct LamStage {
-  T C[SEG * N];             // Tile<T, N>
-  T DY[SEG * 32];           // XHalf<T>: the workgroup's 32 columns of dy
+struct SweepStage {
+  T M[SEG * N];             // Tile<T, N>: B (forward sweep) or C (adjoint sweep)
+  T V[SEG * 32];            // XHalf<T>: the workgroup's 32 columns of x (forward) or dy (adjoint)
   float dtraw[SEG];
 };
+constexpr int SWEEP_NST = 3;     // stages: segments fetched two ahead
 template <typename T, int N>
-struct LamSmem {
-  LamStage<T, N> st[2];
-  float ec[N / 32][SEG];    // per wave: e^{c_t} (0 past the end)
+struct SweepSmem {
+  SweepStage<T, N> st[SWEEP_NST];
+  float w[N / 32][SEG];     // per wave: per-token weight of the segment
 };
 
+// One workgroup per (direction, 32-column half pt of P, head, batch); compute wave nt owns state tile (nt, pt),
+// and one more wave only fetches: it keeps two segments in flight (global -> LDS) and waits for them with
+// exact counts, which the compute waves, whose state stores share the same counter, could not.
+//   forward (dir 0): S = h, segments first to last, weights w_s = e^{c_end - c_s} dt_s on B^T x:
+//       stores the entering state of every segment, S <- e^{c_end} S + sum_s B_s^T w_s x_s
+//   adjoint (dir 1): S = lam, segments last to first, weights w_t = e^{c_t} on C^T dy:
+//       stores lam_out of every segment, S <- e^{c_end} S + sum_t C_t^T w_t dy_t, finally dh0 = S.
+// Both directions run in one launch (independent workgroups).
 template <typename T, int N>
-__global__ __launch_bounds__(64 * (N / 32)) void ssd_bwd_lambda_kernel(SsdBwdParams q) {
+__global__ __launch_bounds__(64 * (N / 32 + 1)) void ssd_bwd_sweep_kernel(SsdBwdParams q) {
   constexpr int NB = N / 32;
-  __shared__ LamSmem<T, N> sm;
+  using TM_ = Tile<T, N>;
+  using TV = XHalf<T>;
+  constexpr int DMA_PER_STAGE = TM_::NBLK + TV::NBLK + 1;
+  __shared__ SweepSmem<T, N> sm;
   const SsdParams& p = q.f;
-  const int pt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int dir = blockIdx.x >> 1, pt = blockIdx.x & 1, h = blockIdx.y, b = blockIdx.z;
   const int g = h / (p.nheads / p.ngroups);
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
+  const int nseg = p.nseg;
+  auto seg_of = [&](int i) { return dir ? nseg - 1 - i : i; };
+  if (w == NB) {
+    // ---- loader wave
+    const T* Mb = reinterpret_cast<const T*>(dir ? p.C : p.B) + (int64_t)b * (dir ? p.C_sb : p.B_sb) + g * N;
+    const int64_t M_sl = dir ? p.C_sl : p.B_sl;
+    const T* Vb = dir ? reinterpret_cast<const T*>(q.dy) + (int64_t)b * q.dy_sb + (int64_t)h * q.dy_sh + 32 * pt
+                      : reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + 32 * pt;
+    const int64_t V_sl = dir ? q.dy_sl : p.x_sl;
+    const float* dtb = p.dt + (int64_t)b * p.dt_sb + h;
+    auto issue = [&](int i) {
+      const int k = seg_of(i), s = i % SWEEP_NST;
+      const int t0 = k * SEG, lst = min(t0 + SEG, p.seqlen) - 1;
+      fetch_tile<T, N>(sm.st[s].M, Mb, M_sl, t0, lst, 0, TM_::NBLK, l);
+      fetch_xhalf<T>(sm.st[s].V, Vb, V_sl, t0, lst, l);
+      fetch_dt(sm.st[s].dtraw, dtb, p.dt_sl, t0, lst, l);
+    };
+    issue(0);
+    if (nseg > 1) issue(1);
+    for (int i = 0; i < nseg; ++i) {
+      if (i + 1 < nseg) wait_vmem_n<DMA_PER_STAGE>();   // stage i landed (only stage i + 1 may be in flight)
+      else wait_vmem();
+      lds_barrier();                                     // publish stage i; iteration i - 1 is done everywhere
+      if (i + 2 < nseg) issue(i + 2);                    // into the stage iteration i - 1 read
+    }
+    return;
+  }
+  // ---- compute waves
   const int nt = w;
   const float Ah = p.A[h], bias = p.dt_bias ? p.dt_bias[h] : 0.f;
   Frag<T> id[2];
 #pragma unroll
   for (int c = 0; c < 2; ++c) id[c] = ident_frag<T>(c, half, l32);
   const int64_t per = (int64_t)HD * N;
-  // lam leaving the last segment = d_final, canonical (p, n) -> block (nt, pt)
-  f32x16 lam = zero16();
-  if (q.d_final) {
-    const float* src = q.d_final + ((int64_t)b * p.nheads + h) * per + (32 * pt + l32) * N + 32 * nt;
+  // initial state, canonical (p, n) -> block (nt, pt): h0 (forward) or d_final (adjoint)
+  const float* s0 = dir ? q.d_final : p.init_state;
+  f32x16 S = zero16();
+  if (s0) {
+    const float* src = s0 + ((int64_t)b * p.nheads + h) * per + (32 * pt + l32) * N + 32 * nt;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const f32x4 v = *reinterpret_cast<const f32x4*>(src + 8 * jj + 4 * half);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) lam[4 * jj + k] = v[k];
+      for (int k = 0; k < 4; ++k) S[4 * jj + k] = v[k];
     }
   }
-  const T* Cb = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb + g * N;
-  const T* dyb = reinterpret_cast<const T*>(q.dy) + (int64_t)b * q.dy_sb + (int64_t)h * q.dy_sh + 32 * pt;
-  const float* dtb = p.dt + (int64_t)b * p.dt_sb + h;
-  auto issue = [&](int k, int s) {
-    const int t0 = k * SEG, lst = min(t0 + SEG, p.seqlen) - 1;
-    constexpr int nblk = Tile<T, N>::NBLK / NB;
-    fetch_tile<T, N>(sm.st[s].C, Cb, p.C_sl, t0, lst, w * nblk, nblk, l);
-    if (w == 0) {
-      fetch_xhalf<T>(sm.st[s].DY, dyb, q.dy_sl, t0, lst, l);
-      fetch_dt(sm.st[s].dtraw, dtb, p.dt_sl, t0, lst, l);
-    }
-  };
-  T* lam_ws = reinterpret_cast<T*>(q.lam);
-  const int nseg = p.nseg;
-  issue(nseg - 1, (nseg - 1) & 1);
-  for (int k = nseg - 1; k >= 0; --k) {
-    const int s = k & 1;
-    wait_vmem();
+  T* out = reinterpret_cast<T*>(dir ? q.lam : q.hin);
+  for (int i = 0; i < nseg; ++i) {
+    const int k = seg_of(i), s = i % SWEEP_NST;
+    // the state entering segment k (forward) / leaving it (adjoint), stored before the update
+    store_state_blk<T>(out + (((int64_t)b * nseg + k) * p.nheads + h) * per, nt, pt, l, S);
     lds_barrier();
-    if (k > 0) issue(k - 1, s ^ 1);
-    store_state_blk<T>(lam_ws + (((int64_t)b * nseg + k) * p.nheads + h) * per, nt, pt, l, lam);
     const int len = min(SEG, p.seqlen - k * SEG);
     float dtv;
     const float cs = seg_decay(p, sm.st[s].dtraw[l], bias, Ah, l, len, dtv);
     const float cend = __shfl(cs, 63);
-    sm.ec[w][l] = (l < len) ? __expf(cs) : 0.f;
+    sm.w[w][l] = dir ? ((l < len) ? __expf(cs) : 0.f) : __expf(cend - cs) * dtv;
     f32x16 acc = zero16();
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
-      const f32x16 ct = mfma_transpose<T, T, N>(sm.st[s].C, 32 * tb, 32 * nt, id, half, l32);   // [t][n]
-      const f32x16 dt_ = xhalf_transpose<T>(sm.st[s].DY, 32 * tb, id, half, l32);              // [t][p]
+      const f32x16 mt = mfma_transpose<T, T, N>(sm.st[s].M, 32 * tb, 32 * nt, id, half, l32);   // [t][n]
+      const f32x16 vt = xhalf_transpose<T>(sm.st[s].V, 32 * tb, id, half, l32);                // [t][p]
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         float e[8];
-        kset_vals(sm.ec[w], 2 * tb + c, half, e);
+        kset_vals(sm.w[w], 2 * tb + c, half, e);
         Frag<T> a;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a.set(j, ct[8 * c + j] * e[j]);
-        acc = mma(a, acc_to_frag<T>(dt_, c), acc);       // [n][p] += sum_t C[t][n] e^{c_t} dy[t][p]
+        for (int j = 0; j < 8; ++j) a.set(j, mt[8 * c + j] * e[j]);
+        acc = mma(a, acc_to_frag<T>(vt, c), acc);       // [n][p] += sum_t M[t][n] w_t V[t][p]
       }
     }
     const float dec = __expf(cend);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) lam[i] = dec * lam[i] + acc[i];
+    for (int j = 0; j < 16; ++j) S[j] = dec * S[j] + acc[j];
   }
-  if (q.dh0) {
+  if (dir && q.dh0) {
     float* dst = q.dh0 + ((int64_t)b * p.nheads + h) * per + (32 * pt + l32) * N + 32 * nt;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       f32x4 v;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) v[k] = lam[4 * jj + k];
+      for (int k = 0; k < 4; ++k) v[k] = S[4 * jj + k];
       *reinterpret_cast<f32x4*>(dst + 8 * jj + 4 * half) = v;
     }
   }
@@ -289,13 +318,22 @@ __global__ __launch_bounds__(64 * (N / 32)) void ssd_bwd_lambda_kernel(SsdBwdPar
 
 // ------------------------------------------------------------------ kernel 3: gradients per segment
 
-template <typename T, int N>
-struct GradSmem {
-  T B[SEG * N];             // Tile<T, N>
-  T C[SEG * N];
-  T X[SEG * HD];            // Tile<T, HD> of the current head
+template <typename T, int N, bool SL>
+struct GradStage {
+  T X[SEG * HD];            // Tile<T, HD> of the head
   T DY[SEG * HD];
   float dtraw[SEG];
+};
+template <typename T, int N>
+struct GradStage<T, N, true> : GradStage<T, N, false> {
+  T Lam[HD * N];            // lam_out and h_in of the head, fragment-native order (as in the workspaces)
+  T Hin[HD * N];
+};
+template <typename T, int N, int NST, bool SL>
+struct GradSmem {
+  GradStage<T, N, SL> st[NST];
+  T B[SEG * N];             // Tile<T, N>
+  T C[SEG * N];
   float cs[2 * (N / 32)][SEG];   // per wave: c_t of the current head
   float dtp[2 * (N / 32)][SEG];  // per wave: processed dt
   float red[2][N / 32][SEG];     // per n-block partial dots: bint, u
@@ -307,6 +345,13 @@ struct GradSmem {
   float cb[3][64 * 16];          // CB[t][s] tiles (t-block, s-block) = (0,0), (1,0), (1,1), accumulator order
   float cbt[3][64 * 16];         // CB^T[s][t] tiles (s-block, t-block) = (0,0), (0,1), (1,1)
 };
+constexpr size_t GRAD_LDS = 160 * 1024;
+// The states of a head are staged in LDS with its tiles where they fit (else read from HBM where used), and
+// the per-head stages are double-buffered (the next head's fetch overlaps this head's work) where two fit.
+template <typename T, int N>
+constexpr bool grad_sl = sizeof(GradSmem<T, N, 1, true>) <= GRAD_LDS;
+template <typename T, int N>
+constexpr int grad_nst = sizeof(GradSmem<T, N, 2, grad_sl<T, N>>) <= GRAD_LDS ? 2 : 1;
 
 // Work split (NW = 2 N/32 waves): wave w owns n-block nb = w % (N/32) and token block r = w / (N/32) of the
 // dB^T [n][s] and dC^T [n][t] tiles; waves 0-3 also own the dx^T [p][s] tile (p-block w & 1, s-block w >> 1).
@@ -315,12 +360,15 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
   constexpr int NB = N / 32, NW = 2 * NB;
   using TB = Tile<T, N>;
   using TX = Tile<T, HD>;
-  __shared__ GradSmem<T, N> sm;
+  constexpr bool SL = grad_sl<T, N>;
+  constexpr int NST = grad_nst<T, N>;
+  __shared__ GradSmem<T, N, NST, SL> sm;
   const SsdParams& p = q.f;
   const int si = blockIdx.x, b = blockIdx.z;
   const int HB = q.heads_per_wg;
   const int hfirst = blockIdx.y * HB;
-  const int g = hfirst / (p.nheads / p.ngroups);
+  const int hpg = p.nheads / p.ngroups;
+  const int g = hfirst / hpg;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
   const int nb = w % NB, r = w / NB;
   const bool dxw = w < 4;
@@ -342,17 +390,28 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
     fetch_tile<T, N>(sm.C, reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb + g * N, p.C_sl, tok0, last,
                      w * nblk, nblk, l);
   }
-  auto fetch_head = [&](int h) {
+  const char* hin_ws = reinterpret_cast<const char*>(q.hin);
+  const char* lam_ws = reinterpret_cast<const char*>(q.lam);
+  // one head's tiles, dt and both states (contiguous HD x N blocks of the workspaces) into stage st
+  auto fetch_head = [&](int h, auto stc) {
+    constexpr int st = decltype(stc)::value;
+    // lane offsets computed here from a laundered lane id: hoisted out of the head loop, the per-lane
+    // addresses would be spilled, and reloading them drains the vector-memory counter before every fetch
+    int l = lane_id();
+    asm volatile("" : "+v"(l));
     constexpr int nblk = TX::NBLK / NW;
-    fetch_tile<T, HD>(sm.X, xb + (int64_t)h * p.x_sh, p.x_sl, tok0, last, w * nblk, nblk, l);
-    fetch_tile<T, HD>(sm.DY, dyb + (int64_t)h * q.dy_sh, q.dy_sl, tok0, last, w * nblk, nblk, l);
-    if (w == 0) fetch_dt(sm.dtraw, dtb + h, p.dt_sl, tok0, last, l);
+    fetch_tile<T, HD>(sm.st[st].X, xb + (int64_t)h * p.x_sh, p.x_sl, tok0, last, w * nblk, nblk, l);
+    fetch_tile<T, HD>(sm.st[st].DY, dyb + (int64_t)h * q.dy_sh, q.dy_sl, tok0, last, w * nblk, nblk, l);
+    if constexpr (SL) {
+      constexpr int sblk = HD * N * (int)sizeof(T) / 1024 / NW;
+      const int64_t soff = (((int64_t)b * p.nseg + si) * p.nheads + h) * per * (int64_t)sizeof(T);
+      fetch_blocks(reinterpret_cast<char*>(sm.st[st].Lam), lam_ws + soff, w * sblk, sblk, l);
+      fetch_blocks(reinterpret_cast<char*>(sm.st[st].Hin), hin_ws + soff, w * sblk, sblk, l);
+    }
+    if (w == 0) fetch_dt(sm.st[st].dtraw, dtb + h, p.dt_sl, tok0, last, l);
   };
-  fetch_head(hfirst);
+  fetch_head(hfirst, std::integral_constant<int, 0>());
   if (w == 0) sm.ddp[l] = 0.f;
-
-  const T* hin_ws = reinterpret_cast<const T*>(p.dtype == DT_BF16 ? p.entering : (void*)p.chunk_states);
-  const T* lam_ws = reinterpret_cast<const T*>(q.lam);
   f32x16 dBacc = zero16(), dCacc = zero16();
 
   wait_vmem();                      // B / C tiles (and the first head's tiles) in LDS
@@ -399,7 +458,12 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       }
     }
   }
-  for (int j = 0; j < HB; ++j) {
+  lds_barrier();                    // CB tiles visible
+  // One head: its stage index is a compile-time constant (the loop below is unrolled by two), so the compiler
+  // sees that the next head's fetch and this head's LDS reads touch different bytes (with a run-time index it
+  // orders every LDS access after the pending fetch).
+  auto head = [&](const int j, auto stc) {
+    constexpr int st = decltype(stc)::value;
     // Lane-derived values are recomputed per head from a laundered lane id (and length): otherwise the
     // compiler keeps dozens of loop-invariant row indices and masks in registers across the head loop.
     int lq = l, lenq = len;
@@ -414,19 +478,26 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       idk[c] = ident_kset<T>(c, half, l32);
     }
     const int h = hfirst + j;
+    auto& sg = sm.st[st];
     const int64_t sidx = (((int64_t)b * p.nseg + si) * p.nheads + h) * per;
+    auto lam_src = [&]() -> const T* {
+      if constexpr (SL) return sg.Lam;
+      else return reinterpret_cast<const T*>(lam_ws) + sidx;
+    };
+    auto hin_src = [&]() -> const T* {
+      if constexpr (SL) return sg.Hin;
+      else return reinterpret_cast<const T*>(hin_ws) + sidx;
+    };
     StateBlk<T> Lb[2], Hb[2];
 #pragma unroll
     for (int pt = 0; pt < 2; ++pt) {
-      Lb[pt] = load_state_blk<T>(lam_ws + sidx, nb, pt, l);
-      Hb[pt] = load_state_blk<T>(hin_ws + sidx, nb, pt, l);
+      Lb[pt] = load_state_blk<T>(lam_src(), nb, pt, l);
+      Hb[pt] = load_state_blk<T>(hin_src(), nb, pt, l);
     }
-    wait_vmem();
-    lds_barrier();
     // ---- decay of this head (lane = token), wave-private copies for per-row reads
     const float Ah = p.A[h];
     const float bias = p.dt_bias ? p.dt_bias[h] : 0.f;
-    const float raw = sm.dtraw[l];
+    const float raw = sg.dtraw[l];
     float dtv;
     const float cs = seg_decay(p, raw, bias, Ah, l, len, dtv);
     const float cend = __shfl(cs, 63);
@@ -447,8 +518,8 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       if (tb >= r) {
 #pragma unroll
         for (int k = 0; k < HD / 16; ++k)
-          a = mma(row_frag<T, T, HD>(sm.DY, 32 * tb + l32, 16 * k + 8 * half),
-                  row_frag<T, T, HD>(sm.X, s_l, 16 * k + 8 * half), a);
+          a = mma(row_frag<T, T, HD>(sg.DY, 32 * tb + l32, 16 * k + 8 * half),
+                  row_frag<T, T, HD>(sg.X, s_l, 16 * k + 8 * half), a);
         float ct[16];
         acc_rows(sm.cs[w], 32 * tb, half, ct);
         float d = 0.f;
@@ -492,7 +563,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       for (int pt = 0; pt < 2; ++pt)
 #pragma unroll
         for (int c = 0; c < 2; ++c)
-          ai = mma(lamT[pt][c], scaled<T>(kset_frag<T, T, HD>(sm.X, s_l, 32 * pt + 16 * c, half), wend_l), ai);
+          ai = mma(lamT[pt][c], scaled<T>(kset_frag<T, T, HD>(sg.X, s_l, 32 * pt + 16 * c, half), wend_l), ai);
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb) {
         if (tb >= r) {
@@ -522,8 +593,8 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       if (sb <= r) {
 #pragma unroll
         for (int k = 0; k < HD / 16; ++k)
-          a = mma(row_frag<T, T, HD>(sm.X, 32 * sb + l32, 16 * k + 8 * half),
-                  row_frag<T, T, HD>(sm.DY, s_l, 16 * k + 8 * half), a);
+          a = mma(row_frag<T, T, HD>(sg.X, 32 * sb + l32, 16 * k + 8 * half),
+                  row_frag<T, T, HD>(sg.DY, s_l, 16 * k + 8 * half), a);
         float cr[16], dr[16];
         acc_rows(sm.cs[w], 32 * sb, half, cr);
         acc_rows(sm.dtp[w], 32 * sb, half, dr);
@@ -572,7 +643,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       for (int pt = 0; pt < 2; ++pt)
 #pragma unroll
         for (int c = 0; c < 2; ++c)
-          ah = mma(hT[pt][c], scaled<T>(kset_frag<T, T, HD>(sm.DY, s_l, 32 * pt + 16 * c, half), ec_l), ah);
+          ah = mma(hT[pt][c], scaled<T>(kset_frag<T, T, HD>(sg.DY, s_l, 32 * pt + 16 * c, half), ec_l), ah);
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         if (sb <= r) {
@@ -616,20 +687,20 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
             const int t = 32 * tb + acc_row(half, i);
             m[i] = (t < len && t >= s_x) ? m[i] * __expf(ct[i] - csx) : 0.f;
           }
-          const f32x16 dyt = mfma_transpose<T, T, HD>(sm.DY, 32 * tb, 32 * pb, id, half, l32);   // [t][p]
+          const f32x16 dyt = mfma_transpose<T, T, HD>(sg.DY, 32 * tb, 32 * pb, id, half, l32);   // [t][p]
 #pragma unroll
           for (int c = 0; c < 2; ++c) ax = mma(acc_to_frag<T>(dyt, c), acc_to_frag<T>(m, c), ax);
         }
       }
 #pragma unroll
       for (int nt = 0; nt < NB; ++nt) {
-        const StateBlk<T> lx = load_state_blk<T>(lam_ws + sidx, nt, pb, l);
+        const StateBlk<T> lx = load_state_blk<T>(lam_src(), nt, pb, l);
 #pragma unroll
         for (int c = 0; c < 2; ++c)
           ax = mma(lx.frag(c), scaled<T>(kset_frag<T, T, N>(sm.B, s_x, 32 * nt + 16 * c, half), wx), ax);
       }
       float dyv[16];
-      acc_cols<T, HD>(sm.DY, s_x, 32 * pb, half, dyv);
+      acc_cols<T, HD>(sg.DY, s_x, 32 * pb, half, dyv);
       float Dv[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i)
@@ -654,14 +725,18 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       }
       if (p.D_per_channel && q.dD && s_x < len) {
         float xv[16];
-        acc_cols<T, HD>(sm.X, s_x, 32 * pb, half, xv);
+        acc_cols<T, HD>(sg.X, s_x, 32 * pb, half, xv);
 #pragma unroll
         for (int i = 0; i < 16; ++i) atomicAdd(&sm.ddp[32 * pb + acc_row(half, i)], xv[i] * dyv[i]);
       }
     }
 
-    lds_barrier();                     // partial dots complete; X / DY / dt free for the next head
-    if (j + 1 < HB) fetch_head(h + 1);
+    // The next head's fetch: into the other stage (head j - 1's, read by nobody since the last barrier) before
+    // the barrier, or, with one stage, after it.  It is issued late on purpose: a spill reload in the work above
+    // would wait for it (the vector-memory counter is shared).
+    if (NST == 2 && j + 1 < HB) fetch_head(h + 1, std::integral_constant<int, st ^ 1>());
+    lds_barrier();                     // partial dots complete; with one stage, X / DY / dt free for the next head
+    if (NST == 1 && j + 1 < HB) fetch_head(h + 1, std::integral_constant<int, 0>());
     if (w == 0) {
       const float colG = sm.colg[l], rowG = sm.rowg[l];
       float bint = 0.f, u = 0.f, lh = 0.f;
@@ -692,30 +767,56 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
         sm.ddp[l] = 0.f;
       }
     }
+    if (j + 1 < HB) {
+      wait_vmem();                     // the next head's stage (and this head's stores)
+      lds_barrier();
+    }
+  };
+  for (int j = 0; j < HB; j += NST) {
+    head(j, std::integral_constant<int, 0>());
+    if constexpr (NST == 2) {
+      if (j + 1 < HB) head(j + 1, std::integral_constant<int, 1>());
+    }
   }
-  // group sums of this block's heads -> fp32 accumulators (b, L, G, N)
+
+  // sums over this block's heads -> partial kb of the group: fp32 (b, L, G, N), plain stores (the partials of a
+  // group's head blocks are added in a fixed order afterwards: no atomics, run-to-run identical results)
   if (s_l < len) {
-    const int64_t row = (((int64_t)b * p.seqlen + tok0 + s_l) * p.ngroups + g) * N + 32 * nb;
+    const int kb = (hfirst % hpg) / HB;
+    const int64_t row = ((((int64_t)kb * p.batch + b) * p.seqlen + tok0 + s_l) * p.ngroups + g) * N + 32 * nb;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      unsafeAtomicAdd(q.dB_acc + row + acc_row(half, i), dBacc[i]);
-      unsafeAtomicAdd(q.dC_acc + row + acc_row(half, i), dCacc[i]);
+    for (int jj = 0; jj < 4; ++jj) {
+      f32x4 vb, vc;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        vb[k] = dBacc[4 * jj + k];
+        vc[k] = dCacc[4 * jj + k];
+      }
+      *reinterpret_cast<f32x4*>(q.dB_part + row + 8 * jj + 4 * half) = vb;
+      *reinterpret_cast<f32x4*>(q.dC_part + row + 8 * jj + 4 * half) = vc;
     }
   }
 }
 
-// ------------------------------------------------------------------ kernel 4: accumulators -> dB, dC
+// ------------------------------------------------------------------ kernel 3: partials -> dB, dC
 
+// out[b, t, g, n] = sum over the nparts head-block partials (fixed order), in the I/O dtype and the caller's strides.
 template <typename T>
-__global__ __launch_bounds__(256) void ssd_bwd_convert_kernel(const float* __restrict__ acc, void* out, int64_t sb,
-                                                              int64_t sl, int L, int GN, int64_t n4) {
+__global__ __launch_bounds__(256) void ssd_bwd_reduce_kernel(const float* __restrict__ part, int nparts,
+                                                             void* out, int64_t sb, int64_t sl, int L, int GN,
+                                                             int64_t n4) {
   const int64_t i4 = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i4 >= n4) return;
   const int64_t e = i4 * 4;
+  f32x4 v = *reinterpret_cast<const f32x4*>(part + e);
+  for (int k = 1; k < nparts; ++k) {
+    const f32x4 u = *reinterpret_cast<const f32x4*>(part + (int64_t)k * n4 * 4 + e);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] += u[j];
+  }
   const int64_t row = e / GN;
   const int col = (int)(e - row * GN);
   const int64_t bb = row / L, t = row - bb * L;
-  const f32x4 v = *reinterpret_cast<const f32x4*>(acc + e);
   T* o = reinterpret_cast<T*>(out) + bb * sb + t * sl + col;
   if constexpr (sizeof(T) == 2) {
     bf16x4 u;
@@ -730,41 +831,43 @@ __global__ __launch_bounds__(256) void ssd_bwd_convert_kernel(const float* __res
 // ------------------------------------------------------------------ host side
 
 struct BwdWorkspace {
-  size_t fwd, lam, acc;
-  size_t total() const { return align256(fwd) + align256(lam) + 2 * align256(acc); }
+  size_t states, part;
+  size_t total() const { return 2 * align256(states) + 2 * align256(part); }
 };
-static BwdWorkspace bwd_workspace(int batch, int seqlen, int nheads, int headdim, int dstate, int ngroups, int dtype) {
+static BwdWorkspace bwd_workspace(int batch, int seqlen, int nheads, int dstate, int ngroups, int dtype,
+                                  int heads_per_wg) {
   const int nseg = (seqlen + SEG - 1) / SEG;
+  const int nparts = (nheads / ngroups) / heads_per_wg;
   BwdWorkspace w;
-  w.fwd = ssd_workspace_bytes(batch, seqlen, nseg, nheads, headdim, dstate, ngroups, dtype);
-  w.lam = (size_t)batch * nseg * nheads * headdim * dstate * (dtype == DT_BF16 ? sizeof(bf16) : sizeof(float));
-  w.acc = (size_t)batch * seqlen * ngroups * dstate * sizeof(float);
+  w.states = (size_t)batch * nseg * nheads * HD * dstate * (dtype == DT_BF16 ? sizeof(bf16) : sizeof(float));
+  w.part = (size_t)nparts * batch * seqlen * ngroups * dstate * sizeof(float);
   return w;
 }
 
-size_t ssd_bwd_workspace_bytes(int batch, int seqlen, int nheads, int headdim, int dstate, int ngroups, int dtype) {
-  return bwd_workspace(batch, seqlen, nheads, headdim, dstate, ngroups, dtype).total();
+size_t ssd_bwd_workspace_bytes(int batch, int seqlen, int nheads, int dstate, int ngroups, int dtype,
+                               int heads_per_wg) {
+  return bwd_workspace(batch, seqlen, nheads, dstate, ngroups, dtype, heads_per_wg).total();
 }
 
 void ssd_bwd_workspace_layout(SsdBwdParams& q, void* workspace) {
-  SsdParams& p = q.f;
-  const BwdWorkspace w = bwd_workspace(p.batch, p.seqlen, p.nheads, p.headdim, p.dstate, p.ngroups, p.dtype);
+  const SsdParams& p = q.f;
+  const BwdWorkspace w = bwd_workspace(p.batch, p.seqlen, p.nheads, p.dstate, p.ngroups, p.dtype, q.heads_per_wg);
   char* c = reinterpret_cast<char*>(workspace);
-  ssd_workspace_layout(p, c);
-  c += align256(w.fwd);
+  q.hin = c;
+  c += align256(w.states);
   q.lam = c;
-  c += align256(w.lam);
-  q.dB_acc = reinterpret_cast<float*>(c);
-  c += align256(w.acc);
-  q.dC_acc = reinterpret_cast<float*>(c);
+  c += align256(w.states);
+  q.dB_part = reinterpret_cast<float*>(c);
+  c += align256(w.part);
+  q.dC_part = reinterpret_cast<float*>(c);
 }
 
 template <typename T, int N>
 static hipError_t launch_bwd_t(const SsdBwdParams& q, hipStream_t st) {
   const SsdParams& p = q.f;
   constexpr int NB = N / 32;
-  hipLaunchKernelGGL((ssd_bwd_lambda_kernel<T, N>), dim3(2, (unsigned)p.nheads, (unsigned)p.batch), dim3(64 * NB), 0,
-                     st, q);
+  hipLaunchKernelGGL((ssd_bwd_sweep_kernel<T, N>), dim3(4, (unsigned)p.nheads, (unsigned)p.batch),
+                     dim3(64 * (NB + 1)), 0, st, q);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_bwd_grad_kernel<T, N>),
@@ -773,44 +876,34 @@ static hipError_t launch_bwd_t(const SsdBwdParams& q, hipStream_t st) {
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int GN = p.ngroups * N;
+  const int nparts = (p.nheads / p.ngroups) / q.heads_per_wg;
   const int64_t n4 = (int64_t)p.batch * p.seqlen * GN / 4;
   const unsigned nblk = (unsigned)((n4 + 255) / 256);
-  hipLaunchKernelGGL((ssd_bwd_convert_kernel<T>), dim3(nblk), dim3(256), 0, st, q.dB_acc, q.dB, q.dB_sb, q.dB_sl,
-                     p.seqlen, GN, n4);
+  hipLaunchKernelGGL((ssd_bwd_reduce_kernel<T>), dim3(nblk), dim3(256), 0, st, q.dB_part, nparts, q.dB, q.dB_sb,
+                     q.dB_sl, p.seqlen, GN, n4);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((ssd_bwd_convert_kernel<T>), dim3(nblk), dim3(256), 0, st, q.dC_acc, q.dC, q.dC_sb, q.dC_sl,
-                     p.seqlen, GN, n4);
+  hipLaunchKernelGGL((ssd_bwd_reduce_kernel<T>), dim3(nblk), dim3(256), 0, st, q.dC_part, nparts, q.dC, q.dC_sb,
+                     q.dC_sl, p.seqlen, GN, n4);
   return hipGetLastError();
 }
 
 hipError_t launch_ssd_bwd(const SsdBwdParams& q, hipStream_t st) {
   const SsdParams& p = q.f;
   ZeroRanges z;
-  z.p[0] = q.dB_acc;  z.n[0] = (int64_t)p.batch * p.seqlen * p.ngroups * p.dstate;
-  z.p[1] = q.dC_acc;  z.n[1] = z.n[0];
-  z.p[2] = q.dA;      z.n[2] = p.nheads;
-  z.p[3] = q.dD;      z.n[3] = p.D_per_channel ? (int64_t)p.nheads * HD : p.nheads;
-  z.p[4] = q.dbias;   z.n[4] = p.nheads;
-  if (p.nseg == 0) { z.p[0] = nullptr; z.p[1] = nullptr; }
-  int64_t most = 0;
-  for (int i = 0; i < 5; ++i)
-    if (z.p[i] && z.n[i] > most) most = z.n[i];
-  if (most > 0) {
-    const int64_t nb256 = (most + 255) / 256;
-    const unsigned gx = (unsigned)(nb256 < 4096 ? nb256 : 4096);
-    hipLaunchKernelGGL(ssd_bwd_zero_kernel, dim3(gx, 5), dim3(256), 0, st, z);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
+  for (int i = 0; i < 5; ++i) { z.p[i] = nullptr; z.n[i] = 0; }
+  z.p[0] = q.dA;      z.n[0] = p.nheads;
+  z.p[1] = q.dD;      z.n[1] = p.D_per_channel ? (int64_t)p.nheads * HD : p.nheads;
+  z.p[2] = q.dbias;   z.n[2] = p.nheads;
+  hipLaunchKernelGGL(ssd_bwd_zero_kernel, dim3(1, 3), dim3(256), 0, st, z);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   if (p.nseg == 0) {
     if (!q.dh0) return hipSuccess;
     const size_t n = (size_t)p.batch * p.nheads * HD * p.dstate;
     hipLaunchKernelGGL(ssd_bwd_copy_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, q.d_final, q.dh0, n);
     return hipGetLastError();
   }
-  hipError_t e = launch_ssd_states(p, st);
-  if (e != hipSuccess) return e;
   if (p.dtype == DT_BF16) {
     if (p.dstate == 128) return launch_bwd_t<bf16, 128>(q, st);
     if (p.dstate == 64) return launch_bwd_t<bf16, 64>(q, st);

@@ -43,7 +43,7 @@ import torch
 from . import _lib
 from ._lib import SsdArgs, SsdBwdArgs, SsuArgs, KdaArgs, Conv1dArgs
 
-__all__ = ["selective_scan", "selective_scan_bwd", "selective_state_update", "recurrent_step", "linear_attn_scan",
+__all__ = ["selective_scan", "selective_scan_bwd", "plan_selective_scan_bwd", "selective_state_update", "recurrent_step", "linear_attn_scan",
            "linear_attn_scan_pair", "linear_attn_scan_single", "linear_attention_scan", "diff_lambda",
            "linear_attn_step", "linear_attention_recurrent",
            "ssd_chunk_len", "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan",
@@ -288,7 +288,7 @@ def _scan_fwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg):
     return y4, fin
 
 
-def _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4, dfin, need_dh0):
+def _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4, dfin, need_dh0, plan_only=False):
     dt_softplus, dt_limit, _ = cfg
     b, L, H, P = x4.shape
     G, N = B4.shape[2], B4.shape[3]
@@ -320,6 +320,10 @@ def _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4, dfin, need_dh0):
     _lib.call("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(nbytes))
     ws = torch.empty(max(int(nbytes.value), 16), device=dev, dtype=torch.uint8)
     a.workspace, a.workspace_bytes = _ptr(ws), nbytes.value
+    if plan_only:
+        return Plan("mh_ssd_chunk_scan_bwd", a, dev,
+                    keep=(x4, dt32, A32, B4, C4, D32, h0, bias32, dy4, dfin, ws),
+                    dx=dx, ddt=ddt, dA=dA, dB=dB, dC=dC, dD=dD, d_initial_state=dh0, d_dt_bias=dbias)
     _lib.call("mh_ssd_chunk_scan_bwd", ct.byref(a), _stream(dev))
     return dx, ddt, dA, dB, dC, dD, dh0, dbias
 
@@ -343,8 +347,15 @@ class _SelectiveScanFn(torch.autograd.Function):
         return dx, ddt, dA, dB, dC, dD, dh0, dbias, None
 
 
+def plan_selective_scan_bwd(*args, **kw):
+    """Validate and allocate once; returns a ``Plan`` whose call launches ``selective_scan_bwd`` into the same
+    gradient buffers (attributes ``dx``, ``ddt``, ``dA``, ``dB``, ``dC``, ``dD``, ``d_initial_state``,
+    ``d_dt_bias``, shaped as the kernels write them)."""
+    return selective_scan_bwd(*args, _plan_only=True, **kw)
+
+
 def selective_scan_bwd(dy, x, dt, A, B, C, D=None, *, d_final_state=None, initial_state=None, dt_bias=None,
-                       dt_softplus=False, dt_limit=None):
+                       dt_softplus=False, dt_limit=None, _plan_only=False):
     """Gradients of ``<dy, y> + <d_final_state, final_state>`` for ``y, final_state = selective_scan(x, dt, A, B,
     C, D, initial_state=..., dt_bias=..., dt_softplus=..., dt_limit=...)`` -- the backward PyTorch autograd runs
     through the reference's scan (mamba2.py:70-130; R/tests/test_mamba2.py:56-71), on the GPU.
@@ -380,8 +391,11 @@ def selective_scan_bwd(dy, x, dt, A, B, C, D=None, *, d_final_state=None, initia
     h0 = None if initial_state is None else initial_state.reshape(b, H, P, N).to(torch.float32).contiguous()
     dy4 = None if dy is None else dy.reshape(b, L, H, P)
     with torch.no_grad():
-        dx, ddt, dA, dB, dC, dD, dh0, dbias = _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32,
-                                                        (dt_softplus, dt_limit, None), dy4, d_final_state, True)
+        res = _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, (dt_softplus, dt_limit, None), dy4, d_final_state,
+                        True, plan_only=_plan_only)
+    if _plan_only:
+        return res
+    dx, ddt, dA, dB, dC, dD, dh0, dbias = res
     out = {"dx": dx.reshape(x.shape), "ddt": ddt, "dA": dA, "dB": dB.reshape(B.shape), "dC": dC.reshape(C.shape),
            "d_initial_state": dh0 if initial_state is None else dh0.reshape(initial_state.shape)}
     if D is not None:
