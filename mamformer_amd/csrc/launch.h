@@ -59,9 +59,6 @@ size_t ssd_workspace_bytes(int batch, int seqlen, int nchunks, int nheads, int h
                            int dtype);
 // Point p's workspace parts into `workspace` (ssd_workspace_bytes of p's sizes).
 void ssd_workspace_layout(SsdParams& p, void* workspace);
-// Kernels 0-2 of the prefill only: the entering state of every chunk, left in the workspace
-// (p.entering for bf16 I/O, p.chunk_states in place for fp32 I/O).
-hipError_t launch_ssd_states(const SsdParams& p, hipStream_t st);
 
 // ------------------------------------------------------------- SSD prefill backward
 struct SsdBwdParams {

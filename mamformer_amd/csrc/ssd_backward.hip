@@ -21,7 +21,7 @@
 //
 // Launches (caller's stream):
 //   0. ssd_bwd_zero      clears dA, dD, d_dt_bias (a kernel, not a memset node).
-//   1. ssd_bwd_sweep     grid (2 directions x 2 halves of P, H, b): the forward direction walks the segments
+//   1. ssd_bwd_sweep     grid (2 directions, H, b): the forward direction walks the segments
 //      first to last and stores the entering state h_in of every 64-token segment; the adjoint direction walks
 //      them last to first, stores lam_out of every segment and finally dh0
 //      (lam <- e^{c_end} lam + sum_t e^{c_t} C_t^T dy_t).  Both into the workspace, fragment-native order.
@@ -199,64 +199,79 @@ __global__ __launch_bounds__(256) void ssd_bwd_copy_kernel(const float* __restri
 template <typename T, int N>
 struct SweepStage {
   T M[SEG * N];             // Tile<T, N>: B (forward sweep) or C (adjoint sweep)
-  T V[SEG * 32];            // XHalf<T>: the workgroup's 32 columns of x (forward) or dy (adjoint)
+  T V[SEG * HD];            // Tile<T, HD>: x (forward) or dy (adjoint)
   float dtraw[SEG];
 };
-constexpr int SWEEP_NST = 3;     // stages: segments fetched two ahead
-template <typename T, int N>
+template <typename T, int N, int NST>
 struct SweepSmem {
-  SweepStage<T, N> st[SWEEP_NST];
-  float w[N / 32][SEG];     // per wave: per-token weight of the segment
+  SweepStage<T, N> st[NST];
+  float w[2 * (N / 32)][SEG];   // per compute wave: per-token weight of the segment
 };
+// The loader waits for the oldest of up to NST - 1 stages in flight with vmcnt(later stages' loads), and vmcnt
+// counts to 63: as many stages as both that and the LDS allow.
+template <typename T, int N>
+constexpr int sweep_dps = Tile<T, N>::NBLK + Tile<T, HD>::NBLK + 1;   // loads per stage
+template <typename T, int N, int K>
+constexpr bool sweep_fits = (K - 2) * sweep_dps<T, N> <= 63 && sizeof(SweepSmem<T, N, K>) <= 160 * 1024;
+template <typename T, int N>
+constexpr int sweep_nst = sweep_fits<T, N, 5> ? 5 : (sweep_fits<T, N, 4> ? 4 : 3);
 
-// One workgroup per (direction, 32-column half pt of P, head, batch); compute wave nt owns state tile (nt, pt),
-// and one more wave only fetches: it keeps two segments in flight (global -> LDS) and waits for them with
-// exact counts, which the compute waves, whose state stores share the same counter, could not.
+template <int DPS>
+__device__ __forceinline__ void wait_stages(int later) {   // wait until at most `later` stages remain in flight
+  switch (later) {
+    case 0: wait_vmem_n<0>(); break;
+    case 1: wait_vmem_n<DPS>(); break;
+    case 2: if constexpr (2 * DPS <= 63) wait_vmem_n<2 * DPS>(); else wait_vmem_n<DPS>(); break;
+    default: if constexpr (3 * DPS <= 63) wait_vmem_n<3 * DPS>(); else wait_vmem_n<DPS>(); break;
+  }
+}
+
+// One workgroup per (direction, head, batch): compute wave w owns state tile (nt, pt) = (w % (N/32), w / (N/32)),
+// and one more wave only fetches: it keeps up to NST - 1 segments in flight (global -> LDS) and waits for them
+// with exact counts, which the compute waves, whose state stores share the same counter, could not.
 //   forward (dir 0): S = h, segments first to last, weights w_s = e^{c_end - c_s} dt_s on B^T x:
 //       stores the entering state of every segment, S <- e^{c_end} S + sum_s B_s^T w_s x_s
 //   adjoint (dir 1): S = lam, segments last to first, weights w_t = e^{c_t} on C^T dy:
 //       stores lam_out of every segment, S <- e^{c_end} S + sum_t C_t^T w_t dy_t, finally dh0 = S.
 // Both directions run in one launch (independent workgroups).
 template <typename T, int N>
-__global__ __launch_bounds__(64 * (N / 32 + 1)) void ssd_bwd_sweep_kernel(SsdBwdParams q) {
-  constexpr int NB = N / 32;
-  using TM_ = Tile<T, N>;
-  using TV = XHalf<T>;
-  constexpr int DMA_PER_STAGE = TM_::NBLK + TV::NBLK + 1;
-  __shared__ SweepSmem<T, N> sm;
+__global__ __launch_bounds__(64 * (2 * (N / 32) + 1)) void ssd_bwd_sweep_kernel(SsdBwdParams q) {
+  constexpr int NB = N / 32, NW = 2 * NB;
+  constexpr int NST = sweep_nst<T, N>;
+  constexpr int DPS = sweep_dps<T, N>;
+  __shared__ SweepSmem<T, N, NST> sm;
   const SsdParams& p = q.f;
-  const int dir = blockIdx.x >> 1, pt = blockIdx.x & 1, h = blockIdx.y, b = blockIdx.z;
+  const int dir = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int g = h / (p.nheads / p.ngroups);
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
   const int nseg = p.nseg;
   auto seg_of = [&](int i) { return dir ? nseg - 1 - i : i; };
-  if (w == NB) {
+  if (w == NW) {
     // ---- loader wave
     const T* Mb = reinterpret_cast<const T*>(dir ? p.C : p.B) + (int64_t)b * (dir ? p.C_sb : p.B_sb) + g * N;
     const int64_t M_sl = dir ? p.C_sl : p.B_sl;
-    const T* Vb = dir ? reinterpret_cast<const T*>(q.dy) + (int64_t)b * q.dy_sb + (int64_t)h * q.dy_sh + 32 * pt
-                      : reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + 32 * pt;
+    const T* Vb = dir ? reinterpret_cast<const T*>(q.dy) + (int64_t)b * q.dy_sb + (int64_t)h * q.dy_sh
+                      : reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh;
     const int64_t V_sl = dir ? q.dy_sl : p.x_sl;
     const float* dtb = p.dt + (int64_t)b * p.dt_sb + h;
     auto issue = [&](int i) {
-      const int k = seg_of(i), s = i % SWEEP_NST;
+      const int k = seg_of(i), s = i % NST;
       const int t0 = k * SEG, lst = min(t0 + SEG, p.seqlen) - 1;
-      fetch_tile<T, N>(sm.st[s].M, Mb, M_sl, t0, lst, 0, TM_::NBLK, l);
-      fetch_xhalf<T>(sm.st[s].V, Vb, V_sl, t0, lst, l);
+      fetch_tile<T, N>(sm.st[s].M, Mb, M_sl, t0, lst, 0, Tile<T, N>::NBLK, l);
+      fetch_tile<T, HD>(sm.st[s].V, Vb, V_sl, t0, lst, 0, Tile<T, HD>::NBLK, l);
       fetch_dt(sm.st[s].dtraw, dtb, p.dt_sl, t0, lst, l);
     };
-    issue(0);
-    if (nseg > 1) issue(1);
+    for (int i = 0; i < NST - 1 && i < nseg; ++i) issue(i);
     for (int i = 0; i < nseg; ++i) {
-      if (i + 1 < nseg) wait_vmem_n<DMA_PER_STAGE>();   // stage i landed (only stage i + 1 may be in flight)
-      else wait_vmem();
+      const int later = min(NST - 2, nseg - 1 - i);      // stages issued after stage i
+      wait_stages<DPS>(later);
       lds_barrier();                                     // publish stage i; iteration i - 1 is done everywhere
-      if (i + 2 < nseg) issue(i + 2);                    // into the stage iteration i - 1 read
+      if (i + NST - 1 < nseg) issue(i + NST - 1);        // into the stage iteration i - 1 read
     }
     return;
   }
   // ---- compute waves
-  const int nt = w;
+  const int nt = w % NB, pt = w / NB;
   const float Ah = p.A[h], bias = p.dt_bias ? p.dt_bias[h] : 0.f;
   Frag<T> id[2];
 #pragma unroll
@@ -276,7 +291,7 @@ __global__ __launch_bounds__(64 * (N / 32 + 1)) void ssd_bwd_sweep_kernel(SsdBwd
   }
   T* out = reinterpret_cast<T*>(dir ? q.lam : q.hin);
   for (int i = 0; i < nseg; ++i) {
-    const int k = seg_of(i), s = i % SWEEP_NST;
+    const int k = seg_of(i), s = i % NST;
     // the state entering segment k (forward) / leaving it (adjoint), stored before the update
     store_state_blk<T>(out + (((int64_t)b * nseg + k) * p.nheads + h) * per, nt, pt, l, S);
     lds_barrier();
@@ -288,8 +303,8 @@ __global__ __launch_bounds__(64 * (N / 32 + 1)) void ssd_bwd_sweep_kernel(SsdBwd
     f32x16 acc = zero16();
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
-      const f32x16 mt = mfma_transpose<T, T, N>(sm.st[s].M, 32 * tb, 32 * nt, id, half, l32);   // [t][n]
-      const f32x16 vt = xhalf_transpose<T>(sm.st[s].V, 32 * tb, id, half, l32);                // [t][p]
+      const f32x16 mt = mfma_transpose<T, T, N>(sm.st[s].M, 32 * tb, 32 * nt, id, half, l32);    // [t][n]
+      const f32x16 vt = mfma_transpose<T, T, HD>(sm.st[s].V, 32 * tb, 32 * pt, id, half, l32);  // [t][p]
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         float e[8];
@@ -316,22 +331,27 @@ __global__ __launch_bounds__(64 * (N / 32 + 1)) void ssd_bwd_sweep_kernel(SsdBwd
   }
 }
 
-// ------------------------------------------------------------------ kernel 3: gradients per segment
+// ------------------------------------------------------------------ kernel 2: gradients per segment
 
-template <typename T, int N, bool SL>
+template <typename T, int N>
 struct GradStage {
   T X[SEG * HD];            // Tile<T, HD> of the head
   T DY[SEG * HD];
   float dtraw[SEG];
 };
-template <typename T, int N>
-struct GradStage<T, N, true> : GradStage<T, N, false> {
+template <typename T, int N, bool SL> struct GradStates {};
+template <typename T, int N> struct GradStates<T, N, true> {
   T Lam[HD * N];            // lam_out and h_in of the head, fragment-native order (as in the workspaces)
   T Hin[HD * N];
 };
+// With 8 waves the dx^T tiles' state contraction is split over the two halves of the workgroup; the first half
+// leaves its partial tile here.
+template <int NW> struct DxPartial { float v[NW == 8 ? 4 : 1][64 * 16]; };
 template <typename T, int N, int NST, bool SL>
 struct GradSmem {
-  GradStage<T, N, SL> st[NST];
+  GradStage<T, N> st[NST];
+  GradStates<T, N, SL> sts;
+  DxPartial<2 * (N / 32)> dxp;
   T B[SEG * N];             // Tile<T, N>
   T C[SEG * N];
   float cs[2 * (N / 32)][SEG];   // per wave: c_t of the current head
@@ -346,12 +366,14 @@ struct GradSmem {
   float cbt[3][64 * 16];         // CB^T[s][t] tiles (s-block, t-block) = (0,0), (0,1), (1,1)
 };
 constexpr size_t GRAD_LDS = 160 * 1024;
-// The states of a head are staged in LDS with its tiles where they fit (else read from HBM where used), and
-// the per-head stages are double-buffered (the next head's fetch overlaps this head's work) where two fit.
+// The per-head tiles are double-buffered (the next head's fetch overlaps this head's work) and the head's states
+// staged in LDS (else read from HBM where used), as far as the LDS allows, in that order of preference.
+template <typename T, int N, int NST, bool SL>
+constexpr bool grad_fits = sizeof(GradSmem<T, N, NST, SL>) <= GRAD_LDS;
 template <typename T, int N>
-constexpr bool grad_sl = sizeof(GradSmem<T, N, 1, true>) <= GRAD_LDS;
+constexpr int grad_nst = (grad_fits<T, N, 2, true> || grad_fits<T, N, 2, false>) ? 2 : 1;
 template <typename T, int N>
-constexpr int grad_nst = sizeof(GradSmem<T, N, 2, grad_sl<T, N>>) <= GRAD_LDS ? 2 : 1;
+constexpr bool grad_sl = grad_fits<T, N, grad_nst<T, N>, true>;
 
 // Work split (NW = 2 N/32 waves): wave w owns n-block nb = w % (N/32) and token block r = w / (N/32) of the
 // dB^T [n][s] and dC^T [n][t] tiles; waves 0-3 also own the dx^T [p][s] tile (p-block w & 1, s-block w >> 1).
@@ -371,7 +393,8 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
   const int g = hfirst / hpg;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
   const int nb = w % NB, r = w / NB;
-  const bool dxw = w < 4;
+  const bool dxw = w < 4;                   // first dx half (all of dx with 4 waves)
+  constexpr bool SPLIT = NW == 8;           // the second half (waves 4-7) takes half of the state contraction
   const int pb = w & 1, sbx = (w >> 1) & 1;
   const int tok0 = si * SEG;
   const int len = min(SEG, p.seqlen - tok0);
@@ -402,15 +425,20 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
     constexpr int nblk = TX::NBLK / NW;
     fetch_tile<T, HD>(sm.st[st].X, xb + (int64_t)h * p.x_sh, p.x_sl, tok0, last, w * nblk, nblk, l);
     fetch_tile<T, HD>(sm.st[st].DY, dyb + (int64_t)h * q.dy_sh, q.dy_sl, tok0, last, w * nblk, nblk, l);
-    if constexpr (SL) {
-      constexpr int sblk = HD * N * (int)sizeof(T) / 1024 / NW;
-      const int64_t soff = (((int64_t)b * p.nseg + si) * p.nheads + h) * per * (int64_t)sizeof(T);
-      fetch_blocks(reinterpret_cast<char*>(sm.st[st].Lam), lam_ws + soff, w * sblk, sblk, l);
-      fetch_blocks(reinterpret_cast<char*>(sm.st[st].Hin), hin_ws + soff, w * sblk, sblk, l);
-    }
     if (w == 0) fetch_dt(sm.st[st].dtraw, dtb + h, p.dt_sl, tok0, last, l);
   };
+  auto fetch_states = [&](int h) {
+    if constexpr (SL) {
+      int l = lane_id();
+      asm volatile("" : "+v"(l));
+      constexpr int sblk = HD * N * (int)sizeof(T) / 1024 / NW;
+      const int64_t soff = (((int64_t)b * p.nseg + si) * p.nheads + h) * per * (int64_t)sizeof(T);
+      fetch_blocks(reinterpret_cast<char*>(sm.sts.Lam), lam_ws + soff, w * sblk, sblk, l);
+      fetch_blocks(reinterpret_cast<char*>(sm.sts.Hin), hin_ws + soff, w * sblk, sblk, l);
+    }
+  };
   fetch_head(hfirst, std::integral_constant<int, 0>());
+  fetch_states(hfirst);
   if (w == 0) sm.ddp[l] = 0.f;
   f32x16 dBacc = zero16(), dCacc = zero16();
 
@@ -481,11 +509,11 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
     auto& sg = sm.st[st];
     const int64_t sidx = (((int64_t)b * p.nseg + si) * p.nheads + h) * per;
     auto lam_src = [&]() -> const T* {
-      if constexpr (SL) return sg.Lam;
+      if constexpr (SL) return sm.sts.Lam;
       else return reinterpret_cast<const T*>(lam_ws) + sidx;
     };
     auto hin_src = [&]() -> const T* {
-      if constexpr (SL) return sg.Hin;
+      if constexpr (SL) return sm.sts.Hin;
       else return reinterpret_cast<const T*>(hin_ws) + sidx;
     };
     StateBlk<T> Lb[2], Hb[2];
@@ -665,46 +693,73 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
     }
 
     __builtin_amdgcn_sched_barrier(0);   // keep the phases apart: bounded register lifetimes
-    // ---- dx^T tile (p-block pb, s-block sbx)
-    if (dxw) {
-      const float csx = __shfl(cs, s_x), dtx = __shfl(dtv, s_x), wx = __expf(cend - csx);
-      f32x16 ax = zero16();
+    // ---- dx^T tile (p-block pb, s-block sbx).  dx = dt_s (intra + e^{c_end - c_s} lam_out B_s) + D dy: the first
+    // half owns intra and, with the split, the state blocks nt < NB/2; the second half the others and the store.
+    float dyv[16], Dv[16];
+    f32x16 ax = zero16();
+    const bool dxB = SPLIT && w >= 4;
+    if (dxw || dxB) {
+      const float csx = __shfl(cs, s_x), wx = __expf(cend - csx);
+      if (dxw) {
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb) {
-        if (tb >= sbx) {
-          f32x16 m;
-          const float* cbp = sm.cb[tb + sbx] + 16 * l;
+        for (int tb = 0; tb < 2; ++tb) {
+          if (tb >= sbx) {
+            f32x16 m;
+            const float* cbp = sm.cb[tb + sbx] + 16 * l;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
+            for (int i = 0; i < 4; ++i) {
+              const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) m[4 * i + k] = v[k];
+              for (int k = 0; k < 4; ++k) m[4 * i + k] = v[k];
+            }
+            float ct[16];
+            acc_rows(sm.cs[w], 32 * tb, half, ct);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int t = 32 * tb + acc_row(half, i);
+              m[i] = (t < len && t >= s_x) ? m[i] * __expf(ct[i] - csx) : 0.f;
+            }
+            const f32x16 dyt = mfma_transpose<T, T, HD>(sg.DY, 32 * tb, 32 * pb, id, half, l32);   // [t][p]
+#pragma unroll
+            for (int c = 0; c < 2; ++c) ax = mma(acc_to_frag<T>(dyt, c), acc_to_frag<T>(m, c), ax);
           }
-          float ct[16];
-          acc_rows(sm.cs[w], 32 * tb, half, ct);
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int t = 32 * tb + acc_row(half, i);
-            m[i] = (t < len && t >= s_x) ? m[i] * __expf(ct[i] - csx) : 0.f;
-          }
-          const f32x16 dyt = mfma_transpose<T, T, HD>(sg.DY, 32 * tb, 32 * pb, id, half, l32);   // [t][p]
-#pragma unroll
-          for (int c = 0; c < 2; ++c) ax = mma(acc_to_frag<T>(dyt, c), acc_to_frag<T>(m, c), ax);
         }
       }
+      constexpr int NT0 = SPLIT ? NB / 2 : NB;
+      const int nt0 = dxB ? NT0 : 0;
 #pragma unroll
-      for (int nt = 0; nt < NB; ++nt) {
+      for (int k = 0; k < NT0; ++k) {
+        const int nt = nt0 + k;
         const StateBlk<T> lx = load_state_blk<T>(lam_src(), nt, pb, l);
 #pragma unroll
         for (int c = 0; c < 2; ++c)
           ax = mma(lx.frag(c), scaled<T>(kset_frag<T, T, N>(sm.B, s_x, 32 * nt + 16 * c, half), wx), ax);
       }
-      float dyv[16];
-      acc_cols<T, HD>(sg.DY, s_x, 32 * pb, half, dyv);
-      float Dv[16];
+      if (!SPLIT || dxB) {
+        acc_cols<T, HD>(sg.DY, s_x, 32 * pb, half, dyv);
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        Dv[i] = p.D ? (p.D_per_channel ? p.D[h * HD + 32 * pb + acc_row(half, i)] : p.D[h]) : 0.f;
+        for (int i = 0; i < 16; ++i)
+          Dv[i] = p.D ? (p.D_per_channel ? p.D[h * HD + 32 * pb + acc_row(half, i)] : p.D[h]) : 0.f;
+        if (p.D_per_channel && q.dD && s_x < len) {
+          float xv[16];
+          acc_cols<T, HD>(sg.X, s_x, 32 * pb, half, xv);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) atomicAdd(&sm.ddp[32 * pb + acc_row(half, i)], xv[i] * dyv[i]);
+        }
+      } else {
+        float* o = sm.dxp.v[w & 3] + 16 * l;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f32x4 v;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[k] = ax[4 * i + k];
+          *reinterpret_cast<f32x4*>(o + 4 * i) = v;
+        }
+      }
+    }
+    // dx = dt_s * ax + D dy, stored by the owner of the finished tile
+    auto store_dx = [&]() {
+      const float dtx = __shfl(dtv, s_x);
       if (s_x < len) {
         T* o = reinterpret_cast<T*>(q.dx) + (int64_t)b * q.dx_sb + (int64_t)(tok0 + s_x) * q.dx_sl +
                (int64_t)h * q.dx_sh + 32 * pb + 4 * half;
@@ -723,20 +778,28 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
           }
         }
       }
-      if (p.D_per_channel && q.dD && s_x < len) {
-        float xv[16];
-        acc_cols<T, HD>(sg.X, s_x, 32 * pb, half, xv);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) atomicAdd(&sm.ddp[32 * pb + acc_row(half, i)], xv[i] * dyv[i]);
-      }
-    }
+    };
+    if (!SPLIT && dxw) store_dx();
 
     // The next head's fetch: into the other stage (head j - 1's, read by nobody since the last barrier) before
     // the barrier, or, with one stage, after it.  It is issued late on purpose: a spill reload in the work above
     // would wait for it (the vector-memory counter is shared).
     if (NST == 2 && j + 1 < HB) fetch_head(h + 1, std::integral_constant<int, st ^ 1>());
-    lds_barrier();                     // partial dots complete; with one stage, X / DY / dt free for the next head
-    if (NST == 1 && j + 1 < HB) fetch_head(h + 1, std::integral_constant<int, 0>());
+    lds_barrier();                     // partial dots and dx partials complete; this head's states no longer read
+    if (j + 1 < HB) {
+      if (NST == 1) fetch_head(h + 1, std::integral_constant<int, 0>());
+      fetch_states(h + 1);
+    }
+    if (dxB) {
+      const float* ip = sm.dxp.v[w & 3] + 16 * l;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(ip + 4 * i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ax[4 * i + k] += v[k];
+      }
+      store_dx();
+    }
     if (w == 0) {
       const float colG = sm.colg[l], rowG = sm.rowg[l];
       float bint = 0.f, u = 0.f, lh = 0.f;
@@ -866,8 +929,8 @@ template <typename T, int N>
 static hipError_t launch_bwd_t(const SsdBwdParams& q, hipStream_t st) {
   const SsdParams& p = q.f;
   constexpr int NB = N / 32;
-  hipLaunchKernelGGL((ssd_bwd_sweep_kernel<T, N>), dim3(4, (unsigned)p.nheads, (unsigned)p.batch),
-                     dim3(64 * (NB + 1)), 0, st, q);
+  hipLaunchKernelGGL((ssd_bwd_sweep_kernel<T, N>), dim3(2, (unsigned)p.nheads, (unsigned)p.batch),
+                     dim3(64 * (2 * NB + 1)), 0, st, q);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_bwd_grad_kernel<T, N>),

@@ -692,7 +692,7 @@ void ssd_workspace_layout(SsdParams& p, void* workspace) {
 }
 
 template <typename T, typename TM, int N, int HG>
-static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st, bool scan) {
+static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st) {
   hipLaunchKernelGGL((ssd_seg_frags_kernel<T, TM, N>), dim3((unsigned)p.nseg, (unsigned)p.ngroups, (unsigned)p.batch),
                      dim3(512), 0, st, p);
   hipError_t e = hipGetLastError();
@@ -705,7 +705,7 @@ static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st, bool scan) {
   dim3 g2((unsigned)((per4 + 255) / 256), (unsigned)(p.batch * p.nheads));
   hipLaunchKernelGGL((ssd_state_pass_kernel<T>), g2, dim3(256), 0, st, p);
   e = hipGetLastError();
-  if (e != hipSuccess || !scan) return e;
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_chunk_scan_kernel<T, TM, N, HG>), grid, dim3(128 * HG), 0, st, p);
   return hipGetLastError();
 }
@@ -716,16 +716,16 @@ constexpr bool ssd_fits = !(sizeof(T) == 4 && N == 128 && HG > 1) &&   // fp32 N
                           bt_blocks<TM, N> % (2 * HG) == 0 && Tile<T, N>::NBLK % (2 * HG) == 0;
 
 template <typename T, typename TM, int N>
-static hipError_t launch_ssd_n(const SsdParams& p, hipStream_t st, bool scan) {
+static hipError_t launch_ssd_n(const SsdParams& p, hipStream_t st) {
   switch (p.heads_per_wg) {
     case 4:
-      if constexpr (ssd_fits<T, TM, N, 4>) return launch_ssd_t<T, TM, N, 4>(p, st, scan);
+      if constexpr (ssd_fits<T, TM, N, 4>) return launch_ssd_t<T, TM, N, 4>(p, st);
       return hipErrorInvalidValue;
     case 2:
-      if constexpr (ssd_fits<T, TM, N, 2>) return launch_ssd_t<T, TM, N, 2>(p, st, scan);
+      if constexpr (ssd_fits<T, TM, N, 2>) return launch_ssd_t<T, TM, N, 2>(p, st);
       return hipErrorInvalidValue;
     case 1:
-      if constexpr (ssd_fits<T, TM, N, 1>) return launch_ssd_t<T, TM, N, 1>(p, st, scan);
+      if constexpr (ssd_fits<T, TM, N, 1>) return launch_ssd_t<T, TM, N, 1>(p, st);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
@@ -738,27 +738,22 @@ __global__ __launch_bounds__(256) void ssd_empty_kernel(const float* __restrict_
   if (i < n) fin[i] = h0 ? h0[i] : 0.f;
 }
 
-static hipError_t launch_ssd_impl(const SsdParams& p, hipStream_t st, bool scan) {
+hipError_t launch_ssd(const SsdParams& p, hipStream_t st) {
   if (p.nchunks == 0) {
-    if (!p.final_state || !scan) return hipSuccess;
+    if (!p.final_state) return hipSuccess;
     const size_t n = (size_t)p.batch * p.nheads * HD * p.dstate;
     hipLaunchKernelGGL(ssd_empty_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p.init_state,
                        p.final_state, n);
     return hipGetLastError();
   }
   if (p.dtype == DT_BF16) {
-    if (p.dstate == 128) return launch_ssd_n<bf16, bf16, 128>(p, st, scan);
-    if (p.dstate == 64) return launch_ssd_n<bf16, bf16, 64>(p, st, scan);
+    if (p.dstate == 128) return launch_ssd_n<bf16, bf16, 128>(p, st);
+    if (p.dstate == 64) return launch_ssd_n<bf16, bf16, 64>(p, st);
   } else {
-    if (p.dstate == 128) return launch_ssd_n<float, float, 128>(p, st, scan);
-    if (p.dstate == 64) return launch_ssd_n<float, float, 64>(p, st, scan);
+    if (p.dstate == 128) return launch_ssd_n<float, float, 128>(p, st);
+    if (p.dstate == 64) return launch_ssd_n<float, float, 64>(p, st);
   }
   return hipErrorInvalidValue;
 }
-
-hipError_t launch_ssd(const SsdParams& p, hipStream_t st) { return launch_ssd_impl(p, st, true); }
-
-// Kernels 0-2 only: the entering state of every chunk (workspace), for the backward pass.
-hipError_t launch_ssd_states(const SsdParams& p, hipStream_t st) { return launch_ssd_impl(p, st, false); }
 
 }  // namespace mh
