@@ -207,27 +207,31 @@ struct SweepSmem {
   SweepStage<T, N> st[NST];
   float w[2 * (N / 32)][SEG];   // per compute wave: per-token weight of the segment
 };
-// The loader waits for the oldest of up to NST - 1 stages in flight with vmcnt(later stages' loads), and vmcnt
-// counts to 63: as many stages as both that and the LDS allow.
+// Two loader waves split each stage's loads (M blocks, V blocks; the first also dt) and wait for the oldest of up
+// to NST - 1 stages in flight with vmcnt(later stages' loads), which counts to 63: as many stages as both that and
+// the LDS allow.
 template <typename T, int N>
-constexpr int sweep_dps = Tile<T, N>::NBLK + Tile<T, HD>::NBLK + 1;   // loads per stage
+constexpr int sweep_dps = Tile<T, N>::NBLK / 2 + Tile<T, HD>::NBLK / 2 + 1;   // loads per stage of loader 0
 template <typename T, int N, int K>
 constexpr bool sweep_fits = (K - 2) * sweep_dps<T, N> <= 63 && sizeof(SweepSmem<T, N, K>) <= 160 * 1024;
 template <typename T, int N>
-constexpr int sweep_nst = sweep_fits<T, N, 5> ? 5 : (sweep_fits<T, N, 4> ? 4 : 3);
+constexpr int sweep_nst = sweep_fits<T, N, 6> ? 6 : (sweep_fits<T, N, 5> ? 5 : (sweep_fits<T, N, 4> ? 4 : 3));
 
+// Wait until at most `later` stages of DPS loads each remain in flight (a smaller count than needed only waits
+// longer).
 template <int DPS>
-__device__ __forceinline__ void wait_stages(int later) {   // wait until at most `later` stages remain in flight
+__device__ __forceinline__ void wait_stages(int later) {
   switch (later) {
     case 0: wait_vmem_n<0>(); break;
     case 1: wait_vmem_n<DPS>(); break;
     case 2: if constexpr (2 * DPS <= 63) wait_vmem_n<2 * DPS>(); else wait_vmem_n<DPS>(); break;
-    default: if constexpr (3 * DPS <= 63) wait_vmem_n<3 * DPS>(); else wait_vmem_n<DPS>(); break;
+    case 3: if constexpr (3 * DPS <= 63) wait_vmem_n<3 * DPS>(); else wait_vmem_n<DPS>(); break;
+    default: if constexpr (4 * DPS <= 63) wait_vmem_n<4 * DPS>(); else wait_vmem_n<DPS>(); break;
   }
 }
 
 // One workgroup per (direction, head, batch): compute wave w owns state tile (nt, pt) = (w % (N/32), w / (N/32)),
-// and one more wave only fetches: it keeps up to NST - 1 segments in flight (global -> LDS) and waits for them
+// and two more waves only fetch: they keep up to NST - 1 segments in flight (global -> LDS) and wait for them
 // with exact counts, which the compute waves, whose state stores share the same counter, could not.
 //   forward (dir 0): S = h, segments first to last, weights w_s = e^{c_end - c_s} dt_s on B^T x:
 //       stores the entering state of every segment, S <- e^{c_end} S + sum_s B_s^T w_s x_s
@@ -235,7 +239,7 @@ __device__ __forceinline__ void wait_stages(int later) {   // wait until at most
 //       stores lam_out of every segment, S <- e^{c_end} S + sum_t C_t^T w_t dy_t, finally dh0 = S.
 // Both directions run in one launch (independent workgroups).
 template <typename T, int N>
-__global__ __launch_bounds__(64 * (2 * (N / 32) + 1)) void ssd_bwd_sweep_kernel(SsdBwdParams q) {
+__global__ __launch_bounds__(64 * (2 * (N / 32) + 2)) void ssd_bwd_sweep_kernel(SsdBwdParams q) {
   constexpr int NB = N / 32, NW = 2 * NB;
   constexpr int NST = sweep_nst<T, N>;
   constexpr int DPS = sweep_dps<T, N>;
@@ -246,8 +250,9 @@ __global__ __launch_bounds__(64 * (2 * (N / 32) + 1)) void ssd_bwd_sweep_kernel(
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
   const int nseg = p.nseg;
   auto seg_of = [&](int i) { return dir ? nseg - 1 - i : i; };
-  if (w == NW) {
-    // ---- loader wave
+  if (w >= NW) {
+    // ---- loader waves (lw = 0, 1: halves of the M and V blocks; lw 0 also dt)
+    const int lw = w - NW;
     const T* Mb = reinterpret_cast<const T*>(dir ? p.C : p.B) + (int64_t)b * (dir ? p.C_sb : p.B_sb) + g * N;
     const int64_t M_sl = dir ? p.C_sl : p.B_sl;
     const T* Vb = dir ? reinterpret_cast<const T*>(q.dy) + (int64_t)b * q.dy_sb + (int64_t)h * q.dy_sh
@@ -257,14 +262,16 @@ __global__ __launch_bounds__(64 * (2 * (N / 32) + 1)) void ssd_bwd_sweep_kernel(
     auto issue = [&](int i) {
       const int k = seg_of(i), s = i % NST;
       const int t0 = k * SEG, lst = min(t0 + SEG, p.seqlen) - 1;
-      fetch_tile<T, N>(sm.st[s].M, Mb, M_sl, t0, lst, 0, Tile<T, N>::NBLK, l);
-      fetch_tile<T, HD>(sm.st[s].V, Vb, V_sl, t0, lst, 0, Tile<T, HD>::NBLK, l);
-      fetch_dt(sm.st[s].dtraw, dtb, p.dt_sl, t0, lst, l);
+      constexpr int mb = Tile<T, N>::NBLK / 2, vb = Tile<T, HD>::NBLK / 2;
+      fetch_tile<T, N>(sm.st[s].M, Mb, M_sl, t0, lst, lw * mb, mb, l);
+      fetch_tile<T, HD>(sm.st[s].V, Vb, V_sl, t0, lst, lw * vb, vb, l);
+      if (lw == 0) fetch_dt(sm.st[s].dtraw, dtb, p.dt_sl, t0, lst, l);
     };
     for (int i = 0; i < NST - 1 && i < nseg; ++i) issue(i);
     for (int i = 0; i < nseg; ++i) {
       const int later = min(NST - 2, nseg - 1 - i);      // stages issued after stage i
-      wait_stages<DPS>(later);
+      if (lw == 0) wait_stages<DPS>(later);                          // loader 0: M, V halves and dt
+      else wait_stages<DPS - 1>(later);                               // loader 1: M, V halves
       lds_barrier();                                     // publish stage i; iteration i - 1 is done everywhere
       if (i + NST - 1 < nseg) issue(i + NST - 1);        // into the stage iteration i - 1 read
     }
@@ -930,7 +937,7 @@ static hipError_t launch_bwd_t(const SsdBwdParams& q, hipStream_t st) {
   const SsdParams& p = q.f;
   constexpr int NB = N / 32;
   hipLaunchKernelGGL((ssd_bwd_sweep_kernel<T, N>), dim3(2, (unsigned)p.nheads, (unsigned)p.batch),
-                     dim3(64 * (2 * NB + 1)), 0, st, q);
+                     dim3(64 * (2 * NB + 2)), 0, st, q);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_bwd_grad_kernel<T, N>),

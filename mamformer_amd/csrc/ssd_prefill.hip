@@ -389,37 +389,72 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_state_kernel(SsdParams p) 
 // fragment order.  The running sum and the final state are fp32.
 template <typename TE>
 __global__ __launch_bounds__(256) void ssd_state_pass_kernel(SsdParams p) {
+  // 8 consecutive workspace elements per thread (16-byte bf16 accesses); the chunk states of up to KB chunks are
+  // loaded before any entering state is stored, so the loads are not ordered behind the stores.
+  constexpr int KB = 8;
   const int bh = blockIdx.y;
   const int b = bh / p.nheads, h = bh - b * p.nheads;
   const int per = HD * p.dstate;                  // state elements per (b, h)
-  const int e4 = (blockIdx.x * 256 + threadIdx.x) * 4;
-  if (e4 >= per) return;
-  const int ci = canon_index(e4, p.dstate);       // 4 consecutive e map to 4 consecutive canonical n
-  f32x4 H;
-  H[0] = H[1] = H[2] = H[3] = 0.f;
-  if (p.init_state) H = *reinterpret_cast<const f32x4*>(p.init_state + (int64_t)bh * per + ci);
-  const float* dec = p.chunk_decay + (int64_t)bh * p.nchunks;
-  for (int k = 0; k < p.nchunks; ++k) {
-    const int64_t idx = (((int64_t)b * p.nchunks + k) * p.nheads + h) * per + e4;
-    f32x4 S;
-    if constexpr (sizeof(TE) == 4) {
-      float* sp = p.chunk_states + idx;
-      S = *reinterpret_cast<const f32x4*>(sp);
-      *reinterpret_cast<f32x4*>(sp) = H;
-    } else {
-      const bf16x4 sb = *reinterpret_cast<const bf16x4*>(reinterpret_cast<const bf16*>(p.chunk_states) + idx);
+  const int e8 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e8 >= per) return;
+  const int ci0 = canon_index(e8, p.dstate), ci1 = canon_index(e8 + 4, p.dstate);   // two runs of 4 canonical n
+  f32x4 H[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) S[i] = (float)sb[i];
-      bf16x4 hb;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) hb[i] = (bf16)H[i];
-      *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(p.entering) + idx) = hb;
-    }
-    const float a = __expf(dec[k]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) H[i] = a * H[i] + S[i];
+  for (int u = 0; u < 2; ++u) H[u][0] = H[u][1] = H[u][2] = H[u][3] = 0.f;
+  if (p.init_state) {
+    H[0] = *reinterpret_cast<const f32x4*>(p.init_state + (int64_t)bh * per + ci0);
+    H[1] = *reinterpret_cast<const f32x4*>(p.init_state + (int64_t)bh * per + ci1);
   }
-  if (p.final_state) *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * per + ci) = H;
+  const float* dec = p.chunk_decay + (int64_t)bh * p.nchunks;
+  for (int k0 = 0; k0 < p.nchunks; k0 += KB) {
+    f32x4 S[KB][2];
+    float a[KB];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      if (k0 + j < p.nchunks) {
+        const int64_t idx = (((int64_t)b * p.nchunks + k0 + j) * p.nheads + h) * per + e8;
+        if constexpr (sizeof(TE) == 4) {
+          S[j][0] = *reinterpret_cast<const f32x4*>(p.chunk_states + idx);
+          S[j][1] = *reinterpret_cast<const f32x4*>(p.chunk_states + idx + 4);
+        } else {
+          const bf16x8 sb = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.chunk_states) + idx);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            S[j][0][i] = (float)sb[i];
+            S[j][1][i] = (float)sb[4 + i];
+          }
+        }
+        a[j] = dec[k0 + j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      if (k0 + j < p.nchunks) {
+        const int64_t idx = (((int64_t)b * p.nchunks + k0 + j) * p.nheads + h) * per + e8;
+        if constexpr (sizeof(TE) == 4) {
+          *reinterpret_cast<f32x4*>(p.chunk_states + idx) = H[0];
+          *reinterpret_cast<f32x4*>(p.chunk_states + idx + 4) = H[1];
+        } else {
+          bf16x8 hb;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            hb[i] = (bf16)H[0][i];
+            hb[4 + i] = (bf16)H[1][i];
+          }
+          *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(p.entering) + idx) = hb;
+        }
+        const float d = __expf(a[j]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) H[u][i] = d * H[u][i] + S[j][u][i];
+      }
+    }
+  }
+  if (p.final_state) {
+    *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * per + ci0) = H[0];
+    *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * per + ci1) = H[1];
+  }
 }
 
 // ------------------------------------------------------------------ kernel 3
@@ -701,8 +736,8 @@ static hipError_t launch_ssd_t(const SsdParams& p, hipStream_t st) {
   hipLaunchKernelGGL((ssd_chunk_state_kernel<T, TM, N, HG>), grid, dim3(128 * HG), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int per4 = HD * N / 4;
-  dim3 g2((unsigned)((per4 + 255) / 256), (unsigned)(p.batch * p.nheads));
+  const int per8 = HD * N / 8;
+  dim3 g2((unsigned)((per8 + 255) / 256), (unsigned)(p.batch * p.nheads));
   hipLaunchKernelGGL((ssd_state_pass_kernel<T>), g2, dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
