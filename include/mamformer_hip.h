@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MH_ABI_VERSION 3
+#define MH_ABI_VERSION 4
 
 /* element types of x / B / C / y / q / k / v / o */
 enum { MH_F32 = 0, MH_BF16 = 1 };
@@ -243,6 +243,30 @@ typedef struct {
 } mh_conv1d_args;
 
 int mh_causal_conv1d_fwd(const mh_conv1d_args* a, void* stream);
+
+/* Backward of mh_causal_conv1d_fwd: the gradient PyTorch autograd forms through
+ *   the reference's nn.Conv1d + F.silu (mamformer/layers/mamba2.py:279-283, :370-405)
+ *   when Mamba2Block is trained (tests/test_mamba2.py:56-71).
+ *   fwd: the forward's arguments (y ignored); dy (b, L, D) like x;
+ *   dx (b, L, D) like x; d_conv_state (b, conv_state_len, D) like conv_state,
+ *   the gradient of the cached rows (NULL: not computed); dweight (D, width)
+ *   fp32 and dbias (D,) fp32 (or NULL) are overwritten with the sums over
+ *   batch and tokens, deterministic (per 32-token-run partials reduced in a
+ *   fixed order in the workspace).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  mh_conv1d_args fwd;
+  const void* dy; int64_t dy_stride_b, dy_stride_l;
+  void* dx; int64_t dx_stride_b, dx_stride_l;
+  void* d_conv_state; int64_t d_conv_state_stride_b, d_conv_state_stride_l;
+  float* dweight;
+  float* dbias;
+  void* workspace; size_t workspace_bytes;
+} mh_conv1d_bwd_args;
+
+/* Bytes of workspace mh_causal_conv1d_bwd needs for these sizes. */
+int mh_conv1d_bwd_workspace_bytes(const mh_conv1d_bwd_args* a, size_t* bytes);
+int mh_causal_conv1d_bwd(const mh_conv1d_bwd_args* a, void* stream);
 
 /* ------------------------------------------------------------------------ */
 int mh_abi_version(void);

@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MH_F32, MH_BF16 = 0, 1
 MH_DT_SOFTPLUS, MH_DT_LIMIT, MH_D_PER_CHANNEL = 1, 2, 4
@@ -112,6 +112,17 @@ class Conv1dArgs(ct.Structure):
 
 MH_CONV_SILU = 1
 
+
+class Conv1dBwdArgs(ct.Structure):
+    _fields_ = [
+        ("fwd", Conv1dArgs),
+        ("dy", _vp), ("dy_stride_b", _i64), ("dy_stride_l", _i64),
+        ("dx", _vp), ("dx_stride_b", _i64), ("dx_stride_l", _i64),
+        ("d_conv_state", _vp), ("d_conv_state_stride_b", _i64), ("d_conv_state_stride_l", _i64),
+        ("dweight", _vp), ("dbias", _vp),
+        ("workspace", _vp), ("workspace_bytes", _sz),
+    ]
+
 # every symbol include/mamformer_hip.h declares
 EXPORTS = (
     "mh_abi_version", "mh_last_error",
@@ -121,6 +132,7 @@ EXPORTS = (
     "mh_kda_chunk_scan_fwd",
     "mh_kda_recurrent_step",
     "mh_causal_conv1d_fwd",
+    "mh_conv1d_bwd_workspace_bytes", "mh_causal_conv1d_bwd",
 )
 
 _lock = threading.Lock()
@@ -158,9 +170,12 @@ def lib():
             h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
             h.mh_kda_recurrent_step.argtypes = [ct.POINTER(KdaStepArgs), _vp]
             h.mh_causal_conv1d_fwd.argtypes = [ct.POINTER(Conv1dArgs), _vp]
+            h.mh_conv1d_bwd_workspace_bytes.argtypes = [ct.POINTER(Conv1dBwdArgs), ct.POINTER(_sz)]
+            h.mh_causal_conv1d_bwd.argtypes = [ct.POINTER(Conv1dBwdArgs), _vp]
             for name in ("mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
                          "mh_ssd_state_update", "mh_kda_chunk_scan_fwd", "mh_kda_recurrent_step",
-                         "mh_causal_conv1d_fwd"):
+                         "mh_causal_conv1d_fwd", "mh_conv1d_bwd_workspace_bytes", "mh_causal_conv1d_bwd",
+                         "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd"):
                 getattr(h, name).restype = ct.c_int
             ver = h.mh_abi_version()
             if ver != ABI_VERSION:

@@ -278,6 +278,48 @@ int ssd_bwd_heads_per_wg(const mh_ssd_args* f) {
   return hb;
 }
 
+int conv_bwd_validate(const mh_conv1d_bwd_args* a) {
+  if (!a) return fail(MH_ERR_NULL, "conv1d_bwd: args is NULL");
+  mh_conv1d_args f = a->fwd;
+  f.y = const_cast<void*>(f.x);   // the forward output is not an input of the backward
+  f.y_stride_b = f.x_stride_b;
+  f.y_stride_l = f.x_stride_l;
+  int rc = conv_validate(&f);
+  if (rc) return rc;
+  const int es = elem_size(f.dtype);
+  if (!a->dweight) return fail(MH_ERR_NULL, "conv1d_bwd: dweight is required");
+  if (f.bias && !a->dbias) return fail(MH_ERR_NULL, "conv1d_bwd: dbias is required when bias is given");
+  if (f.seqlen > 0) {
+    if (!a->dy || !a->dx) return fail(MH_ERR_NULL, "conv1d_bwd: dy and dx are required");
+    if (!aligned16(a->dy) || !aligned16(a->dx)) return fail(MH_ERR_ALIGN, "conv1d_bwd: dy, dx must be 16-byte aligned");
+    if (!stride_ok(a->dy_stride_b, es) || !stride_ok(a->dy_stride_l, es) || !stride_ok(a->dx_stride_b, es) ||
+        !stride_ok(a->dx_stride_l, es))
+      return fail(MH_ERR_ALIGN, "conv1d_bwd: strides must be multiples of 16 bytes");
+    if (a->dy_stride_l < f.dim || a->dx_stride_l < f.dim)
+      return fail(MH_ERR_STRIDE, "conv1d_bwd: token stride smaller than dim (channels must be contiguous)");
+  }
+  if (a->d_conv_state && f.conv_state_len > 0) {
+    if (!aligned16(a->d_conv_state)) return fail(MH_ERR_ALIGN, "conv1d_bwd: d_conv_state must be 16-byte aligned");
+    if (!stride_ok(a->d_conv_state_stride_b, es) || !stride_ok(a->d_conv_state_stride_l, es))
+      return fail(MH_ERR_ALIGN, "conv1d_bwd: strides must be multiples of 16 bytes");
+    if (a->d_conv_state_stride_l < f.dim)
+      return fail(MH_ERR_STRIDE, "conv1d_bwd: token stride smaller than dim (channels must be contiguous)");
+  }
+  return MH_OK;
+}
+
+void conv_fill(const mh_conv1d_args* a, mh::Conv1dParams& p) {
+  memset(&p, 0, sizeof(p));
+  p.batch = (int)a->batch; p.seqlen = (int)a->seqlen; p.dim = (int)a->dim; p.width = (int)a->width;
+  p.dtype = a->dtype; p.silu = (a->flags & MH_CONV_SILU) != 0;
+  p.cs_len = (int)a->conv_state_len;
+  p.x = a->x; p.x_sb = a->x_stride_b; p.x_sl = a->x_stride_l;
+  p.weight = a->weight; p.bias = a->bias;
+  p.conv_state = a->conv_state_len > 0 ? a->conv_state : nullptr;
+  p.cs_sb = a->conv_state_stride_b; p.cs_sl = a->conv_state_stride_l;
+  p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l;
+}
+
 }  // namespace
 
 extern "C" {
@@ -373,16 +415,38 @@ int mh_causal_conv1d_fwd(const mh_conv1d_args* a, void* stream) {
   int rc = conv_validate(a);
   if (rc) return rc;
   mh::Conv1dParams p;
-  memset(&p, 0, sizeof(p));
-  p.batch = (int)a->batch; p.seqlen = (int)a->seqlen; p.dim = (int)a->dim; p.width = (int)a->width;
-  p.dtype = a->dtype; p.silu = (a->flags & MH_CONV_SILU) != 0;
-  p.cs_len = (int)a->conv_state_len;
-  p.x = a->x; p.x_sb = a->x_stride_b; p.x_sl = a->x_stride_l;
-  p.weight = a->weight; p.bias = a->bias;
-  p.conv_state = a->conv_state_len > 0 ? a->conv_state : nullptr;
-  p.cs_sb = a->conv_state_stride_b; p.cs_sl = a->conv_state_stride_l;
-  p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l;
+  conv_fill(a, p);
   return hip_status(mh::launch_conv1d(p, reinterpret_cast<hipStream_t>(stream)), "causal_conv1d_fwd");
+}
+
+int mh_conv1d_bwd_workspace_bytes(const mh_conv1d_bwd_args* a, size_t* bytes) {
+  if (!bytes) return fail(MH_ERR_NULL, "conv1d_bwd: bytes output is NULL");
+  int rc = conv_bwd_validate(a);
+  if (rc) return rc;
+  *bytes = mh::conv1d_bwd_workspace_bytes((int)a->fwd.batch, (int)a->fwd.seqlen, (int)a->fwd.dim, (int)a->fwd.width);
+  return MH_OK;
+}
+
+int mh_causal_conv1d_bwd(const mh_conv1d_bwd_args* a, void* stream) {
+  int rc = conv_bwd_validate(a);
+  if (rc) return rc;
+  const mh_conv1d_args* f = &a->fwd;
+  const size_t need = mh::conv1d_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->dim, (int)f->width);
+  if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+    return fail(MH_ERR_WORKSPACE, "conv1d_bwd: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
+                a->workspace_bytes);
+  mh::Conv1dBwdParams q;
+  memset(&q, 0, sizeof(q));
+  conv_fill(f, q.f);
+  q.f.y = nullptr;
+  q.dy = a->dy; q.dy_sb = a->dy_stride_b; q.dy_sl = a->dy_stride_l;
+  q.dx = a->dx; q.dx_sb = a->dx_stride_b; q.dx_sl = a->dx_stride_l;
+  q.dweight = a->dweight; q.dbias = f->bias ? a->dbias : nullptr;
+  if (f->conv_state_len > 0 && a->d_conv_state) {
+    q.dcs = a->d_conv_state; q.dcs_sb = a->d_conv_state_stride_b; q.dcs_sl = a->d_conv_state_stride_l;
+  }
+  mh::conv1d_bwd_workspace_layout(q, a->workspace);
+  return hip_status(mh::launch_conv1d_bwd(q, reinterpret_cast<hipStream_t>(stream)), "causal_conv1d_bwd");
 }
 
 int mh_ssd_bwd_workspace_bytes(const mh_ssd_bwd_args* a, size_t* bytes) {

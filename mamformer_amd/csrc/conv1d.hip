@@ -106,6 +106,179 @@ __global__ __launch_bounds__(256) void conv1d_kernel(Conv1dParams p) {
   }
 }
 
+// Backward: with u = bias + sum_j w_j xin[t - (K-1) + j] (recomputed) and du = dy * act'(u),
+//   dx[s] = sum_j w_j du[s + (K-1) - j],   dw_j += du[t] xin[t - (K-1) + j],   dbias += du[t].
+// A thread owns 8 channels and the TT tokens of its run for dx, dw and dbias, and recomputes du on the K-1
+// tokens after the run (the halo dx needs); the threads of run 0 also write the cached rows' gradient
+//   d_conv_state[S_c + s] = sum_j w_j du[s + (K-1) - j]  (s = -S_c .. -1)  when it is asked for.
+// dw / dbias leave as one fp32 partial per (batch, run), summed in a fixed order by conv1d_reduce_kernel.
+template <typename T, int K>
+__global__ __launch_bounds__(256) void conv1d_bwd_kernel(Conv1dBwdParams q) {
+  const Conv1dParams& p = q.f;
+  const int c8 = blockIdx.x * 256 + threadIdx.x;
+  const int d0 = c8 * CV;
+  if (d0 >= p.dim) return;
+  const int b = blockIdx.z;
+  const int t0 = blockIdx.y * TT;
+  const T* xb = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + d0;
+  const T* sb = p.conv_state ? reinterpret_cast<const T*>(p.conv_state) + (int64_t)b * p.cs_sb + d0 : nullptr;
+  const T* dyb = reinterpret_cast<const T*>(q.dy) + (int64_t)b * q.dy_sb + d0;
+  T* dxb = reinterpret_cast<T*>(q.dx) + (int64_t)b * q.dx_sb + d0;
+
+  float w[K][CV];
+#pragma unroll
+  for (int i = 0; i < CV; ++i)
+#pragma unroll
+    for (int j = 0; j < K; ++j) w[j][i] = p.weight[(int64_t)(d0 + i) * K + j];
+  float bias[CV];
+#pragma unroll
+  for (int i = 0; i < CV; ++i) bias[i] = p.bias ? p.bias[d0 + i] : 0.f;
+
+  float win[K][CV];       // win[j] = xin[t - (K-1) + j] for the current t
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) {
+    const int tp = t0 - (K - 1) + j;
+    if (tp >= 0) {
+      load8<T>(xb + (int64_t)tp * p.x_sl, win[j]);
+    } else if (sb && tp >= -p.cs_len) {
+      load8<T>(sb + (int64_t)(p.cs_len + tp) * p.cs_sl, win[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < CV; ++i) win[j][i] = 0.f;
+    }
+  }
+  float duw[K][CV];       // duw[K-1-j] = du[t - j]
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+#pragma unroll
+    for (int i = 0; i < CV; ++i) duw[j][i] = 0.f;
+  float dw[K][CV], db[CV];
+#pragma unroll
+  for (int i = 0; i < CV; ++i) {
+    db[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < K; ++j) dw[j][i] = 0.f;
+  }
+  const int tend = min(p.seqlen, t0 + TT);          // this run's tokens: [t0, tend)
+  const int tlast = min(p.seqlen, tend + K - 1);    // du needed up to tlast - 1
+  // gradient rows this thread stores: [slo, tend); run 0 also owns the cached rows -cs_len .. -1
+  const int slo = (t0 == 0 && q.dcs) ? -p.cs_len : t0;
+  T* dcsb = q.dcs ? reinterpret_cast<T*>(q.dcs) + (int64_t)b * q.dcs_sb + d0 : nullptr;
+  auto row = [&](int s) { return s >= 0 ? dxb + (int64_t)s * q.dx_sl : dcsb + (int64_t)(p.cs_len + s) * q.dcs_sl; };
+  for (int t = t0; t < tlast; ++t) {
+    load8<T>(xb + (int64_t)t * p.x_sl, win[K - 1]);
+    float g[CV];
+    load8<T>(dyb + (int64_t)t * q.dy_sl, g);
+    float du[CV];
+#pragma unroll
+    for (int i = 0; i < CV; ++i) {
+      float u = bias[i];
+#pragma unroll
+      for (int j = 0; j < K; ++j) u += w[j][i] * win[j][i];
+      if (p.silu) {
+        const float sg = 1.f / (1.f + __expf(-u));
+        du[i] = g[i] * sg * (1.f + u * (1.f - sg));
+      } else {
+        du[i] = g[i];
+      }
+    }
+    if (t < tend) {
+#pragma unroll
+      for (int i = 0; i < CV; ++i) {
+        db[i] += du[i];
+#pragma unroll
+        for (int j = 0; j < K; ++j) dw[j][i] += du[i] * win[j][i];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j)
+#pragma unroll
+      for (int i = 0; i < CV; ++i) {
+        duw[j][i] = duw[j + 1][i];
+        win[j][i] = win[j + 1][i];
+      }
+#pragma unroll
+    for (int i = 0; i < CV; ++i) duw[K - 1][i] = du[i];
+    const int s = t - (K - 1);
+    if (s >= slo) {
+      float o[CV];
+#pragma unroll
+      for (int i = 0; i < CV; ++i) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < K; ++j) acc += w[j][i] * duw[K - 1 - j][i];
+        o[i] = acc;
+      }
+      store8<T>(row(s), o);
+    }
+  }
+  // rows whose du window runs past the sequence end (du = 0 there).  The window advances one zero per s
+  // from s = tlast - (K-1) (the first s the main loop did not emit), so its last slot is du[s + K - 1]
+  // even when that s lies before slo (runs shorter than K - 1 tokens).
+  for (int s = tlast - (K - 1); s < tend; ++s) {
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j)
+#pragma unroll
+      for (int i = 0; i < CV; ++i) duw[j][i] = duw[j + 1][i];
+#pragma unroll
+    for (int i = 0; i < CV; ++i) duw[K - 1][i] = 0.f;
+    if (s < slo) continue;
+    float o[CV];
+#pragma unroll
+    for (int i = 0; i < CV; ++i) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < K; ++j) acc += w[j][i] * duw[K - 1 - j][i];
+      o[i] = acc;
+    }
+    store8<T>(row(s), o);
+  }
+  const int64_t part = (int64_t)b * gridDim.y + blockIdx.y;
+#pragma unroll
+  for (int i = 0; i < CV; ++i) {
+    q.db_part[part * p.dim + d0 + i] = db[i];
+#pragma unroll
+    for (int j = 0; j < K; ++j) q.dw_part[(part * p.dim + d0 + i) * K + j] = dw[j][i];
+  }
+}
+
+// dweight (D, K) and dbias (D,) = sums over the nparts partials, in a fixed order.
+__global__ __launch_bounds__(256) void conv1d_reduce_kernel(const float* __restrict__ dw_part,
+                                                            const float* __restrict__ db_part, int nparts, int dim,
+                                                            int K, float* __restrict__ dw, float* __restrict__ db) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  const int nw = dim * K;
+  if (e < nw) {
+    float acc = 0.f;
+    for (int k = 0; k < nparts; ++k) acc += dw_part[(int64_t)k * nw + e];
+    dw[e] = acc;
+  } else if (e < nw + dim && db) {
+    const int d = e - nw;
+    float acc = 0.f;
+    for (int k = 0; k < nparts; ++k) acc += db_part[(int64_t)k * dim + d];
+    db[d] = acc;
+  }
+}
+
+template <typename T>
+hipError_t launch_bwd_t(const Conv1dBwdParams& q, hipStream_t st) {
+  const Conv1dParams& p = q.f;
+  const int nrun = (p.seqlen + TT - 1) / TT;
+  dim3 grid((unsigned)((p.dim / CV + 255) / 256), (unsigned)nrun, (unsigned)p.batch);
+  switch (p.width) {
+#define CASE(K) case K: hipLaunchKernelGGL((conv1d_bwd_kernel<T, K>), grid, dim3(256), 0, st, q); break;
+    CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
+#undef CASE
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int n = p.dim * p.width + p.dim;
+  hipLaunchKernelGGL(conv1d_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, q.dw_part, q.db_part,
+                     p.batch * nrun, p.dim, p.width, q.dweight, q.dbias);
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_t(const Conv1dParams& p, hipStream_t st) {
   dim3 grid((unsigned)((p.dim / CV + 255) / 256), (unsigned)((p.seqlen + TT - 1) / TT), (unsigned)p.batch);
@@ -123,6 +296,52 @@ hipError_t launch_t(const Conv1dParams& p, hipStream_t st) {
 hipError_t launch_conv1d(const Conv1dParams& p, hipStream_t st) {
   if (p.seqlen == 0) return hipSuccess;
   return p.dtype == DT_BF16 ? launch_t<bf16>(p, st) : launch_t<float>(p, st);
+}
+
+// Empty sequence: zero weight, bias and cached-row gradients (kernels, not memset nodes).
+template <typename T>
+__global__ __launch_bounds__(256) void conv1d_zero_rows_kernel(T* __restrict__ d, int64_t sb, int64_t sl, int dim) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c < dim) d[(int64_t)blockIdx.z * sb + (int64_t)blockIdx.y * sl + c] = (T)0.f;
+}
+
+__global__ __launch_bounds__(256) void conv1d_zero_kernel(float* __restrict__ dw, float* __restrict__ db, int nw,
+                                                          int nd) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e < nw) dw[e] = 0.f;
+  else if (e < nw + nd && db) db[e - nw] = 0.f;
+}
+
+size_t conv1d_bwd_workspace_bytes(int batch, int seqlen, int dim, int width) {
+  const size_t nparts = (size_t)batch * ((seqlen + TT - 1) / TT);
+  return nparts * dim * (width + 1) * sizeof(float);
+}
+
+void conv1d_bwd_workspace_layout(Conv1dBwdParams& q, void* workspace) {
+  const Conv1dParams& p = q.f;
+  const size_t nparts = (size_t)p.batch * ((p.seqlen + TT - 1) / TT);
+  q.dw_part = reinterpret_cast<float*>(workspace);
+  q.db_part = q.dw_part + nparts * p.dim * p.width;
+}
+
+hipError_t launch_conv1d_bwd(const Conv1dBwdParams& q, hipStream_t st) {
+  const Conv1dParams& p = q.f;
+  if (p.seqlen == 0) {
+    const int n = p.dim * p.width + p.dim;
+    hipLaunchKernelGGL(conv1d_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, q.dweight, q.dbias,
+                       p.dim * p.width, p.dim);
+    if (q.dcs && p.cs_len > 0) {
+      const dim3 g((unsigned)((p.dim + 255) / 256), (unsigned)p.cs_len, (unsigned)p.batch);
+      if (p.dtype == DT_BF16)
+        hipLaunchKernelGGL(conv1d_zero_rows_kernel<bf16>, g, dim3(256), 0, st, reinterpret_cast<bf16*>(q.dcs),
+                           q.dcs_sb, q.dcs_sl, p.dim);
+      else
+        hipLaunchKernelGGL(conv1d_zero_rows_kernel<float>, g, dim3(256), 0, st, reinterpret_cast<float*>(q.dcs),
+                           q.dcs_sb, q.dcs_sl, p.dim);
+    }
+    return hipGetLastError();
+  }
+  return p.dtype == DT_BF16 ? launch_bwd_t<bf16>(q, st) : launch_bwd_t<float>(q, st);
 }
 
 }  // namespace mh

@@ -129,4 +129,18 @@ struct Conv1dParams {
 };
 hipError_t launch_conv1d(const Conv1dParams& p, hipStream_t st);
 
+struct Conv1dBwdParams {
+  Conv1dParams f;              // forward inputs (y unused)
+  const void* dy; int64_t dy_sb, dy_sl;
+  void* dx; int64_t dx_sb, dx_sl;
+  float* dweight;              // (dim, width)
+  float* dbias;                // (dim,) or null
+  void* dcs; int64_t dcs_sb, dcs_sl;   // gradient of the cs_len cached rows, or null
+  float* dw_part;              // workspace: per (batch, 32-token run) partial sums
+  float* db_part;
+};
+hipError_t launch_conv1d_bwd(const Conv1dBwdParams& q, hipStream_t st);
+size_t conv1d_bwd_workspace_bytes(int batch, int seqlen, int dim, int width);
+void conv1d_bwd_workspace_layout(Conv1dBwdParams& q, void* workspace);
+
 }  // namespace mh

@@ -41,7 +41,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import SsdArgs, SsdBwdArgs, SsuArgs, KdaArgs, Conv1dArgs
+from ._lib import SsdArgs, SsdBwdArgs, SsuArgs, KdaArgs, Conv1dArgs, Conv1dBwdArgs
 
 __all__ = ["selective_scan", "selective_scan_bwd", "plan_selective_scan_bwd", "selective_state_update", "recurrent_step", "linear_attn_scan",
            "linear_attn_scan_pair", "linear_attn_scan_single", "linear_attention_scan", "diff_lambda",
@@ -441,13 +441,74 @@ def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size):
     return hs.to(x4.dtype)
 
 
+def _conv_args(x, w, bc, cs, silu):
+    b, L, Dm = x.shape
+    a = Conv1dArgs()
+    a.batch, a.seqlen, a.dim, a.width = b, L, Dm, w.shape[1]
+    a.dtype = _DT[x.dtype]
+    a.flags = _lib.MH_CONV_SILU if silu else 0
+    a.x, a.x_stride_b, a.x_stride_l = _ptr(x), x.stride(0), x.stride(1)
+    a.weight, a.bias = _ptr(w), _ptr(bc)
+    if cs is not None and cs.shape[1] > 0:
+        a.conv_state, a.conv_state_len = _ptr(cs), cs.shape[1]
+        a.conv_state_stride_b, a.conv_state_stride_l = cs.stride(0), cs.stride(1)
+    return a
+
+
+def _conv_fwd(xc, w, bc, cs, silu):
+    y = torch.empty(xc.shape, device=xc.device, dtype=xc.dtype)
+    a = _conv_args(xc, w, bc, cs, silu)
+    a.y, a.y_stride_b, a.y_stride_l = _ptr(y), y.stride(0), y.stride(1)
+    _lib.call("mh_causal_conv1d_fwd", ct.byref(a), _stream(xc.device))
+    return y
+
+
+def _conv_bwd(dy, xc, w, bc, cs, silu, need_dcs):
+    dy = _inner_contig(dy.to(xc.dtype))
+    dx = torch.empty(xc.shape, device=xc.device, dtype=xc.dtype)
+    dcs = torch.empty(cs.shape, device=xc.device, dtype=xc.dtype) if (need_dcs and cs is not None) else None
+    dw = torch.empty(w.shape, device=xc.device, dtype=torch.float32)
+    db = torch.empty(w.shape[0], device=xc.device, dtype=torch.float32) if bc is not None else None
+    q = Conv1dBwdArgs()
+    q.fwd = _conv_args(xc, w, bc, cs, silu)
+    q.dy, q.dy_stride_b, q.dy_stride_l = _ptr(dy), dy.stride(0), dy.stride(1)
+    q.dx, q.dx_stride_b, q.dx_stride_l = _ptr(dx), dx.stride(0), dx.stride(1)
+    if dcs is not None:
+        q.d_conv_state, q.d_conv_state_stride_b, q.d_conv_state_stride_l = _ptr(dcs), dcs.stride(0), dcs.stride(1)
+    q.dweight, q.dbias = _ptr(dw), _ptr(db)
+    n = ct.c_size_t()
+    _lib.call("mh_conv1d_bwd_workspace_bytes", ct.byref(q), ct.byref(n))
+    ws = torch.empty(max(n.value, 16), device=xc.device, dtype=torch.uint8)
+    q.workspace, q.workspace_bytes = _ptr(ws), ws.numel()
+    _lib.call("mh_causal_conv1d_bwd", ct.byref(q), _stream(xc.device))
+    return dx, dw, db, dcs
+
+
+class _CausalConv1dFn(torch.autograd.Function):
+    """Autograd node of the HIP conv: forward = ``mh_causal_conv1d_fwd``, backward = ``mh_causal_conv1d_bwd``."""
+
+    @staticmethod
+    def forward(ctx, xc, w, bc, cs, silu):
+        y = _conv_fwd(xc, w, bc, cs, silu)
+        ctx.save_for_backward(xc, w, bc, cs)
+        ctx.silu = silu
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        xc, w, bc, cs = ctx.saved_tensors
+        dx, dw, db, dcs = _conv_bwd(dy, xc, w, bc, cs, ctx.silu, ctx.needs_input_grad[3])
+        return dx, dw, db, dcs, None
+
+
 def causal_conv1d(x, weight, bias=None, conv_state=None, *, silu=False):
     """Causal depthwise conv1d over channels-last x (b, L, D) on the GPU (+ SiLU when ``silu``).
 
     ``Mamba2Block._causal_conv1d`` counterpart (R/mamformer/layers/mamba2.py:370-405): weight (D, 1, K) or
     (D, K) as ``nn.Conv1d(D, D, K, groups=D)`` holds it, optional bias (D,); ``conv_state`` (b, S_c, D) with
     S_c <= K-1 are the cached raw inputs prepended on the incremental path (:388-390).  Returns y (b, L, D)
-    in the dtype of x (fp32 accumulation).
+    in the dtype of x (fp32 accumulation).  Differentiable in x, weight, bias and conv_state (backward
+    ``mh_causal_conv1d_bwd``, what autograd forms through the reference's conv + SiLU when the block trains).
     """
     _require_cuda("causal_conv1d", x, weight, bias, conv_state)
     if x.dim() != 3:
@@ -466,19 +527,11 @@ def causal_conv1d(x, weight, bias=None, conv_state=None, *, silu=False):
         if conv_state.shape[1] > K - 1:
             conv_state = conv_state[:, -(K - 1):] if K > 1 else conv_state[:, :0]
         cs = _inner_contig(conv_state.to(x.dtype))
-    y = torch.empty((b, L, Dm), device=x.device, dtype=x.dtype)
-    a = Conv1dArgs()
-    a.batch, a.seqlen, a.dim, a.width = b, L, Dm, K
-    a.dtype = _DT[x.dtype]
-    a.flags = _lib.MH_CONV_SILU if silu else 0
-    a.x, a.x_stride_b, a.x_stride_l = _ptr(xc), xc.stride(0), xc.stride(1)
-    a.weight, a.bias = _ptr(w), _ptr(bc)
-    if cs is not None and cs.shape[1] > 0:
-        a.conv_state, a.conv_state_len = _ptr(cs), cs.shape[1]
-        a.conv_state_stride_b, a.conv_state_stride_l = cs.stride(0), cs.stride(1)
-    a.y, a.y_stride_b, a.y_stride_l = _ptr(y), y.stride(0), y.stride(1)
-    _lib.call("mh_causal_conv1d_fwd", ct.byref(a), _stream(x.device))
-    return y
+    if cs is not None and cs.shape[1] == 0:
+        cs = None
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (xc, w, bc, cs)):
+        return _CausalConv1dFn.apply(xc, w, bc, cs, silu)
+    return _conv_fwd(xc, w, bc, cs, silu)
 
 
 def plan_selective_state_update(*args, **kw):

@@ -30,7 +30,7 @@ import numpy as np
 
 from .ssd import _expand_D, _groups_of, process_dt, softplus
 
-__all__ = ["ssd_backward", "dt_chain"]
+__all__ = ["ssd_backward", "dt_chain", "causal_conv1d_backward"]
 
 
 def dt_chain(dt_raw, dt_bias=None, dt_softplus=False, dt_limit=None):
@@ -122,3 +122,43 @@ def ssd_backward(x, dt_raw, A, B, C, D, dy, d_final=None, initial_state=None, dt
         Dn = np.asarray(D)
         res["dD"] = dDhp.sum(axis=1) if Dn.shape == (H,) else dDhp.reshape(Dn.shape)
     return res
+
+
+def causal_conv1d_backward(x, weight, bias, dy, conv_state=None, silu=False, with_state_grad=False):
+    """Gradients of <dy, y> for y = act(conv(x)), the causal depthwise conv of ``oracle.ssd.ref_causal_conv1d``
+    (R/mamformer/layers/mamba2.py:370-405) followed, when ``silu``, by the SiLU of mamba2.py:282-283.
+
+    With xin = [conv_state; x] (S cached rows first), u[t] = bias + sum_j w[:, j] xin[S + t - (K-1) + j] and
+    du = dy * act'(u) (act'(u) = s (1 + u (1 - s)), s = sigmoid(u), for the SiLU):
+        dxin[i] = sum_j w[:, j] du[i - S + (K-1) - j]   (du = 0 outside 0..L-1),
+        dw[:, j] = sum_{b,t} du[t] xin[S + t - (K-1) + j],   dbias = sum_{b,t} du[t].
+    Returns dx = dxin[:, S:] (b, L, D), dweight (D, K), dbias (D,) in float64, and with ``with_state_grad``
+    also d_conv_state = dxin[:, :S] (b, S, D).
+    """
+    from .ssd import ref_causal_conv1d
+
+    x = np.asarray(x, np.float64)
+    dy = np.asarray(dy, np.float64)
+    b, L, D = x.shape
+    w = np.asarray(weight, np.float64).reshape(D, -1)
+    K = w.shape[1]
+    u = ref_causal_conv1d(x, w, bias, conv_state)
+    if silu:
+        sg = 1.0 / (1.0 + np.exp(-u))
+        du = dy * sg * (1.0 + u * (1.0 - sg))
+    else:
+        du = dy
+    S = 0 if conv_state is None else np.asarray(conv_state).shape[1]
+    xin = x if conv_state is None else np.concatenate([np.asarray(conv_state, np.float64), x], axis=1)
+    pad = np.concatenate([np.zeros((b, K - 1, D)), xin], axis=1)          # pad[:, i] = xin[i - (K-1)]
+    dxin = np.zeros((b, S + L, D))
+    dw = np.zeros((D, K))
+    for j in range(K):
+        # y_t uses pad[S + t + j] = xin[S + t + j - (K-1)]  (t = 0..L-1)
+        dw[:, j] = np.einsum("btd,btd->d", du, pad[:, S + j:S + j + L])
+        for t in range(L):
+            i = S + t + j - (K - 1)
+            if i >= 0:
+                dxin[:, i] += w[None, :, j] * du[:, t]
+    res = (dxin[:, S:], dw, du.sum(axis=(0, 1)))
+    return res + (dxin[:, :S],) if with_state_grad else res

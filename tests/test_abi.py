@@ -10,7 +10,7 @@ import torch
 
 import mamformer_amd
 from mamformer_amd import _lib
-from mamformer_amd._lib import SsdBwdArgs, Conv1dArgs, KdaArgs, SsdArgs, SsuArgs
+from mamformer_amd._lib import SsdBwdArgs, Conv1dArgs, Conv1dBwdArgs, KdaArgs, SsdArgs, SsuArgs
 
 ROOT = Path(__file__).resolve().parent.parent
 
@@ -297,3 +297,50 @@ def test_ssd_bwd_rejects_small_workspace():
     a.workspace, a.workspace_bytes = ct.c_void_p(8192), 64
     assert _rc("mh_ssd_chunk_scan_bwd", ct.byref(a), None) == -7
     assert _rc("mh_ssd_chunk_scan_bwd", None, None) == -1
+
+
+def _good_conv_bwd():
+    q = Conv1dBwdArgs()
+    q.fwd = _good_conv()
+    q.fwd.y = None                                       # the forward output is not an input of the backward
+    q.fwd.y_stride_b = q.fwd.y_stride_l = 0
+    fake = ct.c_void_p(8192)
+    q.dy = q.dx = q.dweight = fake
+    q.dy_stride_l = q.dx_stride_l = 256
+    q.dy_stride_b = q.dx_stride_b = 50 * 256
+    return q
+
+
+def test_conv1d_bwd_workspace():
+    q = _good_conv_bwd()
+    n = ct.c_size_t()
+    assert _rc("mh_conv1d_bwd_workspace_bytes", ct.byref(q), ct.byref(n)) == 0
+    # one fp32 (dweight, dbias) partial per (batch, 32-token run)
+    assert n.value == 2 * 2 * 256 * (4 + 1) * 4
+    q.fwd.seqlen = 0
+    assert _rc("mh_conv1d_bwd_workspace_bytes", ct.byref(q), ct.byref(n)) == 0 and n.value == 0
+
+
+@pytest.mark.parametrize("mutate,code,word", [
+    (lambda q: setattr(q, "dweight", None), -1, b"dweight"),
+    (lambda q: setattr(q, "dy", None), -1, b"dy"),
+    (lambda q: setattr(q.fwd, "bias", ct.c_void_p(4096)), -1, b"dbias"),
+    (lambda q: setattr(q, "dx", ct.c_void_p(8192 + 4)), -5, b"aligned"),
+    (lambda q: setattr(q, "dy_stride_l", 100), -5, b"16 bytes"),
+    (lambda q: setattr(q, "dx_stride_l", 128), -4, b"token stride"),
+    (lambda q: setattr(q.fwd, "width", 9), -6, b"width"),
+])
+def test_conv1d_bwd_rejects_bad_arguments(mutate, code, word):
+    q = _good_conv_bwd()
+    mutate(q)
+    n = ct.c_size_t()
+    assert _rc("mh_conv1d_bwd_workspace_bytes", ct.byref(q), ct.byref(n)) == code
+    assert word in _lib.lib().mh_last_error()
+    assert _rc("mh_causal_conv1d_bwd", ct.byref(q), None) == code
+
+
+def test_conv1d_bwd_rejects_small_workspace():
+    q = _good_conv_bwd()
+    q.workspace, q.workspace_bytes = ct.c_void_p(8192), 64
+    assert _rc("mh_causal_conv1d_bwd", ct.byref(q), None) == -7
+    assert _rc("mh_causal_conv1d_bwd", None, None) == -1

@@ -160,3 +160,44 @@ def test_planted_mistakes_are_caught(rng, plant):
         got = ssd_bwd.ssd_backward(x, dtp, A, B, C, D, dy, d_final=dfin)
         got["dx"] = got["dx"] - dtp[..., None] * np.einsum("blgn,blgn->blg", B, C).repeat(2, axis=2)[..., None] * dy
     assert max(rel_l2(got[k], ref[k]) for k in GRADS) > 1e-3
+
+
+@pytest.mark.parametrize("silu,K,S", [(True, 4, 0), (False, 3, 2), (True, 2, 1), (True, 1, 0)])
+def test_conv1d_backward_matches_autograd(rng, silu, K, S):
+    """Against torch autograd of F.conv1d (depthwise, left padding K-1, cached rows prepended) + SiLU, float64."""
+    b, L, D = 2, 9, 5
+    x = rng.standard_normal((b, L, D))
+    w = rng.standard_normal((D, K))
+    bias = rng.standard_normal(D)
+    dy = rng.standard_normal((b, L, D))
+    cs = rng.standard_normal((b, S, D)) if S else None
+    xt = torch.tensor(x, requires_grad=True)
+    wt = torch.tensor(w, requires_grad=True)
+    bt = torch.tensor(bias, requires_grad=True)
+    cst = torch.tensor(cs, requires_grad=True) if S else None
+    xin = xt if cs is None else torch.cat([cst, xt], dim=1)
+    u = torch.nn.functional.conv1d(torch.nn.functional.pad(xin.transpose(1, 2), (K - 1, 0)), wt[:, None, :], bt,
+                                   groups=D).transpose(1, 2)[:, -L:]
+    y = torch.nn.functional.silu(u) if silu else u
+    (y * torch.tensor(dy)).sum().backward()
+    dx, dw, db, dcs = ssd_bwd.causal_conv1d_backward(x, w, bias, dy, conv_state=cs, silu=silu, with_state_grad=True)
+    assert rel_l2(dx, xt.grad.numpy()) < 1e-12
+    assert rel_l2(dw, wt.grad.numpy()) < 1e-12
+    assert rel_l2(db, bt.grad.numpy()) < 1e-12
+    assert dcs.shape == (b, S, D)
+    if S:
+        assert rel_l2(dcs, cst.grad.numpy()) < 1e-12
+
+
+def test_conv1d_backward_planted_mistake_is_caught(rng):
+    """A reversed kernel (convolution instead of the reference's cross-correlation) in the oracle's dx fails."""
+    b, L, D, K = 1, 7, 3, 4
+    x, w, bias, dy = rng.standard_normal((b, L, D)), rng.standard_normal((D, K)), rng.standard_normal(D), \
+        rng.standard_normal((b, L, D))
+    dx, _, _ = ssd_bwd.causal_conv1d_backward(x, w, bias, dy, silu=True)
+    dx_flip, _, _ = ssd_bwd.causal_conv1d_backward(x, w[:, ::-1], bias, dy, silu=True)
+    xt = torch.tensor(x, requires_grad=True)
+    u = torch.nn.functional.conv1d(torch.nn.functional.pad(xt.transpose(1, 2), (K - 1, 0)),
+                                   torch.tensor(w)[:, None, :], torch.tensor(bias), groups=D).transpose(1, 2)
+    (torch.nn.functional.silu(u) * torch.tensor(dy)).sum().backward()
+    assert rel_l2(dx, xt.grad.numpy()) < 1e-12 and rel_l2(dx_flip, xt.grad.numpy()) > 1e-2
