@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MH_ABI_VERSION 4
+#define MH_ABI_VERSION 5
 
 /* element types of x / B / C / y / q / k / v / o */
 enum { MH_F32 = 0, MH_BF16 = 1 };
@@ -186,6 +186,37 @@ typedef struct {
 } mh_kda_args;
 
 int mh_kda_chunk_scan_fwd(const mh_kda_args* a, void* stream);
+
+/* Backward of the reference-mode scan (fwd.mode == MH_KDA_REFERENCE): the
+ *   gradient PyTorch autograd forms through LinearDiffAttention._linear_attention_scan
+ *   (mamformer/layers/kda_diff.py:357-478) when the layer is trained.
+ *   fwd: the forward's arguments (o, o2, final_state, final_z ignored).
+ *   flags MH_KDA_BWD_DIFF: do1 is the gradient of the fused differential output
+ *     (o1 - lam o2) / (1 - lam + 1e-8) (needs q2; lam from fwd.lam / lam_per_head)
+ *     and d_lam (H,) fp32, if given, receives its gradient w.r.t. lam;
+ *   otherwise do1 / do2 are the gradients of o1 / o2 (do2 NULL = zero).
+ *   d_final_state (B,H,dk,dv) / d_final_z (B,H,dk) fp32: gradients of the final
+ *   state and normaliser, or NULL (zero).
+ *   Outputs dq1, dq2 (when q2), dk, dv (B,H,S,128) bf16 (zero beyond kernel_dim
+ *   for dq, dk); d_initial_state / d_initial_z fp32 or NULL.
+ *   Supported: bf16, dk = dv = 128.
+ * ---------------------------------------------------------------------- */
+enum { MH_KDA_BWD_DIFF = 1 };
+
+typedef struct {
+  mh_kda_args fwd;
+  int32_t flags;
+  const void* do1; const void* do2;
+  const float* d_final_state; const float* d_final_z;
+  void* dq1; void* dq2; void* dk; void* dv;
+  float* d_initial_state; float* d_initial_z;
+  float* d_lam;
+  void* workspace; size_t workspace_bytes;
+} mh_kda_bwd_args;
+
+/* Bytes of workspace mh_kda_chunk_scan_bwd needs for these sizes. */
+int mh_kda_bwd_workspace_bytes(const mh_kda_bwd_args* a, size_t* bytes);
+int mh_kda_chunk_scan_bwd(const mh_kda_bwd_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
  * One-token step of the reference-mode scan (KDA decode).

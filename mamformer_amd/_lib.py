@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 MH_F32, MH_BF16 = 0, 1
 MH_DT_SOFTPLUS, MH_DT_LIMIT, MH_D_PER_CHANNEL = 1, 2, 4
@@ -99,6 +99,21 @@ class KdaStepArgs(ct.Structure):
     ]
 
 
+class KdaBwdArgs(ct.Structure):
+    _fields_ = [
+        ("fwd", KdaArgs), ("flags", _i32),
+        ("do1", _vp), ("do2", _vp),
+        ("d_final_state", _vp), ("d_final_z", _vp),
+        ("dq1", _vp), ("dq2", _vp), ("dk", _vp), ("dv", _vp),
+        ("d_initial_state", _vp), ("d_initial_z", _vp),
+        ("d_lam", _vp),
+        ("workspace", _vp), ("workspace_bytes", _sz),
+    ]
+
+
+MH_KDA_BWD_DIFF = 1
+
+
 class Conv1dArgs(ct.Structure):
     _fields_ = [
         ("batch", _i64), ("seqlen", _i64), ("dim", _i64), ("width", _i64),
@@ -129,7 +144,7 @@ EXPORTS = (
     "mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
     "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",
     "mh_ssd_state_update",
-    "mh_kda_chunk_scan_fwd",
+    "mh_kda_chunk_scan_fwd", "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
     "mh_kda_recurrent_step",
     "mh_causal_conv1d_fwd",
     "mh_conv1d_bwd_workspace_bytes", "mh_causal_conv1d_bwd",
@@ -169,13 +184,16 @@ def lib():
             h.mh_ssd_state_update.argtypes = [ct.POINTER(SsuArgs), _vp]
             h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
             h.mh_kda_recurrent_step.argtypes = [ct.POINTER(KdaStepArgs), _vp]
+            h.mh_kda_bwd_workspace_bytes.argtypes = [ct.POINTER(KdaBwdArgs), ct.POINTER(_sz)]
+            h.mh_kda_chunk_scan_bwd.argtypes = [ct.POINTER(KdaBwdArgs), _vp]
             h.mh_causal_conv1d_fwd.argtypes = [ct.POINTER(Conv1dArgs), _vp]
             h.mh_conv1d_bwd_workspace_bytes.argtypes = [ct.POINTER(Conv1dBwdArgs), ct.POINTER(_sz)]
             h.mh_causal_conv1d_bwd.argtypes = [ct.POINTER(Conv1dBwdArgs), _vp]
             for name in ("mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
                          "mh_ssd_state_update", "mh_kda_chunk_scan_fwd", "mh_kda_recurrent_step",
                          "mh_causal_conv1d_fwd", "mh_conv1d_bwd_workspace_bytes", "mh_causal_conv1d_bwd",
-                         "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd"):
+                         "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",
+                         "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd"):
                 getattr(h, name).restype = ct.c_int
             ver = h.mh_abi_version()
             if ver != ABI_VERSION:

@@ -157,7 +157,8 @@ int kda_validate(const mh_kda_args* a) {
   if (a->mode != MH_KDA_GATED && a->mode != MH_KDA_REFERENCE) return fail(MH_ERR_UNSUPPORTED, "kda: unknown mode %d", a->mode);
   if (a->dk != 128 || a->dv != 128)
     return fail(MH_ERR_UNSUPPORTED, "kda: dk=%lld dv=%lld not supported (128, 128)", (long long)a->dk, (long long)a->dv);
-  if (!a->q1 || !a->k || !a->v || !a->o) return fail(MH_ERR_NULL, "kda: q1, k, v, o are required");
+  if (a->seqlen > 0 && (!a->q1 || !a->k || !a->v || !a->o))
+    return fail(MH_ERR_NULL, "kda: q1, k, v, o are required");
   if (a->mode == MH_KDA_REFERENCE) {
     if (a->kernel_dim <= 0) return fail(MH_ERR_SHAPE, "kda: kernel_dim must be positive");
     if (a->g) return fail(MH_ERR_SHAPE, "kda: reference mode takes no gate g");
@@ -320,6 +321,42 @@ void conv_fill(const mh_conv1d_args* a, mh::Conv1dParams& p) {
   p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l;
 }
 
+void kda_fill(const mh_kda_args* a, mh::KdaParams& p) {
+  memset(&p, 0, sizeof(p));
+  p.batch = (int)a->batch; p.nheads = (int)a->nheads; p.seqlen = (int)a->seqlen; p.dk = (int)a->dk;
+  p.dv = (int)a->dv; p.dtype = a->dtype; p.mode = a->mode;
+  p.kernel_dim = a->kernel_dim < (int32_t)a->dk ? a->kernel_dim : (int32_t)a->dk;
+  p.lam = a->lam; p.lam_h = a->lam_per_head;
+  p.q1 = a->q1; p.q2 = a->q2; p.k = a->k; p.v = a->v; p.g = a->g;
+  p.init_state = a->initial_state; p.init_z = a->initial_z;
+  p.final_state = a->final_state; p.final_z = a->final_z;
+  p.o = a->o; p.o2 = a->o2;
+}
+
+int kda_bwd_validate(const mh_kda_bwd_args* a) {
+  if (!a) return fail(MH_ERR_NULL, "kda_bwd: args is NULL");
+  mh_kda_args f = a->fwd;
+  if (!f.o) f.o = const_cast<void*>(f.v);   // the forward outputs are not inputs of the backward
+  f.o2 = nullptr;
+  int rc = kda_validate(&f);
+  if (rc) return rc;
+  if (f.mode != MH_KDA_REFERENCE)
+    return fail(MH_ERR_UNSUPPORTED, "kda_bwd: only the reference mode has a backward (the gated operator has no "
+                                    "reference training path)");
+  if (a->flags & ~MH_KDA_BWD_DIFF) return fail(MH_ERR_UNSUPPORTED, "kda_bwd: unknown flags 0x%x", a->flags);
+  const bool diff = (a->flags & MH_KDA_BWD_DIFF) != 0;
+  if (diff && !f.q2 && f.seqlen > 0) return fail(MH_ERR_NULL, "kda_bwd: the differential output needs q2");
+  if (diff && a->do2) return fail(MH_ERR_SHAPE, "kda_bwd: do2 is not used with the differential output");
+  if (f.seqlen > 0 && !a->do1) return fail(MH_ERR_NULL, "kda_bwd: do1 is required");
+  if (f.seqlen > 0 && (!a->dq1 || !a->dk || !a->dv || (f.q2 && !a->dq2)))
+    return fail(MH_ERR_NULL, "kda_bwd: dq1, dk, dv (and dq2 with q2) are required");
+  if (!f.q2 && f.seqlen > 0 && (a->dq2 || a->do2)) return fail(MH_ERR_NULL, "kda_bwd: dq2 / do2 given without q2");
+  if (!aligned16(a->do1) || (a->do2 && !aligned16(a->do2)) || !aligned16(a->dq1) || (a->dq2 && !aligned16(a->dq2)) ||
+      !aligned16(a->dk) || !aligned16(a->dv))
+    return fail(MH_ERR_ALIGN, "kda_bwd: tensors must be 16-byte aligned");
+  return MH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -385,16 +422,41 @@ int mh_kda_chunk_scan_fwd(const mh_kda_args* a, void* stream) {
   int rc = kda_validate(a);
   if (rc) return rc;
   mh::KdaParams p;
-  memset(&p, 0, sizeof(p));
-  p.batch = (int)a->batch; p.nheads = (int)a->nheads; p.seqlen = (int)a->seqlen; p.dk = (int)a->dk;
-  p.dv = (int)a->dv; p.dtype = a->dtype; p.mode = a->mode;
-  p.kernel_dim = a->kernel_dim < (int32_t)a->dk ? a->kernel_dim : (int32_t)a->dk;
-  p.lam = a->lam; p.lam_h = a->lam_per_head;
-  p.q1 = a->q1; p.q2 = a->q2; p.k = a->k; p.v = a->v; p.g = a->g;
-  p.init_state = a->initial_state; p.init_z = a->initial_z;
-  p.final_state = a->final_state; p.final_z = a->final_z;
-  p.o = a->o; p.o2 = a->o2;
+  kda_fill(a, p);
   return hip_status(mh::launch_kda(p, reinterpret_cast<hipStream_t>(stream)), "kda_chunk_scan_fwd");
+}
+
+int mh_kda_bwd_workspace_bytes(const mh_kda_bwd_args* a, size_t* bytes) {
+  if (!bytes) return fail(MH_ERR_NULL, "kda_bwd: bytes output is NULL");
+  int rc = kda_bwd_validate(a);
+  if (rc) return rc;
+  const mh_kda_args* f = &a->fwd;
+  *bytes = mh::kda_bwd_workspace_bytes((int)f->batch, (int)f->nheads, (int)f->seqlen, f->q2 ? 2 : 1);
+  return MH_OK;
+}
+
+int mh_kda_chunk_scan_bwd(const mh_kda_bwd_args* a, void* stream) {
+  int rc = kda_bwd_validate(a);
+  if (rc) return rc;
+  const mh_kda_args* f = &a->fwd;
+  const int nq = f->q2 ? 2 : 1;
+  const size_t need = mh::kda_bwd_workspace_bytes((int)f->batch, (int)f->nheads, (int)f->seqlen, nq);
+  if (f->seqlen > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+    return fail(MH_ERR_WORKSPACE, "kda_bwd: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
+                a->workspace_bytes);
+  mh::KdaBwdParams q;
+  memset(&q, 0, sizeof(q));
+  kda_fill(f, q.f);
+  q.f.o = nullptr; q.f.o2 = nullptr; q.f.final_state = nullptr; q.f.final_z = nullptr;
+  q.nq = nq;
+  q.diff = (a->flags & MH_KDA_BWD_DIFF) != 0;
+  q.do1 = a->do1; q.do2 = q.diff ? nullptr : a->do2;
+  q.d_final = a->d_final_state; q.d_final_z = a->d_final_z;
+  q.dq1 = a->dq1; q.dq2 = a->dq2; q.dk = a->dk; q.dv = a->dv;
+  q.dS0 = a->d_initial_state; q.dz0 = a->d_initial_z;
+  q.dlam = q.diff ? a->d_lam : nullptr;
+  if (f->seqlen > 0) mh::kda_bwd_workspace_layout(q, a->workspace);
+  return hip_status(mh::launch_kda_bwd(q, reinterpret_cast<hipStream_t>(stream)), "kda_chunk_scan_bwd");
 }
 
 int mh_kda_recurrent_step(const mh_kda_step_args* a, void* stream) {

@@ -102,6 +102,25 @@ struct KdaParams {
 };
 hipError_t launch_kda(const KdaParams& p, hipStream_t st);
 
+// Backward of the reference-mode scan (kda_backward.hip).
+struct KdaBwdParams {
+  KdaParams f;               // forward inputs (mode 1; o, o2, final_state, final_z unused)
+  int nq;                    // query streams (1 or 2)
+  int diff;                  // 1: do1 is the gradient of the fused (o1 - lam o2) / (1 - lam + 1e-8)
+  const void* do1; const void* do2;     // (B,H,S,dv) bf16; null = zero
+  const float* d_final;      // (B,H,dk,dv) gradient of the final state, or null
+  const float* d_final_z;    // (B,H,dk) gradient of the final normaliser, or null
+  void* dq1; void* dq2; void* dk; void* dv;   // (B,H,S,128) bf16
+  float* dS0;                // (B,H,dk,dv) or null
+  float* dz0;                // (B,H,dk) or null
+  float* dlam;               // (H,) or null (diff mode)
+  float* nbuf; float* dnbuf; // workspace: n_t and dn_t per (query, b, h, token)
+  float* lam_part;           // workspace: sum dout . o_i per (query, b, h)
+};
+hipError_t launch_kda_bwd(const KdaBwdParams& q, hipStream_t st);
+size_t kda_bwd_workspace_bytes(int batch, int nheads, int seqlen, int nq);
+void kda_bwd_workspace_layout(KdaBwdParams& q, void* workspace);
+
 // ------------------------------------------------------------- KDA one-token step
 struct KdaStepParams {
   int batch, nheads, dk, dv, dtype;

@@ -47,7 +47,7 @@ __all__ = ["selective_scan", "selective_scan_bwd", "plan_selective_scan_bwd", "s
            "linear_attn_scan_pair", "linear_attn_scan_single", "linear_attention_scan", "diff_lambda",
            "linear_attn_step", "linear_attention_recurrent",
            "ssd_chunk_len", "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan",
-           "plan_linear_attn_step", "causal_conv1d"]
+           "plan_linear_attn_step", "causal_conv1d", "linear_attn_scan_bwd"]
 
 _DT = {torch.float32: _lib.MH_F32, torch.bfloat16: _lib.MH_BF16}
 
@@ -712,6 +712,14 @@ def linear_attn_scan(q1, q2, k, v, *, g=None, lam=0.8, mode="gated", kernel_dim=
         if not ref_mode or initial_z.numel() != Bb * H * dk:
             raise ValueError("linear_attn_scan: initial_z (B, H, dk) is a reference-mode input")
         z0 = initial_z.reshape(Bb, H, dk).to(torch.float32).contiguous()
+    if not _plan_only and torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (q1c, q2c, kc, vc, gc, lam_h, s0, z0)):
+        if not ref_mode:
+            raise RuntimeError("linear_attn_scan: the gated operator has no backward (it has no reference "
+                               "training path); use mode='reference' or call it under torch.no_grad()")
+        cfg = (a_kernel_dim(kernel_dim, dk), pair, return_final_state, lam_f)
+        outs = _KdaRefFn.apply(q1c, q2c, kc, vc, lam_h, s0, z0, cfg)
+        return outs if len(outs) > 1 else outs[0]
     o = torch.empty((Bb, H, S, dv), device=q1.device, dtype=q1.dtype)
     o2 = torch.empty((Bb, H, S, dv), device=q1.device, dtype=q1.dtype) if pair else None
     fin = torch.empty((Bb, H, dk, dv), device=q1.device, dtype=torch.float32) if return_final_state else None
@@ -737,6 +745,119 @@ def linear_attn_scan(q1, q2, k, v, *, g=None, lam=0.8, mode="gated", kernel_dim=
     if return_final_state:
         out = out + ((fin, finz) if ref_mode else (fin,))
     return out if len(out) > 1 else out[0]
+
+
+def a_kernel_dim(kernel_dim, dk):
+    return int(kernel_dim) if kernel_dim is not None else dk
+
+
+class _KdaRefFn(torch.autograd.Function):
+    """Autograd node of the reference-mode KDA scan: forward = ``mh_kda_chunk_scan_fwd``, backward =
+    ``mh_kda_chunk_scan_bwd`` (the gradient autograd forms through kda_diff.py:357-478)."""
+
+    @staticmethod
+    def forward(ctx, q1, q2, k, v, lam_h, s0, z0, cfg):
+        kd, pair, ret_fin, lam_f = cfg
+        res = linear_attn_scan(q1, q2, k, v, mode="reference", kernel_dim=kd, lam=lam_h if lam_h is not None
+                               else lam_f, initial_state=s0, initial_z=z0, return_final_state=ret_fin, pair=pair)
+        res = res if isinstance(res, tuple) else (res,)
+        ctx.save_for_backward(q1, q2, k, v, lam_h, s0, z0)
+        ctx.cfg = cfg
+        return res
+
+    @staticmethod
+    def backward(ctx, *grads):
+        q1, q2, k, v, lam_h, s0, z0 = ctx.saved_tensors
+        kd, pair, ret_fin, lam_f = ctx.cfg
+        n_o = 2 if pair else 1
+        g_o = list(grads[:n_o])
+        g_fin, g_finz = (grads[n_o], grads[n_o + 1]) if ret_fin else (None, None)
+        r = linear_attn_scan_bwd(q1, q2, k, v, kernel_dim=kd, lam=lam_h if lam_h is not None else lam_f,
+                                 do1=g_o[0], do2=g_o[1] if pair else None, pair=pair, initial_state=s0,
+                                 initial_z=z0, d_final_state=g_fin, d_final_z=g_finz,
+                                 need_initial=(ctx.needs_input_grad[5] or ctx.needs_input_grad[6]))
+        dlam = r.get("d_lam") if (lam_h is not None and ctx.needs_input_grad[4]) else None
+        return (r["dq1"], r.get("dq2"), r["dk"], r["dv"], dlam,
+                r.get("d_initial_state") if ctx.needs_input_grad[5] else None,
+                r.get("d_initial_z") if ctx.needs_input_grad[6] else None, None)
+
+
+def linear_attn_scan_bwd(q1, q2, k, v, *, kernel_dim=None, lam=0.8, do1=None, do2=None, pair=False,
+                         initial_state=None, initial_z=None, d_final_state=None, d_final_z=None, need_initial=True):
+    """Gradients of the reference-mode scan (``linear_attn_scan(..., mode="reference")``) on the GPU.
+
+    Loss = <do1, o1> + <do2, o2> (``pair=True``), <do1, out> for the fused differential output
+    out = (o1 - lam o2) / (1 - lam + 1e-8) (two queries, ``pair=False``) or <do1, o1> (single query), plus
+    <d_final_state, S_final> + <d_final_z, z_final>.  Shapes as ``linear_attn_scan``; any gradient may be None
+    (zero).  Returns a dict: dq1, dq2 (with q2), dk, dv (dtype of q1), d_lam (H,) fp32 for the differential
+    output, and with ``need_initial`` d_initial_state (B, H, dk, dv) and d_initial_z (B, H, dk) fp32.
+    """
+    _require_cuda("linear_attn_scan_bwd", q1, q2, k, v, do1, do2, initial_state, initial_z, d_final_state,
+                  d_final_z)
+    Bb, H, S, dk = q1.shape
+    dv = v.shape[-1]
+    if q1.dtype not in _DT or any(t is not None and t.dtype != q1.dtype for t in (q2, k, v)):
+        raise TypeError("linear_attn_scan_bwd: q1, q2, k, v must share a dtype")
+    if pair and q2 is None:
+        raise ValueError("linear_attn_scan_bwd: pair=True needs q2")
+    diff = q2 is not None and not pair
+    q1c, kc, vc = q1.contiguous(), k.contiguous(), v.contiguous()
+    q2c = q2.contiguous() if q2 is not None else None
+
+    def grad_like(t):
+        return None if t is None else t.to(q1.dtype).contiguous()
+
+    do1c = grad_like(do1) if do1 is not None else torch.zeros_like(vc)
+    do2c = grad_like(do2) if (pair and do2 is not None) else None
+    lam_h = None
+    if torch.is_tensor(lam):
+        lam_h = lam.to(device=q1.device, dtype=torch.float32).reshape(-1).contiguous()
+        lam_f = 0.0
+    else:
+        lam_f = float(lam)
+
+    def f32(t, n):
+        if t is None:
+            return None
+        if t.numel() != n:
+            raise ValueError("linear_attn_scan_bwd: state tensors must be (B, H, dk, dv) / (B, H, dk)")
+        return t.to(torch.float32).contiguous()
+
+    s0, z0 = f32(initial_state, Bb * H * dk * dv), f32(initial_z, Bb * H * dk)
+    dfs, dfz = f32(d_final_state, Bb * H * dk * dv), f32(d_final_z, Bb * H * dk)
+    dq1 = torch.empty_like(q1c)
+    dq2 = torch.empty_like(q2c) if q2c is not None else None
+    dkk, dvv = torch.empty_like(kc), torch.empty_like(vc)
+    dS0 = torch.empty((Bb, H, dk, dv), device=q1.device, dtype=torch.float32) if need_initial else None
+    dz0 = torch.empty((Bb, H, dk), device=q1.device, dtype=torch.float32) if need_initial else None
+    dlam = torch.empty(H, device=q1.device, dtype=torch.float32) if diff else None
+    a = _lib.KdaBwdArgs()
+    f = a.fwd
+    f.batch, f.nheads, f.seqlen, f.dk, f.dv = Bb, H, S, dk, dv
+    f.dtype = _DT[q1.dtype]
+    f.mode = _lib.MH_KDA_REFERENCE
+    f.kernel_dim = a_kernel_dim(kernel_dim, dk)
+    f.lam, f.lam_per_head = lam_f, _ptr(lam_h)
+    f.q1, f.q2, f.k, f.v = _ptr(q1c), _ptr(q2c), _ptr(kc), _ptr(vc)
+    f.initial_state, f.initial_z = _ptr(s0), _ptr(z0)
+    a.flags = _lib.MH_KDA_BWD_DIFF if diff else 0
+    a.do1, a.do2 = _ptr(do1c), _ptr(do2c)
+    a.d_final_state, a.d_final_z = _ptr(dfs), _ptr(dfz)
+    a.dq1, a.dq2, a.dk, a.dv = _ptr(dq1), _ptr(dq2), _ptr(dkk), _ptr(dvv)
+    a.d_initial_state, a.d_initial_z, a.d_lam = _ptr(dS0), _ptr(dz0), _ptr(dlam)
+    n = ct.c_size_t()
+    _lib.call("mh_kda_bwd_workspace_bytes", ct.byref(a), ct.byref(n))
+    ws = torch.empty(max(n.value, 16), device=q1.device, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = _ptr(ws), ws.numel()
+    _lib.call("mh_kda_chunk_scan_bwd", ct.byref(a), _stream(q1.device))
+    res = {"dq1": dq1, "dk": dkk, "dv": dvv}
+    if dq2 is not None:
+        res["dq2"] = dq2
+    if dlam is not None:
+        res["d_lam"] = dlam
+    if need_initial:
+        res["d_initial_state"], res["d_initial_z"] = dS0, dz0
+    return res
 
 
 def linear_attn_scan_pair(q1, q2, k, v, kernel_dim, block_k=128, block_d=128, group_h=0):

@@ -19,6 +19,8 @@ and this module states its gradient as the adjoint recurrence, token by token:
     dphi(k_t) = Lam_t v_t + zeta_t,       dv_t = Lam_t^T phi(k_t)
     dS_0 = Lam_0,  dz_0 = zeta_0          (gradients of the initial state and normaliser)
 
+starting from Lam_L = d_final_state, zeta_L = d_final_z (zero unless the final state enters the loss).
+
 with dq = dphi(q) * phi'(q) (phi' = 1 above 0, e^x at or below, 0 beyond channel K) and the same for dk.
 Pinned in ``tests/test_oracle_kda_bwd.py`` against torch autograd of the attention-matrix form
 (row-normalised causal phi(q) phi(k)^T weights), against finite differences, and by planted mistakes.
@@ -39,8 +41,10 @@ def phi_grad(x, K):
     return np.where(x > 0, 1.0, np.exp(np.minimum(x, 0.0)))
 
 
-def ref_scan_pair_backward(q1, q2, k, v, kernel_dim, do1, do2=None, initial_state=None, initial_z=None):
-    """Gradients of <do1, o1> + <do2, o2> for (o1, o2) = the reference-mode scan (``oracle.kda.ref_scan_pair``).
+def ref_scan_pair_backward(q1, q2, k, v, kernel_dim, do1, do2=None, initial_state=None, initial_z=None,
+                           d_final_state=None, d_final_z=None):
+    """Gradients of <do1, o1> + <do2, o2> (+ <d_final_state, S_L> + <d_final_z, z_L>) for (o1, o2, S_L, z_L) =
+    the reference-mode scan (``oracle.kda.ref_scan_pair``).
 
     q1, q2, k (B, H, S, Dk); v, do1, do2 (B, H, S, D); q2 / do2 None for a single query stream.
     Returns a dict of float64 arrays: dq1, dq2 (absent without q2), dk shaped like q1 (zero beyond channel
@@ -67,8 +71,8 @@ def ref_scan_pair_backward(q1, q2, k, v, kernel_dim, do1, do2=None, initial_stat
     os_ = [np.zeros((Bb, H, S, D)) for _ in qs]
     dpk = np.zeros((Bb, H, S, K))
     dv = np.zeros_like(v)
-    lam_ = np.zeros((Bb, H, K, D))
-    zeta = np.zeros((Bb, H, K))
+    lam_ = np.zeros((Bb, H, K, D)) if d_final_state is None else np.array(d_final_state, np.float64)
+    zeta = np.zeros((Bb, H, K)) if d_final_z is None else np.array(d_final_z, np.float64).reshape(Bb, H, K)
     for t in reversed(range(S)):
         for i, p in enumerate(ps):
             num = np.einsum("bhk,bhkd->bhd", p[:, :, t], Ss[t])

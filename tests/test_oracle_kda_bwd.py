@@ -71,6 +71,28 @@ def test_pair_backward_matches_autograd_of_matrix_form(K, init):
         assert rel_l2(r["dz0"], tz0.grad.numpy()) < 1e-10
 
 
+def test_final_state_gradients_match_autograd():
+    rng = np.random.default_rng(41)
+    q1, q2, k, v = make(rng, S=8)
+    B, H, S, Dk = q1.shape
+    D = v.shape[-1]
+    S0, z0 = rng.standard_normal((B, H, Dk, D)) * 0.5, rng.uniform(0.5, 2.0, (B, H, Dk))
+    dF, dFz = rng.standard_normal((B, H, Dk, D)), rng.standard_normal((B, H, Dk))
+    do1 = rng.standard_normal((B, H, S, D))
+    r = obwd.ref_scan_pair_backward(q1, q2, k, v, Dk, do1, None, initial_state=S0, initial_z=z0,
+                                    d_final_state=dF, d_final_z=dFz)
+    T = lambda a: torch.tensor(a, dtype=torch.float64, requires_grad=True)
+    tq1, tq2, tk, tv, tS0, tz0 = map(T, (q1, q2, k, v, S0, z0))
+    o1 = matrix_form(tq1, tk, tv, Dk, tS0, tz0)
+    pk = F.elu(tk) + 1.0
+    SL = tS0 + pk.transpose(-1, -2) @ tv
+    zL = tz0 + pk.sum(2)
+    ((o1 * torch.tensor(do1)).sum() + (SL * torch.tensor(dF)).sum() + (zL * torch.tensor(dFz)).sum()).backward()
+    for name, t in (("dq1", tq1), ("dk", tk), ("dv", tv), ("dS0", tS0), ("dz0", tz0)):
+        assert rel_l2(r[name], t.grad.numpy()) < 1e-10, name
+    assert np.all(r["dq2"] == 0)
+
+
 def test_single_query_backward_matches_autograd():
     rng = np.random.default_rng(9)
     q1, _, k, v = make(rng, S=7)
