@@ -15,8 +15,9 @@ a step from the previous one.  The same JSON line carries:
   (``oracle/baseline.py``, mamba2.py:84-126 structure) timed on the host cores
   on a bounded token sample of the same workload.
 * ``decode`` -- selective state update at B=64 and B=256 (HBM GB/s vs 8 TB/s).
-* ``other`` -- ssd4 (128K prefill with state carry), kda5 (gated KDA scan) and ssd2_bwd (the backward of
-  the ssd2 prefill: all input gradients from dy and d_final).
+* ``other`` -- ssd4 (128K prefill with state carry), kda5 (gated KDA scan), ssd2_bwd (the backward of
+  the ssd2 prefill: all input gradients from dy and d_final) and kda5_bwd (the backward of the reference-mode
+  KDA scan with the fused differential output at the kda5 shape: dq1, dq2, dk, dv and d lambda).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu] [--only LEGS]
                        [--copy-calibration BYTES]
@@ -85,6 +86,19 @@ def kda_alg(cfg):
     B, H, S, K, V, Q = cfg.batch, cfg.nheads, cfg.seqlen, cfg.dk, cfg.dv, cfg.chunk
     nbytes = B * H * S * (3 * K * 2 + V * 2 + K * 4 + V * 2) + B * H * K * V * 4
     flops = B * H * (S // Q) * (2 * Q * Q * K + 2 * Q * Q * V + 4 * Q * K * V)
+    return nbytes, flops
+
+
+def kda_bwd_alg(cfg):
+    """Backward of the reference-mode scan with the fused differential output (the training path of
+    LinearDiffAttention): q1, q2, k, v, dout read and dq1, dq2, dk, dv written (bf16).  FLOPs of the chunked
+    gradient per (b, h, chunk Q), both queries: the recomputed forward products (A, A V, phi(q) S), the
+    gradient products (G, G phi(k), dnum S^T, W g, phi(k) dS, Psi M, dS v) and the two state updates."""
+    B, H, S, K, V, Q = cfg.batch, cfg.nheads, cfg.seqlen, cfg.dk, cfg.dv, 64
+    nbytes = B * H * S * (5 * K * 2 + 4 * V * 2)
+    per_q = 2 * Q * Q * (2 * K + 2 * V) + 3 * 2 * Q * K * V       # kernel A, one query
+    comb = 2 * Q * Q * (3 * K + 2 * V) + 3 * 2 * Q * K * V        # kernel B, combined stream
+    flops = B * H * (S // Q) * (2 * per_q + comb)
     return nbytes, flops
 
 
@@ -164,6 +178,30 @@ def bench_ssd_bwd(cfg, steps, warmup, nsets):
                alg_bytes=nbytes, alg_flops=flops, hbm_GBs=nbytes / t / 1e9, tflops=flops / t / 1e12,
                roofline_frac=t_roof / t)
     del plans
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_kda_bwd(cfg, steps, warmup):
+    import mamformer_amd as mh
+    from mamformer_amd import workloads as W
+
+    inp = W.kda_inputs(cfg, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(cfg.seed + 7)
+    dout = (torch.randn(inp["v"].shape, device="cuda", generator=g) / cfg.dv ** 0.5).to(inp["v"].dtype)
+    lam = mh.diff_lambda(torch.linspace(-2.0, 3.0, cfg.nheads, device="cuda"))
+
+    def step():
+        mh.linear_attn_scan_bwd(inp["q1"], inp["q2"], inp["k"], inp["v"], kernel_dim=cfg.dk, lam=lam, do1=dout,
+                                need_initial=False)
+
+    wall, ev = time_plans([step], steps, warmup)
+    nbytes, flops = kda_bwd_alg(cfg)
+    t = ev * 1e-3
+    res = dict(mtok_s=cfg.batch * cfg.seqlen / t / 1e6, us_per_step=ev * 1e3, wall_us_per_step=wall * 1e3,
+               alg_bytes=nbytes, alg_flops=flops, hbm_GBs=nbytes / t / 1e9, tflops=flops / t / 1e12,
+               roofline_frac=max(nbytes / PEAK_HBM, flops / PEAK_BF16) / t)
+    del inp, dout
     torch.cuda.empty_cache()
     return res
 
@@ -260,7 +298,7 @@ def measured_traffic(workload="ssd2"):
 
 # ----------------------------------------------------------------- main
 
-LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd2_bwd", "ssd1", "cpu")
+LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd2_bwd", "kda5_bwd", "ssd1", "cpu")
 
 
 def main():
@@ -363,6 +401,11 @@ def main():
         r = bench_ssd_bwd(cfg, max(10, args.steps // 2), 5, nsets=3)
         log(f"ssd2 backward: {r['us_per_step']:.1f} us, {r['tflops']:.0f} TFLOP/s, roofline {r['roofline_frac']:.3f}")
         other["ssd2_bwd"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+    if "kda5_bwd" in legs:
+        r = bench_kda_bwd(W.KDA5, max(5, args.steps // 10), 2)
+        log(f"kda5 backward (reference mode, differential output): {r['us_per_step']:.0f} us, "
+            f"{r['tflops']:.0f} TFLOP/s, roofline {r['roofline_frac']:.3f}")
+        other["kda5_bwd"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
     if "ssd1" in legs:
         r, _, _ = bench_ssd(W.SSD1, args.steps, args.warmup, nsets=1, chunk=64)
         other["ssd1"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}

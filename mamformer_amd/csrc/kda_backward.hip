@@ -86,6 +86,7 @@ struct QSmem {
   float z[2][BD];         // z' before this chunk / after it
   float vs[2][BD];        // Vsum
   float cs[2][BD];        // column sums of S' over k < kernel_dim (= sum_s K1_s v_s)
+  float part[3][4][BD];   // per 16-token quarter: sums of phi'(k), v, K1 v over the chunk
   float qs[BC];           // Q_t
   float k1[BC];           // K1_s
   float kpre[BC];         // sum_{s <= t} K1_s (in-chunk)
@@ -118,6 +119,7 @@ struct KVSmem {
   bf16 MT[BC * P64];      // M^T[s][t] = g_t . v_s          (s <= t)
   bf16 SB[BD * P128];     // dS[k][d] (bf16)
   float dz[BD];
+  float part[4][BD];      // per 16-token quarter: sums of Xi
 };
 
 __device__ __forceinline__ void query_coef(const KdaBwdParams& q, int h, int qi, float& coef) {
@@ -181,6 +183,18 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
   for (int pos = 0, ci = 0; pos < S; pos += BC, ++ci) {
     const int len = min(BC, S - pos);
     const int zc = ci & 1;
+    if (ci > 0 && tid < BD) {      // z', Vsum, column sums past the previous chunk (fixed-order sums)
+      float a0 = sm.z[zc ^ 1][tid], a1 = sm.vs[zc ^ 1][tid], a2 = sm.cs[zc ^ 1][tid];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a0 += sm.part[0][j][tid];
+        a1 += sm.part[1][j][tid];
+        a2 += sm.part[2][j][tid];
+      }
+      sm.z[zc][tid] = a0;
+      sm.vs[zc][tid] = a1;
+      sm.cs[zc][tid] = a2;
+    }
     // ---- phase 0: phi'(q), phi'(k), v, do tiles, Q_t and K1_s; S' into LDS
     for (int e = tid; e < BC * (BD / 8); e += NT) {
       const int t = e >> 4, c0 = (e & 15) * 8;
@@ -405,17 +419,19 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
       for (int c = 0; c < BC / 16; ++c)
         Sacc[i] = mma(frag_col(sm.PK, P128, 32 * (2 * tt + i), 16 * c), frag_col(sm.VV, P128, 32 * dt, 16 * c),
                       Sacc[i]);
-    if (tid < BD) {
-      float zs = sm.z[zc][tid], vsn = sm.vs[zc][tid], csn = sm.cs[zc][tid];
-      for (int s_ = 0; s_ < BC; ++s_) {
-        zs += (float)sm.PK[s_ * P128 + tid];
-        const float vv = (float)sm.VV[s_ * P128 + tid];
+    {
+      const int col = tid & (BD - 1), qt = tid >> 7;
+      float zs = 0.f, vsn = 0.f, csn = 0.f;
+#pragma unroll 4
+      for (int s_ = 16 * qt; s_ < 16 * qt + 16; ++s_) {
+        zs += (float)sm.PK[s_ * P128 + col];
+        const float vv = (float)sm.VV[s_ * P128 + col];
         vsn += vv;
         csn += sm.k1[s_] * vv;
       }
-      sm.z[zc ^ 1][tid] = zs;
-      sm.vs[zc ^ 1][tid] = vsn;
-      sm.cs[zc ^ 1][tid] = csn;
+      sm.part[0][qt][col] = zs;
+      sm.part[1][qt][col] = vsn;
+      sm.part[2][qt][col] = csn;
     }
     lds_barrier();
   }
@@ -595,12 +611,15 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
 #pragma unroll
         for (int c = 0; c < BC / 16; ++c)
           dS[i] = mma(frag_col(sm.PS, P128, 32 * (ktb + i), 16 * c), frag_col(sm.DN, P128, 32 * dt, 16 * c), dS[i]);
-      if (tid < BD) {
+      {
+        const int col = tid & (BD - 1), qt = tid >> 7;
         float a = 0.f;
-        for (int t = 0; t < BC; ++t) a += (float)sm.XI[t * P128 + tid];
-        sm.dz[tid] += a;
+#pragma unroll 4
+        for (int t = 16 * qt; t < 16 * qt + 16; ++t) a += (float)sm.XI[t * P128 + col];
+        sm.part[qt][col] = a;
       }
       lds_barrier();
+      if (tid < BD) sm.dz[tid] += sm.part[0][tid] + sm.part[1][tid] + sm.part[2][tid] + sm.part[3][tid];
     }
 
     const int s_ = 32 * st + l32;
