@@ -10,7 +10,7 @@ import torch
 
 import mamformer_amd
 from mamformer_amd import _lib
-from mamformer_amd._lib import SsdBwdArgs, Conv1dArgs, Conv1dBwdArgs, KdaArgs, SsdArgs, SsuArgs
+from mamformer_amd._lib import SsdBwdArgs, Conv1dArgs, Conv1dBwdArgs, KdaArgs, KdaBwdArgs, SsdArgs, SsuArgs
 
 ROOT = Path(__file__).resolve().parent.parent
 
@@ -344,3 +344,50 @@ def test_conv1d_bwd_rejects_small_workspace():
     q.workspace, q.workspace_bytes = ct.c_void_p(8192), 64
     assert _rc("mh_causal_conv1d_bwd", ct.byref(q), None) == -7
     assert _rc("mh_causal_conv1d_bwd", None, None) == -1
+
+
+def _good_kda_bwd(diff=True):
+    a = KdaBwdArgs()
+    f = a.fwd
+    f.batch, f.nheads, f.seqlen, f.dk, f.dv = 2, 4, 300, 128, 128
+    f.dtype, f.mode, f.kernel_dim, f.lam = _lib.MH_BF16, _lib.MH_KDA_REFERENCE, 128, 0.8
+    fake = ct.c_void_p(4096)
+    f.q1 = f.q2 = f.k = f.v = fake
+    a.flags = _lib.MH_KDA_BWD_DIFF if diff else 0
+    a.do1 = a.dq1 = a.dq2 = a.dk = a.dv = ct.c_void_p(8192)
+    return a
+
+
+def test_kda_bwd_workspace():
+    a = _good_kda_bwd()
+    n = ct.c_size_t()
+    assert _rc("mh_kda_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+    # n_t and dn_t per (query, b, h, token), plus per-(b, h) lambda partial sums (two queries and the baseline)
+    assert n.value == (2 * 2 * 8 * 300 + 3 * 8) * 4
+    a.fwd.seqlen = 0
+    assert _rc("mh_kda_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+
+
+@pytest.mark.parametrize("mutate,code,word", [
+    (lambda a: setattr(a.fwd, "mode", _lib.MH_KDA_GATED), -6, b"reference mode"),
+    (lambda a: setattr(a, "do1", None), -1, b"do1"),
+    (lambda a: setattr(a, "dk", None), -1, b"dk"),
+    (lambda a: setattr(a.fwd, "q2", None), -1, b"q2"),
+    (lambda a: setattr(a, "do2", ct.c_void_p(4096)), -2, b"do2"),
+    (lambda a: setattr(a, "flags", 6), -6, b"flags"),
+    (lambda a: setattr(a, "dv", ct.c_void_p(8192 + 8)), -5, b"aligned"),
+    (lambda a: setattr(a.fwd, "dk", 64), -6, b"dk"),
+])
+def test_kda_bwd_rejects_bad_arguments(mutate, code, word):
+    a = _good_kda_bwd()
+    mutate(a)
+    n = ct.c_size_t()
+    assert _rc("mh_kda_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == code
+    assert word in _lib.lib().mh_last_error()
+    assert _rc("mh_kda_chunk_scan_bwd", ct.byref(a), None) == code
+
+
+def test_kda_bwd_rejects_small_workspace():
+    a = _good_kda_bwd(diff=False)
+    a.workspace, a.workspace_bytes = ct.c_void_p(8192), 64
+    assert _rc("mh_kda_chunk_scan_bwd", ct.byref(a), None) == -7
