@@ -131,7 +131,19 @@ __device__ __forceinline__ void query_coef(const KdaBwdParams& q, int h, int qi,
   }
 }
 
-__device__ __forceinline__ float phic_f(float x) { return x > 0.f ? x : expm1f(x); }   // phi(x) - 1
+// phi(x) - 1 = elu(x): x above 0; the Taylor series of e^x - 1 to x^5 on (-0.5, 0] (truncation below
+// |x|^5 / 720 relative, under the bf16 rounding the values get); e^x - 1 below -0.5.
+__device__ __forceinline__ float phic_f(float x) {
+  if (x > 0.f) return x;
+  if (x > -0.5f) {
+    float t = fmaf(x, 1.f / 120.f, 1.f / 24.f);
+    t = fmaf(x, t, 1.f / 6.f);
+    t = fmaf(x, t, 0.5f);
+    t = fmaf(x, t, 1.f);
+    return x * t;
+  }
+  return __expf(x) - 1.f;
+}
 
 }  // namespace
 
@@ -212,7 +224,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
         const float cq = ch ? phic_f(xq) : 0.f, ck = ch ? phic_f(xk) : 0.f;
         qo[j] = (bf16)cq;
         ko[j] = (bf16)ck;
-        qsum += ch ? phi_f(xq) : 0.f;
+        qsum += ch ? 1.f + cq : 0.f;
         ksum += ck;
         vo[j] = in ? vv[j] : (bf16)0.f;
         doo[j] = (in && dop) ? dv[j] : (bf16)0.f;
