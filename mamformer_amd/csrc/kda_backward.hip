@@ -20,8 +20,10 @@
 //
 // kda_ref_bwd_q_kernel   grid (B*H, nq): one query stream per workgroup, forward walk: dq, and n, dn per
 //                        token into the workspace (plus sum(dout . o_i) for the lambda gradient).
-// kda_ref_bwd_kv_kernel  grid (B*H): reverse walk over the query streams (one combined stream for the
-//                        differential output): dk, dv, dS0, dz0.
+// kda_ref_bwd_segsum_kernel grid (nseg - 1, B*H): per sequence segment, its sum of adjoint-state
+//                        contributions, so that the segments' reverse walks run side by side.
+// kda_ref_bwd_kv_kernel  grid (nseg, B*H): reverse walk of one segment over the query streams (one combined
+//                        stream for the differential output): dk, dv, and (segment 0) dS0, dz0.
 // kda_ref_bwd_lam_kernel grid (1): d lambda per head from the per-(b, h) partial sums, fixed order.
 // 8 waves per workgroup; every product is a 32x32x16 bf16 MFMA over LDS tiles whose operands are read
 // along rows (two 8-byte reads) or down columns (eight 2-byte reads), so no transposed copies are kept.
@@ -468,11 +470,104 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
   }
 }
 
+// Psi, Xi and g of stream js for the chunk at pos (len tokens) into LDS (zero rows beyond len).
+__device__ __forceinline__ void stage_stream(const KdaBwdParams& q, KVSmem& sm, int js, int bh, int pos, int len,
+                                             const float (&coef)[2]) {
+  const KdaParams& p = q.f;
+  const int nbh = p.batch * p.nheads, S = p.seqlen, kd = p.kernel_dim;
+  const int64_t rowbase = (int64_t)bh * S;
+  const int nqs = q.diff ? 2 : 1;          // queries folded into this stream
+  const bf16* qps[2];
+  const float* nbs[2];
+  const float* dbs[2];
+  float cf[2];
+  for (int i = 0; i < nqs; ++i) {
+    const int qi = q.diff ? i : js;
+    qps[i] = reinterpret_cast<const bf16*>(qi == 0 ? p.q1 : p.q2);
+    nbs[i] = q.nbuf + ((int64_t)qi * nbh + bh) * S + pos;
+    dbs[i] = q.dnbuf + ((int64_t)qi * nbh + bh) * S + pos;
+    cf[i] = q.diff ? coef[qi] : 1.f;
+  }
+  const bf16* gp = reinterpret_cast<const bf16*>(q.diff ? q.do1 : (js == 0 ? q.do1 : q.do2));
+  for (int e = threadIdx.x; e < BC * (BD / 8); e += NT) {
+    const int t = e >> 4, c0 = (e & 15) * 8;
+    const bool in = t < len;
+    const int64_t r = (rowbase + pos + (in ? t : 0)) * BD + c0;
+    float ps[8], xi[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ps[j] = xi[j] = 0.f;
+    for (int i = 0; i < nqs; ++i) {
+      const bf16x8 qv = ld8(qps[i] + r);
+      const float sc = in ? cf[i] / nbs[i][t] : 0.f;
+      const float dn = in ? dbs[i][t] : 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float ph = (c0 + j < kd) ? phi_f((float)qv[j]) : 0.f;
+        ps[j] += sc * ph;
+        xi[j] += dn * ph;
+      }
+    }
+    bf16x8 g8;
+    if (gp) g8 = ld8(gp + r);
+    bf16x8 po, xo, go;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      po[j] = (bf16)ps[j];
+      xo[j] = (bf16)xi[j];
+      go[j] = (in && gp) ? g8[j] : (bf16)0.f;
+    }
+    *reinterpret_cast<bf16x8*>(&sm.PS[t * P128 + c0]) = po;
+    *reinterpret_cast<bf16x8*>(&sm.XI[t * P128 + c0]) = xo;
+    *reinterpret_cast<bf16x8*>(&sm.DN[t * P128 + c0]) = go;
+  }
+}
+
+// Sum of one segment's contributions to the adjoint state, sum_t Psi_t^T g_t and sum_t Xi_t over its
+// chunks and streams, for the kv-walk of the segments before it.  grid (nseg - 1, B*H): segment
+// blockIdx.x + 1 (segment 0's sum is never needed).
+__global__ __launch_bounds__(NT) void kda_ref_bwd_segsum_kernel(KdaBwdParams q) {
+  __shared__ KVSmem sm;
+  const KdaParams& p = q.f;
+  const int bh = blockIdx.y, seg = blockIdx.x + 1, h = bh % p.nheads;
+  const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
+  const int tid = threadIdx.x;
+  const int nch = (p.seqlen + BC - 1) / BC;
+  const int c_begin = seg * q.seg_chunks, c_end = min(nch, c_begin + q.seg_chunks);
+  const int nstream = q.diff ? 1 : q.nq;
+  float coef[2];
+  query_coef(q, h, 0, coef[0]);
+  query_coef(q, h, 1, coef[1]);
+  const int dt = w & 3, ktb = 2 * (w >> 2);
+  f32x16 acc[2] = {zero16(), zero16()};
+  float zacc = 0.f;
+  for (int ci = c_begin; ci < c_end; ++ci) {
+    const int pos = ci * BC, len = min(BC, p.seqlen - pos);
+    for (int js = 0; js < nstream; ++js) {
+      stage_stream(q, sm, js, bh, pos, len, coef);
+      lds_barrier();
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int c = 0; c < BC / 16; ++c)
+          acc[i] = mma(frag_col(sm.PS, P128, 32 * (ktb + i), 16 * c), frag_col(sm.DN, P128, 32 * dt, 16 * c), acc[i]);
+      if (tid < BD)
+        for (int t = 0; t < BC; ++t) zacc += (float)sm.XI[t * P128 + tid];
+      lds_barrier();
+    }
+  }
+  float* o = q.segsum + ((int64_t)seg * p.batch * p.nheads + bh) * (BD * BD + BD);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[(32 * (ktb + i) + acc_row(half, r)) * BD + 32 * dt + l32] = acc[i][r];
+  if (tid < BD) o[BD * BD + tid] = zacc;
+}
+
 __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
   __shared__ KVSmem sm;
   const KdaParams& p = q.f;
   const int nbh = p.batch * p.nheads;
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.y, seg = blockIdx.x;
   const int h = bh % p.nheads;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
   const int tid = threadIdx.x;
@@ -481,26 +576,35 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
   const bf16* kp = reinterpret_cast<const bf16*>(p.k);
   const bf16* vp = reinterpret_cast<const bf16*>(p.v);
   const int nstream = q.diff ? 1 : q.nq;
+  const int nseg = gridDim.x;
   float coef[2];
   query_coef(q, h, 0, coef[0]);
   query_coef(q, h, 1, coef[1]);
   const int dt = w & 3, ktb = 2 * (w >> 2);     // dS tiles (ktb + i, dt)
   const int x4 = w & 3, st = w >> 2;            // output tiles: dv^T (d-block x4, s-block st), dphi(k)^T (k-block x4)
 
+  // the adjoint after this segment: the final-state gradient plus the later segments' sums (fixed order)
   f32x16 dS[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     dS[i] = zero16();
-    if (q.d_final) {
-      const float* s0 = q.d_final + (int64_t)bh * BD * BD;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dS[i][r] = s0[(32 * (ktb + i) + acc_row(half, r)) * BD + 32 * dt + l32];
+    for (int r = 0; r < 16; ++r) {
+      const int e = (32 * (ktb + i) + acc_row(half, r)) * BD + 32 * dt + l32;
+      float a = q.d_final ? q.d_final[(int64_t)bh * BD * BD + e] : 0.f;
+      for (int j = nseg - 1; j > seg; --j) a += q.segsum[((int64_t)j * nbh + bh) * (BD * BD + BD) + e];
+      dS[i][r] = a;
     }
   }
-  if (tid < BD) sm.dz[tid] = q.d_final_z ? q.d_final_z[(int64_t)bh * BD + tid] : 0.f;
+  if (tid < BD) {
+    float a = q.d_final_z ? q.d_final_z[(int64_t)bh * BD + tid] : 0.f;
+    for (int j = nseg - 1; j > seg; --j) a += q.segsum[((int64_t)j * nbh + bh) * (BD * BD + BD) + BD * BD + tid];
+    sm.dz[tid] = a;
+  }
 
   const int nch = (S + BC - 1) / BC;
-  for (int ci = nch - 1; ci >= 0; --ci) {
+  const int c_begin = seg * q.seg_chunks, c_end = min(nch, c_begin + q.seg_chunks);
+  for (int ci = c_end - 1; ci >= c_begin; --ci) {
     const int pos = ci * BC, len = min(BC, S - pos);
     for (int e = tid; e < BC * (BD / 8); e += NT) {
       const int t = e >> 4, c0 = (e & 15) * 8;
@@ -534,50 +638,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
     for (int r = 0; r < 16; ++r) gk[r] += sm.dz[32 * x4 + acc_row(half, r)];
 
     for (int js = 0; js < nstream; ++js) {
-      const int nqs = q.diff ? 2 : 1;          // queries folded into this stream
-      const bf16* qps[2];
-      const float* nbs[2];
-      const float* dbs[2];
-      float cf[2];
-      for (int i = 0; i < nqs; ++i) {
-        const int qi = q.diff ? i : js;
-        qps[i] = reinterpret_cast<const bf16*>(qi == 0 ? p.q1 : p.q2);
-        nbs[i] = q.nbuf + ((int64_t)qi * nbh + bh) * S + pos;
-        dbs[i] = q.dnbuf + ((int64_t)qi * nbh + bh) * S + pos;
-        cf[i] = q.diff ? coef[qi] : 1.f;
-      }
-      const bf16* gp = reinterpret_cast<const bf16*>(q.diff ? q.do1 : (js == 0 ? q.do1 : q.do2));
-      for (int e = tid; e < BC * (BD / 8); e += NT) {
-        const int t = e >> 4, c0 = (e & 15) * 8;
-        const bool in = t < len;
-        const int64_t r = (rowbase + pos + (in ? t : 0)) * BD + c0;
-        float ps[8], xi[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ps[j] = xi[j] = 0.f;
-        for (int i = 0; i < nqs; ++i) {
-          const bf16x8 qv = ld8(qps[i] + r);
-          const float sc = in ? cf[i] / nbs[i][t] : 0.f;
-          const float dn = in ? dbs[i][t] : 0.f;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float ph = (c0 + j < kd) ? phi_f((float)qv[j]) : 0.f;
-            ps[j] += sc * ph;
-            xi[j] += dn * ph;
-          }
-        }
-        bf16x8 g8;
-        if (gp) g8 = ld8(gp + r);
-        bf16x8 po, xo, go;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          po[j] = (bf16)ps[j];
-          xo[j] = (bf16)xi[j];
-          go[j] = (in && gp) ? g8[j] : (bf16)0.f;
-        }
-        *reinterpret_cast<bf16x8*>(&sm.PS[t * P128 + c0]) = po;
-        *reinterpret_cast<bf16x8*>(&sm.XI[t * P128 + c0]) = xo;
-        *reinterpret_cast<bf16x8*>(&sm.DN[t * P128 + c0]) = go;
-      }
+      stage_stream(q, sm, js, bh, pos, len, coef);
       lds_barrier();
 
       // W^T (waves 0..2) and M^T (waves 3..5) tiles, (t-block, s-block) = (0,0), (1,0), (1,1)
@@ -655,6 +716,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
     lds_barrier();
   }
 
+  if (seg != 0) return;
   if (q.dS0) {
     float* o = q.dS0 + (int64_t)bh * BD * BD;
 #pragma unroll
@@ -691,9 +753,19 @@ __global__ __launch_bounds__(256) void kda_ref_bwd_empty_kernel(KdaBwdParams q, 
   if (q.dz0 && i < nz) q.dz0[i] = q.d_final_z ? q.d_final_z[i] : 0.f;
 }
 
+// Segments of the kv-walk per (b, h): enough workgroups to cover the 256 CUs, at least 4 chunks each.
+int kda_bwd_segments(int batch, int nheads, int seqlen) {
+  const int nbh = batch * nheads, nch = (seqlen + BC - 1) / BC;
+  int nseg = (256 + nbh - 1) / nbh;
+  nseg = min(nseg, max(1, nch / 4));
+  return max(1, min(nseg, 8));
+}
+
 size_t kda_bwd_workspace_bytes(int batch, int nheads, int seqlen, int nq) {
   const size_t nbh = (size_t)batch * nheads;
-  return (2 * (size_t)nq * nbh * seqlen + (size_t)(nq + 1) * nbh) * sizeof(float);
+  const int nseg = kda_bwd_segments(batch, nheads, seqlen);
+  return (2 * (size_t)nq * nbh * seqlen + (size_t)(nq + 1) * nbh + (size_t)nseg * nbh * (BD * BD + BD)) *
+         sizeof(float);
 }
 
 void kda_bwd_workspace_layout(KdaBwdParams& q, void* workspace) {
@@ -701,6 +773,11 @@ void kda_bwd_workspace_layout(KdaBwdParams& q, void* workspace) {
   q.nbuf = reinterpret_cast<float*>(workspace);
   q.dnbuf = q.nbuf + n;
   q.lam_part = q.dnbuf + n;
+  q.segsum = q.lam_part + (size_t)(q.nq + 1) * nbh;
+  q.nseg = kda_bwd_segments(q.f.batch, q.f.nheads, q.f.seqlen);
+  const int nch = (q.f.seqlen + BC - 1) / BC;
+  q.seg_chunks = (nch + q.nseg - 1) / q.nseg;
+  q.nseg = (nch + q.seg_chunks - 1) / q.seg_chunks;   // no empty trailing segment
 }
 
 hipError_t launch_kda_bwd(const KdaBwdParams& q, hipStream_t st) {
@@ -713,7 +790,12 @@ hipError_t launch_kda_bwd(const KdaBwdParams& q, hipStream_t st) {
     hipLaunchKernelGGL(kda_ref_bwd_q_kernel, dim3((unsigned)nbh, (unsigned)q.nq), dim3(NT), 0, st, q);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kda_ref_bwd_kv_kernel, dim3((unsigned)nbh), dim3(NT), 0, st, q);
+    if (q.nseg > 1) {
+      hipLaunchKernelGGL(kda_ref_bwd_segsum_kernel, dim3((unsigned)(q.nseg - 1), (unsigned)nbh), dim3(NT), 0, st, q);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kda_ref_bwd_kv_kernel, dim3((unsigned)q.nseg, (unsigned)nbh), dim3(NT), 0, st, q);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !q.dlam) return e;

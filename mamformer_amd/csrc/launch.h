@@ -116,6 +116,8 @@ struct KdaBwdParams {
   float* dlam;               // (H,) or null (diff mode)
   float* nbuf; float* dnbuf; // workspace: n_t and dn_t per (query, b, h, token)
   float* lam_part;           // workspace: sum dout . o_i per (query, b, h)
+  float* segsum;             // workspace: per (segment, b, h) adjoint-state sums (dk*dv + dk floats)
+  int nseg, seg_chunks;      // kv-walk segments per (b, h) and 64-token chunks per segment
 };
 hipError_t launch_kda_bwd(const KdaBwdParams& q, hipStream_t st);
 size_t kda_bwd_workspace_bytes(int batch, int nheads, int seqlen, int nq);

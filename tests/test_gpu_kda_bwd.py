@@ -5,7 +5,8 @@ Tolerance: global relative L2 <= 1e-2 on every gradient (bf16 I/O; the kernels r
 fp32 accumulation).  Cases: the pair outputs (triton_linear_attn_scan's contract), the fused differential
 output with the lambda gradient through sigmoid and the 0.99 clamp (LinearDiffAttention._linear_attention_scan),
 a single query stream, kernel_dim below head_dim, an initial state and normaliser with their gradients,
-final-state gradients, ragged last chunks (S = 1, 70, 130, 200) and S = 0.  A longer sequence (S = 2048) is
+final-state gradients, ragged last chunks (S = 1, 70, 130, 200), S = 0, and S = 600 / 700 where the reverse
+walk is split into segments that run side by side.  A longer sequence (S = 2048) is
 checked through a leading slice: with the output gradient zero after T0 every gradient past T0 is exactly zero
 and the earlier ones equal the truncated problem's.  No float atomics: two calls agree bit for bit.
 """
@@ -31,6 +32,7 @@ def inputs(seed, B, H, S, D=128, scale=4.0):
 @pytest.mark.parametrize("B,H,S,kd,init,dfin", [
     (1, 2, 64, 128, False, False), (2, 2, 130, 128, True, True), (1, 1, 1, 128, False, False),
     (1, 3, 200, 100, True, False), (2, 1, 70, 37, False, True),
+    (1, 2, 600, 128, True, True),      # 10 chunks: the reverse walk runs as two segments side by side
 ])
 def test_pair_backward_vs_oracle(B, H, S, kd, init, dfin):
     q1, q2, k, v, do1, do2 = inputs(S + 7 * H + kd, B, H, S)
@@ -64,7 +66,7 @@ def test_pair_backward_vs_oracle(B, H, S, kd, init, dfin):
     assert torch.all(r["dq1"][..., kd:] == 0) and torch.all(r["dk"][..., kd:] == 0)
 
 
-@pytest.mark.parametrize("S", [96, 257])
+@pytest.mark.parametrize("S", [96, 257, 700])
 def test_diff_output_autograd_vs_oracle(S):
     B, H = 2, 4
     q1, q2, k, v, dout, _ = inputs(S, B, H, S)
