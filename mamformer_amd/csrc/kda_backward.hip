@@ -39,6 +39,7 @@ constexpr int BD = 128;      // dk = dv
 constexpr int P128 = 136;    // bf16 row pitch of 128-wide tiles
 constexpr int P64 = 72;      // bf16 row pitch of 64-wide tiles
 constexpr int NT = 512;      // threads per workgroup
+constexpr int SEG_PARTS = 2; // workgroups per segment in the segment-sum pass
 
 __device__ __forceinline__ float phi_f(float x) { return x > 0.f ? x + 1.f : __expf(x); }
 
@@ -522,24 +523,29 @@ __device__ __forceinline__ void stage_stream(const KdaBwdParams& q, KVSmem& sm, 
   }
 }
 
-// Sum of one segment's contributions to the adjoint state, sum_t Psi_t^T g_t and sum_t Xi_t over its
-// chunks and streams, for the kv-walk of the segments before it.  grid (nseg - 1, B*H): segment
-// blockIdx.x + 1 (segment 0's sum is never needed).
+// Sum of the contributions of one part of a segment to the adjoint state, sum_t Psi_t^T g_t and
+// sum_t Xi_t over its chunks and streams, for the kv-walk of the segments before it.
+// grid ((nseg - 1) * SEG_PARTS, B*H): part blockIdx.x % SEG_PARTS of segment blockIdx.x / SEG_PARTS + 1
+// (segment 0's sum is never needed).
 __global__ __launch_bounds__(NT) void kda_ref_bwd_segsum_kernel(KdaBwdParams q) {
   __shared__ KVSmem sm;
   const KdaParams& p = q.f;
-  const int bh = blockIdx.y, seg = blockIdx.x + 1, h = bh % p.nheads;
+  const int bh = blockIdx.y, seg = blockIdx.x / SEG_PARTS + 1, part = blockIdx.x % SEG_PARTS;
+  const int h = bh % p.nheads;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
   const int tid = threadIdx.x;
   const int nch = (p.seqlen + BC - 1) / BC;
-  const int c_begin = seg * q.seg_chunks, c_end = min(nch, c_begin + q.seg_chunks);
+  const int pc = (q.seg_chunks + SEG_PARTS - 1) / SEG_PARTS;
+  const int c_begin = seg * q.seg_chunks + part * pc;
+  const int c_end = min(min(nch, (seg + 1) * q.seg_chunks), c_begin + pc);
   const int nstream = q.diff ? 1 : q.nq;
   float coef[2];
   query_coef(q, h, 0, coef[0]);
   query_coef(q, h, 1, coef[1]);
   const int dt = w & 3, ktb = 2 * (w >> 2);
   f32x16 acc[2] = {zero16(), zero16()};
-  float zacc = 0.f;
+  const int col = tid & (BD - 1), qt = tid >> 7;
+  float zacc = 0.f;                          // this thread's column, tokens 16 qt .. 16 qt + 15 of every chunk
   for (int ci = c_begin; ci < c_end; ++ci) {
     const int pos = ci * BC, len = min(BC, p.seqlen - pos);
     for (int js = 0; js < nstream; ++js) {
@@ -550,12 +556,15 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_segsum_kernel(KdaBwdParams q) 
 #pragma unroll
         for (int c = 0; c < BC / 16; ++c)
           acc[i] = mma(frag_col(sm.PS, P128, 32 * (ktb + i), 16 * c), frag_col(sm.DN, P128, 32 * dt, 16 * c), acc[i]);
-      if (tid < BD)
-        for (int t = 0; t < BC; ++t) zacc += (float)sm.XI[t * P128 + tid];
+#pragma unroll 4
+      for (int t = 16 * qt; t < 16 * qt + 16; ++t) zacc += (float)sm.XI[t * P128 + col];
       lds_barrier();
     }
   }
-  float* o = q.segsum + ((int64_t)seg * p.batch * p.nheads + bh) * (BD * BD + BD);
+  sm.part[qt][col] = zacc;
+  lds_barrier();
+  if (tid < BD) zacc = sm.part[0][tid] + sm.part[1][tid] + sm.part[2][tid] + sm.part[3][tid];
+  float* o = q.segsum + ((int64_t)(seg * SEG_PARTS + part) * p.batch * p.nheads + bh) * (BD * BD + BD);
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -592,13 +601,15 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
     for (int r = 0; r < 16; ++r) {
       const int e = (32 * (ktb + i) + acc_row(half, r)) * BD + 32 * dt + l32;
       float a = q.d_final ? q.d_final[(int64_t)bh * BD * BD + e] : 0.f;
-      for (int j = nseg - 1; j > seg; --j) a += q.segsum[((int64_t)j * nbh + bh) * (BD * BD + BD) + e];
+      for (int j = SEG_PARTS * nseg - 1; j >= SEG_PARTS * (seg + 1); --j)
+        a += q.segsum[((int64_t)j * nbh + bh) * (BD * BD + BD) + e];
       dS[i][r] = a;
     }
   }
   if (tid < BD) {
     float a = q.d_final_z ? q.d_final_z[(int64_t)bh * BD + tid] : 0.f;
-    for (int j = nseg - 1; j > seg; --j) a += q.segsum[((int64_t)j * nbh + bh) * (BD * BD + BD) + BD * BD + tid];
+    for (int j = SEG_PARTS * nseg - 1; j >= SEG_PARTS * (seg + 1); --j)
+      a += q.segsum[((int64_t)j * nbh + bh) * (BD * BD + BD) + BD * BD + tid];
     sm.dz[tid] = a;
   }
 
@@ -764,8 +775,8 @@ int kda_bwd_segments(int batch, int nheads, int seqlen) {
 size_t kda_bwd_workspace_bytes(int batch, int nheads, int seqlen, int nq) {
   const size_t nbh = (size_t)batch * nheads;
   const int nseg = kda_bwd_segments(batch, nheads, seqlen);
-  return (2 * (size_t)nq * nbh * seqlen + (size_t)(nq + 1) * nbh + (size_t)nseg * nbh * (BD * BD + BD)) *
-         sizeof(float);
+  return (2 * (size_t)nq * nbh * seqlen + (size_t)(nq + 1) * nbh +
+          (size_t)SEG_PARTS * nseg * nbh * (BD * BD + BD)) * sizeof(float);
 }
 
 void kda_bwd_workspace_layout(KdaBwdParams& q, void* workspace) {
@@ -791,7 +802,8 @@ hipError_t launch_kda_bwd(const KdaBwdParams& q, hipStream_t st) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (q.nseg > 1) {
-      hipLaunchKernelGGL(kda_ref_bwd_segsum_kernel, dim3((unsigned)(q.nseg - 1), (unsigned)nbh), dim3(NT), 0, st, q);
+      hipLaunchKernelGGL(kda_ref_bwd_segsum_kernel, dim3((unsigned)((q.nseg - 1) * SEG_PARTS), (unsigned)nbh),
+                         dim3(NT), 0, st, q);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }

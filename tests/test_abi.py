@@ -363,8 +363,8 @@ def test_kda_bwd_workspace():
     n = ct.c_size_t()
     assert _rc("mh_kda_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
     # n_t and dn_t per (query, b, h, token), per-(b, h) lambda partial sums (two queries and the baseline), and
-    # one adjoint-state sum (128 x 128 + 128) per reverse-walk segment and (b, h) (one segment: 5 chunks)
-    assert n.value == (2 * 2 * 8 * 300 + 3 * 8 + 8 * (128 * 128 + 128)) * 4
+    # two adjoint-state sums (128 x 128 + 128) per reverse-walk segment and (b, h) (one segment: 5 chunks)
+    assert n.value == (2 * 2 * 8 * 300 + 3 * 8 + 2 * 8 * (128 * 128 + 128)) * 4
     a.fwd.seqlen = 0
     assert _rc("mh_kda_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
 
