@@ -364,10 +364,8 @@ struct GradSmem {
   float cs[2 * (N / 32)][SEG];   // per wave: c_t of the current head
   float dtp[2 * (N / 32)][SEG];  // per wave: processed dt
   float red[2][N / 32][SEG];     // per n-block partial dots: bint, u
-  Frag<T> xd[3][2][64];          // L o XD tiles (t-block, s-block) = (0,0), (1,0), (1,1), B-operand fragments
-  Frag<T> xt[3][2][64];          // (L o XD o dt)^T tiles (s-block, t-block) = (0,0), (0,1), (1,1)
-  float colg[3][32];             // per XD tile: sum_t (M o XD)[t][s], from the fp32 tile
-  float rowg[3][32];             // per XD^T tile: sum_s (M o XD)[t][s] dt_s, from the fp32 tile
+  float colg[SEG];               // sum_t (M o XD)[t][s], from fp32 tiles
+  float rowg[SEG];               // sum_s (M o XD)[t][s] dt_s, from fp32 tiles
   float lh[N / 32];              // <lam_out, h_in> per n-block
   float dd[2];                   // trace of dy x^T per diagonal 32-block
   float ddp[HD];                 // per-channel dD partial
@@ -542,77 +540,52 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
     sm.dtp[w][l] = dtv;
     const float cs_l = __shfl(cs, s_l), dt_l = __shfl(dtv, s_l);
 
-    // ---- the six distinct XD tiles of the head, one per wave 0..5, shared through LDS:
-    //      XD[t][s] = dy_t . x_s masked and decayed (L o XD; (t-block, s-block) = (0,0), (1,0), (1,1)) and
-    //      XD^T[s][t] masked, decayed and scaled by dt_s ((s-block, t-block) = (0,0), (0,1), (1,1)), as B-operand
-    //      fragments.  The per-token sums of M o XD that the decay gradient needs (colG, rowG) are taken from
-    //      these fp32 tiles, not from the bf16-operand products: the two sums cancel pairwise in da, and only
-    //      identically rounded copies cancel.
-    if (w < 3) {
-      const int tb = w == 0 ? 0 : 1, rr = w == 2 ? 1 : 0;
-      const int s_p = 32 * rr + l32;
-      const float cs_p = __shfl(cs, s_p);
+    // ---- XD[t][s] = dy_t . x_s (tiles tb >= r, column block r), masked and decayed (L o XD), as
+    //      B-operand fragments (column s, k = t)
+    // The per-token sums of M o XD that the decay gradient needs (colG here, rowG below) are taken from
+    // these fp32 tiles, not from the bf16-operand products: the two sums cancel pairwise in da, and only
+    // identically rounded copies cancel.
+    Frag<T> XDf[2][2];
+    float colg = 0.f;
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
       f32x16 a = zero16();
+      if (tb >= r) {
 #pragma unroll
-      for (int k = 0; k < HD / 16; ++k)
-        a = mma(row_frag<T, T, HD>(sg.DY, 32 * tb + l32, 16 * k + 8 * half),
-                row_frag<T, T, HD>(sg.X, s_p, 16 * k + 8 * half), a);
-      float ct[16];
-      acc_rows(sm.cs[w], 32 * tb, half, ct);
-      float d = 0.f;
+        for (int k = 0; k < HD / 16; ++k)
+          a = mma(row_frag<T, T, HD>(sg.DY, 32 * tb + l32, 16 * k + 8 * half),
+                  row_frag<T, T, HD>(sg.X, s_l, 16 * k + 8 * half), a);
+        float ct[16];
+        acc_rows(sm.cs[w], 32 * tb, half, ct);
+        float d = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int t = 32 * tb + acc_row(half, i);
-        a[i] = (t < len && t >= s_p) ? a[i] * __expf(ct[i] - cs_p) : 0.f;
-        d += (t == s_p) ? a[i] : 0.f;
+        for (int i = 0; i < 16; ++i) {
+          const int t = 32 * tb + acc_row(half, i);
+          a[i] = (t < len && t >= s_l) ? a[i] * __expf(ct[i] - cs_l) : 0.f;
+          d += (t == s_l) ? a[i] : 0.f;
+        }
+        if (nb == 0) {
+          // trace of dy x^T (per-head D): the diagonal block (r, r)
+          if (tb == r) {
+            d = wave_sum(d);
+            if (l == 0) sm.dd[r] = d;
+          }
+          const float* cbp = sm.cb[tb + r] + 16 * l;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) colg += v[k] * a[4 * i + k];
+          }
+        }
       }
-      if (tb == rr) {                    // trace of dy x^T (per-head D): the diagonal blocks
-        d = wave_sum(d);
-        if (l == 0) sm.dd[rr] = d;
-      }
-      float cg = 0.f;
-      const float* cbp = sm.cb[w] + 16 * l;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) cg += v[k] * a[4 * i + k];
-      }
-      cg += __shfl_xor(cg, 32);
-      if (half == 0) sm.colg[w][l32] = cg;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) sm.xd[w][c][l] = acc_to_frag<T>(a, c);
-    } else if (w < 6) {
-      const int ti = w - 3, sb = ti == 2 ? 1 : 0, rr = ti == 0 ? 0 : 1;
-      const int t_p = 32 * rr + l32;
-      const float cs_p = __shfl(cs, t_p);
-      f32x16 a = zero16();
-#pragma unroll
-      for (int k = 0; k < HD / 16; ++k)
-        a = mma(row_frag<T, T, HD>(sg.X, 32 * sb + l32, 16 * k + 8 * half),
-                row_frag<T, T, HD>(sg.DY, t_p, 16 * k + 8 * half), a);
-      float cr[16], dr[16];
-      acc_rows(sm.cs[w], 32 * sb, half, cr);
-      acc_rows(sm.dtp[w], 32 * sb, half, dr);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int s_ = 32 * sb + acc_row(half, i);
-        a[i] = (t_p < len && s_ <= t_p) ? a[i] * __expf(cs_p - cr[i]) * dr[i] : 0.f;
-      }
-      float rg = 0.f;
-      const float* cbp = sm.cbt[ti] + 16 * l;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) rg += v[k] * a[4 * i + k];
-      }
-      rg += __shfl_xor(rg, 32);
-      if (half == 0) sm.rowg[ti][l32] = rg;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) sm.xt[ti][c][l] = acc_to_frag<T>(a, c);
+      for (int c = 0; c < 2; ++c) XDf[tb][c] = acc_to_frag<T>(a, c);
     }
-    lds_barrier();                     // the shared XD tiles are in LDS
+    if (nb == 0) {
+      colg += __shfl_xor(colg, 32);
+      if (half == 0) sm.colg[s_l] = colg;
+    }
     __builtin_amdgcn_sched_barrier(0);   // keep the phases apart: bounded register lifetimes
     // ---- dB^T tile (n-block nb, s-block r): inter part from lam_out, intra part from C^T (L o XD)
     {
@@ -629,10 +602,9 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb) {
         if (tb >= r) {
-          const int ti = r == 0 ? tb : 2;
           const f32x16 ct = mfma_transpose<T, T, N>(sm.C, 32 * tb, 32 * nb, id, half, l32);   // [t][n]
 #pragma unroll
-          for (int c = 0; c < 2; ++c) aa = mma(acc_to_frag<T>(ct, c), sm.xd[ti][c][l], aa);
+          for (int c = 0; c < 2; ++c) aa = mma(acc_to_frag<T>(ct, c), XDf[tb][c], aa);
         }
       }
       float Bv[16];
@@ -647,6 +619,43 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       if (half == 0) sm.red[0][nb][s_l] = sI;
     }
     __builtin_amdgcn_sched_barrier(0);   // keep the phases apart: bounded register lifetimes
+    // ---- XD^T[s][t] (tiles sb <= r, column block r), masked, decayed, scaled by dt_s: (column t, k = s)
+    Frag<T> XTf[2][2];
+    float rowg = 0.f;
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      f32x16 a = zero16();
+      if (sb <= r) {
+#pragma unroll
+        for (int k = 0; k < HD / 16; ++k)
+          a = mma(row_frag<T, T, HD>(sg.X, 32 * sb + l32, 16 * k + 8 * half),
+                  row_frag<T, T, HD>(sg.DY, s_l, 16 * k + 8 * half), a);
+        float cr[16], dr[16];
+        acc_rows(sm.cs[w], 32 * sb, half, cr);
+        acc_rows(sm.dtp[w], 32 * sb, half, dr);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int s = 32 * sb + acc_row(half, i);
+          a[i] = (s_l < len && s <= s_l) ? a[i] * __expf(cs_l - cr[i]) * dr[i] : 0.f;
+        }
+        if (nb == 0) {
+          const float* cbp = sm.cbt[sb + r] + 16 * l;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) rowg += v[k] * a[4 * i + k];
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) XTf[sb][c] = acc_to_frag<T>(a, c);
+    }
+    if (nb == 0) {
+      rowg += __shfl_xor(rowg, 32);
+      if (half == 0) sm.rowg[s_l] = rowg;
+    }
+
     // <lam_out, h_in> over the blocks of n-block nb (one wave per n-block)
     if (r == 0) {
       float d = 0.f;
@@ -673,10 +682,9 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         if (sb <= r) {
-          const int ti = r == 0 ? 0 : (sb == 0 ? 1 : 2);
           const f32x16 bt = mfma_transpose<T, T, N>(sm.B, 32 * sb, 32 * nb, id, half, l32);   // [s][n]
 #pragma unroll
-          for (int c = 0; c < 2; ++c) ac = mma(acc_to_frag<T>(bt, c), sm.xt[ti][c][l], ac);
+          for (int c = 0; c < 2; ++c) ac = mma(acc_to_frag<T>(bt, c), XTf[sb][c], ac);
         }
       }
       float Cv[16];
@@ -800,8 +808,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       store_dx();
     }
     if (w == 0) {
-      const float colG = l < 32 ? sm.colg[0][l] + sm.colg[1][l] : sm.colg[2][l - 32];
-      const float rowG = l < 32 ? sm.rowg[0][l] : sm.rowg[1][l - 32] + sm.rowg[2][l - 32];
+      const float colG = sm.colg[l], rowG = sm.rowg[l];
       float bint = 0.f, u = 0.f, lh = 0.f;
 #pragma unroll
       for (int k = 0; k < NB; ++k) {
