@@ -185,6 +185,23 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
   // sum dout . Vsum / cnt (the same for both queries)
   float lam_acc = 0.f, base_acc = 0.f;
 
+  // The next chunk's q, k, v, do are loaded into registers during this chunk's state update (two 16-byte
+  // chunks of each per thread: row e >> 4, columns 8 (e & 15), e = tid + 512 i), hiding their latency.
+  bf16x8 tq[2], tk[2], tv[2], td[2];
+  auto load_tiles = [&](int p0) {
+    const int ln = min(BC, S - p0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + NT * i, t = e >> 4, c0 = (e & 15) * 8;
+      const int64_t r = (rowbase + p0 + (t < ln ? t : 0)) * BD + c0;
+      tq[i] = ld8(qp + r);
+      tk[i] = ld8(kp + r);
+      tv[i] = ld8(vp + r);
+      if (dop) td[i] = ld8(dop + r);
+    }
+  };
+  if (S > 0) load_tiles(0);
+
   for (int pos = 0, ci = 0; pos < S; pos += BC, ++ci) {
     const int len = min(BC, S - pos);
     const int zc = ci & 1;
@@ -202,13 +219,12 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
     }
     // ---- phase 0: phi'(q), phi'(k), v, do tiles, Q_t and K1_s; S' into LDS
     const bool full = len == BC && kd == BD && dop != nullptr;    // no row or channel masks
-    for (int e = tid; e < BC * (BD / 8); e += NT) {
-      const int t = e >> 4, c0 = (e & 15) * 8;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + NT * i, t = e >> 4, c0 = (e & 15) * 8;
       const bool in = t < len;
-      const int64_t r = (rowbase + pos + (in ? t : 0)) * BD + c0;
-      const bf16x8 qv = ld8(qp + r), kv = ld8(kp + r), vv = ld8(vp + r);
-      bf16x8 dv;
-      if (dop) dv = ld8(dop + r);
+      const bf16x8 qv = tq[i], kv = tk[i], vv = tv[i];
+      const bf16x8 dv = td[i];
       bf16x8 qo, ko, vo, doo;
       float qsum = 0.f, ksum = 0.f;
       if (full) {
@@ -431,6 +447,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
       }
     }
 
+    if (pos + BC < S) load_tiles(pos + BC);
     // ---- phase 6: S' += phi'(k)^T v (own tiles); z', Vsum and the column sums of S' move past the chunk
 #pragma unroll
     for (int i = 0; i < 2; ++i)
