@@ -354,6 +354,17 @@ template <typename T, int N> struct GradStates<T, N, true> {
 // With 8 waves the dx^T tiles' state contraction is split over the two halves of the workgroup; the first half
 // leaves its partial tile here.
 template <int NW> struct DxPartial { float v[NW == 8 ? 4 : 1][64 * 16]; };
+// The six distinct masked/decayed dy.x^T tiles of a head as B-operand fragments: L o XD (t-block, s-block) =
+// (0,0), (1,0), (1,1) and (L o XD o dt)^T (s-block, t-block) = (0,0), (0,1), (1,1).  Shared through LDS for bf16
+// (one wave forms each); fp32 fragments are twice the size and do not fit, so each wave forms its own.
+template <typename T>
+struct XdTiles {
+  Frag<T> xd[3][2][64];
+  Frag<T> xt[3][2][64];
+};
+template <>
+struct XdTiles<float> {};
+
 template <typename T, int N, int NST, bool SL>
 struct GradSmem {
   GradStage<T, N> st[NST];
@@ -364,8 +375,9 @@ struct GradSmem {
   float cs[2 * (N / 32)][SEG];   // per wave: c_t of the current head
   float dtp[2 * (N / 32)][SEG];  // per wave: processed dt
   float red[2][N / 32][SEG];     // per n-block partial dots: bint, u
-  float colg[SEG];               // sum_t (M o XD)[t][s], from fp32 tiles
-  float rowg[SEG];               // sum_s (M o XD)[t][s] dt_s, from fp32 tiles
+  XdTiles<T> xds;                // bf16: the head's XD tiles, formed once and shared (fp32: per wave, none here)
+  float colg[3][32];             // per XD tile (t-block, s-block) = (0,0), (1,0), (1,1): sum_t (M o XD)[t][s]
+  float rowg[3][32];             // per XD^T tile (s-block, t-block) = (0,0), (0,1), (1,1): sum_s (M o XD)[t][s] dt_s
   float lh[N / 32];              // <lam_out, h_in> per n-block
   float dd[2];                   // trace of dy x^T per diagonal 32-block
   float ddp[HD];                 // per-channel dD partial
@@ -540,51 +552,127 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
     sm.dtp[w][l] = dtv;
     const float cs_l = __shfl(cs, s_l), dt_l = __shfl(dtv, s_l);
 
-    // ---- XD[t][s] = dy_t . x_s (tiles tb >= r, column block r), masked and decayed (L o XD), as
-    //      B-operand fragments (column s, k = t)
-    // The per-token sums of M o XD that the decay gradient needs (colG here, rowG below) are taken from
-    // these fp32 tiles, not from the bf16-operand products: the two sums cancel pairwise in da, and only
-    // identically rounded copies cancel.
-    Frag<T> XDf[2][2];
-    float colg = 0.f;
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-      f32x16 a = zero16();
-      if (tb >= r) {
+    constexpr bool SHARE = sizeof(T) == 2;
+    Frag<T> XDf[2][2], XTf[2][2];        // per-wave tiles (fp32 only)
+    if constexpr (SHARE) {
+      // the six distinct XD tiles of the head, wave w forming tiles w, w + NW, ... (same masks, decays and sums
+      // as the per-wave path below; each wave reads its own copies of the decays)
+      for (int tix = w; tix < 6; tix += NW) {
+      if (tix < 3) {
+        const int tb = tix == 0 ? 0 : 1, rr = tix == 2 ? 1 : 0;
+        const int s_p = 32 * rr + l32;
+        const float cs_p = __shfl(cs, s_p);
+        f32x16 a = zero16();
 #pragma unroll
         for (int k = 0; k < HD / 16; ++k)
           a = mma(row_frag<T, T, HD>(sg.DY, 32 * tb + l32, 16 * k + 8 * half),
-                  row_frag<T, T, HD>(sg.X, s_l, 16 * k + 8 * half), a);
+                  row_frag<T, T, HD>(sg.X, s_p, 16 * k + 8 * half), a);
         float ct[16];
         acc_rows(sm.cs[w], 32 * tb, half, ct);
         float d = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int t = 32 * tb + acc_row(half, i);
-          a[i] = (t < len && t >= s_l) ? a[i] * __expf(ct[i] - cs_l) : 0.f;
-          d += (t == s_l) ? a[i] : 0.f;
+          a[i] = (t < len && t >= s_p) ? a[i] * __expf(ct[i] - cs_p) : 0.f;
+          d += (t == s_p) ? a[i] : 0.f;
         }
-        if (nb == 0) {
-          // trace of dy x^T (per-head D): the diagonal block (r, r)
-          if (tb == r) {
-            d = wave_sum(d);
-            if (l == 0) sm.dd[r] = d;
-          }
-          const float* cbp = sm.cb[tb + r] + 16 * l;
+        if (tb == rr) {
+          d = wave_sum(d);
+          if (l == 0) sm.dd[rr] = d;
+        }
+        float cg = 0.f;
+        const float* cbp = sm.cb[tix] + 16 * l;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) colg += v[k] * a[4 * i + k];
+          for (int k = 0; k < 4; ++k) cg += v[k] * a[4 * i + k];
+        }
+        cg += __shfl_xor(cg, 32);
+        if (half == 0) sm.colg[tix][l32] = cg;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) sm.xds.xd[tix][c][l] = acc_to_frag<T>(a, c);
+      } else {
+        const int ti = tix - 3, sb = ti == 2 ? 1 : 0, rr = ti == 0 ? 0 : 1;
+        const int t_p = 32 * rr + l32;
+        const float cs_p = __shfl(cs, t_p);
+        f32x16 a = zero16();
+#pragma unroll
+        for (int k = 0; k < HD / 16; ++k)
+          a = mma(row_frag<T, T, HD>(sg.X, 32 * sb + l32, 16 * k + 8 * half),
+                  row_frag<T, T, HD>(sg.DY, t_p, 16 * k + 8 * half), a);
+        float cr[16], dr[16];
+        acc_rows(sm.cs[w], 32 * sb, half, cr);
+        acc_rows(sm.dtp[w], 32 * sb, half, dr);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int s_ = 32 * sb + acc_row(half, i);
+          a[i] = (t_p < len && s_ <= t_p) ? a[i] * __expf(cs_p - cr[i]) * dr[i] : 0.f;
+        }
+        float rg = 0.f;
+        const float* cbp = sm.cbt[ti] + 16 * l;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) rg += v[k] * a[4 * i + k];
+        }
+        rg += __shfl_xor(rg, 32);
+        if (half == 0) sm.rowg[ti][l32] = rg;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) sm.xds.xt[ti][c][l] = acc_to_frag<T>(a, c);
+      }
+      }
+      lds_barrier();                     // the shared XD tiles are in LDS
+    } else {
+      // ---- XD[t][s] = dy_t . x_s (tiles tb >= r, column block r), masked and decayed (L o XD), as
+      //      B-operand fragments (column s, k = t)
+      // The per-token sums of M o XD that the decay gradient needs (colG here, rowG below) are taken from
+      // these fp32 tiles, not from the bf16-operand products: the two sums cancel pairwise in da, and only
+      // identically rounded copies cancel.
+      float colg = 0.f;
+  #pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        f32x16 a = zero16();
+        if (tb >= r) {
+  #pragma unroll
+          for (int k = 0; k < HD / 16; ++k)
+            a = mma(row_frag<T, T, HD>(sg.DY, 32 * tb + l32, 16 * k + 8 * half),
+                    row_frag<T, T, HD>(sg.X, s_l, 16 * k + 8 * half), a);
+          float ct[16];
+          acc_rows(sm.cs[w], 32 * tb, half, ct);
+          float d = 0.f;
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int t = 32 * tb + acc_row(half, i);
+            a[i] = (t < len && t >= s_l) ? a[i] * __expf(ct[i] - cs_l) : 0.f;
+            d += (t == s_l) ? a[i] : 0.f;
           }
+          if (nb == 0) {
+            // trace of dy x^T (per-head D): the diagonal block (r, r)
+            if (tb == r) {
+              d = wave_sum(d);
+              if (l == 0) sm.dd[r] = d;
+            }
+            const float* cbp = sm.cb[tb + r] + 16 * l;
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
+  #pragma unroll
+              for (int k = 0; k < 4; ++k) colg += v[k] * a[4 * i + k];
+            }
+          }
+        }
+  #pragma unroll
+        for (int c = 0; c < 2; ++c) XDf[tb][c] = acc_to_frag<T>(a, c);
+      }
+      if (nb == 0) {
+        colg += __shfl_xor(colg, 32);
+        if (half == 0) {
+          sm.colg[r == 0 ? 0 : 2][l32] = colg;      // the s-block's sum over its t-blocks
+          if (r == 0) sm.colg[1][l32] = 0.f;
         }
       }
-#pragma unroll
-      for (int c = 0; c < 2; ++c) XDf[tb][c] = acc_to_frag<T>(a, c);
-    }
-    if (nb == 0) {
-      colg += __shfl_xor(colg, 32);
-      if (half == 0) sm.colg[s_l] = colg;
     }
     __builtin_amdgcn_sched_barrier(0);   // keep the phases apart: bounded register lifetimes
     // ---- dB^T tile (n-block nb, s-block r): inter part from lam_out, intra part from C^T (L o XD)
@@ -604,7 +692,10 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
         if (tb >= r) {
           const f32x16 ct = mfma_transpose<T, T, N>(sm.C, 32 * tb, 32 * nb, id, half, l32);   // [t][n]
 #pragma unroll
-          for (int c = 0; c < 2; ++c) aa = mma(acc_to_frag<T>(ct, c), XDf[tb][c], aa);
+          for (int c = 0; c < 2; ++c) {
+            if constexpr (SHARE) aa = mma(acc_to_frag<T>(ct, c), sm.xds.xd[r == 0 ? tb : 2][c][l], aa);
+            else aa = mma(acc_to_frag<T>(ct, c), XDf[tb][c], aa);
+          }
         }
       }
       float Bv[16];
@@ -619,41 +710,46 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       if (half == 0) sm.red[0][nb][s_l] = sI;
     }
     __builtin_amdgcn_sched_barrier(0);   // keep the phases apart: bounded register lifetimes
-    // ---- XD^T[s][t] (tiles sb <= r, column block r), masked, decayed, scaled by dt_s: (column t, k = s)
-    Frag<T> XTf[2][2];
-    float rowg = 0.f;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      f32x16 a = zero16();
-      if (sb <= r) {
-#pragma unroll
-        for (int k = 0; k < HD / 16; ++k)
-          a = mma(row_frag<T, T, HD>(sg.X, 32 * sb + l32, 16 * k + 8 * half),
-                  row_frag<T, T, HD>(sg.DY, s_l, 16 * k + 8 * half), a);
-        float cr[16], dr[16];
-        acc_rows(sm.cs[w], 32 * sb, half, cr);
-        acc_rows(sm.dtp[w], 32 * sb, half, dr);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int s = 32 * sb + acc_row(half, i);
-          a[i] = (s_l < len && s <= s_l) ? a[i] * __expf(cs_l - cr[i]) * dr[i] : 0.f;
-        }
-        if (nb == 0) {
-          const float* cbp = sm.cbt[sb + r] + 16 * l;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) rowg += v[k] * a[4 * i + k];
+    if constexpr (!SHARE) {
+      // ---- XD^T[s][t] (tiles sb <= r, column block r), masked, decayed, scaled by dt_s: (column t, k = s)
+      float rowg = 0.f;
+  #pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        f32x16 a = zero16();
+        if (sb <= r) {
+  #pragma unroll
+          for (int k = 0; k < HD / 16; ++k)
+            a = mma(row_frag<T, T, HD>(sg.X, 32 * sb + l32, 16 * k + 8 * half),
+                    row_frag<T, T, HD>(sg.DY, s_l, 16 * k + 8 * half), a);
+          float cr[16], dr[16];
+          acc_rows(sm.cs[w], 32 * sb, half, cr);
+          acc_rows(sm.dtp[w], 32 * sb, half, dr);
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int s = 32 * sb + acc_row(half, i);
+            a[i] = (s_l < len && s <= s_l) ? a[i] * __expf(cs_l - cr[i]) * dr[i] : 0.f;
+          }
+          if (nb == 0) {
+            const float* cbp = sm.cbt[sb + r] + 16 * l;
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const f32x4 v = *reinterpret_cast<const f32x4*>(cbp + 4 * i);
+  #pragma unroll
+              for (int k = 0; k < 4; ++k) rowg += v[k] * a[4 * i + k];
+            }
           }
         }
+  #pragma unroll
+        for (int c = 0; c < 2; ++c) XTf[sb][c] = acc_to_frag<T>(a, c);
       }
-#pragma unroll
-      for (int c = 0; c < 2; ++c) XTf[sb][c] = acc_to_frag<T>(a, c);
-    }
-    if (nb == 0) {
-      rowg += __shfl_xor(rowg, 32);
-      if (half == 0) sm.rowg[s_l] = rowg;
+      if (nb == 0) {
+        rowg += __shfl_xor(rowg, 32);
+        if (half == 0) {
+          sm.rowg[r == 0 ? 0 : 1][l32] = rowg;      // the t-block's sum over its s-blocks
+          if (r == 1) sm.rowg[2][l32] = 0.f;
+        }
+      }
+
     }
 
     // <lam_out, h_in> over the blocks of n-block nb (one wave per n-block)
@@ -684,7 +780,10 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
         if (sb <= r) {
           const f32x16 bt = mfma_transpose<T, T, N>(sm.B, 32 * sb, 32 * nb, id, half, l32);   // [s][n]
 #pragma unroll
-          for (int c = 0; c < 2; ++c) ac = mma(acc_to_frag<T>(bt, c), XTf[sb][c], ac);
+          for (int c = 0; c < 2; ++c) {
+            if constexpr (SHARE) ac = mma(acc_to_frag<T>(bt, c), sm.xds.xt[r == 0 ? 0 : (sb == 0 ? 1 : 2)][c][l], ac);
+            else ac = mma(acc_to_frag<T>(bt, c), XTf[sb][c], ac);
+          }
         }
       }
       float Cv[16];
@@ -808,7 +907,8 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       store_dx();
     }
     if (w == 0) {
-      const float colG = sm.colg[l], rowG = sm.rowg[l];
+      const float colG = l < 32 ? sm.colg[0][l] + sm.colg[1][l] : sm.colg[2][l - 32];
+      const float rowG = l < 32 ? sm.rowg[0][l] : sm.rowg[1][l - 32] + sm.rowg[2][l - 32];
       float bint = 0.f, u = 0.f, lh = 0.f;
 #pragma unroll
       for (int k = 0; k < NB; ++k) {
