@@ -17,7 +17,9 @@ a step from the previous one.  The same JSON line carries:
 * ``decode`` -- selective state update at B=64 and B=256 (HBM GB/s vs 8 TB/s).
 * ``other`` -- ssd4 (128K prefill with state carry), kda5 (gated KDA scan), ssd2_bwd (the backward of
   the ssd2 prefill: all input gradients from dy and d_final) and kda5_bwd (the backward of the reference-mode
-  KDA scan with the fused differential output at the kda5 shape: dq1, dq2, dk, dv and d lambda).
+  KDA scan with the fused differential output at the kda5 shape: dq1, dq2, dk, dv and d lambda), conv1d (the
+  layer's conv + SiLU forward and backward at the ssd2 layer shape), kda5_ref (the reference-mode scan at the kda5
+  shape) and kda_step (the KDA decode step, B 64, H 32).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu] [--only LEGS]
                        [--copy-calibration BYTES]
@@ -206,6 +208,80 @@ def bench_kda_bwd(cfg, steps, warmup):
     return res
 
 
+def bench_conv1d(steps, warmup):
+    """Causal conv1d + SiLU (the Mamba layer prologue) at the ssd2 layer shape: x (2, 4096, d_inner 4096) bf16, width 4.
+    Forward: x read, y written; backward: x and dy read, dx written (dweight / dbias and the per-run partials are
+    small).  Launched through fixed-buffer plans, timed with HIP events."""
+    import ctypes as ct
+    from mamformer_amd import _lib, ops
+    b, L, D, K = 2, 4096, 4096, 4
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(b, L, D, device="cuda", generator=g).to(torch.bfloat16)
+    dy = torch.randn(b, L, D, device="cuda", generator=g).to(torch.bfloat16)
+    w = (0.5 * torch.randn(D, K, device="cuda", generator=g)).contiguous()
+    bias = torch.randn(D, device="cuda", generator=g)
+    y = torch.empty_like(x)
+    a = ops._conv_args(x, w, bias, None, True)
+    a.y, a.y_stride_b, a.y_stride_l = ops._ptr(y), y.stride(0), y.stride(1)
+    fwd = ops.Plan("mh_causal_conv1d_fwd", a, x.device, keep=(x, w, bias, y))
+    dx = torch.empty_like(x)
+    dw = torch.empty_like(w)
+    db = torch.empty_like(bias)
+    q = _lib.Conv1dBwdArgs()
+    q.fwd = ops._conv_args(x, w, bias, None, True)
+    q.dy, q.dy_stride_b, q.dy_stride_l = ops._ptr(dy), dy.stride(0), dy.stride(1)
+    q.dx, q.dx_stride_b, q.dx_stride_l = ops._ptr(dx), dx.stride(0), dx.stride(1)
+    q.dweight, q.dbias = ops._ptr(dw), ops._ptr(db)
+    n = ct.c_size_t()
+    _lib.call("mh_conv1d_bwd_workspace_bytes", ct.byref(q), ct.byref(n))
+    ws = torch.empty(n.value, device="cuda", dtype=torch.uint8)
+    q.workspace, q.workspace_bytes = ws.data_ptr(), n.value
+    bwd = ops.Plan("mh_causal_conv1d_bwd", q, x.device, keep=(x, w, bias, dy, dx, dw, db, ws))
+    xb = b * L * D * 2
+    res = {}
+    for name, plan, nbytes in (("fwd", fwd, 2 * xb), ("bwd", bwd, 3 * xb)):
+        _, ev = time_plans([plan], steps, warmup)
+        t = ev * 1e-3
+        res[name] = dict(us_per_step=ev * 1e3, alg_bytes=nbytes, hbm_GBs=nbytes / t / 1e9,
+                         roofline_frac=nbytes / PEAK_HBM / t)
+    return res
+
+
+def bench_kda_ref(cfg, steps, warmup):
+    """Reference-mode KDA scan (phi = elu + 1, normaliser, fused differential output) at the kda5 shape:
+    q1, q2, k, v read and the output written (bf16)."""
+    import mamformer_amd as mh
+    from mamformer_amd import workloads as W
+    inp = W.kda_inputs(cfg, device="cuda")
+    lam = mh.diff_lambda(torch.linspace(-2.0, 3.0, cfg.nheads, device="cuda"))
+    plan = mh.plan_linear_attn_scan(inp["q1"], inp["q2"], inp["k"], inp["v"], mode="reference", kernel_dim=cfg.dk,
+                                    lam=lam)
+    _, ev = time_plans([plan], steps, warmup)
+    nbytes = cfg.batch * cfg.nheads * cfg.seqlen * (4 * cfg.dk * 2 + cfg.dv * 2)
+    t = ev * 1e-3
+    res = dict(mtok_s=cfg.batch * cfg.seqlen / t / 1e6, us_per_step=ev * 1e3, alg_bytes=nbytes,
+               hbm_GBs=nbytes / t / 1e9, roofline_frac=nbytes / PEAK_HBM / t)
+    del plan, inp
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_kda_step(steps, warmup, batch=64, nheads=32, dk=128, dv=128):
+    """KDA decode: one reference-mode recurrent step (phi applied in the kernel) for `batch` sequences of `nheads`
+    heads: the fp32 state and normaliser read and written in place, q1, q2, k, v, o per head."""
+    import mamformer_amd as mh
+    g = torch.Generator(device="cuda").manual_seed(5)
+    state = 0.1 * torch.randn(batch, nheads, dk, dv, device="cuda", generator=g)
+    z = torch.rand(batch, nheads, dk, device="cuda", generator=g) + 1.0
+    mk = lambda d: (torch.randn(batch, nheads, d, device="cuda", generator=g) / d ** 0.5).to(torch.bfloat16)
+    q1, q2, k, v = mk(dk), mk(dk), mk(dk), mk(dv)
+    plan = mh.plan_linear_attn_step(state, z, q1, q2, k, v, lam=0.8, kernel_dim=dk)
+    _, ev = time_plans([plan], steps, warmup)
+    nbytes = batch * nheads * (2 * dk * dv * 4 + 2 * dk * 4 + 3 * dk * 2 + 2 * dv * 2)
+    t = ev * 1e-3
+    return dict(us_per_step=ev * 1e3, alg_bytes=nbytes, hbm_GBs=nbytes / t / 1e9, roofline_frac=nbytes / PEAK_HBM / t)
+
+
 def bench_decode(cfg, steps, warmup, nsets):
     import mamformer_amd as mh
     from mamformer_amd import workloads as W
@@ -298,7 +374,7 @@ def measured_traffic(workload="ssd2"):
 
 # ----------------------------------------------------------------- main
 
-LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd2_bwd", "kda5_bwd", "ssd1", "cpu")
+LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd2_bwd", "kda5_bwd", "conv1d", "kda5_ref", "kda_step", "ssd1", "cpu")
 
 
 def main():
@@ -406,6 +482,22 @@ def main():
         log(f"kda5 backward (reference mode, differential output): {r['us_per_step']:.0f} us, "
             f"{r['tflops']:.0f} TFLOP/s, roofline {r['roofline_frac']:.3f}")
         other["kda5_bwd"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+    if "conv1d" in legs:
+        r = bench_conv1d(args.steps, args.warmup)
+        log(f"conv1d+SiLU (b2 L4096 D4096 K4 bf16): forward {r['fwd']['us_per_step']:.1f} us "
+            f"({r['fwd']['roofline_frac']:.3f} of 8 TB/s), backward {r['bwd']['us_per_step']:.1f} us "
+            f"({r['bwd']['roofline_frac']:.3f})")
+        other["conv1d"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                           for k, v in r.items()}
+    if "kda5_ref" in legs:
+        r = bench_kda_ref(W.KDA5, max(5, args.steps // 5), 3)
+        log(f"kda5 reference mode (differential output): {r['us_per_step']:.0f} us, roofline {r['roofline_frac']:.3f}")
+        other["kda5_ref"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+    if "kda_step" in legs:
+        r = bench_kda_step(args.steps, args.warmup)
+        log(f"KDA decode step B=64 H=32: {r['us_per_step']:.1f} us, {r['hbm_GBs']:.0f} GB/s "
+            f"({r['roofline_frac']:.3f} of 8 TB/s)")
+        other["kda_step"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
     if "ssd1" in legs:
         r, _, _ = bench_ssd(W.SSD1, args.steps, args.warmup, nsets=1, chunk=64)
         other["ssd1"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
