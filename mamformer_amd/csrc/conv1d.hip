@@ -21,7 +21,8 @@ namespace mh {
 namespace {
 
 constexpr int CV = 8;      // channels per thread
-constexpr int TT = 32;     // tokens per thread
+constexpr int TT = 32;     // tokens per thread in the backward (one dweight/dbias partial per run)
+constexpr int TTF = 16;    // tokens per thread in the forward (twice the workgroups of TT, to fill the CUs)
 constexpr int KMAX = 8;
 
 template <typename T>
@@ -53,13 +54,41 @@ __device__ __forceinline__ void store8(T* p, const float (&v)[CV]) {
   }
 }
 
+// A row of 8 channels as loaded (converted to fp32 when used), so that a group of rows can be in flight at once:
+// a run walks its tokens in order, and one load per step would put the full memory latency on every token.
+template <typename T> struct Raw8;
+template <> struct Raw8<bf16> { bf16x8 v; };
+template <> struct Raw8<float> { f32x4 a, b; };
+template <typename T>
+__device__ __forceinline__ Raw8<T> ldraw(const T* p) {
+  Raw8<T> r;
+  if constexpr (sizeof(T) == 2) {
+    r.v = *reinterpret_cast<const bf16x8*>(p);
+  } else {
+    r.a = *reinterpret_cast<const f32x4*>(p);
+    r.b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ void cvt8(const Raw8<T>& r, float (&v)[CV]) {
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int i = 0; i < CV; ++i) v[i] = (float)r.v[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[i] = r.a[i]; v[4 + i] = r.b[i]; }
+  }
+}
+constexpr int RG = 8;      // rows loaded together
+
 template <typename T, int K>
 __global__ __launch_bounds__(256) void conv1d_kernel(Conv1dParams p) {
   const int c8 = blockIdx.x * 256 + threadIdx.x;
   const int d0 = c8 * CV;
   if (d0 >= p.dim) return;
   const int b = blockIdx.z;
-  const int t0 = blockIdx.y * TT;
+  const int t0 = blockIdx.y * TTF;
   const T* xb = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + d0;
   const T* sb = p.conv_state ? reinterpret_cast<const T*>(p.conv_state) + (int64_t)b * p.cs_sb + d0 : nullptr;
   T* yb = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_sb + d0;
@@ -87,9 +116,8 @@ __global__ __launch_bounds__(256) void conv1d_kernel(Conv1dParams p) {
       for (int i = 0; i < CV; ++i) win[j][i] = 0.f;
     }
   }
-  const int t1 = min(p.seqlen, t0 + TT);
-  for (int t = t0; t < t1; ++t) {
-    load8<T>(xb + (int64_t)t * p.x_sl, win[K - 1]);
+  const int t1 = min(p.seqlen, t0 + TTF);
+  auto emit = [&](int t) {               // win[K-1] holds row t
     float o[CV];
 #pragma unroll
     for (int i = 0; i < CV; ++i) {
@@ -103,6 +131,21 @@ __global__ __launch_bounds__(256) void conv1d_kernel(Conv1dParams p) {
     for (int j = 0; j < K - 1; ++j)
 #pragma unroll
       for (int i = 0; i < CV; ++i) win[j][i] = win[j + 1][i];
+  };
+  int t = t0;
+  for (; t + RG <= t1; t += RG) {
+    Raw8<T> rx[RG];
+#pragma unroll
+    for (int r = 0; r < RG; ++r) rx[r] = ldraw<T>(xb + (int64_t)(t + r) * p.x_sl);
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      cvt8<T>(rx[r], win[K - 1]);
+      emit(t + r);
+    }
+  }
+  for (; t < t1; ++t) {
+    load8<T>(xb + (int64_t)t * p.x_sl, win[K - 1]);
+    emit(t);
   }
 }
 
@@ -165,10 +208,7 @@ __global__ __launch_bounds__(256) void conv1d_bwd_kernel(Conv1dBwdParams q) {
   const int slo = (t0 == 0 && q.dcs) ? -p.cs_len : t0;
   T* dcsb = q.dcs ? reinterpret_cast<T*>(q.dcs) + (int64_t)b * q.dcs_sb + d0 : nullptr;
   auto row = [&](int s) { return s >= 0 ? dxb + (int64_t)s * q.dx_sl : dcsb + (int64_t)(p.cs_len + s) * q.dcs_sl; };
-  for (int t = t0; t < tlast; ++t) {
-    load8<T>(xb + (int64_t)t * p.x_sl, win[K - 1]);
-    float g[CV];
-    load8<T>(dyb + (int64_t)t * q.dy_sl, g);
+  auto step = [&](int t, const float (&g)[CV]) {   // win[K-1] holds x row t, g the output gradient of row t
     float du[CV];
 #pragma unroll
     for (int i = 0; i < CV; ++i) {
@@ -211,6 +251,28 @@ __global__ __launch_bounds__(256) void conv1d_bwd_kernel(Conv1dBwdParams q) {
       }
       store8<T>(row(s), o);
     }
+  };
+  int t = t0;
+  for (; t + RG <= tlast; t += RG) {
+    Raw8<T> rx[RG], rg[RG];
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      rx[r] = ldraw<T>(xb + (int64_t)(t + r) * p.x_sl);
+      rg[r] = ldraw<T>(dyb + (int64_t)(t + r) * q.dy_sl);
+    }
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      float g[CV];
+      cvt8<T>(rx[r], win[K - 1]);
+      cvt8<T>(rg[r], g);
+      step(t + r, g);
+    }
+  }
+  for (; t < tlast; ++t) {
+    float g[CV];
+    load8<T>(xb + (int64_t)t * p.x_sl, win[K - 1]);
+    load8<T>(dyb + (int64_t)t * q.dy_sl, g);
+    step(t, g);
   }
   // rows whose du window runs past the sequence end (du = 0 there).  The window advances one zero per s
   // from s = tlast - (K-1) (the first s the main loop did not emit), so its last slot is du[s + K - 1]
@@ -242,21 +304,28 @@ __global__ __launch_bounds__(256) void conv1d_bwd_kernel(Conv1dBwdParams q) {
   }
 }
 
-// dweight (D, K) and dbias (D,) = sums over the nparts partials, in a fixed order.
+// dweight (D, K) and dbias (D,) = sums over the nparts partials, in a fixed order: 64 outputs per workgroup, each
+// output's partials split over 4 slices of the workgroup (partial k to slice k % 4), the slices added in order.
 __global__ __launch_bounds__(256) void conv1d_reduce_kernel(const float* __restrict__ dw_part,
                                                             const float* __restrict__ db_part, int nparts, int dim,
                                                             int K, float* __restrict__ dw, float* __restrict__ db) {
-  const int e = blockIdx.x * 256 + threadIdx.x;
-  const int nw = dim * K;
-  if (e < nw) {
-    float acc = 0.f;
-    for (int k = 0; k < nparts; ++k) acc += dw_part[(int64_t)k * nw + e];
-    dw[e] = acc;
-  } else if (e < nw + dim && db) {
-    const int d = e - nw;
-    float acc = 0.f;
-    for (int k = 0; k < nparts; ++k) acc += db_part[(int64_t)k * dim + d];
-    db[d] = acc;
+  __shared__ float red[4][64];
+  const int lo = threadIdx.x & 63, sl = threadIdx.x >> 6;
+  const int e = blockIdx.x * 64 + lo;
+  const int nw = dim * K, n = nw + (db ? dim : 0);
+  float acc = 0.f;
+  if (e < n) {
+    const float* src = e < nw ? dw_part + e : db_part + (e - nw);
+    const int64_t stride = e < nw ? nw : dim;
+#pragma unroll 8
+    for (int k = sl; k < nparts; k += 4) acc += src[(int64_t)k * stride];
+  }
+  red[sl][lo] = acc;
+  __syncthreads();
+  if (sl == 0 && e < n) {
+    const float v = ((red[0][lo] + red[1][lo]) + red[2][lo]) + red[3][lo];
+    if (e < nw) dw[e] = v;
+    else db[e - nw] = v;
   }
 }
 
@@ -274,14 +343,14 @@ hipError_t launch_bwd_t(const Conv1dBwdParams& q, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int n = p.dim * p.width + p.dim;
-  hipLaunchKernelGGL(conv1d_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, q.dw_part, q.db_part,
+  hipLaunchKernelGGL(conv1d_reduce_kernel, dim3((unsigned)((n + 63) / 64)), dim3(256), 0, st, q.dw_part, q.db_part,
                      p.batch * nrun, p.dim, p.width, q.dweight, q.dbias);
   return hipGetLastError();
 }
 
 template <typename T>
 hipError_t launch_t(const Conv1dParams& p, hipStream_t st) {
-  dim3 grid((unsigned)((p.dim / CV + 255) / 256), (unsigned)((p.seqlen + TT - 1) / TT), (unsigned)p.batch);
+  dim3 grid((unsigned)((p.dim / CV + 255) / 256), (unsigned)((p.seqlen + TTF - 1) / TTF), (unsigned)p.batch);
   switch (p.width) {
 #define CASE(K) case K: hipLaunchKernelGGL((conv1d_kernel<T, K>), grid, dim3(256), 0, st, p); break;
     CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
