@@ -439,6 +439,35 @@ struct KdaRefSmem {
   Frag<bf16> Alo[3 * NQ][2][64];         // ... and the bf16 rounding remainder (A = A + Alo to ~2^-17)
 };
 
+// Register-staged raw rows of one segment: per thread 4 16-byte chunks of k and of each query (element
+// e = tid + 256 i: token e >> 4, channels 8 (e & 15) ..), 2 of v (token e >> 3, columns 8 (e & 7) ..).
+template <int NQ>
+struct KdaRefStage {
+  bf16x8 k[4], q[NQ][4];
+  uint4 v[2];
+};
+
+template <int NQ>
+__device__ __forceinline__ void kda_ref_load(KdaRefStage<NQ>& g, const bf16* const (&qp)[2], const bf16* kk,
+                                             const bf16* vv, int64_t rowbase, int pos, int len, int v0, int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tid + 256 * i;
+    const int t = e >> 4, k0 = (e & 15) * 8;
+    const int64_t r = (rowbase + pos + min(t, len - 1)) * DK + k0;
+    g.k[i] = *reinterpret_cast<const bf16x8*>(kk + r);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) g.q[j][i] = *reinterpret_cast<const bf16x8*>(qp[j] + r);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int e = tid + 256 * i;
+    const int t = e >> 3, c0 = (e & 7) * 8;
+    g.v[i] = t < len ? *reinterpret_cast<const uint4*>(vv + (rowbase + pos + t) * 128 + v0 + c0)
+                     : make_uint4(0, 0, 0, 0);
+  }
+}
+
 }  // namespace
 
 template <int NQ>
@@ -466,7 +495,7 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
   const float lam = p.lam_h ? p.lam_h[h] : p.lam;
   const float inv_1ml = 1.f / (1.f - lam + 1e-8f);
   const int64_t rowbase = (int64_t)bh * S;
-  const bf16* qp[2] = {reinterpret_cast<const bf16*>(p.q1), reinterpret_cast<const bf16*>(p.q2)};
+  const bf16* const qp[2] = {reinterpret_cast<const bf16*>(p.q1), reinterpret_cast<const bf16*>(p.q2)};
   const bf16* kk = reinterpret_cast<const bf16*>(p.k);
   const bf16* vv = reinterpret_cast<const bf16*>(p.v);
   bf16* op[2] = {reinterpret_cast<bf16*>(p.o), reinterpret_cast<bf16*>(p.o2)};
@@ -487,35 +516,46 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
   }
   if (tid < DK) sm.z[tid] = p.init_z ? p.init_z[(int64_t)bh * DK + tid] : 0.f;
 
+  static_assert(SEGK * (DK / 8) == 4 * 256 && SEGK * (DVH / 8) == 2 * 256, "staging covers a segment");
+  KdaRefStage<NQ> stg;
+  if (S > 0) kda_ref_load<NQ>(stg, qp, kk, vv, rowbase, 0, min(SEGK, S), v0, tid);
   for (int pos = 0; pos < S; pos += SEGK) {
     const int len = min(SEGK, S - pos);
-    // ---- phase B: phi(q_i), phi(k), v tiles
-    for (int e = tid; e < SEGK * (DK / 8); e += 256) {
+    // ---- phase B: phi(q_i), phi(k), v tiles from the staged rows; then stage the next segment's rows
+#pragma unroll
+    for (int ie = 0; ie < 4; ++ie) {
+      const int e = tid + 256 * ie;
       const int t = e >> 4, k0 = (e & 15) * 8;
       const bool in = t < len;
-      const int64_t r = (rowbase + pos + min(t, len - 1)) * DK + k0;
-      const bf16x8 kv8 = *reinterpret_cast<const bf16x8*>(kk + r);
+      const bf16x8 kv8 = stg.k[ie];
       bf16x8 qv8[NQ];
 #pragma unroll
-      for (int i = 0; i < NQ; ++i) qv8[i] = *reinterpret_cast<const bf16x8*>(qp[i] + r);
+      for (int i = 0; i < NQ; ++i) qv8[i] = stg.q[i][ie];
       bf16x8 ko;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ko[j] = (bf16)((in && k0 + j < kd) ? phi1((float)kv8[j]) : 0.f);
+      for (int j = 0; j < 8; ++j) {   // computed unconditionally, then selected: no branch per element
+        const float f = phi1((float)kv8[j]);
+        ko[j] = (bf16)((in && k0 + j < kd) ? f : 0.f);
+      }
       *reinterpret_cast<bf16x8*>(&sm.Kt[t * SM::PK + k0]) = ko;
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
         bf16x8 qo;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qo[j] = (bf16)((in && k0 + j < kd) ? phi1((float)qv8[i][j]) : 0.f);
+        for (int j = 0; j < 8; ++j) {
+          const float f = phi1((float)qv8[i][j]);
+          qo[j] = (bf16)((in && k0 + j < kd) ? f : 0.f);
+        }
         *reinterpret_cast<bf16x8*>(&sm.Q[i][t * SM::PK + k0]) = qo;
       }
     }
-    for (int e = tid; e < SEGK * (DVH / 8); e += 256) {
+#pragma unroll
+    for (int ie = 0; ie < 2; ++ie) {
+      const int e = tid + 256 * ie;
       const int t = e >> 3, c0 = (e & 7) * 8;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (t < len) val = *reinterpret_cast<const uint4*>(vv + (rowbase + pos + t) * 128 + v0 + c0);
-      *reinterpret_cast<uint4*>(&sm.V[t * SM::PV + c0]) = val;
+      *reinterpret_cast<uint4*>(&sm.V[t * SM::PV + c0]) = stg.v[ie];
     }
+    if (pos + SEGK < S) kda_ref_load<NQ>(stg, qp, kk, vv, rowbase, pos + SEGK, min(SEGK, S - pos - SEGK), v0, tid);
     __syncthreads();
 
     // ---- phase B2: phi(q_i,t) . z_prev  (4 adjacent lanes per (query, token), 32 channels each)
