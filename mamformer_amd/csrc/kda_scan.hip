@@ -522,33 +522,36 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
   for (int pos = 0; pos < S; pos += SEGK) {
     const int len = min(SEGK, S - pos);
     // ---- phase B: phi(q_i), phi(k), v tiles from the staged rows; then stage the next segment's rows
+    auto stage = [&](auto MASKc) {     // MASK: zero tokens past the segment end and channels past kernel_dim
+      constexpr bool MASK = decltype(MASKc)::value;
 #pragma unroll
-    for (int ie = 0; ie < 4; ++ie) {
-      const int e = tid + 256 * ie;
-      const int t = e >> 4, k0 = (e & 15) * 8;
-      const bool in = t < len;
-      const bf16x8 kv8 = stg.k[ie];
-      bf16x8 qv8[NQ];
+      for (int ie = 0; ie < 4; ++ie) {
+        const int e = tid + 256 * ie;
+        const int t = e >> 4, k0 = (e & 15) * 8;
+        const bool in = t < len;
+        const bf16x8 kv8 = stg.k[ie];
+        bf16x8 ko;
 #pragma unroll
-      for (int i = 0; i < NQ; ++i) qv8[i] = stg.q[i][ie];
-      bf16x8 ko;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {   // computed unconditionally, then selected: no branch per element
-        const float f = phi1((float)kv8[j]);
-        ko[j] = (bf16)((in && k0 + j < kd) ? f : 0.f);
-      }
-      *reinterpret_cast<bf16x8*>(&sm.Kt[t * SM::PK + k0]) = ko;
-#pragma unroll
-      for (int i = 0; i < NQ; ++i) {
-        bf16x8 qo;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float f = phi1((float)qv8[i][j]);
-          qo[j] = (bf16)((in && k0 + j < kd) ? f : 0.f);
+        for (int j = 0; j < 8; ++j) {   // computed unconditionally, then selected: no branch per element
+          const float f = phi1((float)kv8[j]);
+          ko[j] = (bf16)((!MASK || (in && k0 + j < kd)) ? f : 0.f);
         }
-        *reinterpret_cast<bf16x8*>(&sm.Q[i][t * SM::PK + k0]) = qo;
+        *reinterpret_cast<bf16x8*>(&sm.Kt[t * SM::PK + k0]) = ko;
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) {
+          const bf16x8 qv8 = stg.q[i][ie];
+          bf16x8 qo;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float f = phi1((float)qv8[j]);
+            qo[j] = (bf16)((!MASK || (in && k0 + j < kd)) ? f : 0.f);
+          }
+          *reinterpret_cast<bf16x8*>(&sm.Q[i][t * SM::PK + k0]) = qo;
+        }
       }
-    }
+    };
+    if (len == SEGK && kd >= DK) stage(std::false_type{});
+    else stage(std::true_type{});
 #pragma unroll
     for (int ie = 0; ie < 2; ++ie) {
       const int e = tid + 256 * ie;
@@ -654,12 +657,15 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
       }
 #pragma unroll
     for (int qi = 0; qi < NQ; ++qi) {
+      // wave kh finishes token tile tt = kh: it adds the intra-segment term of that tile and hands its
+      // read-out partial of the other tile to the partner wave (same vt, other k-half)
       if (kh == 0) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           o[qi][0] = mma(vf[c], sm.A[3 * qi + 0][c][l], o[qi][0]);
           o[qi][0] = mma(vf[c], sm.Alo[3 * qi + 0][c][l], o[qi][0]);
         }
+        sm.red[vt][qi][1][l] = o[qi][1];
       } else {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -669,7 +675,6 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
           o[qi][1] = mma(vf[2 + c], sm.Alo[3 * qi + 2][c][l], o[qi][1]);
         }
         sm.red[vt][qi][0][l] = o[qi][0];
-        sm.red[vt][qi][1][l] = o[qi][1];
       }
     }
     // state update (no decay): S[k][v] += sum_s phi(k_s)[k] v_s[v]
@@ -688,35 +693,35 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
       St[i] = acc;
     }
     __syncthreads();
-    if (kh == 0) {
+    auto finish = [&](auto TTc) {
+      constexpr int tt = decltype(TTc)::value;
+      const int tl = 32 * tt + l32;
+      if (tl < len) {
+        float res[NQ][16];
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int tl = 32 * tt + l32;
-        if (tl < len) {
-          float res[NQ][16];
+        for (int qi = 0; qi < NQ; ++qi) {
+          const float nr = sm.zq[qi][tl] + (tt == 0 ? sm.nrm[qi][0][l32] : sm.nrm[qi][1][l32] + sm.nrm[qi][2][l32]);
+          const float inv = 1.f / (nr + 1e-8f);
+          const f32x16 other = sm.red[vt][qi][tt][l];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) res[qi][r] = (o[qi][tt][r] + other[r]) * inv;
+        }
+        if (fuse_diff) {
+          bf16* orow = op[0] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = (bf16)((res[0][r] - lam * res[NQ - 1][r]) * inv_1ml);
+        } else {
 #pragma unroll
           for (int qi = 0; qi < NQ; ++qi) {
-            const float nr = sm.zq[qi][tl] + (tt == 0 ? sm.nrm[qi][0][l32] : sm.nrm[qi][1][l32] + sm.nrm[qi][2][l32]);
-            const float inv = 1.f / (nr + 1e-8f);
-            const f32x16 other = sm.red[vt][qi][tt][l];
+            bf16* orow = op[qi] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) res[qi][r] = (o[qi][tt][r] + other[r]) * inv;
-          }
-          if (fuse_diff) {
-            bf16* orow = op[0] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = (bf16)((res[0][r] - lam * res[NQ - 1][r]) * inv_1ml);
-          } else {
-#pragma unroll
-            for (int qi = 0; qi < NQ; ++qi) {
-              bf16* orow = op[qi] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
-#pragma unroll
-              for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = (bf16)res[qi][r];
-            }
+            for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = (bf16)res[qi][r];
           }
         }
       }
-    }
+    };
+    if (kh == 0) finish(std::integral_constant<int, 0>{});
+    else finish(std::integral_constant<int, 1>{});
     __syncthreads();
   }
 
