@@ -561,8 +561,9 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
     if (pos + SEGK < S) kda_ref_load<NQ>(stg, qp, kk, vv, rowbase, pos + SEGK, min(SEGK, S - pos - SEGK), v0, tid);
     __syncthreads();
 
-    // ---- phase B2: phi(q_i,t) . z_prev  (4 adjacent lanes per (query, token), 32 channels each)
-    for (int it = tid; it < NQ * SEGK * 4; it += 256) {
+    // ---- phase B2: phi(q_i,t) . z_prev  (4 adjacent lanes per (query, token), 32 channels each).
+    // Waves 0-1 take one item per lane (they form two A tiles in phase C), waves 2-3 the rest (one tile).
+    for (int it = tid; it < NQ * SEGK * 4; it += (tid < 128 ? NQ * SEGK * 4 : 128)) {
       const int i = it / (SEGK * 4), t = (it >> 2) % SEGK, qq = it & 3;
       const bf16* row = &sm.Q[i][t * SM::PK + 32 * qq];
       float acc = 0.f;
@@ -618,11 +619,13 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
     __syncthreads();
 
     // ---- z update (z_prev was consumed by phase B2 before the barrier)
-    {
-      const int kc = tid & 127, th = tid >> 7;
+    // by the k-half 0 waves, whose read-out phase below has half the intra-segment MFMAs of the k-half 1 waves;
+    // one lane per channel, in token order
+    if (tid < DK) {
       float zs = 0.f;
-      for (int t = th * 32; t < th * 32 + 32; ++t) zs += (float)sm.Kt[t * SM::PK + kc];
-      atomicAdd(&sm.z[kc], zs);
+#pragma unroll 8
+      for (int t = 0; t < SEGK; ++t) zs += (float)sm.Kt[t * SM::PK + tid];
+      sm.z[tid] += zs;
     }
 
     // ---- phase D: per wave (v-tile vt, k-half kh)
