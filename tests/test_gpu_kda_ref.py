@@ -158,3 +158,15 @@ def test_ref_kda5_shape_properties():
     check("kda5 ref o2[-256:]", o2[:, :2, -n:], r2, 1e-2)
     check("kda5 ref final S", fin[:, :2], rs, 1e-2)
     check("kda5 ref final z", finz[:, :2], rz, 1e-3)
+
+
+def test_ref_scan_is_bit_reproducible():
+    """The normaliser's running sum z is added in a fixed order (one lane per channel, tokens in order) and every
+    other reduction is a fixed MFMA or shuffle sequence, so two calls give identical bits: outputs, final S and z."""
+    B, H, S = 2, 3, 300
+    x = {k: dev(v, BF) for k, v in inputs(B, H, S, 77).items()}
+    say("ref scan reproducibility")
+    runs = [mh.linear_attn_scan(x["q1"], x["q2"], x["k"], x["v"], mode="reference", kernel_dim=128, pair=True,
+                                return_final_state=True) for _ in range(2)]
+    for a, b, name in zip(runs[0], runs[1], ("o1", "o2", "final S", "final z")):
+        assert torch.equal(a, b), name
