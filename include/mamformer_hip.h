@@ -9,7 +9,9 @@
  *
  * Conventions
  *  - All tensor pointers are device pointers owned by the caller; the library
- *    never allocates device memory and never synchronises the stream.
+ *    never allocates device memory at run time and never synchronises the
+ *    stream (its one static device array, the scratch of
+ *    mh_ssd_chunk_scan_fwd_noalloc, is created with the code object).
  *  - Strides are in elements.  The innermost dimension of every tensor is
  *    contiguous; 16-byte vector access requires 16-byte aligned base pointers
  *    and row strides that are multiples of 16 bytes (checked).
@@ -29,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MH_ABI_VERSION 5
+#define MH_ABI_VERSION 6
 
 /* element types of x / B / C / y / q / k / v / o */
 enum { MH_F32 = 0, MH_BF16 = 1 };
@@ -91,6 +93,18 @@ int mh_ssd_workspace_bytes(const mh_ssd_args* a, size_t* bytes);
 /* Resolved chunk_len (auto choice when a->chunk_len == 0). */
 int mh_ssd_chunk_len(const mh_ssd_args* a, int64_t* chunk_len);
 int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream);
+
+/* Same prefill, allocating nothing: no counterpart in the reference.  For callers that cannot allocate
+ *   device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ *   a->workspace / a->workspace_bytes are ignored: the kernels use a file-scope static device array of
+ *   MH_NOALLOC_SCRATCH_BYTES, one per GPU the library runs on, held until the process ends.  Sizes whose
+ *   workspace (mh_ssd_workspace_bytes) exceeds it are rejected with MH_ERR_WORKSPACE before any HIP
+ *   call.  Every call on one GPU uses that GPU's single array: calls that overlap in time on one GPU
+ *   (several streams or host threads) race and must be serialised by the caller.  The first call on
+ *   each GPU looks up the array's device address (hipGetSymbolAddress), which allocates nothing.
+ *   Results are bit-identical to mh_ssd_chunk_scan_fwd's for the same arguments. */
+#define MH_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int mh_ssd_chunk_scan_fwd_noalloc(const mh_ssd_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
  * SSD chunked-scan prefill backward.

@@ -12,7 +12,10 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
 
-ABI_VERSION = 5
+ABI_VERSION = 6
+
+# bytes of the static device scratch behind mh_ssd_chunk_scan_fwd_noalloc (MH_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 MH_F32, MH_BF16 = 0, 1
 MH_DT_SOFTPLUS, MH_DT_LIMIT, MH_D_PER_CHANNEL = 1, 2, 4
@@ -141,7 +144,7 @@ class Conv1dBwdArgs(ct.Structure):
 # every symbol include/mamformer_hip.h declares
 EXPORTS = (
     "mh_abi_version", "mh_last_error",
-    "mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
+    "mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd", "mh_ssd_chunk_scan_fwd_noalloc",
     "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",
     "mh_ssd_state_update",
     "mh_kda_chunk_scan_fwd", "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
@@ -179,6 +182,7 @@ def lib():
             h.mh_ssd_workspace_bytes.argtypes = [ct.POINTER(SsdArgs), ct.POINTER(_sz)]
             h.mh_ssd_chunk_len.argtypes = [ct.POINTER(SsdArgs), ct.POINTER(_i64)]
             h.mh_ssd_chunk_scan_fwd.argtypes = [ct.POINTER(SsdArgs), _vp]
+            h.mh_ssd_chunk_scan_fwd_noalloc.argtypes = [ct.POINTER(SsdArgs), _vp]
             h.mh_ssd_bwd_workspace_bytes.argtypes = [ct.POINTER(SsdBwdArgs), ct.POINTER(_sz)]
             h.mh_ssd_chunk_scan_bwd.argtypes = [ct.POINTER(SsdBwdArgs), _vp]
             h.mh_ssd_state_update.argtypes = [ct.POINTER(SsuArgs), _vp]
@@ -190,6 +194,7 @@ def lib():
             h.mh_conv1d_bwd_workspace_bytes.argtypes = [ct.POINTER(Conv1dBwdArgs), ct.POINTER(_sz)]
             h.mh_causal_conv1d_bwd.argtypes = [ct.POINTER(Conv1dBwdArgs), _vp]
             for name in ("mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd",
+                         "mh_ssd_chunk_scan_fwd_noalloc",
                          "mh_ssd_state_update", "mh_kda_chunk_scan_fwd", "mh_kda_recurrent_step",
                          "mh_causal_conv1d_fwd", "mh_conv1d_bwd_workspace_bytes", "mh_causal_conv1d_bwd",
                          "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",

@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/mamformer_hip.h"
 #include "launch.h"
 
@@ -213,6 +215,39 @@ int conv_validate(const mh_conv1d_args* a) {
   return MH_OK;
 }
 
+// ------------------------------------------------------------------ static scratch (no-allocation entry)
+// The workspace of mh_ssd_chunk_scan_fwd_noalloc: one array per GPU, created with the code object and held
+// until the process ends.  Host code never passes `scratch` itself to a kernel (its host-side name is not a
+// device address); it uses the per-device address hipGetSymbolAddress returns, looked up once per device.
+__device__ __align__(256) unsigned char scratch[MH_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to (the current device for the null stream).
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipStreamGetDevice(stream, &dev);
+  if (e != hipSuccess) return hip_status(e, "ssd_noalloc: hipStreamGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(MH_ERR_UNSUPPORTED, "ssd_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_status(e, "ssd_noalloc: hipGetDevice");
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_status(e, "ssd_noalloc: hipSetDevice");
+    void* addr = nullptr;
+    const hipError_t es = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (cur != dev && (e = hipSetDevice(cur)) != hipSuccess) return hip_status(e, "ssd_noalloc: hipSetDevice");
+    if (es != hipSuccess) return hip_status(es, "ssd_noalloc: hipGetSymbolAddress(scratch)");
+    if (!addr) return fail(MH_ERR_HIP, "ssd_noalloc: hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_addr[dev] = addr;
+  }
+  *out = g_scratch_addr[dev];
+  return MH_OK;
+}
+
 // Forward parameter block from a validated argument struct (workspace not laid out).
 void ssd_fill(const mh_ssd_args* a, int64_t cl, int64_t nchunks, mh::SsdParams& p) {
   memset(&p, 0, sizeof(p));
@@ -393,6 +428,27 @@ int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream) {
   ssd_fill(a, cl, nchunks, p);
   if (nchunks > 0) mh::ssd_workspace_layout(p, a->workspace);
   return hip_status(mh::launch_ssd(p, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_fwd");
+}
+
+int mh_ssd_chunk_scan_fwd_noalloc(const mh_ssd_args* a, void* stream) {
+  int64_t cl = 0;
+  int rc = ssd_validate(a, &cl);
+  if (rc) return rc;
+  const int64_t nchunks = (a->seqlen + cl - 1) / cl;
+  const size_t need = mh::ssd_workspace_bytes((int)a->batch, (int)a->seqlen, (int)nchunks, (int)a->nheads,
+                                              (int)a->headdim, (int)a->dstate, (int)a->ngroups, a->dtype);
+  if (need > MH_NOALLOC_SCRATCH_BYTES)
+    return fail(MH_ERR_WORKSPACE, "ssd_noalloc: these sizes need %zu bytes of workspace, more than the %zu-byte static "
+                "scratch (call mh_ssd_chunk_scan_fwd with a caller workspace)", need, (size_t)MH_NOALLOC_SCRATCH_BYTES);
+  mh::SsdParams p;
+  ssd_fill(a, cl, nchunks, p);
+  if (nchunks > 0) {
+    void* ws = nullptr;
+    rc = scratch_address(reinterpret_cast<hipStream_t>(stream), &ws);
+    if (rc) return rc;
+    mh::ssd_workspace_layout(p, ws);
+  }
+  return hip_status(mh::launch_ssd(p, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_fwd_noalloc");
 }
 
 int mh_ssd_state_update(const mh_ssu_args* a, void* stream) {

@@ -88,6 +88,28 @@ def test_ssd_rejects_null_and_misaligned_pointers_and_small_workspace():
     assert _rc("mh_ssd_chunk_scan_fwd", None, None) == -1
 
 
+def test_ssd_noalloc_validates_and_rejects_sizes_beyond_its_static_scratch():
+    # the 128K shape of the benchmark (b1 L131072 H128 N128 G8) needs far more workspace than the scratch
+    a = _good_ssd()
+    b, L, H, P, N, G = 1, 131072, 128, 64, 128, 8
+    a.batch, a.seqlen, a.nheads, a.ngroups = b, L, H, G
+    a.x_stride_l = a.y_stride_l = H * P
+    a.x_stride_b = a.y_stride_b = L * H * P
+    a.B_stride_l = a.C_stride_l = G * N
+    a.B_stride_b = a.C_stride_b = L * G * N
+    a.dt_stride_l, a.dt_stride_b = H, L * H
+    n = ct.c_size_t()
+    assert _rc("mh_ssd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+    assert n.value > _lib.NOALLOC_SCRATCH_BYTES
+    assert _rc("mh_ssd_chunk_scan_fwd_noalloc", ct.byref(a), None) == -7
+    assert b"static" in _lib.lib().mh_last_error()
+    # argument checks come first, exactly as for the workspace entry point
+    a = _good_ssd()
+    a.C = None
+    assert _rc("mh_ssd_chunk_scan_fwd_noalloc", ct.byref(a), None) == -1
+    assert _rc("mh_ssd_chunk_scan_fwd_noalloc", None, None) == -1
+
+
 def test_ssd_and_state_update_validate_the_output_gate():
     a = _good_ssd()
     a.z, a.z_stride_b, a.z_stride_l, a.z_stride_h = ct.c_void_p(4096), a.y_stride_b, a.y_stride_l, a.y_stride_h
