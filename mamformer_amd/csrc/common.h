@@ -96,6 +96,13 @@ __device__ __forceinline__ Frag<TM> acc_to_frag_scaled(const f32x16& acc, int c,
 
 // ---------------------------------------------------------------- wave helpers
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// The lane index recomputed where it is used (v_mbcnt in a volatile asm): address arithmetic built on it is not
+// hoisted out of loops, where it would hold registers for the whole loop.
+__device__ __forceinline__ int lane_id_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
 // Wave index within the workgroup, in a scalar register (wave-uniform for the compiler).
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
@@ -173,7 +180,8 @@ __device__ __forceinline__ float softplus_f(float x) {
   return __logf(1.f + e);
 }
 
-// silu(x) = x / (1 + e^{-x}); e^{-x} overflowing to +inf gives -0 (the limit) for very negative x.
-__device__ __forceinline__ float silu_f(float x) { return __fdividef(x, 1.f + __expf(-x)); }
+// silu(x) = x / (1 + e^{-x}), the quotient through the hardware reciprocal (v_rcp_f32, 1 ulp) rather than an
+// IEEE division sequence; e^{-x} overflowing to +inf gives -0 (the limit) for very negative x.
+__device__ __forceinline__ float silu_f(float x) { return x * __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 }  // namespace mh

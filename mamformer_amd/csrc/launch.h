@@ -52,8 +52,14 @@ struct SsdParams {
   void* seg_frags;       // workspace: [batch][ngroups][nseg] shared MFMA fragments of each 64-token segment
   void* entering;        // workspace (bf16 I/O): bf16 entering states, chunk_states order
   int nseg;              // ceil(seqlen / 64)
+  int state_perm;        // workspace states in state_row_perm row order (two-pass prefill)
 };
 hipError_t launch_ssd(const SsdParams& p, hipStream_t st);
+// The two-pass bf16 prefill (ssd_lookback.hip): sizes it implements, and its launch.
+bool ssd_lb_supported(int dtype, int dstate);
+hipError_t launch_ssd_lb(const SsdParams& p, hipStream_t st);
+// Entering states from chunk states (ssd_state_pass_kernel): H_0 = h0, H_{k+1} = e^{T_k} H_k + S_k.
+hipError_t launch_ssd_state_pass(const SsdParams& p, hipStream_t st);
 size_t ssd_frag_bytes(int dtype, int dstate);
 size_t ssd_workspace_bytes(int batch, int seqlen, int nchunks, int nheads, int headdim, int dstate, int ngroups,
                            int dtype);

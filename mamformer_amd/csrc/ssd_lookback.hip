@@ -1,0 +1,817 @@
+// Mamba-2 SSD chunked-scan prefill for gfx950, bf16 I/O, in two passes over the sequence.
+//
+// Recurrence (per batch b, head h with group g = h / (H/G), channel p, state n):
+//     h_t = exp(A_h dt_t) h_{t-1} + dt_t x_t[p] B_t[g, n]
+//     y_t[p] = sum_n C_t[g, n] h_t[p, n] + D x_t[p]
+// -- the reference's selective_scan (mamformer/layers/mamba2.py:84-126) in the per-head SSD form, with an
+// optional initial state and the final state returned for the decode cache.
+//
+// Pass 1, ssd_lb_state_kernel, one workgroup per (chunk, batch, block of HG heads): the chunk-local state
+//     S_k[p, n] = sum_{s in k} exp(sum_{s < tau in k} A dt_tau) dt_s x_s[p] B_s[n]
+// and the chunk's total log-decay T_k.  The chunk is walked from its last 64-token segment to its first, so
+// every decay factor is taken relative to the chunk end and is at most 1: the accumulators never need
+// rescaling.  The per-token weight w_s multiplies x on the MFMA unit (xs = diag(w) x, x read transposed out
+// of LDS with ds_read_b64_tr_b16).  S_k leaves in bf16, in MFMA fragment order with its state rows permuted
+// (state_row_perm), the order in which the scan's read-out meets C in natural column order.
+//
+// Pass 2, ssd_lb_scan_kernel, same workgroups: the entering state
+//     H_k = sum_{j<k} exp(T_{j+1} + .. + T_{k-1}) S_j  +  exp(T_0 + .. + T_{k-1}) h0
+// is summed straight from pass 1's chunk states (a look-back over at most LB_MAX - 1 predecessors; longer
+// sequences get the entering states from ssd_state_pass_kernel between the passes), then the chunk is walked
+// forward in 64-token segments with the running state in MFMA accumulators, carried lazily as
+// H_true = e^kappa H so that one scaled operand xs_s = e^{-kappa-cs_s} dt_s x_s serves both the state update
+// H += B^T xs and the intra-segment term (cs_t the in-segment inclusive cumulative log-decay):
+//     y_t = e^{kappa + cs_t} (C_t H^T + sum_{s<=t} (C_t . B_s) xs_s) + D x_t,   kappa += cs_end.
+// The three masked (C B^T) tiles of a segment are formed once per workgroup and shared through LDS.  A
+// segment whose own decay range exceeds LB_FACT_RANGE takes an exact per-element path (wave-uniform branch).
+//
+// Work split (both passes): a workgroup owns HG heads of one group, one wave per head (one wave per SIMD);
+// a wave's state is its head's 64 columns p as two 32-column halves of N/32 accumulator tiles (rows n, columns
+// p), so every B / C operand fragment it reads from LDS feeds one MFMA per half, and the decay, the weights
+// and the diagonal operands are formed once for both halves.  Every segment's tiles (x, B, C, dt) are fetched
+// straight into LDS (global_load_lds) ahead of use, in the Sub64 layout (tiles.h): every LDS access of the
+// loops is one lane offset (a few per kernel) plus an immediate, the stage being a compile-time index (the
+// segment loop is unrolled by the number of stages).
+#include <type_traits>
+
+#include "common.h"
+#include "launch.h"
+#include "ssd_shared.h"
+#include "tiles.h"
+
+namespace mh {
+
+namespace {
+
+constexpr float LB_FACT_RANGE = 60.f;   // max exponent of an operand scale factor (pass 2)
+constexpr size_t LB_LDS_BYTES = 160 * 1024;
+
+template <int v> using IC = std::integral_constant<int, v>;
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// ds_read_b64_tr_b16: within each 16-lane group the four lanes 4k..4k+3 name a row of 16 consecutive 16-bit
+// elements (4 each, 8-byte aligned) and lane j of the group receives element j of rows k = 0..3.
+__device__ __forceinline__ i16x4 ds_tr16(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+}
+
+// Lane offsets (elements) of the access patterns, each valid for every sub-tile and token block.
+struct LaneOffs {
+  int tr[2];     // transposed read: rows 4 half + (lane & 15) / 4 (+ 8 for [1]), columns 16 ((lane >> 4) & 1) + 4 (lane & 3)
+  int trp[2];    // the same with the column pieces 4-7 and 8-11 of each 16 swapped (lane j gets column state_row_perm(j))
+  int row[2];    // row fragment: row lane % 32, columns 16 c + 8 half, [c]
+  int piece[4];  // 8-byte row pieces: row lane % 32, columns 8 q + 4 half, [q]
+};
+__device__ __forceinline__ LaneOffs lane_offs(int l) {
+  const int half = l >> 5, l32 = l & 31, i = l & 15;
+  const int tc = 16 * ((l >> 4) & 1) + 4 * (i & 3);
+  const int tcp = 16 * ((l >> 4) & 1) + 4 * (((i & 1) << 1) | ((i >> 1) & 1));
+  LaneOffs o;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) o.tr[e] = Sub64::off(4 * half + (i >> 2) + 8 * e, tc);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) o.trp[e] = Sub64::off(4 * half + (i >> 2) + 8 * e, tcp);
+#pragma unroll
+  for (int c = 0; c < 2; ++c) o.row[c] = Sub64::off(l32, 16 * c + 8 * half);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o.piece[q] = Sub64::off(l32, 8 * q + 4 * half);
+  return o;
+}
+
+// MFMA operand fragment read transposed from a Sub64 sub-tile: the lane's column is lane % 32 (state_row_perm
+// of it with the trp offsets) and its 8 k-values are the tokens row0 + KSET(half, 0..7) (row0 % 16 == 0).  The
+// same registers serve as an A operand (row = tile column) or a B operand (column = tile column).
+__device__ __forceinline__ Frag<bf16> tr_frag(const bf16* sub, int row0, const int (&off)[2]) {
+  const i16x4 a = ds_tr16(sub + row0 * Sub64::W + off[0]);
+  const i16x4 b = ds_tr16(sub + row0 * Sub64::W + off[1]);
+  Frag<bf16> f;
+  f.v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+  return f;
+}
+// Row fragment: row row0 + lane % 32 (row0 % 32 == 0), the 8 consecutive columns 16 c + 8 half of a sub-tile.
+__device__ __forceinline__ Frag<bf16> row_frag64(const bf16* sub, int row0, int c, const LaneOffs& lo) {
+  Frag<bf16> f;
+  f.v = *reinterpret_cast<const bf16x8*>(sub + row0 * Sub64::W + lo.row[c]);
+  return f;
+}
+
+// Diagonal A-operand fragments (k-steps c = 0, 1) of one 32-token block, D[s][s'] = w_s [s == s'].  Lane
+// (row s = lane % 32, half) holds its diagonal element only in k-step s >> 4 at position
+// (s & 3) + 4 ((s >> 3) & 1), and only when half == (s >> 2) & 1 (the KSET order); the masks below select
+// that 16-bit slot.
+struct DiagMask {
+  uint32_t m[2][4];
+};
+__device__ __forceinline__ DiagMask diag_mask(int l) {
+  const int s = l & 31, half = l >> 5;
+  const bool on = half == ((s >> 2) & 1);
+  const int cc = s >> 4, jj = (s & 3) + 4 * ((s >> 3) & 1);
+  DiagMask d;
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      d.m[c][q] = (on && c == cc && q == (jj >> 1)) ? ((jj & 1) ? 0xffff0000u : 0x0000ffffu) : 0u;
+  return d;
+}
+__device__ __forceinline__ void diag_frags(float w, const DiagMask& dm, Frag<bf16> (&f)[2]) {
+  const uint32_t b = (uint32_t)__builtin_bit_cast(uint16_t, (bf16)w);
+  const uint32_t d = b | (b << 16);
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    u32x4 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = d & dm.m[c][q];
+    f[c].v = __builtin_bit_cast(bf16x8, v);
+  }
+}
+
+// The value of lane (32 * st + lane % 32) in every lane: [0] for st = 0, [1] for st = 1.
+__device__ __forceinline__ void halves(float v, float (&o)[2]) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  o[0] = __uint_as_float(r[0]);
+  o[1] = __uint_as_float(r[1]);
+}
+
+// Workgroup -> (chunk k, chain = batch * (H / HG) + head block).  Workgroups are dealt to the 8 XCDs
+// round-robin by index; when the chains split evenly over them, every chunk of a chain runs on one XCD, so the
+// scan finds its predecessors' chunk states and the x tiles pass 1 just read in that XCD's L2.
+__device__ __forceinline__ void lb_block(int nchunks, int nchains, int& k, int& chain) {
+  const int i = blockIdx.x;
+  if ((nchains & 7) == 0) {
+    const int cpx = nchains >> 3, s = i >> 3;
+    chain = (i & 7) + 8 * (s % cpx);
+    k = s / cpx;
+  } else {
+    k = i % nchunks;
+    chain = i / nchunks;
+  }
+}
+
+// xs = diag(w) x for the wave's PH 64 x 32 halves of its head (Sub64 sub-tiles at x + ph ELEMS): B-operand
+// fragments xa[ph][2 * st + c] (k = token of block st, k-step c; column = p).  wb[st] = w of token
+// 32 st + lane % 32.
+template <int PH>
+__device__ __forceinline__ void scaled_x(const bf16* x, const float (&wb)[2], const DiagMask& dm, const LaneOffs& lo,
+                                         Frag<bf16> (&xa)[PH][4]) {
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    Frag<bf16> dg[2];
+    diag_frags(wb[st], dm, dg);
+#pragma unroll
+    for (int ph = 0; ph < PH; ++ph) {
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int c = 0; c < 2; ++c) acc = mma(dg[c], tr_frag(x + ph * Sub64::ELEMS, 32 * st + 16 * c, lo.tr), acc);
+      xa[ph][2 * st] = acc_to_frag<bf16>(acc, 0);
+      xa[ph][2 * st + 1] = acc_to_frag<bf16>(acc, 1);
+    }
+  }
+}
+
+// H[ph][n][p] += sum_s B^T[n][s] xs[ph][s][p] over the segment's 64 tokens, B^T read transposed from the B tile
+// with the state rows in state_row_perm order; the fragments of tile nt + 1 are requested before tile nt's
+// MFMAs.
+template <int N, int PH>
+__device__ __forceinline__ void lb_state_update(f32x16 (&H)[PH][N / 32], const bf16* btile,
+                                                const Frag<bf16> (&xa)[PH][4], const LaneOffs& lo) {
+  Frag<bf16> cur[4], nxt[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) cur[c] = tr_frag(btile, 16 * c, lo.trp);
+#pragma unroll
+  for (int nt = 0; nt < N / 32; ++nt) {
+    if (nt + 1 < N / 32) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) nxt[c] = tr_frag(btile + (nt + 1) * Sub64::ELEMS, 16 * c, lo.trp);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int ph = 0; ph < PH; ++ph) H[ph][nt] = mma(cur[c], xa[ph][c], H[ph][nt]);
+    if (nt + 1 < N / 32) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) cur[c] = nxt[c];
+    }
+  }
+}
+
+// Read-out of the state entering the segment, Y^T[ph][tt][p][t] = sum_n H[ph][p][n] C[32 tt + t][n] (C as natural
+// row fragments: the permuted state rows meet natural column order in the KSET-ordered accumulator fragments),
+// fused per 32-row state tile with the state update H += B^T xs; the fragments of tile nt + 1 are requested
+// before tile nt's MFMAs.
+template <int N, int PH>
+__device__ __forceinline__ void readout(f32x16 (&H)[PH][N / 32], f32x16 (&Y)[PH][2], const bf16* ctile,
+                                        const bf16* btile, const Frag<bf16> (&xa)[PH][4], const LaneOffs& lo) {
+  Frag<bf16> cc[4], cb[4], nc[4], nb[4];   // C: [2 c + tt], B: [c]
+  auto load = [&](int nt, Frag<bf16> (&fc)[4], Frag<bf16> (&fb)[4]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) fc[2 * c + tt] = row_frag64(ctile + nt * Sub64::ELEMS, 32 * tt, c, lo);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) fb[c] = tr_frag(btile + nt * Sub64::ELEMS, 16 * c, lo.trp);
+  };
+  load(0, cc, cb);
+#pragma unroll
+  for (int nt = 0; nt < N / 32; ++nt) {
+    if (nt + 1 < N / 32) load(nt + 1, nc, nb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const Frag<bf16> hf = acc_to_frag<bf16>(H[ph][nt], c);
+        Y[ph][0] = mma(hf, cc[2 * c], Y[ph][0]);
+        Y[ph][1] = mma(hf, cc[2 * c + 1], Y[ph][1]);
+      }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int ph = 0; ph < PH; ++ph) H[ph][nt] = mma(cb[c], xa[ph][c], H[ph][nt]);
+    if (nt + 1 < N / 32) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        cc[c] = nc[c];
+        cb[c] = nb[c];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ pass 1
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Waves of a workgroup: HG heads of one group, 2 / PH waves per head, each owning PH of the head's two
+// 32-column halves (columns 32 (ph0 + ph) .. of x, y and the state).
+template <int HG, int PH>
+constexpr int lb_waves = HG * (2 / PH);
+
+// Per-wave constants of a workgroup's chunk (both passes).
+struct LbWave {
+  int w, l, hw, ph0, c0, c1, last, nseg;
+  float Ah, dtb;
+  const bf16* xg;     // x of the wave's head, token 0, column 0
+  const bf16* Bg;     // B of the head's group, token 0
+  const bf16* Cg;     // C of the head's group, token 0
+  const float* dtg;   // dt of the wave's head, token 0
+};
+template <int N, int HG, int PH>
+__device__ __forceinline__ LbWave lb_wave(const SsdParams& p, int& k, int& b, int& h) {
+  const int nhb = p.nheads / HG;
+  int chain;
+  lb_block(p.nchunks, p.batch * nhb, k, chain);
+  b = chain / nhb;
+  LbWave c;
+  c.w = wave_id();
+  c.l = lane_id();
+  c.hw = c.w / (2 / PH);
+  c.ph0 = PH == 2 ? 0 : (c.w & 1);
+  h = (chain - b * nhb) * HG + c.hw;
+  const int g = h / (p.nheads / p.ngroups);
+  c.c0 = k * p.chunk_len;
+  c.c1 = min(p.seqlen, c.c0 + p.chunk_len);
+  c.last = p.seqlen - 1;
+  c.nseg = (c.c1 - c.c0 + SEG - 1) / SEG;
+  c.Ah = p.A[h];
+  c.dtb = p.dt_bias ? p.dt_bias[h] : 0.f;
+  c.xg = reinterpret_cast<const bf16*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh;
+  c.Bg = reinterpret_cast<const bf16*>(p.B) + (int64_t)b * p.B_sb + (int64_t)g * N;
+  c.Cg = reinterpret_cast<const bf16*>(p.C) + (int64_t)b * p.C_sb + (int64_t)g * N;
+  c.dtg = p.dt + (int64_t)b * p.dt_sb + h;
+  return c;
+}
+
+template <int N, int HG>
+struct LbStateStage {
+  bf16 X[HG][2][Sub64::ELEMS];    // per head: its x tile, two 32-column halves
+  bf16 Bt[N / 32][Sub64::ELEMS];  // B tile
+  float dt[HG][SEG];              // per head: raw dt
+};
+template <int N, int HG>
+constexpr int lb_state_nbuf = 3 * sizeof(LbStateStage<N, HG>) <= LB_LDS_BYTES ? 3 : 2;
+
+// Segment si of the chunk into a pass-1 stage: every wave issues exactly N / 8 / NW + 4 PH + 1 loads (its
+// share of the B tile, its halves of its head's x tile, its head's dt; rows past the end of the sequence are
+// clamped).
+template <int N, int HG, int PH>
+__device__ __forceinline__ void lb_state_fetch(const SsdParams& p, const LbWave& c,
+                                               LbStateStage<N, HG>* __restrict__ s, int si) {
+  constexpr int BB = N / 8 / lb_waves<HG, PH>;
+  const int pos = c.c0 + si * SEG;
+  fetch_sub64(&s->Bt[0][0], c.Bg, p.B_sl, pos, c.last, c.w * BB, BB);
+  fetch_sub64(&s->X[c.hw][0][0], c.xg, p.x_sl, pos, c.last, 4 * c.ph0, 4 * PH);
+  fetch_dt(s->dt[c.hw], c.dtg, p.dt_sl, pos, c.last, lane_id_here());
+}
+
+// Segment si of pass 1's reverse walk, its tiles in stage `cur`; segment fsi (if >= 0) is fetched into
+// stage `nxt`.  The stage pointers are __restrict__: the compiler otherwise makes every LDS read wait for all
+// outstanding global -> LDS loads (it cannot tell that they write another stage).  `more`: the fetch of the
+// next segment of the walk is in flight.
+template <int N, int HG, int PH, int NBUF>
+__device__ __forceinline__ void lb_state_segment(const SsdParams& p, const LbWave& c,
+                                                 const LbStateStage<N, HG>* __restrict__ cur,
+                                                 LbStateStage<N, HG>* __restrict__ nxt, int si, int fsi, bool more,
+                                                 f32x16 (&S)[PH][N / 32], float& R, const DiagMask& dm,
+                                                 const LaneOffs& lo) {
+  constexpr int LOADS = N / 8 / lb_waves<HG, PH> + 4 * PH + 1;
+  if (NBUF == 3 && more) wait_vmem_n<LOADS>();             // this segment's loads; the next one's may fly
+  else wait_vmem();
+  lds_barrier();                                           // the segment's tiles are in LDS for every wave
+  if (fsi >= 0) lb_state_fetch<N, HG, PH>(p, c, nxt, fsi);
+  const int pos = c.c0 + si * SEG;
+  float dtv;
+  const float cs = seg_decay(p, cur->dt[c.hw][c.l], c.dtb, c.Ah, pos + c.l, c.c1, dtv);
+  const float cse = readlane_f(cs, SEG - 1);
+  // weight of token s relative to the chunk end: exp(R + cse - cs_s) dt_s <= dt_s
+  float wb[2];
+  halves(__expf(R + cse - cs) * dtv, wb);
+  Frag<bf16> xa[PH][4];
+  scaled_x<PH>(&cur->X[c.hw][c.ph0][0], wb, dm, lo, xa);
+  lb_state_update<N, PH>(S, &cur->Bt[0][0], xa, lo);
+  R += cse;
+}
+
+template <int N, int HG, int PH>
+__global__ __launch_bounds__(64 * HG * (2 / PH)) void ssd_lb_state_kernel(SsdParams p) {
+  constexpr int NT = N / 32;
+  constexpr int NBUF = lb_state_nbuf<N, HG>;
+  static_assert((N / 8) % lb_waves<HG, PH> == 0, "B tile split evenly over the waves");
+  __shared__ LbStateStage<N, HG> st[NBUF];
+  int k, b, h;
+  const LbWave c = lb_wave<N, HG, PH>(p, k, b, h);
+  const int nseg = c.nseg, l = c.l;
+  const DiagMask dm = diag_mask(l);
+  const LaneOffs lo = lane_offs(l);
+  f32x16 S[PH][NT];
+#pragma unroll
+  for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) S[ph][nt] = zero16();
+  float R = 0.f;                                           // log-decay of the segments after the current one
+  // segments are walked last to first: iteration it handles segment nseg - 1 - it, in stage it % NBUF, and
+  // fetches segment nseg - it - NBUF into the stage freed by the previous iteration
+#pragma unroll
+  for (int d = 0; d < NBUF - 1; ++d)
+    if (d < nseg) lb_state_fetch<N, HG, PH>(p, c, &st[d], nseg - 1 - d);
+  for (int it = 0; it < nseg; it += NBUF) {
+#pragma unroll
+    for (int u = 0; u < NBUF; ++u)
+      if (it + u < nseg) {
+        const int si = nseg - 1 - it - u;
+        lb_state_segment<N, HG, PH, NBUF>(p, c, &st[u], &st[(u + NBUF - 1) % NBUF], si, si - (NBUF - 1),
+                                          it + u + 1 < nseg, S, R, dm, lo);
+      }
+  }
+  // chunk-local state in fragment order (bf16) and the chunk's log-decay
+  const int64_t obase = (((int64_t)b * p.nchunks + k) * p.nheads + h) * (HD * N);
+#pragma unroll
+  for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      bf16x8* o8 = reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(p.chunk_states) + obase +
+                                             frag_off(nt, c.ph0 + ph, l));
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        bf16x8 v;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (bf16)S[ph][nt][8 * q + i];
+        o8[q] = v;
+      }
+    }
+  if (c.ph0 == 0 && l == 0) p.chunk_decay[((int64_t)b * p.nheads + h) * p.nchunks + k] = R;
+}
+
+// ------------------------------------------------------------------ pass 2
+
+constexpr int LB_DSEG = 4;   // segments per decay block: their in-segment decays are formed together
+
+// Two stages of segment tiles.  ds_read / ds_write take a 16-bit byte immediate: the B and C tiles of both
+// stages lie in the first 64 KB and the x tiles of both stages in one 64 KB window, so each lane access
+// pattern needs one address register for every stage and tile.
+template <int N, int HG, int NW>
+struct LbScanSmem {
+  bf16 Bt[2][N / 32][Sub64::ELEMS];   // B tile per stage
+  bf16 Ct[2][N / 32][Sub64::ELEMS];   // C tile per stage
+  Frag<bf16> mt[3][2][64];            // masked (C B^T)^T tiles (s0,t0), (s0,t1), (s1,t1) as B-operand fragments
+  float dec[NW][LB_DSEG][2][SEG];     // per wave: [0] cs_t, [1] dt_t of its head, segments of the decay block
+  float dcol[HG][HD];                 // D per column of each head
+  bf16 X[2][HG][2][Sub64::ELEMS];     // per stage and head: its x tile (two halves); y staged in place
+};
+
+// Masked (C B^T)^T tile ti of the segment: acc[s][t] = C_t . B_s for s <= t, as two B-operand fragments.
+template <int N>
+__device__ __forceinline__ void cb_tile(int ti, const bf16* btile, const bf16* ctile, Frag<bf16>* out,
+                                        const LaneOffs& lo, int l) {
+  const int st = (ti == 2) ? 1 : 0, tt = (ti == 0) ? 0 : 1;
+  const int half = l >> 5, l32 = l & 31;
+  f32x16 acc = zero16();
+#pragma unroll
+  for (int c = 0; c < N / 16; ++c)
+    acc = mma(row_frag64(btile + (c >> 1) * Sub64::ELEMS, 32 * st, c & 1, lo),
+              row_frag64(ctile + (c >> 1) * Sub64::ELEMS, 32 * tt, c & 1, lo), acc);
+  if (st == tt) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (acc_row(half, r) > l32) acc[r] = 0.f;
+  }
+  out[l] = acc_to_frag<bf16>(acc, 0);
+  out[64 + l] = acc_to_frag<bf16>(acc, 1);
+}
+
+// y rows staged in the wave's PH Sub64 halves (x + ph ELEMS): the 16-byte chunks of rows e / 4
+// (e = lane + 64 i), column 8 (e % 4) of half ph, as v[4 ph + i].
+template <int PH>
+__device__ __forceinline__ void load_y64(const bf16* x, uint4 (&v)[4 * PH]) {
+  const int lane = lane_id_here();
+#pragma unroll
+  for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      v[4 * ph + i] = *reinterpret_cast<const uint4*>(x + ph * Sub64::ELEMS + Sub64::off(e >> 2, 8 * (e & 3)));
+    }
+}
+// Rows [0, len) of the staged chunks to HBM (dst at the column of the wave's first half).
+template <int PH>
+__device__ __forceinline__ void store_y64(bf16* dst, int64_t row_stride, const uint4 (&v)[4 * PH], int len) {
+  const int lane = lane_id_here();
+#pragma unroll
+  for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      if ((e >> 2) < len)
+        *reinterpret_cast<uint4*>(dst + (int64_t)(e >> 2) * row_stride + 32 * ph + 8 * (e & 3)) = v[4 * ph + i];
+    }
+}
+// Gate rows z of the wave's halves in the lane order of load_y64 (rows past rmax re-read row rmax).
+template <int PH>
+__device__ __forceinline__ void load_z64(const bf16* src, int64_t row_stride, int rmax, uint4 (&v)[4 * PH]) {
+  const int lane = lane_id_here();
+#pragma unroll
+  for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      v[4 * ph + i] =
+          *reinterpret_cast<const uint4*>(src + (int64_t)min(e >> 2, rmax) * row_stride + 32 * ph + 8 * (e & 3));
+    }
+}
+template <int M>
+__device__ __forceinline__ void gate_rows(uint4 (&v)[M], const uint4 (&z)[M]) {
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    bf16x8 y = __builtin_bit_cast(bf16x8, v[i]);
+    const bf16x8 g = __builtin_bit_cast(bf16x8, z[i]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = (bf16)((float)y[j] * silu_f((float)g[j]));
+    v[i] = __builtin_bit_cast(uint4, y);
+  }
+}
+
+// H[ph][nt] += f S on the MFMA unit, for the wave's halves of one state S in bf16 fragment order
+// (v[ph][nt][c] = the B-operand fragment of k-step c of tile (nt, ph0 + ph)): A = f I, with f split into bf16
+// parts f_hi + f_lo (LO: else f is taken as exact in bf16), so the sum keeps about 16 bits of f.
+template <int N, int PH, bool LO>
+__device__ __forceinline__ void add_state(f32x16 (&H)[PH][N / 32], const bf16x8 (&v)[PH][N / 32][2], float f,
+                                          const DiagMask& dm) {
+  Frag<bf16> dh[2], dl[2];
+  const float fh = (float)(bf16)f;
+  diag_frags(fh, dm, dh);
+  if constexpr (LO) diag_frags(f - fh, dm, dl);
+#pragma unroll
+  for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+    for (int nt = 0; nt < N / 32; ++nt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        Frag<bf16> s;
+        s.v = v[ph][nt][c];
+        H[ph][nt] = mma(dh[c], s, H[ph][nt]);
+        if constexpr (LO) H[ph][nt] = mma(dl[c], s, H[ph][nt]);
+      }
+}
+
+// Segment tiles of pass 2 into one stage (bt, ct: the tiles; xw: the wave's first x half): every wave issues
+// exactly 2 N / 8 / NW + 4 PH loads.
+template <int N, int HG, int PH>
+__device__ __forceinline__ void lb_scan_fetch(const SsdParams& p, const LbWave& c, bf16* __restrict__ bt,
+                                              bf16* __restrict__ ct, bf16* __restrict__ xw, int si) {
+  constexpr int BB = N / 8 / lb_waves<HG, PH>;
+  const int pos = c.c0 + si * SEG;
+  fetch_sub64(bt, c.Bg, p.B_sl, pos, c.last, c.w * BB, BB);
+  fetch_sub64(ct, c.Cg, p.C_sl, pos, c.last, c.w * BB, BB);
+  fetch_sub64(xw - 4 * c.ph0 * 512, c.xg, p.x_sl, pos, c.last, 4 * c.ph0, 4 * PH);
+}
+// Raw dt of the LB_DSEG segments from s0 into the dt slots of the wave's decay block (LB_DSEG loads; tokens
+// past the sequence re-read its last one), and their forming in place into cs and dt (tokens past the chunk
+// get dt = 0).
+__device__ __forceinline__ void lb_dt_fetch(const SsdParams& p, const LbWave& c, float* __restrict__ dec, int s0) {
+  const int lane = lane_id_here();
+#pragma unroll
+  for (int j = 0; j < LB_DSEG; ++j)
+    fetch_dt(dec + (2 * j + 1) * SEG, c.dtg, p.dt_sl, min(c.c0 + (s0 + j) * SEG, c.last), c.last, lane);
+}
+__device__ __forceinline__ void lb_dt_form(const SsdParams& p, const LbWave& c, float* __restrict__ dec, int s0) {
+#pragma unroll
+  for (int j = 0; j < LB_DSEG; ++j) {
+    float dtv;
+    const float cs = seg_decay(p, dec[(2 * j + 1) * SEG + c.l], c.dtb, c.Ah, c.c0 + (s0 + j) * SEG + c.l, c.c1, dtv);
+    dec[2 * j * SEG + c.l] = cs;
+    dec[(2 * j + 1) * SEG + c.l] = dtv;
+  }
+}
+
+// Segment si of pass 2, its tiles in the stage (bt, ct, xw: the wave's first x half); the other stage (bt_n,
+// ct_n, xw_n) holds the staged y of segment si - 1 and receives segment si + 1.  All LDS pointers a global ->
+// LDS load may write are __restrict__ parameters: the compiler otherwise makes every LDS read wait for all
+// outstanding global -> LDS loads (it cannot tell that they write the other stage).
+template <int N, int HG, int PH, bool GATE>
+__device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave& c, int si,
+                                                const bf16* __restrict__ bt, const bf16* __restrict__ ct,
+                                                bf16* __restrict__ xw, bf16* __restrict__ bt_n,
+                                                bf16* __restrict__ ct_n, bf16* __restrict__ xw_n,
+                                                float* __restrict__ dec, Frag<bf16>* mt, const float* dcol,
+                                                bf16* yg, const bf16* zg, f32x16 (&H)[PH][N / 32], float& kappa,
+                                                uint4 (&zv)[4 * PH], const DiagMask& dm, const LaneOffs& lo) {
+  constexpr int NT = N / 32, NW = lb_waves<HG, PH>;
+  constexpr int LOADS = 2 * (N / 8 / NW) + 4 * PH;
+  constexpr int ZL = 4 * PH;                               // gate loads per segment
+  const int l = c.l, half = l >> 5, l32 = l & 31, nseg = c.nseg;
+  const int pos = c.c0 + si * SEG;
+  // this segment's tiles (the next segment's may still fly before the loop, the gate loads of the previous
+  // segment afterwards: they are issued after the fetch)
+  if (si == 0 && nseg > 1) wait_vmem_n<LOADS>();
+  else wait_vmem_n<GATE ? ZL : 0>();
+  // y of the previous (full) segment, staged by this wave in the other stage: out before it is refilled
+  if (si > 0) {
+    uint4 yv[4 * PH];
+    load_y64<PH>(xw_n, yv);
+    if constexpr (GATE) gate_rows(yv, zv);
+    store_y64<PH>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, yv, SEG);
+  }
+  // this head's in-segment decay (lane = token)
+  const int dj = si % LB_DSEG;
+  const float cs = dec[2 * dj * SEG + l];
+  const float dtv = dec[(2 * dj + 1) * SEG + l];
+  lds_barrier();                                           // tiles in LDS; the other stage is free
+  if (si > 0 && si + 1 < nseg) lb_scan_fetch<N, HG, PH>(p, c, bt_n, ct_n, xw_n, si + 1);
+  if constexpr (GATE) load_z64<PH>(zg + (int64_t)pos * p.z_sl, p.z_sl, c.c1 - 1 - pos, zv);
+  const bool dnext = dj == LB_DSEG - 1 && si + 1 < nseg;  // the next decay block is due
+  if (dnext) lb_dt_fetch(p, c, dec, si + 1);
+  const float cse = readlane_f(cs, SEG - 1);
+  // ---- the segment's three masked C B^T tiles, tile ti by wave ti % NW
+  for (int ti = c.w; ti < 3; ti += NW) cb_tile<N>(ti, bt, ct, mt + 128 * ti, lo, l);
+  // ---- tokens [a, bnd) per pass: the scale factors e^{-kappa - cs_s} of a pass stay within
+  // e^LB_FACT_RANGE, so a segment whose decay range exceeds it takes several passes (a token's own decay,
+  // however large, is applied to the state at the start of its pass)
+  int a = 0;
+  for (int pass = 0;; ++pass) {
+    // the tile reads of a pass stay inside the pass loop (hoisted, the C and B fragments would hold their
+    // registers through it): the tile pointers are offset by an opaque zero
+    int z0 = 0;
+    asm volatile("" : "+s"(z0));
+    const bf16* btp = bt + z0;
+    const bf16* ctp = ct + z0;
+    bf16* xwp = xw + z0;
+    const float csa = readlane_f(cs, a);
+    const uint64_t over = __builtin_amdgcn_ballot_w64(l > a && cs < csa - LB_FACT_RANGE);
+    const int bnd = over ? (int)__builtin_ctzll(over) : SEG;
+    if (-(kappa + readlane_f(cs, bnd - 1)) > LB_FACT_RANGE) {
+      const float e = __expf(kappa + csa);               // renormalise: kappa <- -cs_a
+#pragma unroll
+      for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) H[ph][nt] *= e;
+      kappa = -csa;
+    }
+    float wb[2], rsb[2];
+    halves(l >= a && l < bnd ? __expf(-kappa - cs) * dtv : 0.f, wb);
+    halves(__expf(kappa + cs), rsb);
+    Frag<bf16> xa[PH][4];
+    scaled_x<PH>(xwp, wb, dm, lo, xa);
+    f32x16 Y[PH][2];
+#pragma unroll
+    for (int ph = 0; ph < PH; ++ph) Y[ph][0] = Y[ph][1] = zero16();
+    // read-out of the state entering the pass and the state update, fused per state tile
+    readout<N, PH>(H, Y, ctp, btp, xa, lo);
+    if (pass == 0) lds_barrier();                          // the masked tiles are in LDS
+#pragma unroll
+    for (int ph = 0; ph < PH; ++ph) {
+      Y[ph][0] = mma(xa[ph][0], mt[l], Y[ph][0]);
+      Y[ph][0] = mma(xa[ph][1], mt[64 + l], Y[ph][0]);
+      Y[ph][1] = mma(xa[ph][0], mt[128 + l], Y[ph][1]);
+      Y[ph][1] = mma(xa[ph][1], mt[192 + l], Y[ph][1]);
+      Y[ph][1] = mma(xa[ph][2], mt[256 + l], Y[ph][1]);
+      Y[ph][1] = mma(xa[ph][3], mt[320 + l], Y[ph][1]);
+    }
+    // ---- epilogue: y[t][p] = rs_t Y^T[p][t] + D_p x[t][p] for the pass's tokens, staged in place of x
+    // (lane = token t)
+#pragma unroll
+    for (int ph = 0; ph < PH; ++ph) {
+      bf16* xt = xwp + ph * Sub64::ELEMS;
+      bf16x4 xv[2][4];
+      f32x4 d4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        d4[q] = *reinterpret_cast<const f32x4*>(dcol + 32 * (c.ph0 + ph) + 8 * q + 4 * half);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+          xv[tt][q] = *reinterpret_cast<const bf16x4*>(xt + 32 * tt * Sub64::W + lo.piece[q]);
+      }
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int t = 32 * tt + l32;
+        if (t >= a && t < bnd) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            bf16x4 yo;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              yo[i] = (bf16)(rsb[tt] * Y[ph][tt][4 * q + i] + d4[q][i] * (float)xv[tt][q][i]);
+            *reinterpret_cast<bf16x4*>(xt + 32 * tt * Sub64::W + lo.piece[q]) = yo;
+          }
+        }
+      }
+    }
+    if (bnd >= SEG) break;
+    a = bnd;
+  }
+  kappa += cse;
+  if (dnext) {
+    wait_vmem();                                           // the next decay block's dt
+    lb_dt_form(p, c, dec, si + 1);
+  }
+}
+
+template <int N, int HG, int PH, bool GATE>
+__global__ __launch_bounds__(64 * HG * (2 / PH)) void ssd_lb_scan_kernel(SsdParams p) {
+  constexpr int NT = N / 32, NW = lb_waves<HG, PH>;
+  static_assert((N / 8) % NW == 0, "B and C tiles split evenly over the waves");
+  constexpr int LOADS = 2 * (N / 8 / NW) + 4 * PH;         // loads one wave issues per segment fetch
+  __shared__ LbScanSmem<N, HG, NW> sm;
+  int k, b, h;
+  const LbWave c = lb_wave<N, HG, PH>(p, k, b, h);
+  const int w = c.w, l = c.l, half = l >> 5, l32 = l & 31, nseg = c.nseg, hw = c.hw, ph0 = c.ph0;
+  bf16* yg = reinterpret_cast<bf16*>(p.y) + (int64_t)b * p.y_sb + (int64_t)h * p.y_sh + 32 * ph0;
+  const bf16* zg =
+      GATE ? reinterpret_cast<const bf16*>(p.z) + (int64_t)b * p.z_sb + (int64_t)h * p.z_sh + 32 * ph0 : nullptr;
+  float* dec = &sm.dec[w][0][0][0];
+  sm.dcol[hw][l] = p.D ? (p.D_per_channel ? p.D[h * HD + l] : p.D[h]) : 0.f;
+  const DiagMask dm = diag_mask(l);
+
+  // ---- entering state H_k (fp32 accumulators, rows n (state_row_perm order), columns p of each half)
+  f32x16 H[PH][NT];
+#pragma unroll
+  for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) H[ph][nt] = zero16();
+  const int64_t per = (int64_t)HD * N;
+  auto load_state = [&](const bf16* s, bf16x8 (&v)[PH][NT][2]) {
+#pragma unroll
+    for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          v[ph][nt][q] = reinterpret_cast<const bf16x8*>(s + frag_off(nt, ph0 + ph, l))[q];
+  };
+  if (p.entering) {
+    // entering states precomputed by ssd_state_pass_kernel (bf16, fragment order)
+    bf16x8 v[PH][NT][2];
+    load_state(reinterpret_cast<const bf16*>(p.entering) + (((int64_t)b * p.nchunks + k) * p.nheads + h) * per, v);
+    lb_dt_fetch(p, c, dec, 0);
+    lb_scan_fetch<N, HG, PH>(p, c, &sm.Bt[0][0][0], &sm.Ct[0][0][0], &sm.X[0][hw][ph0][0], 0);
+    add_state<N, PH, false>(H, v, 1.f, dm);
+  } else {
+    // look-back: lane i < k holds T_i; f_j = exp(T_{j+1} + .. + T_{k-1}) = exp(P_{k-1} - P_j), and the initial
+    // state enters with exp(P_{k-1}).  Three predecessor states are in flight at a time (indices past k - 1
+    // re-read state k - 1 and are not summed).
+    const float* T = p.chunk_decay + ((int64_t)b * p.nheads + h) * p.nchunks;
+    const bf16* sbase = reinterpret_cast<const bf16*>(p.chunk_states) + ((int64_t)b * p.nchunks * p.nheads + h) * per;
+    const int64_t cstride = (int64_t)p.nheads * per;       // elements between consecutive chunks
+    const float tl = l < k ? T[l] : 0.f;
+    bf16x8 v[3][PH][NT][2];
+    if (k > 0) {
+#pragma unroll
+      for (int u = 0; u < 3; ++u) load_state(sbase + min(u, k - 1) * cstride, v[u]);
+    }
+    lb_dt_fetch(p, c, dec, 0);
+    lb_scan_fetch<N, HG, PH>(p, c, &sm.Bt[0][0][0], &sm.Ct[0][0][0], &sm.X[0][hw][ph0][0], 0);
+    const float Pi = wave_incl_scan(tl);
+    const float Ptot = readlane_f(Pi, 63);
+    const float f = __expf(Ptot - Pi);
+    if (p.init_state) {
+      const float e0 = __expf(Ptot);
+#pragma unroll
+      for (int ph = 0; ph < PH; ++ph) {
+        const float* h0 = p.init_state + ((int64_t)b * p.nheads + h) * per + (int64_t)(32 * (ph0 + ph) + l32) * N;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 hv = *reinterpret_cast<const f32x4*>(h0 + 32 * nt + state_row_perm(8 * q + 4 * half));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) H[ph][nt][4 * q + i] = e0 * hv[i];
+          }
+      }
+    }
+    for (int j = 0; j < k; j += 3) {
+#pragma unroll
+      for (int u = 0; u < 3; ++u)
+        if (j + u < k) {
+          add_state<N, PH, true>(H, v[u], readlane_f(f, j + u), dm);
+          if (j + u + 3 < k) load_state(sbase + (j + u + 3) * cstride, v[u]);
+        }
+    }
+  }
+  wait_vmem_n<LOADS>();                                    // the first decay block (segment 0's tiles may fly)
+  lb_dt_form(p, c, dec, 0);
+  if (nseg > 1) lb_scan_fetch<N, HG, PH>(p, c, &sm.Bt[1][0][0], &sm.Ct[1][0][0], &sm.X[1][hw][ph0][0], 1);
+
+  const LaneOffs lo = lane_offs(l);
+  float kappa = 0.f;                                       // H_true = e^kappa H
+  uint4 zv[4 * PH];                                        // gate rows of the segment whose y is staged
+  for (int si = 0; si < nseg; ++si) {
+    const int cur = si & 1;
+    lb_scan_segment<N, HG, PH, GATE>(p, c, si, &sm.Bt[cur][0][0], &sm.Ct[cur][0][0], &sm.X[cur][hw][ph0][0],
+                                     &sm.Bt[cur ^ 1][0][0], &sm.Ct[cur ^ 1][0][0], &sm.X[cur ^ 1][hw][ph0][0],
+                                     dec, &sm.mt[0][0][0], sm.dcol[hw], yg, zg, H, kappa, zv, dm, lo);
+  }
+  // y of the last segment
+  {
+    const int si = nseg - 1;
+    const int pos = c.c0 + si * SEG;
+    uint4 yv[4 * PH];
+    load_y64<PH>(&sm.X[si & 1][hw][ph0][0], yv);
+    if constexpr (GATE) gate_rows(yv, zv);
+    store_y64<PH>(yg + (int64_t)pos * p.y_sl, p.y_sl, yv, c.c1 - pos);
+  }
+  // final state (last chunk): H_true = e^kappa H, canonical (b, H, P, N) fp32
+  if (p.final_state && k == p.nchunks - 1) {
+    const float e = __expf(kappa);
+#pragma unroll
+    for (int ph = 0; ph < PH; ++ph) {
+      float* fo = p.final_state + ((int64_t)b * p.nheads + h) * per + (int64_t)(32 * (ph0 + ph) + l32) * N;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          f32x4 v;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = e * H[ph][nt][4 * q + i];
+          *reinterpret_cast<f32x4*>(fo + 32 * nt + state_row_perm(8 * q + 4 * half)) = v;
+        }
+    }
+  }
+}
+
+constexpr int LB_PH = 1;   // halves per wave of the two-pass prefill (1: two waves per head)
+
+template <int N, int HG>
+hipError_t launch_lb_t(const SsdParams& p, hipStream_t stream) {
+  constexpr int NW = lb_waves<HG, LB_PH>;
+  dim3 grid((unsigned)(p.nchunks * p.batch * (p.nheads / HG)));
+  hipLaunchKernelGGL((ssd_lb_state_kernel<N, HG, LB_PH>), grid, dim3(64 * NW), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.entering) {
+    SsdParams q = p;
+    q.final_state = nullptr;                               // the scan writes the final state
+    q.state_perm = 1;                                      // the chunk states' rows are in state_row_perm order
+    e = launch_ssd_state_pass(q, stream);
+    if (e != hipSuccess) return e;
+  }
+  if (p.z) hipLaunchKernelGGL((ssd_lb_scan_kernel<N, HG, LB_PH, true>), grid, dim3(64 * NW), 0, stream, p);
+  else hipLaunchKernelGGL((ssd_lb_scan_kernel<N, HG, LB_PH, false>), grid, dim3(64 * NW), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int N>
+hipError_t launch_lb_n(const SsdParams& p, hipStream_t stream) {
+  switch (p.heads_per_wg) {
+    case 4: return launch_lb_t<N, 4>(p, stream);
+    case 2: return launch_lb_t<N, 2>(p, stream);
+    case 1: return launch_lb_t<N, 1>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool ssd_lb_supported(int dtype, int dstate) { return dtype == DT_BF16 && (dstate == 64 || dstate == 128); }
+
+hipError_t launch_ssd_lb(const SsdParams& p, hipStream_t stream) {
+  if (p.dstate == 128) return launch_lb_n<128>(p, stream);
+  if (p.dstate == 64) return launch_lb_n<64>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace mh

@@ -397,7 +397,7 @@ __global__ __launch_bounds__(256) void ssd_state_pass_kernel(SsdParams p) {
   const int per = HD * p.dstate;                  // state elements per (b, h)
   const int e8 = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (e8 >= per) return;
-  const int ci0 = canon_index(e8, p.dstate), ci1 = canon_index(e8 + 4, p.dstate);   // two runs of 4 canonical n
+  const int ci0 = canon_index(e8, p.dstate, p.state_perm), ci1 = canon_index(e8 + 4, p.dstate, p.state_perm);   // two runs of 4 canonical n
   f32x4 H[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) H[u][0] = H[u][1] = H[u][2] = H[u][3] = 0.f;
@@ -692,6 +692,8 @@ size_t ssd_frag_bytes(int dtype, int dstate) {
 
 // Workspace parts, each 256-byte aligned: chunk-local states (bf16 for bf16 I/O, fp32 otherwise), chunk
 // log-decays, per-segment shared fragments, bf16 entering states (bf16 I/O only).
+// The two-pass bf16 path (ssd_lookback.hip) needs no segment fragments, and bf16 entering states only when the
+// scan does not sum them itself (more than LB_MAX chunks).
 struct SsdWorkspace {
   size_t states, decay, frags, entering;
   size_t total() const { return align256(states) + align256(decay) + align256(frags) + align256(entering); }
@@ -700,11 +702,12 @@ static SsdWorkspace ssd_workspace(int batch, int seqlen, int nchunks, int nheads
                                   int ngroups, int dtype) {
   const size_t nstate = (size_t)batch * nchunks * nheads * headdim * dstate;
   const size_t nseg = (size_t)(seqlen + SEG - 1) / SEG;
+  const bool lb = ssd_lb_supported(dtype, dstate);
   SsdWorkspace w;
   w.states = nstate * (dtype == DT_BF16 ? sizeof(bf16) : sizeof(float));
   w.decay = (size_t)batch * nheads * nchunks * sizeof(float);
-  w.frags = (size_t)batch * ngroups * nseg * ssd_frag_bytes(dtype, dstate);
-  w.entering = dtype == DT_BF16 ? nstate * sizeof(bf16) : 0;
+  w.frags = lb ? 0 : (size_t)batch * ngroups * nseg * ssd_frag_bytes(dtype, dstate);
+  w.entering = (dtype == DT_BF16 && (!lb || nchunks > LB_MAX)) ? nstate * sizeof(bf16) : 0;
   return w;
 }
 
@@ -721,9 +724,9 @@ void ssd_workspace_layout(SsdParams& p, void* workspace) {
   c += align256(w.states);
   p.chunk_decay = reinterpret_cast<float*>(c);
   c += align256(w.decay);
-  p.seg_frags = c;
+  p.seg_frags = w.frags ? c : nullptr;
   c += align256(w.frags);
-  p.entering = c;
+  p.entering = w.entering ? c : nullptr;
 }
 
 template <typename T, typename TM, int N, int HG>
@@ -773,6 +776,14 @@ __global__ __launch_bounds__(256) void ssd_empty_kernel(const float* __restrict_
   if (i < n) fin[i] = h0 ? h0[i] : 0.f;
 }
 
+hipError_t launch_ssd_state_pass(const SsdParams& p, hipStream_t st) {
+  const int per8 = HD * p.dstate / 8;
+  dim3 g2((unsigned)((per8 + 255) / 256), (unsigned)(p.batch * p.nheads));
+  if (p.dtype == DT_BF16) hipLaunchKernelGGL((ssd_state_pass_kernel<bf16>), g2, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((ssd_state_pass_kernel<float>), g2, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
 hipError_t launch_ssd(const SsdParams& p, hipStream_t st) {
   if (p.nchunks == 0) {
     if (!p.final_state) return hipSuccess;
@@ -781,6 +792,7 @@ hipError_t launch_ssd(const SsdParams& p, hipStream_t st) {
                        p.final_state, n);
     return hipGetLastError();
   }
+  if (ssd_lb_supported(p.dtype, p.dstate)) return launch_ssd_lb(p, st);
   if (p.dtype == DT_BF16) {
     if (p.dstate == 128) return launch_ssd_n<bf16, bf16, 128>(p, st);
     if (p.dstate == 64) return launch_ssd_n<bf16, bf16, 64>(p, st);

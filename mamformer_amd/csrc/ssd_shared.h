@@ -8,6 +8,9 @@
 namespace mh {
 
 constexpr int HD = 64;               // headdim handled by the SSD kernels
+// Two-pass prefill: most chunks whose entering states the scan sums itself from the chunk states (more
+// chunks get them from ssd_state_pass_kernel).
+constexpr int LB_MAX = 8;
 
 __host__ __device__ __forceinline__ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
@@ -32,11 +35,21 @@ __device__ __forceinline__ float seg_decay(const SsdParams& p, float dtraw, floa
 // 16 consecutive values per lane.  Offset (elements) of tile (nt, pt)'s block of lane l:
 __device__ __forceinline__ int frag_off(int nt, int pt, int l) { return ((nt * 2 + pt) * 64 + l) * 16; }
 
-// Workspace element e (fragment-native order) <-> canonical state index p * N + n.
-__device__ __forceinline__ int canon_index(int e, int N) {
+// Row permutation of the two-pass prefill's states: within each 16-row group, 4-row blocks 1 and 2 are
+// swapped, so that accumulator row 16 c + KSET(half, j) holds state n = 16 c + 8 half + j (the state rows a
+// KSET-ordered read-out fragment meets in natural column order).
+__host__ __device__ __forceinline__ int state_row_perm(int r) {
+  const int m = (r >> 2) & 3;
+  return (r & ~12) | ((((m & 1) << 1) | (m >> 1)) << 2);
+}
+
+// Workspace element e (fragment-native order) <-> canonical state index p * N + n (perm: rows permuted by
+// state_row_perm, the two-pass prefill's order).
+__device__ __forceinline__ int canon_index(int e, int N, bool perm = false) {
   const int r = e & 15, lane = (e >> 4) & 63, tile = e >> 10;
   const int pt = tile & 1, nt = tile >> 1;
-  return (32 * pt + (lane & 31)) * N + 32 * nt + acc_row(lane >> 5, r);
+  const int row = acc_row(lane >> 5, r);
+  return (32 * pt + (lane & 31)) * N + 32 * nt + (perm ? state_row_perm(row) : row);
 }
 
 }  // namespace mh

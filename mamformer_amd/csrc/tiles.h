@@ -59,6 +59,20 @@ struct XHalf {
   __device__ static __forceinline__ int chunk(int r, int c) { return r * W + (c ^ swz(r)) * EPC; }
 };
 
+// 64-token tile of 32 16-bit columns (64-byte rows) whose 16-byte chunks are XOR-swizzled by (row >> 2) & 3;
+// wider tiles are stored as consecutive such sub-tiles, one per 32-column slice.  With this layout the
+// transposed reads (ds_read_b64_tr_b16: 8 rows x 64 bytes), row fragments (16 bytes of 32 rows) and
+// 8-byte row accesses of 32 rows all spread over the LDS banks without conflicts beyond their minimum, and a
+// lane's offset within a sub-tile depends only on its lane bits for every access pattern the kernels use.
+struct Sub64 {
+  static constexpr int W = 32;
+  static constexpr int ELEMS = SEG * W;             // elements per sub-tile (4 KB of bf16)
+  // element offset of (row r, column col) for col % 4 == 0, col < 32
+  __host__ __device__ static constexpr int off(int r, int col) {
+    return r * W + ((((col >> 3) ^ (r >> 2)) & 3) << 3) + (col & 7);
+  }
+};
+
 // Direct global -> LDS load of `bytes` (16 or 4) per lane from a wave-uniform base plus a 32-bit lane
 // offset (scalar-base addressing: no 64-bit per-lane address arithmetic).  Token strides are validated on
 // the host so that a segment's span (SEG rows) stays below 2 GiB.
@@ -88,6 +102,24 @@ __device__ __forceinline__ void fetch_tile(T* dst, const T* src, int64_t row_str
     const int c = phys ^ (r & TL::MASK);
     const uint32_t off = (uint32_t)(min(r, rmax) * (int)row_stride + c * TL::EPC) * (uint32_t)sizeof(T);
     dma_lds<16>(base, off, dst + blk * (1024 / (int)sizeof(T)));
+  }
+}
+
+// Direct fetch of 1 KB blocks [blk0, blk0 + nblk) of a Sub64-tiled bf16 tile of W columns (W / 32 sub-tiles of
+// 4 blocks each): lane i of a block writes LDS bytes [16 i, 16 i + 16), i.e. row 16 (blk % 4) + i / 4 of
+// sub-tile blk / 4 at physical chunk i % 4, so it fetches the logical chunk the swizzle places there.  Rows past
+// `last_tok` re-read the last valid row.  The lane offsets are recomputed per call (lane_id_here).
+__device__ __forceinline__ void fetch_sub64(bf16* dst, const bf16* src, int64_t row_stride, int tok0, int last_tok,
+                                            int blk0, int nblk) {
+  const bf16* base = src + (int64_t)tok0 * row_stride;   // wave-uniform
+  const int rmax = last_tok - tok0;
+  const int lane = lane_id_here();
+  for (int q = 0; q < nblk; ++q) {
+    const int blk = blk0 + q;
+    const int r = 16 * (blk & 3) + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    const uint32_t off = (uint32_t)(min(r, rmax) * (int)row_stride + 32 * (blk >> 2) + 8 * c) * 2u;
+    dma_lds<16>(base, off, dst + blk * 512);
   }
 }
 

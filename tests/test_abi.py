@@ -57,7 +57,8 @@ def test_ssd_workspace_and_chunk_len():
     cl = ct.c_int64()
     assert _rc("mh_ssd_chunk_len", ct.byref(a), ct.byref(cl)) == 0
     nch = -(-300 // cl.value)
-    assert n.value >= 2 * nch * 8 * 64 * 128 * 4 + 2 * 8 * nch * 4
+    # at least the bf16 chunk states (b, nchunks, H, P, N) and the fp32 chunk log-decays (b, H, nchunks)
+    assert n.value >= 2 * nch * 8 * 64 * 128 * 2 + 2 * 8 * nch * 4
     a.chunk_len = 128
     assert _rc("mh_ssd_chunk_len", ct.byref(a), ct.byref(cl)) == 0 and cl.value == 128
 

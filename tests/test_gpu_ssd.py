@@ -126,6 +126,32 @@ def test_ssd_extreme_decay_cuts_segments():
     check("final", fin, f_ref, 1e-4)
 
 
+@pytest.mark.parametrize("N,chunk,init", [(128, 256, False), (64, 128, True), (128, 64, True), (128, 1024, True)])
+def test_ssd_extreme_decay_bf16_multipass(N, chunk, init):
+    """bf16 I/O with per-step log-decays from about -0.01 to below -100 per head: a 64-token segment whose decay
+    range exceeds the factorisation bound is scanned in several token ranges, the state renormalised at each
+    range start.  Several chunks (look-back over predecessor states, or entering states past the look-back
+    limit at chunk 64), a chunk of 11 segments (several decay blocks), a partial last segment and an optional
+    initial state."""
+    g = torch.Generator().manual_seed(N + chunk)
+    b, L, H, P = 2, 650, 8, 64
+    x = torch.randn(b, L, H, P, generator=g).to(torch.bfloat16)
+    B = torch.randn(b, L, 1, N, generator=g).to(torch.bfloat16)
+    C = torch.randn(b, L, 1, N, generator=g).to(torch.bfloat16)
+    dt = torch.exp(torch.randn(b, L, H, generator=g) * 2.0)          # 0.02 .. 50
+    A = torch.tensor([-16.0, -2.0, -0.5, -0.01, -4.0, -1.0, -0.1, -8.0])
+    h0 = torch.randn(b, H, P, N, generator=g) if init else None
+    say(f"extreme decay bf16 N={N} chunk={chunk} init={init}")
+    y, fin = mh.selective_scan(dev(x, torch.bfloat16), dev(dt), dev(A), dev(B, torch.bfloat16),
+                               dev(C, torch.bfloat16), None, return_final_state=True, chunk_size=chunk,
+                               initial_state=dev(h0))
+    y_ref, f_ref = ref.ssd_direct(x.double().numpy(), dt.double().numpy(), A.double().numpy(),
+                                  B.double().numpy(), C.double().numpy(),
+                                  initial_state=None if h0 is None else h0.double().numpy())
+    check("y", y, y_ref, 1e-2)
+    check("final", fin, f_ref, 1e-2)
+
+
 @pytest.mark.parametrize("dtype,L,H,N,chunk", [(torch.bfloat16, 1000, 8, 128, 256), (torch.float32, 333, 4, 64, None),
                                                (torch.float32, 200, 2, 128, 64)])
 def test_ssd_output_gate_vs_oracle(dtype, L, H, N, chunk):
