@@ -7,10 +7,11 @@ with inputs resident in HBM.  A step is one ``selective_scan`` pass over one
 batch; three input/output buffer sets rotate so the 256 MB MALL cannot serve
 a step from the previous one.  The same JSON line carries:
 
-* ``roofline`` -- one launch of the prefill op (``mh_ssd_chunk_scan_fwd``:
-  seg_frags + chunk_state + state_pass + chunk_scan dispatches): algorithmic bytes per
-  launch (compulsory I/O only) / average launch duration from HIP events on
-  the launch stream, against 8 TB/s (the op is HBM-bound by intensity).
+* ``roofline`` -- one launch of the prefill op (``mh_ssd_chunk_scan_fwd``: the
+  ``ssd_lb_state_kernel`` (chunk states) and ``ssd_lb_scan_kernel`` (look-back +
+  scan) dispatches): algorithmic bytes per launch (compulsory I/O only) / average
+  launch duration from HIP events on the launch stream, against 8 TB/s (the op is
+  HBM-bound by intensity).
 * ``cpu_baseline`` -- the reference's pure-PyTorch CPU prefill
   (``oracle/baseline.py``, mamba2.py:84-126 structure) timed on the host cores
   on a bounded token sample of the same workload.
@@ -441,12 +442,17 @@ def main():
         out["value"] = round(head["mtok_s"], 3)
         out["ms_per_step"] = round(wall, 5)
         out["config"]["chunk_len"] = head["chunk_len"]
+        out["config"]["chunk_len_note"] = (
+            "state-passing chunk of the kernels, chosen by mh_ssd_chunk_len: 512 gives one 8-wave workgroup per CU "
+            "(2 x 8 chunks x 16 head blocks = 256); chunk 256 doubles the chunk-state traffic and the look-back "
+            "length and measured slower. The workload's chunk 256 is the chunk of the reference's Triton kernels; "
+            "the outputs do not depend on the chunk length")
         tr = measured_traffic()
         out["roofline"] = {
             "bound": "hbm", "achieved": round(head["hbm_GBs"], 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "frac": round(head["hbm_GBs"] / (PEAK_HBM / 1e9), 4),
             "traffic": None if tr is None else tr["bytes_per_launch"],
-            "kernel": "mh_ssd_chunk_scan_fwd (ssd_seg_frags + ssd_chunk_state + ssd_state_pass + ssd_chunk_scan)",
+            "kernel": "mh_ssd_chunk_scan_fwd (ssd_lb_state_kernel + ssd_lb_scan_kernel)",
             "alg_bytes_per_launch": head["alg_bytes"], "alg_flops_per_launch": head["alg_flops"],
             "launch_us": round(head["us_per_step"], 2),
             "mfma_frac": round(head["alg_flops"] / (head["us_per_step"] * 1e-6) / PEAK_BF16, 4),

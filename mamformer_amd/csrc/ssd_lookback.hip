@@ -258,6 +258,7 @@ struct LbWave {
   int w, l, hw, ph0, c0, c1, last, nseg;
   float Ah, dtb;
   const bf16* xg;     // x of the wave's head, token 0, column 0
+  const bf16* xg0;    // x of the workgroup's first head, token 0, column 0
   const bf16* Bg;     // B of the head's group, token 0
   const bf16* Cg;     // C of the head's group, token 0
   const float* dtg;   // dt of the wave's head, token 0
@@ -282,6 +283,7 @@ __device__ __forceinline__ LbWave lb_wave(const SsdParams& p, int& k, int& b, in
   c.Ah = p.A[h];
   c.dtb = p.dt_bias ? p.dt_bias[h] : 0.f;
   c.xg = reinterpret_cast<const bf16*>(p.x) + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh;
+  c.xg0 = c.xg - (int64_t)c.hw * p.x_sh;
   c.Bg = reinterpret_cast<const bf16*>(p.B) + (int64_t)b * p.B_sb + (int64_t)g * N;
   c.Cg = reinterpret_cast<const bf16*>(p.C) + (int64_t)b * p.C_sb + (int64_t)g * N;
   c.dtg = p.dt + (int64_t)b * p.dt_sb + h;
@@ -392,18 +394,24 @@ __global__ __launch_bounds__(64 * HG * (2 / PH)) void ssd_lb_state_kernel(SsdPar
 
 constexpr int LB_DSEG = 4;   // segments per decay block: their in-segment decays are formed together
 
-// Two stages of segment tiles.  ds_read / ds_write take a 16-bit byte immediate: the B and C tiles of both
-// stages lie in the first 64 KB and the x tiles of both stages in one 64 KB window, so each lane access
-// pattern needs one address register for every stage and tile.
+// One stage of segment tiles, at most 64 KB: every access is one base register plus a 16-bit immediate.
+template <int N, int HG>
+struct LbScanStage {
+  bf16 Bt[N / 32][Sub64::ELEMS];      // B tile
+  bf16 Ct[N / 32][Sub64::ELEMS];      // C tile
+  bf16 X[HG][2][Sub64::ELEMS];        // per head: its x tile (two halves)
+};
 template <int N, int HG, int NW>
 struct LbScanSmem {
-  bf16 Bt[2][N / 32][Sub64::ELEMS];   // B tile per stage
-  bf16 Ct[2][N / 32][Sub64::ELEMS];   // C tile per stage
+  LbScanStage<N, HG> st[2];
   Frag<bf16> mt[3][2][64];            // masked (C B^T)^T tiles (s0,t0), (s0,t1), (s1,t1) as B-operand fragments
   float dec[NW][LB_DSEG][2][SEG];     // per wave: [0] cs_t, [1] dt_t of its head, segments of the decay block
   float dcol[HG][HD];                 // D per column of each head
-  bf16 X[2][HG][2][Sub64::ELEMS];     // per stage and head: its x tile (two halves); y staged in place
 };
+// Waves that fetch the segment tiles (the last lb_fetch_waves of the workgroup; the first three compute the
+// masked C B^T tiles meanwhile when there are enough waves).
+template <int NW>
+constexpr int lb_fetch_waves = NW >= 4 ? NW / 2 : NW;
 
 // Masked (C B^T)^T tile ti of the segment: acc[s][t] = C_t . B_s for s <= t, as two B-operand fragments.
 template <int N>
@@ -425,54 +433,19 @@ __device__ __forceinline__ void cb_tile(int ti, const bf16* btile, const bf16* c
   out[64 + l] = acc_to_frag<bf16>(acc, 1);
 }
 
-// y rows staged in the wave's PH Sub64 halves (x + ph ELEMS): the 16-byte chunks of rows e / 4
-// (e = lane + 64 i), column 8 (e % 4) of half ph, as v[4 ph + i].
+// Gate values z in the epilogue's lane layout: z[ph][tt][q] = the 4 values of row 32 tt + lane % 32, columns
+// 32 ph + 8 q + 4 (lane / 32) .. + 3 (src at the segment's first row and the wave's first column; rows past rmax
+// re-read row rmax).
 template <int PH>
-__device__ __forceinline__ void load_y64(const bf16* x, uint4 (&v)[4 * PH]) {
-  const int lane = lane_id_here();
+__device__ __forceinline__ void load_z_pieces(const bf16* src, int64_t row_stride, int rmax, bf16x4 (&z)[PH][2][4]) {
+  const int lane = lane_id_here(), half = lane >> 5, l32 = lane & 31;
 #pragma unroll
-  for (int ph = 0; ph < PH; ++ph)
+  for (int tt = 0; tt < 2; ++tt) {
+    const bf16* row = src + (int64_t)min(32 * tt + l32, rmax) * row_stride + 4 * half;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane + 64 * i;
-      v[4 * ph + i] = *reinterpret_cast<const uint4*>(x + ph * Sub64::ELEMS + Sub64::off(e >> 2, 8 * (e & 3)));
-    }
-}
-// Rows [0, len) of the staged chunks to HBM (dst at the column of the wave's first half).
-template <int PH>
-__device__ __forceinline__ void store_y64(bf16* dst, int64_t row_stride, const uint4 (&v)[4 * PH], int len) {
-  const int lane = lane_id_here();
+    for (int ph = 0; ph < PH; ++ph)
 #pragma unroll
-  for (int ph = 0; ph < PH; ++ph)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane + 64 * i;
-      if ((e >> 2) < len)
-        *reinterpret_cast<uint4*>(dst + (int64_t)(e >> 2) * row_stride + 32 * ph + 8 * (e & 3)) = v[4 * ph + i];
-    }
-}
-// Gate rows z of the wave's halves in the lane order of load_y64 (rows past rmax re-read row rmax).
-template <int PH>
-__device__ __forceinline__ void load_z64(const bf16* src, int64_t row_stride, int rmax, uint4 (&v)[4 * PH]) {
-  const int lane = lane_id_here();
-#pragma unroll
-  for (int ph = 0; ph < PH; ++ph)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane + 64 * i;
-      v[4 * ph + i] =
-          *reinterpret_cast<const uint4*>(src + (int64_t)min(e >> 2, rmax) * row_stride + 32 * ph + 8 * (e & 3));
-    }
-}
-template <int M>
-__device__ __forceinline__ void gate_rows(uint4 (&v)[M], const uint4 (&z)[M]) {
-#pragma unroll
-  for (int i = 0; i < M; ++i) {
-    bf16x8 y = __builtin_bit_cast(bf16x8, v[i]);
-    const bf16x8 g = __builtin_bit_cast(bf16x8, z[i]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = (bf16)((float)y[j] * silu_f((float)g[j]));
-    v[i] = __builtin_bit_cast(uint4, y);
+      for (int q = 0; q < 4; ++q) z[ph][tt][q] = *reinterpret_cast<const bf16x4*>(row + 32 * ph + 8 * q);
   }
 }
 
@@ -499,16 +472,31 @@ __device__ __forceinline__ void add_state(f32x16 (&H)[PH][N / 32], const bf16x8 
       }
 }
 
-// Segment tiles of pass 2 into one stage (bt, ct: the tiles; xw: the wave's first x half): every wave issues
-// exactly 2 N / 8 / NW + 4 PH loads.
-template <int N, int HG, int PH>
-__device__ __forceinline__ void lb_scan_fetch(const SsdParams& p, const LbWave& c, bf16* __restrict__ bt,
-                                              bf16* __restrict__ ct, bf16* __restrict__ xw, int si) {
-  constexpr int BB = N / 8 / lb_waves<HG, PH>;
+// Segment tiles of pass 2 into one stage, by the fetching waves: each issues exactly lb_fetch_loads loads
+// (its share of the B and C tiles and XB of the HG x 8 blocks of the heads' x tiles); the other waves none.
+template <int N, int HG, int NW>
+struct LbFetch {
+  static constexpr int ND = lb_fetch_waves<NW>;
+  static constexpr int BB = N / 8 / ND;                    // B (and C) blocks per fetching wave
+  static constexpr int XB = HG * 8 / ND;                   // x blocks per fetching wave
+  static constexpr int LOADS = 2 * BB + XB;
+  static_assert((N / 8) % ND == 0 && (HG * 8) % ND == 0 && (XB % 8 == 0 || 8 % XB == 0), "fetch split");
+};
+template <int N, int HG, int NW>
+__device__ __forceinline__ void lb_scan_fetch(const SsdParams& p, const LbWave& c, LbScanStage<N, HG>* __restrict__ s,
+                                              int si) {
+  using F = LbFetch<N, HG, NW>;
+  const int d = c.w - (NW - F::ND);
+  if (d < 0) return;
   const int pos = c.c0 + si * SEG;
-  fetch_sub64(bt, c.Bg, p.B_sl, pos, c.last, c.w * BB, BB);
-  fetch_sub64(ct, c.Cg, p.C_sl, pos, c.last, c.w * BB, BB);
-  fetch_sub64(xw - 4 * c.ph0 * 512, c.xg, p.x_sl, pos, c.last, 4 * c.ph0, 4 * PH);
+  fetch_sub64(&s->Bt[0][0], c.Bg, p.B_sl, pos, c.last, d * F::BB, F::BB);
+  fetch_sub64(&s->Ct[0][0], c.Cg, p.C_sl, pos, c.last, d * F::BB, F::BB);
+  constexpr int XS = F::XB < 8 ? F::XB : 8;                // blocks per head piece
+#pragma unroll
+  for (int q = 0; q < F::XB; q += XS) {
+    const int gb = d * F::XB + q, hd = gb / 8;
+    fetch_sub64(&s->X[hd][0][0], c.xg0 + (int64_t)hd * p.x_sh, p.x_sl, pos, c.last, gb % 8, XS);
+  }
 }
 // Raw dt of the LB_DSEG segments from s0 into the dt slots of the wave's decay block (LB_DSEG loads; tokens
 // past the sequence re-read its last one), and their forming in place into cs and dt (tokens past the chunk
@@ -529,41 +517,37 @@ __device__ __forceinline__ void lb_dt_form(const SsdParams& p, const LbWave& c, 
   }
 }
 
-// Segment si of pass 2, its tiles in the stage (bt, ct, xw: the wave's first x half); the other stage (bt_n,
-// ct_n, xw_n) holds the staged y of segment si - 1 and receives segment si + 1.  All LDS pointers a global ->
-// LDS load may write are __restrict__ parameters: the compiler otherwise makes every LDS read wait for all
-// outstanding global -> LDS loads (it cannot tell that they write the other stage).
+// Segment si of pass 2, its tiles in stage `cur`; stage `nxt` receives segment si + 1.  The stage (and decay block) pointers are __restrict__: the compiler otherwise makes
+// every LDS read wait for all outstanding global -> LDS loads (it cannot tell that they write the other stage).
 template <int N, int HG, int PH, bool GATE>
 __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave& c, int si,
-                                                const bf16* __restrict__ bt, const bf16* __restrict__ ct,
-                                                bf16* __restrict__ xw, bf16* __restrict__ bt_n,
-                                                bf16* __restrict__ ct_n, bf16* __restrict__ xw_n,
-                                                float* __restrict__ dec, Frag<bf16>* mt, const float* dcol,
-                                                bf16* yg, const bf16* zg, f32x16 (&H)[PH][N / 32], float& kappa,
-                                                uint4 (&zv)[4 * PH], const DiagMask& dm, const LaneOffs& lo) {
+                                                LbScanStage<N, HG>* __restrict__ cur,
+                                                LbScanStage<N, HG>* __restrict__ nxt, float* __restrict__ dec,
+                                                Frag<bf16>* mt, const float* dcol, bf16* yg, const bf16* zg,
+                                                f32x16 (&H)[PH][N / 32], float& kappa, const DiagMask& dm,
+                                                const LaneOffs& lo) {
   constexpr int NT = N / 32, NW = lb_waves<HG, PH>;
-  constexpr int LOADS = 2 * (N / 8 / NW) + 4 * PH;
-  constexpr int ZL = 4 * PH;                               // gate loads per segment
+  constexpr int LOADS = LbFetch<N, HG, NW>::LOADS;
+  const bf16* bt = &cur->Bt[0][0];
+  const bf16* ct = &cur->Ct[0][0];
+  const bf16* xw = &cur->X[c.hw][c.ph0][0];
   const int l = c.l, half = l >> 5, l32 = l & 31, nseg = c.nseg;
   const int pos = c.c0 + si * SEG;
-  // this segment's tiles (the next segment's may still fly before the loop, the gate loads of the previous
-  // segment afterwards: they are issued after the fetch)
-  if (si == 0 && nseg > 1) wait_vmem_n<LOADS>();
-  else wait_vmem_n<GATE ? ZL : 0>();
-  // y of the previous (full) segment, staged by this wave in the other stage: out before it is refilled
-  if (si > 0) {
-    uint4 yv[4 * PH];
-    load_y64<PH>(xw_n, yv);
-    if constexpr (GATE) gate_rows(yv, zv);
-    store_y64<PH>(yg + (int64_t)(pos - SEG) * p.y_sl, p.y_sl, yv, SEG);
+  // this segment's tiles: segment 0's here (segment 1's may still fly); a later segment's were waited for
+  // before the previous segment's y stores (loads and stores share vmcnt, so a counted wait past stores
+  // is not exact)
+  if (si == 0) {
+    if (nseg > 1) wait_vmem_n<LOADS>();
+    else wait_vmem();
   }
   // this head's in-segment decay (lane = token)
   const int dj = si % LB_DSEG;
   const float cs = dec[2 * dj * SEG + l];
   const float dtv = dec[(2 * dj + 1) * SEG + l];
   lds_barrier();                                           // tiles in LDS; the other stage is free
-  if (si > 0 && si + 1 < nseg) lb_scan_fetch<N, HG, PH>(p, c, bt_n, ct_n, xw_n, si + 1);
-  if constexpr (GATE) load_z64<PH>(zg + (int64_t)pos * p.z_sl, p.z_sl, c.c1 - 1 - pos, zv);
+  if (si > 0 && si + 1 < nseg) lb_scan_fetch<N, HG, NW>(p, c, nxt, si + 1);
+  bf16x4 zq[PH][2][4];
+  if constexpr (GATE) load_z_pieces<PH>(zg + (int64_t)pos * p.z_sl, p.z_sl, c.c1 - 1 - pos, zq);
   const bool dnext = dj == LB_DSEG - 1 && si + 1 < nseg;  // the next decay block is due
   if (dnext) lb_dt_fetch(p, c, dec, si + 1);
   const float cse = readlane_f(cs, SEG - 1);
@@ -580,7 +564,7 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
     asm volatile("" : "+s"(z0));
     const bf16* btp = bt + z0;
     const bf16* ctp = ct + z0;
-    bf16* xwp = xw + z0;
+    const bf16* xwp = xw + z0;
     const float csa = readlane_f(cs, a);
     const uint64_t over = __builtin_amdgcn_ballot_w64(l > a && cs < csa - LB_FACT_RANGE);
     const int bnd = over ? (int)__builtin_ctzll(over) : SEG;
@@ -612,11 +596,13 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
       Y[ph][1] = mma(xa[ph][2], mt[256 + l], Y[ph][1]);
       Y[ph][1] = mma(xa[ph][3], mt[320 + l], Y[ph][1]);
     }
-    // ---- epilogue: y[t][p] = rs_t Y^T[p][t] + D_p x[t][p] for the pass's tokens, staged in place of x
-    // (lane = token t)
+    // ---- epilogue: y[t][p] = rs_t Y^T[p][t] + D_p x[t][p] (times silu(z[t][p]) with the gate) for the pass's
+    // tokens, stored from the accumulator layout (lane = token t, 8-byte pieces of 4 columns).  Before the
+    // first stores: every load of this wave is complete, in particular the next segment's tiles.
+    if (pass == 0) wait_vmem();
 #pragma unroll
     for (int ph = 0; ph < PH; ++ph) {
-      bf16* xt = xwp + ph * Sub64::ELEMS;
+      const bf16* xt = xwp + ph * Sub64::ELEMS;
       bf16x4 xv[2][4];
       f32x4 d4[4];
 #pragma unroll
@@ -629,14 +615,18 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int t = 32 * tt + l32;
-        if (t >= a && t < bnd) {
+        if (t >= a && t < bnd && pos + t < c.c1) {
+          bf16* yrow = yg + (int64_t)(pos + t) * p.y_sl + 32 * ph + 4 * half;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             bf16x4 yo;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              yo[i] = (bf16)(rsb[tt] * Y[ph][tt][4 * q + i] + d4[q][i] * (float)xv[tt][q][i]);
-            *reinterpret_cast<bf16x4*>(xt + 32 * tt * Sub64::W + lo.piece[q]) = yo;
+            for (int i = 0; i < 4; ++i) {
+              float yv = rsb[tt] * Y[ph][tt][4 * q + i] + d4[q][i] * (float)xv[tt][q][i];
+              if constexpr (GATE) yv *= silu_f((float)zq[ph][tt][q][i]);
+              yo[i] = (bf16)yv;
+            }
+            *reinterpret_cast<bf16x4*>(yrow + 8 * q) = yo;
           }
         }
       }
@@ -645,17 +635,15 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
     a = bnd;
   }
   kappa += cse;
-  if (dnext) {
-    wait_vmem();                                           // the next decay block's dt
-    lb_dt_form(p, c, dec, si + 1);
-  }
+  if (dnext) lb_dt_form(p, c, dec, si + 1);                // its dt was waited for before the y stores
 }
 
 template <int N, int HG, int PH, bool GATE>
 __global__ __launch_bounds__(64 * HG * (2 / PH)) void ssd_lb_scan_kernel(SsdParams p) {
   constexpr int NT = N / 32, NW = lb_waves<HG, PH>;
   static_assert((N / 8) % NW == 0, "B and C tiles split evenly over the waves");
-  constexpr int LOADS = 2 * (N / 8 / NW) + 4 * PH;         // loads one wave issues per segment fetch
+  constexpr int LOADS = LbFetch<N, HG, NW>::LOADS;         // loads a fetching wave issues per segment
+  constexpr int LB_SLOTS = PH == 1 ? 4 : 3;                // predecessor states in flight in the look-back
   __shared__ LbScanSmem<N, HG, NW> sm;
   int k, b, h;
   const LbWave c = lb_wave<N, HG, PH>(p, k, b, h);
@@ -688,23 +676,23 @@ __global__ __launch_bounds__(64 * HG * (2 / PH)) void ssd_lb_scan_kernel(SsdPara
     bf16x8 v[PH][NT][2];
     load_state(reinterpret_cast<const bf16*>(p.entering) + (((int64_t)b * p.nchunks + k) * p.nheads + h) * per, v);
     lb_dt_fetch(p, c, dec, 0);
-    lb_scan_fetch<N, HG, PH>(p, c, &sm.Bt[0][0][0], &sm.Ct[0][0][0], &sm.X[0][hw][ph0][0], 0);
+    lb_scan_fetch<N, HG, NW>(p, c, &sm.st[0], 0);
     add_state<N, PH, false>(H, v, 1.f, dm);
   } else {
     // look-back: lane i < k holds T_i; f_j = exp(T_{j+1} + .. + T_{k-1}) = exp(P_{k-1} - P_j), and the initial
-    // state enters with exp(P_{k-1}).  Three predecessor states are in flight at a time (indices past k - 1
-    // re-read state k - 1 and are not summed).
+    // state enters with exp(P_{k-1}).  LB_SLOTS predecessor states are in flight at a time (indices past
+    // k - 1 re-read state k - 1 and are not summed).
     const float* T = p.chunk_decay + ((int64_t)b * p.nheads + h) * p.nchunks;
     const bf16* sbase = reinterpret_cast<const bf16*>(p.chunk_states) + ((int64_t)b * p.nchunks * p.nheads + h) * per;
     const int64_t cstride = (int64_t)p.nheads * per;       // elements between consecutive chunks
     const float tl = l < k ? T[l] : 0.f;
-    bf16x8 v[3][PH][NT][2];
+    bf16x8 v[LB_SLOTS][PH][NT][2];
     if (k > 0) {
 #pragma unroll
-      for (int u = 0; u < 3; ++u) load_state(sbase + min(u, k - 1) * cstride, v[u]);
+      for (int u = 0; u < LB_SLOTS; ++u) load_state(sbase + min(u, k - 1) * cstride, v[u]);
     }
     lb_dt_fetch(p, c, dec, 0);
-    lb_scan_fetch<N, HG, PH>(p, c, &sm.Bt[0][0][0], &sm.Ct[0][0][0], &sm.X[0][hw][ph0][0], 0);
+    lb_scan_fetch<N, HG, NW>(p, c, &sm.st[0], 0);
     const float Pi = wave_incl_scan(tl);
     const float Ptot = readlane_f(Pi, 63);
     const float f = __expf(Ptot - Pi);
@@ -723,36 +711,25 @@ __global__ __launch_bounds__(64 * HG * (2 / PH)) void ssd_lb_scan_kernel(SsdPara
           }
       }
     }
-    for (int j = 0; j < k; j += 3) {
+    for (int j = 0; j < k; j += LB_SLOTS) {
 #pragma unroll
-      for (int u = 0; u < 3; ++u)
+      for (int u = 0; u < LB_SLOTS; ++u)
         if (j + u < k) {
           add_state<N, PH, true>(H, v[u], readlane_f(f, j + u), dm);
-          if (j + u + 3 < k) load_state(sbase + (j + u + 3) * cstride, v[u]);
+          if (j + u + LB_SLOTS < k) load_state(sbase + (j + u + LB_SLOTS) * cstride, v[u]);
         }
     }
   }
   wait_vmem_n<LOADS>();                                    // the first decay block (segment 0's tiles may fly)
   lb_dt_form(p, c, dec, 0);
-  if (nseg > 1) lb_scan_fetch<N, HG, PH>(p, c, &sm.Bt[1][0][0], &sm.Ct[1][0][0], &sm.X[1][hw][ph0][0], 1);
+  if (nseg > 1) lb_scan_fetch<N, HG, NW>(p, c, &sm.st[1], 1);
 
   const LaneOffs lo = lane_offs(l);
   float kappa = 0.f;                                       // H_true = e^kappa H
-  uint4 zv[4 * PH];                                        // gate rows of the segment whose y is staged
   for (int si = 0; si < nseg; ++si) {
     const int cur = si & 1;
-    lb_scan_segment<N, HG, PH, GATE>(p, c, si, &sm.Bt[cur][0][0], &sm.Ct[cur][0][0], &sm.X[cur][hw][ph0][0],
-                                     &sm.Bt[cur ^ 1][0][0], &sm.Ct[cur ^ 1][0][0], &sm.X[cur ^ 1][hw][ph0][0],
-                                     dec, &sm.mt[0][0][0], sm.dcol[hw], yg, zg, H, kappa, zv, dm, lo);
-  }
-  // y of the last segment
-  {
-    const int si = nseg - 1;
-    const int pos = c.c0 + si * SEG;
-    uint4 yv[4 * PH];
-    load_y64<PH>(&sm.X[si & 1][hw][ph0][0], yv);
-    if constexpr (GATE) gate_rows(yv, zv);
-    store_y64<PH>(yg + (int64_t)pos * p.y_sl, p.y_sl, yv, c.c1 - pos);
+    lb_scan_segment<N, HG, PH, GATE>(p, c, si, &sm.st[cur], &sm.st[cur ^ 1], dec, &sm.mt[0][0][0], sm.dcol[hw],
+                                     yg, zg, H, kappa, dm, lo);
   }
   // final state (last chunk): H_true = e^kappa H, canonical (b, H, P, N) fp32
   if (p.final_state && k == p.nchunks - 1) {
