@@ -92,7 +92,10 @@ class Mamba2Layer(nn.Module):
         dt = self.dt_proj(x_act)                                 # (b, L, H); softplus(+ dt_bias) in the kernel
         Bm = self.B_proj(x_act).view(b, L, self.ngroups, self.d_state)
         Cm = self.C_proj(x_act).view(b, L, self.ngroups, self.d_state)
-        A = -torch.exp(self.A_log.float())
+        # A_log is clamped to [-5, 5] on the prefill path only, as the reference does (clamp in the scan,
+        # mamba2.py:87; none in the decode step, :441-443)
+        A_log = self.A_log.float()
+        A = -torch.exp(A_log if incremental else A_log.clamp(-5.0, 5.0))
         D = self.D.float()
         h_states = None
         # the z-gate y * silu(z) (:337-338) is applied by the kernels as y is stored
@@ -140,15 +143,14 @@ def kda_linear_attention(q1, q2, k, v, lambda_raw, kernel_dim, use_cache=False, 
         z_prev = torch.zeros((Bb, H, K, 1), device=q1.device, dtype=torch.float32)
     lam = ops.diff_lambda(lambda_raw)
     if S == 1 and use_cache:
-        # the step updates full-width (dk = D) fp32 copies in place: rows >= K stay zero (phi is 0 there)
-        St = torch.zeros((Bb, H, Dh, Dh), device=q1.device, dtype=torch.float32)
-        zt = torch.zeros((Bb, H, Dh), device=q1.device, dtype=torch.float32)
-        St[:, :, :K] = S_prev
-        zt[:, :, :K] = z_prev[..., 0]
-        out = ops.linear_attn_step(St, zt, q1, q2, k, v, lam=lam, kernel_dim=K, apply_phi=True)
+        # one in-place step (dk = K) on fp32 copies of the cache, which become the new cache (the reference
+        # returns new tensors): the state has K rows, so only the first K channels of q and k enter
+        St = S_prev.clone(memory_format=torch.contiguous_format)
+        zt = z_prev.clone(memory_format=torch.contiguous_format)
+        out = ops.linear_attn_step(St, zt, q1[..., :K], q2[..., :K], k[..., :K], v, lam=lam, kernel_dim=K,
+                                   apply_phi=True)
         out = out.reshape(Bb, H, 1, Dh)
-        new_cache = {"S": St[:, :, :K].contiguous(), "z": zt[:, :, :K, None].contiguous(), "attn_type": "linear"}
-        return out, new_cache
+        return out, {"S": St, "z": zt, "attn_type": "linear"}
     if not use_cache:
         return ops.linear_attention_scan(q1, q2, k, v, K, lambda_raw), None
     out, S_new, z_new = ops.linear_attn_scan(q1, q2, k, v, mode="reference", kernel_dim=K, lam=lam,

@@ -238,16 +238,16 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
         z4 = _inner_contig(z4)
     if not _plan_only and torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (x4, dt32, A32, B4, C4, D32, bias32, h0, z4)):
-        if return_h_states:
-            raise NotImplementedError("selective_scan: return_h_states is not differentiable")
-        y4, fin = _SelectiveScanFn.apply(x4, dt32, A32, B4, C4, D32, h0, bias32,
-                                         (dt_softplus, dt_limit, chunk_size))
+        cfg = (dt_softplus, dt_limit, chunk_size)
+        y4, fin = _SelectiveScanFn.apply(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg)
         if z4 is not None:
             y4 = y4 * torch.nn.functional.silu(z4)
-        y = y4.reshape(x.shape) if x.dim() == 3 else y4
-        if not return_final_state:
-            return y
-        return y, (fin.reshape(b, H * P, N) if x.dim() == 3 else fin)
+        out = [y4.reshape(x.shape) if x.dim() == 3 else y4]
+        if return_h_states:
+            out.append(_h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=True))
+        if return_final_state:
+            out.append(fin.reshape(b, H * P, N) if x.dim() == 3 else fin)
+        return out[0] if len(out) == 1 else tuple(out)
     y4 = torch.empty((b, L, H, P), device=x.device, dtype=x.dtype)
     fin = torch.empty((b, H, P, N), device=x.device, dtype=torch.float32) if return_final_state else None
     args = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, y4, fin, chunk_size, z4)
@@ -296,6 +296,8 @@ def _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4, dfin, need_dh0, 
     if dy4 is None:
         dy4 = torch.zeros((b, L, H, P), device=dev, dtype=x4.dtype)
     dy4 = _inner_contig(dy4.to(x4.dtype))
+    if dy4.stride(2) < P:                 # a broadcast gradient (e.g. of a sum over heads): the kernels need
+        dy4 = dy4.contiguous()            # each head's row of P values in its own place
     dfin = None if dfin is None else dfin.reshape(b, H, P, N).to(torch.float32).contiguous()
     dx = torch.empty((b, L, H, P), device=dev, dtype=x4.dtype)
     ddt = torch.empty((b, L, H), device=dev, dtype=torch.float32)
@@ -405,7 +407,7 @@ def selective_scan_bwd(dy, x, dt, A, B, C, D=None, *, d_final_state=None, initia
     return out
 
 
-def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size):
+def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=False):
     """h_states[b, t, n] = mean over (h, p) of the state h_t[h, p, n] (mamba2.py:114-116).
 
     The channel sum of the state is itself an SSD output once the roles of x and B are swapped: with
@@ -414,6 +416,10 @@ def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size):
     (dstate' = P), C' = 1, D' = 0, and the same dt and A per head, the recurrence gives
     h'_t[h', n', p] = h_t[h, p, 64q + n'], so y'_t[h', n'] = sum_p h_t[h, p, 64q + n'].  The same kernels
     compute it; the mean over heads is a reduction over the head axis.
+
+    ``grad``: through the autograd node of the scan (backward = ``mh_ssd_chunk_scan_bwd`` of the swapped
+    problem, with C' materialised as ones since the backward reads no broadcast C); the gathers and repeats
+    of B, dt, A, dt_bias and h0 carry their gradients back to the caller's tensors.
     """
     b, L, H, P = x4.shape
     G, N = B4.shape[2], B4.shape[3]
@@ -430,6 +436,10 @@ def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size):
     h0s = None
     if h0 is not None:
         h0s = h0.view(b, H, P, Q, 64).permute(0, 1, 3, 4, 2).reshape(b, H * Q, 64, P).contiguous()
+    if grad:
+        Cs = torch.ones((b, L, H, P), device=x4.device, dtype=x4.dtype)
+        ys, _ = _SelectiveScanFn.apply(xs, dts, As, Bs, Cs, None, h0s, bias_s, (dt_softplus, dt_limit, chunk_size))
+        return (ys.reshape(b, L, H, N).to(torch.float32).sum(dim=2) / float(H * P)).to(x4.dtype)
     ys = torch.empty((b, L, H * Q, 64), device=x4.device, dtype=x4.dtype)
     args = _ssd_args(xs, dts, As, Bs, Cs, None, bias_s, dt_softplus, dt_limit, h0s, ys, None, chunk_size)
     nbytes = ct.c_size_t()

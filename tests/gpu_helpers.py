@@ -39,3 +39,12 @@ def check(name, out, ref, tol):
     say(f"{name}: rel_l2={e:.3e} max_abs={m:.3e} tol={tol:.0e}")
     assert e <= tol, f"{name}: rel_l2 {e:.3e} > {tol:.0e}"
     return e
+
+
+def check_per_head(name, out, ref, tol, axis=1):
+    """check() on every head separately (heads along `axis`): outputs whose scale differs by orders of magnitude
+    between heads (the differential output's 1 / (1 - lambda)) cannot hide one head's error in another's norm."""
+    out = host(out) if torch.is_tensor(out) else np.asarray(out)
+    ref = np.asarray(ref)
+    return max(check(f"{name}[head {i}]", np.take(out, i, axis=axis), np.take(ref, i, axis=axis), tol)
+               for i in range(out.shape[axis]))

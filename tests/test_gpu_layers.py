@@ -2,7 +2,8 @@
 
 * ``causal_conv1d`` (HIP) vs ``oracle.ssd.ref_causal_conv1d`` (mamba2.py:370-405), with and without the
   cached raw rows, bias and fused SiLU;
-* ``selective_scan(return_h_states=True)`` vs ``oracle.ssd.ssd_h_states`` (mamba2.py:114-116);
+* ``selective_scan(return_h_states=True)`` vs ``oracle.ssd.ssd_h_states`` (mamba2.py:114-116), and its
+  gradients under autograd vs autograd of the float64 recurrence;
 * ``Mamba2Layer`` (A3 dispatch and cache, mamba2.py:249-364) vs the same layer composed in float64 from the
   oracle pieces, and prefill + one incremental step vs one longer prefill;
 * ``kda_linear_attention`` (A13 state semantics, kda_diff.py:286-338) vs the reference-mode KDA oracle.
@@ -71,15 +72,77 @@ def test_h_states_vs_oracle(dtype, G, N, h0):
     check("h_states last row = mean of final state", hs[:, -1], host(fin).mean(axis=(1, 2)), TOL[dtype])
 
 
+def _scan_recurrence_f64(x, dt_raw, A, B, C, D, bias, h0):
+    """The scan written as its plain recurrence in float64 torch (autograd gives the reference gradients):
+    dt = softplus(dt_raw + bias); h_t = e^{A dt_t} h_{t-1} + dt_t x_t B_t^T; y_t = C_t h_t + D x_t;
+    h_states_t = mean over (h, p) of h_t (mamba2.py:98-116)."""
+    b, L, H, P = x.shape
+    G = B.shape[2]
+    gidx = torch.arange(H) // (H // G)
+    dt = F.softplus(dt_raw + bias)
+    h = h0 if h0 is not None else torch.zeros(b, H, P, B.shape[3], dtype=torch.float64)
+    ys, hs = [], []
+    for t in range(L):
+        h = torch.exp(A * dt[:, t])[..., None, None] * h + \
+            (dt[:, t, :, None, None] * x[:, t, :, :, None]) * B[:, t][:, gidx][:, :, None, :]
+        ys.append(torch.einsum("bhpn,bhn->bhp", h, C[:, t][:, gidx]) + D[:, None] * x[:, t])
+        hs.append(h.mean(dim=(1, 2)))
+    return torch.stack(ys, 1), torch.stack(hs, 1), h
+
+
+@pytest.mark.parametrize("dtype,G,N,h0", [(torch.float32, 1, 64, False), (torch.float32, 2, 128, True),
+                                          (torch.bfloat16, 1, 128, True)])
+def test_h_states_autograd_vs_recurrence(dtype, G, N, h0):
+    """selective_scan(return_h_states=True) under autograd (the path Mamba2Layer trains through with
+    return_h_states, hybrid.py:383-395): every input gradient of <wy, y> + <wh, h_states> + <wf, final_state>
+    against autograd of the float64 recurrence."""
+    g = torch.Generator().manual_seed(31 + N + G)
+    b, L, H, P = 1, 70, 4, 64
+    q = lambda t: t.to(dtype).to(torch.float64)       # inputs exactly representable in the I/O dtype
+    x, B, C = q(torch.randn(b, L, H, P, generator=g)), q(torch.randn(b, L, G, N, generator=g)), \
+        q(torch.randn(b, L, G, N, generator=g))
+    dt_raw = torch.randn(b, L, H, generator=g, dtype=torch.float64) - 1.0
+    bias = 0.3 * torch.randn(H, generator=g, dtype=torch.float64)
+    A = -torch.exp(torch.rand(H, generator=g, dtype=torch.float64) * 2.5)
+    D = 1 + 0.1 * torch.randn(H, generator=g, dtype=torch.float64)
+    s0 = 0.1 * torch.randn(b, H, P, N, generator=g, dtype=torch.float64) if h0 else None
+    wy = torch.randn(b, L, H, P, generator=g, dtype=torch.float64)
+    wh = torch.randn(b, L, N, generator=g, dtype=torch.float64) * 10.0
+    wf = torch.randn(b, H, P, N, generator=g, dtype=torch.float64) * 0.1
+    say(f"h_states autograd G={G} N={N} h0={h0} {dtype}")
+    leaves = dict(x=dev(x, dtype), dt=dev(dt_raw), A=dev(A), B=dev(B, dtype), C=dev(C, dtype), D=dev(D),
+                  bias=dev(bias), h0=dev(s0) if h0 else None)
+    for t in leaves.values():
+        if t is not None:
+            t.requires_grad_()
+    y, hs, fin = mh.selective_scan(leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], leaves["D"],
+                                   return_h_states=True, return_final_state=True, initial_state=leaves["h0"],
+                                   dt_bias=leaves["bias"], dt_softplus=True)
+    loss = (y.float() * dev(wy)).sum() + (hs.float() * dev(wh)).sum() + (fin * dev(wf)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    r = dict(x=x, dt=dt_raw, A=A, B=B, C=C, D=D, bias=bias, h0=s0)
+    for t in r.values():
+        if t is not None:
+            t.requires_grad_()
+    ry, rhs, rfin = _scan_recurrence_f64(r["x"], r["dt"], r["A"], r["B"], r["C"], r["D"], r["bias"], r["h0"])
+    check("h_states", hs, rhs.detach().numpy(), TOL[dtype])
+    ((ry * wy).sum() + (rhs * wh).sum() + (rfin * wf).sum()).backward()
+    for name in ("x", "dt", "A", "B", "C", "D", "bias") + (("h0",) if h0 else ()):
+        check(f"d{name}", leaves[name].grad, r[name].grad.numpy(), TOL[dtype])
+
+
 # ----------------------------------------------------------------- Mamba2Layer
 
-def _layer_ref(layer, u, use_cache_state=None):
-    """Float64 composition of the layer from the oracle pieces (no cache)."""
+def _layer_ref(layer, u, cache=None):
+    """Float64 composition of the layer from the oracle pieces.  Without a cache: the prefill, A_log clamped to
+    [-5, 5] (mamba2.py:87); with one (conv_state, ssm_state): the decode step, A_log unclamped (:441-443)."""
     P64 = {k: v.detach().double().cpu().numpy() for k, v in layer.named_parameters()}
     un = u.detach().double().cpu().numpy()
     xz = un @ P64["in_proj.weight"].T
     x, z = np.split(xz, 2, axis=-1)
-    xc = ref.ref_causal_conv1d(x, P64["conv_weight"])
+    conv_state = None if cache is None else host(cache["conv_state"])
+    xc = ref.ref_causal_conv1d(x, P64["conv_weight"], conv_state=conv_state)
     xa = xc / (1.0 + np.exp(-xc))
     dt_raw = (xa @ P64["dt_proj.0.weight"].T) @ P64["dt_proj.1.weight"].T
     Bm = xa @ P64["B_proj.weight"].T
@@ -87,9 +150,10 @@ def _layer_ref(layer, u, use_cache_state=None):
     b, L, _ = un.shape
     H, Pd, G, N = layer.nheads, layer.headdim, layer.ngroups, layer.d_state
     dt = ref.softplus(dt_raw + P64["dt_bias"])
-    A = -np.exp(P64["A_log"])
+    A = -np.exp(P64["A_log"] if cache is not None else np.clip(P64["A_log"], -5.0, 5.0))
+    h0 = None if cache is None else host(cache["ssm_state"]).reshape(b, H, Pd, N)
     y, fin = ref.ssd_direct(xa.reshape(b, L, H, Pd), dt, A, Bm.reshape(b, L, G, N), Cm.reshape(b, L, G, N),
-                            P64["D"])
+                            P64["D"], initial_state=h0)
     hs = ref.ssd_h_states(xa.reshape(b, L, H, Pd), dt, A, Bm.reshape(b, L, G, N))
     y = y.reshape(b, L, H * Pd) * (z / (1.0 + np.exp(-z)))
     out = y @ P64["out_proj.weight"].T
@@ -117,6 +181,29 @@ def test_mamba2_layer_forward_vs_oracle(G, N):
     check("layer ssm_state", cache2["ssm_state"], r_fin, 1e-4)
     assert cache2["ssm_state"].shape == (2, 256, N)
     assert torch.equal(cache2["conv_state"], layer.in_proj(u)[:, -3:, :256])
+
+
+def test_mamba2_layer_A_log_clamped_in_prefill_only():
+    """A_log beyond [-5, 5]: the prefill uses exp(clamp(A_log)) (mamba2.py:87), the decode step exp(A_log)
+    (:441-443), as the reference does."""
+    torch.manual_seed(13)
+    layer = Mamba2Layer(256, d_state=64, expand=1, headdim=64, ngroups=1, device="cuda", dtype=torch.float32)
+    with torch.no_grad():
+        layer.A_log.copy_(torch.tensor([6.0, -6.0, 1.0, 5.5], device="cuda"))
+        for lin in layer.dt_proj:
+            lin.weight.normal_(std=0.05)
+    u = torch.randn(2, 40, 256, device="cuda")
+    say("Mamba2Layer A_log clamp: prefill vs decode")
+    with torch.no_grad():
+        pre, c = layer(u[:, :39], use_cache=True)
+        step, c2 = layer(u[:, 39:], use_cache=True, cache=c)
+    torch.cuda.synchronize()
+    r_pre, r_fin, _, _ = _layer_ref(layer, u[:, :39])
+    check("prefill (clamped A)", pre, r_pre, 1e-4)
+    check("prefill state", c["ssm_state"], r_fin, 1e-4)
+    r_step, r_sfin, _, _ = _layer_ref(layer, u[:, 39:], cache=c)
+    check("step (unclamped A)", step, r_step, 1e-4)
+    check("step state", c2["ssm_state"], r_sfin, 1e-4)
 
 
 def test_mamba2_layer_prefill_then_step_equals_longer_prefill():
