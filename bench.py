@@ -14,7 +14,9 @@ a step from the previous one.  The same JSON line carries:
   HBM-bound by intensity).
 * ``cpu_baseline`` -- the reference's pure-PyTorch CPU prefill
   (``oracle/baseline.py``, mamba2.py:84-126 structure) timed on the host cores
-  on a bounded token sample of the same workload.
+  on a bounded token sample of the same workload, with the CPU model, core counts
+  and torch threads; ``other`` holds the decode step at B = 64 and 256 and the
+  reference-mode KDA operator at the kda5 shape.
 * ``decode`` -- selective state update at B=64 and B=256 (HBM GB/s vs 8 TB/s).
 * ``other`` -- ssd4 (128K prefill with state carry), kda5 (gated KDA scan), ssd2_bwd (the backward of
   the ssd2 prefill: all input gradients from dy and d_final) and kda5_bwd (the backward of the reference-mode
@@ -321,25 +323,86 @@ def bench_kda(cfg, steps, warmup):
 
 # ----------------------------------------------------------------- CPU baseline (reference algorithm on the host)
 
-def cpu_baseline(cfg, sample_len):
+def _cpu_info():
+    """CPU model, logical CPU counts and the thread count the CPU legs use: the smallest of os.cpu_count(), the
+    process's affinity set and OMP_NUM_THREADS (the host share a GPU box grants one GPU)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = nproc
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = min(nproc, affinity, int(omp) if omp and omp.isdigit() and int(omp) > 0 else nproc)
+    return dict(cpu_model=model, nproc=nproc, affinity=affinity, omp_num_threads=omp, threads=threads)
+
+
+def _median_time(fn, runs):
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def cpu_baseline(cfg, sample_len, kda_sample=512):
+    """The reference's pure-PyTorch CPU path (oracle/baseline.py restates it at its cost structure) on the host:
+    the ssd2 prefill (headline comparator), the c3 decode step at B = 64 and 256, and the reference-mode KDA
+    operator at the kda5 shape on a leading slice of ``kda_sample`` tokens (fixed work per token)."""
     from mamformer_amd import workloads as W
     from oracle import baseline as BL
 
-    cores = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(cores)
+    info = _cpu_info()
+    torch.set_num_threads(info["threads"])
     inp = W.ssd_inputs(cfg.scaled(seqlen=sample_len))
     x4, dt, A, B, C, D = (inp[k] for k in ("x", "dt", "A", "B", "C", "D"))
     BL.ssd_prefill_sample(x4[:, :16], dt[:, :16], A, B[:, :16], C[:, :16], D)      # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        BL.ssd_prefill_sample(x4, dt, A, B, C, D)
-        times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
-    return dict(value=cfg.batch * sample_len / t / 1e6, unit="Mtok/s", cores=cores, kind="port",
-                sample=(f"{cfg.name} full width (b{cfg.batch} d_inner {cfg.nheads * cfg.headdim} N{cfg.dstate}), "
-                        f"first {sample_len} of {cfg.seqlen} tokens, fp32, median of 3 runs ({t:.2f} s each); "
-                        f"torch {torch.__version__} threads={torch.get_num_threads()}"))
+    t = _median_time(lambda: BL.ssd_prefill_sample(x4, dt, A, B, C, D), 3)
+    del inp, x4, B, C
+    res = dict(value=cfg.batch * sample_len / t / 1e6, unit="Mtok/s", cores=info["threads"], kind="port",
+               sample=(f"{cfg.name} full width (b{cfg.batch} d_inner {cfg.nheads * cfg.headdim} N{cfg.dstate}), "
+                       f"first {sample_len} of {cfg.seqlen} tokens, fp32, median of 3 runs ({t:.2f} s each); "
+                       f"torch {torch.__version__} threads={torch.get_num_threads()}"),
+               cpu_model=info["cpu_model"], nproc=info["nproc"], affinity=info["affinity"],
+               omp_num_threads=info["omp_num_threads"], torch_threads=torch.get_num_threads())
+    extra = {}
+    # c3 decode: one _recurrent_step (mamba2.py:431-458) at d_inner = H*P, fp32 state (b, d_inner, N)
+    for bsz in (64, 256):
+        c = W.DEC3.scaled(batch=bsz)
+        d_inner, N = c.nheads * c.headdim, c.dstate
+        g = torch.Generator().manual_seed(c.seed)
+        h = 0.1 * torch.randn(bsz, d_inner, N, generator=g)
+        x_t, dt_t = torch.randn(bsz, d_inner, generator=g), torch.rand(bsz, d_inner, generator=g) * 0.1
+        B_t, C_t = torch.randn(bsz, N, generator=g), torch.randn(bsz, N, generator=g)
+        A_log, Dv = torch.zeros(N), torch.ones(d_inner)
+        BL.recurrent_step_cpu(x_t, dt_t, B_t, C_t, h, A_log, Dv)
+        td = _median_time(lambda: BL.recurrent_step_cpu(x_t, dt_t, B_t, C_t, h, A_log, Dv), 5)
+        nbytes = decode_alg(c)
+        extra[f"decode_B{bsz}"] = dict(us_per_step=round(td * 1e6, 1), GBs=round(nbytes / td / 1e9, 2),
+                                       sample=f"dec3 B={bsz} one step, fp32, median of 5")
+        del h
+    # c5: LinearDiffAttention._linear_attention_scan (kda_diff.py:357-478) at the kda5 shape, leading slice
+    c = W.KDA5.scaled(seqlen=kda_sample)
+    q = W.kda_inputs(c)
+    lr = torch.full((c.nheads,), 1.386)                 # sigmoid(1.386) = 0.8, the workload's lambda
+    BL.linear_attention_scan_cpu(q["q1"][:, :, :64], q["q2"][:, :, :64], q["k"][:, :, :64], q["v"][:, :, :64],
+                                 c.dk, lr)
+    tk = _median_time(lambda: BL.linear_attention_scan_cpu(q["q1"], q["q2"], q["k"], q["v"], c.dk, lr), 3)
+    extra["kda5"] = dict(mtok_s=c.batch * kda_sample / tk / 1e6, s_per_run=round(tk, 2),
+                         sample=(f"kda5 full width (B{c.batch} H{c.nheads} D{c.dk}), first {kda_sample} of "
+                                 f"{W.KDA5.seqlen} tokens, the reference's ungated normalised operator, bf16, "
+                                 f"median of 3"))
+    res["other"] = extra
+    return res
 
 
 # ----------------------------------------------------------------- HBM traffic calibration
@@ -512,7 +575,10 @@ def main():
     if "cpu" in legs:
         log(f"cpu baseline: reference prefill on {args.cpu_sample} tokens of ssd2")
         out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_sample)
-        log(f"cpu: {out['cpu_baseline']['value']:.4f} Mtok/s")
+        cb = out["cpu_baseline"]
+        log(f"cpu ({cb['cpu_model']}, {cb['cores']} threads of nproc {cb['nproc']}): ssd2 {cb['value']:.4f} Mtok/s; "
+            f"decode B=64 {cb['other']['decode_B64']['GBs']} GB/s, B=256 {cb['other']['decode_B256']['GBs']} GB/s; "
+            f"kda5 {cb['other']['kda5']['mtok_s']:.4f} Mtok/s")
     print(json.dumps(out), flush=True)
 
 

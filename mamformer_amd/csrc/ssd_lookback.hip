@@ -137,13 +137,14 @@ __device__ __forceinline__ void halves(float v, float (&o)[2]) {
 }
 
 // Workgroup -> (chunk k, chain = batch * (H / HG) + head block).  Workgroups are dealt to the 8 XCDs
-// round-robin by index; when the chains split evenly over them, every chunk of a chain runs on one XCD, so the
-// scan finds its predecessors' chunk states and the x tiles pass 1 just read in that XCD's L2.
+// round-robin by index; when the chains split evenly over them, XCD x runs every chunk of the consecutive
+// chains [x cpx, (x + 1) cpx): the scan finds its predecessors' chunk states in that XCD's L2, and the head
+// blocks sharing a group's B and C tiles (consecutive chains) read them through as few L2s as possible.
 __device__ __forceinline__ void lb_block(int nchunks, int nchains, int& k, int& chain) {
   const int i = blockIdx.x;
   if ((nchains & 7) == 0) {
     const int cpx = nchains >> 3, s = i >> 3;
-    chain = (i & 7) + 8 * (s % cpx);
+    chain = (i & 7) * cpx + s % cpx;
     k = s / cpx;
   } else {
     k = i % nchunks;
