@@ -63,8 +63,11 @@ enum {
  *   (mamformer/kernels/triton_ssd.py:508-564), in the per-head SSD convention:
  *   x (b, L, H, P), dt (b, L, H) fp32, A (H,) fp32 (A <= 0), B/C (b, L, G, N),
  *   D (H,) or (H*P,) fp32 or NULL, initial_state / final_state (b, H, P, N) fp32.
- *   y (b, L, H, P) in the dtype of x.  Supported: P = 64, N in {64, 128},
+ *   y (b, L, H, P) in the dtype of x.  Supported: P = 64, N a multiple of 8 up to 256,
  *   H % G == 0.  chunk_len = state-passing chunk (multiple of 64; 0 = auto).
+ *   The kernels tile N = 64 and 128; other N run as compositions of them (N < 64 zero-padded to 64,
+ *   64 < N < 128 to 128, N > 128 as two 128-column halves whose outputs are summed), with B, C and
+ *   the state pieces in the workspace.
  * ---------------------------------------------------------------------- */
 typedef struct {
   int64_t batch, seqlen, nheads, headdim, dstate, ngroups;
@@ -99,7 +102,8 @@ int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream);
  *   a->workspace / a->workspace_bytes are ignored: the kernels use a file-scope static device array of
  *   MH_NOALLOC_SCRATCH_BYTES, one per GPU the library runs on, held until the process ends.  Sizes whose
  *   workspace (mh_ssd_workspace_bytes) exceeds it are rejected with MH_ERR_WORKSPACE before any HIP
- *   call.  Every call on one GPU uses that GPU's single array: calls that overlap in time on one GPU
+ *   call, and so is a dstate the kernels do not tile directly (anything but 64 and 128: those compositions
+ *   need the caller's workspace), with MH_ERR_UNSUPPORTED.  Every call on one GPU uses that GPU's single array: calls that overlap in time on one GPU
  *   (several streams or host threads) race and must be serialised by the caller.  The first call on
  *   each GPU looks up the array's device address (hipGetSymbolAddress), which allocates nothing.
  *   Results are bit-identical to mh_ssd_chunk_scan_fwd's for the same arguments. */
@@ -117,7 +121,7 @@ int mh_ssd_chunk_scan_fwd_noalloc(const mh_ssd_args* a, void* stream);
  *   (NULL: zero / not wanted); ddt (b, L, H) fp32, the gradient w.r.t. the raw dt (through
  *   dt_bias, softplus and the clamp per fwd.flags); dA (H,) fp32; dB, dC (b, L, G, N) in the dtype
  *   of x; dD like D (NULL when D is NULL); d_dt_bias (H,) fp32 or NULL.  Every output is
- *   overwritten.  Same supported sizes as the forward.
+ *   overwritten.  Same supported sizes (and compositions) as the forward.
  * ---------------------------------------------------------------------- */
 typedef struct {
   mh_ssd_args fwd;

@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "../../include/mamformer_hip.h"
@@ -40,7 +41,8 @@ int ssd_heads_per_wg(const mh_ssd_args* a) {
   const int64_t hpg = a->nheads / a->ngroups;
   // fp32 tiles with N = 128 are twice the bf16 size: one head per workgroup
   // keeps the running state and operands in registers.
-  int hg = (a->dtype == MH_F32 && a->dstate == 128) ? 1 : 4;
+  const int64_t n = a->dstate <= 64 ? 64 : 128;                 // dstate the kernels run
+  int hg = (a->dtype == MH_F32 && n == 128) ? 1 : 4;
   while (hg > 1 && (hpg % hg) != 0) hg >>= 1;
   return hg;
 }
@@ -70,8 +72,8 @@ int ssd_validate(const mh_ssd_args* a, int64_t* chunk_len_out) {
   const int es = elem_size(a->dtype);
   if (!es) return fail(MH_ERR_DTYPE, "ssd: unknown dtype %d", a->dtype);
   if (a->headdim != 64) return fail(MH_ERR_UNSUPPORTED, "ssd: headdim %lld not supported (64)", (long long)a->headdim);
-  if (a->dstate != 64 && a->dstate != 128)
-    return fail(MH_ERR_UNSUPPORTED, "ssd: dstate %lld not supported (64, 128)", (long long)a->dstate);
+  if (a->dstate % 8 || a->dstate > 256)
+    return fail(MH_ERR_UNSUPPORTED, "ssd: dstate %lld not supported (a multiple of 8 up to 256)", (long long)a->dstate);
   int64_t cl = a->chunk_len;
   if (cl == 0) cl = ssd_auto_chunk(a);
   if (cl < 64 || cl % 64 || cl > (1 << 20))
@@ -314,6 +316,291 @@ int ssd_bwd_heads_per_wg(const mh_ssd_args* f) {
   return hb;
 }
 
+hipError_t ssd_launch_bwd_native(const mh_ssd_bwd_args* a, hipStream_t st) {
+  const mh_ssd_args* f = &a->fwd;
+  mh::SsdBwdParams q;
+  memset(&q, 0, sizeof(q));
+  const int64_t nseg = (f->seqlen + 63) / 64;
+  ssd_fill(f, 64, nseg, q.f);
+  q.f.y = nullptr;
+  q.f.final_state = nullptr;
+  q.f.z = nullptr;
+  q.dy = a->dy; q.dy_sb = a->dy_stride_b; q.dy_sl = a->dy_stride_l; q.dy_sh = a->dy_stride_h;
+  q.d_final = a->d_final_state;
+  q.dx = a->dx; q.dx_sb = a->dx_stride_b; q.dx_sl = a->dx_stride_l; q.dx_sh = a->dx_stride_h;
+  q.ddt = a->ddt; q.ddt_sb = a->ddt_stride_b; q.ddt_sl = a->ddt_stride_l;
+  q.dA = a->dA; q.dD = f->D ? a->dD : nullptr; q.dbias = a->d_dt_bias; q.dh0 = a->d_initial_state;
+  q.dB = a->dB; q.dB_sb = a->dB_stride_b; q.dB_sl = a->dB_stride_l;
+  q.dC = a->dC; q.dC_sb = a->dC_stride_b; q.dC_sl = a->dC_stride_l;
+  q.heads_per_wg = ssd_bwd_heads_per_wg(f);
+  if (nseg > 0) mh::ssd_bwd_workspace_layout(q, a->workspace);
+  return mh::launch_ssd_bwd(q, st);
+}
+
+// ------------------------------------------------------------------ SSD state sizes by composition
+// The prefill and backward kernels tile dstate 64 and 128.  Other sizes (multiples of 8 up to 256) run as
+// compositions: up to 64 zero-padded at 64, up to 128 zero-padded at 128, above 128 as two runs over the
+// 128-column halves of B, C and the state, the second half zero-padded (widen.hip states why these are
+// exact); the pieces of B, C and the states pass through the workspace.
+bool ssd_native_dstate(int64_t n) { return n == 64 || n == 128; }
+int64_t ssd_inner_dstate(int64_t n) { return n <= 64 ? 64 : 128; }
+size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
+char* at(void* base, size_t off) { return reinterpret_cast<char*>(base) + off; }
+
+struct SsdWide {
+  int64_t ni;              // dstate of the inner runs
+  int pieces;              // 1 (padded) or 2 (halves)
+  bool copy_bc;            // B / C (and dB / dC) pieces pass through the workspace
+  size_t inner;            // workspace of one inner run (at offset 0)
+  size_t oB, oC, oS0, oS1, oX2, oT2, oH2, oH3, total;
+};
+
+// Forward: oS0 = initial-state piece, oS1 = final-state piece, oX2 = y of the second half.
+void ssd_wide_fwd_plan(const mh_ssd_args* a, int64_t cl, SsdWide& w) {
+  const int es = elem_size(a->dtype);
+  const int64_t b = a->batch, L = a->seqlen, H = a->nheads, P = a->headdim, G = a->ngroups;
+  w.ni = ssd_inner_dstate(a->dstate);
+  w.pieces = a->dstate > 128 ? 2 : 1;
+  w.copy_bc = a->dstate != w.pieces * w.ni || G > 1;
+  const int64_t nchunks = (L + cl - 1) / cl;
+  w.inner = nchunks > 0 ? mh::ssd_workspace_bytes((int)b, (int)L, (int)nchunks, (int)H, (int)P, (int)w.ni, (int)G,
+                                                  a->dtype) : 0;
+  const size_t bc = w.copy_bc ? (size_t)(b * L * G * w.ni * es) : 0, st = (size_t)(b * H * P * w.ni * 4);
+  size_t off = a256(w.inner);
+  w.oB = off; off += a256(bc);
+  w.oC = off; off += a256(bc);
+  w.oS0 = off; off += a->initial_state ? a256(st) : 0;
+  w.oS1 = off; off += a->final_state ? a256(st) : 0;
+  w.oX2 = off; off += w.pieces == 2 ? a256((size_t)(b * L * H * P * es)) : 0;
+  w.oT2 = w.oH2 = w.oH3 = off;
+  w.total = off;
+}
+
+// Column piece q of a (b, L, G, N) B/C-shaped tensor into a (b, L, G, ni) workspace buffer (zero-padded), or back.
+mh::ColCopy bc_in(const mh_ssd_args* a, const void* src, int64_t sb, int64_t sl, void* dst, int64_t ni, int q) {
+  mh::ColCopy c{};
+  c.es = elem_size(a->dtype);
+  c.d0 = a->batch; c.d1 = a->seqlen; c.d2 = a->ngroups;
+  c.ncols = ni; c.nvalid = std::min<int64_t>(ni, a->dstate - q * ni);
+  c.src = src; c.s0 = sb; c.s1 = sl; c.s2 = a->dstate; c.scol0 = q * ni;
+  c.dst = dst; c.t2 = ni; c.t1 = a->ngroups * ni; c.t0 = a->seqlen * c.t1; c.tcol0 = 0;
+  return c;
+}
+mh::ColCopy bc_out(const mh_ssd_args* a, const void* src, void* dst, int64_t tb, int64_t tl, int64_t ni, int q) {
+  mh::ColCopy c{};
+  c.es = elem_size(a->dtype);
+  c.d0 = a->batch; c.d1 = a->seqlen; c.d2 = a->ngroups;
+  c.ncols = c.nvalid = std::min<int64_t>(ni, a->dstate - q * ni);
+  c.src = src; c.s2 = ni; c.s1 = a->ngroups * ni; c.s0 = a->seqlen * c.s1; c.scol0 = 0;
+  c.dst = dst; c.t0 = tb; c.t1 = tl; c.t2 = a->dstate; c.tcol0 = q * ni;
+  return c;
+}
+// Column piece q of a (b, H, P, N) fp32 state into a (b, H, P, ni) buffer (zero-padded), or back.
+mh::ColCopy state_in(const mh_ssd_args* a, const float* src, void* dst, int64_t ni, int q) {
+  mh::ColCopy c{};
+  c.es = 4;
+  c.d0 = a->batch; c.d1 = a->nheads; c.d2 = a->headdim;
+  c.ncols = ni; c.nvalid = std::min<int64_t>(ni, a->dstate - q * ni);
+  c.src = src; c.s2 = a->dstate; c.s1 = a->headdim * c.s2; c.s0 = a->nheads * c.s1; c.scol0 = q * ni;
+  c.dst = dst; c.t2 = ni; c.t1 = a->headdim * ni; c.t0 = a->nheads * c.t1; c.tcol0 = 0;
+  return c;
+}
+mh::ColCopy state_out(const mh_ssd_args* a, const void* src, float* dst, int64_t ni, int q) {
+  mh::ColCopy c{};
+  c.es = 4;
+  c.d0 = a->batch; c.d1 = a->nheads; c.d2 = a->headdim;
+  c.ncols = c.nvalid = std::min<int64_t>(ni, a->dstate - q * ni);
+  c.src = src; c.s2 = ni; c.s1 = a->headdim * ni; c.s0 = a->nheads * c.s1; c.scol0 = 0;
+  c.dst = dst; c.t2 = a->dstate; c.t1 = a->headdim * c.t2; c.t0 = a->nheads * c.t1; c.tcol0 = q * ni;
+  return c;
+}
+
+// The inner forward arguments of piece q (B, C, D and the state pointers set; outputs by the caller).
+mh_ssd_args ssd_piece(const mh_ssd_args* a, const SsdWide& w, void* ws, int q) {
+  const int es = elem_size(a->dtype);
+  mh_ssd_args in = *a;
+  in.dstate = w.ni;
+  if (w.copy_bc) {
+    in.B = at(ws, w.oB); in.C = at(ws, w.oC);
+    in.B_stride_l = in.C_stride_l = a->ngroups * w.ni;
+    in.B_stride_b = in.C_stride_b = a->seqlen * a->ngroups * w.ni;
+  } else {                 // one group: the half is a column offset with the caller's strides
+    in.B = reinterpret_cast<const char*>(a->B) + q * w.ni * es;
+    in.C = reinterpret_cast<const char*>(a->C) + q * w.ni * es;
+  }
+  if (q > 0) { in.D = nullptr; in.flags &= ~MH_D_PER_CHANNEL; }    // D x enters y once
+  in.initial_state = a->initial_state ? reinterpret_cast<const float*>(at(ws, w.oS0)) : nullptr;
+  in.final_state = nullptr;
+  in.z = nullptr;
+  in.workspace = ws; in.workspace_bytes = w.inner;
+  return in;
+}
+
+hipError_t ssd_launch_native(const mh_ssd_args* a, int64_t cl, void* ws, hipStream_t st) {
+  const int64_t nchunks = (a->seqlen + cl - 1) / cl;
+  mh::SsdParams p;
+  ssd_fill(a, cl, nchunks, p);
+  if (nchunks > 0) mh::ssd_workspace_layout(p, ws);
+  return mh::launch_ssd(p, st);
+}
+
+int ssd_fwd_wide(const mh_ssd_args* a, int64_t cl, hipStream_t st) {
+  SsdWide w;
+  ssd_wide_fwd_plan(a, cl, w);
+  void* ws = a->workspace;
+  const int es = elem_size(a->dtype);
+  const int64_t b = a->batch, L = a->seqlen, H = a->nheads, P = a->headdim;
+  hipError_t e = hipSuccess;
+  for (int q = 0; q < w.pieces && e == hipSuccess; ++q) {
+    mh_ssd_args in = ssd_piece(a, w, ws, q);
+    in.chunk_len = cl;
+    if (q == 0) {
+      in.y = a->y;
+      if (w.pieces == 1) in.z = a->z;
+    } else {
+      in.y = at(ws, w.oX2);
+      in.y_stride_h = P; in.y_stride_l = H * P; in.y_stride_b = L * H * P;
+    }
+    if (a->final_state) in.final_state = reinterpret_cast<float*>(at(ws, w.oS1));
+    int64_t clin = 0;
+    const int rc = ssd_validate(&in, &clin);
+    if (rc) return rc;
+    if (w.copy_bc && L > 0) {
+      e = mh::launch_col_copy(bc_in(a, a->B, a->B_stride_b, a->B_stride_l, at(ws, w.oB), w.ni, q), st);
+      if (e == hipSuccess) e = mh::launch_col_copy(bc_in(a, a->C, a->C_stride_b, a->C_stride_l, at(ws, w.oC), w.ni, q), st);
+    }
+    if (e == hipSuccess && a->initial_state) e = mh::launch_col_copy(state_in(a, a->initial_state, at(ws, w.oS0), w.ni, q), st);
+    if (e == hipSuccess) e = ssd_launch_native(&in, cl, ws, st);
+    if (e == hipSuccess && a->final_state) e = mh::launch_col_copy(state_out(a, at(ws, w.oS1), a->final_state, w.ni, q), st);
+  }
+  if (e == hipSuccess && w.pieces == 2) {
+    mh::RowAdd r{};
+    r.es = es; r.d0 = b; r.d1 = L; r.d2 = H; r.ncols = P;
+    r.dst = a->y; r.t0 = a->y_stride_b; r.t1 = a->y_stride_l; r.t2 = a->y_stride_h;
+    r.src = at(ws, w.oX2); r.s2 = P; r.s1 = H * P; r.s0 = L * H * P;
+    r.gate = a->z; r.g0 = a->z_stride_b; r.g1 = a->z_stride_l; r.g2 = a->z_stride_h;
+    e = mh::launch_row_add(r, st);
+  }
+  return hip_status(e, "ssd_chunk_scan_fwd");
+}
+
+// Backward: oS0 = initial-state piece, oS1 = d_final_state piece, oH2 = d_initial_state piece; for two halves
+// the second half's dx (oX2), ddt (oT2), dA and d_dt_bias (oH3) before they are added to the first half's.
+void ssd_wide_bwd_plan(const mh_ssd_bwd_args* a, SsdWide& w) {
+  const mh_ssd_args* f = &a->fwd;
+  const int es = elem_size(f->dtype);
+  const int64_t b = f->batch, L = f->seqlen, H = f->nheads, P = f->headdim, G = f->ngroups;
+  w.ni = ssd_inner_dstate(f->dstate);
+  w.pieces = f->dstate > 128 ? 2 : 1;
+  w.copy_bc = f->dstate != w.pieces * w.ni || G > 1;
+  w.inner = L > 0 ? mh::ssd_bwd_workspace_bytes((int)b, (int)L, (int)H, (int)w.ni, (int)G, f->dtype,
+                                                ssd_bwd_heads_per_wg(f)) : 0;
+  const size_t bc = w.copy_bc ? (size_t)(b * L * G * w.ni * es) : 0, st = (size_t)(b * H * P * w.ni * 4);
+  size_t off = a256(w.inner);
+  w.oB = off; off += a256(2 * bc);           // B piece, then dB piece
+  w.oC = off; off += a256(2 * bc);           // C piece, then dC piece
+  w.oS0 = off; off += f->initial_state ? a256(st) : 0;
+  w.oS1 = off; off += a->d_final_state ? a256(st) : 0;
+  w.oH2 = off; off += a->d_initial_state ? a256(st) : 0;
+  const bool two = w.pieces == 2;
+  w.oX2 = off; off += two ? a256((size_t)(b * L * H * P * es)) : 0;
+  w.oT2 = off; off += two ? a256((size_t)(b * L * H * 4)) : 0;
+  w.oH3 = off; off += two ? a256((size_t)(2 * H * 4)) : 0;
+  w.total = off;
+}
+
+int ssd_bwd_wide(const mh_ssd_bwd_args* a, hipStream_t st) {
+  const mh_ssd_args* f = &a->fwd;
+  SsdWide w;
+  ssd_wide_bwd_plan(a, w);
+  void* ws = a->workspace;
+  const int es = elem_size(f->dtype);
+  const int64_t b = f->batch, L = f->seqlen, H = f->nheads, P = f->headdim, G = f->ngroups;
+  const size_t bc = w.copy_bc ? (size_t)(b * L * G * w.ni * es) : 0;
+  hipError_t e = hipSuccess;
+  for (int q = 0; q < w.pieces && e == hipSuccess; ++q) {
+    mh_ssd_bwd_args in = *a;
+    in.fwd = ssd_piece(f, w, ws, q);
+    in.fwd.workspace = nullptr; in.fwd.workspace_bytes = 0;
+    in.d_final_state = a->d_final_state ? reinterpret_cast<const float*>(at(ws, w.oS1)) : nullptr;
+    in.d_initial_state = a->d_initial_state ? reinterpret_cast<float*>(at(ws, w.oH2)) : nullptr;
+    if (w.copy_bc) {
+      in.dB = at(ws, w.oB + bc); in.dC = at(ws, w.oC + bc);
+      in.dB_stride_l = in.dC_stride_l = G * w.ni;
+      in.dB_stride_b = in.dC_stride_b = L * G * w.ni;
+    } else {
+      in.dB = at(a->dB, q * w.ni * es); in.dC = at(a->dC, q * w.ni * es);
+    }
+    if (q > 0) {
+      in.dx = at(ws, w.oX2); in.dx_stride_h = P; in.dx_stride_l = H * P; in.dx_stride_b = L * H * P;
+      in.ddt = reinterpret_cast<float*>(at(ws, w.oT2)); in.ddt_stride_l = H; in.ddt_stride_b = L * H;
+      in.dA = reinterpret_cast<float*>(at(ws, w.oH3));
+      in.dD = nullptr;
+      if (a->d_dt_bias) in.d_dt_bias = reinterpret_cast<float*>(at(ws, w.oH3)) + H;
+    }
+    in.workspace = ws; in.workspace_bytes = w.inner;
+    const int rc = ssd_bwd_validate(&in);
+    if (rc) return rc;
+    if (w.copy_bc && L > 0) {
+      e = mh::launch_col_copy(bc_in(f, f->B, f->B_stride_b, f->B_stride_l, at(ws, w.oB), w.ni, q), st);
+      if (e == hipSuccess) e = mh::launch_col_copy(bc_in(f, f->C, f->C_stride_b, f->C_stride_l, at(ws, w.oC), w.ni, q), st);
+    }
+    if (e == hipSuccess && f->initial_state) e = mh::launch_col_copy(state_in(f, f->initial_state, at(ws, w.oS0), w.ni, q), st);
+    if (e == hipSuccess && a->d_final_state) e = mh::launch_col_copy(state_in(f, a->d_final_state, at(ws, w.oS1), w.ni, q), st);
+    if (e == hipSuccess) e = ssd_launch_bwd_native(&in, st);
+    if (e == hipSuccess && w.copy_bc && L > 0) {
+      e = mh::launch_col_copy(bc_out(f, at(ws, w.oB + bc), a->dB, a->dB_stride_b, a->dB_stride_l, w.ni, q), st);
+      if (e == hipSuccess) e = mh::launch_col_copy(bc_out(f, at(ws, w.oC + bc), a->dC, a->dC_stride_b, a->dC_stride_l, w.ni, q), st);
+    }
+    if (e == hipSuccess && a->d_initial_state) e = mh::launch_col_copy(state_out(f, at(ws, w.oH2), a->d_initial_state, w.ni, q), st);
+  }
+  if (e == hipSuccess && w.pieces == 2) {
+    mh::RowAdd r{};
+    r.es = es; r.d0 = b; r.d1 = L; r.d2 = H; r.ncols = P;
+    r.dst = a->dx; r.t0 = a->dx_stride_b; r.t1 = a->dx_stride_l; r.t2 = a->dx_stride_h;
+    r.src = at(ws, w.oX2); r.s2 = P; r.s1 = H * P; r.s0 = L * H * P;
+    e = mh::launch_row_add(r, st);
+    if (e == hipSuccess) {
+      mh::RowAdd t{};
+      t.es = 4; t.d0 = b; t.d1 = L; t.d2 = 1; t.ncols = H;
+      t.dst = a->ddt; t.t0 = a->ddt_stride_b; t.t1 = a->ddt_stride_l;
+      t.src = at(ws, w.oT2); t.s0 = L * H; t.s1 = H;
+      e = mh::launch_row_add(t, st);
+    }
+    for (int k = 0; k < 2 && e == hipSuccess; ++k) {
+      float* dst = k == 0 ? a->dA : a->d_dt_bias;
+      if (!dst) continue;
+      mh::RowAdd t{};
+      t.es = 4; t.d0 = t.d1 = t.d2 = 1; t.ncols = H;
+      t.dst = dst; t.src = reinterpret_cast<float*>(at(ws, w.oH3)) + k * H;
+      e = mh::launch_row_add(t, st);
+    }
+  }
+  return hip_status(e, "ssd_chunk_scan_bwd");
+}
+
+// Workspace bytes of the forward (validated arguments, resolved chunk length) and of the backward.
+size_t ssd_fwd_need(const mh_ssd_args* a, int64_t cl) {
+  if (!ssd_native_dstate(a->dstate)) {
+    SsdWide w;
+    ssd_wide_fwd_plan(a, cl, w);
+    return w.total;
+  }
+  const int64_t nchunks = (a->seqlen + cl - 1) / cl;
+  return nchunks > 0 ? mh::ssd_workspace_bytes((int)a->batch, (int)a->seqlen, (int)nchunks, (int)a->nheads,
+                                               (int)a->headdim, (int)a->dstate, (int)a->ngroups, a->dtype) : 0;
+}
+size_t ssd_bwd_need(const mh_ssd_bwd_args* a) {
+  const mh_ssd_args* f = &a->fwd;
+  if (!ssd_native_dstate(f->dstate)) {
+    SsdWide w;
+    ssd_wide_bwd_plan(a, w);
+    return w.total;
+  }
+  return f->seqlen > 0 ? mh::ssd_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate,
+                                                     (int)f->ngroups, f->dtype, ssd_bwd_heads_per_wg(f)) : 0;
+}
+
 int conv_bwd_validate(const mh_conv1d_bwd_args* a) {
   if (!a) return fail(MH_ERR_NULL, "conv1d_bwd: args is NULL");
   mh_conv1d_args f = a->fwd;
@@ -409,9 +696,7 @@ int mh_ssd_workspace_bytes(const mh_ssd_args* a, size_t* bytes) {
   int64_t cl = 0;
   int rc = ssd_validate(a, &cl);
   if (rc) return rc;
-  const int64_t nchunks = (a->seqlen + cl - 1) / cl;
-  *bytes = mh::ssd_workspace_bytes((int)a->batch, (int)a->seqlen, (int)nchunks, (int)a->nheads, (int)a->headdim,
-                                   (int)a->dstate, (int)a->ngroups, a->dtype);
+  *bytes = ssd_fwd_need(a, cl);
   return MH_OK;
 }
 
@@ -419,21 +704,20 @@ int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream) {
   int64_t cl = 0;
   int rc = ssd_validate(a, &cl);
   if (rc) return rc;
-  const int64_t nchunks = (a->seqlen + cl - 1) / cl;
-  const size_t need = mh::ssd_workspace_bytes((int)a->batch, (int)a->seqlen, (int)nchunks, (int)a->nheads,
-                                              (int)a->headdim, (int)a->dstate, (int)a->ngroups, a->dtype);
-  if (nchunks > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+  const size_t need = ssd_fwd_need(a, cl);
+  if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
     return fail(MH_ERR_WORKSPACE, "ssd: workspace of %zu bytes (16-byte aligned) required, got %zu", need, a->workspace_bytes);
-  mh::SsdParams p;
-  ssd_fill(a, cl, nchunks, p);
-  if (nchunks > 0) mh::ssd_workspace_layout(p, a->workspace);
-  return hip_status(mh::launch_ssd(p, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_fwd");
+  if (!ssd_native_dstate(a->dstate)) return ssd_fwd_wide(a, cl, reinterpret_cast<hipStream_t>(stream));
+  return hip_status(ssd_launch_native(a, cl, a->workspace, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_fwd");
 }
 
 int mh_ssd_chunk_scan_fwd_noalloc(const mh_ssd_args* a, void* stream) {
   int64_t cl = 0;
   int rc = ssd_validate(a, &cl);
   if (rc) return rc;
+  if (!ssd_native_dstate(a->dstate))
+    return fail(MH_ERR_UNSUPPORTED, "ssd_noalloc: dstate %lld runs as a composition of 64/128-column scans that needs "
+                "a caller workspace (call mh_ssd_chunk_scan_fwd)", (long long)a->dstate);
   const int64_t nchunks = (a->seqlen + cl - 1) / cl;
   const size_t need = mh::ssd_workspace_bytes((int)a->batch, (int)a->seqlen, (int)nchunks, (int)a->nheads,
                                               (int)a->headdim, (int)a->dstate, (int)a->ngroups, a->dtype);
@@ -571,9 +855,7 @@ int mh_ssd_bwd_workspace_bytes(const mh_ssd_bwd_args* a, size_t* bytes) {
   if (!bytes) return fail(MH_ERR_NULL, "ssd_bwd: bytes output is NULL");
   int rc = ssd_bwd_validate(a);
   if (rc) return rc;
-  const mh_ssd_args* f = &a->fwd;
-  *bytes = mh::ssd_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate,
-                                       (int)f->ngroups, f->dtype, ssd_bwd_heads_per_wg(f));
+  *bytes = ssd_bwd_need(a);
   return MH_OK;
 }
 
@@ -581,28 +863,12 @@ int mh_ssd_chunk_scan_bwd(const mh_ssd_bwd_args* a, void* stream) {
   int rc = ssd_bwd_validate(a);
   if (rc) return rc;
   const mh_ssd_args* f = &a->fwd;
-  const size_t need = mh::ssd_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate,
-                                                  (int)f->ngroups, f->dtype, ssd_bwd_heads_per_wg(f));
-  if (f->seqlen > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+  const size_t need = ssd_bwd_need(a);
+  if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
     return fail(MH_ERR_WORKSPACE, "ssd_bwd: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
                 a->workspace_bytes);
-  mh::SsdBwdParams q;
-  memset(&q, 0, sizeof(q));
-  const int64_t nseg = (f->seqlen + 63) / 64;
-  ssd_fill(f, 64, nseg, q.f);
-  q.f.y = nullptr;
-  q.f.final_state = nullptr;
-  q.f.z = nullptr;
-  q.dy = a->dy; q.dy_sb = a->dy_stride_b; q.dy_sl = a->dy_stride_l; q.dy_sh = a->dy_stride_h;
-  q.d_final = a->d_final_state;
-  q.dx = a->dx; q.dx_sb = a->dx_stride_b; q.dx_sl = a->dx_stride_l; q.dx_sh = a->dx_stride_h;
-  q.ddt = a->ddt; q.ddt_sb = a->ddt_stride_b; q.ddt_sl = a->ddt_stride_l;
-  q.dA = a->dA; q.dD = f->D ? a->dD : nullptr; q.dbias = a->d_dt_bias; q.dh0 = a->d_initial_state;
-  q.dB = a->dB; q.dB_sb = a->dB_stride_b; q.dB_sl = a->dB_stride_l;
-  q.dC = a->dC; q.dC_sb = a->dC_stride_b; q.dC_sl = a->dC_stride_l;
-  q.heads_per_wg = ssd_bwd_heads_per_wg(f);
-  if (nseg > 0) mh::ssd_bwd_workspace_layout(q, a->workspace);
-  return hip_status(mh::launch_ssd_bwd(q, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_bwd");
+  if (!ssd_native_dstate(f->dstate)) return ssd_bwd_wide(a, reinterpret_cast<hipStream_t>(stream));
+  return hip_status(ssd_launch_bwd_native(a, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_bwd");
 }
 
 }  // extern "C"

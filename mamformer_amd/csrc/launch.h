@@ -170,4 +170,24 @@ hipError_t launch_conv1d_bwd(const Conv1dBwdParams& q, hipStream_t st);
 size_t conv1d_bwd_workspace_bytes(int batch, int seqlen, int dim, int width);
 void conv1d_bwd_workspace_layout(Conv1dBwdParams& q, void* workspace);
 
+// ------------------------------------------------------------- widening helpers (widen.hip)
+// dst[i0,i1,i2][tcol0 + c] = c < nvalid ? src[i0,i1,i2][scol0 + c] : 0   for c < ncols
+// (element offsets: i0 * s0 + i1 * s1 + i2 * s2 for the source, t0..t2 for the destination).
+struct ColCopy {
+  int es;                      // element size: 2 (bf16) or 4 (fp32)
+  int64_t d0, d1, d2, ncols, nvalid;
+  const void* src; int64_t s0, s1, s2, scol0;
+  void* dst; int64_t t0, t1, t2, tcol0;
+};
+hipError_t launch_col_copy(const ColCopy& c, hipStream_t st);
+// dst[row][c] = (dst[row][c] + src[row][c]) * (gate ? silu(gate[row][c]) : 1), summed in fp32.
+struct RowAdd {
+  int es;
+  int64_t d0, d1, d2, ncols;
+  void* dst; int64_t t0, t1, t2;
+  const void* src; int64_t s0, s1, s2;
+  const void* gate; int64_t g0, g1, g2;
+};
+hipError_t launch_row_add(const RowAdd& a, hipStream_t st);
+
 }  // namespace mh

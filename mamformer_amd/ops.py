@@ -423,8 +423,14 @@ def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, 
     """
     b, L, H, P = x4.shape
     G, N = B4.shape[2], B4.shape[3]
-    if P != 64 or N % 64:
-        raise NotImplementedError("selective_scan: return_h_states needs headdim 64 and dstate a multiple of 64")
+    if P != 64:
+        raise NotImplementedError("selective_scan: return_h_states needs headdim 64")
+    if N % 64:                            # zero-padded state columns beyond N stay zero
+        pad = 64 - N % 64
+        B4 = torch.nn.functional.pad(B4, (0, pad))
+        h0 = None if h0 is None else torch.nn.functional.pad(h0, (0, pad))
+        hs = _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad)
+        return hs[..., :N]
     Q = N // 64
     gidx = torch.arange(H, device=x4.device) // (H // G)
     xs = B4[:, :, gidx, :].reshape(b, L, H * Q, 64).contiguous()                # x'

@@ -64,7 +64,7 @@ def test_ssd_workspace_and_chunk_len():
 
 
 @pytest.mark.parametrize("field,value,code", [
-    ("headdim", 32, -6), ("dstate", 96, -6), ("dtype", 7, -3), ("ngroups", 3, -2), ("batch", 0, -2),
+    ("headdim", 32, -6), ("dstate", 100, -6), ("dstate", 264, -6), ("dtype", 7, -3), ("ngroups", 3, -2), ("batch", 0, -2),
     ("chunk_len", 100, -2), ("x_stride_l", 8 * 64 + 1, -5), ("B_stride_l", 64, -4),
 ])
 def test_ssd_rejects_bad_arguments(field, value, code):
@@ -73,6 +73,29 @@ def test_ssd_rejects_bad_arguments(field, value, code):
     n = ct.c_size_t()
     assert _rc("mh_ssd_workspace_bytes", ct.byref(a), ct.byref(n)) == code
     assert _lib.lib().mh_last_error()
+
+
+@pytest.mark.parametrize("N", [8, 16, 32, 96, 200, 256])
+def test_ssd_composed_dstate_workspace(N):
+    """dstate outside the 64 / 128 tiles is accepted; its workspace holds an inner run's plus the pieces of B, C
+    and the states; the no-allocation entry point declines it (MH_ERR_UNSUPPORTED) before any HIP call."""
+    a = _good_ssd()
+    G, L, b = a.ngroups, a.seqlen, a.batch
+    a.dstate = N
+    a.B_stride_l = a.C_stride_l = G * N
+    a.B_stride_b = a.C_stride_b = L * G * N
+    n = ct.c_size_t()
+    assert _rc("mh_ssd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+    ni = 64 if N <= 64 else 128
+    a2 = _good_ssd()
+    a2.dstate = ni
+    a2.B_stride_l = a2.C_stride_l = G * ni
+    a2.B_stride_b = a2.C_stride_b = L * G * ni
+    n2 = ct.c_size_t()
+    assert _rc("mh_ssd_workspace_bytes", ct.byref(a2), ct.byref(n2)) == 0
+    assert n.value >= n2.value + 2 * b * L * G * ni * 2       # inner run + B and C pieces (bf16)
+    assert _rc("mh_ssd_chunk_scan_fwd_noalloc", ct.byref(a), None) == -6
+    assert b"composition" in _lib.lib().mh_last_error()
 
 
 def test_ssd_rejects_null_and_misaligned_pointers_and_small_workspace():
@@ -304,7 +327,7 @@ def test_ssd_bwd_workspace_and_validation():
     (lambda a: setattr(a, "dB", ct.c_void_p(8192 + 4)), -5, b"aligned"),
     (lambda a: setattr(a, "dx_stride_h", 32), -4, b"head stride"),
     (lambda a: setattr(a, "dC_stride_l", 64), -4, b"token stride"),
-    (lambda a: setattr(a.fwd, "dstate", 96), -6, b"dstate"),
+    (lambda a: setattr(a.fwd, "dstate", 100), -6, b"dstate"),
 ])
 def test_ssd_bwd_rejects_bad_arguments(mutate, code, word):
     a = _good_bwd()

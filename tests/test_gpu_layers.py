@@ -91,7 +91,8 @@ def _scan_recurrence_f64(x, dt_raw, A, B, C, D, bias, h0):
 
 
 @pytest.mark.parametrize("dtype,G,N,h0", [(torch.float32, 1, 64, False), (torch.float32, 2, 128, True),
-                                          (torch.bfloat16, 1, 128, True)])
+                                          (torch.bfloat16, 1, 128, True), (torch.float32, 1, 32, True),
+                                          (torch.float32, 2, 256, False)])
 def test_h_states_autograd_vs_recurrence(dtype, G, N, h0):
     """selective_scan(return_h_states=True) under autograd (the path Mamba2Layer trains through with
     return_h_states, hybrid.py:383-395): every input gradient of <wy, y> + <wh, h_states> + <wf, final_state>
@@ -160,7 +161,7 @@ def _layer_ref(layer, u, cache=None):
     return out, fin.reshape(b, H * Pd, N), hs, x
 
 
-@pytest.mark.parametrize("G,N", [(1, 64), (2, 128)])
+@pytest.mark.parametrize("G,N", [(1, 64), (2, 128), (1, 16), (2, 32), (1, 256)])
 def test_mamba2_layer_forward_vs_oracle(G, N):
     torch.manual_seed(11)
     layer = Mamba2Layer(256, d_state=N, expand=1, headdim=64, ngroups=G, device="cuda", dtype=torch.float32)

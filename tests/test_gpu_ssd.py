@@ -182,6 +182,43 @@ def test_ssd_output_gate_vs_oracle(dtype, L, H, N, chunk):
     assert torch.equal(y3.view(b, L, H, P), y)
 
 
+@pytest.mark.parametrize("N,G,dtype,h0,gate,dmode", [
+    (16, 1, torch.bfloat16, False, False, "head"),       # the reference's scan fixture (tests/test_mamba2.py:22-30)
+    (8, 1, torch.float32, True, False, "head"),          # its per-seqlen case (tests/test_mamba2.py:74-80)
+    (32, 2, torch.float32, True, True, "channel"),       # the debug preset's d_state
+    (96, 1, torch.bfloat16, True, False, None),          # padded to 128
+    (256, 1, torch.bfloat16, True, True, "head"),        # two halves, B / C halves read in place
+    (256, 2, torch.float32, True, True, "channel"),      # two halves through the workspace
+    (200, 1, torch.float32, False, False, "head"),       # two halves, the second padded
+], ids=lambda v: str(v).replace("torch.", ""))
+def test_ssd_composed_dstate_vs_oracle(N, G, dtype, h0, gate, dmode):
+    """dstate outside the kernels' 64 / 128 tiles: zero-padded or split into 128-column halves by the C ABI.
+    y (gated or not), the final state and an initial state against the direct float64 recurrence."""
+    g = torch.Generator().manual_seed(N * 7 + G)
+    b, L, H, P = 2, 203, 4, 64
+    x = torch.randn(b, L, H, P, generator=g).to(dtype)
+    B = torch.randn(b, L, G, N, generator=g).to(dtype)
+    C = torch.randn(b, L, G, N, generator=g).to(dtype)
+    dt = torch.rand(b, L, H, generator=g) * 0.2 + 0.01
+    A = -torch.exp(torch.rand(H, generator=g) * 2.0)
+    D = None if dmode is None else torch.randn(H if dmode == "head" else H * P, generator=g)
+    s0 = 0.3 * torch.randn(b, H, P, N, generator=g) if h0 else None
+    z = torch.randn(b, L, H, P, generator=g).to(dtype) if gate else None
+    say(f"composed dstate N={N} G={G} {dtype} h0={h0} gate={gate} D={dmode}")
+    y, fin = mh.selective_scan(dev(x, dtype), dev(dt), dev(A), dev(B, dtype), dev(C, dtype), dev(D),
+                               return_final_state=True, initial_state=dev(s0), z=dev(z, dtype), chunk_size=64)
+    torch.cuda.synchronize()
+    y_ref, f_ref = ref.ssd_direct(x.double().numpy(), dt.double().numpy(), A.double().numpy(), B.double().numpy(),
+                                  C.double().numpy(), None if D is None else D.double().numpy(),
+                                  initial_state=None if s0 is None else s0.double().numpy())
+    if gate:
+        zr = z.double().numpy()
+        y_ref = y_ref * (zr / (1.0 + np.exp(-zr)))
+    check("y", y, y_ref, TOL[dtype])
+    check("final", fin, f_ref, TOL[dtype])
+    assert fin.shape == (b, H, P, N)
+
+
 def test_ssd_empty_sequence():
     h0 = torch.randn(1, 4, 64, 64, device="cuda")
     x = torch.zeros(1, 0, 4, 64, device="cuda")

@@ -79,6 +79,14 @@ CASES = [
     (1, 7, 2, 64, 1, torch.float32, True, True, False, None, "channel", 6),
     (1, 65, 16, 128, 2, torch.bfloat16, False, True, True, None, "head", 7),
     (1, 320, 16, 64, 4, torch.float32, True, False, True, None, "head", 8),
+    # dstate outside the 64 / 128 tiles (composed by the C ABI: zero-padded, or two 128-column halves)
+    (2, 32, 4, 16, 1, torch.float32, True, True, True, None, "head", 9),       # the reference fixture's sizes
+    (1, 150, 4, 32, 2, torch.bfloat16, True, True, True, None, "channel", 10),
+    (1, 99, 2, 8, 1, torch.float32, False, True, False, None, "head", 11),
+    (1, 140, 4, 256, 1, torch.bfloat16, True, True, True, None, "head", 12),  # halves read in place
+    (1, 70, 4, 256, 2, torch.float32, True, True, True, (0.05, 0.4), "channel", 13),
+    (1, 66, 2, 200, 1, torch.float32, True, False, True, None, None, 14),     # second half padded
+    (1, 130, 2, 96, 2, torch.float32, False, True, True, None, "head", 15),
 ]
 
 
@@ -147,6 +155,22 @@ def test_bwd_empty_sequence():
                               dev(np.ones(H)), d_final_state=dev(dfin), dt_bias=dev(np.zeros(H)), dt_softplus=True)
     torch.cuda.synchronize()
     assert g["dx"].shape == x.shape and g["dB"].shape == B.shape
+    assert float(g["dA"].abs().max()) == 0.0 and float(g["dD"].abs().max()) == 0.0
+    assert float(g["d_dt_bias"].abs().max()) == 0.0
+    assert np.array_equal(host(g["d_initial_state"]), dfin.astype(np.float32).astype(np.float64))
+
+
+@pytest.mark.parametrize("N", [32, 256])
+def test_bwd_empty_sequence_composed(N):
+    """L = 0 through the composed paths: d_initial_state = d_final_state column for column, zero dA / dD."""
+    say(f"bwd L=0 N={N}")
+    b, H = 1, 2
+    dfin = np.random.default_rng(N).standard_normal((b, H, 64, N))
+    x = torch.zeros((b, 0, H, 64), device="cuda", dtype=torch.float32)
+    B = torch.zeros((b, 0, 1, N), device="cuda", dtype=torch.float32)
+    g = mh.selective_scan_bwd(x, x, torch.zeros((b, 0, H), device="cuda"), dev(-np.ones(H)), B, B,
+                              dev(np.ones(H)), d_final_state=dev(dfin), dt_bias=dev(np.zeros(H)), dt_softplus=True)
+    torch.cuda.synchronize()
     assert float(g["dA"].abs().max()) == 0.0 and float(g["dD"].abs().max()) == 0.0
     assert float(g["d_dt_bias"].abs().max()) == 0.0
     assert np.array_equal(host(g["d_initial_state"]), dfin.astype(np.float32).astype(np.float64))
