@@ -182,7 +182,9 @@ int mh_ssd_state_update(const mh_ssu_args* a, void* stream);
  *   and LinearDiffAttention._linear_attention_scan
  *   (mamformer/layers/kda_diff.py:357-478): writes o1 and o2 separately.
  * initial_state / final_state (B,H,dk,dv) fp32 may be NULL.
- * Supported: dk = dv = 128.
+ * Supported: dtype bf16 or fp32 (q, k, v, o share it), dk and dv each 64 or 128.  bf16 with
+ *   dk = dv = 128 runs the bf16-MFMA kernels; every other combination runs kernels whose
+ *   products are fp32 MFMA (fp32-accurate, for the fp32 I/O tolerance of 1e-4).
  * ---------------------------------------------------------------------- */
 enum { MH_KDA_GATED = 0, MH_KDA_REFERENCE = 1 };
 
@@ -215,9 +217,9 @@ int mh_kda_chunk_scan_fwd(const mh_kda_args* a, void* stream);
  *   otherwise do1 / do2 are the gradients of o1 / o2 (do2 NULL = zero).
  *   d_final_state (B,H,dk,dv) / d_final_z (B,H,dk) fp32: gradients of the final
  *   state and normaliser, or NULL (zero).
- *   Outputs dq1, dq2 (when q2), dk, dv (B,H,S,128) bf16 (zero beyond kernel_dim
+ *   Outputs dq1, dq2 (when q2), dk, dv (B,H,S,dk / dv) in the I/O dtype (zero beyond kernel_dim
  *   for dq, dk); d_initial_state / d_initial_z fp32 or NULL.
- *   Supported: bf16, dk = dv = 128.
+ *   Supported: as the forward (bf16 or fp32, dk and dv each 64 or 128).
  * ---------------------------------------------------------------------- */
 enum { MH_KDA_BWD_DIFF = 1 };
 

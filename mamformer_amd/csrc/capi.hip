@@ -157,10 +157,10 @@ int kda_validate(const mh_kda_args* a) {
     return fail(MH_ERR_SHAPE, "kda: sizes must be positive");
   if (a->batch * a->nheads > 0x7fffffffLL || a->seqlen > kMaxDim) return fail(MH_ERR_SHAPE, "kda: sizes out of range");
   if (!elem_size(a->dtype)) return fail(MH_ERR_DTYPE, "kda: unknown dtype %d", a->dtype);
-  if (a->dtype != MH_BF16) return fail(MH_ERR_UNSUPPORTED, "kda: only bf16 q/k/v/o are supported");
   if (a->mode != MH_KDA_GATED && a->mode != MH_KDA_REFERENCE) return fail(MH_ERR_UNSUPPORTED, "kda: unknown mode %d", a->mode);
-  if (a->dk != 128 || a->dv != 128)
-    return fail(MH_ERR_UNSUPPORTED, "kda: dk=%lld dv=%lld not supported (128, 128)", (long long)a->dk, (long long)a->dv);
+  if ((a->dk != 64 && a->dk != 128) || (a->dv != 64 && a->dv != 128))
+    return fail(MH_ERR_UNSUPPORTED, "kda: dk=%lld dv=%lld not supported (each 64 or 128)", (long long)a->dk,
+                (long long)a->dv);
   if (a->seqlen > 0 && (!a->q1 || !a->k || !a->v || !a->o))
     return fail(MH_ERR_NULL, "kda: q1, k, v, o are required");
   if (a->mode == MH_KDA_REFERENCE) {

@@ -816,8 +816,11 @@ hipError_t launch_kda_bwd(const KdaBwdParams& q, hipStream_t st) {
   const KdaParams& p = q.f;
   const int nbh = p.batch * p.nheads;
   if (p.seqlen == 0) {
-    const size_t ns = (size_t)nbh * BD * BD, nz = (size_t)nbh * BD;
+    const size_t ns = (size_t)nbh * p.dk * p.dv, nz = (size_t)nbh * p.dk;
     hipLaunchKernelGGL(kda_ref_bwd_empty_kernel, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, st, q, ns, nz);
+  } else if (kda_precise_path(p)) {
+    hipError_t e = launch_kda_bwd_precise(q, st);
+    if (e != hipSuccess) return e;
   } else {
     hipLaunchKernelGGL(kda_ref_bwd_q_kernel, dim3((unsigned)nbh, (unsigned)q.nq), dim3(NT), 0, st, q);
     hipError_t e = hipGetLastError();

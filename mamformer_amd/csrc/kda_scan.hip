@@ -744,13 +744,13 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
 hipError_t launch_kda(const KdaParams& p, hipStream_t st) {
   const int nbh = p.batch * p.nheads;
   if (p.seqlen == 0) {
-    const size_t ns = p.final_state ? (size_t)nbh * DK * 128 : 0, nz = p.final_z ? (size_t)nbh * DK : 0;
+    const size_t ns = p.final_state ? (size_t)nbh * p.dk * p.dv : 0, nz = p.final_z ? (size_t)nbh * p.dk : 0;
     const size_t n = ns > nz ? ns : nz;
     if (n) hipLaunchKernelGGL(kda_empty_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p.init_state,
                               p.final_state, ns, p.init_z, p.final_z, nz);
     return hipGetLastError();
   }
-  if (p.dtype != DT_BF16) return hipErrorInvalidValue;
+  if (kda_precise_path(p)) return launch_kda_precise(p, st);
   const dim3 grid((unsigned)(2 * nbh));
   if (p.mode == 0) {
     hipLaunchKernelGGL(kda_gated_kernel, grid, dim3(64 * KW), 0, st, p);

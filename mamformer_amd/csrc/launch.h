@@ -113,10 +113,10 @@ struct KdaBwdParams {
   KdaParams f;               // forward inputs (mode 1; o, o2, final_state, final_z unused)
   int nq;                    // query streams (1 or 2)
   int diff;                  // 1: do1 is the gradient of the fused (o1 - lam o2) / (1 - lam + 1e-8)
-  const void* do1; const void* do2;     // (B,H,S,dv) bf16; null = zero
+  const void* do1; const void* do2;     // (B,H,S,dv) in the I/O dtype; null = zero
   const float* d_final;      // (B,H,dk,dv) gradient of the final state, or null
   const float* d_final_z;    // (B,H,dk) gradient of the final normaliser, or null
-  void* dq1; void* dq2; void* dk; void* dv;   // (B,H,S,128) bf16
+  void* dq1; void* dq2; void* dk; void* dv;   // (B,H,S,dk) / (B,H,S,dv) in the I/O dtype
   float* dS0;                // (B,H,dk,dv) or null
   float* dz0;                // (B,H,dk) or null
   float* dlam;               // (H,) or null (diff mode)
@@ -126,6 +126,11 @@ struct KdaBwdParams {
   int nseg, seg_chunks;      // kv-walk segments per (b, h) and 64-token chunks per segment
 };
 hipError_t launch_kda_bwd(const KdaBwdParams& q, hipStream_t st);
+// fp32-arithmetic kernels (kda_precise.hip) for everything but bf16 with dk = dv = 128; launch_kda and
+// launch_kda_bwd route there.
+bool kda_precise_path(const KdaParams& p);
+hipError_t launch_kda_precise(const KdaParams& p, hipStream_t st);
+hipError_t launch_kda_bwd_precise(const KdaBwdParams& q, hipStream_t st);
 size_t kda_bwd_workspace_bytes(int batch, int nheads, int seqlen, int nq);
 void kda_bwd_workspace_layout(KdaBwdParams& q, void* workspace);
 

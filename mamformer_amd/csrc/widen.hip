@@ -9,8 +9,6 @@
 //     per state column given dt and A, so y = y(half 0) + y(half 1) with D
 //     applied in one of them, the gate after the sum, and the gradients of
 //     dt, A, dt_bias and x summed over the halves.
-//   * KDA head size 64: q, k (and g) zero-padded to 128 channels and v to 128
-//     columns (kda_* entry points).
 // col_copy moves a column window of a 3-level row set (zero-filling columns
 // beyond the source window); row_add adds one such row set into another,
 // optionally multiplying by silu(gate) as it stores.

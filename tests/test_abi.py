@@ -184,14 +184,16 @@ def test_kda_rejects_bad_arguments():
     a.batch, a.nheads, a.seqlen, a.dk, a.dv = 1, 2, 10, 128, 128
     a.dtype = _lib.MH_BF16
     a.q1 = a.q2 = a.k = a.v = a.o = ct.c_void_p(4096)
-    a.dk = 64
+    a.dk = 96                             # head sizes 64 and 128 (each of dk, dv) only
     assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -6
-    a.dk = 128
+    a.dk, a.dv = 128, 256
+    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -6
+    a.dv = 128
     a.v = None
     assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -1
     a.v = ct.c_void_p(4096)
-    a.dtype = _lib.MH_F32
-    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -6
+    a.dtype = 5
+    assert _rc("mh_kda_chunk_scan_fwd", ct.byref(a), None) == -3
 
 
 def test_ops_refuse_cpu_tensors():
@@ -423,7 +425,7 @@ def test_kda_bwd_workspace():
     (lambda a: setattr(a, "do2", ct.c_void_p(4096)), -2, b"do2"),
     (lambda a: setattr(a, "flags", 6), -6, b"flags"),
     (lambda a: setattr(a, "dv", ct.c_void_p(8192 + 8)), -5, b"aligned"),
-    (lambda a: setattr(a.fwd, "dk", 64), -6, b"dk"),
+    (lambda a: setattr(a.fwd, "dk", 96), -6, b"dk"),
 ])
 def test_kda_bwd_rejects_bad_arguments(mutate, code, word):
     a = _good_kda_bwd()
