@@ -53,7 +53,9 @@ enum {
 enum {
   MH_DT_SOFTPLUS = 1,      /* dt <- softplus(dt + dt_bias)   (mamba2.py:293, 304) */
   MH_DT_LIMIT = 2,         /* dt <- clamp(dt, dt_min, dt_max) after softplus */
-  MH_D_PER_CHANNEL = 4     /* D has nheads*headdim entries instead of nheads */
+  MH_D_PER_CHANNEL = 4,    /* D has nheads*headdim entries instead of nheads */
+  MH_A_PER_STATE = 8,      /* decode only: A has dstate entries, one per state column (dA[p, n] = exp(A[n] dt)) */
+  MH_DT_PER_CHANNEL = 16   /* decode only: dt (and dt_bias) have nheads*headdim entries, one per channel */
 };
 
 /* ------------------------------------------------------------------------
@@ -148,7 +150,10 @@ int mh_ssd_chunk_scan_bwd(const mh_ssd_bwd_args* a, void* stream);
  *   state (b, H, P, N) fp32 read from state_in and written to state_out (the
  *   two may alias: in-place update), x (b, H, P), dt (b, H) fp32 raw (bias,
  *   softplus and clamp applied per flags), A (H,), B/C (b, G, N), D, y (b, H, P).
- *   Supported: N in {16, 32, 64, 128, 256}, H % G == 0.
+ *   The reference's own parameterisation (a decay rate per state column, -exp(A_log) (N,), and a step
+ *   size per channel, dt (b, d_inner), mamba2.py:440-446) is the flags MH_A_PER_STATE (A holds N
+ *   entries) and MH_DT_PER_CHANNEL (dt and dt_bias hold H*P entries per row, d_inner = H*P).
+ *   Supported: N in {8, 16, 32, 64, 128, 256}, H % G == 0.
  * ---------------------------------------------------------------------- */
 typedef struct {
   int64_t batch, nheads, headdim, dstate, ngroups;

@@ -18,7 +18,7 @@ ABI_VERSION = 6
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
 MH_F32, MH_BF16 = 0, 1
-MH_DT_SOFTPLUS, MH_DT_LIMIT, MH_D_PER_CHANNEL = 1, 2, 4
+MH_DT_SOFTPLUS, MH_DT_LIMIT, MH_D_PER_CHANNEL, MH_A_PER_STATE, MH_DT_PER_CHANNEL = 1, 2, 4, 8, 16
 MH_KDA_GATED, MH_KDA_REFERENCE = 0, 1
 MH_KDA_PHI = 1
 

@@ -80,6 +80,9 @@ int ssd_validate(const mh_ssd_args* a, int64_t* chunk_len_out) {
     return fail(MH_ERR_SHAPE, "ssd: chunk_len %lld must be a positive multiple of 64", (long long)a->chunk_len);
   if ((a->flags & MH_DT_LIMIT) && !(a->dt_min <= a->dt_max))
     return fail(MH_ERR_SHAPE, "ssd: dt_min > dt_max");
+  if (a->flags & (MH_A_PER_STATE | MH_DT_PER_CHANNEL))
+    return fail(MH_ERR_UNSUPPORTED, "ssd: MH_A_PER_STATE / MH_DT_PER_CHANNEL are decode-step flags (the chunked "
+                                    "scan factorises a per-head decay)");
   if (!a->A) return fail(MH_ERR_NULL, "ssd: A is required");
   if (a->seqlen > 0 && (!a->x || !a->dt || !a->B || !a->C || !a->y))
     return fail(MH_ERR_NULL, "ssd: x, dt, A, B, C, y are required");
@@ -127,8 +130,8 @@ int ssu_validate(const mh_ssu_args* a) {
   const int es = elem_size(a->dtype);
   if (!es) return fail(MH_ERR_DTYPE, "state_update: unknown dtype %d", a->dtype);
   switch (a->dstate) {
-    case 16: case 32: case 64: case 128: case 256: break;
-    default: return fail(MH_ERR_UNSUPPORTED, "state_update: dstate %lld not supported (16..256, power of two)",
+    case 8: case 16: case 32: case 64: case 128: case 256: break;
+    default: return fail(MH_ERR_UNSUPPORTED, "state_update: dstate %lld not supported (8..256, power of two)",
                          (long long)a->dstate);
   }
   if ((a->flags & MH_DT_LIMIT) && !(a->dt_min <= a->dt_max)) return fail(MH_ERR_SHAPE, "state_update: dt_min > dt_max");
@@ -139,7 +142,8 @@ int ssu_validate(const mh_ssu_args* a) {
   if (a->z && a->z_stride_b < a->nheads * a->headdim)
     return fail(MH_ERR_STRIDE, "state_update: z batch stride smaller than a row ((h, p) contiguous)");
   if (a->x_stride_b < a->nheads * a->headdim || a->y_stride_b < a->nheads * a->headdim ||
-      a->B_stride_b < a->ngroups * a->dstate || a->C_stride_b < a->ngroups * a->dstate || a->dt_stride_b < a->nheads)
+      a->B_stride_b < a->ngroups * a->dstate || a->C_stride_b < a->ngroups * a->dstate ||
+      a->dt_stride_b < ((a->flags & MH_DT_PER_CHANNEL) ? a->nheads * a->headdim : a->nheads))
     return fail(MH_ERR_STRIDE, "state_update: batch stride smaller than a row ((h, p) / (g, n) / h contiguous)");
   if (a->state_in != a->state_out) {
     const uintptr_t bytes = (uintptr_t)(a->batch * a->nheads * a->headdim * a->dstate * 4);
@@ -745,6 +749,8 @@ int mh_ssd_state_update(const mh_ssu_args* a, void* stream) {
   p.dt_softplus = (a->flags & MH_DT_SOFTPLUS) != 0;
   p.has_dt_limit = (a->flags & MH_DT_LIMIT) != 0;
   p.D_per_channel = (a->flags & MH_D_PER_CHANNEL) != 0;
+  p.A_per_state = (a->flags & MH_A_PER_STATE) != 0;
+  p.dt_per_channel = (a->flags & MH_DT_PER_CHANNEL) != 0;
   p.dt_min = a->dt_min; p.dt_max = a->dt_max;
   p.state_in = a->state_in; p.state_out = a->state_out;
   p.x = a->x; p.x_stride_b = a->x_stride_b;

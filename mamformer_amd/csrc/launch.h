@@ -13,6 +13,7 @@ enum { DT_F32 = 0, DT_BF16 = 1 };
 struct SsuParams {
   int batch, nheads, headdim, dstate, ngroups, dtype;
   int dt_softplus, has_dt_limit, D_per_channel;
+  int A_per_state, dt_per_channel;           // the reference's per-state A / per-channel dt
   float dt_min, dt_max;
   const float* state_in;
   float* state_out;

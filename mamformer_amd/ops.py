@@ -556,15 +556,16 @@ def plan_selective_state_update(*args, **kw):
 
 
 def selective_state_update(state, x, dt, A, B, C, D=None, *, dt_bias=None, dt_softplus=True, dt_limit=None,
-                           out_state=None, z=None, _plan_only=False):
+                           out_state=None, z=None, A_per_state=False, _plan_only=False):
     """One-token SSD state update on the GPU, in place by default.
 
     state (b, H, P, N) fp32 (updated in place unless ``out_state`` is given);
-    x (b, H, P); dt (b, H) raw (``dt_softplus``/``dt_bias``/``dt_limit`` applied
-    in the kernel, as the decode path of mamba2.py:293 does before the step);
-    A (H,); B, C (b, N) or (b, G, N); D (H,), (H, P) or None; optional gate z (b, H, P) like x:
-    y <- y * silu(z) (mamba2.py:337-338).  Returns y (b, H, P).
-    Semantics of ``Mamba2Block._recurrent_step`` (R/mamformer/layers/mamba2.py:431-458).
+    x (b, H, P); dt (b, H) raw, or (b, H, P) one step per channel (``dt_softplus``/``dt_bias``/``dt_limit``
+    applied in the kernel, as the decode path of mamba2.py:293 does before the step; dt_bias then (H*P,));
+    A (H,), or with ``A_per_state`` (N,) one decay rate per state column; B, C (b, N) or (b, G, N);
+    D (H,), (H, P) or None; optional gate z (b, H, P) like x: y <- y * silu(z) (mamba2.py:337-338).
+    Returns y (b, H, P).  Semantics of ``Mamba2Block._recurrent_step`` (R/mamformer/layers/mamba2.py:431-458);
+    with per-channel dt and per-state A it is the reference's own parameterisation.
     """
     _require_cuda("selective_state_update", state, x, dt, A, B, C, D, dt_bias, out_state, z)
     if state.dim() != 4 or state.dtype != torch.float32:
@@ -579,23 +580,24 @@ def selective_state_update(state, x, dt, A, B, C, D=None, *, dt_bias=None, dt_so
     if B3.shape[0] != b or B3.shape[2] != N or C3.shape != B3.shape:
         raise ValueError("selective_state_update: B/C must be (b, N) or (b, G, N)")
     G = B3.shape[1]
-    if dt.shape != (b, H):
-        raise ValueError(f"selective_state_update: dt must be {(b, H)}")
+    dt_chan = dt.dim() == 3
+    if dt.shape != ((b, H, P) if dt_chan else (b, H)):
+        raise ValueError(f"selective_state_update: dt must be {(b, H)} or {(b, H, P)}")
     if not state.is_contiguous():
         raise ValueError("selective_state_update: state must be contiguous (it is updated in place)")
     xs = x if (x.stride(-1) == 1 and x.stride(-2) == P) else x.contiguous()
     Bs = B3 if (B3.stride(-1) == 1 and B3.stride(-2) == N) else B3.contiguous()
     Cs = C3 if (C3.stride(-1) == 1 and C3.stride(-2) == N) else C3.contiguous()
-    if A.numel() != H:
-        raise ValueError(f"selective_state_update: A must have H = {H} entries")
+    if A.numel() != (N if A_per_state else H):
+        raise ValueError(f"selective_state_update: A must have {'N' if A_per_state else 'H'} entries")
     if D is not None and D.numel() not in (H, H * P):
         raise ValueError("selective_state_update: D must have H or H*P entries")
-    if dt_bias is not None and dt_bias.numel() != H:
-        raise ValueError(f"selective_state_update: dt_bias must have H = {H} entries")
+    if dt_bias is not None and dt_bias.numel() != (H * P if dt_chan else H):
+        raise ValueError(f"selective_state_update: dt_bias must have one entry per {'channel' if dt_chan else 'head'}")
     if H % G:
         raise ValueError("selective_state_update: nheads must be a multiple of ngroups")
     dt32 = dt.to(torch.float32)
-    if dt32.stride(-1) != 1:
+    if dt32.stride(-1) != 1 or (dt_chan and dt32.stride(-2) != P):
         dt32 = dt32.contiguous()
     A32, D32, bias32 = _f32c(A), _f32c(D.reshape(-1) if D is not None else None), _f32c(dt_bias)
     dst = state if out_state is None else out_state
@@ -616,6 +618,10 @@ def selective_state_update(state, x, dt, A, B, C, D=None, *, dt_bias=None, dt_so
         a.dt_min, a.dt_max = float(dt_limit[0]), float(dt_limit[1])
     if D32 is not None and D32.numel() == H * P and P != 1:
         flags |= _lib.MH_D_PER_CHANNEL
+    if A_per_state:
+        flags |= _lib.MH_A_PER_STATE
+    if dt_chan:
+        flags |= _lib.MH_DT_PER_CHANNEL
     a.flags = flags
     a.state_in, a.state_out = _ptr(state), _ptr(dst)
     a.x, a.x_stride_b = _ptr(xs), xs.stride(0)
@@ -657,6 +663,31 @@ def recurrent_step(x, dt, B, C, h_prev, A, D, *, dt_bias=None, dt_softplus=False
     zl = z[:, -1].reshape(b, H, P) if z is not None else None
     y = selective_state_update(state.contiguous(), x[:, -1].reshape(b, H, P), dt[:, -1], A, Bl, Cl, D,
                                dt_bias=dt_bias, dt_softplus=dt_softplus, dt_limit=dt_limit, out_state=out, z=zl)
+    return y.reshape(b, 1, d_inner), out.view(b, d_inner, N)
+
+
+def recurrent_step_reference(x, dt, B, C, h_prev, A_log, D):
+    """``Mamba2Block._recurrent_step`` (R/mamformer/layers/mamba2.py:407-458) in the reference's own
+    parameterisation, on the GPU: a decay rate per state column and a step per channel,
+        a[c, n] = exp(-exp(A_log[n]) dt[c]),  h[c, n] <- a[c, n] h[c, n] + dt[c] x[c] B[n],
+        y[c] = sum_n C[n] h[c, n] + D[c] x[c].
+    x, dt (b, seqlen, d_inner) -- only the last token is used (:435-438), dt already positive (the block
+    applies softplus before the call); B, C (b, seqlen, N); h_prev (b, d_inner, N) or None (zeros,
+    :448-449); A_log (N,) unclamped (:441-443); D (d_inner,).  Returns (y_t (b, 1, d_inner) in the dtype of x,
+    h_t (b, d_inner, N) float32), a new state as the reference returns.
+    """
+    b, _, d_inner = x.shape
+    N = B.shape[-1]
+    P = next(p for p in (64, 32, 16, 8, 4, 2, 1) if d_inner % p == 0)    # channels per kernel row group
+    H = d_inner // P
+    if h_prev is None:
+        state = torch.zeros((b, H, P, N), device=x.device, dtype=torch.float32)
+    else:
+        state = h_prev.reshape(b, H, P, N).to(torch.float32).contiguous()
+    out = torch.empty((b, H, P, N), device=x.device, dtype=torch.float32)
+    A = -torch.exp(A_log.to(torch.float32))
+    y = selective_state_update(state, x[:, -1].reshape(b, H, P), dt[:, -1].reshape(b, H, P), A, B[:, -1],
+                               C[:, -1], D, dt_softplus=False, out_state=out, A_per_state=True)
     return y.reshape(b, 1, d_inner), out.view(b, d_inner, N)
 
 

@@ -440,3 +440,30 @@ def test_kda_bwd_rejects_small_workspace():
     a = _good_kda_bwd(diff=False)
     a.workspace, a.workspace_bytes = ct.c_void_p(8192), 64
     assert _rc("mh_kda_chunk_scan_bwd", ct.byref(a), None) == -7
+
+
+def test_flag_values_match_the_header():
+    """Every MH_* enum value the Python side uses equals the header's."""
+    import re
+    text = (Path(__file__).resolve().parents[1] / "include" / "mamformer_hip.h").read_text()
+    vals = {m.group(1): int(m.group(2)) for m in re.finditer(r"\b(MH_[A-Z0-9_]+)\s*=\s*(-?\d+)", text)}
+    for name in ("MH_F32", "MH_BF16", "MH_DT_SOFTPLUS", "MH_DT_LIMIT", "MH_D_PER_CHANNEL", "MH_A_PER_STATE",
+                 "MH_DT_PER_CHANNEL", "MH_KDA_GATED", "MH_KDA_REFERENCE", "MH_KDA_PHI", "MH_KDA_BWD_DIFF",
+                 "MH_CONV_SILU"):
+        assert vals[name] == getattr(_lib, name), name
+
+
+def test_prefill_rejects_decode_only_flags():
+    for flag in (_lib.MH_A_PER_STATE, _lib.MH_DT_PER_CHANNEL):
+        a = _good_ssd()
+        a.flags = flag
+        n = ct.c_size_t()
+        assert _rc("mh_ssd_workspace_bytes", ct.byref(a), ct.byref(n)) == -6
+        assert b"decode" in _lib.lib().mh_last_error()
+
+
+def test_state_update_per_channel_dt_needs_a_row_of_steps():
+    a = _good_ssu()
+    a.flags = _lib.MH_DT_PER_CHANNEL
+    a.dt_stride_b = a.nheads                  # one step per head is too short a row for per-channel steps
+    assert _rc("mh_ssd_state_update", ct.byref(a), None) == -4

@@ -27,7 +27,7 @@ def test_decode_golden_three_steps():
     check("state", state, z["state"], 1e-4)
 
 
-@pytest.mark.parametrize("N", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("N", [8, 16, 32, 64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_decode_all_dstates(N, dtype):
     g = torch.Generator().manual_seed(N)
@@ -129,3 +129,35 @@ def test_recurrent_step_wrapper_returns_new_state():
                                            C[:, -1].numpy(), D.numpy(), dt_softplus=False)
     check("y", y.view(b, H, P), y_ref, 1e-4)
     check("h", hn.view(b, H, P, N), h_ref, 1e-4)
+
+
+@pytest.mark.parametrize("b,d_inner,N,dtype,h0", [
+    (2, 64, 16, torch.float32, False),      # the reference fixture's sizes (tests/test_mamba2.py:22-30)
+    (2, 32, 8, torch.float32, True),        # its per-seqlen case (tests/test_mamba2.py:74-80)
+    (3, 256, 32, torch.bfloat16, True),     # the debug preset's d_state
+    (2, 4096, 128, torch.bfloat16, True),
+])
+def test_reference_form_step_vs_oracle(b, d_inner, N, dtype, h0):
+    """recurrent_step_reference: the reference's own decode parameterisation (A_log per state, dt per channel,
+    mamba2.py:431-458) against the oracle's restatement, five steps chained through the returned state."""
+    g = torch.Generator().manual_seed(d_inner + N)
+    A_log = torch.log(torch.linspace(0.5, 8.0, N))
+    D = torch.ones(d_inner) + 0.1 * torch.randn(d_inner, generator=g)
+    h = torch.randn(b, d_inner, N, generator=g) * 0.1 if h0 else None
+    hr = None if h is None else h.double().numpy()
+    hd = dev(h)
+    say(f"reference-form step b={b} d_inner={d_inner} N={N} {dtype} h0={h0}")
+    for step in range(5):
+        x = torch.randn(b, 2, d_inner, generator=g).to(dtype)
+        dt = torch.nn.functional.softplus(torch.randn(b, 2, d_inner, generator=g))
+        B = torch.randn(b, 2, N, generator=g).to(dtype)
+        C = torch.randn(b, 2, N, generator=g).to(dtype)
+        y, hd_new = mh.recurrent_step_reference(dev(x, dtype), dev(dt), dev(B, dtype), dev(C, dtype), hd,
+                                                dev(A_log), dev(D))
+        torch.cuda.synchronize()
+        y_ref, hr = ref.ref_recurrent_step(x.double().numpy(), dt.double().numpy(), B.double().numpy(),
+                                           C.double().numpy(), hr, A_log.double().numpy(), D.double().numpy())
+        assert y.shape == (b, 1, d_inner) and y.dtype == dtype and hd_new.shape == (b, d_inner, N)
+        check(f"y[{step}]", y, y_ref, 1e-2 if dtype == torch.bfloat16 else 1e-4)
+        check(f"h[{step}]", hd_new, hr, 1e-4)
+        hd = hd_new
