@@ -539,9 +539,6 @@ def main():
         r = bench_kda(W.KDA5, max(5, args.steps // 5), 3)
         log(f"kda5: {r['mtok_s']:.1f} Mtok/s, {r['us_per_step']:.0f} us, roofline {r['roofline_frac']:.3f}")
         other["kda5"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
-        tr = measured_traffic("kda5")
-        if tr is not None:
-            other["kda5"]["traffic"] = tr["bytes_per_launch"]
     if "ssd2_bwd" in legs:
         r = bench_ssd_bwd(cfg, max(10, args.steps // 2), 5, nsets=3)
         log(f"ssd2 backward: {r['us_per_step']:.1f} us, {r['tflops']:.0f} TFLOP/s, roofline {r['roofline_frac']:.3f}")
@@ -570,6 +567,13 @@ def main():
     if "ssd1" in legs:
         r, _, _ = bench_ssd(W.SSD1, args.steps, args.warmup, nsets=1, chunk=64)
         other["ssd1"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+    # measured HBM bytes per launch (PMC, copy-calibrated) next to each leg's algorithmic bytes
+    for key, entry in [(k, v) for k, v in other.items() if k not in ("conv1d", "ssd1")] + \
+            [(f"conv1d_{k}", v) for k, v in other.get("conv1d", {}).items()] + \
+            [(k, v) for k, v in out.get("decode", {}).items()]:
+        tr = measured_traffic(key)
+        if tr is not None:
+            entry["traffic"] = tr["bytes_per_launch"]
     if other:
         out["other"] = other
     if "cpu" in legs:
