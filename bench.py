@@ -162,6 +162,30 @@ def bench_ssd(cfg, steps, warmup, nsets, chunk=None):
     return res, wall, ev
 
 
+def bench_ssd_hstates(cfg, steps, warmup):
+    """Cost of return_h_states at the headline shape: selective_scan with and without h_states through the same
+    Python entry (allocation of outputs and workspace included in both), and the h_states computation alone
+    (the second run of the prefill kernels with x and B swapped, plus the mean over heads)."""
+    import mamformer_amd as mh
+    from mamformer_amd import ops
+    from mamformer_amd import workloads as W
+
+    inp = W.ssd_inputs(cfg, device="cuda")
+    args = (inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"])
+    x4 = inp["x"]
+    B4 = inp["B"] if inp["B"].dim() == 4 else inp["B"].unsqueeze(2)
+    with torch.no_grad():
+        _, plain = time_plans([lambda: mh.selective_scan(*args, return_final_state=True)], steps, warmup)
+        _, both = time_plans([lambda: mh.selective_scan(*args, return_h_states=True, return_final_state=True)],
+                             steps, warmup)
+        _, alone = time_plans([lambda: ops._h_states(x4, inp["dt"], inp["A"], B4, None, None, False, None, None)],
+                              steps, warmup)
+    del inp
+    torch.cuda.empty_cache()
+    return dict(us_plain=plain * 1e3, us_with_h_states=both * 1e3, us_h_states=alone * 1e3,
+                overhead=both / plain)
+
+
 def bench_ssd_bwd(cfg, steps, warmup, nsets):
     import mamformer_amd as mh
     from mamformer_amd import workloads as W
@@ -438,7 +462,8 @@ def measured_traffic(workload="ssd2"):
 
 # ----------------------------------------------------------------- main
 
-LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd2_bwd", "kda5_bwd", "conv1d", "kda5_ref", "kda_step", "ssd1", "cpu")
+LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd2_bwd", "kda5_bwd", "conv1d", "kda5_ref", "kda_step", "ssd1",
+        "ssd2_hstates", "cpu")
 
 
 def main():
@@ -564,6 +589,11 @@ def main():
         log(f"KDA decode step B=64 H=32: {r['us_per_step']:.1f} us, {r['hbm_GBs']:.0f} GB/s "
             f"({r['roofline_frac']:.3f} of 8 TB/s)")
         other["kda_step"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+    if "ssd2_hstates" in legs:
+        r = bench_ssd_hstates(cfg, max(10, args.steps // 5), 3)
+        log(f"ssd2 return_h_states: {r['us_with_h_states']:.1f} us with h_states vs {r['us_plain']:.1f} us without "
+            f"(h_states alone {r['us_h_states']:.1f} us, x{r['overhead']:.2f})")
+        other["ssd2_hstates"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
     if "ssd1" in legs:
         r, _, _ = bench_ssd(W.SSD1, args.steps, args.warmup, nsets=1, chunk=64)
         other["ssd1"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}

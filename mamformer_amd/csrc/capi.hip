@@ -498,7 +498,7 @@ void ssd_wide_bwd_plan(const mh_ssd_bwd_args* a, SsdWide& w) {
   w.pieces = f->dstate > 128 ? 2 : 1;
   w.copy_bc = f->dstate != w.pieces * w.ni || G > 1;
   w.inner = L > 0 ? mh::ssd_bwd_workspace_bytes((int)b, (int)L, (int)H, (int)w.ni, (int)G, f->dtype,
-                                                ssd_bwd_heads_per_wg(f)) : 0;
+                                                ssd_bwd_heads_per_wg(f), (f->flags & MH_D_PER_CHANNEL) != 0) : 0;
   const size_t bc = w.copy_bc ? (size_t)(b * L * G * w.ni * es) : 0, st = (size_t)(b * H * P * w.ni * 4);
   size_t off = a256(w.inner);
   w.oB = off; off += a256(2 * bc);           // B piece, then dB piece
@@ -602,7 +602,8 @@ size_t ssd_bwd_need(const mh_ssd_bwd_args* a) {
     return w.total;
   }
   return f->seqlen > 0 ? mh::ssd_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate,
-                                                     (int)f->ngroups, f->dtype, ssd_bwd_heads_per_wg(f)) : 0;
+                                                     (int)f->ngroups, f->dtype, ssd_bwd_heads_per_wg(f),
+                                                     (f->flags & MH_D_PER_CHANNEL) != 0) : 0;
 }
 
 int conv_bwd_validate(const mh_conv1d_bwd_args* a) {

@@ -84,11 +84,13 @@ struct SsdBwdParams {
   float* dC_part;
   void* hin;                 // workspace: state entering every 64-token segment, (b, nseg, H) x fragment order
   void* lam;                 // workspace: adjoint of the state leaving every segment, same layout
+  float* part_s;             // workspace: (b, nseg, H, 3) per-segment dA, d_dt_bias, dD (per head) partials
+  float* part_dc;            // workspace: (b, nseg, H, 2, P) per-segment, per-token-half dD partials (per channel)
   int heads_per_wg;          // heads of one group handled by a workgroup of the gradient kernel (HB)
 };
 hipError_t launch_ssd_bwd(const SsdBwdParams& p, hipStream_t st);
 size_t ssd_bwd_workspace_bytes(int batch, int seqlen, int nheads, int dstate, int ngroups, int dtype,
-                               int heads_per_wg);
+                               int heads_per_wg, int d_per_channel);
 void ssd_bwd_workspace_layout(SsdBwdParams& p, void* workspace);
 
 // ------------------------------------------------------------- KDA

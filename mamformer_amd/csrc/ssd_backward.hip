@@ -27,7 +27,7 @@
 //      (lam <- e^{c_end} lam + sum_t e^{c_t} C_t^T dy_t).  Both into the workspace, fragment-native order.
 //   2. ssd_bwd_grad      grid (nseg, H / HB, b): one workgroup per (segment, block of HB heads of a group),
 //      fully parallel; dx and ddt stored directly, dB / dC summed over the block's heads in registers and
-//      stored as one fp32 partial per head block; dA / dD / dt_bias with float atomics.
+//      stored as one fp32 partial per head block; dA / dD / dt_bias as per-segment partials.
 //   3. ssd_bwd_reduce    partials -> dB, dC (fixed summation order) in the I/O dtype and the caller's strides.
 // Token-contracted products take their transposed operands from the MFMA unit (identity products), as in
 // the forward; all accumulation is fp32.
@@ -178,7 +178,7 @@ struct ZeroRanges {
   float* p[5];
   int64_t n[5];
 };
-// (dA, dD and d_dt_bias are sums of float atomics over the segment workgroups)
+// (an empty sequence's dA, dD and d_dt_bias; otherwise the partial sums' reduction writes them)
 __global__ __launch_bounds__(256) void ssd_bwd_zero_kernel(ZeroRanges z) {
   const int r = blockIdx.y;
   float* p = z.p[r];
@@ -380,7 +380,6 @@ struct GradSmem {
   float rowg[3][32];             // per XD^T tile (s-block, t-block) = (0,0), (0,1), (1,1): sum_s (M o XD)[t][s] dt_s
   float lh[N / 32];              // <lam_out, h_in> per n-block
   float dd[2];                   // trace of dy x^T per diagonal 32-block
-  float ddp[HD];                 // per-channel dD partial
   float cb[3][64 * 16];          // CB[t][s] tiles (t-block, s-block) = (0,0), (1,0), (1,1), accumulator order
   float cbt[3][64 * 16];         // CB^T[s][t] tiles (s-block, t-block) = (0,0), (0,1), (1,1)
 };
@@ -458,7 +457,6 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
   };
   fetch_head(hfirst, std::integral_constant<int, 0>());
   fetch_states(hfirst);
-  if (w == 0) sm.ddp[l] = 0.f;
   f32x16 dBacc = zero16(), dCacc = zero16();
 
   wait_vmem();                      // B / C tiles (and the first head's tiles) in LDS
@@ -846,11 +844,19 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
 #pragma unroll
         for (int i = 0; i < 16; ++i)
           Dv[i] = p.D ? (p.D_per_channel ? p.D[h * HD + 32 * pb + acc_row(half, i)] : p.D[h]) : 0.f;
-        if (p.D_per_channel && q.dD && s_x < len) {
+        if (p.D_per_channel && q.dD) {
+          // per-channel dD of this token half: sum over the lane-half's 32 tokens in a fixed shuffle order,
+          // one partial per (segment, head, token half) in the workspace, summed in order by the reduce kernel
           float xv[16];
           acc_cols<T, HD>(sg.X, s_x, 32 * pb, half, xv);
+          float* dst = q.part_dc + ((((int64_t)b * p.nseg + si) * p.nheads + h) * 2 + sbx) * HD + 32 * pb;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) atomicAdd(&sm.ddp[32 * pb + acc_row(half, i)], xv[i] * dyv[i]);
+          for (int i = 0; i < 16; ++i) {
+            float v = s_x < len ? xv[i] * dyv[i] : 0.f;
+#pragma unroll
+            for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+            if (l32 == 0) dst[acc_row(half, i)] = v;
+          }
         }
       } else {
         float* o = sm.dxp.v[w & 3] + 16 * l;
@@ -927,14 +933,11 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       if (valid) q.ddt[(int64_t)b * q.ddt_sb + (int64_t)(tok0 + l) * q.ddt_sl + h] = ddr;
       const float sdA = wave_sum(valid ? dtv * da : 0.f);
       const float sdb = wave_sum(ddr);
-      if (l == 0) {
-        unsafeAtomicAdd(&q.dA[h], sdA);
-        if (q.dbias) unsafeAtomicAdd(&q.dbias[h], sdb);
-        if (q.dD && !p.D_per_channel) unsafeAtomicAdd(&q.dD[h], sm.dd[0] + sm.dd[1]);
-      }
-      if (q.dD && p.D_per_channel) {
-        unsafeAtomicAdd(&q.dD[h * HD + l], sm.ddp[l]);
-        sm.ddp[l] = 0.f;
+      if (l == 0) {                    // this segment's partials, summed in a fixed order by the reduce kernel
+        float* ps = q.part_s + (((int64_t)b * p.nseg + si) * p.nheads + h) * 3;
+        ps[0] = sdA;
+        ps[1] = sdb;
+        ps[2] = sm.dd[0] + sm.dd[1];
       }
     }
     if (j + 1 < HB) {
@@ -998,30 +1001,65 @@ __global__ __launch_bounds__(256) void ssd_bwd_reduce_kernel(const float* __rest
   }
 }
 
+// dA, d_dt_bias and dD from the per-(batch, segment, head) partials, summed in a fixed order (deterministic):
+// one wave per output, lane k taking partials k, k + 64, ... in order, then a fixed shuffle tree.  Output o < H:
+// dA, d_dt_bias, dD (per head) of head o; o = H + h * P + c: dD[h, c] (per channel, both token halves).
+__global__ __launch_bounds__(256) void ssd_bwd_param_reduce_kernel(SsdBwdParams q) {
+  const SsdParams& p = q.f;
+  const int o = blockIdx.x * 4 + wave_id(), l = lane_id();
+  const int H = p.nheads, nbs = p.batch * p.nseg;
+  if (o < H) {
+    float a = 0.f, bi = 0.f, d = 0.f;
+    for (int k = l; k < nbs; k += 64) {
+      const float* ps = q.part_s + ((int64_t)k * H + o) * 3;
+      a += ps[0];
+      bi += ps[1];
+      d += ps[2];
+    }
+    a = wave_sum(a);
+    bi = wave_sum(bi);
+    d = wave_sum(d);
+    if (l == 0) {
+      q.dA[o] = a;
+      if (q.dbias) q.dbias[o] = bi;
+      if (q.dD && !p.D_per_channel) q.dD[o] = d;
+    }
+  } else if (q.dD && p.D_per_channel && o < H + H * HD) {
+    const int h = (o - H) / HD, c = (o - H) % HD;
+    float d = 0.f;
+    for (int k = l; k < 2 * nbs; k += 64) d += q.part_dc[(((int64_t)(k >> 1) * H + h) * 2 + (k & 1)) * HD + c];
+    d = wave_sum(d);
+    if (l == 0) q.dD[h * HD + c] = d;
+  }
+}
+
 // ------------------------------------------------------------------ host side
 
 struct BwdWorkspace {
-  size_t states, part;
-  size_t total() const { return 2 * align256(states) + 2 * align256(part); }
+  size_t states, part, ps, pc;
+  size_t total() const { return 2 * align256(states) + 2 * align256(part) + align256(ps) + align256(pc); }
 };
 static BwdWorkspace bwd_workspace(int batch, int seqlen, int nheads, int dstate, int ngroups, int dtype,
-                                  int heads_per_wg) {
+                                  int heads_per_wg, int d_per_channel) {
   const int nseg = (seqlen + SEG - 1) / SEG;
   const int nparts = (nheads / ngroups) / heads_per_wg;
   BwdWorkspace w;
   w.states = (size_t)batch * nseg * nheads * HD * dstate * (dtype == DT_BF16 ? sizeof(bf16) : sizeof(float));
   w.part = (size_t)nparts * batch * seqlen * ngroups * dstate * sizeof(float);
+  w.ps = (size_t)batch * nseg * nheads * 3 * sizeof(float);
+  w.pc = d_per_channel ? (size_t)batch * nseg * nheads * 2 * HD * sizeof(float) : 0;
   return w;
 }
 
 size_t ssd_bwd_workspace_bytes(int batch, int seqlen, int nheads, int dstate, int ngroups, int dtype,
-                               int heads_per_wg) {
-  return bwd_workspace(batch, seqlen, nheads, dstate, ngroups, dtype, heads_per_wg).total();
+                               int heads_per_wg, int d_per_channel) {
+  return bwd_workspace(batch, seqlen, nheads, dstate, ngroups, dtype, heads_per_wg, d_per_channel).total();
 }
 
 void ssd_bwd_workspace_layout(SsdBwdParams& q, void* workspace) {
   const SsdParams& p = q.f;
-  const BwdWorkspace w = bwd_workspace(p.batch, p.seqlen, p.nheads, p.dstate, p.ngroups, p.dtype, q.heads_per_wg);
+  const BwdWorkspace w = bwd_workspace(p.batch, p.seqlen, p.nheads, p.dstate, p.ngroups, p.dtype, q.heads_per_wg,
+                                       p.D_per_channel);
   char* c = reinterpret_cast<char*>(workspace);
   q.hin = c;
   c += align256(w.states);
@@ -1030,6 +1068,10 @@ void ssd_bwd_workspace_layout(SsdBwdParams& q, void* workspace) {
   q.dB_part = reinterpret_cast<float*>(c);
   c += align256(w.part);
   q.dC_part = reinterpret_cast<float*>(c);
+  c += align256(w.part);
+  q.part_s = reinterpret_cast<float*>(c);
+  c += align256(w.ps);
+  q.part_dc = w.pc ? reinterpret_cast<float*>(c) : nullptr;
 }
 
 template <typename T, int N>
@@ -1055,6 +1097,10 @@ static hipError_t launch_bwd_t(const SsdBwdParams& q, hipStream_t st) {
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((ssd_bwd_reduce_kernel<T>), dim3(nblk), dim3(256), 0, st, q.dC_part, nparts, q.dC, q.dC_sb,
                      q.dC_sl, p.seqlen, GN, n4);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int nout = p.nheads * (1 + (p.D_per_channel && q.dD ? HD : 0));
+  hipLaunchKernelGGL(ssd_bwd_param_reduce_kernel, dim3((unsigned)((nout + 3) / 4)), dim3(256), 0, st, q);
   return hipGetLastError();
 }
 

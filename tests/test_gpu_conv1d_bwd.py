@@ -84,8 +84,9 @@ def test_conv1d_bwd_weight_grad_is_deterministic():
         assert torch.equal(a, c)
 
 
-def _layer_ref64(layer, u):
-    """float64 CPU restatement of Mamba2Layer.forward (full scan, no cache) with autograd leaves."""
+def _layer_ref64(layer, u, with_h_states=False):
+    """float64 CPU restatement of Mamba2Layer.forward (full scan, no cache) with autograd leaves; with
+    ``with_h_states`` also the per-token mean of the state over the channels."""
     P = {k: v.detach().to("cpu", torch.float64).requires_grad_() for k, v in layer.named_parameters()}
     u64 = u.detach().to("cpu", torch.float64).requires_grad_()
     b, L, _ = u.shape
@@ -103,13 +104,17 @@ def _layer_ref64(layer, u):
     gidx = torch.arange(H) // (H // G)
     x4 = xa.view(b, L, H, Pd)
     h = torch.zeros(b, H, Pd, N, dtype=torch.float64)
-    ys = []
+    ys, hs = [], []
     for t in range(L):
         a = torch.exp(A[None, :] * dt[:, t])
         h = a[:, :, None, None] * h + (dt[:, t, :, None, None] * x4[:, t, :, :, None]) * Bm[:, t][:, gidx][:, :, None]
         ys.append(torch.einsum("bhpn,bhn->bhp", h, Cm[:, t][:, gidx]) + P["D"][None, :, None] * x4[:, t])
+        hs.append(h.mean(dim=(1, 2)))                       # h_states: mean over the channels (mamba2.py:114-116)
     y = torch.stack(ys, 1).reshape(b, L, layer.d_inner) * F.silu(z)
-    return F.linear(y, P["out_proj.weight"], P.get("out_proj.bias")), P, u64
+    out = F.linear(y, P["out_proj.weight"], P.get("out_proj.bias"))
+    if with_h_states:
+        return out, torch.stack(hs, 1), P, u64
+    return out, P, u64
 
 
 @pytest.mark.parametrize("G,bias", [(1, False), (2, True)])
@@ -132,6 +137,34 @@ def test_mamba2_layer_gradients_vs_float64_reference(G, bias):
     ref, P, u64 = _layer_ref64(layer, u)
     (ref * gout.cpu().double()).sum().backward()
     check("layer out", out, ref.detach().numpy(), 1e-4)
+    check("du", u.grad, u64.grad.numpy(), 1e-3)
+    for name, p in layer.named_parameters():
+        assert p.grad is not None, f"{name}: no gradient reached the parameter"
+        check(f"d{name}", p.grad, P[name].grad.numpy(), 1e-3)
+
+
+@pytest.mark.parametrize("G,N", [(1, 64), (2, 32)])
+def test_mamba2_layer_h_states_gradients_vs_float64_reference(G, N):
+    """Mamba2Layer(..., return_h_states=True) trained through both outputs (the fusion layers' use,
+    hybrid.py:383-395): the gradient of <gout, out> + <ghs, h_states> w.r.t. the input and every parameter against
+    autograd of the float64 restatement."""
+    torch.manual_seed(41 + G)
+    layer = Mamba2Layer(128, d_state=N, expand=2, headdim=64, ngroups=G, device="cuda", dtype=torch.float32)
+    with torch.no_grad():
+        for name, p in layer.named_parameters():
+            if name.endswith("weight"):
+                p.normal_(0.0, 0.2 if "dt_proj" not in name else 0.05)
+    u = torch.randn(2, 45, 128, device="cuda", requires_grad=True)
+    gout = torch.randn(2, 45, 128, device="cuda")
+    ghs = torch.randn(2, 45, N, device="cuda") * 20.0      # h_states is small (a mean over d_inner channels)
+    say(f"Mamba2Layer h_states gradients G={G} N={N}")
+    out, _, hs = layer(u, return_h_states=True)
+    ((out * gout).sum() + (hs * ghs).sum()).backward()
+    torch.cuda.synchronize()
+    ref, rhs, P, u64 = _layer_ref64(layer, u, with_h_states=True)
+    ((ref * gout.cpu().double()).sum() + (rhs * ghs.cpu().double()).sum()).backward()
+    check("layer out", out, ref.detach().numpy(), 1e-4)
+    check("h_states", hs, rhs.detach().numpy(), 1e-4)
     check("du", u.grad, u64.grad.numpy(), 1e-3)
     for name, p in layer.named_parameters():
         assert p.grad is not None, f"{name}: no gradient reached the parameter"
