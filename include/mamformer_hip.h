@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MH_ABI_VERSION 6
+#define MH_ABI_VERSION 7
 
 /* element types of x / B / C / y / q / k / v / o */
 enum { MH_F32 = 0, MH_BF16 = 1 };
@@ -111,6 +111,14 @@ int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream);
  *   Results are bit-identical to mh_ssd_chunk_scan_fwd's for the same arguments. */
 #define MH_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int mh_ssd_chunk_scan_fwd_noalloc(const mh_ssd_args* a, void* stream);
+
+/* h_states of the prefill: hs (b, L, N) in the dtype of x, hs[b, t, n] = mean over (h, p) of the state after
+ *   token t -- the h_states output of selective_scan / _selective_scan_impl (mamformer/layers/mamba2.py:114-116).
+ *   Takes the forward's argument block (x, dt, A, B, dt flags, dt_bias, initial_state, workspace; y,
+ *   final_state, C, D, z and chunk_len are not used) and computes the state's channel sums, which need one
+ *   scalar per (token, head): sum_p x.  Supported: nheads <= 128, and the forward's dstate range. */
+int mh_ssd_h_states_workspace_bytes(const mh_ssd_args* a, size_t* bytes);
+int mh_ssd_h_states(const mh_ssd_args* a, void* h_states, void* stream);
 
 /* ------------------------------------------------------------------------
  * SSD chunked-scan prefill backward.

@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # bytes of the static device scratch behind mh_ssd_chunk_scan_fwd_noalloc (MH_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -146,6 +146,7 @@ EXPORTS = (
     "mh_abi_version", "mh_last_error",
     "mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd", "mh_ssd_chunk_scan_fwd_noalloc",
     "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",
+    "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states",
     "mh_ssd_state_update",
     "mh_kda_chunk_scan_fwd", "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
     "mh_kda_recurrent_step",
@@ -186,6 +187,8 @@ def lib():
             h.mh_ssd_bwd_workspace_bytes.argtypes = [ct.POINTER(SsdBwdArgs), ct.POINTER(_sz)]
             h.mh_ssd_chunk_scan_bwd.argtypes = [ct.POINTER(SsdBwdArgs), _vp]
             h.mh_ssd_state_update.argtypes = [ct.POINTER(SsuArgs), _vp]
+            h.mh_ssd_h_states_workspace_bytes.argtypes = [ct.POINTER(SsdArgs), ct.POINTER(_sz)]
+            h.mh_ssd_h_states.argtypes = [ct.POINTER(SsdArgs), _vp, _vp]
             h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
             h.mh_kda_recurrent_step.argtypes = [ct.POINTER(KdaStepArgs), _vp]
             h.mh_kda_bwd_workspace_bytes.argtypes = [ct.POINTER(KdaBwdArgs), ct.POINTER(_sz)]
@@ -198,7 +201,8 @@ def lib():
                          "mh_ssd_state_update", "mh_kda_chunk_scan_fwd", "mh_kda_recurrent_step",
                          "mh_causal_conv1d_fwd", "mh_conv1d_bwd_workspace_bytes", "mh_causal_conv1d_bwd",
                          "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",
-                         "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd"):
+                         "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
+                         "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states"):
                 getattr(h, name).restype = ct.c_int
             ver = h.mh_abi_version()
             if ver != ABI_VERSION:

@@ -740,6 +740,45 @@ int mh_ssd_chunk_scan_fwd_noalloc(const mh_ssd_args* a, void* stream) {
   return hip_status(mh::launch_ssd(p, reinterpret_cast<hipStream_t>(stream)), "ssd_chunk_scan_fwd_noalloc");
 }
 
+// h_states: the forward's argument block (y, final_state, z, chunk_len and the no-allocation scratch unused).
+int hs_validate(const mh_ssd_args* a) {
+  if (!a) return fail(MH_ERR_NULL, "ssd_h_states: args is NULL");
+  mh_ssd_args g = *a;
+  g.y = const_cast<void*>(g.x); g.y_stride_b = g.x_stride_b; g.y_stride_l = g.x_stride_l; g.y_stride_h = g.x_stride_h;
+  g.z = nullptr;
+  g.chunk_len = 64;
+  int rc = ssd_validate(&g, nullptr);
+  if (rc) return rc;
+  if (!mh::ssd_hs_supported((int)a->nheads, (int)a->dstate))
+    return fail(MH_ERR_UNSUPPORTED, "ssd_h_states: nheads %lld > 128 not supported", (long long)a->nheads);
+  return MH_OK;
+}
+
+int mh_ssd_h_states_workspace_bytes(const mh_ssd_args* a, size_t* bytes) {
+  if (!bytes) return fail(MH_ERR_NULL, "ssd_h_states: bytes output is NULL");
+  int rc = hs_validate(a);
+  if (rc) return rc;
+  *bytes = mh::ssd_hs_workspace_bytes((int)a->batch, (int)a->seqlen, (int)a->nheads, (int)a->dstate);
+  return MH_OK;
+}
+
+int mh_ssd_h_states(const mh_ssd_args* a, void* h_states, void* stream) {
+  int rc = hs_validate(a);
+  if (rc) return rc;
+  if (a->seqlen > 0 && !h_states) return fail(MH_ERR_NULL, "ssd_h_states: h_states output is NULL");
+  if (!aligned16(h_states)) return fail(MH_ERR_ALIGN, "ssd_h_states: h_states must be 16-byte aligned");
+  const size_t need = mh::ssd_hs_workspace_bytes((int)a->batch, (int)a->seqlen, (int)a->nheads, (int)a->dstate);
+  if (a->seqlen > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+    return fail(MH_ERR_WORKSPACE, "ssd_h_states: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
+                a->workspace_bytes);
+  mh::SsdParams p;
+  ssd_fill(a, 64, (a->seqlen + 63) / 64, p);
+  mh::HsParams q;
+  q.hs = h_states;
+  if (a->seqlen > 0) mh::ssd_hs_workspace_layout(p, q, a->workspace);
+  return hip_status(mh::launch_ssd_hs(p, q, reinterpret_cast<hipStream_t>(stream)), "ssd_h_states");
+}
+
 int mh_ssd_state_update(const mh_ssu_args* a, void* stream) {
   int rc = ssu_validate(a);
   if (rc) return rc;

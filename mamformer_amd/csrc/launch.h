@@ -67,6 +67,19 @@ size_t ssd_workspace_bytes(int batch, int seqlen, int nchunks, int nheads, int h
 // Point p's workspace parts into `workspace` (ssd_workspace_bytes of p's sizes).
 void ssd_workspace_layout(SsdParams& p, void* workspace);
 
+// h_states of the prefill (ssd_hstates.hip): mean over (h, p) of the state after every token.
+struct HsParams {
+  void* hs;                  // (b, L, N) in the I/O dtype
+  float* z;                  // workspace: (b, nseg, H, N) per-segment state sums (local, then entering)
+  float* dec;                // workspace: (b, nseg, H) segment decays
+  float* u;                  // workspace: (b, L, H) dt * sum_p x
+};
+bool ssd_hs_supported(int nheads, int dstate);
+size_t ssd_hs_workspace_bytes(int batch, int seqlen, int nheads, int dstate);
+// Lays out q's workspace parts and sets p.nseg to this pass's segment count.
+void ssd_hs_workspace_layout(SsdParams& p, HsParams& q, void* workspace);
+hipError_t launch_ssd_hs(const SsdParams& p, const HsParams& q, hipStream_t st);
+
 // ------------------------------------------------------------- SSD prefill backward
 struct SsdBwdParams {
   SsdParams f;               // forward sizes and inputs (no forward workspace)

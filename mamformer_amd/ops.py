@@ -170,7 +170,8 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
         B, C: (b, L, N) (one group, as the reference) or (b, L, G, N); dtype of x.
         D: (H,), (H*P,) or None.
         return_h_states: also return h_states (b, L, N), the per-token mean of the state over the
-            H*P channels (mamba2.py:114-116); computed by a second run of the same kernels (see below).
+            H*P channels (mamba2.py:114-116); computed by ``mh_ssd_h_states`` from the state's channel sums,
+            which need one scalar per (token, head) (see ``_h_states``).
         return_final_state: also return the state after the last token,
             shaped (b, H*P, N) for 3-D x (the reference's (b, d_inner, d_state)) or (b, H, P, N).
         chunk_size: state-passing chunk length (multiple of 64); None picks it from the shape.
@@ -410,6 +411,65 @@ def selective_scan_bwd(dy, x, dt, A, B, C, D=None, *, d_final_state=None, initia
 def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=False):
     """h_states[b, t, n] = mean over (h, p) of the state h_t[h, p, n] (mamba2.py:114-116).
 
+    Computed by ``mh_ssd_h_states`` (the channel sums of the state follow a recurrence with one scalar input per
+    (token, head), sum_p x); with ``grad`` through an autograd node whose backward differentiates the equivalent
+    swapped prefill below.  More than 128 heads take the swapped prefill in the forward as well.
+    """
+    cfg = (dt_softplus, dt_limit, chunk_size)
+    if grad:
+        return _HStatesFn.apply(x4, dt32, A32, B4, h0, bias32, cfg)
+    if x4.shape[2] > 128:
+        return _h_states_swap(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size)
+    return _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit)
+
+
+def _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
+    b, L, H, P = x4.shape
+    N = B4.shape[3]
+    hs = torch.empty((b, L, N), device=x4.device, dtype=x4.dtype)
+    args = _ssd_args(x4, dt32, A32, B4, B4, None, bias32, dt_softplus, dt_limit, h0, x4, None, 64)
+    nbytes = ct.c_size_t()
+    _lib.call("mh_ssd_h_states_workspace_bytes", ct.byref(args), ct.byref(nbytes))
+    ws = torch.empty(max(int(nbytes.value), 16), device=x4.device, dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = _ptr(ws), nbytes.value
+    _lib.call("mh_ssd_h_states", ct.byref(args), _ptr(hs), _stream(x4.device))
+    return hs
+
+
+class _HStatesFn(torch.autograd.Function):
+    """h_states with its gradient: forward = ``mh_ssd_h_states``; backward = autograd of the swapped prefill
+    (``_h_states_swap``), recomputed here on the saved inputs."""
+
+    @staticmethod
+    def forward(ctx, x4, dt32, A32, B4, h0, bias32, cfg):
+        ctx.save_for_backward(x4, dt32, A32, B4, h0, bias32)
+        ctx.cfg = cfg
+        if x4.shape[2] > 128:
+            return _h_states_swap(x4, dt32, A32, B4, h0, bias32, *cfg)
+        return _h_states_kernel(x4, dt32, A32, B4, h0, bias32, cfg[0], cfg[1])
+
+    @staticmethod
+    def backward(ctx, ghs):
+        saved = ctx.saved_tensors
+        leaves = [None if t is None else t.detach().requires_grad_(bool(need))
+                  for t, need in zip(saved, ctx.needs_input_grad[:6])]
+        with torch.enable_grad():
+            hs = _h_states_swap(*leaves, *ctx.cfg, grad=True)
+        want = [t for t in leaves if t is not None and t.requires_grad]
+        got = torch.autograd.grad(hs, want, ghs, allow_unused=True) if want else ()
+        grads, k = [], 0
+        for t in leaves:
+            if t is not None and t.requires_grad:
+                grads.append(got[k])
+                k += 1
+            else:
+                grads.append(None)
+        return (*grads, None)
+
+
+def _h_states_swap(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=False):
+    """h_states by a second run of the prefill kernels on a swapped problem (used for the gradient).
+
     The channel sum of the state is itself an SSD output once the roles of x and B are swapped: with
     heads h' = (h, q) over the two 64-wide halves q of the state dimension n, headdim' = 64 (n' = n - 64q),
     x'_t[h', n'] = B_t[g(h), 64q + n'], one group per original head with B'_t[h, p] = x_t[h, p]
@@ -429,7 +489,7 @@ def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, 
         pad = 64 - N % 64
         B4 = torch.nn.functional.pad(B4, (0, pad))
         h0 = None if h0 is None else torch.nn.functional.pad(h0, (0, pad))
-        hs = _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad)
+        hs = _h_states_swap(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad)
         return hs[..., :N]
     Q = N // 64
     gidx = torch.arange(H, device=x4.device) // (H // G)

@@ -90,6 +90,27 @@ def _scan_recurrence_f64(x, dt_raw, A, B, C, D, bias, h0):
     return torch.stack(ys, 1), torch.stack(hs, 1), h
 
 
+@pytest.mark.parametrize("dtype,A_scale", [(torch.float32, 40.0), (torch.bfloat16, 200.0)])
+def test_h_states_extreme_decay_vs_oracle(dtype, A_scale):
+    """Decay ranges far beyond what one factorised product holds within a 32-token segment (heads with
+    A dt up to -A_scale per token next to slow ones): those heads take the direct exponential path."""
+    g = torch.Generator().manual_seed(int(A_scale))
+    b, L, H, P, N, G = 2, 150, 8, 64, 64, 2
+    x = torch.randn(b, L, H, P, generator=g)
+    B = torch.randn(b, L, G, N, generator=g)
+    C = torch.randn(b, L, G, N, generator=g)
+    dt = torch.rand(b, L, H, generator=g) + 0.05
+    A = -torch.tensor([A_scale, 0.5, 3.0, A_scale / 4, 0.01, 10.0, A_scale, 1.0])
+    s0 = torch.randn(b, H, P, N, generator=g) * 0.1
+    say(f"h_states extreme decay {dtype} A_scale={A_scale}")
+    _, hs = mh.selective_scan(dev(x, dtype), dev(dt), dev(A), dev(B, dtype), dev(C, dtype), None,
+                              return_h_states=True, initial_state=dev(s0))
+    torch.cuda.synchronize()
+    r = ref.ssd_h_states(host(dev(x, dtype)), dt.double().numpy(), A.double().numpy(), host(dev(B, dtype)),
+                         initial_state=s0.double().numpy())
+    check("h_states", hs, r, TOL[dtype])
+
+
 @pytest.mark.parametrize("dtype,G,N,h0", [(torch.float32, 1, 64, False), (torch.float32, 2, 128, True),
                                           (torch.bfloat16, 1, 128, True), (torch.float32, 1, 32, True),
                                           (torch.float32, 2, 256, False)])
