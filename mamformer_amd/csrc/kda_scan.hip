@@ -437,22 +437,29 @@ struct KdaRefSmem {
   f32x16 red[2][NQ][2][64];              // k-half 1 read-out partials: vt, query, t-tile, lane
   Frag<bf16> A[3 * NQ][2][64];           // masked A^T tiles as B-operand fragments (bf16 high part)
   Frag<bf16> Alo[3 * NQ][2][64];         // ... and the bf16 rounding remainder (A = A + Alo to ~2^-17)
+  float xb[NQ == 2 ? 2 : 1][2][64][16];  // fused differential output: query 2's normalised rows (vt, tt, lane)
 };
 
-// Register-staged raw rows of one segment: per thread 4 16-byte chunks of k and of each query (element
-// e = tid + 256 i: token e >> 4, channels 8 (e & 15) ..), 2 of v (token e >> 3, columns 8 (e & 7) ..).
+// Threads of a reference-mode workgroup: 4 waves per query stream (v-tile x k-half each).
+template <int NQ>
+constexpr int kda_ref_threads = 256 * NQ;
+
+// Register-staged raw rows of one segment: per thread 16-byte chunks of k and of each query (element
+// e = tid + NT i: token e >> 4, channels 8 (e & 15) ..) and of v (token e >> 3, columns 8 (e & 7) ..).
 template <int NQ>
 struct KdaRefStage {
-  bf16x8 k[4], q[NQ][4];
-  uint4 v[2];
+  static constexpr int KC = 4 / NQ, VC = 2 / NQ;
+  bf16x8 k[KC], q[NQ][KC];
+  uint4 v[VC];
 };
 
 template <int NQ>
 __device__ __forceinline__ void kda_ref_load(KdaRefStage<NQ>& g, const bf16* const (&qp)[2], const bf16* kk,
                                              const bf16* vv, int64_t rowbase, int pos, int len, int v0, int tid) {
+  constexpr int NT = kda_ref_threads<NQ>;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tid + 256 * i;
+  for (int i = 0; i < KdaRefStage<NQ>::KC; ++i) {
+    const int e = tid + NT * i;
     const int t = e >> 4, k0 = (e & 15) * 8;
     const int64_t r = (rowbase + pos + min(t, len - 1)) * DK + k0;
     g.k[i] = *reinterpret_cast<const bf16x8*>(kk + r);
@@ -460,8 +467,8 @@ __device__ __forceinline__ void kda_ref_load(KdaRefStage<NQ>& g, const bf16* con
     for (int j = 0; j < NQ; ++j) g.q[j][i] = *reinterpret_cast<const bf16x8*>(qp[j] + r);
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int e = tid + 256 * i;
+  for (int i = 0; i < KdaRefStage<NQ>::VC; ++i) {
+    const int e = tid + NT * i;
     const int t = e >> 3, c0 = (e & 7) * 8;
     g.v[i] = t < len ? *reinterpret_cast<const uint4*>(vv + (rowbase + pos + t) * 128 + v0 + c0)
                      : make_uint4(0, 0, 0, 0);
@@ -470,11 +477,15 @@ __device__ __forceinline__ void kda_ref_load(KdaRefStage<NQ>& g, const bf16* con
 
 }  // namespace
 
+// 4 NQ waves: wave w has v-tile vt = w & 1, k-half kh = (w >> 1) & 1 and query stream qw = w >> 2; the two query
+// streams' waves keep their own copy of the state tiles.
 template <int NQ>
-__global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
+__global__ __launch_bounds__(256 * NQ) void kda_ref_kernel(KdaParams p) {
   __shared__ KdaRefSmem<NQ> sm;
   using SM = KdaRefSmem<NQ>;
   using TM = bf16;
+  constexpr int NT = kda_ref_threads<NQ>, NW = NT / 64;
+  constexpr int KC = KdaRefStage<NQ>::KC, VC = KdaRefStage<NQ>::VC;
   const int nbh = p.batch * p.nheads;
   int bh, vh;
   const int L = blockIdx.x;
@@ -487,7 +498,7 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
   }
   const int h = bh % p.nheads;
   const int w = wave_id(), l = lane_id(), half = l >> 5, l32 = l & 31;
-  const int vt = w & 1, kh = w >> 1;
+  const int vt = w & 1, kh = (w >> 1) & 1, qw = w >> 2;
   const int tid = threadIdx.x;
   const int S = p.seqlen;
   const int kd = p.kernel_dim;
@@ -516,7 +527,7 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
   }
   if (tid < DK) sm.z[tid] = p.init_z ? p.init_z[(int64_t)bh * DK + tid] : 0.f;
 
-  static_assert(SEGK * (DK / 8) == 4 * 256 && SEGK * (DVH / 8) == 2 * 256, "staging covers a segment");
+  static_assert(SEGK * (DK / 8) == KC * NT && SEGK * (DVH / 8) == VC * NT, "staging covers a segment");
   KdaRefStage<NQ> stg;
   if (S > 0) kda_ref_load<NQ>(stg, qp, kk, vv, rowbase, 0, min(SEGK, S), v0, tid);
   for (int pos = 0; pos < S; pos += SEGK) {
@@ -525,8 +536,8 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
     auto stage = [&](auto MASKc) {     // MASK: zero tokens past the segment end and channels past kernel_dim
       constexpr bool MASK = decltype(MASKc)::value;
 #pragma unroll
-      for (int ie = 0; ie < 4; ++ie) {
-        const int e = tid + 256 * ie;
+      for (int ie = 0; ie < KC; ++ie) {
+        const int e = tid + NT * ie;
         const int t = e >> 4, k0 = (e & 15) * 8;
         const bool in = t < len;
         const bf16x8 kv8 = stg.k[ie];
@@ -553,17 +564,18 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
     if (len == SEGK && kd >= DK) stage(std::false_type{});
     else stage(std::true_type{});
 #pragma unroll
-    for (int ie = 0; ie < 2; ++ie) {
-      const int e = tid + 256 * ie;
+    for (int ie = 0; ie < VC; ++ie) {
+      const int e = tid + NT * ie;
       const int t = e >> 3, c0 = (e & 7) * 8;
       *reinterpret_cast<uint4*>(&sm.V[t * SM::PV + c0]) = stg.v[ie];
     }
     if (pos + SEGK < S) kda_ref_load<NQ>(stg, qp, kk, vv, rowbase, pos + SEGK, min(SEGK, S - pos - SEGK), v0, tid);
     __syncthreads();
 
-    // ---- phase B2: phi(q_i,t) . z_prev  (4 adjacent lanes per (query, token), 32 channels each).
-    // Waves 0-1 take one item per lane (they form two A tiles in phase C), waves 2-3 the rest (one tile).
-    for (int it = tid; it < NQ * SEGK * 4; it += (tid < 128 ? NQ * SEGK * 4 : 128)) {
+    // ---- phase B2: phi(q_i,t) . z_prev  (4 adjacent lanes per (query, token), 32 channels each: one item
+    // per thread)
+    {
+      const int it = tid;
       const int i = it / (SEGK * 4), t = (it >> 2) % SEGK, qq = it & 3;
       const bf16* row = &sm.Q[i][t * SM::PK + 32 * qq];
       float acc = 0.f;
@@ -579,7 +591,7 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
     }
 
     // ---- phase C: masked A^T tiles (query, s-tile, t-tile) and their row sums
-    for (int ti = w; ti < 3 * NQ; ti += 4) {
+    for (int ti = w; ti < 3 * NQ; ti += NW) {
       const int qi = ti / 3, tile = ti - 3 * qi;
       const int st = (tile == 2) ? 1 : 0, tt = (tile == 0) ? 0 : 1;
       f32x16 acc = zero16();
@@ -635,50 +647,46 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) vf[c].set(j, (float)sm.V[(16 * c + kset(half, j)) * SM::PV + 32 * vt + l32]);
 
-    f32x16 o[NQ][2];
+    // read-out of this wave's query stream qw: o[tt] for both t-tiles over this wave's k-half
+    f32x16 o[2];
 #pragma unroll
-    for (int qi = 0; qi < NQ; ++qi)
+    for (int tt = 0; tt < 2; ++tt) {
+      f32x16 acc = zero16();
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        f32x16 acc = zero16();
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int kt = 2 * kh + i;
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            const Frag<TM> sa = acc_to_frag<TM>(St[i], c);
-            Frag<TM> qb;
-            const bf16* row = &sm.Q[qi][(32 * tt + l32) * SM::PK + 32 * kt + 16 * c];
-            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + 4 * half);
-            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 8 + 4 * half);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { qb.v[j] = lo[j]; qb.v[4 + j] = hi[j]; }
-            acc = mma(sa, qb, acc);
-          }
-        }
-        o[qi][tt] = acc;
-      }
-#pragma unroll
-    for (int qi = 0; qi < NQ; ++qi) {
-      // wave kh finishes token tile tt = kh: it adds the intra-segment term of that tile and hands its
-      // read-out partial of the other tile to the partner wave (same vt, other k-half)
-      if (kh == 0) {
+      for (int i = 0; i < 2; ++i) {
+        const int kt = 2 * kh + i;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          o[qi][0] = mma(vf[c], sm.A[3 * qi + 0][c][l], o[qi][0]);
-          o[qi][0] = mma(vf[c], sm.Alo[3 * qi + 0][c][l], o[qi][0]);
-        }
-        sm.red[vt][qi][1][l] = o[qi][1];
-      } else {
+          const Frag<TM> sa = acc_to_frag<TM>(St[i], c);
+          Frag<TM> qb;
+          const bf16* row = &sm.Q[qw][(32 * tt + l32) * SM::PK + 32 * kt + 16 * c];
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + 4 * half);
+          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 8 + 4 * half);
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          o[qi][1] = mma(vf[c], sm.A[3 * qi + 1][c][l], o[qi][1]);
-          o[qi][1] = mma(vf[c], sm.Alo[3 * qi + 1][c][l], o[qi][1]);
-          o[qi][1] = mma(vf[2 + c], sm.A[3 * qi + 2][c][l], o[qi][1]);
-          o[qi][1] = mma(vf[2 + c], sm.Alo[3 * qi + 2][c][l], o[qi][1]);
+          for (int j = 0; j < 4; ++j) { qb.v[j] = lo[j]; qb.v[4 + j] = hi[j]; }
+          acc = mma(sa, qb, acc);
         }
-        sm.red[vt][qi][0][l] = o[qi][0];
       }
+      o[tt] = acc;
+    }
+    // wave kh finishes token tile tt = kh: it adds the intra-segment term of that tile and hands its
+    // read-out partial of the other tile to the partner wave (same vt and query, other k-half)
+    if (kh == 0) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        o[0] = mma(vf[c], sm.A[3 * qw + 0][c][l], o[0]);
+        o[0] = mma(vf[c], sm.Alo[3 * qw + 0][c][l], o[0]);
+      }
+      sm.red[vt][qw][1][l] = o[1];
+    } else {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        o[1] = mma(vf[c], sm.A[3 * qw + 1][c][l], o[1]);
+        o[1] = mma(vf[c], sm.Alo[3 * qw + 1][c][l], o[1]);
+        o[1] = mma(vf[2 + c], sm.A[3 * qw + 2][c][l], o[1]);
+        o[1] = mma(vf[2 + c], sm.Alo[3 * qw + 2][c][l], o[1]);
+      }
+      sm.red[vt][qw][0][l] = o[0];
     }
     // state update (no decay): S[k][v] += sum_s phi(k_s)[k] v_s[v]
 #pragma unroll
@@ -696,39 +704,50 @@ __global__ __launch_bounds__(256) void kda_ref_kernel(KdaParams p) {
       St[i] = acc;
     }
     __syncthreads();
+    // normalised rows of token tile tt = kh for query qw
+    float res[16];
+    const int tl = 32 * kh + l32;
+    const bool valid = tl < len;
     auto finish = [&](auto TTc) {
       constexpr int tt = decltype(TTc)::value;
-      const int tl = 32 * tt + l32;
-      if (tl < len) {
-        float res[NQ][16];
+      if (valid) {
+        const float nr = sm.zq[qw][tl] + (tt == 0 ? sm.nrm[qw][0][l32] : sm.nrm[qw][1][l32] + sm.nrm[qw][2][l32]);
+        const float inv = 1.f / (nr + 1e-8f);
+        const f32x16 other = sm.red[vt][qw][tt][l];
 #pragma unroll
-        for (int qi = 0; qi < NQ; ++qi) {
-          const float nr = sm.zq[qi][tl] + (tt == 0 ? sm.nrm[qi][0][l32] : sm.nrm[qi][1][l32] + sm.nrm[qi][2][l32]);
-          const float inv = 1.f / (nr + 1e-8f);
-          const f32x16 other = sm.red[vt][qi][tt][l];
-#pragma unroll
-          for (int r = 0; r < 16; ++r) res[qi][r] = (o[qi][tt][r] + other[r]) * inv;
-        }
-        if (fuse_diff) {
-          bf16* orow = op[0] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = (bf16)((res[0][r] - lam * res[NQ - 1][r]) * inv_1ml);
-        } else {
-#pragma unroll
-          for (int qi = 0; qi < NQ; ++qi) {
-            bf16* orow = op[qi] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = (bf16)res[qi][r];
-          }
-        }
+        for (int r = 0; r < 16; ++r) res[r] = (o[tt][r] + other[r]) * inv;
       }
     };
     if (kh == 0) finish(std::integral_constant<int, 0>{});
     else finish(std::integral_constant<int, 1>{});
-    __syncthreads();
+    if (!fuse_diff) {
+      if (valid) {
+        bf16* orow = op[qw] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) orow[acc_row(half, r)] = (bf16)res[r];
+      }
+      __syncthreads();
+    } else {
+      // the differential combination (o1 - lam o2) / (1 - lam + 1e-8): query 2's waves hand their rows over
+      if (qw == 1 && valid) {
+#pragma unroll
+        for (int r = 0; r < 16; r += 4)
+          *reinterpret_cast<f32x4*>(&sm.xb[vt][kh][l][r]) = f32x4{res[r], res[r + 1], res[r + 2], res[r + 3]};
+      }
+      __syncthreads();
+      if (qw == 0 && valid) {
+        bf16* orow = op[0] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
+#pragma unroll
+        for (int r = 0; r < 16; r += 4) {
+          const f32x4 r2 = *reinterpret_cast<const f32x4*>(&sm.xb[vt][kh][l][r]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) orow[acc_row(half, r + j)] = (bf16)((res[r + j] - lam * r2[j]) * inv_1ml);
+        }
+      }
+    }
   }
 
-  if (p.final_state) {
+  if (p.final_state && qw == 0) {
     float* sf_out = p.final_state + (int64_t)bh * DK * 128;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -755,9 +774,9 @@ hipError_t launch_kda(const KdaParams& p, hipStream_t st) {
   if (p.mode == 0) {
     hipLaunchKernelGGL(kda_gated_kernel, grid, dim3(64 * KW), 0, st, p);
   } else if (p.q2) {
-    hipLaunchKernelGGL(kda_ref_kernel<2>, grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL(kda_ref_kernel<2>, grid, dim3(kda_ref_threads<2>), 0, st, p);
   } else {
-    hipLaunchKernelGGL(kda_ref_kernel<1>, grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL(kda_ref_kernel<1>, grid, dim3(kda_ref_threads<1>), 0, st, p);
   }
   return hipGetLastError();
 }
