@@ -180,10 +180,27 @@ def bench_ssd_hstates(cfg, steps, warmup):
                              steps, warmup)
         _, alone = time_plans([lambda: ops._h_states(x4, inp["dt"], inp["A"], B4, None, None, False, None, None)],
                               steps, warmup)
+    # training: forward + backward of <gy, y> (+ <ghs, h_states>) through autograd
+    leaves = [t.clone().requires_grad_() for t in (inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"])]
+    gy = torch.randn_like(inp["x"])
+    ghs = torch.randn((cfg.batch, cfg.seqlen, cfg.dstate), device="cuda", dtype=inp["x"].dtype)
+
+    def train(with_hs):
+        def step():
+            out = mh.selective_scan(*leaves, return_h_states=with_hs)
+            y = out[0] if with_hs else out
+            loss = (y.float() * gy.float()).sum()
+            if with_hs:
+                loss = loss + (out[1].float() * ghs.float()).sum()
+            torch.autograd.grad(loss, leaves)
+        return step
+
+    _, tr_plain = time_plans([train(False)], max(5, steps // 5), 2)
+    _, tr_both = time_plans([train(True)], max(5, steps // 5), 2)
     del inp
     torch.cuda.empty_cache()
     return dict(us_plain=plain * 1e3, us_with_h_states=both * 1e3, us_h_states=alone * 1e3,
-                overhead=both / plain)
+                overhead=both / plain, us_train_plain=tr_plain * 1e3, us_train_with_h_states=tr_both * 1e3)
 
 
 def bench_ssd_bwd(cfg, steps, warmup, nsets):
@@ -592,7 +609,8 @@ def main():
     if "ssd2_hstates" in legs:
         r = bench_ssd_hstates(cfg, max(10, args.steps // 5), 3)
         log(f"ssd2 return_h_states: {r['us_with_h_states']:.1f} us with h_states vs {r['us_plain']:.1f} us without "
-            f"(h_states alone {r['us_h_states']:.1f} us, x{r['overhead']:.2f})")
+            f"(h_states alone {r['us_h_states']:.1f} us, x{r['overhead']:.2f}); forward + backward "
+            f"{r['us_train_with_h_states']:.0f} us with vs {r['us_train_plain']:.0f} us without")
         other["ssd2_hstates"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
     if "ssd1" in legs:
         r, _, _ = bench_ssd(W.SSD1, args.steps, args.warmup, nsets=1, chunk=64)

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MH_ABI_VERSION 7
+#define MH_ABI_VERSION 8
 
 /* element types of x / B / C / y / q / k / v / o */
 enum { MH_F32 = 0, MH_BF16 = 1 };
@@ -119,6 +119,28 @@ int mh_ssd_chunk_scan_fwd_noalloc(const mh_ssd_args* a, void* stream);
  *   scalar per (token, head): sum_p x.  Supported: nheads <= 128, and the forward's dstate range. */
 int mh_ssd_h_states_workspace_bytes(const mh_ssd_args* a, size_t* bytes);
 int mh_ssd_h_states(const mh_ssd_args* a, void* h_states, void* stream);
+
+/* Backward of h_states: the autograd backward of the mean over (h, p) of the states
+ *   (mamformer/layers/mamba2.py:114-116) taken through the scan, i.e. the gradients of <dhs, h_states> for the
+ *   call described by `fwd` (read as mh_ssd_h_states reads it).  dhs (b, L, N) contiguous in the dtype of x;
+ *   dx (b, L, H, P) and dB (b, L, G, N) contiguous in the dtype of x; ddt (b, L, H) contiguous fp32 (w.r.t. the
+ *   raw dt, through dt_bias, softplus and the clamp); dA (H,) fp32; d_dt_bias (H,) fp32 (required when
+ *   fwd.dt_bias is set, else ignored); d_initial_state (b, H, P, N) fp32 or NULL.  Every output is overwritten
+ *   (C, D and the gate get no gradient from h_states; the caller adds these to the output's gradients).
+ *   Supported: nheads <= 128, dstate <= 128. */
+typedef struct {
+  mh_ssd_args fwd;
+  const void* dhs;
+  void* dx;
+  float* ddt;
+  float* dA;
+  void* dB;
+  float* d_dt_bias;
+  float* d_initial_state;
+  void* workspace; size_t workspace_bytes;
+} mh_ssd_hs_bwd_args;
+int mh_ssd_h_states_bwd_workspace_bytes(const mh_ssd_hs_bwd_args* a, size_t* bytes);
+int mh_ssd_h_states_bwd(const mh_ssd_hs_bwd_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
  * SSD chunked-scan prefill backward.

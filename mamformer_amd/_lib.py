@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # bytes of the static device scratch behind mh_ssd_chunk_scan_fwd_noalloc (MH_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -59,6 +59,15 @@ class SsdBwdArgs(ct.Structure):
         ("dB", _vp), ("dB_stride_b", _i64), ("dB_stride_l", _i64),
         ("dC", _vp), ("dC_stride_b", _i64), ("dC_stride_l", _i64),
         ("dD", _vp), ("d_dt_bias", _vp), ("d_initial_state", _vp),
+        ("workspace", _vp), ("workspace_bytes", _sz),
+    ]
+
+
+class SsdHsBwdArgs(ct.Structure):
+    _fields_ = [
+        ("fwd", SsdArgs),
+        ("dhs", _vp), ("dx", _vp), ("ddt", _vp), ("dA", _vp), ("dB", _vp),
+        ("d_dt_bias", _vp), ("d_initial_state", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
     ]
 
@@ -147,6 +156,7 @@ EXPORTS = (
     "mh_ssd_workspace_bytes", "mh_ssd_chunk_len", "mh_ssd_chunk_scan_fwd", "mh_ssd_chunk_scan_fwd_noalloc",
     "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",
     "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states",
+    "mh_ssd_h_states_bwd_workspace_bytes", "mh_ssd_h_states_bwd",
     "mh_ssd_state_update",
     "mh_kda_chunk_scan_fwd", "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
     "mh_kda_recurrent_step",
@@ -189,6 +199,8 @@ def lib():
             h.mh_ssd_state_update.argtypes = [ct.POINTER(SsuArgs), _vp]
             h.mh_ssd_h_states_workspace_bytes.argtypes = [ct.POINTER(SsdArgs), ct.POINTER(_sz)]
             h.mh_ssd_h_states.argtypes = [ct.POINTER(SsdArgs), _vp, _vp]
+            h.mh_ssd_h_states_bwd_workspace_bytes.argtypes = [ct.POINTER(SsdHsBwdArgs), ct.POINTER(_sz)]
+            h.mh_ssd_h_states_bwd.argtypes = [ct.POINTER(SsdHsBwdArgs), _vp]
             h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
             h.mh_kda_recurrent_step.argtypes = [ct.POINTER(KdaStepArgs), _vp]
             h.mh_kda_bwd_workspace_bytes.argtypes = [ct.POINTER(KdaBwdArgs), ct.POINTER(_sz)]
@@ -202,7 +214,8 @@ def lib():
                          "mh_causal_conv1d_fwd", "mh_conv1d_bwd_workspace_bytes", "mh_causal_conv1d_bwd",
                          "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",
                          "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
-                         "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states"):
+                         "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states",
+                         "mh_ssd_h_states_bwd_workspace_bytes", "mh_ssd_h_states_bwd"):
                 getattr(h, name).restype = ct.c_int
             ver = h.mh_abi_version()
             if ver != ABI_VERSION:

@@ -54,7 +54,7 @@ int64_t ssd_auto_chunk(const mh_ssd_args* a) {
   int64_t want = (a->seqlen * units + target - 1) / target;     // tokens per workgroup
   want = ((want + 63) / 64) * 64;
   if (want < 256) want = 256;
-  if (want > 4096) want = 4096;
+  if (want > 16384) want = 16384;
   return want;
 }
 
@@ -741,7 +741,7 @@ int mh_ssd_chunk_scan_fwd_noalloc(const mh_ssd_args* a, void* stream) {
 }
 
 // h_states: the forward's argument block (y, final_state, z, chunk_len and the no-allocation scratch unused).
-int hs_validate(const mh_ssd_args* a) {
+static int hs_validate(const mh_ssd_args* a) {
   if (!a) return fail(MH_ERR_NULL, "ssd_h_states: args is NULL");
   mh_ssd_args g = *a;
   g.y = const_cast<void*>(g.x); g.y_stride_b = g.x_stride_b; g.y_stride_l = g.x_stride_l; g.y_stride_h = g.x_stride_h;
@@ -758,7 +758,7 @@ int mh_ssd_h_states_workspace_bytes(const mh_ssd_args* a, size_t* bytes) {
   if (!bytes) return fail(MH_ERR_NULL, "ssd_h_states: bytes output is NULL");
   int rc = hs_validate(a);
   if (rc) return rc;
-  *bytes = mh::ssd_hs_workspace_bytes((int)a->batch, (int)a->seqlen, (int)a->nheads, (int)a->dstate);
+  *bytes = mh::ssd_hs_workspace_bytes((int)a->batch, (int)a->seqlen, (int)a->nheads, (int)a->dstate, false);
   return MH_OK;
 }
 
@@ -767,7 +767,7 @@ int mh_ssd_h_states(const mh_ssd_args* a, void* h_states, void* stream) {
   if (rc) return rc;
   if (a->seqlen > 0 && !h_states) return fail(MH_ERR_NULL, "ssd_h_states: h_states output is NULL");
   if (!aligned16(h_states)) return fail(MH_ERR_ALIGN, "ssd_h_states: h_states must be 16-byte aligned");
-  const size_t need = mh::ssd_hs_workspace_bytes((int)a->batch, (int)a->seqlen, (int)a->nheads, (int)a->dstate);
+  const size_t need = mh::ssd_hs_workspace_bytes((int)a->batch, (int)a->seqlen, (int)a->nheads, (int)a->dstate, false);
   if (a->seqlen > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
     return fail(MH_ERR_WORKSPACE, "ssd_h_states: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
                 a->workspace_bytes);
@@ -775,8 +775,54 @@ int mh_ssd_h_states(const mh_ssd_args* a, void* h_states, void* stream) {
   ssd_fill(a, 64, (a->seqlen + 63) / 64, p);
   mh::HsParams q;
   q.hs = h_states;
-  if (a->seqlen > 0) mh::ssd_hs_workspace_layout(p, q, a->workspace);
+  if (a->seqlen > 0) mh::ssd_hs_workspace_layout(p, q, a->workspace, false);
   return hip_status(mh::launch_ssd_hs(p, q, reinterpret_cast<hipStream_t>(stream)), "ssd_h_states");
+}
+
+static int hs_bwd_validate(const mh_ssd_hs_bwd_args* a) {
+  if (!a) return fail(MH_ERR_NULL, "ssd_h_states_bwd: args is NULL");
+  int rc = hs_validate(&a->fwd);
+  if (rc) return rc;
+  const mh_ssd_args* f = &a->fwd;
+  if (!mh::ssd_hs_bwd_supported((int)f->nheads, (int)f->dstate))
+    return fail(MH_ERR_UNSUPPORTED, "ssd_h_states_bwd: nheads %lld / dstate %lld not supported (<= 128 each)",
+                (long long)f->nheads, (long long)f->dstate);
+  if (!a->dA) return fail(MH_ERR_NULL, "ssd_h_states_bwd: dA is NULL");
+  if (f->dt_bias && !a->d_dt_bias) return fail(MH_ERR_NULL, "ssd_h_states_bwd: d_dt_bias is NULL while dt_bias is set");
+  if (f->seqlen > 0 && (!a->dhs || !a->dx || !a->ddt || !a->dB))
+    return fail(MH_ERR_NULL, "ssd_h_states_bwd: dhs, dx, ddt and dB are required");
+  if (!aligned16(a->dhs) || !aligned16(a->dx) || !aligned16(a->dB) || !aligned16(a->d_initial_state))
+    return fail(MH_ERR_ALIGN, "ssd_h_states_bwd: dhs, dx, dB and d_initial_state must be 16-byte aligned");
+  return MH_OK;
+}
+
+int mh_ssd_h_states_bwd_workspace_bytes(const mh_ssd_hs_bwd_args* a, size_t* bytes) {
+  if (!bytes) return fail(MH_ERR_NULL, "ssd_h_states_bwd: bytes output is NULL");
+  int rc = hs_bwd_validate(a);
+  if (rc) return rc;
+  const mh_ssd_args* f = &a->fwd;
+  *bytes = mh::ssd_hs_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate, true);
+  return MH_OK;
+}
+
+int mh_ssd_h_states_bwd(const mh_ssd_hs_bwd_args* a, void* stream) {
+  int rc = hs_bwd_validate(a);
+  if (rc) return rc;
+  const mh_ssd_args* f = &a->fwd;
+  const size_t need = mh::ssd_hs_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate, true);
+  if (f->seqlen > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+    return fail(MH_ERR_WORKSPACE, "ssd_h_states_bwd: workspace of %zu bytes (16-byte aligned) required, got %zu",
+                need, a->workspace_bytes);
+  mh::SsdParams p;
+  ssd_fill(f, 64, (f->seqlen + 63) / 64, p);
+  mh::HsParams q;
+  memset(&q, 0, sizeof(q));
+  q.dhs = a->dhs; q.dx = a->dx; q.ddt = a->ddt; q.dA = a->dA; q.dB = a->dB;
+  q.d_dt_bias = f->dt_bias ? a->d_dt_bias : nullptr;
+  if (f->seqlen > 0) mh::ssd_hs_workspace_layout(p, q, a->workspace, true);
+  else p.nseg = 0;
+  return hip_status(mh::launch_ssd_hs_bwd(p, q, a->d_initial_state, reinterpret_cast<hipStream_t>(stream)),
+                    "ssd_h_states_bwd");
 }
 
 int mh_ssd_state_update(const mh_ssu_args* a, void* stream) {

@@ -72,13 +72,26 @@ struct HsParams {
   void* hs;                  // (b, L, N) in the I/O dtype
   float* z;                  // workspace: (b, nseg, H, N) per-segment state sums (local, then entering)
   float* dec;                // workspace: (b, nseg, H) segment decays
-  float* u;                  // workspace: (b, L, H) dt * sum_p x
+  float* u;                  // workspace: (b, L, H) sum_p x
+  // backward
+  const void* dhs;           // (b, L, N) gradient of h_states, I/O dtype
+  void* dx;                  // (b, L, H, P) contiguous, I/O dtype
+  float* ddt;                // (b, L, H) fp32 (w.r.t. the raw dt)
+  float* dA;                 // (H,)
+  void* dB;                  // (b, L, G, N) contiguous, I/O dtype
+  float* d_dt_bias;          // (H,) or null
+  float* lam;                // workspace: (b, nseg, H, N) the adjoint's local parts, then the adjoint entering
+  float* part;               // workspace: (b, nseg, H, 2) dA and d_dt_bias partials
 };
 bool ssd_hs_supported(int nheads, int dstate);
-size_t ssd_hs_workspace_bytes(int batch, int seqlen, int nheads, int dstate);
+bool ssd_hs_bwd_supported(int nheads, int dstate);
+size_t ssd_hs_workspace_bytes(int batch, int seqlen, int nheads, int dstate, bool backward);
 // Lays out q's workspace parts and sets p.nseg to this pass's segment count.
-void ssd_hs_workspace_layout(SsdParams& p, HsParams& q, void* workspace);
+void ssd_hs_workspace_layout(SsdParams& p, HsParams& q, void* workspace, bool backward);
 hipError_t launch_ssd_hs(const SsdParams& p, const HsParams& q, hipStream_t st);
+// Gradients of <dhs, h_states> w.r.t. x, dt (raw), A, B, dt_bias and the initial state (dh0, (b, H, P, N), may
+// be null).
+hipError_t launch_ssd_hs_bwd(const SsdParams& p, const HsParams& q, float* dh0, hipStream_t st);
 
 // ------------------------------------------------------------- SSD prefill backward
 struct SsdBwdParams {

@@ -436,9 +436,33 @@ def _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
     return hs
 
 
+def _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
+    """Gradients of <ghs, h_states> by ``mh_ssd_h_states_bwd``: (dx, ddt, dA, dB, d h0, d dt_bias)."""
+    b, L, H, P = x4.shape
+    G, N = B4.shape[2], B4.shape[3]
+    dev = x4.device
+    ghs = ghs.to(x4.dtype).contiguous()
+    dx = torch.empty((b, L, H, P), device=dev, dtype=x4.dtype)
+    ddt = torch.empty((b, L, H), device=dev, dtype=torch.float32)
+    dA = torch.empty((H,), device=dev, dtype=torch.float32)
+    dB = torch.empty((b, L, G, N), device=dev, dtype=B4.dtype)
+    dh0 = None if h0 is None else torch.empty((b, H, P, N), device=dev, dtype=torch.float32)
+    dbias = None if bias32 is None else torch.empty((H,), device=dev, dtype=torch.float32)
+    a = _lib.SsdHsBwdArgs()
+    a.fwd = _ssd_args(x4, dt32, A32, B4, B4, None, bias32, dt_softplus, dt_limit, h0, x4, None, 64)
+    a.dhs, a.dx, a.ddt, a.dA, a.dB = _ptr(ghs), _ptr(dx), _ptr(ddt), _ptr(dA), _ptr(dB)
+    a.d_dt_bias, a.d_initial_state = _ptr(dbias), _ptr(dh0)
+    nbytes = ct.c_size_t()
+    _lib.call("mh_ssd_h_states_bwd_workspace_bytes", ct.byref(a), ct.byref(nbytes))
+    ws = torch.empty(max(int(nbytes.value), 16), device=dev, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = _ptr(ws), nbytes.value
+    _lib.call("mh_ssd_h_states_bwd", ct.byref(a), _stream(dev))
+    return dx, ddt, dA, dB, dh0, dbias
+
+
 class _HStatesFn(torch.autograd.Function):
-    """h_states with its gradient: forward = ``mh_ssd_h_states``; backward = autograd of the swapped prefill
-    (``_h_states_swap``), recomputed here on the saved inputs."""
+    """h_states with its gradient: forward = ``mh_ssd_h_states``; backward = ``mh_ssd_h_states_bwd`` (nheads and
+    dstate <= 128), else autograd of the swapped prefill (``_h_states_swap``) recomputed on the saved inputs."""
 
     @staticmethod
     def forward(ctx, x4, dt32, A32, B4, h0, bias32, cfg):
@@ -451,6 +475,12 @@ class _HStatesFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, ghs):
         saved = ctx.saved_tensors
+        x4, B4 = saved[0], saved[3]
+        if x4.shape[2] <= 128 and B4.shape[3] <= 128 and x4.shape[3] == 64:
+            dx, ddt, dA, dB, dh0, dbias = _h_states_bwd_kernel(ghs, *saved, ctx.cfg[0], ctx.cfg[1])
+            need = ctx.needs_input_grad
+            return (dx if need[0] else None, ddt if need[1] else None, dA if need[2] else None,
+                    dB if need[3] else None, dh0 if need[4] else None, dbias if need[5] else None, None)
         leaves = [None if t is None else t.detach().requires_grad_(bool(need))
                   for t, need in zip(saved, ctx.needs_input_grad[:6])]
         with torch.enable_grad():

@@ -113,10 +113,11 @@ def test_ssd_rejects_null_and_misaligned_pointers_and_small_workspace():
 
 
 def test_ssd_noalloc_validates_and_rejects_sizes_beyond_its_static_scratch():
-    # the 128K shape of the benchmark (b1 L131072 H128 N128 G8) needs far more workspace than the scratch
+    # the 128K shape of the benchmark (b1 L131072 H128 N128 G8) in 4096-token chunks needs more workspace than
+    # the scratch
     a = _good_ssd()
     b, L, H, P, N, G = 1, 131072, 128, 64, 128, 8
-    a.batch, a.seqlen, a.nheads, a.ngroups = b, L, H, G
+    a.batch, a.seqlen, a.nheads, a.ngroups, a.chunk_len = b, L, H, G, 4096
     a.x_stride_l = a.y_stride_l = H * P
     a.x_stride_b = a.y_stride_b = L * H * P
     a.B_stride_l = a.C_stride_l = G * N
@@ -207,7 +208,7 @@ def test_ops_refuse_cpu_tensors():
 
 def test_chunk_len_auto_choice():
     assert mamformer_amd.ssd_chunk_len(2, 4096, 64, 64, 128, 1) % 64 == 0
-    assert mamformer_amd.ssd_chunk_len(1, 131072, 128, 64, 128, 8) == 4096
+    assert mamformer_amd.ssd_chunk_len(1, 131072, 128, 64, 128, 8) == 16384
     assert mamformer_amd.ssd_chunk_len(1, 512, 8, 64, 64, 1, chunk_size=128) == 128
 
 
@@ -467,3 +468,38 @@ def test_state_update_per_channel_dt_needs_a_row_of_steps():
     a.flags = _lib.MH_DT_PER_CHANNEL
     a.dt_stride_b = a.nheads                  # one step per head is too short a row for per-channel steps
     assert _rc("mh_ssd_state_update", ct.byref(a), None) == -4
+
+
+def _good_hs_bwd():
+    a = _lib.SsdHsBwdArgs()
+    a.fwd = _good_ssd()
+    fake = ct.c_void_p(4096)
+    a.dhs = a.dx = a.ddt = a.dA = a.dB = fake
+    return a
+
+
+def test_h_states_workspace_and_bwd_validation():
+    a = _good_ssd()
+    n, nb = ct.c_size_t(), ct.c_size_t()
+    assert _rc("mh_ssd_h_states_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+    g = _good_hs_bwd()
+    assert _rc("mh_ssd_h_states_bwd_workspace_bytes", ct.byref(g), ct.byref(nb)) == 0
+    # the backward adds the adjoint's per-segment sums (b, nseg, H, N) fp32 to the forward's workspace
+    b, L, H, N = 2, 300, 8, 128
+    assert nb.value >= n.value + b * (-(-L // 32)) * H * N * 4
+    g.dA = None
+    assert _rc("mh_ssd_h_states_bwd", ct.byref(g), None) == -1
+    g = _good_hs_bwd()
+    g.fwd.dt_bias = ct.c_void_p(4096)            # d_dt_bias required with dt_bias
+    assert _rc("mh_ssd_h_states_bwd", ct.byref(g), None) == -1
+    assert b"d_dt_bias" in _lib.lib().mh_last_error()
+    g = _good_hs_bwd()
+    g.fwd.dstate, g.fwd.B_stride_l, g.fwd.C_stride_l = 256, 2 * 256, 2 * 256
+    g.fwd.B_stride_b = g.fwd.C_stride_b = 300 * 2 * 256
+    assert _rc("mh_ssd_h_states_bwd_workspace_bytes", ct.byref(g), ct.byref(nb)) == -6
+    g = _good_hs_bwd()
+    g.dx = ct.c_void_p(4100)
+    assert _rc("mh_ssd_h_states_bwd", ct.byref(g), None) == -5
+    g = _good_hs_bwd()
+    g.workspace, g.workspace_bytes = ct.c_void_p(4096), 16
+    assert _rc("mh_ssd_h_states_bwd", ct.byref(g), None) == -7

@@ -154,6 +154,115 @@ def test_h_states_autograd_vs_recurrence(dtype, G, N, h0):
         check(f"d{name}", leaves[name].grad, r[name].grad.numpy(), TOL[dtype])
 
 
+def _h_states_f64(x, dt_raw, A, B, bias, h0, limit):
+    """h_states alone as the plain float64 recurrence of the full state (autograd gives the reference gradients):
+    dt = clamp(softplus(dt_raw + bias), *limit); h_t = e^{A dt_t} h_{t-1} + dt_t x_t B_t^T; h_states_t = mean over
+    (h, p) of h_t (mamba2.py:98-116)."""
+    b, L, H, P = x.shape
+    G = B.shape[2]
+    gidx = torch.arange(H) // (H // G)
+    dt = F.softplus(dt_raw + bias)
+    if limit is not None:
+        dt = dt.clamp(*limit)
+    h = h0 if h0 is not None else torch.zeros(b, H, P, B.shape[3], dtype=torch.float64)
+    hs = []
+    for t in range(L):
+        h = torch.exp(A * dt[:, t])[..., None, None] * h + \
+            (dt[:, t, :, None, None] * x[:, t, :, :, None]) * B[:, t][:, gidx][:, :, None, :]
+        hs.append(h.mean(dim=(1, 2)))
+    return torch.stack(hs, 1) if hs else torch.zeros(b, 0, B.shape[3], dtype=torch.float64)
+
+
+@pytest.mark.parametrize("dtype,b,L,H,G,N,h0,limit,A_scale", [
+    (torch.float32, 1, 70, 4, 1, 64, True, None, 2.5),
+    (torch.float32, 2, 97, 6, 2, 128, False, (0.05, 0.9), 2.5),
+    (torch.bfloat16, 1, 64, 8, 1, 128, True, None, 2.5),
+    (torch.float32, 2, 1, 8, 4, 16, True, None, 2.5),
+    (torch.float32, 1, 45, 6, 3, 24, True, None, 2.5),
+    (torch.float32, 1, 40, 128, 2, 128, True, None, 2.5),
+    (torch.float32, 1, 150, 8, 2, 64, True, None, 60.0),
+    (torch.bfloat16, 2, 33, 5, 1, 8, False, (0.01, 2.0), 2.5),
+])
+def test_h_states_gradients_alone_vs_recurrence(dtype, b, L, H, G, N, h0, limit, A_scale):
+    """The gradient of <wh, h_states> alone (mh_ssd_h_states_bwd, nheads and dstate <= 128) w.r.t. x, the raw dt,
+    A, B, dt_bias and the initial state against autograd of the float64 full-state recurrence: ragged segment
+    ends, several groups, odd heads per group, the clamp's zero gradient, 128 heads, one token, and decays far
+    beyond e^-80 per 32-token segment (A_scale)."""
+    g = torch.Generator().manual_seed(L * 13 + H + N)
+    P = 64
+    q = lambda t: t.to(dtype).to(torch.float64)
+    x, B = q(torch.randn(b, L, H, P, generator=g)), q(torch.randn(b, L, G, N, generator=g))
+    dt_raw = torch.randn(b, L, H, generator=g, dtype=torch.float64) - 1.0
+    bias = 0.3 * torch.randn(H, generator=g, dtype=torch.float64)
+    A = -torch.exp(torch.rand(H, generator=g, dtype=torch.float64) * np.log(A_scale))
+    s0 = 0.1 * torch.randn(b, H, P, N, generator=g, dtype=torch.float64) if h0 else None
+    wh = torch.randn(b, L, N, generator=g, dtype=torch.float64) * 10.0
+    say(f"h_states gradients alone {dtype} b={b} L={L} H={H} G={G} N={N} h0={h0} limit={limit} A_scale={A_scale}")
+    leaves = dict(x=dev(x, dtype), dt=dev(dt_raw), A=dev(A), B=dev(B, dtype), bias=dev(bias),
+                  h0=dev(s0) if h0 else None)
+    for t in leaves.values():
+        if t is not None:
+            t.requires_grad_()
+    C = dev(torch.zeros(b, L, G, N), dtype)
+    _, hs = mh.selective_scan(leaves["x"], leaves["dt"], leaves["A"], leaves["B"], C, None, return_h_states=True,
+                              initial_state=leaves["h0"], dt_bias=leaves["bias"], dt_softplus=True, dt_limit=limit)
+    (hs.float() * dev(wh)).sum().backward()
+    torch.cuda.synchronize()
+    r = dict(x=x, dt=dt_raw, A=A, B=B, bias=bias, h0=s0)
+    for t in r.values():
+        if t is not None:
+            t.requires_grad_()
+    rhs = _h_states_f64(r["x"], r["dt"], r["A"], r["B"], r["bias"], r["h0"], limit)
+    check("h_states", hs, rhs.detach().numpy(), TOL[dtype])
+    (rhs * wh).sum().backward()
+    for name in ("x", "dt", "A", "B", "bias") + (("h0",) if h0 else ()):
+        check(f"d{name}", leaves[name].grad, r[name].grad.numpy(), TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_h_states_bwd_matches_swapped_prefill_backward_at_size(dtype):
+    """At a training size (b2 L2048 H64 N128) the dedicated h_states backward and autograd through the swapped
+    prefill (the prefill backward kernels on the problem with x and B exchanged) give the same gradients."""
+    from mamformer_amd import ops
+    g = torch.Generator(device="cuda").manual_seed(5)
+    b, L, H, P, G, N = 2, 2048, 64, 64, 1, 128
+    x = torch.randn(b, L, H, P, device="cuda", generator=g).to(dtype)
+    B = torch.randn(b, L, G, N, device="cuda", generator=g).to(dtype)
+    dt = torch.randn(b, L, H, device="cuda", generator=g) - 2.0
+    A = -torch.exp(torch.rand(H, device="cuda", generator=g) * 2.0)
+    bias = 0.2 * torch.randn(H, device="cuda", generator=g)
+    h0 = 0.1 * torch.randn(b, H, P, N, device="cuda", generator=g)
+    ghs = torch.randn(b, L, N, device="cuda", generator=g).to(dtype)
+    say(f"h_states bwd vs swapped prefill at size {dtype}")
+    got = ops._h_states_bwd_kernel(ghs, x, dt, A, B, h0, bias, True, None)
+    leaves = [t.detach().clone().requires_grad_() for t in (x, dt, A, B, h0, bias)]
+    hs = ops._h_states_swap(*leaves[:5], leaves[5], True, None, None, grad=True)
+    want = torch.autograd.grad(hs, leaves, ghs)
+    torch.cuda.synchronize()
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    for name, a_, w_ in zip(("dx", "ddt", "dA", "dB", "dh0", "dbias"), got, want):
+        check(name, a_, w_.double().cpu().numpy(), tol)
+
+
+def test_h_states_bwd_empty_sequence():
+    """L = 0: no token reaches h_states, so every gradient is zero (and the initial state's too)."""
+    from mamformer_amd import ops
+    b, H, P, G, N = 2, 4, 64, 1, 32
+    x = torch.zeros(b, 0, H, P, device="cuda")
+    B = torch.zeros(b, 0, G, N, device="cuda")
+    dt = torch.zeros(b, 0, H, device="cuda")
+    A = -torch.ones(H, device="cuda")
+    h0 = torch.randn(b, H, P, N, device="cuda")
+    bias = torch.ones(H, device="cuda")
+    say("h_states bwd empty sequence")
+    dx, ddt, dA, dB, dh0, dbias = ops._h_states_bwd_kernel(torch.zeros(b, 0, N, device="cuda"), x, dt, A, B, h0,
+                                                           bias, True, None)
+    torch.cuda.synchronize()
+    assert dx.shape == (b, 0, H, P) and dB.shape == (b, 0, G, N)
+    for t in (dA, dh0, dbias):
+        assert torch.count_nonzero(t).item() == 0
+
+
 # ----------------------------------------------------------------- Mamba2Layer
 
 def _layer_ref(layer, u, cache=None):
