@@ -53,8 +53,8 @@ struct HsSmem {
 
 // dt, c and u = dt xs of segment si into LDS, xs = sum_p x computed from x (local pass, and written to the
 // workspace) or read from it (out pass).
-template <typename T, bool FROM_WS>
-__device__ void hs_prologue(const SsdParams& p, const HsParams& q, HsSmem& sm, int b, int si, int len) {
+template <typename T, bool FROM_WS, typename Smem>
+__device__ void hs_prologue(const SsdParams& p, const HsParams& q, Smem& sm, int b, int si, int len) {
   const int H = p.nheads, tid = threadIdx.x;
   const int64_t tok0 = (int64_t)si * HS_SEG;
   float* uws = q.u + ((int64_t)b * p.seqlen + tok0) * H;
@@ -320,40 +320,23 @@ __global__ __launch_bounds__(256) void ssd_hs_out_kernel(SsdParams p, HsParams q
 
 // ---------------------------------------------------------------- backward
 // Gradients of <ghs, hs> for ghs the gradient of h_states.  With g_t = ghs_t / (H P) (the same for every head),
-// the adjoint of Z^h_t is lambda^h_t = g_t + a^h_{t+1} lambda^h_{t+1}.  Per 32-token segment, with c the in-segment
-// cumsum of A dt, a_t = e^{A dt_t}, Zin the state sum entering the segment and Lam the adjoint handed in from the
-// right (a lambda of the next segment's first token):
-//   lambda_t = sum_{t' >= t} e^{c_t' - c_t} g_t' + e^{c_31 - c_t} Lam,
-//   Z_{t-1}  = e^{c_{t-1}} Zin + sum_{s < t} e^{c_{t-1} - c_s} u_s B_s,
-//   du_t = lambda_t . B_t = Y[t][t] + e^{c_31 - c_t} R[t]          (M[t'][s] = g_t' . B_s, R[s] = Lam . B_s),
-//   q_t  = lambda_t . Z_{t-1} = e^{c_31 - c_t + c_{t-1}} Zin . Lam + e^{c_{t-1}} Y2[t]
-//          + e^{c_31 - c_t} sum_{s<t} e^{c_{t-1} - c_s} u_s R[s] + sum_{s<t} e^{c_{t-1} - c_s} u_s Y[t][s],
-//   Y[t][s] = sum_{t' >= t} e^{c_t' - c_t} M[t'][s] = M[t][s] + a_{t+1} Y[t+1][s]   (Y2 likewise from P[t'] = Zin . g_t'),
-//   dB_t = sum_h u^h_t lambda^h_t = sum_{t' >= t} V[t][t'] g_t' + sum_h u^h_t e^{c_31 - c_t} Lam^h,
-//          V[t][t'] = sum_h u^h_t e^{c_t' - c_t},
-// then d dt_t = A a_t q_t + xs_t du_t (through bias, softplus and clamp), d xs_t = dt_t du_t (dx[t][h][p] for every
-// p), dA = sum dt a q and d h0[h][p][n] = the adjoint before the first token.  Every exponent is <= 0.
-//   ssd_hsb_local_kernel (segment, batch): GL[h][n] = sum_t e^{c_t} g_t[n] (the segment's part of the adjoint
-//                        handed to the left).
-//   ssd_hsb_carry_kernel (batch, head, n): Lam of every segment, right to left (in place over GL), and d h0.
-//   ssd_hsb_main_kernel  (segment, batch): du, q, dB, dx, ddt and per-segment dA / d_dt_bias partials.
+// the adjoint of Z^h_t is lambda^h_t = g_t + a^h_{t+1} lambda^h_{t+1}, a_t = e^{A dt_t}, and
+//   du_t = lambda_t . B_t,   q_t = lambda_t . Z_{t-1},   dB_t = sum_h u^h_t lambda^h_t,
+//   d dt_t = A a_t q_t + xs_t du_t (through bias, softplus and clamp),   d xs_t = dt_t du_t (dx[t][h][p], every p),
+//   dA = sum_t dt_t a_t q_t,   d h0[h][p][n] = a_0 lambda_0 (the adjoint of the state sum before the first token).
+// Per 32-token segment with Zin the state sum entering it and Lam = a lambda of the next segment's first token:
+//   ssd_hsb_local_kernel (segment, batch): the forward's local pass (xs, Zloc, segment decay) and
+//                        GL[h][n] = sum_t e^{c_t} g_t[n] (c the in-segment inclusive cumsum of A dt), the
+//                        segment's part of the adjoint handed to the left.
+//   ssd_hsb_carry_kernel (batch, head, n): Zin of every segment left to right (in place over Zloc) and Lam of
+//                        every segment right to left (in place over GL), then d h0.
+//   ssd_hsb_main_kernel  (segment, batch): one head per wave at a time, lanes over the state columns: the two
+//                        recurrences inside the segment run directly (Z forward from Zin, lambda backward from
+//                        Lam; every factor a <= 1), du and q as lane partials reduced across the wave, dB summed
+//                        over the waves in a fixed order, dx, ddt and per-segment dA / d_dt_bias partials.
 //   ssd_hsb_reduce_kernel: dA and d_dt_bias summed over (batch, segment) in a fixed order.
-constexpr int HSB_MAXH = 128, HSB_MAXN = 128;
-
-struct HsbSmem {
-  float c[HS_SEG][HSB_MAXH];     // raw dt, then the in-segment cumsum of A dt
-  float d[HS_SEG][HSB_MAXH];     // processed dt (0 past the end)
-  float xs[HS_SEG][HSB_MAXH];    // sum_p x (0 past the end)
-  float g[HS_SEG][HSB_MAXN];     // ghs / (H P)
-  float Bt[HS_SEG][HSB_MAXN];    // B of one group
-  float M[HS_SEG][HS_SEG + 1];   // g_t' . B_s
-  float V[HS_SEG][HS_SEG + 1];   // sum_h u_t e^{c_t' - c_t}  (t' >= t)
-  float q[HS_SEG][HSB_MAXH];     // q_t, then d xs_t
-  float du[HS_SEG][HSB_MAXH];
-  float R[HSB_MAXH][HS_SEG + 1]; // Lam . B_s
-  float P[HSB_MAXH][HS_SEG + 1]; // Zin . g_t'
-  float S1[HSB_MAXH], cend[HSB_MAXH];
-};
+constexpr int HSB_MAXH = 128, HSB_MAXN = 128;   // state columns: two per lane
+constexpr int HSB_WAVES = 4, HSB_WAVES_LOC = 8;
 
 __device__ __forceinline__ float hsb_dt_chain(const SsdParams& p, float raw, float bias) {
   const float u = raw + bias;
@@ -366,73 +349,112 @@ __device__ __forceinline__ float hsb_dt_chain(const SsdParams& p, float raw, flo
   return g;
 }
 
-// g of the segment (0 past the end) into g[t][n]
+__device__ __forceinline__ float hsb_readlane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// g of the segment into g[t][n] (0 past the end and for n >= N, so whole rows of W columns can be read)
 template <typename T, int W>
 __device__ void hsb_load_g(const SsdParams& p, const HsParams& q, float (*g)[W], int b, int si, int len) {
   const int N = p.dstate;
   const float scale = 1.f / ((float)p.nheads * (float)p.headdim);
   const T* src = reinterpret_cast<const T*>(q.dhs) + ((int64_t)b * p.seqlen + (int64_t)si * HS_SEG) * N;
-  for (int e = threadIdx.x; e < HS_SEG * N; e += blockDim.x) {
-    const int t = e / N, n = e % N;
-    g[t][n] = t < len ? to_f32(src[(int64_t)t * N + n]) * scale : 0.f;
+  for (int e = threadIdx.x; e < HS_SEG * W; e += blockDim.x) {
+    const int t = e / W, n = e % W;
+    g[t][n] = (t < len && n < N) ? to_f32(src[(int64_t)t * N + n]) * scale : 0.f;
   }
 }
 
+struct HsbLocSmem {
+  float c[HS_SEG][HSB_MAXH];     // as in HsSmem
+  float u[HS_SEG][HSB_MAXH];
+  float g[HS_SEG][HSB_MAXN];     // ghs / (H P) (0 past the end and beyond N)
+  float B[HS_SEG][HSB_MAXN];     // B of one group (likewise)
+  float cend[HSB_MAXH], mid[HSB_MAXH];
+  int wide[HSB_MAXH];
+};
+
+// One head per wave at a time, lanes over pairs of state columns, the per-token weights broadcast from lane t:
+// GL[h][n] = sum_t e^{c_t} g_t[n] and Zloc[h][n] = sum_s e^{c_end - c_s} u_s B_s[n].
 template <typename T>
-__global__ __launch_bounds__(256) void ssd_hsb_local_kernel(SsdParams p, HsParams q) {
-  __shared__ HsSmem sm;
-  const int si = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int H = p.nheads, N = p.dstate, N8 = N / 8;
-  const int len = min(HS_SEG, p.seqlen - si * HS_SEG);
-  hs_prologue<T, true>(p, q, sm, b, si, len);
-  hsb_load_g<T, HS_MAXN>(p, q, sm.Bt, b, si, len);           // g in the B buffer
-  __syncthreads();
-  for (int e = tid; e < HS_SEG * H; e += blockDim.x) {
-    const int t = e / H, h = e % H;
-    sm.Ei[t][h] = __expf(sm.c[t][h]);
-  }
-  __syncthreads();
+__global__ __launch_bounds__(64 * HSB_WAVES_LOC) void ssd_hsb_local_kernel(SsdParams p, HsParams q) {
+  __shared__ HsbLocSmem sm;
+  const int si = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int H = p.nheads, N = p.dstate, G = p.ngroups, hpg = H / G;
+  const int64_t tok0 = (int64_t)si * HS_SEG;
+  const int len = min(HS_SEG, p.seqlen - (int)tok0);
+  const int n0 = 2 * l, t = l & 31;
+  hs_prologue<T, false>(p, q, sm, b, si, len);
+  hsb_load_g<T, HSB_MAXN>(p, q, sm.g, b, si, len);
   float* gl = q.lam + (((int64_t)b * p.nseg + si) * H) * N;
-  for (int e = tid; e < H * N8; e += blockDim.x) {
-    const int h = e / N8, n0 = 8 * (e % N8);
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int t = 0; t < HS_SEG; ++t) {
-      float gv[8];
-      ld8f(&sm.Bt[t][n0], gv);
-      const float w = sm.Ei[t][h];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += w * gv[j];
+  float* zl = q.z + (((int64_t)b * p.nseg + si) * H) * N;
+  for (int gi = 0; gi < G; ++gi) {
+    __syncthreads();                   // c, u, g stored; the previous group's B no longer read
+    {
+      const T* Bb = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)gi * N;
+      for (int e = tid; e < HS_SEG * HSB_MAXN; e += blockDim.x) {
+        const int s = e / HSB_MAXN, n = e % HSB_MAXN;
+        sm.B[s][n] = (s < len && n < N) ? to_f32(Bb[(tok0 + s) * p.B_sl + n]) : 0.f;
+      }
     }
-    float* o = gl + (int64_t)h * N + n0;
-    *reinterpret_cast<f32x4*>(o) = f32x4{acc[0], acc[1], acc[2], acc[3]};
-    *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+    __syncthreads();
+    for (int h = gi * hpg + w; h < (gi + 1) * hpg; h += HSB_WAVES_LOC) {
+      const float c = sm.c[t][h];
+      const float ei = __expf(c), wt = __expf(sm.cend[h] - c) * sm.u[t][h];   // both exponents <= 0
+      float g0 = 0.f, g1 = 0.f, z0 = 0.f, z1 = 0.f;
+#pragma unroll
+      for (int s = 0; s < HS_SEG; ++s) {
+        const float es = hsb_readlane(ei, s), ws = hsb_readlane(wt, s);
+        const float2 gv = *reinterpret_cast<const float2*>(&sm.g[s][n0]);
+        const float2 bv = *reinterpret_cast<const float2*>(&sm.B[s][n0]);
+        g0 += es * gv.x;
+        g1 += es * gv.y;
+        z0 += ws * bv.x;
+        z1 += ws * bv.y;
+      }
+      if (n0 < N) {
+        *reinterpret_cast<float2*>(gl + (int64_t)h * N + n0) = float2{g0, g1};
+        *reinterpret_cast<float2*>(zl + (int64_t)h * N + n0) = float2{z0, z1};
+      }
+    }
   }
+  if (tid < H) q.dec[((int64_t)b * p.nseg + si) * H + tid] = __expf(sm.cend[tid]);
 }
 
+// Both carries of one (batch, head, column): forward Zin_{k+1} = dec_k Zin_k + Zloc_k from the summed initial
+// state, backward Lam_{k-1} = dec_k Lam_k + GL_k from Lam_last = 0; 16 segments of each chain loaded together.
 __global__ __launch_bounds__(256) void ssd_hsb_carry_kernel(SsdParams p, HsParams q, float* dh0) {
-  const int H = p.nheads, N = p.dstate, P = p.headdim;
+  const int H = p.nheads, N = p.dstate, P = p.headdim, ns = p.nseg;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)p.batch * H * N) return;
   const int n = (int)(i % N), h = (int)((i / N) % H), b = (int)(i / ((int64_t)N * H));
-  float* lp = q.lam + ((int64_t)b * p.nseg * H + h) * N + n;
-  const float* dp = q.dec + (int64_t)b * p.nseg * H + h;
-  const int64_t ls = (int64_t)H * N;
+  float Z = 0.f;
+  if (p.init_state) {
+    const float* s0 = p.init_state + (((int64_t)b * H + h) * P) * N + n;
+    for (int k = 0; k < P; ++k) Z += s0[(int64_t)k * N];
+  }
+  float* zp = q.z + ((int64_t)b * ns * H + h) * N + n;
+  float* lp = q.lam + ((int64_t)b * ns * H + h) * N + n;
+  const float* dp = q.dec + (int64_t)b * ns * H + h;
+  const int64_t zs = (int64_t)H * N;
   float L = 0.f;
-  // right to left, 16 segments' loads issued together per batch of steps
-  for (int k1 = p.nseg - 1; k1 >= 0; k1 -= 16) {
-    float gl[16], d[16];
+  for (int s0 = 0; s0 < ns; s0 += 16) {
+    float zl[16], df[16], gl[16], db[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      const int si = k1 - k;
-      gl[k] = si >= 0 ? lp[si * ls] : 0.f;
-      d[k] = si >= 0 ? dp[(int64_t)si * H] : 1.f;
+      const int sf = s0 + k, sb = ns - 1 - s0 - k;
+      zl[k] = sf < ns ? zp[sf * zs] : 0.f;
+      df[k] = sf < ns ? dp[(int64_t)sf * H] : 1.f;
+      gl[k] = sb >= 0 ? lp[sb * zs] : 0.f;
+      db[k] = sb >= 0 ? dp[(int64_t)sb * H] : 1.f;
     }
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      const int si = k1 - k;
-      if (si >= 0) lp[si * ls] = L;                  // the adjoint handed into segment si from the right
-      L = d[k] * L + gl[k];
+      const int sf = s0 + k, sb = ns - 1 - s0 - k;
+      if (sf < ns) zp[sf * zs] = Z;      // the state sum entering segment sf
+      Z = df[k] * Z + zl[k];
+      if (sb >= 0) lp[sb * zs] = L;      // the adjoint handed into segment sb from the right
+      L = db[k] * L + gl[k];
     }
   }
   if (dh0) {
@@ -441,189 +463,199 @@ __global__ __launch_bounds__(256) void ssd_hsb_carry_kernel(SsdParams p, HsParam
   }
 }
 
+// One step of the reduction below for lane mask M over the first K values.
+template <int M, int K, int NV>
+__device__ __forceinline__ void hsb_rs_step(float (&v)[NV], int l) {
+  const bool up = (l & M) != 0;
+#pragma unroll
+  for (int k = 0; k < K / 2; ++k) {
+    const float keep = up ? v[k + K / 2] : v[k], send = up ? v[k] : v[k + K / 2];
+    v[k] = keep + __shfl_xor(send, M, 64);
+  }
+}
+
+// Sum over the 64 lanes of v[k] for every k, lanes 2k and 2k + 1 ending with the sum of v[k]: at each step the
+// lanes whose mask bit is set keep the upper half of their values and trade the lower half with the partner.
+__device__ __forceinline__ float hsb_reduce_scatter(float (&v)[32]) {
+  const int l = lane_id();
+  // mask 32: v_permlane32_swap hands the lower lanes the partner's first half and the upper ones its second
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 16]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  // mask 16: v_permlane16_swap, the same within each half
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 8]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  hsb_rs_step<8, 8>(v, l);
+  hsb_rs_step<4, 4>(v, l);
+  hsb_rs_step<2, 2>(v, l);
+  return v[0] + __shfl_xor(v[0], 1, 64);
+}
+
+struct HsbSmem {
+  float g[HS_SEG][HSB_MAXN];     // ghs / (H P) (0 past the end and beyond N)
+  float B[HS_SEG][HSB_MAXN];     // B of one group (likewise)
+  float dB[HS_SEG][HSB_MAXN];    // the group's dB, summed over the waves in wave order
+};
+
 template <typename T>
-__global__ __launch_bounds__(256) void ssd_hsb_main_kernel(SsdParams p, HsParams q) {
+__global__ __launch_bounds__(64 * HSB_WAVES) void ssd_hsb_main_kernel(SsdParams p, HsParams q) {
   __shared__ HsbSmem sm;
-  const int si = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int w = wave_id(), l = lane_id();
-  const int H = p.nheads, N = p.dstate, N8 = N / 8, G = p.ngroups, hpg = H / G;
+  const int si = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int H = p.nheads, N = p.dstate, G = p.ngroups, hpg = H / G;
   const int64_t tok0 = (int64_t)si * HS_SEG;
   const int len = min(HS_SEG, p.seqlen - (int)tok0);
+  const int n0 = 2 * l;                // this lane's two state columns (zero rows beyond N)
+  const int t = l & 31;                // this lane's token in the per-token steps (both halves hold it)
+  const bool tv = t < len;
+  const float* dtb = p.dt + (int64_t)b * p.dt_sb + tok0 * p.dt_sl;
+  const float* xsw = q.u + ((int64_t)b * p.seqlen + tok0) * H;
   const float* zin = q.z + (((int64_t)b * p.nseg + si) * H) * N;
   const float* lam = q.lam + (((int64_t)b * p.nseg + si) * H) * N;
-  // ---- dt (processed), c, xs
-  const float* dtb = p.dt + (int64_t)b * p.dt_sb;
-  const float* xsw = q.u + ((int64_t)b * p.seqlen + tok0) * H;
-  for (int e = tid; e < HS_SEG * H; e += blockDim.x) {
-    const int t = e / H, h = e % H;
-    sm.c[t][h] = t < len ? dtb[(tok0 + t) * p.dt_sl + h] : 0.f;
-    sm.xs[t][h] = t < len ? xsw[(int64_t)t * H + h] : 0.f;
-  }
+  float* part = q.part + (((int64_t)b * p.nseg + si) * H) * 2;
+  T* dxb = reinterpret_cast<T*>(q.dx) + ((int64_t)b * p.seqlen + tok0) * H * HD;
+  float* ddtb = q.ddt + ((int64_t)b * p.seqlen + tok0) * H;
   hsb_load_g<T, HSB_MAXN>(p, q, sm.g, b, si, len);
-  __syncthreads();
-  for (int h = tid; h < H; h += blockDim.x) {
-    const float A = p.A[h];
-    float c = 0.f;
-    for (int t = 0; t < HS_SEG; ++t) {
-      const float d = t < len ? hs_dt(p, sm.c[t][h], h) : 0.f;
-      c += A * d;
-      sm.d[t][h] = d;
-      sm.c[t][h] = c;
-    }
-    sm.cend[h] = c;
-  }
-  // ---- P[h][t'] = Zin^h . g_t',  S1[h] = Zin^h . Lam^h
-  for (int e = tid; e < H * HS_SEG; e += blockDim.x) {
-    const int h = e / HS_SEG, t = e % HS_SEG;
-    const float* zr = zin + (int64_t)h * N;
-    float a = 0.f;
-    for (int n = 0; n < N; n += 4) {
-      const f32x4 z4 = *reinterpret_cast<const f32x4*>(zr + n);
-      a += z4[0] * sm.g[t][n] + z4[1] * sm.g[t][n + 1] + z4[2] * sm.g[t][n + 2] + z4[3] * sm.g[t][n + 3];
-    }
-    sm.P[h][t] = a;
-  }
-  for (int h = tid; h < H; h += blockDim.x) {
-    const float* zr = zin + (int64_t)h * N;
-    const float* lr = lam + (int64_t)h * N;
-    float a = 0.f;
-    for (int n = 0; n < N; n += 4) {
-      const f32x4 z4 = *reinterpret_cast<const f32x4*>(zr + n), l4 = *reinterpret_cast<const f32x4*>(lr + n);
-      a += z4[0] * l4[0] + z4[1] * l4[1] + z4[2] * l4[2] + z4[3] * l4[3];
-    }
-    sm.S1[h] = a;
-  }
   for (int gi = 0; gi < G; ++gi) {
-    __syncthreads();                   // c, d, g ready; the previous group's B, M, V no longer read
+    __syncthreads();                   // g stored; the previous group's B and dB no longer read
     {
       const T* Bb = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)gi * N;
-      for (int e = tid; e < HS_SEG * N; e += blockDim.x) {
-        const int t = e / N, n = e % N;
-        sm.Bt[t][n] = t < len ? to_f32(Bb[(tok0 + t) * p.B_sl + n]) : 0.f;
+      for (int e = tid; e < HS_SEG * HSB_MAXN; e += blockDim.x) {
+        const int s = e / HSB_MAXN, n = e % HSB_MAXN;
+        sm.B[s][n] = (s < len && n < N) ? to_f32(Bb[(tok0 + s) * p.B_sl + n]) : 0.f;
       }
     }
     __syncthreads();
-    // M[t'][s] = g_t' . B_s;  R[h][s] = Lam^h . B_s;  V[t][t'] = sum_{h in group} u_t e^{c_t' - c_t} (t' >= t)
-    for (int e = tid; e < HS_SEG * HS_SEG; e += blockDim.x) {
-      const int tp = e / HS_SEG, s_ = e % HS_SEG;
-      float a = 0.f;
-      for (int n = 0; n < N; ++n) a += sm.g[tp][n] * sm.Bt[s_][n];
-      sm.M[tp][s_] = a;
-      float v = 0.f;
-      const int t = tp, t2 = s_;        // V[t][t2], t2 >= t
-      if (t2 >= t)
-        for (int h = gi * hpg; h < (gi + 1) * hpg; ++h)
-          v += sm.d[t][h] * sm.xs[t][h] * __expf(sm.c[t2][h] - sm.c[t][h]);
-      sm.V[t][t2] = v;
-    }
-    for (int e = tid; e < hpg * HS_SEG; e += blockDim.x) {
-      const int h = gi * hpg + e / HS_SEG, s_ = e % HS_SEG;
-      const float* lr = lam + (int64_t)h * N;
-      float a = 0.f;
-      for (int n = 0; n < N; n += 4) {
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(lr + n);
-        a += l4[0] * sm.Bt[s_][n] + l4[1] * sm.Bt[s_][n + 1] + l4[2] * sm.Bt[s_][n + 2] + l4[3] * sm.Bt[s_][n + 3];
-      }
-      sm.R[h][s_] = a;
-    }
-    __syncthreads();
-    // Y columns, two heads per wave (lane half = head, lane % 32 = s), walking t from the segment end
-    for (int h0 = gi * hpg + 2 * w; h0 < (gi + 1) * hpg; h0 += 8) {
-      const int h = h0 + (l >> 5), s_ = l & 31;
-      const bool hv = h < (gi + 1) * hpg;
-      const int hh = hv ? h : h0;
-      const float cs = sm.c[s_][hh], us = sm.d[s_][hh] * sm.xs[s_][hh];
-      float y = 0.f;
-      for (int t = HS_SEG - 1; t >= 0; --t) {
-        const float an = t + 1 < HS_SEG ? __expf(sm.c[t + 1][hh] - sm.c[t][hh]) : 0.f;
-        y = sm.M[t][s_] + an * y;
-        const float cm1 = t > 0 ? sm.c[t - 1][hh] : 0.f;
-        float term = s_ < t ? __expf(cm1 - cs) * us * y : 0.f;
+    float acc[HS_SEG][2];              // this wave's part of dB for the group's heads it handles
 #pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) term += __shfl_xor(term, o, 64);
-        if (hv) {
-          if (s_ == t) sm.du[t][hh] = y + __expf(sm.cend[hh] - sm.c[t][hh]) * sm.R[hh][t];
-          if (s_ == 0) sm.q[t][hh] = term;
+    for (int s = 0; s < HS_SEG; ++s) acc[s][0] = acc[s][1] = 0.f;
+    // the global inputs of a head (raw dt and xs of token t, Zin and Lam of the lane's columns), loaded one
+    // head ahead so that their latency overlaps the previous head's work
+    const int hend = (gi + 1) * hpg;
+    float nraw = 0.f, nxs = 0.f;
+    float2 nz = {0.f, 0.f}, nl = {0.f, 0.f};
+    auto fetch = [&](int hh) {
+      nraw = tv ? dtb[(int64_t)t * p.dt_sl + hh] : 0.f;
+      nxs = tv ? xsw[(int64_t)t * H + hh] : 0.f;
+      if (n0 < N) {
+        nz = *reinterpret_cast<const float2*>(zin + (int64_t)hh * N + n0);
+        nl = *reinterpret_cast<const float2*>(lam + (int64_t)hh * N + n0);
+      }
+    };
+    if (gi * hpg + w < hend) fetch(gi * hpg + w);
+    for (int h = gi * hpg + w; h < hend; h += HSB_WAVES) {
+      // per-token scalars, token t in lanes t and t + 32
+      const float raw = nraw, xs = nxs;
+      float Z0 = nz.x, Z1 = nz.y, L0 = nl.x, L1 = nl.y;
+      if (h + HSB_WAVES < hend) fetch(h + HSB_WAVES);
+      const float A = p.A[h];
+      const float d = tv ? hs_dt(p, raw, h) : 0.f;
+      const float a = __expf(A * d);   // 1 past the end
+      const float u = d * xs;
+      // The segment in two halves of 16 tokens (Z_{s-1} kept for one half at a time): forward to Z_15, then
+      // for s = 16 .. 31 and again from Zin for s = 0 .. 15, Z_{s-1} of every token (Z_s = a_s Z_{s-1} + u_s B_s),
+      // and backward lambda_s = g_s + a_{s+1} lambda_{s+1} (lambda_31 = g_31 + Lam) with the lane partials of
+      // du_s = lambda_s . B_s and q_s = lambda_s . Z_{s-1}, and u_s lambda_s into dB.
+      const float Zi0 = Z0, Zi1 = Z1;
+#pragma unroll
+      for (int s = 0; s < HS_SEG / 2; ++s) {
+        const float as = hsb_readlane(a, s), us = hsb_readlane(u, s);
+        const float2 bv = *reinterpret_cast<const float2*>(&sm.B[s][n0]);
+        Z0 = as * Z0 + us * bv.x;
+        Z1 = as * Z1 + us * bv.y;
+      }
+      float r[2];
+#pragma unroll
+      for (int hf = 1; hf >= 0; --hf) {
+        const int s0 = 16 * hf;
+        if (hf == 0) {
+          Z0 = Zi0;
+          Z1 = Zi1;
+        }
+        float zp[16][2];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const int s = s0 + k;
+          zp[k][0] = Z0;
+          zp[k][1] = Z1;
+          if (k < 15) {
+            const float as = hsb_readlane(a, s), us = hsb_readlane(u, s);
+            const float2 bv = *reinterpret_cast<const float2*>(&sm.B[s][n0]);
+            Z0 = as * Z0 + us * bv.x;
+            Z1 = as * Z1 + us * bv.y;
+          }
+        }
+        float v[32];
+#pragma unroll
+        for (int k = 15; k >= 0; --k) {
+          const int s = s0 + k;
+          const float2 gv = *reinterpret_cast<const float2*>(&sm.g[s][n0]);
+          const float an = s == HS_SEG - 1 ? 1.f : hsb_readlane(a, s + 1);
+          L0 = gv.x + an * L0;
+          L1 = gv.y + an * L1;
+          const float2 bv = *reinterpret_cast<const float2*>(&sm.B[s][n0]);
+          v[k] = L0 * bv.x + L1 * bv.y;
+          v[16 + k] = L0 * zp[k][0] + L1 * zp[k][1];
+          const float us = hsb_readlane(u, s);
+          acc[s][0] += us * L0;
+          acc[s][1] += us * L1;
+        }
+        r[hf] = hsb_reduce_scatter(v);   // lanes 2k, 2k + 1: du_{s0 + k} (k < 16), q_{s0 + k - 16} (k >= 16)
+      }
+      const int src = (2 * t) & 31;
+      const float du0 = __shfl(r[0], src, 64), du1 = __shfl(r[1], src, 64);
+      const float q0 = __shfl(r[0], 32 + src, 64), q1 = __shfl(r[1], 32 + src, 64);
+      const float du = t < 16 ? du0 : du1, qv = t < 16 ? q0 : q1;
+      float dA = 0.f, db = 0.f;
+      if (l < 32 && tv) {
+        const float bias = p.dt_bias ? p.dt_bias[h] : 0.f;
+        const float ddr = (A * a * qv + xs * du) * hsb_dt_chain(p, raw, bias);
+        ddtb[(int64_t)t * H + h] = ddr;
+        dA = d * a * qv;
+        db = ddr;
+      }
+      dA = wave_sum(dA);
+      db = wave_sum(db);
+      if (l == 0) {
+        part[2 * h] = dA;
+        part[2 * h + 1] = db;
+      }
+      // dx[t][h][p] = dt_t du_t for every p: lane t writes the first half of the row, lane t + 32 the second
+      if (tv) {
+        const float dxs = d * du;
+        T* o = dxb + ((int64_t)t * H + h) * HD + (l >> 5) * (HD / 2);
+        if constexpr (sizeof(T) == 2) {
+          bf16x8 v8;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v8[j] = (bf16)dxs;
+#pragma unroll
+          for (int k = 0; k < HD / 16; ++k) *reinterpret_cast<bf16x8*>(o + 8 * k) = v8;
+        } else {
+#pragma unroll
+          for (int k = 0; k < HD / 8; ++k) *reinterpret_cast<f32x4*>(o + 4 * k) = f32x4{dxs, dxs, dxs, dxs};
         }
       }
     }
-    // dB_t[n] = sum_{t' >= t} V[t][t'] g_t'[n] + sum_{h in group} u_t e^{c_31 - c_t} Lam^h[n]
+    // dB of the group: the waves' parts added in wave order
+    for (int k = 0; k < HSB_WAVES; ++k) {
+      if (w == k) {
+#pragma unroll
+        for (int s = 0; s < HS_SEG; ++s) {
+          float2* o = reinterpret_cast<float2*>(&sm.dB[s][n0]);
+          const float2 prev = k == 0 ? float2{0.f, 0.f} : *o;
+          *o = float2{prev.x + acc[s][0], prev.y + acc[s][1]};
+        }
+      }
+      __syncthreads();
+    }
     T* dB = reinterpret_cast<T*>(q.dB) + ((int64_t)b * p.seqlen + tok0) * G * N + (int64_t)gi * N;
-    for (int e = tid; e < HS_SEG * N8; e += blockDim.x) {
-      const int t = e / N8, n0 = 8 * (e % N8);
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int tp = t; tp < HS_SEG; ++tp) {
-        float gv[8];
-        ld8f(&sm.g[tp][n0], gv);
-        const float v = sm.V[t][tp];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] += v * gv[j];
-      }
-      for (int h = gi * hpg; h < (gi + 1) * hpg; ++h) {
-        const float e2 = sm.d[t][h] * sm.xs[t][h] * __expf(sm.cend[h] - sm.c[t][h]);
-        const float* lr = lam + (int64_t)h * N + n0;
-        const f32x4 a4 = *reinterpret_cast<const f32x4*>(lr), b4 = *reinterpret_cast<const f32x4*>(lr + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[j] += e2 * a4[j];
-          acc[4 + j] += e2 * b4[j];
-        }
-      }
-      if (t < len) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) dB[(int64_t)t * G * N + n0 + j] = from_f32<T>(acc[j]);
-      }
-    }
-  }
-  __syncthreads();
-  // ---- per head: the remaining terms of q, then d dt, d xs and the dA / d_dt_bias partials
-  float* part = q.part + (((int64_t)b * p.nseg + si) * H) * 2;
-  for (int h = tid; h < H; h += blockDim.x) {
-    const float A = p.A[h], S1 = sm.S1[h], ce = sm.cend[h];
-    const float bias = p.dt_bias ? p.dt_bias[h] : 0.f;
-    float y2 = 0.f;
-    for (int t = HS_SEG - 1; t >= 0; --t) {
-      const float an = t + 1 < HS_SEG ? __expf(sm.c[t + 1][h] - sm.c[t][h]) : 0.f;
-      y2 = sm.P[h][t] + an * y2;
-      const float cm1 = t > 0 ? sm.c[t - 1][h] : 0.f;
-      sm.q[t][h] += __expf(cm1) * y2;
-    }
-    float acc = 0.f, dA = 0.f, db = 0.f;
-    for (int t = 0; t < HS_SEG; ++t) {
-      const float cm1 = t > 0 ? sm.c[t - 1][h] : 0.f;
-      const float ec = __expf(ce - sm.c[t][h]);
-      const float qv = sm.q[t][h] + ec * (__expf(cm1) * S1 + acc);
-      const float at = __expf(sm.c[t][h] - cm1);
-      const float d = sm.d[t][h], xs = sm.xs[t][h], du = sm.du[t][h];
-      acc = at * acc + d * xs * sm.R[h][t];
-      if (t < len) {
-        const float raw = dtb[(tok0 + t) * p.dt_sl + h];
-        const float ddr = (A * at * qv + xs * du) * hsb_dt_chain(p, raw, bias);
-        q.ddt[((int64_t)b * p.seqlen + tok0 + t) * H + h] = ddr;
-        dA += d * at * qv;
-        db += ddr;
-      }
-      sm.q[t][h] = d * du;               // d xs
-    }
-    part[2 * h] = dA;
-    part[2 * h + 1] = db;
-  }
-  __syncthreads();
-  // ---- dx[t][h][p] = d xs_t^h for every p
-  T* dx = reinterpret_cast<T*>(q.dx) + ((int64_t)b * p.seqlen + tok0) * H * HD;
-  for (int e = tid; e < len * H; e += blockDim.x) {
-    const int t = e / H, h = e % H;
-    const float v = sm.q[t][h];
-    T* o = dx + ((int64_t)t * H + h) * HD;
-    if constexpr (sizeof(T) == 2) {
-      bf16x8 v8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v8[j] = (bf16)v;
-#pragma unroll
-      for (int k = 0; k < HD / 8; ++k) *reinterpret_cast<bf16x8*>(o + 8 * k) = v8;
-    } else {
-#pragma unroll
-      for (int k = 0; k < HD / 4; ++k) *reinterpret_cast<f32x4*>(o + 4 * k) = f32x4{v, v, v, v};
+    for (int e = tid; e < len * N; e += blockDim.x) {
+      const int s = e / N, n = e % N;
+      dB[(int64_t)s * G * N + n] = from_f32<T>(sm.dB[s][n]);
     }
   }
 }
@@ -683,15 +715,12 @@ hipError_t launch_ssd_hs_bwd(const SsdParams& p, const HsParams& q, float* dh0, 
     hipLaunchKernelGGL(ssd_hsb_reduce_kernel, dim3((unsigned)((p.nheads + 3) / 4)), dim3(256), 0, st, p, q);
     return hipGetLastError();
   }
-  // the forward's local contributions and entering sums, then the adjoint's
-  if (bf) hipLaunchKernelGGL(ssd_hs_local_kernel<bf16>, grid, dim3(256), 0, st, p, q);
-  else hipLaunchKernelGGL(ssd_hs_local_kernel<float>, grid, dim3(256), 0, st, p, q);
-  hipLaunchKernelGGL(ssd_hs_carry_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, st, p, q);
-  if (bf) hipLaunchKernelGGL(ssd_hsb_local_kernel<bf16>, grid, dim3(256), 0, st, p, q);
-  else hipLaunchKernelGGL(ssd_hsb_local_kernel<float>, grid, dim3(256), 0, st, p, q);
+  // the segments' local sums of the state and of the adjoint, both carries, then the gradients
+  if (bf) hipLaunchKernelGGL(ssd_hsb_local_kernel<bf16>, grid, dim3(64 * HSB_WAVES_LOC), 0, st, p, q);
+  else hipLaunchKernelGGL(ssd_hsb_local_kernel<float>, grid, dim3(64 * HSB_WAVES_LOC), 0, st, p, q);
   hipLaunchKernelGGL(ssd_hsb_carry_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, st, p, q, dh0);
-  if (bf) hipLaunchKernelGGL(ssd_hsb_main_kernel<bf16>, grid, dim3(256), 0, st, p, q);
-  else hipLaunchKernelGGL(ssd_hsb_main_kernel<float>, grid, dim3(256), 0, st, p, q);
+  if (bf) hipLaunchKernelGGL(ssd_hsb_main_kernel<bf16>, grid, dim3(64 * HSB_WAVES), 0, st, p, q);
+  else hipLaunchKernelGGL(ssd_hsb_main_kernel<float>, grid, dim3(64 * HSB_WAVES), 0, st, p, q);
   hipLaunchKernelGGL(ssd_hsb_reduce_kernel, dim3((unsigned)((p.nheads + 3) / 4)), dim3(256), 0, st, p, q);
   return hipGetLastError();
 }
