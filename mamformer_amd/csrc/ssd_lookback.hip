@@ -721,7 +721,9 @@ __global__ __launch_bounds__(64 * HG * (2 / PH)) void ssd_lb_scan_kernel(SsdPara
         }
     }
   }
-  wait_vmem_n<LOADS>();                                    // the first decay block (segment 0's tiles may fly)
+  // the first decay block: a fetching wave lets its segment-0 tile loads fly, the others have none in flight
+  if (w >= NW - LbFetch<N, HG, NW>::ND) wait_vmem_n<LOADS>();
+  else wait_vmem();
   lb_dt_form(p, c, dec, 0);
   if (nseg > 1) lb_scan_fetch<N, HG, NW>(p, c, &sm.st[1], 1);
 
