@@ -558,6 +558,7 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
   // e^LB_FACT_RANGE, so a segment whose decay range exceeds it takes several passes (a token's own decay,
   // however large, is applied to the state at the start of its pass)
   int a = 0;
+  bf16x4 yb[PH][2][4];                                     // without the gate: the segment's y pieces over the passes
   for (int pass = 0;; ++pass) {
     // the tile reads of a pass stay inside the pass loop (hoisted, the C and B fragments would hold their
     // registers through it): the tile pointers are offset by an opaque zero
@@ -598,9 +599,10 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
       Y[ph][1] = mma(xa[ph][3], mt[320 + l], Y[ph][1]);
     }
     // ---- epilogue: y[t][p] = rs_t Y^T[p][t] + D_p x[t][p] (times silu(z[t][p]) with the gate) for the pass's
-    // tokens, stored from the accumulator layout (lane = token t, 8-byte pieces of 4 columns).  Before the
-    // first stores: every load of this wave is complete, in particular the next segment's tiles.
-    if (pass == 0) wait_vmem();
+    // tokens, in the accumulator layout (lane = token t, 8-byte pieces of 4 columns).  With the gate they are
+    // stored from there (before the first stores every load of this wave is complete, in particular the next
+    // segment's tiles); without it they are kept for the segment's row-chunk stores below.
+    if (GATE && pass == 0) wait_vmem();
 #pragma unroll
     for (int ph = 0; ph < PH; ++ph) {
       const bf16* xt = xwp + ph * Sub64::ELEMS;
@@ -616,7 +618,7 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int t = 32 * tt + l32;
-        if (t >= a && t < bnd && pos + t < c.c1) {
+        if (t >= a && t < bnd && (!GATE || pos + t < c.c1)) {
           bf16* yrow = yg + (int64_t)(pos + t) * p.y_sl + 32 * ph + 4 * half;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -627,13 +629,39 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
               if constexpr (GATE) yv *= silu_f((float)zq[ph][tt][q][i]);
               yo[i] = (bf16)yv;
             }
-            *reinterpret_cast<bf16x4*>(yrow + 8 * q) = yo;
+            if constexpr (GATE) *reinterpret_cast<bf16x4*>(yrow + 8 * q) = yo;
+            else yb[ph][tt][q] = yo;
           }
         }
       }
     }
     if (bnd >= SEG) break;
     a = bnd;
+  }
+  if constexpr (!GATE) {
+    // y through the wave's own x sub-tile (no longer read; the same swizzled layout) into 16-byte row chunks:
+    // a store instruction then writes 16 rows of 64 contiguous bytes instead of 32 rows of 16, which the
+    // memory system drains at about twice the rate.  Before the stores: every load of this wave is complete,
+    // in particular the next segment's tiles.
+#pragma unroll
+    for (int ph = 0; ph < PH; ++ph) {
+      bf16* ys = &cur->X[c.hw][c.ph0][0] + ph * Sub64::ELEMS;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) *reinterpret_cast<bf16x4*>(ys + 32 * tt * Sub64::W + lo.piece[q]) = yb[ph][tt][q];
+    }
+    wait_vmem();
+#pragma unroll
+    for (int ph = 0; ph < PH; ++ph) {
+      const bf16* ys = &cur->X[c.hw][c.ph0][0] + ph * Sub64::ELEMS;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = (l >> 2) + 16 * j, ch = l & 3;
+        const uint4 v = *reinterpret_cast<const uint4*>(ys + Sub64::off(r, 8 * ch));
+        if (pos + r < c.c1) *reinterpret_cast<uint4*>(yg + (int64_t)(pos + r) * p.y_sl + 32 * ph + 8 * ch) = v;
+      }
+    }
   }
   kappa += cse;
   if (dnext) lb_dt_form(p, c, dec, si + 1);                // its dt was waited for before the y stores
