@@ -380,7 +380,8 @@ struct GradSmem {
   float rowg[3][32];             // per XD^T tile (s-block, t-block) = (0,0), (0,1), (1,1): sum_s (M o XD)[t][s] dt_s
   float lh[N / 32];              // <lam_out, h_in> per n-block
   float dd[2];                   // trace of dy x^T per diagonal 32-block
-  float cb[3][64 * 16];          // CB[t][s] tiles (t-block, s-block) = (0,0), (1,0), (1,1), accumulator order
+  alignas(16) float cb[3][64 * 16];   // CB[t][s] tiles (t-block, s-block) = (0,0), (1,0), (1,1), accumulator
+                                      // order (16-byte aligned: read and written as f32x4)
   float cbt[3][64 * 16];         // CB^T[s][t] tiles (s-block, t-block) = (0,0), (0,1), (1,1)
 };
 constexpr size_t GRAD_LDS = 160 * 1024;
