@@ -28,6 +28,8 @@ constexpr int HS_SEG = 32;       // tokens per segment
 constexpr int HS_MAXH = 128;     // heads held in LDS
 constexpr int HS_MAXN = 256;
 constexpr int HS_ZH = 32;        // heads of entering sums staged in LDS at a time
+constexpr int HS_HP = HS_MAXH + 1;   // row pitch of the per-(token, head) arrays: a column (one head, 32 tokens)
+                                     // then spans 32 banks
 constexpr float PR = 80.f;       // largest in-segment range of c factorised as E F
 
 __device__ __forceinline__ float hs_dt(const SsdParams& p, float d, int h) {
@@ -38,11 +40,11 @@ __device__ __forceinline__ float hs_dt(const SsdParams& p, float d, int h) {
 }
 
 struct HsSmem {
-  float c[HS_SEG][HS_MAXH];      // raw dt, then the in-segment inclusive cumsum of A dt (flat past the end)
-  float u[HS_SEG][HS_MAXH];      // dt xs (0 past the end); local pass: e^{c_end - c_s} dt xs
-  float E[HS_SEG][HS_MAXH];      // out pass: e^{c_t - m}
-  float F[HS_SEG][HS_MAXH];      // out pass: e^{m - c_s} u_s
-  float Ei[HS_SEG][HS_MAXH];     // out pass: e^{c_t}
+  float c[HS_SEG][HS_HP];        // raw dt, then the in-segment inclusive cumsum of A dt (flat past the end)
+  float u[HS_SEG][HS_HP];        // dt xs (0 past the end); local pass: e^{c_end - c_s} dt xs
+  float E[HS_SEG][HS_HP];        // out pass: e^{c_t - m}
+  float F[HS_SEG][HS_HP];        // out pass: e^{m - c_s} u_s
+  float Ei[HS_SEG][HS_HP];       // out pass: e^{c_t}
   float Bt[HS_SEG][HS_MAXN];     // B of one group
   float Zs[HS_ZH][HS_MAXN];      // out pass: entering state sums of HS_ZH heads
   float W[HS_SEG][HS_SEG + 4];   // W_g[t][s]
@@ -366,8 +368,8 @@ __device__ void hsb_load_g(const SsdParams& p, const HsParams& q, float (*g)[W],
 }
 
 struct HsbLocSmem {
-  float c[HS_SEG][HSB_MAXH];     // as in HsSmem
-  float u[HS_SEG][HSB_MAXH];
+  float c[HS_SEG][HS_HP];        // as in HsSmem
+  float u[HS_SEG][HS_HP];
   float g[HS_SEG][HSB_MAXN];     // ghs / (H P) (0 past the end and beyond N)
   float B[HS_SEG][HSB_MAXN];     // B of one group (likewise)
   float cend[HSB_MAXH], mid[HSB_MAXH];
