@@ -29,6 +29,7 @@
 // along rows (two 8-byte reads) or down columns (eight 2-byte reads), so no transposed copies are kept.
 #include "common.h"
 #include "launch.h"
+#include "tiles.h"
 
 namespace mh {
 
@@ -58,21 +59,9 @@ __device__ __forceinline__ Frag<bf16> frag_row(const bf16* M, int pitch, int r0,
   }
   return f;
 }
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-
-// Fragment with k-values M[k0 + KSET(half, j)][c0 + l32] (k runs down a column of M), by two transposing reads
-// (ds_read_b64_tr_b16: within each 16-lane group, lanes 4r..4r+3 name 16 consecutive elements of row r = 0..3 and
-// lane i of the group receives element i of the four rows): rows k0 + 4 half + 0..3, then 8 further down.
-// Requires 8-byte aligned rows (every pitch here is a multiple of 8 elements) and c0 % 32 == 0.
+// Fragment with k-values M[k0 + KSET(half, j)][c0 + l32] (k runs down a column of M): two transposing reads.
 __device__ __forceinline__ Frag<bf16> frag_col(const bf16* M, int pitch, int c0, int k0) {
-  const int l = lane_id(), half = l >> 5, i = l & 15;
-  const bf16* p = M + (k0 + 4 * half + (i >> 2)) * pitch + c0 + 16 * ((l >> 4) & 1) + 4 * (i & 3);
-  const i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
-  const i16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 8 * pitch));
-  Frag<bf16> f;
-  f.v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
-  return f;
+  return col_frag_tr(M, pitch, c0, k0);
 }
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }

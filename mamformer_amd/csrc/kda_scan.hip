@@ -643,9 +643,7 @@ __global__ __launch_bounds__(256 * NQ) void kda_ref_kernel(KdaParams p) {
     // ---- phase D: per wave (v-tile vt, k-half kh)
     Frag<TM> vf[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) vf[c].set(j, (float)sm.V[(16 * c + kset(half, j)) * SM::PV + 32 * vt + l32]);
+    for (int c = 0; c < 4; ++c) vf[c] = col_frag_tr(sm.V, SM::PV, 32 * vt, 16 * c);
 
     // read-out of this wave's query stream qw: o[tt] for both t-tiles over this wave's k-half
     f32x16 o[2];
@@ -692,15 +690,9 @@ __global__ __launch_bounds__(256 * NQ) void kda_ref_kernel(KdaParams p) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int kt = 2 * kh + i;
-      const int krow = 32 * kt + l32;
       f32x16 acc = St[i];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        Frag<TM> kf;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) kf.v[j] = sm.Kt[(16 * c + kset(half, j)) * SM::PK + krow];
-        acc = mma(kf, vf[c], acc);
-      }
+      for (int c = 0; c < 4; ++c) acc = mma(col_frag_tr(sm.Kt, SM::PK, 32 * kt, 16 * c), vf[c], acc);
       St[i] = acc;
     }
     __syncthreads();

@@ -252,6 +252,24 @@ __device__ __forceinline__ Frag<TM> xrow_frag(const T* tile, int r, int e0) {
   }
   return f;
 }
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+
+// Fragment with k-values M[k0 + KSET(half, j)][c0 + lane % 32] (k runs down a column of a row-major bf16 LDS
+// tile of the given pitch), by two transposing reads (ds_read_b64_tr_b16: within each 16-lane group, lanes
+// 4r..4r+3 name 4 consecutive elements each of row r = 0..3, 16 in all, and lane i of the group receives element
+// i of the four rows): rows k0 + 4 half + 0..3, then 8 further down.  Rows 8-byte aligned (pitch % 4 == 0),
+// c0 % 32 == 0.
+__device__ __forceinline__ Frag<bf16> col_frag_tr(const bf16* M, int pitch, int c0, int k0) {
+  const int l = threadIdx.x & 63, half = l >> 5, i = l & 15;
+  const bf16* p = M + (k0 + 4 * half + (i >> 2)) * pitch + c0 + 16 * ((l >> 4) & 1) + 4 * (i & 3);
+  const i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
+  const i16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 8 * pitch));
+  Frag<bf16> f;
+  f.v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+  return f;
+}
+
 // KSET fragment of row r (base % 16 == 0): columns base+4*half+{0..3} and base+8+4*half+{0..3}.
 template <typename TM, typename T, int W>
 __device__ __forceinline__ Frag<TM> kset_frag(const T* tile, int r, int base, int half) {
