@@ -73,11 +73,11 @@ template <> struct StateBlk<float> {
 template <typename T>
 __device__ __forceinline__ StateBlk<T> load_state_blk(const T* base, int nt, int pt, int l) {
   StateBlk<T> s;
-  const T* q = base + frag_off(nt, pt, l);
   if constexpr (sizeof(T) == 2) {
-    s.v[0] = *reinterpret_cast<const bf16x8*>(q);
-    s.v[1] = *reinterpret_cast<const bf16x8*>(q + 8);
+    s.v[0] = *reinterpret_cast<const bf16x8*>(base + frag_off_bf(nt, pt, l, 0));
+    s.v[1] = *reinterpret_cast<const bf16x8*>(base + frag_off_bf(nt, pt, l, 1));
   } else {
+    const T* q = base + frag_off(nt, pt, l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) s.v[i] = *reinterpret_cast<const f32x4*>(q + 4 * i);
   }
@@ -85,14 +85,14 @@ __device__ __forceinline__ StateBlk<T> load_state_blk(const T* base, int nt, int
 }
 template <typename T>
 __device__ __forceinline__ void store_state_blk(T* base, int nt, int pt, int l, const f32x16& a) {
-  T* q = base + frag_off(nt, pt, l);
   if constexpr (sizeof(T) == 2) {
     bf16x8 lo, hi;
 #pragma unroll
     for (int i = 0; i < 8; ++i) { lo[i] = (bf16)a[i]; hi[i] = (bf16)a[8 + i]; }
-    *reinterpret_cast<bf16x8*>(q) = lo;
-    *reinterpret_cast<bf16x8*>(q + 8) = hi;
+    *reinterpret_cast<bf16x8*>(base + frag_off_bf(nt, pt, l, 0)) = lo;
+    *reinterpret_cast<bf16x8*>(base + frag_off_bf(nt, pt, l, 1)) = hi;
   } else {
+    T* q = base + frag_off(nt, pt, l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f32x4 v;

@@ -378,14 +378,12 @@ __global__ __launch_bounds__(64 * HG * (2 / PH)) void ssd_lb_state_kernel(SsdPar
   for (int ph = 0; ph < PH; ++ph)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      bf16x8* o8 = reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(p.chunk_states) + obase +
-                                             frag_off(nt, c.ph0 + ph, l));
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         bf16x8 v;
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = (bf16)S[ph][nt][8 * q + i];
-        o8[q] = v;
+        *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(p.chunk_states) + obase + frag_off_bf(nt, c.ph0 + ph, l, q)) = v;
       }
     }
   if (c.ph0 == 0 && l == 0) p.chunk_decay[((int64_t)b * p.nheads + h) * p.nchunks + k] = R;
@@ -698,7 +696,7 @@ __global__ __launch_bounds__(64 * HG * (2 / PH)) void ssd_lb_scan_kernel(SsdPara
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int q = 0; q < 2; ++q)
-          v[ph][nt][q] = reinterpret_cast<const bf16x8*>(s + frag_off(nt, ph0 + ph, l))[q];
+          v[ph][nt][q] = *reinterpret_cast<const bf16x8*>(s + frag_off_bf(nt, ph0 + ph, l, q));
   };
   if (p.entering) {
     // entering states precomputed by ssd_state_pass_kernel (bf16, fragment order)

@@ -42,7 +42,7 @@
 // head's x tile, so it stages its y columns in place of x and writes them to
 // HBM one segment later.  LDS tiles are XOR-swizzled per row for
 // conflict-free fragment reads; the chunk-state workspace is kept in MFMA
-// fragment order (64 contiguous bytes per lane).
+// fragment order (frag_off / frag_off_bf).
 // bf16 I/O uses 32x32x16 bf16 MFMAs, fp32 I/O 32x32x2 fp32 MFMAs; accumulation is fp32.
 #include "common.h"
 #include "launch.h"
@@ -361,13 +361,12 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_state_kernel(SsdParams p) 
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     if constexpr (sizeof(T) == 2) {
-      bf16x8* o8 = reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(p.chunk_states) + obase + frag_off(nt, ph, l));
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         bf16x8 v;
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = (bf16)S[nt][8 * q + i];
-        o8[q] = v;
+        *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(p.chunk_states) + obase + frag_off_bf(nt, ph, l, q)) = v;
       }
     } else {
       f32x4* o4 = reinterpret_cast<f32x4*>(p.chunk_states + obase + frag_off(nt, ph, l));
@@ -397,7 +396,9 @@ __global__ __launch_bounds__(256) void ssd_state_pass_kernel(SsdParams p) {
   const int per = HD * p.dstate;                  // state elements per (b, h)
   const int e8 = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (e8 >= per) return;
-  const int ci0 = canon_index(e8, p.dstate, p.state_perm), ci1 = canon_index(e8 + 4, p.dstate, p.state_perm);   // two runs of 4 canonical n
+  const bool bfs = sizeof(TE) == 2;               // bf16 states in the frag_off_bf order
+  const int ci0 = canon_index(e8, p.dstate, p.state_perm, bfs);   // two runs of 4 canonical n
+  const int ci1 = canon_index(e8 + 4, p.dstate, p.state_perm, bfs);
   f32x4 H[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) H[u][0] = H[u][1] = H[u][2] = H[u][3] = 0.f;
@@ -503,11 +504,10 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       if constexpr (sizeof(T) == 2) {
-        const bf16x8* h8 = reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.entering) + hidx +
-                                                           frag_off(nt, ph, l));
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-          const bf16x8 v = h8[q];
+          const bf16x8 v = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.entering) + hidx +
+                                                             frag_off_bf(nt, ph, l, q));
 #pragma unroll
           for (int i = 0; i < 8; ++i) H[nt][8 * q + i] = (float)v[i];
         }
