@@ -151,6 +151,21 @@ __device__ __forceinline__ Frag<T> scaled(Frag<T> f, float s) {
   return f;
 }
 
+// Operand fragments f[c] of the transposed 32x32 block of a Tile<T, W> at rows r0.., columns q0..: lane = column
+// q0 + lane % 32, k = row r0 + 16 c + KSET.  bf16: two transposing LDS reads each; fp32: the identity product.
+template <typename T, int W>
+__device__ __forceinline__ void tr_frags(const T* tile, int r0, int q0, const Frag<T> (&id)[2], int half, int l32,
+                                         Frag<T> (&f)[2]) {
+  if constexpr (sizeof(T) == 2) {
+    f[0] = col_frag_tr_tile<W>(tile, q0, r0);
+    f[1] = col_frag_tr_tile<W>(tile, q0, r0 + 16);
+  } else {
+    const f32x16 d = mfma_transpose<T, T, W>(tile, r0, q0, id, half, l32);
+    f[0] = acc_to_frag<T>(d, 0);
+    f[1] = acc_to_frag<T>(d, 1);
+  }
+}
+
 // x^T-style transpose of a 32-column half tile (XHalf layout): D[r][q] = tile[r0 + r][q], lane = column q.
 template <typename T>
 __device__ __forceinline__ f32x16 xhalf_transpose(const T* tile, int r0, const Frag<T> (&id)[2], int half, int l32) {
@@ -310,16 +325,17 @@ __global__ __launch_bounds__(64 * (2 * (N / 32) + 2)) void ssd_bwd_sweep_kernel(
     f32x16 acc = zero16();
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
-      const f32x16 mt = mfma_transpose<T, T, N>(sm.st[s].M, 32 * tb, 32 * nt, id, half, l32);    // [t][n]
-      const f32x16 vt = mfma_transpose<T, T, HD>(sm.st[s].V, 32 * tb, 32 * pt, id, half, l32);  // [t][p]
+      Frag<T> mf[2], vf[2];
+      tr_frags<T, N>(sm.st[s].M, 32 * tb, 32 * nt, id, half, l32, mf);    // lane n, k = t
+      tr_frags<T, HD>(sm.st[s].V, 32 * tb, 32 * pt, id, half, l32, vf);   // lane p, k = t
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         float e[8];
         kset_vals(sm.w[w], 2 * tb + c, half, e);
         Frag<T> a;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a.set(j, mt[8 * c + j] * e[j]);
-        acc = mma(a, acc_to_frag<T>(vt, c), acc);       // [n][p] += sum_t M[t][n] w_t V[t][p]
+        for (int j = 0; j < 8; ++j) a.set(j, mf[c].get(j) * e[j]);
+        acc = mma(a, vf[c], acc);                        // [n][p] += sum_t M[t][n] w_t V[t][p]
       }
     }
     const float dec = __expf(cend);
@@ -689,11 +705,12 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb) {
         if (tb >= r) {
-          const f32x16 ct = mfma_transpose<T, T, N>(sm.C, 32 * tb, 32 * nb, id, half, l32);   // [t][n]
+          Frag<T> ct[2];
+          tr_frags<T, N>(sm.C, 32 * tb, 32 * nb, id, half, l32, ct);   // lane n, k = t
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
-            if constexpr (SHARE) aa = mma(acc_to_frag<T>(ct, c), sm.xds.xd[r == 0 ? tb : 2][c][l], aa);
-            else aa = mma(acc_to_frag<T>(ct, c), XDf[tb][c], aa);
+            if constexpr (SHARE) aa = mma(ct[c], sm.xds.xd[r == 0 ? tb : 2][c][l], aa);
+            else aa = mma(ct[c], XDf[tb][c], aa);
           }
         }
       }
@@ -777,11 +794,12 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         if (sb <= r) {
-          const f32x16 bt = mfma_transpose<T, T, N>(sm.B, 32 * sb, 32 * nb, id, half, l32);   // [s][n]
+          Frag<T> bt[2];
+          tr_frags<T, N>(sm.B, 32 * sb, 32 * nb, id, half, l32, bt);   // lane n, k = s
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
-            if constexpr (SHARE) ac = mma(acc_to_frag<T>(bt, c), sm.xds.xt[r == 0 ? 0 : (sb == 0 ? 1 : 2)][c][l], ac);
-            else ac = mma(acc_to_frag<T>(bt, c), XTf[sb][c], ac);
+            if constexpr (SHARE) ac = mma(bt[c], sm.xds.xt[r == 0 ? 0 : (sb == 0 ? 1 : 2)][c][l], ac);
+            else ac = mma(bt[c], XTf[sb][c], ac);
           }
         }
       }
@@ -824,9 +842,10 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
               const int t = 32 * tb + acc_row(half, i);
               m[i] = (t < len && t >= s_x) ? m[i] * __expf(ct[i] - csx) : 0.f;
             }
-            const f32x16 dyt = mfma_transpose<T, T, HD>(sg.DY, 32 * tb, 32 * pb, id, half, l32);   // [t][p]
+            Frag<T> dyt[2];
+            tr_frags<T, HD>(sg.DY, 32 * tb, 32 * pb, id, half, l32, dyt);   // lane p, k = t
 #pragma unroll
-            for (int c = 0; c < 2; ++c) ax = mma(acc_to_frag<T>(dyt, c), acc_to_frag<T>(m, c), ax);
+            for (int c = 0; c < 2; ++c) ax = mma(dyt[c], acc_to_frag<T>(m, c), ax);
           }
         }
       }

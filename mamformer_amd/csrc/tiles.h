@@ -270,6 +270,22 @@ __device__ __forceinline__ Frag<bf16> col_frag_tr(const bf16* M, int pitch, int 
   return f;
 }
 
+// The same fragment from a swizzled Tile<bf16, W> (k = row, c0 % 32 == 0): each lane's 8-byte piece lies inside
+// one 16-byte chunk, whose place in its row the swizzle gives.
+template <int W>
+__device__ __forceinline__ Frag<bf16> col_frag_tr_tile(const bf16* M, int c0, int k0) {
+  using TL = Tile<bf16, W>;
+  const int l = threadIdx.x & 63, half = l >> 5, i = l & 15;
+  const int r = k0 + 4 * half + (i >> 2), col = c0 + 16 * ((l >> 4) & 1) + 4 * (i & 3);
+  const bf16* p0 = M + TL::chunk(r, col >> 3) + (col & 7);
+  const bf16* p1 = M + TL::chunk(r + 8, col >> 3) + (col & 7);
+  const i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p0));
+  const i16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p1));
+  Frag<bf16> f;
+  f.v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+  return f;
+}
+
 // KSET fragment of row r (base % 16 == 0): columns base+4*half+{0..3} and base+8+4*half+{0..3}.
 template <typename TM, typename T, int W>
 __device__ __forceinline__ Frag<TM> kset_frag(const T* tile, int r, int base, int half) {
