@@ -29,8 +29,13 @@ typedef __attribute__((address_space(1))) void glb_void_t;
 // ------------------------------------------------------------------ LDS tiles
 
 // B / C tiles: SEG rows of W elements, unpadded, 16-byte chunks XOR-swizzled by
-// row (chunk c of row r lives at chunk c ^ (r & MASK)) so the lanes of one LDS
-// access phase, reading the same column of consecutive rows, hit distinct banks.
+// row (chunk c of row r lives at chunk c ^ swz(r)) so the lanes of one LDS
+// access phase hit distinct banks.  bf16 rows of 128 and 64 elements use swizzles
+// under which both access shapes are conflict-free, whether the LDS has 32 or 64
+// banks: 16-byte reads of one chunk in 8 or 16 consecutive rows, and the
+// transposing reads (ds_read_b64_tr_b16), whose 16- or 32-lane phase reads 32 or
+// 64 contiguous bytes of each of 4 consecutive rows (the rows' chunk sets then
+// differ in bits 1-2 and in bits 2-3 of the chunk index).  Other tiles use r & MASK.
 template <typename T, int W>
 struct Tile {
   static constexpr int EPC = 16 / (int)sizeof(T);   // elements per 16-byte chunk
@@ -38,7 +43,15 @@ struct Tile {
   static constexpr int MASK = (CPR < 16 ? CPR : 16) - 1;
   static constexpr int RPB = 64 / CPR;              // rows per 1 KB block (one wave-wide direct load)
   static constexpr int NBLK = SEG / RPB;            // 1 KB blocks per tile
-  __device__ static __forceinline__ int chunk(int r, int c) { return r * W + (c ^ (r & MASK)) * EPC; }
+  __device__ static __forceinline__ int swz(int r) {
+    if constexpr (sizeof(T) == 2 && W == 128)
+      return (((r ^ (r >> 3)) & 1) << 3) | (((r >> 1) & 1) << 2) | ((r & 1) << 1) | ((r >> 2) & 1);
+    else if constexpr (sizeof(T) == 2 && W == 64)
+      return (((r >> 1) & 1) << 2) | (((r ^ (r >> 1) ^ (r >> 3)) & 1) << 1) | ((r >> 2) & 1);
+    else
+      return r & MASK;
+  }
+  __device__ static __forceinline__ int chunk(int r, int c) { return r * W + (c ^ swz(r)) * EPC; }
 };
 
 // One wave's half of a head's x tile: SEG token rows x 32 columns.  Rows of 64
@@ -99,7 +112,7 @@ __device__ __forceinline__ void fetch_tile(T* dst, const T* src, int64_t row_str
   for (int q = 0; q < nblk; ++q) {
     const int blk = blk0 + q;
     const int r = blk * TL::RPB + rr;
-    const int c = phys ^ (r & TL::MASK);
+    const int c = phys ^ TL::swz(r);
     const uint32_t off = (uint32_t)(min(r, rmax) * (int)row_stride + c * TL::EPC) * (uint32_t)sizeof(T);
     dma_lds<16>(base, off, dst + blk * (1024 / (int)sizeof(T)));
   }
