@@ -37,7 +37,7 @@ namespace {
 
 constexpr int BC = 64;       // tokens per chunk
 constexpr int BD = 128;      // dk = dv
-constexpr int P128 = 136;    // bf16 row pitch of 128-wide tiles
+constexpr int P128 = 152;    // bf16 row pitch of 128-wide tiles (76 words: transposing and row reads spread over the banks)
 constexpr int P64 = 72;      // bf16 row pitch of 64-wide tiles
 constexpr int NT = 512;      // threads per workgroup
 constexpr int SEG_PARTS = 2; // workgroups per segment in the segment-sum pass

@@ -426,7 +426,7 @@ __device__ __forceinline__ float phi1(float x) { return x > 0.f ? x + 1.f : __ex
 
 template <int NQ>
 struct KdaRefSmem {
-  static constexpr int PK = DK + 8;      // bf16 row pitch
+  static constexpr int PK = DK + 24;     // bf16 row pitch (76 words: transposing and row reads spread over the banks)
   static constexpr int PV = DVH + 8;
   bf16 Q[NQ][SEGK * PK];                 // phi(q_i)
   bf16 Kt[SEGK * PK];                    // phi(k), zero rows beyond the segment
