@@ -427,11 +427,11 @@ __device__ __forceinline__ float phi1(float x) { return x > 0.f ? x + 1.f : __ex
 template <int NQ>
 struct KdaRefSmem {
   static constexpr int PK = DK + 24;     // bf16 row pitch (76 words: transposing and row reads spread over the banks)
-  static constexpr int PV = DVH + 8;
+  static constexpr int PV = DVH + 32;    // 48 words: the transposing reads of V spread over the banks
   bf16 Q[NQ][SEGK * PK];                 // phi(q_i)
   bf16 Kt[SEGK * PK];                    // phi(k), zero rows beyond the segment
   bf16 V[SEGK * PV];                     // v[:, V-half], zero rows beyond the segment
-  float z[DK];                           // running sum of phi(k) before this segment
+  alignas(16) float z[DK];               // running sum of phi(k) before this segment
   float zq[NQ][SEGK];                    // phi(q_i,t) . z
   float nrm[NQ][3][32];                  // row sums of the masked A tiles
   f32x16 red[2][NQ][2][64];              // k-half 1 read-out partials: vt, query, t-tile, lane
@@ -582,8 +582,10 @@ __global__ __launch_bounds__(256 * NQ) void kda_ref_kernel(KdaParams p) {
 #pragma unroll
       for (int c = 0; c < 32; c += 8) {
         const bf16x8 q8 = *reinterpret_cast<const bf16x8*>(row + c);
+        const f32x4 z0 = *reinterpret_cast<const f32x4*>(&sm.z[32 * qq + c]);
+        const f32x4 z1 = *reinterpret_cast<const f32x4*>(&sm.z[32 * qq + c + 4]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc += (float)q8[j] * sm.z[32 * qq + c + j];
+        for (int j = 0; j < 8; ++j) acc += (float)q8[j] * (j < 4 ? z0[j] : z1[j - 4]);
       }
       acc += __shfl_xor(acc, 1, 64);
       acc += __shfl_xor(acc, 2, 64);
