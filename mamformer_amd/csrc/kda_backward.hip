@@ -82,7 +82,7 @@ struct QSmem {
   bf16 DN[BC * P128];     // raw output gradient, then dnum
   bf16 AM[BC * P64];      // A'[t][s] = phi'(q_t) . phi'(k_s) (s <= t)
   bf16 GM[BC * P64];      // G[t][s] (s <= t)
-  bf16 SB[BD * P128];     // S' before this chunk (bf16)
+  bf16 SB[BD * P128];     // S' before this chunk (bf16), transposed: row d, column k
   float z[2][BD];         // z' before this chunk / after it
   float vs[2][BD];        // Vsum
   float cs[2][BD];        // column sums of S' over k < kernel_dim (= sum_s K1_s v_s)
@@ -117,7 +117,7 @@ struct KVSmem {
   bf16 DN[BC * P128];     // g
   bf16 WT[BC * P64];      // W^T[s][t] = phi(k_s) . Psi_t   (s <= t)
   bf16 MT[BC * P64];      // M^T[s][t] = g_t . v_s          (s <= t)
-  bf16 SB[BD * P128];     // dS[k][d] (bf16)
+  bf16 SB[BD * P128];     // dS (bf16), transposed: row d, column k
   float dz[BD];
   float part[4][BD];      // per 16-token quarter: sums of Xi
 };
@@ -263,11 +263,16 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
       *reinterpret_cast<bf16x8*>(&sm.VV[t * P128 + c0]) = vo;
       *reinterpret_cast<bf16x8*>(&sm.DN[t * P128 + c0]) = doo;
     }
+    // S'^T: the lane's column d holds 4 consecutive k per accumulator group, one 8-byte store each
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        sm.SB[(32 * (2 * tt + i) + acc_row(half, r)) * P128 + 32 * dt + l32] = (bf16)Sacc[i][r];
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (bf16)Sacc[i][4 * g + j];
+        *reinterpret_cast<bf16x4*>(&sm.SB[(32 * dt + l32) * P128 + 32 * (2 * tt + i) + 8 * g + 4 * half]) = v;
+      }
     lds_barrier();
 
     // ---- phase 1: A' tiles (t-block, s-block) = (0,0), (1,0), (1,1) by waves 0..2, computed transposed so
@@ -324,7 +329,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
     f32x16 u = zero16(), vsum = zero16();
 #pragma unroll
     for (int c = 0; c < BD / 16; ++c)
-      u = mma(frag_col(sm.SB, P128, 32 * dt, 16 * c), frag_row(sm.PQ, P128, 32 * tt, 16 * c), u);
+      u = mma(frag_row(sm.SB, P128, 32 * dt, 16 * c), frag_row(sm.PQ, P128, 32 * tt, 16 * c), u);
     for (int c = 0; c < ns; ++c) {
       const Frag<bf16> vf = frag_col(sm.VV, P128, 32 * dt, 16 * c);
       u = mma(vf, frag_row(sm.AM, P64, 32 * tt, 16 * c), u);
@@ -424,7 +429,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
         gq = mma(frag_col(sm.PK, P128, 32 * kt, 16 * c), frag_row(sm.GM, P64, 32 * tt, 16 * c), gq);
 #pragma unroll
       for (int c = 0; c < BD / 16; ++c)
-        gq = mma(frag_row(sm.SB, P128, 32 * kt, 16 * c), frag_row(sm.DN, P128, 32 * tt, 16 * c), gq);
+        gq = mma(frag_col(sm.SB, P128, 32 * kt, 16 * c), frag_row(sm.DN, P128, 32 * tt, 16 * c), gq);
       if (tin) {
         const float dn = sm.dnn[t], R = sm.rr[t];
         bf16* out = dqp + (rowbase + pos + t) * BD + 32 * kt;
@@ -652,16 +657,20 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        sm.SB[(32 * (ktb + i) + acc_row(half, r)) * P128 + 32 * dt + l32] = (bf16)dS[i][r];
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (bf16)dS[i][4 * g + j];
+        *reinterpret_cast<bf16x4*>(&sm.SB[(32 * dt + l32) * P128 + 32 * (ktb + i) + 8 * g + 4 * half]) = v;
+      }
     lds_barrier();
 
     // contributions of the later chunks through dS, dz
     f32x16 gv = zero16(), gk = zero16();
 #pragma unroll
     for (int c = 0; c < BD / 16; ++c) {
-      gv = mma(frag_col(sm.SB, P128, 32 * x4, 16 * c), frag_row(sm.PK, P128, 32 * st, 16 * c), gv);
-      gk = mma(frag_row(sm.SB, P128, 32 * x4, 16 * c), frag_row(sm.VV, P128, 32 * st, 16 * c), gk);
+      gv = mma(frag_row(sm.SB, P128, 32 * x4, 16 * c), frag_row(sm.PK, P128, 32 * st, 16 * c), gv);
+      gk = mma(frag_col(sm.SB, P128, 32 * x4, 16 * c), frag_row(sm.VV, P128, 32 * st, 16 * c), gk);
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) gk[r] += sm.dz[32 * x4 + acc_row(half, r)];
