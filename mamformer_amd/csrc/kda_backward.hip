@@ -83,12 +83,12 @@ struct QSmem {
   bf16 AM[BC * P64];      // A'[t][s] = phi'(q_t) . phi'(k_s) (s <= t)
   bf16 GM[BC * P64];      // G[t][s] (s <= t)
   bf16 SB[BD * P128];     // S' before this chunk (bf16), transposed: row d, column k
-  float z[2][BD];         // z' before this chunk / after it
-  float vs[2][BD];        // Vsum
-  float cs[2][BD];        // column sums of S' over k < kernel_dim (= sum_s K1_s v_s)
+  alignas(16) float z[2][BD];    // z' before this chunk / after it
+  alignas(16) float vs[2][BD];   // Vsum
+  alignas(16) float cs[2][BD];   // column sums of S' over k < kernel_dim (= sum_s K1_s v_s)
   float part[3][4][BD];   // per 16-token quarter: sums of phi'(k), v, K1 v over the chunk
   float qs[BC];           // Q_t
-  float k1[BC];           // K1_s
+  alignas(16) float k1[BC];      // K1_s
   float kpre[BC];         // sum_{s <= t} K1_s (in-chunk)
   float zq[BC];           // phi(q_t) . z'
   float nr[2][BC];        // row sums of the A' tiles of s-block 0 / 1
@@ -310,10 +310,12 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
 #pragma unroll
       for (int c = 0; c < 32; c += 8) {
         const bf16x8 q8 = *reinterpret_cast<const bf16x8*>(row + c);
+        const f32x4 z0 = *reinterpret_cast<const f32x4*>(&sm.z[zc][32 * qq + c]);
+        const f32x4 z1 = *reinterpret_cast<const f32x4*>(&sm.z[zc][32 * qq + c + 4]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int k = 32 * qq + c + j;
-          acc += (k < kd ? 1.f + (float)q8[j] : 0.f) * sm.z[zc][k];
+          acc += (k < kd ? 1.f + (float)q8[j] : 0.f) * (j < 4 ? z0[j] : z1[j - 4]);
         }
       }
       acc += __shfl_xor(acc, 1, 64);
@@ -334,11 +336,13 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
       const Frag<bf16> vf = frag_col(sm.VV, P128, 32 * dt, 16 * c);
       u = mma(vf, frag_row(sm.AM, P64, 32 * tt, 16 * c), u);
       Frag<bf16> ones, k1f;
+      float k1v[8];
+      kset_vals(sm.k1, c, half, k1v);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int s_ = 16 * c + kset(half, j);
         ones.v[j] = (bf16)(s_ <= t ? 1.f : 0.f);
-        k1f.v[j] = (bf16)(s_ <= t ? sm.k1[s_] : 0.f);
+        k1f.v[j] = (bf16)(s_ <= t ? k1v[j] : 0.f);
       }
       vsum = mma(vf, ones, vsum);
       u = mma(vf, k1f, u);
@@ -353,12 +357,13 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const bf16x4 r4 = *reinterpret_cast<const bf16x4*>(&sm.DN[t * P128 + 32 * dt + 8 * g + 4 * half]);
+      const f32x4 cs4 = *reinterpret_cast<const f32x4*>(&sm.cs[zc][32 * dt + 8 * g + 4 * half]);
+      const f32x4 vs4 = *reinterpret_cast<const f32x4*>(&sm.vs[zc][32 * dt + 8 * g + 4 * half]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int rr = 4 * g + i;
-        const int d = 32 * dt + 8 * g + 4 * half + i;
-        const float uu = u[rr] + sm.cs[zc][d];
-        const float vt = vsum[rr] + sm.vs[zc][d];
+        const float uu = u[rr] + cs4[i];
+        const float vt = vsum[rr] + vs4[i];
         raw[rr] = (float)r4[i];
         part += raw[rr] * ((Q * vt + uu) * inv);
         rpart += raw[rr] * ((a + 1e-8f) * vt - cnt * uu);
@@ -437,11 +442,12 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
         for (int g = 0; g < 4; ++g) {
           const int k0 = 8 * g + 4 * half;
           const bf16x4 ph = *reinterpret_cast<const bf16x4*>(&sm.PQ[t * P128 + 32 * kt + k0]);
+          const f32x4 z4 = *reinterpret_cast<const f32x4*>(&sm.z[zc][32 * kt + k0]);
           bf16x4 o4;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int k = 32 * kt + k0 + i;
-            const float dphi = gq[4 * g + i] + sm.z[zc][k] * dn + R;
+            const float dphi = gq[4 * g + i] + z4[i] * dn + R;
             o4[i] = (bf16)(k < kd ? dphi * fminf(1.f + (float)ph[i], 1.f) : 0.f);
           }
           *reinterpret_cast<bf16x4*>(out + k0) = o4;
