@@ -118,7 +118,7 @@ struct KVSmem {
   bf16 WT[BC * P64];      // W^T[s][t] = phi(k_s) . Psi_t   (s <= t)
   bf16 MT[BC * P64];      // M^T[s][t] = g_t . v_s          (s <= t)
   bf16 SB[BD * P128];     // dS (bf16), transposed: row d, column k
-  float dz[BD];
+  alignas(16) float dz[BD];
   float part[4][BD];      // per 16-token quarter: sums of Xi
 };
 
@@ -573,8 +573,10 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_segsum_kernel(KdaBwdParams q) 
   query_coef(q, h, 1, coef[1]);
   const int dt = w & 3, ktb = 2 * (w >> 2);
   f32x16 acc[2] = {zero16(), zero16()};
-  const int col = tid & (BD - 1), qt = tid >> 7;
-  float zacc = 0.f;                          // this thread's column, tokens 16 qt .. 16 qt + 15 of every chunk
+  const int c8 = tid & 15, tg = tid >> 4;   // this thread's sums of Xi: columns 8 c8 .., tokens 2 tg, 2 tg + 1
+  float z8[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) z8[j] = 0.f;
   for (int ci = c_begin; ci < c_end; ++ci) {
     const int pos = ci * BC, len = min(BC, p.seqlen - pos);
     for (int js = 0; js < nstream; ++js) {
@@ -585,14 +587,33 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_segsum_kernel(KdaBwdParams q) 
 #pragma unroll
         for (int c = 0; c < BC / 16; ++c)
           acc[i] = mma(frag_col(sm.PS, P128, 32 * (ktb + i), 16 * c), frag_col(sm.DN, P128, 32 * dt, 16 * c), acc[i]);
-#pragma unroll 4
-      for (int t = 16 * qt; t < 16 * qt + 16; ++t) zacc += (float)sm.XI[t * P128 + col];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const bf16x8 x = ld8(&sm.XI[(2 * tg + u) * P128 + 8 * c8]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) z8[j] += (float)x[j];
+      }
       lds_barrier();
     }
   }
-  sm.part[qt][col] = zacc;
+  // fixed-order sum over the 32 token pairs: the 4 of a wave by shuffles, then the 8 waves through LDS (PS is
+  // no longer read)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    z8[j] += __shfl_xor(z8[j], 16, 64);
+    z8[j] += __shfl_xor(z8[j], 32, 64);
+  }
+  float* zp = reinterpret_cast<float*>(sm.PS);
+  if (l < 16) {
+    *reinterpret_cast<f32x4*>(&zp[w * BD + 8 * c8]) = f32x4{z8[0], z8[1], z8[2], z8[3]};
+    *reinterpret_cast<f32x4*>(&zp[w * BD + 8 * c8 + 4]) = f32x4{z8[4], z8[5], z8[6], z8[7]};
+  }
   lds_barrier();
-  if (tid < BD) zacc = sm.part[0][tid] + sm.part[1][tid] + sm.part[2][tid] + sm.part[3][tid];
+  float zacc = 0.f;
+  if (tid < BD) {
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) zacc += zp[i * BD + tid];
+  }
   float* o = q.segsum + ((int64_t)(seg * SEG_PARTS + part) * p.batch * p.nheads + bh) * (BD * BD + BD);
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -679,7 +700,11 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
       gk = mma(frag_col(sm.SB, P128, 32 * x4, 16 * c), frag_row(sm.VV, P128, 32 * st, 16 * c), gk);
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) gk[r] += sm.dz[32 * x4 + acc_row(half, r)];
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sm.dz[32 * x4 + 8 * g + 4 * half]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) gk[4 * g + j] += d4[j];
+    }
 
     for (int js = 0; js < nstream; ++js) {
       stage_stream(q, sm, js, bh, pos, len, coef);
