@@ -66,6 +66,16 @@ __device__ __forceinline__ Frag<bf16> frag_col(const bf16* M, int pitch, int c0,
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
+// Inclusive prefix sum within each 16-lane row (row_shr 1, 2, 4, 8; lanes without a source add 0): lane 15 of a
+// row holds the row's total.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xf, 0xf, false));
+  return v;
+}
+
 // Kernel A works on centered features phi' = phi - m (m[k] = 1 for k < kernel_dim): for inputs of small
 // magnitude phi is close to 1 and the gradient of q lives in the deviations, which bf16 holds to 2^-9 of
 // phi' but only to 2^-9 of 1 in phi.  The state splits the same way, S = m Vsum^T + S', z = m cnt + z'
@@ -249,12 +259,10 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
           doo[j] = (in && dop) ? dv[j] : (bf16)0.f;
         }
       }
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) {
-        qsum += __shfl_xor(qsum, o, 64);
-        ksum += __shfl_xor(ksum, o, 64);
-      }
-      if ((e & 15) == 0) {
+      // the token's 16 chunks are one 16-lane row: prefix sums on the DPP crossbar, the total in its last lane
+      qsum = row_sum16(qsum);
+      ksum = row_sum16(ksum);
+      if ((e & 15) == 15) {
         sm.qs[t] = qsum;
         sm.k1[t] = ksum;
       }
