@@ -136,6 +136,19 @@ __device__ __forceinline__ float wave_incl_scan_dpp(float v) {
   return v;
 }
 
+// v of this lane plus v of the lane 32 away, the same sum in both lanes (v_permlane32_swap: no LDS permute).
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over each group of 4 lanes (quad permutes on the DPP crossbar), the same in the 4 lanes.
+__device__ __forceinline__ float sum_quad(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -300,7 +300,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
         if (32 * st + acc_row(half, r) > t) acc[r] = 0.f;
         rs += acc[r];
       }
-      rs += __shfl_xor(rs, 32, 64);
+      rs = sum_halves(rs);
       if (half == 0) sm.nr[st][t] = rs;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -326,8 +326,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
           acc += (k < kd ? 1.f + (float)q8[j] : 0.f) * (j < 4 ? z0[j] : z1[j - 4]);
         }
       }
-      acc += __shfl_xor(acc, 1, 64);
-      acc += __shfl_xor(acc, 2, 64);
+      acc = sum_quad(acc);
       if (qq == 0) sm.zq[t] = acc;
     }
     lds_barrier();
@@ -378,9 +377,9 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
         bpart += raw[rr] * vt;
       }
     }
-    part += __shfl_xor(part, 32, 64);
-    rpart += __shfl_xor(rpart, 32, 64);
-    bpart += __shfl_xor(bpart, 32, 64);
+    part = sum_halves(part);
+    rpart = sum_halves(rpart);
+    bpart = sum_halves(bpart);
     if (half == 0) {
       sm.dnp[dt][t] = part;
       sm.rp[dt][t] = rpart;
@@ -609,7 +608,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_segsum_kernel(KdaBwdParams q) 
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     z8[j] += __shfl_xor(z8[j], 16, 64);
-    z8[j] += __shfl_xor(z8[j], 32, 64);
+    z8[j] = sum_halves(z8[j]);
   }
   float* zp = reinterpret_cast<float*>(sm.PS);
   if (l < 16) {

@@ -587,8 +587,7 @@ __global__ __launch_bounds__(256 * NQ) void kda_ref_kernel(KdaParams p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc += (float)q8[j] * (j < 4 ? z0[j] : z1[j - 4]);
       }
-      acc += __shfl_xor(acc, 1, 64);
-      acc += __shfl_xor(acc, 2, 64);
+      acc = sum_quad(acc);
       if (qq == 0) sm.zq[i][t] = acc;
     }
 
@@ -612,7 +611,7 @@ __global__ __launch_bounds__(256 * NQ) void kda_ref_kernel(KdaParams p) {
         if (!(s_ <= tl && s_ < len)) acc[r] = 0.f;
         rs += acc[r];
       }
-      rs += __shfl_xor(rs, 32, 64);
+      rs = sum_halves(rs);
       if (half == 0) sm.nrm[qi][tile][l32] = rs;
       // The normaliser uses the fp32 row sums, so the weights that multiply v must carry
       // more than bf16 precision or their rounding (independent per entry) does not cancel

@@ -603,7 +603,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
 #pragma unroll
           for (int k = 0; k < 4; ++k) cg += v[k] * a[4 * i + k];
         }
-        cg += __shfl_xor(cg, 32);
+        cg = sum_halves(cg);
         if (half == 0) sm.colg[tix][l32] = cg;
 #pragma unroll
         for (int c = 0; c < 2; ++c) sm.xds.xd[tix][c][l] = acc_to_frag<T>(a, c);
@@ -632,7 +632,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
 #pragma unroll
           for (int k = 0; k < 4; ++k) rg += v[k] * a[4 * i + k];
         }
-        rg += __shfl_xor(rg, 32);
+        rg = sum_halves(rg);
         if (half == 0) sm.rowg[ti][l32] = rg;
 #pragma unroll
         for (int c = 0; c < 2; ++c) sm.xds.xt[ti][c][l] = acc_to_frag<T>(a, c);
@@ -682,7 +682,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
         for (int c = 0; c < 2; ++c) XDf[tb][c] = acc_to_frag<T>(a, c);
       }
       if (nb == 0) {
-        colg += __shfl_xor(colg, 32);
+        colg = sum_halves(colg);
         if (half == 0) {
           sm.colg[r == 0 ? 0 : 2][l32] = colg;      // the s-block's sum over its t-blocks
           if (r == 0) sm.colg[1][l32] = 0.f;
@@ -722,7 +722,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
         sI += ai[i] * Bv[i];
         dBacc[i] += dt_l * (ai[i] + aa[i]);
       }
-      sI += __shfl_xor(sI, 32);
+      sI = sum_halves(sI);
       if (half == 0) sm.red[0][nb][s_l] = sI;
     }
     __builtin_amdgcn_sched_barrier(0);   // keep the phases apart: bounded register lifetimes
@@ -759,7 +759,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
         for (int c = 0; c < 2; ++c) XTf[sb][c] = acc_to_frag<T>(a, c);
       }
       if (nb == 0) {
-        rowg += __shfl_xor(rowg, 32);
+        rowg = sum_halves(rowg);
         if (half == 0) {
           sm.rowg[r == 0 ? 0 : 1][l32] = rowg;      // the t-block's sum over its s-blocks
           if (r == 1) sm.rowg[2][l32] = 0.f;
@@ -811,7 +811,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
         sU += ah[i] * Cv[i];
         dCacc[i] += ah[i] + ac[i];
       }
-      sU += __shfl_xor(sU, 32);
+      sU = sum_halves(sU);
       if (half == 0) sm.red[1][nb][s_l] = sU;
     }
 
