@@ -96,7 +96,7 @@ struct QSmem {
   alignas(16) float z[2][BD];    // z' before this chunk / after it
   alignas(16) float vs[2][BD];   // Vsum
   alignas(16) float cs[2][BD];   // column sums of S' over k < kernel_dim (= sum_s K1_s v_s)
-  float part[3][4][BD];   // per 16-token quarter: sums of phi'(k), v, K1 v over the chunk
+  alignas(16) float part[3][8][BD];   // per 8-token group: sums of phi'(k), v, K1 v over the chunk
   float qs[BC];           // Q_t
   alignas(16) float k1[BC];      // K1_s
   float kpre[BC];         // sum_{s <= t} K1_s (in-chunk)
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
     if (ci > 0 && tid < BD) {      // z', Vsum, column sums past the previous chunk (fixed-order sums)
       float a0 = sm.z[zc ^ 1][tid], a1 = sm.vs[zc ^ 1][tid], a2 = sm.cs[zc ^ 1][tid];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 8; ++j) {
         a0 += sm.part[0][j][tid];
         a1 += sm.part[1][j][tid];
         a2 += sm.part[2][j][tid];
@@ -471,18 +471,28 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
         Sacc[i] = mma(frag_col(sm.PK, P128, 32 * (2 * tt + i), 16 * c), frag_col(sm.VV, P128, 32 * dt, 16 * c),
                       Sacc[i]);
     {
-      const int col = tid & (BD - 1), qt = tid >> 7;
-      float zs = 0.f, vsn = 0.f, csn = 0.f;
-#pragma unroll 4
-      for (int s_ = 16 * qt; s_ < 16 * qt + 16; ++s_) {
-        zs += (float)sm.PK[s_ * P128 + col];
-        const float vv = (float)sm.VV[s_ * P128 + col];
-        vsn += vv;
-        csn += sm.k1[s_] * vv;
+      // columns 2 cp, 2 cp + 1 and tokens 8 tg .. 8 tg + 7 per thread: 4-byte row reads, K1 as two 16-byte reads
+      const int cp = tid & 63, tg = tid >> 6;
+      float zs[2] = {0.f, 0.f}, vsn[2] = {0.f, 0.f}, csn[2] = {0.f, 0.f};
+      const f32x4 k1a = *reinterpret_cast<const f32x4*>(&sm.k1[8 * tg]);
+      const f32x4 k1b = *reinterpret_cast<const f32x4*>(&sm.k1[8 * tg + 4]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int s_ = 8 * tg + u;
+        const bf16x2 pk = *reinterpret_cast<const bf16x2*>(&sm.PK[s_ * P128 + 2 * cp]);
+        const bf16x2 vv = *reinterpret_cast<const bf16x2*>(&sm.VV[s_ * P128 + 2 * cp]);
+        const float k1s = u < 4 ? k1a[u] : k1b[u - 4];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const float v = (float)vv[c];
+          zs[c] += (float)pk[c];
+          vsn[c] += v;
+          csn[c] += k1s * v;
+        }
       }
-      sm.part[0][qt][col] = zs;
-      sm.part[1][qt][col] = vsn;
-      sm.part[2][qt][col] = csn;
+      *reinterpret_cast<f32x2*>(&sm.part[0][tg][2 * cp]) = f32x2{zs[0], zs[1]};
+      *reinterpret_cast<f32x2*>(&sm.part[1][tg][2 * cp]) = f32x2{vsn[0], vsn[1]};
+      *reinterpret_cast<f32x2*>(&sm.part[2][tg][2 * cp]) = f32x2{csn[0], csn[1]};
     }
     lds_barrier();
   }
