@@ -129,7 +129,7 @@ struct KVSmem {
   bf16 MT[BC * P64];      // M^T[s][t] = g_t . v_s          (s <= t)
   bf16 SB[BD * P128];     // dS (bf16), transposed: row d, column k
   alignas(16) float dz[BD];
-  float part[4][BD];      // per 16-token quarter: sums of Xi
+  alignas(16) float part[8][BD];   // per 8-token group: sums of Xi
 };
 
 __device__ __forceinline__ void query_coef(const KdaBwdParams& q, int h, int qi, float& coef) {
@@ -771,14 +771,24 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
         for (int c = 0; c < BC / 16; ++c)
           dS[i] = mma(frag_col(sm.PS, P128, 32 * (ktb + i), 16 * c), frag_col(sm.DN, P128, 32 * dt, 16 * c), dS[i]);
       {
-        const int col = tid & (BD - 1), qt = tid >> 7;
-        float a = 0.f;
-#pragma unroll 4
-        for (int t = 16 * qt; t < 16 * qt + 16; ++t) a += (float)sm.XI[t * P128 + col];
-        sm.part[qt][col] = a;
+        // columns 2 cp, 2 cp + 1 and tokens 8 tg .. 8 tg + 7 per thread (4-byte row reads)
+        const int cp = tid & 63, tg = tid >> 6;
+        float a[2] = {0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const bf16x2 x = *reinterpret_cast<const bf16x2*>(&sm.XI[(8 * tg + u) * P128 + 2 * cp]);
+          a[0] += (float)x[0];
+          a[1] += (float)x[1];
+        }
+        *reinterpret_cast<f32x2*>(&sm.part[tg][2 * cp]) = f32x2{a[0], a[1]};
       }
       lds_barrier();
-      if (tid < BD) sm.dz[tid] += sm.part[0][tid] + sm.part[1][tid] + sm.part[2][tid] + sm.part[3][tid];
+      if (tid < BD) {
+        float d = sm.dz[tid];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) d += sm.part[j][tid];
+        sm.dz[tid] = d;
+      }
     }
 
     const int s_ = 32 * st + l32;
