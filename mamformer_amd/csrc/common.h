@@ -136,6 +136,15 @@ __device__ __forceinline__ float wave_incl_scan_dpp(float v) {
   return v;
 }
 
+// v of lane `lane` (wave-uniform) in every lane: v_readlane, no LDS permute.
+__device__ __forceinline__ float lane_val(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+// v of lane 32 x + lane % 32 (x = 0 or 1, wave-uniform) in every lane, by v_permlane32_swap.
+__device__ __forceinline__ float from_half(float v, int x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(x ? r[1] : r[0]);
+}
 // v of this lane plus v of the lane 32 away, the same sum in both lanes (v_permlane32_swap: no LDS permute).
 __device__ __forceinline__ float sum_halves(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);

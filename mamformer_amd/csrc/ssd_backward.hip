@@ -320,7 +320,7 @@ __global__ __launch_bounds__(64 * (2 * (N / 32) + 2)) void ssd_bwd_sweep_kernel(
     const int len = min(SEG, p.seqlen - k * SEG);
     float dtv;
     const float cs = seg_decay(p, sm.st[s].dtraw[l], bias, Ah, l, len, dtv);
-    const float cend = __shfl(cs, 63);
+    const float cend = lane_val(cs, 63);
     sm.w[w][l] = dir ? ((l < len) ? __expf(cs) : 0.f) : __expf(cend - cs) * dtv;
     f32x16 acc = zero16();
 #pragma unroll
@@ -562,10 +562,10 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
     const float raw = sg.dtraw[l];
     float dtv;
     const float cs = seg_decay(p, raw, bias, Ah, l, len, dtv);
-    const float cend = __shfl(cs, 63);
+    const float cend = lane_val(cs, 63);
     sm.cs[w][l] = cs;
     sm.dtp[w][l] = dtv;
-    const float cs_l = __shfl(cs, s_l), dt_l = __shfl(dtv, s_l);
+    const float cs_l = from_half(cs, r), dt_l = from_half(dtv, r);
 
     constexpr bool SHARE = sizeof(T) == 2;
     Frag<T> XDf[2][2], XTf[2][2];        // per-wave tiles (fp32 only)
@@ -576,7 +576,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       if (tix < 3) {
         const int tb = tix == 0 ? 0 : 1, rr = tix == 2 ? 1 : 0;
         const int s_p = 32 * rr + l32;
-        const float cs_p = __shfl(cs, s_p);
+        const float cs_p = from_half(cs, rr);
         f32x16 a = zero16();
 #pragma unroll
         for (int k = 0; k < HD / 16; ++k)
@@ -610,7 +610,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       } else {
         const int ti = tix - 3, sb = ti == 2 ? 1 : 0, rr = ti == 0 ? 0 : 1;
         const int t_p = 32 * rr + l32;
-        const float cs_p = __shfl(cs, t_p);
+        const float cs_p = from_half(cs, rr);
         f32x16 a = zero16();
 #pragma unroll
         for (int k = 0; k < HD / 16; ++k)
@@ -822,7 +822,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
     f32x16 ax = zero16();
     const bool dxB = SPLIT && w >= 4;
     if (dxw || dxB) {
-      const float csx = __shfl(cs, s_x), wx = __expf(cend - csx);
+      const float csx = from_half(cs, sbx), wx = __expf(cend - csx);
       if (dxw) {
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
@@ -891,7 +891,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
     }
     // dx = dt_s * ax + D dy, stored by the owner of the finished tile
     auto store_dx = [&]() {
-      const float dtx = __shfl(dtv, s_x);
+      const float dtx = from_half(dtv, sbx);
       if (s_x < len) {
         T* o = reinterpret_cast<T*>(q.dx) + (int64_t)b * q.dx_sb + (int64_t)(tok0 + s_x) * q.dx_sl +
                (int64_t)h * q.dx_sh + 32 * pb + 4 * half;
@@ -946,7 +946,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
       const float qv = valid ? rowG - dtv * colG + u : 0.f;
       const float vv = dtv * bint;
       const float qi = wave_incl_scan_dpp(qv);
-      const float qtot = __shfl(qi, 63);
+      const float qtot = lane_val(qi, 63);
       const float vi = wave_incl_scan_dpp(vv);
       const float da = (qtot - qi + qv) + __expf(cend) * lh + (vi - vv);
       const float ddr = valid ? (colG + bint + Ah * da) * dt_chain(p, raw, bias) : 0.f;

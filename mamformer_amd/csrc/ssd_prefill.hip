@@ -322,7 +322,7 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_state_kernel(SsdParams p) 
     }
     float dtv;
     const float cs = seg_decay(p, sg.dt[w][ll], dtb, Ah, pos + l, c1, dtv);
-    const float cse = __shfl(cs, 63, 64);
+    const float cse = lane_val(cs, 63);
     float wsc;                                             // per-token operand scale (wave-uniform choice)
     if (-cse > FACT_RANGE) {                               // very strong decay: carry S exactly through it
       const float e = __expf(kappa + cse);
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(128 * HG) void ssd_chunk_scan_kernel(SsdParams p) {
     // ---- this head's in-segment decay (lane = token).  H_true = e^kappa H (kappa <= 0 carried lazily).
     float dtv;
     const float cs = seg_decay(p, sg.dt[w][ll], dtb, Ah, pos + l, c1, dtv);
-    const float cse = __shfl(cs, 63, 64);
+    const float cse = lane_val(cs, 63);
     const bool fact = (-cse <= FACT_RANGE);               // wave-uniform
     if (!fact || -(kappa + cse) > FACT_RANGE) {
       const float e = __expf(kappa);
