@@ -517,57 +517,79 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
   }
 }
 
-// Psi, Xi and g of stream js for the chunk at pos (len tokens) into LDS (zero rows beyond len).
-__device__ __forceinline__ void stage_stream(const KdaBwdParams& q, KVSmem& sm, int js, int bh, int pos, int len,
-                                             const float (&coef)[2]) {
+// Raw rows of one (chunk, stream) for this thread's two 16-byte chunks e = tid + NT u (row e >> 4, columns
+// 8 (e & 15)): the queries folded into the stream, n and dn of the row, and the stream's output gradient.  Loaded a
+// (chunk, stream) ahead, so that the global latency hides behind the current one's products.
+struct StreamRaw {
+  bf16x8 q[2][2];         // [u][query of the stream]
+  bf16x8 g[2];
+  float nb[2][2], db[2][2];
+};
+__device__ __forceinline__ void load_stream(const KdaBwdParams& q, StreamRaw& s, int js, int bh, int pos, int len) {
   const KdaParams& p = q.f;
-  const int nbh = p.batch * p.nheads, S = p.seqlen, kd = p.kernel_dim;
+  const int nbh = p.batch * p.nheads, S = p.seqlen;
   const int64_t rowbase = (int64_t)bh * S;
   const int nqs = q.diff ? 2 : 1;          // queries folded into this stream
-  const bf16* qps[2];
-  const float* nbs[2];
-  const float* dbs[2];
-  float cf[2];
-  for (int i = 0; i < nqs; ++i) {
-    const int qi = q.diff ? i : js;
-    qps[i] = reinterpret_cast<const bf16*>(qi == 0 ? p.q1 : p.q2);
-    nbs[i] = q.nbuf + ((int64_t)qi * nbh + bh) * S + pos;
-    dbs[i] = q.dnbuf + ((int64_t)qi * nbh + bh) * S + pos;
-    cf[i] = q.diff ? coef[qi] : 1.f;
-  }
   const bf16* gp = reinterpret_cast<const bf16*>(q.diff ? q.do1 : (js == 0 ? q.do1 : q.do2));
-  for (int e = threadIdx.x; e < BC * (BD / 8); e += NT) {
-    const int t = e >> 4, c0 = (e & 15) * 8;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int e = threadIdx.x + NT * u, t = e >> 4, c0 = (e & 15) * 8;
     const bool in = t < len;
     const int64_t r = (rowbase + pos + (in ? t : 0)) * BD + c0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (i < nqs) {
+        const int qi = q.diff ? i : js;
+        s.q[u][i] = ld8(reinterpret_cast<const bf16*>(qi == 0 ? p.q1 : p.q2) + r);
+        const int64_t nrow = ((int64_t)qi * nbh + bh) * S + pos + t;
+        s.nb[u][i] = in ? q.nbuf[nrow] : 1.f;
+        s.db[u][i] = in ? q.dnbuf[nrow] : 0.f;
+      }
+    }
+    if (gp) s.g[u] = ld8(gp + r);
+  }
+}
+// Psi, Xi and g of stream js for the chunk (len tokens) from its raw rows into LDS (zero rows beyond len).
+__device__ __forceinline__ void put_stream(const KdaBwdParams& q, KVSmem& sm, const StreamRaw& s, int js, int len,
+                                           const float (&coef)[2]) {
+  const int kd = q.f.kernel_dim;
+  const int nqs = q.diff ? 2 : 1;
+  const bool has_g = q.diff ? q.do1 != nullptr : (js == 0 ? q.do1 : q.do2) != nullptr;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int e = threadIdx.x + NT * u, t = e >> 4, c0 = (e & 15) * 8;
+    const bool in = t < len;
     float ps[8], xi[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) ps[j] = xi[j] = 0.f;
-    for (int i = 0; i < nqs; ++i) {
-      const bf16x8 qv = ld8(qps[i] + r);
-      const float sc = in ? cf[i] / nbs[i][t] : 0.f;
-      const float dn = in ? dbs[i][t] : 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float ph = (c0 + j < kd) ? phi_f((float)qv[j]) : 0.f;
-        ps[j] += sc * ph;
-        xi[j] += dn * ph;
+    for (int i = 0; i < 2; ++i) {
+      if (i < nqs) {
+        const int qi = q.diff ? i : js;
+        const float cf = q.diff ? coef[qi] : 1.f;
+        const float sc = in ? cf / s.nb[u][i] : 0.f;
+        const float dn = in ? s.db[u][i] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float ph = (c0 + j < kd) ? phi_f((float)s.q[u][i][j]) : 0.f;
+          ps[j] += sc * ph;
+          xi[j] += dn * ph;
+        }
       }
     }
-    bf16x8 g8;
-    if (gp) g8 = ld8(gp + r);
     bf16x8 po, xo, go;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       po[j] = (bf16)ps[j];
       xo[j] = (bf16)xi[j];
-      go[j] = (in && gp) ? g8[j] : (bf16)0.f;
+      go[j] = (in && has_g) ? s.g[u][j] : (bf16)0.f;
     }
     *reinterpret_cast<bf16x8*>(&sm.PS[t * P128 + c0]) = po;
     *reinterpret_cast<bf16x8*>(&sm.XI[t * P128 + c0]) = xo;
     *reinterpret_cast<bf16x8*>(&sm.DN[t * P128 + c0]) = go;
   }
 }
+
 
 // Sum of the contributions of one part of a segment to the adjoint state, sum_t Psi_t^T g_t and
 // sum_t Xi_t over its chunks and streams, for the kv-walk of the segments before it.
@@ -594,10 +616,14 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_segsum_kernel(KdaBwdParams q) 
   float z8[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) z8[j] = 0.f;
+  StreamRaw sr;
+  if (c_begin < c_end) load_stream(q, sr, 0, bh, c_begin * BC, min(BC, p.seqlen - c_begin * BC));
   for (int ci = c_begin; ci < c_end; ++ci) {
     const int pos = ci * BC, len = min(BC, p.seqlen - pos);
     for (int js = 0; js < nstream; ++js) {
-      stage_stream(q, sm, js, bh, pos, len, coef);
+      put_stream(q, sm, sr, js, len, coef);
+      if (js + 1 < nstream) load_stream(q, sr, js + 1, bh, pos, len);            // the next (chunk, stream)
+      else if (ci + 1 < c_end) load_stream(q, sr, 0, bh, pos + BC, min(BC, p.seqlen - pos - BC));
       lds_barrier();
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -682,6 +708,8 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
 
   const int nch = (S + BC - 1) / BC;
   const int c_begin = seg * q.seg_chunks, c_end = min(nch, c_begin + q.seg_chunks);
+  StreamRaw sr;
+  if (c_end > c_begin) load_stream(q, sr, 0, bh, (c_end - 1) * BC, min(BC, S - (c_end - 1) * BC));
   for (int ci = c_end - 1; ci >= c_begin; --ci) {
     const int pos = ci * BC, len = min(BC, S - pos);
     for (int e = tid; e < BC * (BD / 8); e += NT) {
@@ -724,7 +752,9 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
     }
 
     for (int js = 0; js < nstream; ++js) {
-      stage_stream(q, sm, js, bh, pos, len, coef);
+      put_stream(q, sm, sr, js, len, coef);
+      if (js + 1 < nstream) load_stream(q, sr, js + 1, bh, pos, len);            // the next (chunk, stream)
+      else if (ci - 1 >= c_begin) load_stream(q, sr, 0, bh, pos - BC, min(BC, S - pos + BC));
       lds_barrier();
 
       // W^T (waves 0..2) and M^T (waves 3..5) tiles, (t-block, s-block) = (0,0), (1,0), (1,1)
