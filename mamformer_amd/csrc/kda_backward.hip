@@ -282,6 +282,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
         *reinterpret_cast<bf16x4*>(&sm.SB[(32 * dt + l32) * P128 + 32 * (2 * tt + i) + 8 * g + 4 * half]) = v;
       }
     lds_barrier();
+    if (pos + BC < S) load_tiles(pos + BC);          // the staged registers are free: the next chunk flies all chunk
 
     // ---- phase 1: A' tiles (t-block, s-block) = (0,0), (1,0), (1,1) by waves 0..2, computed transposed so
     // the row sums are lane-local; in-chunk prefix sums of K1 by wave 3; phi(q_t) . z' by waves 4..7.
@@ -462,7 +463,6 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_q_kernel(KdaBwdParams q) {
       }
     }
 
-    if (pos + BC < S) load_tiles(pos + BC);
     // ---- phase 6: S' += phi'(k)^T v (own tiles); z', Vsum and the column sums of S' move past the chunk
 #pragma unroll
     for (int i = 0; i < 2; ++i)
