@@ -709,14 +709,28 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
   const int nch = (S + BC - 1) / BC;
   const int c_begin = seg * q.seg_chunks, c_end = min(nch, c_begin + q.seg_chunks);
   StreamRaw sr;
-  if (c_end > c_begin) load_stream(q, sr, 0, bh, (c_end - 1) * BC, min(BC, S - (c_end - 1) * BC));
+  bf16x8 kr[2], vr[2];                          // the chunk's k and v rows, loaded a chunk ahead
+  auto load_kv = [&](int p0) {
+    const int ln = min(BC, S - p0);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + NT * u, t = e >> 4, c0 = (e & 15) * 8;
+      const int64_t r = (rowbase + p0 + (t < ln ? t : 0)) * BD + c0;
+      kr[u] = ld8(kp + r);
+      vr[u] = ld8(vp + r);
+    }
+  };
+  if (c_end > c_begin) {
+    load_stream(q, sr, 0, bh, (c_end - 1) * BC, min(BC, S - (c_end - 1) * BC));
+    load_kv((c_end - 1) * BC);
+  }
   for (int ci = c_end - 1; ci >= c_begin; --ci) {
     const int pos = ci * BC, len = min(BC, S - pos);
-    for (int e = tid; e < BC * (BD / 8); e += NT) {
-      const int t = e >> 4, c0 = (e & 15) * 8;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + NT * u, t = e >> 4, c0 = (e & 15) * 8;
       const bool in = t < len;
-      const int64_t r = (rowbase + pos + (in ? t : 0)) * BD + c0;
-      const bf16x8 kv = ld8(kp + r), vv = ld8(vp + r);
+      const bf16x8 kv = kr[u], vv = vr[u];
       bf16x8 ko, vo;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -736,6 +750,7 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
         *reinterpret_cast<bf16x4*>(&sm.SB[(32 * dt + l32) * P128 + 32 * (ktb + i) + 8 * g + 4 * half]) = v;
       }
     lds_barrier();
+    if (ci - 1 >= c_begin) load_kv(pos - BC);
 
     // contributions of the later chunks through dS, dz
     f32x16 gv = zero16(), gk = zero16();
