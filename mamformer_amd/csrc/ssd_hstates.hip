@@ -200,19 +200,30 @@ __global__ __launch_bounds__(256) void ssd_hs_carry_kernel(SsdParams p, HsParams
   float* zp = q.z + ((int64_t)b * p.nseg * H + h) * N + n;
   const float* dp = q.dec + (int64_t)b * p.nseg * H + h;
   const int64_t zs = (int64_t)H * N;
-  // 16 segments' loads issued together, then the 16 steps of the chain: the load latency is paid once per 16
-  for (int s0 = 0; s0 < p.nseg; s0 += 16) {
-    float zl[16], d[16];
+  // 16 segments' loads issued together, the next 16's while the chain runs through these (two buffers)
+  auto ld = [&](int s0, float (&zl)[16], float (&d)[16]) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       const bool in = s0 + k < p.nseg;
       zl[k] = in ? zp[(s0 + k) * zs] : 0.f;
       d[k] = in ? dp[(int64_t)(s0 + k) * H] : 1.f;
     }
+  };
+  auto step = [&](int s0, const float (&zl)[16], const float (&d)[16]) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       if (s0 + k < p.nseg) zp[(s0 + k) * zs] = Z;    // the state sum entering segment s0 + k
       Z = d[k] * Z + zl[k];
+    }
+  };
+  float za[16], da[16], zb[16], dbf[16];
+  if (p.nseg > 0) ld(0, za, da);
+  for (int s0 = 0; s0 < p.nseg; s0 += 32) {
+    if (s0 + 16 < p.nseg) ld(s0 + 16, zb, dbf);
+    step(s0, za, da);
+    if (s0 + 16 < p.nseg) {
+      if (s0 + 32 < p.nseg) ld(s0 + 32, za, da);
+      step(s0 + 16, zb, dbf);
     }
   }
 }
@@ -440,23 +451,37 @@ __global__ __launch_bounds__(256) void ssd_hsb_carry_kernel(SsdParams p, HsParam
   const float* dp = q.dec + (int64_t)b * ns * H + h;
   const int64_t zs = (int64_t)H * N;
   float L = 0.f;
-  for (int s0 = 0; s0 < ns; s0 += 16) {
-    float zl[16], df[16], gl[16], db[16];
+  // 16 segments of each chain loaded together, the next 16's while the chains run through these (two buffers;
+  // the loads read segments neither chain has written yet)
+  struct Batch { float zl[16], df[16], gl[16], db[16]; };
+  auto ld = [&](int s0, Batch& t) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       const int sf = s0 + k, sb = ns - 1 - s0 - k;
-      zl[k] = sf < ns ? zp[sf * zs] : 0.f;
-      df[k] = sf < ns ? dp[(int64_t)sf * H] : 1.f;
-      gl[k] = sb >= 0 ? lp[sb * zs] : 0.f;
-      db[k] = sb >= 0 ? dp[(int64_t)sb * H] : 1.f;
+      t.zl[k] = sf < ns ? zp[sf * zs] : 0.f;
+      t.df[k] = sf < ns ? dp[(int64_t)sf * H] : 1.f;
+      t.gl[k] = sb >= 0 ? lp[sb * zs] : 0.f;
+      t.db[k] = sb >= 0 ? dp[(int64_t)sb * H] : 1.f;
     }
+  };
+  auto step = [&](int s0, const Batch& t) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       const int sf = s0 + k, sb = ns - 1 - s0 - k;
       if (sf < ns) zp[sf * zs] = Z;      // the state sum entering segment sf
-      Z = df[k] * Z + zl[k];
+      Z = t.df[k] * Z + t.zl[k];
       if (sb >= 0) lp[sb * zs] = L;      // the adjoint handed into segment sb from the right
-      L = db[k] * L + gl[k];
+      L = t.db[k] * L + t.gl[k];
+    }
+  };
+  Batch ba, bb;
+  if (ns > 0) ld(0, ba);
+  for (int s0 = 0; s0 < ns; s0 += 32) {
+    if (s0 + 16 < ns) ld(s0 + 16, bb);
+    step(s0, ba);
+    if (s0 + 16 < ns) {
+      if (s0 + 32 < ns) ld(s0 + 32, ba);
+      step(s0 + 16, bb);
     }
   }
   if (dh0) {
