@@ -165,7 +165,7 @@ def bench_ssd(cfg, steps, warmup, nsets, chunk=None):
 def bench_ssd_hstates(cfg, steps, warmup):
     """Cost of return_h_states at the headline shape: selective_scan with and without h_states through the same
     Python entry (allocation of outputs and workspace included in both), and the h_states computation alone
-    (the second run of the prefill kernels with x and B swapped, plus the mean over heads)."""
+    (``mh_ssd_h_states``: the local, carry and output kernels over the state's channel sums)."""
     import mamformer_amd as mh
     from mamformer_amd import ops
     from mamformer_amd import workloads as W

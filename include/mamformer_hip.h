@@ -107,7 +107,9 @@ int mh_ssd_chunk_scan_fwd(const mh_ssd_args* a, void* stream);
  *   call, and so is a dstate the kernels do not tile directly (anything but 64 and 128: those compositions
  *   need the caller's workspace), with MH_ERR_UNSUPPORTED.  Every call on one GPU uses that GPU's single array: calls that overlap in time on one GPU
  *   (several streams or host threads) race and must be serialised by the caller.  The first call on
- *   each GPU looks up the array's device address (hipGetSymbolAddress), which allocates nothing.
+ *   each GPU looks up the array's device address (hipGetSymbolAddress), which allocates nothing; make that
+ *   first call outside stream capture (a capture may refuse the lookup), after which the entry point can be
+ *   captured into a HIP graph and replayed (it records kernel launches only).
  *   Results are bit-identical to mh_ssd_chunk_scan_fwd's for the same arguments. */
 #define MH_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int mh_ssd_chunk_scan_fwd_noalloc(const mh_ssd_args* a, void* stream);

@@ -347,6 +347,8 @@ struct PBwdSmem {
   float n[CT], dn[CT], dot[CT];
   float dotp[DV / 32][CT];
   float lam[BW];
+  float dov[CT];                   // q-walk: do_t . Vsum_t (Vsum_t = sum of v over the tokens up to t)
+  float vsum[DV];                  // q-walk: sum of v over the chunks before this one
 };
 
 // Output-gradient pointer and coefficient of query stream qi (see KdaBwdParams).
@@ -384,7 +386,11 @@ __global__ __launch_bounds__(64 * BW) void kda_precise_bwd_q_kernel(KdaBwdParams
   for (int e = tid; e < DK * DV; e += 64 * BW)
     sm.M[(e / DV) * PV + e % DV] = p.init_state ? p.init_state[(int64_t)bh * DK * DV + e] : 0.f;
   if (tid < DK) sm.z[tid] = p.init_z ? p.init_z[(int64_t)bh * DK + tid] : 0.f;
-  float lam_acc = 0.f;                          // sum_t do_t . o_t (threads t < CT)
+  // lambda gradient pieces (threads t < CT): sum_t do_t . (o_t - Vsum_t / cnt_t) and, once, sum_t do_t . Vsum_t /
+  // cnt_t.  In reference mode o1 ~ o2 ~ Vsum / cnt (phi ~ 1), so the two queries' centred sums keep the digits
+  // that d lambda (their difference) needs.
+  float lam_acc = 0.f, base_acc = 0.f;
+  if (tid < DV) sm.vsum[tid] = 0.f;
   __syncthreads();
 
   for (int pos = 0; pos < S; pos += CT) {
@@ -412,7 +418,17 @@ __global__ __launch_bounds__(64 * BW) void kda_precise_bwd_q_kernel(KdaBwdParams
       sm.n[tid] = n + qz + 1e-8f;
     }
     __syncthreads();
-    // num tiles (rows t, v-tile): sum_s A[t][s] v_s + phi(q_t) S; per row the partial of do_t . num_t
+    // num tiles (rows t, v-tile): sum_s A[t][s] v_s + phi(q_t) S; per row the partial of do_t . num_t.
+    // Wave DV / 32: do_t . Vsum_t = do_t . vsum + sum_{s <= t} v_s . do_t (masked column sums of V do^T).
+    if (w == DV / 32) {
+      const f32x16 acc = tile_mma<false, true, PV, PV, DV>(zero16(), sm.V, 0, sm.D, 0, half, l32);
+      float d = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) d += acc_row(half, r) <= l32 ? acc[r] : 0.f;
+      for (int c = half * (DV / 2); c < (half + 1) * (DV / 2); ++c) d += sm.D[l32 * PV + c] * sm.vsum[c];
+      d += __shfl_xor(d, 32, 64);
+      if (half == 0) sm.dov[l32] = d;
+    }
     if (w < DV / 32) {
       f32x16 acc = tile_mma<false, false, PC, PV, CT>(zero16(), sm.A, 0, sm.V, 32 * w, half, l32);
       acc = tile_mma<false, false, PK, PV, DK>(acc, sm.Q, 0, sm.M, 32 * w, half, l32);
@@ -431,7 +447,9 @@ __global__ __launch_bounds__(64 * BW) void kda_precise_bwd_q_kernel(KdaBwdParams
       const float n = sm.n[tid];
       sm.dn[tid] = tid < len ? -coef * d / (n * n) : 0.f;
       if (tid < len) {
-        lam_acc += d / n;
+        const float base = sm.dov[tid] / (float)(pos + tid + 1);
+        lam_acc += d / n - base;
+        base_acc += base;
         nbuf[pos + tid] = n;
         dnbuf[pos + tid] = -coef * d / (n * n);
       }
@@ -481,14 +499,20 @@ __global__ __launch_bounds__(64 * BW) void kda_precise_bwd_q_kernel(KdaBwdParams
       for (int s = 0; s < CT; ++s) zs += sm.K[s * PK + tid];
       sm.z[tid] += zs;
     }
+    if (tid < DV) {                                        // rows past len are zero
+      float vs = 0.f;
+      for (int s = 0; s < CT; ++s) vs += sm.V[s * PV + tid];
+      sm.vsum[tid] += vs;
+    }
     __syncthreads();
   }
-  // sum_t do_t . o_i,t for the lambda gradient (no centering correction: slot nq holds 0)
+  // P_i = sum do . (o_i - Vsum / cnt) in slot qi and, from the first query, B = sum do . Vsum / cnt in slot nq
   if (tid < 64) {
-    float v = wave_sum(tid < CT ? lam_acc : 0.f);
+    const float v = wave_sum(tid < CT ? lam_acc : 0.f);
+    const float b = wave_sum(tid < CT ? base_acc : 0.f);
     if (tid == 0) {
       q.lam_part[(int64_t)qi * nbh + bh] = v;
-      if (qi == 0) q.lam_part[(int64_t)q.nq * nbh + bh] = 0.f;
+      if (qi == 0) q.lam_part[(int64_t)q.nq * nbh + bh] = b;
     }
   }
 }

@@ -117,4 +117,5 @@ def ref_attention_scan_backward(q1, q2, k, v, kernel_dim, lambda_raw, dout):
     lr = np.asarray(lambda_raw, np.float64)
     sg = 1.0 / (1.0 + np.exp(-lr))
     dlr = dlam * sg * (1.0 - sg) * (sg <= 0.99)
-    return {"dq1": r["dq1"], "dq2": r["dq2"], "dk": r["dk"], "dv": r["dv"], "d_lambda_raw": dlr}
+    # o1, o2 ride along so that a check can scale d_lambda_raw by the magnitude of the terms it sums
+    return {"dq1": r["dq1"], "dq2": r["dq2"], "dk": r["dk"], "dv": r["dv"], "d_lambda_raw": dlr, "o1": o1, "o2": o2}

@@ -18,7 +18,7 @@ import torch
 import mamformer_amd as mh
 from oracle import kda as okda
 from oracle import kda_bwd as obwd
-from tests.gpu_helpers import check_per_head, check, dev, host, say
+from tests.gpu_helpers import check_lambda_bound, check_per_head, check, dev, host, lambda_term_scale, say
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-2
@@ -85,9 +85,12 @@ def test_diff_output_autograd_vs_oracle(S):
         check_per_head(name, t.grad, ref[name], TOL)
     # d lam_h = c^2 sum dout . (o1 - o2): with random dout the sum cancels down to about 1/sqrt(B S D) of its
     # terms, and o1 - o2 (o1 ~ o2 in reference mode) carries the bf16-operand rounding of the recomputed
-    # outputs, so one head's value is not a meaningful 1e-2 target; the vector over heads is, and
-    # test_diff_lambda_gradient_per_head checks every head with a coherent dout
+    # outputs, so one head's value is not a meaningful 1e-2 target.  Checked three ways: the vector over heads
+    # to 1e-2; every head within 4e-3 (about the bf16 unit roundoff) of the summed magnitude of its terms; and
+    # every head to 1e-2 with a coherent dout (test_diff_lambda_gradient_per_head)
     check("d_lambda_raw", tl.grad, ref["d_lambda_raw"], TOL)
+    scale = lambda_term_scale(dout.double().numpy(), ref["o1"], ref["o2"], lr.double().numpy())
+    check_lambda_bound("d_lambda_raw", tl.grad, ref["d_lambda_raw"], scale, 4e-3)
     assert tl.grad[3].item() == 0.0
 
 

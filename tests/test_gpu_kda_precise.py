@@ -19,7 +19,8 @@ import torch
 import mamformer_amd as mh
 from oracle import kda as okda
 from oracle import kda_bwd as obwd
-from tests.gpu_helpers import TOL, check, dev, host, say
+from tests.gpu_helpers import (TOL, check, check_lambda_bound, check_per_head, dev, host, lambda_term_scale,
+                               say)
 
 pytestmark = pytest.mark.gpu
 F32, BF = torch.float32, torch.bfloat16
@@ -132,7 +133,8 @@ def test_ref_fused_diff_and_single_vs_oracle(dtype, D):
     out = mh.linear_attention_scan(tq1, tq2, tk, tv, D, dev(lr))
     single = mh.linear_attn_scan_single(tq1, tk, tv, D)
     torch.cuda.synchronize()
-    check("fused diff", out, okda.ref_attention_scan(q1, q2, k, v, D, lr.double().numpy()), TOL[dtype])
+    # per head: the differential output scales the heads by 1 / (1 - lambda), up to 100 at the clamp
+    check_per_head("fused diff", out, okda.ref_attention_scan(q1, q2, k, v, D, lr.double().numpy()), TOL[dtype])
     r1, _, _, _ = okda.ref_scan_pair(q1, q1, k, v, D)
     check("single", single, r1, TOL[dtype])
 
@@ -192,9 +194,38 @@ def test_diff_output_autograd_vs_oracle(dtype, D):
     torch.cuda.synchronize()
     ref = obwd.ref_attention_scan_backward(q1, q2, k, v, D, lr.double().numpy(), dout)
     for name, t in zip(("dq1", "dq2", "dk", "dv"), leaves):
-        check(name, t.grad, ref[name], TOL[dtype])
-    check("d_lambda_raw", tl.grad, ref["d_lambda_raw"], TOL[dtype] if dtype == F32 else 5e-2)
+        check_per_head(name, t.grad, ref[name], TOL[dtype])
+    check("d_lambda_raw", tl.grad, ref["d_lambda_raw"], TOL[dtype])
+    # every head against the summed magnitude of its (cancelling) terms; fp32 arithmetic throughout
+    scale = lambda_term_scale(dout, ref["o1"], ref["o2"], lr.double().numpy())
+    check_lambda_bound("d_lambda_raw", tl.grad, ref["d_lambda_raw"], scale, 1e-4 if dtype == F32 else 4e-3)
     assert tl.grad[3].item() == 0.0
+
+
+@pytest.mark.parametrize("dtype,D,S", [(F32, 64, 160), (F32, 128, 160), (BF, 64, 160), (F32, 64, 2048),
+                                       (BF, 64, 2048)], ids=ids)
+def test_diff_lambda_gradient_per_head(dtype, D, S):
+    """The lambda gradient of every head with dout along o1 - o2 (from the oracle's forward), so each head's sum
+    c^2 sum dout . (o1 - o2) is coherent rather than a cancelling random sum: a wrong term or sign in the lambda
+    chain moves it by O(1).  S = 2048 runs 64 chunks through the centred partial sums."""
+    B, H = 2, 4
+    g = torch.Generator().manual_seed(3 * D + S)
+    q1, tq1 = rnd(g, (B, H, S, D), dtype, 4.0 / D ** 0.5)
+    q2, tq2 = rnd(g, (B, H, S, D), dtype, 4.0 / D ** 0.5)
+    k, tk = rnd(g, (B, H, S, D), dtype, 4.0 / D ** 0.5)
+    v, tv = rnd(g, (B, H, S, D), dtype)
+    lr = torch.tensor([-1.0, 0.4, 2.5, 3.5])
+    o1, o2, _, _ = okda.ref_scan_pair(q1, q2, k, v, D)
+    dout_t = torch.tensor(o1 - o2).to(dtype)
+    dout = dout_t.double().numpy()
+    say(f"precise lambda gradient per head (coherent dout) {dtype} D={D} S={S}")
+    leaves = [t.clone().requires_grad_() for t in (tq1, tq2, tk, tv)]
+    tl = dev(lr).requires_grad_()
+    out = mh.linear_attention_scan(*leaves, D, tl)
+    out.backward(dev(dout_t, dtype))
+    torch.cuda.synchronize()
+    ref = obwd.ref_attention_scan_backward(q1, q2, k, v, D, lr.double().numpy(), dout)
+    check_per_head("d_lambda_raw", tl.grad, ref["d_lambda_raw"], TOL[dtype], axis=0)
 
 
 def test_empty_sequence_head64():
