@@ -345,6 +345,45 @@ def bench_decode(cfg, steps, warmup, nsets):
     return res
 
 
+PEAK_EXP = 256 * 4 * 4 * 2.4e9   # exponentials/s: the transcendental unit at a quarter of the 16-lane VALU rate
+PEAK_VALU = 256 * 4 * 16 * 2.4e9  # fp32 lane operations/s without packed math (16-lane SIMDs, 4 per CU)
+
+
+def bench_ref_scan(steps, warmup, batch=2, seqlen=4096, d_inner=2048, dstate=128):
+    """The reference-parameterised prefill (``selective_scan_reference``: A per state, dt and D per channel,
+    mamba2.py:70-130) at the reference's 1b preset width (d_inner 2048, N 128; config.py:833-843), bf16, with and
+    without h_states.  Bound by one exponential per (token, channel, state): ``exp_roofline_us`` is that count at
+    the transcendental rate, ``valu_roofline_us`` adds the four fp32 operations per element (decay argument,
+    B dt x, the state update and the C read-out) at the VALU rate, sharing the same issue slots."""
+    import mamformer_amd as mh
+
+    g = torch.Generator(device="cuda").manual_seed(21)
+    plans, plans_hs = [], []
+    for _ in range(3):
+        x = torch.randn(batch, seqlen, d_inner, device="cuda", generator=g).to(torch.bfloat16)
+        dt = torch.nn.functional.softplus(torch.randn(batch, seqlen, d_inner, device="cuda", generator=g) - 2.0)
+        A_log = torch.log(torch.linspace(0.5, 8.0, dstate, device="cuda"))
+        B = torch.randn(batch, seqlen, dstate, device="cuda", generator=g).to(torch.bfloat16)
+        C = torch.randn(batch, seqlen, dstate, device="cuda", generator=g).to(torch.bfloat16)
+        D = torch.ones(d_inner, device="cuda")
+        plans.append(mh.plan_selective_scan_reference(x, dt, A_log, B, C, D, return_final_state=True))
+        plans_hs.append(mh.plan_selective_scan_reference(x, dt, A_log, B, C, D, True, True))
+    _, ev = time_plans(plans, steps, warmup)
+    _, ev_hs = time_plans(plans_hs, steps, warmup)
+    elems = batch * seqlen * d_inner * dstate
+    t_exp = elems / PEAK_EXP
+    t_valu = elems * (4 + 4) / PEAK_VALU
+    nbytes = batch * seqlen * (d_inner * (2 + 4 + 2) + 2 * dstate * 2) + batch * d_inner * dstate * 4
+    t = ev * 1e-3
+    res = dict(us_per_step=ev * 1e3, us_with_h_states=ev_hs * 1e3, mtok_s=batch * seqlen / t / 1e6,
+               exp_roofline_us=t_exp * 1e6, valu_roofline_us=t_valu * 1e6, exp_frac=t_exp / t, valu_frac=t_valu / t,
+               alg_bytes=nbytes, hbm_frac=nbytes / PEAK_HBM / t,
+               shape=f"b{batch} L{seqlen} d_inner{d_inner} N{dstate} bf16")
+    del plans, plans_hs
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_kda(cfg, steps, warmup):
     import mamformer_amd as mh
     from mamformer_amd import workloads as W
@@ -479,7 +518,7 @@ def measured_traffic(workload="ssd2"):
 
 # ----------------------------------------------------------------- main
 
-LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd2_bwd", "kda5_bwd", "conv1d", "kda5_ref", "kda_step", "ssd1",
+LEGS = ("ssd2", "decode", "ssd4", "kda5", "ssd2_bwd", "kda5_bwd", "conv1d", "kda5_ref", "kda_step", "ssd1", "ref1b",
         "ssd2_hstates", "cpu")
 
 
@@ -560,7 +599,9 @@ def main():
             "kernel": "mh_ssd_chunk_scan_fwd (ssd_lb_state_kernel + ssd_lb_scan_kernel)",
             "alg_bytes_per_launch": head["alg_bytes"], "alg_flops_per_launch": head["alg_flops"],
             "launch_us": round(head["us_per_step"], 2),
-            "mfma_frac": round(head["alg_flops"] / (head["us_per_step"] * 1e-6) / PEAK_BF16, 4),
+            # algorithmic FLOPs / time / dense bf16 peak (not a counter; the MFMA-busy counters of the two kernels
+            # are in profiles/sq_counters_ssd2_prefill.md)
+            "alg_flop_frac": round(head["alg_flops"] / (head["us_per_step"] * 1e-6) / PEAK_BF16, 4),
         }
         if tr is not None:
             out["roofline"]["traffic_source"] = tr.get("source")
@@ -612,6 +653,11 @@ def main():
             f"(h_states alone {r['us_h_states']:.1f} us, x{r['overhead']:.2f}); forward + backward "
             f"{r['us_train_with_h_states']:.0f} us with vs {r['us_train_plain']:.0f} us without")
         other["ssd2_hstates"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+    if "ref1b" in legs:
+        r = bench_ref_scan(max(5, args.steps // 10), 3)
+        log(f"reference-form prefill ({r['shape']}): {r['us_per_step']:.0f} us ({r['us_with_h_states']:.0f} us with "
+            f"h_states), exp roofline {r['exp_roofline_us']:.0f} us -> {r['exp_frac']:.3f}, VALU {r['valu_frac']:.3f}")
+        other["ref1b"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
     if "ssd1" in legs:
         r, _, _ = bench_ssd(W.SSD1, args.steps, args.warmup, nsets=1, chunk=64)
         other["ssd1"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MH_ABI_VERSION 8
+#define MH_ABI_VERSION 9
 
 /* element types of x / B / C / y / q / k / v / o */
 enum { MH_F32 = 0, MH_BF16 = 1 };
@@ -121,6 +121,21 @@ int mh_ssd_chunk_scan_fwd_noalloc(const mh_ssd_args* a, void* stream);
  *   scalar per (token, head): sum_p x.  Supported: nheads <= 128, and the forward's dstate range. */
 int mh_ssd_h_states_workspace_bytes(const mh_ssd_args* a, size_t* bytes);
 int mh_ssd_h_states(const mh_ssd_args* a, void* h_states, void* stream);
+
+/* The reference's own scan form: selective_scan / _selective_scan_impl (mamformer/layers/mamba2.py:31-130)
+ *   literally, with a decay rate per state column and a step size per channel,
+ *     h_t[c, n] = exp(A[n] dt_t[c]) h_{t-1}[c, n] + dt_t[c] x_t[c] B_t[n],  y_t[c] = sum_n C_t[n] h_t[c, n] + D[c] x_t[c]
+ *   for the d_inner = nheads * headdim channels c (the caller passes A = -exp(clamp(A_log, -5, 5)), mamba2.py:87-90).
+ *   Takes mh_ssd_args with flags MH_A_PER_STATE | MH_DT_PER_CHANNEL (required): A (dstate,) fp32; dt (b, L,
+ *   d_inner) fp32 with dt_bias (d_inner,) and the softplus / limit flags as in the decode step; x, y and z (b, L,
+ *   d_inner) with contiguous channels (x_stride_h = headdim); B, C (b, L, dstate) (ngroups 1); D (d_inner,) with
+ *   MH_D_PER_CHANNEL or (nheads,) or NULL; initial_state / final_state (b, d_inner, dstate) fp32 or NULL (the
+ *   reference starts from zero); chunk_len is ignored.  h_states (b, L, dstate) in the dtype of x, the mean over
+ *   channels of the state after every token (mamba2.py:114-116), or NULL; it needs the workspace
+ *   mh_ssd_ref_scan_workspace_bytes(a, 1, ..) gives (0 bytes without h_states).  Supported: dstate in {16, 32,
+ *   64, 128, 256}, d_inner a multiple of 16.  No backward. */
+int mh_ssd_ref_scan_workspace_bytes(const mh_ssd_args* a, int h_states, size_t* bytes);
+int mh_ssd_ref_scan_fwd(const mh_ssd_args* a, void* h_states, void* stream);
 
 /* Backward of h_states: the autograd backward of the mean over (h, p) of the states
  *   (mamformer/layers/mamba2.py:114-116) taken through the scan, i.e. the gradients of <dhs, h_states> for the

@@ -10,10 +10,11 @@ prologue); layer-level counterparts in ``mamformer_amd.layers``.  They run hand-
 from .ops import (Plan, causal_conv1d, diff_lambda, linear_attention_recurrent, linear_attention_scan, linear_attn_scan,
                   linear_attn_scan_pair, linear_attn_scan_single, linear_attn_step, plan_linear_attn_scan,
                   plan_linear_attn_step, plan_selective_scan, plan_selective_scan_bwd, plan_selective_state_update, recurrent_step,
-                  recurrent_step_reference,
+                  recurrent_step_reference, selective_scan_reference, plan_selective_scan_reference,
                   selective_scan, selective_scan_bwd, selective_state_update, ssd_chunk_len, linear_attn_scan_bwd)
 
-__all__ = ["selective_scan", "selective_scan_bwd", "selective_state_update", "recurrent_step", "recurrent_step_reference", "linear_attn_scan",
+__all__ = ["selective_scan", "selective_scan_bwd", "selective_state_update", "recurrent_step", "recurrent_step_reference", "selective_scan_reference",
+           "plan_selective_scan_reference", "linear_attn_scan",
            "linear_attn_scan_pair", "linear_attn_scan_single", "linear_attention_scan", "diff_lambda",
            "linear_attn_step", "linear_attention_recurrent",
            "ssd_chunk_len", "Plan", "plan_selective_scan", "plan_selective_scan_bwd", "plan_selective_state_update", "plan_linear_attn_scan",

@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # bytes of the static device scratch behind mh_ssd_chunk_scan_fwd_noalloc (MH_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -157,6 +157,7 @@ EXPORTS = (
     "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",
     "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states",
     "mh_ssd_h_states_bwd_workspace_bytes", "mh_ssd_h_states_bwd",
+    "mh_ssd_ref_scan_workspace_bytes", "mh_ssd_ref_scan_fwd",
     "mh_ssd_state_update",
     "mh_kda_chunk_scan_fwd", "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
     "mh_kda_recurrent_step",
@@ -201,6 +202,8 @@ def lib():
             h.mh_ssd_h_states.argtypes = [ct.POINTER(SsdArgs), _vp, _vp]
             h.mh_ssd_h_states_bwd_workspace_bytes.argtypes = [ct.POINTER(SsdHsBwdArgs), ct.POINTER(_sz)]
             h.mh_ssd_h_states_bwd.argtypes = [ct.POINTER(SsdHsBwdArgs), _vp]
+            h.mh_ssd_ref_scan_workspace_bytes.argtypes = [ct.POINTER(SsdArgs), ct.c_int, ct.POINTER(_sz)]
+            h.mh_ssd_ref_scan_fwd.argtypes = [ct.POINTER(SsdArgs), _vp, _vp]
             h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
             h.mh_kda_recurrent_step.argtypes = [ct.POINTER(KdaStepArgs), _vp]
             h.mh_kda_bwd_workspace_bytes.argtypes = [ct.POINTER(KdaBwdArgs), ct.POINTER(_sz)]
@@ -215,7 +218,8 @@ def lib():
                          "mh_ssd_bwd_workspace_bytes", "mh_ssd_chunk_scan_bwd",
                          "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
                          "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states",
-                         "mh_ssd_h_states_bwd_workspace_bytes", "mh_ssd_h_states_bwd"):
+                         "mh_ssd_h_states_bwd_workspace_bytes", "mh_ssd_h_states_bwd",
+                         "mh_ssd_ref_scan_workspace_bytes", "mh_ssd_ref_scan_fwd"):
                 getattr(h, name).restype = ct.c_int
             ver = h.mh_abi_version()
             if ver != ABI_VERSION:

@@ -20,7 +20,7 @@ LIB_NAME = "libmamformer_hip.so"
 LIB_PATH = HERE / LIB_NAME
 OFFLOAD_ARCH = "gfx950"
 
-SOURCES = ["ssd_decode.hip", "ssd_prefill.hip", "ssd_lookback.hip", "ssd_hstates.hip", "ssd_backward.hip", "kda_scan.hip", "kda_backward.hip", "kda_precise.hip", "kda_step.hip", "conv1d.hip", "widen.hip", "capi.hip"]
+SOURCES = ["ssd_decode.hip", "ssd_prefill.hip", "ssd_lookback.hip", "ssd_hstates.hip", "ssd_refform.hip", "ssd_backward.hip", "kda_scan.hip", "kda_backward.hip", "kda_precise.hip", "kda_step.hip", "conv1d.hip", "widen.hip", "capi.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={OFFLOAD_ARCH}",

@@ -779,6 +779,65 @@ int mh_ssd_h_states(const mh_ssd_args* a, void* h_states, void* stream) {
   return hip_status(mh::launch_ssd_hs(p, q, reinterpret_cast<hipStream_t>(stream)), "ssd_h_states");
 }
 
+// ---------------------------------------------------------------- the reference's own scan form
+static int rf_validate(const mh_ssd_args* a, bool h_states) {
+  if (!a) return fail(MH_ERR_NULL, "ssd_ref_scan: args is NULL");
+  if (a->batch <= 0 || a->seqlen < 0 || a->nheads <= 0 || a->headdim <= 0)
+    return fail(MH_ERR_SHAPE, "ssd_ref_scan: batch, nheads, headdim must be positive and seqlen >= 0");
+  const int64_t di = a->nheads * a->headdim;
+  if (a->batch * di > 0x7fffffffLL || a->seqlen > 0x7fffffffLL / 16)
+    return fail(MH_ERR_SHAPE, "ssd_ref_scan: sizes out of range");
+  const int es = elem_size(a->dtype);
+  if (!es) return fail(MH_ERR_DTYPE, "ssd_ref_scan: unknown dtype %d", a->dtype);
+  if ((a->flags & (MH_A_PER_STATE | MH_DT_PER_CHANNEL)) != (MH_A_PER_STATE | MH_DT_PER_CHANNEL))
+    return fail(MH_ERR_SHAPE, "ssd_ref_scan: the reference form takes MH_A_PER_STATE | MH_DT_PER_CHANNEL");
+  if (!mh::ssd_rf_supported((int)a->dstate))
+    return fail(MH_ERR_UNSUPPORTED, "ssd_ref_scan: dstate %lld not supported (16, 32, 64, 128, 256)",
+                (long long)a->dstate);
+  if (a->ngroups != 1) return fail(MH_ERR_UNSUPPORTED, "ssd_ref_scan: one group of B / C (ngroups 1)");
+  if (di % 16) return fail(MH_ERR_UNSUPPORTED, "ssd_ref_scan: d_inner = nheads * headdim must be a multiple of 16");
+  if ((a->flags & MH_DT_LIMIT) && !(a->dt_min <= a->dt_max)) return fail(MH_ERR_SHAPE, "ssd_ref_scan: dt_min > dt_max");
+  if (!a->A) return fail(MH_ERR_NULL, "ssd_ref_scan: A is required");
+  if (a->seqlen > 0 && (!a->x || !a->dt || !a->B || !a->C || !a->y))
+    return fail(MH_ERR_NULL, "ssd_ref_scan: x, dt, A, B, C, y are required");
+  if (a->x_stride_h != a->headdim || a->y_stride_h != a->headdim || (a->z && a->z_stride_h != a->headdim))
+    return fail(MH_ERR_STRIDE, "ssd_ref_scan: the channels of a token (heads x headdim) must be contiguous in x, y, z");
+  if (a->x_stride_l < di || a->y_stride_l < di || a->dt_stride_l < di || (a->z && a->z_stride_l < di))
+    return fail(MH_ERR_STRIDE, "ssd_ref_scan: token stride smaller than d_inner");
+  if (a->x_stride_b < 0 || a->dt_stride_b < 0 || a->y_stride_b < 0 || a->B_stride_b < 0 || a->C_stride_b < 0)
+    return fail(MH_ERR_STRIDE, "ssd_ref_scan: negative batch stride");
+  if (a->B_stride_l < a->dstate || a->C_stride_l < a->dstate)
+    return fail(MH_ERR_STRIDE, "ssd_ref_scan: B / C token stride smaller than dstate");
+  if (!aligned16(a->dt) || (a->dt_stride_l % 4) || (a->dt_stride_b % 4) || !aligned16(a->dt_bias))
+    return fail(MH_ERR_ALIGN, "ssd_ref_scan: dt rows and dt_bias must be 16-byte aligned");
+  if (!aligned16(a->B) || !aligned16(a->C) || !stride_ok(a->B_stride_b, es) || !stride_ok(a->B_stride_l, es) ||
+      !stride_ok(a->C_stride_b, es) || !stride_ok(a->C_stride_l, es))
+    return fail(MH_ERR_ALIGN, "ssd_ref_scan: B, C and their strides must be 16-byte aligned");
+  if (!aligned16(a->y) || !stride_ok(a->y_stride_b, es) || !stride_ok(a->y_stride_l, es))
+    return fail(MH_ERR_ALIGN, "ssd_ref_scan: y and its strides must be 16-byte aligned");
+  (void)h_states;
+  return MH_OK;
+}
+
+static void rf_fill(const mh_ssd_args* a, mh::RfParams& p) {
+  p = mh::RfParams{};
+  p.batch = (int)a->batch; p.seqlen = (int)a->seqlen; p.d_inner = (int)(a->nheads * a->headdim);
+  p.headdim = (int)a->headdim; p.dstate = (int)a->dstate; p.dtype = a->dtype == MH_BF16 ? mh::DT_BF16 : mh::DT_F32;
+  p.dt_softplus = (a->flags & MH_DT_SOFTPLUS) != 0;
+  p.has_dt_limit = (a->flags & MH_DT_LIMIT) != 0;
+  p.D_per_channel = (a->flags & MH_D_PER_CHANNEL) != 0;
+  p.dt_min = a->dt_min; p.dt_max = a->dt_max;
+  p.x = a->x; p.x_sb = a->x_stride_b; p.x_sl = a->x_stride_l;
+  p.dt = a->dt; p.dt_sb = a->dt_stride_b; p.dt_sl = a->dt_stride_l;
+  p.A = a->A;
+  p.B = a->B; p.B_sb = a->B_stride_b; p.B_sl = a->B_stride_l;
+  p.C = a->C; p.C_sb = a->C_stride_b; p.C_sl = a->C_stride_l;
+  p.D = a->D; p.dt_bias = a->dt_bias; p.init_state = a->initial_state;
+  p.y = a->y; p.y_sb = a->y_stride_b; p.y_sl = a->y_stride_l;
+  p.z = a->z; p.z_sb = a->z_stride_b; p.z_sl = a->z_stride_l;
+  p.final_state = a->final_state;
+}
+
 static int hs_bwd_validate(const mh_ssd_hs_bwd_args* a) {
   if (!a) return fail(MH_ERR_NULL, "ssd_h_states_bwd: args is NULL");
   int rc = hs_validate(&a->fwd);
@@ -794,6 +853,30 @@ static int hs_bwd_validate(const mh_ssd_hs_bwd_args* a) {
   if (!aligned16(a->dhs) || !aligned16(a->dx) || !aligned16(a->dB) || !aligned16(a->d_initial_state))
     return fail(MH_ERR_ALIGN, "ssd_h_states_bwd: dhs, dx, dB and d_initial_state must be 16-byte aligned");
   return MH_OK;
+}
+
+int mh_ssd_ref_scan_workspace_bytes(const mh_ssd_args* a, int h_states, size_t* bytes) {
+  if (!bytes) return fail(MH_ERR_NULL, "ssd_ref_scan: bytes output is NULL");
+  const int rc = rf_validate(a, h_states != 0);
+  if (rc) return rc;
+  *bytes = mh::ssd_rf_workspace_bytes((int)a->batch, (int)a->seqlen, (int)(a->nheads * a->headdim), (int)a->dstate,
+                                      h_states != 0);
+  return MH_OK;
+}
+
+int mh_ssd_ref_scan_fwd(const mh_ssd_args* a, void* h_states, void* stream) {
+  const int rc = rf_validate(a, h_states != nullptr);
+  if (rc) return rc;
+  const size_t need = mh::ssd_rf_workspace_bytes((int)a->batch, (int)a->seqlen, (int)(a->nheads * a->headdim),
+                                                 (int)a->dstate, h_states != nullptr);
+  if (need && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+    return fail(MH_ERR_WORKSPACE, "ssd_ref_scan: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
+                a->workspace_bytes);
+  mh::RfParams p;
+  rf_fill(a, p);
+  p.hs = h_states;
+  p.hs_part = reinterpret_cast<float*>(a->workspace);
+  return hip_status(mh::launch_ssd_rf(p, reinterpret_cast<hipStream_t>(stream)), "ssd_ref_scan");
 }
 
 int mh_ssd_h_states_bwd_workspace_bytes(const mh_ssd_hs_bwd_args* a, size_t* bytes) {

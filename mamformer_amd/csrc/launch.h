@@ -67,6 +67,30 @@ size_t ssd_workspace_bytes(int batch, int seqlen, int nchunks, int nheads, int h
 // Point p's workspace parts into `workspace` (ssd_workspace_bytes of p's sizes).
 void ssd_workspace_layout(SsdParams& p, void* workspace);
 
+// The reference's own scan form (ssd_refform.hip): a decay rate per state (A (N,), negative) and a step size per
+// channel (dt (b, L, d_inner)), one group of B / C; x, y, z (b, L, d_inner) with contiguous channels.
+struct RfParams {
+  int batch, seqlen, d_inner, headdim, dstate, dtype;
+  int dt_softplus, has_dt_limit, D_per_channel;
+  float dt_min, dt_max;
+  const void* x; int64_t x_sb, x_sl;
+  const float* dt; int64_t dt_sb, dt_sl;
+  const float* A;            // (N,) decay rates
+  const void* B; int64_t B_sb, B_sl;
+  const void* C; int64_t C_sb, C_sl;
+  const float* D;            // (d_inner,) or (d_inner / headdim,) or null
+  const float* dt_bias;      // (d_inner,) or null
+  const float* init_state;   // (b, d_inner, N) or null
+  void* y; int64_t y_sb, y_sl;
+  const void* z; int64_t z_sb, z_sl;   // optional gate
+  float* final_state;        // (b, d_inner, N) or null
+  void* hs;                  // (b, L, N) h_states in the I/O dtype, or null
+  float* hs_part;            // workspace: per-channel-block sums of the states, (b, blocks, L, N)
+};
+bool ssd_rf_supported(int dstate);
+size_t ssd_rf_workspace_bytes(int batch, int seqlen, int d_inner, int dstate, bool h_states);
+hipError_t launch_ssd_rf(const RfParams& p, hipStream_t st);
+
 // h_states of the prefill (ssd_hstates.hip): mean over (h, p) of the state after every token.
 struct HsParams {
   void* hs;                  // (b, L, N) in the I/O dtype

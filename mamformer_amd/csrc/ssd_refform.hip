@@ -1,0 +1,438 @@
+// The reference's own selective scan (mamformer/layers/mamba2.py:70-130) for gfx950: a decay rate per state
+// column and a step size per channel,
+//     h_t[c, n] = exp(A_n dt_t[c]) h_{t-1}[c, n] + dt_t[c] x_t[c] B_t[n],   y_t[c] = sum_n C_t[n] h_t[c, n] + D_c x_t[c]
+// with A_n = -exp(clamp(A_log_n, -5, 5)) formed by the caller.  The decay differs per (channel, state), so the
+// recurrence has no matrix-unit factorisation (the per-head SSD form does): every (token, channel, state) costs
+// one exponential and a few fused multiply-adds, and the kernels are bound by that VALU work.
+//
+// rf_scan_kernel, one workgroup per (batch, block of channels), walking the whole sequence:
+//   LPC = 32 lanes per channel (16 for N = 16), each owning N / 32 consecutive states, so the sum over states
+//   that forms y runs on the DPP crossbar (quad permutes, the row mirrors, then the row-15 broadcast that adds
+//   the two rows of a channel); a wave holds 2 channels, a workgroup of 4 waves 8.  Blocks of TB tokens of B, C
+//   (fp32), dt, x and the gate are staged in LDS (two stages; the next block's rows are loaded into registers
+//   while the current block computes, and each token's LDS values are read one token ahead), y is collected per
+//   block in LDS and stored as rows of the workgroup's channels.
+// rf_hs_kernel (h_states, the per-token mean of the state over all channels, mamba2.py:114-116):
+//   lane = channel (256 channels per workgroup), a workgroup per (batch, channel block, group of 4 states), so
+//   that the sum over channels is a reduce-scatter inside the wave (v_permlane32_swap, v_permlane16_swap, then the
+//   DPP row sums) plus a sum over the 4 waves; the per-block sums go to a workspace and rf_hs_reduce_kernel adds
+//   them in a fixed order (deterministic).
+#include "common.h"
+#include "launch.h"
+#include "ssd_shared.h"
+
+namespace mh {
+
+namespace {
+
+constexpr int RF_NT = 256;           // threads per workgroup (both kernels)
+constexpr int HS_CPB = 256;          // channels per workgroup of h_states
+constexpr int HS_NS = 4;             // states per thread of h_states
+constexpr int HS_TB = 16;            // tokens per block of h_states
+constexpr float LOG2E = 1.4426950408889634f;
+
+// Lanes per channel of the scan, states per lane, channels per workgroup, tokens per LDS block.
+template <int N> constexpr int rf_lpc() { return N >= 32 ? 32 : 16; }
+template <int N> constexpr int rf_ns() { return N / rf_lpc<N>(); }
+template <int N> constexpr int rf_cpb() { return 4 * (64 / rf_lpc<N>()); }
+template <int N> constexpr int rf_tb() { return N <= 128 ? 32 : 16; }
+
+// Per-lane token prologue: dt <- clamp(softplus?(dt + bias), dt_min, dt_max).
+__device__ __forceinline__ float rf_dt(const RfParams& p, float raw, float bias) {
+  float d = raw + bias;
+  if (p.dt_softplus) d = softplus_f(d);
+  if (p.has_dt_limit) d = fminf(fmaxf(d, p.dt_min), p.dt_max);
+  return d;
+}
+
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dppf(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, false));
+}
+// Sum over each 16-lane row, in every lane of the row: quad permutes, then the half-row and row mirrors.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dppf<0xB1>(v);      // quad_perm 1,0,3,2
+  v += dppf<0x4E>(v);      // quad_perm 2,3,0,1
+  v += dppf<0x141>(v);     // row_half_mirror
+  v += dppf<0x140>(v);     // row_mirror
+  return v;
+}
+
+// 8 consecutive elements of a row: load, convert to fp32, pack from fp32, store.
+template <typename T> struct Row8;
+template <> struct Row8<bf16> {
+  uint4 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ void set(const float* s) {
+    bf16x8 b;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) b[j] = (bf16)s[j];
+    v = __builtin_bit_cast(uint4, b);
+  }
+  __device__ __forceinline__ void store(bf16* d) const { *reinterpret_cast<uint4*>(d) = v; }
+  __device__ __forceinline__ void store_f32(float* d) const {
+    const bf16x8 b = __builtin_bit_cast(bf16x8, v);
+    reinterpret_cast<float4*>(d)[0] = float4{(float)b[0], (float)b[1], (float)b[2], (float)b[3]};
+    reinterpret_cast<float4*>(d)[1] = float4{(float)b[4], (float)b[5], (float)b[6], (float)b[7]};
+  }
+};
+template <> struct Row8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = reinterpret_cast<const float4*>(p)[0];
+    b = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ __forceinline__ void set(const float* s) {
+    a = float4{s[0], s[1], s[2], s[3]};
+    b = float4{s[4], s[5], s[6], s[7]};
+  }
+  __device__ __forceinline__ void store(float* d) const {
+    reinterpret_cast<float4*>(d)[0] = a;
+    reinterpret_cast<float4*>(d)[1] = b;
+  }
+  __device__ __forceinline__ void store_f32(float* d) const { store(d); }
+};
+
+template <int N, int TB, int CPB>
+struct RfStage {
+  float B[TB][N];
+  float C[TB][N];
+  float dt[TB][CPB];        // processed dt (0 past the sequence)
+  float x[TB][CPB];         // x (0 past the sequence)
+  float z[TB][CPB];         // gate (GATE only)
+};
+template <int N, int TB, int CPB>
+struct RfSmem {
+  RfStage<N, TB, CPB> st[2];
+  float y[2][TB][CPB];
+};
+
+// The rows of one token block held in registers between its load and its LDS store: thread i owns the 8-element
+// pieces i, i + 256, .. of B and of C (TB rows of N), and, for i < TB * CPB / 4, one 4-element piece of dt, x, z.
+template <typename T, int N, int TB, int CPB>
+struct RfRegs {
+  static constexpr int NP = TB * N / 8;                     // 8-element pieces of B (and of C) per block
+  static constexpr int PB = (NP + RF_NT - 1) / RF_NT;      // per thread
+  static constexpr int NQ = TB * CPB / 4;                  // 4-element pieces of dt (x, z) per block
+  Row8<T> b[PB], c[PB];
+  float4 dt;
+  float xv[4], zv[4];
+};
+
+// Workgroup -> (batch, channel block): runs of 4 consecutive blocks go to the same XCD (workgroups are dealt to
+// the 8 XCDs round-robin), so the x, y and z lines they share are read or written through one L2.
+__device__ __forceinline__ void rf_block(int nblk, int nper, int& b, int& cb) {
+  const int i = blockIdx.x;
+  int j = i;
+  if ((nblk & 31) == 0) j = 4 * ((i & 7) + 8 * (i >> 5)) + ((i >> 3) & 3);
+  b = j / nper;
+  cb = j % nper;
+}
+
+template <typename T, int N, int TB, int CPB, bool GATE>
+__device__ __forceinline__ void rf_load(const RfParams& p, RfRegs<T, N, TB, CPB>& r, int b, int c0, int t0) {
+  using R = RfRegs<T, N, TB, CPB>;
+  const int tid = threadIdx.x;
+  const int last = p.seqlen - 1;
+  const T* Bp = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb;
+  const T* Cp = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb;
+#pragma unroll
+  for (int q = 0; q < R::PB; ++q) {
+    const int e = min(tid + q * RF_NT, R::NP - 1);        // piece: row e / (N / 8), columns 8 (e % (N / 8))
+    const int row = min(t0 + e / (N / 8), last), col = 8 * (e % (N / 8));
+    r.b[q].load(Bp + (int64_t)row * p.B_sl + col);
+    r.c[q].load(Cp + (int64_t)row * p.C_sl + col);
+  }
+  if (tid < R::NQ) {
+    const int row = t0 + tid / (CPB / 4), col = 4 * (tid % (CPB / 4));
+    const int rr = min(row, last);
+    const bool in = row <= last;
+    const float4 raw = *reinterpret_cast<const float4*>(p.dt + (int64_t)b * p.dt_sb + (int64_t)rr * p.dt_sl + c0 + col);
+    const float4 bias = p.dt_bias ? *reinterpret_cast<const float4*>(p.dt_bias + c0 + col) : float4{0.f, 0.f, 0.f, 0.f};
+    r.dt = float4{in ? rf_dt(p, raw.x, bias.x) : 0.f, in ? rf_dt(p, raw.y, bias.y) : 0.f,
+                  in ? rf_dt(p, raw.z, bias.z) : 0.f, in ? rf_dt(p, raw.w, bias.w) : 0.f};
+    const T* xp = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)rr * p.x_sl + c0 + col;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.xv[j] = in ? to_f32(xp[j]) : 0.f;
+    if constexpr (GATE) {
+      const T* zp = reinterpret_cast<const T*>(p.z) + (int64_t)b * p.z_sb + (int64_t)rr * p.z_sl + c0 + col;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.zv[j] = to_f32(zp[j]);
+    }
+  }
+}
+
+template <typename T, int N, int TB, int CPB, bool GATE>
+__device__ __forceinline__ void rf_store(const RfRegs<T, N, TB, CPB>& r, RfStage<N, TB, CPB>& s) {
+  using R = RfRegs<T, N, TB, CPB>;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int q = 0; q < R::PB; ++q) {
+    const int e = tid + q * RF_NT;
+    if (R::NP % RF_NT != 0 && e >= R::NP) break;
+    r.b[q].store_f32(&s.B[e / (N / 8)][8 * (e % (N / 8))]);
+    r.c[q].store_f32(&s.C[e / (N / 8)][8 * (e % (N / 8))]);
+  }
+  if (tid < R::NQ) {
+    const int row = tid / (CPB / 4), col = 4 * (tid % (CPB / 4));
+    *reinterpret_cast<float4*>(&s.dt[row][col]) = r.dt;
+    *reinterpret_cast<float4*>(&s.x[row][col]) = float4{r.xv[0], r.xv[1], r.xv[2], r.xv[3]};
+    if constexpr (GATE) *reinterpret_cast<float4*>(&s.z[row][col]) = float4{r.zv[0], r.zv[1], r.zv[2], r.zv[3]};
+  }
+}
+
+// One token's operands, read from LDS a token ahead of their use.
+template <int NS>
+struct RfTok {
+  float dt, x, b[NS], c[NS];
+};
+template <int N, int TB, int CPB, int NS>
+__device__ __forceinline__ void rf_tok(const RfStage<N, TB, CPB>& s, int t, int cl, int n0, RfTok<NS>& o) {
+  o.dt = s.dt[t][cl];
+  o.x = s.x[t][cl];
+  if constexpr (NS % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < NS; q += 4) {
+      const float4 b4 = *reinterpret_cast<const float4*>(&s.B[t][n0 + q]);
+      const float4 c4 = *reinterpret_cast<const float4*>(&s.C[t][n0 + q]);
+      o.b[q] = b4.x; o.b[q + 1] = b4.y; o.b[q + 2] = b4.z; o.b[q + 3] = b4.w;
+      o.c[q] = c4.x; o.c[q + 1] = c4.y; o.c[q + 2] = c4.z; o.c[q + 3] = c4.w;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      o.b[q] = s.B[t][n0 + q];
+      o.c[q] = s.C[t][n0 + q];
+    }
+  }
+}
+
+template <typename T, int N, bool GATE>
+__global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
+  constexpr int TB = rf_tb<N>(), LPC = rf_lpc<N>(), NS = rf_ns<N>(), CPB = rf_cpb<N>();
+  __shared__ RfSmem<N, TB, CPB> sm;
+  const int nper = p.d_inner / CPB;
+  int b, cb;
+  rf_block(p.batch * nper, nper, b, cb);
+  const int c0 = cb * CPB;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int cl = (64 / LPC) * w + lane / LPC, g = lane % LPC;   // channel within the workgroup, its state group
+  const int c = c0 + cl;
+  const int n0 = g * NS;
+  // the lane that ends up with the channel's y: after the row sums (and, for two rows, the row-15 broadcast
+  // into the channel's second row) every lane of the last row holds it; take the row's last lane
+  const bool ylane = g == LPC - 1;
+  float k2[NS], h[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    k2[s] = p.A[n0 + s] * LOG2E;                           // exp(A dt) = 2^(A log2(e) dt)
+    h[s] = p.init_state ? p.init_state[((int64_t)b * p.d_inner + c) * N + n0 + s] : 0.f;
+  }
+  const float Dc = p.D ? (p.D_per_channel ? p.D[c] : p.D[c / p.headdim]) : 0.f;
+  const int nblk = (p.seqlen + TB - 1) / TB;
+  RfRegs<T, N, TB, CPB> r;
+  if (nblk > 0) {
+    rf_load<T, N, TB, CPB, GATE>(p, r, b, c0, 0);
+    rf_store<T, N, TB, CPB, GATE>(r, sm.st[0]);
+  }
+  if (nblk > 1) rf_load<T, N, TB, CPB, GATE>(p, r, b, c0, TB);
+  __syncthreads();
+  T* yb = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_sb + c0;
+  for (int k = 0; k < nblk; ++k) {
+    const RfStage<N, TB, CPB>& s = sm.st[k & 1];
+    float (*ys)[CPB] = sm.y[k & 1];
+    RfTok<NS> cur, nxt;
+    rf_tok<N, TB, CPB, NS>(s, 0, cl, n0, cur);
+#pragma unroll 2
+    for (int t = 0; t < TB; ++t) {
+      if (t + 1 < TB) rf_tok<N, TB, CPB, NS>(s, t + 1, cl, n0, nxt);
+      const float u = cur.dt * cur.x;
+      float yp = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < NS; ++s2) {
+        const float a = __builtin_amdgcn_exp2f(cur.dt * k2[s2]);
+        h[s2] = fmaf(a, h[s2], u * cur.b[s2]);
+        yp = fmaf(cur.c[s2], h[s2], yp);
+      }
+      yp = row_sum16(yp);
+      if constexpr (LPC == 32) yp += dppf<0x142, 0xa>(yp);   // row_bcast:15 -> rows 1, 3: both rows of a channel
+      if (ylane) {
+        float yv = yp + Dc * cur.x;
+        if constexpr (GATE) yv *= silu_f(s.z[t][cl]);
+        ys[t][cl] = yv;
+      }
+      cur = nxt;
+    }
+    if (k + 1 < nblk) rf_store<T, N, TB, CPB, GATE>(r, sm.st[(k + 1) & 1]);
+    if (k + 2 < nblk) rf_load<T, N, TB, CPB, GATE>(p, r, b, c0, (k + 2) * TB);
+    __syncthreads();
+    // y rows of this block: CPB channels = CPB / 8 pieces of 8 per token
+    if (tid < TB * (CPB / 8)) {
+      const int t = tid / (CPB / 8), piece = tid % (CPB / 8);
+      const int row = k * TB + t;
+      if (row < p.seqlen) {
+        Row8<T> o;
+        o.set(&ys[t][8 * piece]);
+        o.store(yb + (int64_t)row * p.y_sl + 8 * piece);
+      }
+    }
+  }
+  if (p.final_state) {
+    float* fo = p.final_state + ((int64_t)b * p.d_inner + c) * N + n0;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) fo[q] = h[q];
+  }
+}
+
+// h_states: sums over the workgroup's 256 channels of every state of group gs (4 states), per token, into
+// part[(b * ncb + cblk) * L + t][N]; channels past d_inner stay zero.
+template <typename T, int N>
+__global__ __launch_bounds__(RF_NT) void rf_hs_kernel(RfParams p) {
+  __shared__ float red[4][HS_TB][HS_NS];
+  __shared__ float4 sB[2][HS_TB];                          // the group's 4 states of B per token
+  const int ncb = (p.d_inner + HS_CPB - 1) / HS_CPB, ngs = N / HS_NS;
+  const int i = blockIdx.x;
+  const int gs = i % ngs, cblk = (i / ngs) % ncb, b = i / (ngs * ncb);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int c = cblk * HS_CPB + tid;
+  const bool on = c < p.d_inner;
+  const int cc = on ? c : p.d_inner - 1;
+  const int n0 = gs * HS_NS;
+  float k2[HS_NS], h[HS_NS];
+#pragma unroll
+  for (int s = 0; s < HS_NS; ++s) {
+    k2[s] = p.A[n0 + s] * LOG2E;
+    h[s] = (on && p.init_state) ? p.init_state[((int64_t)b * p.d_inner + c) * N + n0 + s] : 0.f;
+  }
+  const float bias = p.dt_bias ? p.dt_bias[cc] : 0.f;
+  const T* xp = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + cc;
+  const float* dtp = p.dt + (int64_t)b * p.dt_sb + cc;
+  const T* Bp = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + n0;
+  float* part = p.hs_part + ((int64_t)b * ncb + cblk) * p.seqlen * N + n0;
+  // the next block's dt, x (every thread) and B (threads < HS_TB) in registers while the current one computes
+  float dn[HS_TB], xn[HS_TB];
+  float4 bn = {0.f, 0.f, 0.f, 0.f};
+  auto load = [&](int t0) {
+#pragma unroll
+    for (int j = 0; j < HS_TB; ++j) {
+      const int t = min(t0 + j, p.seqlen - 1);
+      dn[j] = dtp[(int64_t)t * p.dt_sl];
+      xn[j] = to_f32(xp[(int64_t)t * p.x_sl]);
+    }
+    if (tid < HS_TB) {
+      const T* bp = Bp + (int64_t)min(t0 + tid, p.seqlen - 1) * p.B_sl;
+      bn = float4{to_f32(bp[0]), to_f32(bp[1]), to_f32(bp[2]), to_f32(bp[3])};
+    }
+  };
+  const int nblk = (p.seqlen + HS_TB - 1) / HS_TB;
+  if (nblk > 0) {
+    load(0);
+    if (tid < HS_TB) sB[0][tid] = bn;
+    __syncthreads();
+  }
+  const bool u32 = lane & 32, u16 = lane & 16;
+  for (int k = 0; k < nblk; ++k) {
+    float dc[HS_TB], xc[HS_TB];
+#pragma unroll
+    for (int j = 0; j < HS_TB; ++j) {
+      dc[j] = dn[j];
+      xc[j] = xn[j];
+    }
+    if (k + 1 < nblk) load((k + 1) * HS_TB);
+#pragma unroll 4
+    for (int j = 0; j < HS_TB; ++j) {
+      const int t = k * HS_TB + j;
+      const bool valid = on && t < p.seqlen;
+      const float dtv = valid ? rf_dt(p, dc[j], bias) : 0.f;
+      const float u = dtv * (valid ? xc[j] : 0.f);
+      const float4 b4 = sB[k & 1][j];
+      const float bv[HS_NS] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+      for (int s = 0; s < HS_NS; ++s) h[s] = fmaf(__builtin_amdgcn_exp2f(dtv * k2[s]), h[s], u * bv[s]);
+      // reduce-scatter over the wave: v_permlane32_swap leaves the lower half-wave states 0-1 and the upper
+      // states 2-3, each summed over its pair of lanes; v_permlane16_swap splits them again within each half;
+      // the DPP row sum then adds the 16 lanes of a row.  Row r (lanes 16 r ..) holds state r.
+      float v2[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(h[q]), __float_as_uint(h[q + 2]), false, false);
+        v2[q] = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+      }
+      const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(v2[0]), __float_as_uint(v2[1]), false, false);
+      float v1 = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+      v1 = row_sum16(v1);
+      if ((lane & 15) == 0) red[w][j][2 * (int)u32 + (int)u16] = v1;
+    }
+    if (k + 1 < nblk && tid < HS_TB) sB[(k + 1) & 1][tid] = bn;
+    __syncthreads();
+    if (tid < HS_TB * HS_NS) {
+      const int j = tid / HS_NS, s = tid % HS_NS;
+      const int t = k * HS_TB + j;
+      if (t < p.seqlen) part[(int64_t)t * N + s] = red[0][j][s] + red[1][j][s] + red[2][j][s] + red[3][j][s];
+    }
+    __syncthreads();
+  }
+}
+
+// hs[b, t, n] = (sum over channel blocks of part) / d_inner, blocks added in order.
+template <typename T>
+__global__ __launch_bounds__(256) void rf_hs_reduce_kernel(RfParams p) {
+  const int ncb = (p.d_inner + HS_CPB - 1) / HS_CPB;
+  const int64_t per = (int64_t)p.seqlen * p.dstate;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)p.batch * per) return;
+  const int64_t b = i / per, r = i % per;
+  float s = 0.f;
+  for (int k = 0; k < ncb; ++k) s += p.hs_part[(b * ncb + k) * per + r];
+  reinterpret_cast<T*>(p.hs)[i] = from_f32<T>(s / (float)p.d_inner);
+}
+
+template <typename T, int N>
+hipError_t launch_rf_t(const RfParams& p, hipStream_t st) {
+  const int nblk = p.batch * (p.d_inner / rf_cpb<N>());
+  if (nblk > 0 && (p.seqlen > 0 || p.final_state)) {
+    // (an empty sequence only writes the final state: the initial state, or zero)
+    if (p.z && p.seqlen > 0) hipLaunchKernelGGL((rf_scan_kernel<T, N, true>), dim3(nblk), dim3(RF_NT), 0, st, p);
+    else hipLaunchKernelGGL((rf_scan_kernel<T, N, false>), dim3(nblk), dim3(RF_NT), 0, st, p);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !p.hs || p.seqlen == 0) return e;
+  const int ncb = (p.d_inner + HS_CPB - 1) / HS_CPB;
+  hipLaunchKernelGGL((rf_hs_kernel<T, N>), dim3(p.batch * ncb * (N / HS_NS)), dim3(RF_NT), 0, st, p);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t tot = (int64_t)p.batch * p.seqlen * N;
+  hipLaunchKernelGGL((rf_hs_reduce_kernel<T>), dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_rf_n(const RfParams& p, hipStream_t st) {
+  switch (p.dstate) {
+    case 16: return launch_rf_t<T, 16>(p, st);
+    case 32: return launch_rf_t<T, 32>(p, st);
+    case 64: return launch_rf_t<T, 64>(p, st);
+    case 128: return launch_rf_t<T, 128>(p, st);
+    case 256: return launch_rf_t<T, 256>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool ssd_rf_supported(int dstate) {
+  return dstate == 16 || dstate == 32 || dstate == 64 || dstate == 128 || dstate == 256;
+}
+
+size_t ssd_rf_workspace_bytes(int batch, int seqlen, int d_inner, int dstate, bool h_states) {
+  if (!h_states) return 0;
+  const size_t ncb = (size_t)(d_inner + HS_CPB - 1) / HS_CPB;
+  return align256((size_t)batch * ncb * seqlen * dstate * 4);
+}
+
+hipError_t launch_ssd_rf(const RfParams& p, hipStream_t st) {
+  if (p.dtype == DT_BF16) return launch_rf_n<bf16>(p, st);
+  return launch_rf_n<float>(p, st);
+}
+
+}  // namespace mh

@@ -43,7 +43,7 @@ import torch
 from . import _lib
 from ._lib import SsdArgs, SsdBwdArgs, SsuArgs, KdaArgs, Conv1dArgs, Conv1dBwdArgs
 
-__all__ = ["selective_scan", "selective_scan_bwd", "plan_selective_scan_bwd", "selective_state_update", "recurrent_step", "linear_attn_scan",
+__all__ = ["selective_scan", "selective_scan_reference", "plan_selective_scan_reference", "selective_scan_bwd", "plan_selective_scan_bwd", "selective_state_update", "recurrent_step", "linear_attn_scan",
            "linear_attn_scan_pair", "linear_attn_scan_single", "linear_attention_scan", "diff_lambda",
            "linear_attn_step", "linear_attention_recurrent",
            "ssd_chunk_len", "Plan", "plan_selective_scan", "plan_selective_state_update", "plan_linear_attn_scan",
@@ -779,6 +779,101 @@ def recurrent_step_reference(x, dt, B, C, h_prev, A_log, D):
     y = selective_state_update(state, x[:, -1].reshape(b, H, P), dt[:, -1].reshape(b, H, P), A, B[:, -1],
                                C[:, -1], D, dt_softplus=False, out_state=out, A_per_state=True)
     return y.reshape(b, 1, d_inner), out.view(b, d_inner, N)
+
+
+def selective_scan_reference(x, dt, A, B, C, D, return_h_states=False, return_final_state=False, *,
+                             initial_state=None, dt_bias=None, dt_softplus=False, dt_limit=None, z=None,
+                             _plan_only=False):
+    """``selective_scan`` (R/mamformer/layers/mamba2.py:31-130) in the reference's own parameterisation, on the GPU:
+    a decay rate per state column and a step size per channel,
+        h_t[c, n] = exp(-exp(clamp(A[n], -5, 5)) dt_t[c]) h_{t-1}[c, n] + dt_t[c] x_t[c] B_t[n],
+        y_t[c] = sum_n C_t[n] h_t[c, n] + D[c] x_t[c].
+    Same arguments and return order as the reference: x, dt (b, L, d_inner) (dt already positive, as the block's
+    softplus leaves it; ``dt_softplus`` / ``dt_bias`` / ``dt_limit`` apply the prologue in-kernel instead), A the
+    log-rates A_log (N,) clamped to [-5, 5] as in :87, B, C (b, L, N), D (d_inner,) or None.  Returns y, or a tuple
+    (y, h_states (b, L, N) in the dtype of x, final_state (b, d_inner, N) float32) as requested (:121-130).
+    ``initial_state`` (b, d_inner, N) seeds the state (the reference starts at zero); ``z`` (b, L, d_inner) applies
+    the block's gate y * silu(z) (mamba2.py:337-338) in the kernel.  x / B / C / z bf16 or fp32 (y in that dtype),
+    state and arithmetic fp32.  Forward only (no autograd)."""
+    _require_cuda("selective_scan_reference", x, dt, A, B, C, D, initial_state, dt_bias, z)
+    if x.dim() != 3 or dt.shape != x.shape:
+        raise ValueError("selective_scan_reference: x and dt must be (batch, seqlen, d_inner)")
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, dt, A, B, C, D, initial_state, z)):
+        raise NotImplementedError("selective_scan_reference: no backward in this build (the per-head selective_scan "
+                                  "is the differentiable path)")
+    b, L, di = x.shape
+    if B.dim() == 4:
+        B, C = B.squeeze(2), C.squeeze(2)
+    N = A.shape[0]
+    if B.shape != (b, L, N) or C.shape != (b, L, N):
+        raise ValueError(f"selective_scan_reference: B and C must be (batch, seqlen, {N})")
+    if x.dtype not in _DT:
+        raise TypeError(f"selective_scan_reference: unsupported dtype {x.dtype}")
+    P = next(p for p in (64, 32, 16) if di % p == 0) if di % 16 == 0 else None
+    if P is None:
+        raise ValueError("selective_scan_reference: d_inner must be a multiple of 16")
+    H = di // P
+    dt32 = _inner_contig(dt.to(torch.float32))
+    if dt32.stride(1) % 4 or dt32.stride(0) % 4:
+        dt32 = dt32.contiguous()
+    rates = (-torch.exp(torch.clamp(A.to(torch.float32), min=-5.0, max=5.0))).contiguous()
+    xc = _inner_contig(x)
+    Bc = _inner_contig(B.to(x.dtype))
+    Cc = _inner_contig(C.to(x.dtype))
+    D32 = _f32c(D)
+    h0 = None if initial_state is None else initial_state.to(torch.float32).reshape(b, di, N).contiguous()
+    bias32 = _f32c(dt_bias)
+    y = torch.empty((b, L, di), device=x.device, dtype=x.dtype)
+    fin = torch.empty((b, di, N), device=x.device, dtype=torch.float32) if return_final_state else None
+    hs = torch.empty((b, L, N), device=x.device, dtype=x.dtype) if return_h_states else None
+    zc = None if z is None else _inner_contig(z.to(x.dtype))
+    a = _ssd_args(xc.view(b, L, H, P), dt32, rates, Bc.view(b, L, 1, N), Cc.view(b, L, 1, N), None, bias32,
+                  dt_softplus, dt_limit, h0, y.view(b, L, H, P), fin, None,
+                  None if zc is None else zc.view(b, L, H, P))
+    flags = a.flags | _lib.MH_A_PER_STATE | _lib.MH_DT_PER_CHANNEL
+    if D32 is not None:
+        a.D = _ptr(D32)
+        if D32.numel() == di:
+            flags |= _lib.MH_D_PER_CHANNEL
+        elif D32.numel() != H:
+            raise ValueError("selective_scan_reference: D must have d_inner entries")
+    a.flags = flags
+    # the (b, L, d_inner) rows: strides of the flattened channel axis
+    a.x_stride_h = a.y_stride_h = P
+    if zc is not None:
+        a.z_stride_h = P
+    n = ct.c_size_t()
+    _lib.call("mh_ssd_ref_scan_workspace_bytes", ct.byref(a), int(return_h_states), ct.byref(n))
+    ws = torch.empty(max(n.value, 1), device=x.device, dtype=torch.uint8) if n.value else None
+    a.workspace, a.workspace_bytes = _ptr(ws), n.value
+    if _plan_only:
+        return _RefScanPlan(a, _ptr(hs), x.device, keep=(xc, dt32, rates, Bc, Cc, D32, h0, bias32, zc, ws), y=y,
+                            h_states=hs, final_state=fin)
+    _lib.call("mh_ssd_ref_scan_fwd", ct.byref(a), _ptr(hs), _stream(x.device))
+    out = [y]
+    if return_h_states:
+        out.append(hs)
+    if return_final_state:
+        out.append(fin)
+    return out[0] if len(out) == 1 else tuple(out)
+
+
+class _RefScanPlan(Plan):
+    """``Plan`` of ``mh_ssd_ref_scan_fwd``, whose h_states pointer is an argument of its own."""
+
+    def __init__(self, args, hs_ptr, device, keep=(), **outputs):
+        super().__init__("mh_ssd_ref_scan_fwd", args, device, keep, **outputs)
+        self._hs = hs_ptr
+
+    def __call__(self, stream=None):
+        s = _stream(self._device) if stream is None else ct.c_void_p(stream)
+        _lib.call(self._fn, ct.byref(self._args), self._hs, s)
+        return self
+
+
+def plan_selective_scan_reference(*args, **kw):
+    """``Plan`` of ``selective_scan_reference`` on fixed buffers (outputs ``y``, ``h_states``, ``final_state``)."""
+    return selective_scan_reference(*args, _plan_only=True, **kw)
 
 
 def plan_linear_attn_scan(*args, **kw):
