@@ -418,9 +418,52 @@ def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, 
     cfg = (dt_softplus, dt_limit, chunk_size)
     if grad:
         return _HStatesFn.apply(x4, dt32, A32, B4, h0, bias32, cfg)
-    if x4.shape[2] > 128:
-        return _h_states_swap(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size)
-    return _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit)
+    return _h_states_fwd(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit)
+
+
+_HS_MAXH = 128    # heads the h_states kernels hold at once (forward and backward)
+_HS_BWD_MAXN = 128  # state columns of the h_states backward kernel
+
+
+def _head_blocks(H, G):
+    """Blocks [h0, h1) of at most 128 heads that never split a group unless a group alone has more than 128 heads
+    (then it is cut into pieces of at most 128).  h_states is a sum over heads, so blocks combine linearly."""
+    hpg = H // G
+    out = []
+    if hpg <= _HS_MAXH:
+        k = _HS_MAXH // hpg
+        for g0 in range(0, G, k):
+            out.append((g0 * hpg, min(G, g0 + k) * hpg))
+    else:
+        for g in range(G):
+            for h0 in range(g * hpg, (g + 1) * hpg, _HS_MAXH):
+                out.append((h0, min(h0 + _HS_MAXH, (g + 1) * hpg)))
+    return out
+
+
+def _h_block_args(x4, dt32, A32, B4, h0, bias32, h0_, h1_):
+    """The inputs restricted to heads [h0_, h1_) and their groups (B / C groups as a contiguous slice)."""
+    H, G = x4.shape[2], B4.shape[2]
+    hpg = H // G
+    g0, g1 = h0_ // hpg, (h1_ - 1) // hpg + 1
+    return (x4[:, :, h0_:h1_], dt32[:, :, h0_:h1_], A32[h0_:h1_].contiguous(), B4[:, :, g0:g1].contiguous(),
+            None if h0 is None else h0[:, h0_:h1_].contiguous(),
+            None if bias32 is None else bias32[h0_:h1_].contiguous(), g0, g1)
+
+
+def _h_states_fwd(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
+    """h_states by ``mh_ssd_h_states``; more than 128 heads run as head blocks whose fp32 h_states are combined
+    with weights H_block / H (the mean over (h, p) is linear in the heads)."""
+    H = x4.shape[2]
+    if H <= _HS_MAXH:
+        return _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit)
+    x32, B32 = x4.to(torch.float32), B4.to(torch.float32)
+    acc = None
+    for h0_, h1_ in _head_blocks(H, B4.shape[2]):
+        xb, db, ab, bb, h0b, biasb, _, _ = _h_block_args(x32, dt32, A32, B32, h0, bias32, h0_, h1_)
+        part = _h_states_kernel(xb, db, ab, bb, h0b, biasb, dt_softplus, dt_limit) * ((h1_ - h0_) / H)
+        acc = part if acc is None else acc + part
+    return acc.to(x4.dtype)
 
 
 def _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
@@ -460,24 +503,69 @@ def _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_lim
     return dx, ddt, dA, dB, dh0, dbias
 
 
+def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
+    """``mh_ssd_h_states_bwd`` for any head count and dstate: the state columns separate (column n of h_states
+    depends on B[..., n] alone; dx, ddt, dA and d dt_bias are sums over columns, dB and d h0 per column), so
+    dstate > 128 runs as column pieces of at most 128; the heads enter h_states as a sum, so more than 128 heads
+    run as head blocks, each with the gradient scaled by H_block / H (its h_states is a mean over its own heads).
+    Every piece is the dedicated kernel; pieces combine in a fixed order (deterministic)."""
+    b, L, H, P = x4.shape
+    G, N = B4.shape[2], B4.shape[3]
+    if N > _HS_BWD_MAXN:
+        outs = []
+        for n0 in range(0, N, _HS_BWD_MAXN):
+            n1 = min(N, n0 + _HS_BWD_MAXN)
+            outs.append(_h_states_bwd_blocks(ghs[..., n0:n1], x4, dt32, A32, B4[..., n0:n1].contiguous(),
+                                             None if h0 is None else h0[..., n0:n1].contiguous(), bias32,
+                                             dt_softplus, dt_limit))
+        dx = sum(o[0].to(torch.float32) for o in outs).to(x4.dtype)
+        ddt = sum(o[1] for o in outs)
+        dA = sum(o[2] for o in outs)
+        dB = torch.cat([o[3] for o in outs], dim=-1)
+        dh0 = None if h0 is None else torch.cat([o[4] for o in outs], dim=-1)
+        dbias = None if bias32 is None else sum(o[5] for o in outs)
+        return dx, ddt, dA, dB, dh0, dbias
+    if H <= _HS_MAXH:
+        return _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit)
+    dev = x4.device
+    dx = torch.empty((b, L, H, P), device=dev, dtype=x4.dtype)
+    ddt = torch.empty((b, L, H), device=dev, dtype=torch.float32)
+    dA = torch.empty((H,), device=dev, dtype=torch.float32)
+    dB = torch.zeros((b, L, G, N), device=dev, dtype=torch.float32)
+    dh0 = None if h0 is None else torch.empty((b, H, P, N), device=dev, dtype=torch.float32)
+    dbias = None if bias32 is None else torch.empty((H,), device=dev, dtype=torch.float32)
+    g32 = ghs.to(torch.float32)
+    for h0_, h1_ in _head_blocks(H, G):
+        xb, db, ab, bb, h0b, biasb, g0, g1 = _h_block_args(x4, dt32, A32, B4, h0, bias32, h0_, h1_)
+        r = _h_states_bwd_kernel(g32 * ((h1_ - h0_) / H), xb, db, ab, bb, h0b, biasb, dt_softplus, dt_limit)
+        dx[:, :, h0_:h1_] = r[0]
+        ddt[:, :, h0_:h1_] = r[1]
+        dA[h0_:h1_] = r[2]
+        dB[:, :, g0:g1] += r[3].to(torch.float32)
+        if dh0 is not None:
+            dh0[:, h0_:h1_] = r[4]
+        if dbias is not None:
+            dbias[h0_:h1_] = r[5]
+    return dx, ddt, dA, dB.to(B4.dtype), dh0, dbias
+
+
 class _HStatesFn(torch.autograd.Function):
-    """h_states with its gradient: forward = ``mh_ssd_h_states``; backward = ``mh_ssd_h_states_bwd`` (nheads and
-    dstate <= 128), else autograd of the swapped prefill (``_h_states_swap``) recomputed on the saved inputs."""
+    """h_states with its gradient: forward = ``mh_ssd_h_states``, backward = ``mh_ssd_h_states_bwd``, each as head
+    blocks and state-column pieces of at most 128 (``_h_states_fwd``, ``_h_states_bwd_blocks``); only a headdim
+    other than 64 (which the prefill itself does not take) would differentiate the swapped prefill instead."""
 
     @staticmethod
     def forward(ctx, x4, dt32, A32, B4, h0, bias32, cfg):
         ctx.save_for_backward(x4, dt32, A32, B4, h0, bias32)
         ctx.cfg = cfg
-        if x4.shape[2] > 128:
-            return _h_states_swap(x4, dt32, A32, B4, h0, bias32, *cfg)
-        return _h_states_kernel(x4, dt32, A32, B4, h0, bias32, cfg[0], cfg[1])
+        return _h_states_fwd(x4, dt32, A32, B4, h0, bias32, cfg[0], cfg[1])
 
     @staticmethod
     def backward(ctx, ghs):
         saved = ctx.saved_tensors
-        x4, B4 = saved[0], saved[3]
-        if x4.shape[2] <= 128 and B4.shape[3] <= 128 and x4.shape[3] == 64:
-            dx, ddt, dA, dB, dh0, dbias = _h_states_bwd_kernel(ghs, *saved, ctx.cfg[0], ctx.cfg[1])
+        x4 = saved[0]
+        if x4.shape[3] == 64:
+            dx, ddt, dA, dB, dh0, dbias = _h_states_bwd_blocks(ghs, *saved, ctx.cfg[0], ctx.cfg[1])
             need = ctx.needs_input_grad
             return (dx if need[0] else None, ddt if need[1] else None, dA if need[2] else None,
                     dB if need[3] else None, dh0 if need[4] else None, dbias if need[5] else None, None)

@@ -182,12 +182,17 @@ def _h_states_f64(x, dt_raw, A, B, bias, h0, limit):
     (torch.float32, 1, 40, 128, 2, 128, True, None, 2.5),
     (torch.float32, 1, 150, 8, 2, 64, True, None, 60.0),
     (torch.bfloat16, 2, 33, 5, 1, 8, False, (0.01, 2.0), 2.5),
+    (torch.float32, 1, 40, 4, 1, 256, True, None, 2.5),        # dstate 256: two column pieces of 128
+    (torch.float32, 1, 33, 192, 3, 64, True, None, 2.5),       # 192 heads: blocks of two groups and one group
+    (torch.float32, 1, 20, 160, 1, 32, False, None, 2.5),      # one group of 160 heads, cut at 128
+    (torch.bfloat16, 1, 30, 136, 2, 200, True, (0.02, 1.5), 2.5),   # both splits at once
 ])
 def test_h_states_gradients_alone_vs_recurrence(dtype, b, L, H, G, N, h0, limit, A_scale):
-    """The gradient of <wh, h_states> alone (mh_ssd_h_states_bwd, nheads and dstate <= 128) w.r.t. x, the raw dt,
-    A, B, dt_bias and the initial state against autograd of the float64 full-state recurrence: ragged segment
-    ends, several groups, odd heads per group, the clamp's zero gradient, 128 heads, one token, and decays far
-    beyond e^-80 per 32-token segment (A_scale)."""
+    """The gradient of <wh, h_states> alone (mh_ssd_h_states_bwd; more than 128 heads or dstate above 128 as head
+    blocks and state-column pieces of the same kernels) w.r.t. x, the raw dt, A, B, dt_bias and the initial state
+    against autograd of the float64 full-state recurrence: ragged segment ends, several groups, odd heads per
+    group, the clamp's zero gradient, 128 to 192 heads, dstate 200 and 256, one token, and decays far beyond e^-80
+    per 32-token segment (A_scale)."""
     g = torch.Generator().manual_seed(L * 13 + H + N)
     P = 64
     q = lambda t: t.to(dtype).to(torch.float64)
