@@ -375,6 +375,28 @@ int mh_causal_conv1d_bwd(const mh_conv1d_bwd_args* a, void* stream);
 int mh_abi_version(void);
 const char* mh_last_error(void);
 
+/* ------------------------------------------------------------------------
+ * The output gate of the Mamba-2 block, y * silu(z) (mamformer/layers/mamba2.py:337-338), for the training path,
+ * where the ungated y is kept for the backward (the inference path gates inside the scan: mh_ssd_args.z).
+ * Tensors (b, L, H, P) in `dtype` with innermost dimension contiguous and the other three strided (elements);
+ * P a multiple of 8, 16-byte aligned rows.
+ *   mh_silu_gate_fwd: out = y * silu(z).
+ *   mh_silu_gate_bwd: with g the gradient of the gated output, dy = g * silu(z) and
+ *                     dz = g * y * silu'(z), silu'(z) = s (1 + z (1 - s)), s = sigmoid(z); fp32 arithmetic.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int64_t batch, seqlen, nheads, headdim;
+  int32_t dtype;
+  int32_t reserved;
+  const void* y;  int64_t y_stride_b, y_stride_l, y_stride_h;
+  const void* z;  int64_t z_stride_b, z_stride_l, z_stride_h;
+  const void* g;  int64_t g_stride_b, g_stride_l, g_stride_h;   /* backward only */
+  void* out;      int64_t out_stride_b, out_stride_l, out_stride_h; /* forward: gated y; backward: dy */
+  void* dz;       int64_t dz_stride_b, dz_stride_l, dz_stride_h;  /* backward only */
+} mh_gate_args;
+int mh_silu_gate_fwd(const mh_gate_args* a, void* stream);
+int mh_silu_gate_bwd(const mh_gate_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -150,6 +150,18 @@ class Conv1dBwdArgs(ct.Structure):
         ("workspace", _vp), ("workspace_bytes", _sz),
     ]
 
+class GateArgs(ct.Structure):
+    _fields_ = [
+        ("batch", _i64), ("seqlen", _i64), ("nheads", _i64), ("headdim", _i64),
+        ("dtype", _i32), ("reserved", _i32),
+        ("y", _vp), ("y_stride_b", _i64), ("y_stride_l", _i64), ("y_stride_h", _i64),
+        ("z", _vp), ("z_stride_b", _i64), ("z_stride_l", _i64), ("z_stride_h", _i64),
+        ("g", _vp), ("g_stride_b", _i64), ("g_stride_l", _i64), ("g_stride_h", _i64),
+        ("out", _vp), ("out_stride_b", _i64), ("out_stride_l", _i64), ("out_stride_h", _i64),
+        ("dz", _vp), ("dz_stride_b", _i64), ("dz_stride_l", _i64), ("dz_stride_h", _i64),
+    ]
+
+
 # every symbol include/mamformer_hip.h declares
 EXPORTS = (
     "mh_abi_version", "mh_last_error",
@@ -158,6 +170,7 @@ EXPORTS = (
     "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states",
     "mh_ssd_h_states_bwd_workspace_bytes", "mh_ssd_h_states_bwd",
     "mh_ssd_ref_scan_workspace_bytes", "mh_ssd_ref_scan_fwd",
+    "mh_silu_gate_fwd", "mh_silu_gate_bwd",
     "mh_ssd_state_update",
     "mh_kda_chunk_scan_fwd", "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
     "mh_kda_recurrent_step",
@@ -204,6 +217,8 @@ def lib():
             h.mh_ssd_h_states_bwd.argtypes = [ct.POINTER(SsdHsBwdArgs), _vp]
             h.mh_ssd_ref_scan_workspace_bytes.argtypes = [ct.POINTER(SsdArgs), ct.c_int, ct.POINTER(_sz)]
             h.mh_ssd_ref_scan_fwd.argtypes = [ct.POINTER(SsdArgs), _vp, _vp]
+            h.mh_silu_gate_fwd.argtypes = [ct.POINTER(GateArgs), _vp]
+            h.mh_silu_gate_bwd.argtypes = [ct.POINTER(GateArgs), _vp]
             h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
             h.mh_kda_recurrent_step.argtypes = [ct.POINTER(KdaStepArgs), _vp]
             h.mh_kda_bwd_workspace_bytes.argtypes = [ct.POINTER(KdaBwdArgs), ct.POINTER(_sz)]
@@ -219,7 +234,8 @@ def lib():
                          "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
                          "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states",
                          "mh_ssd_h_states_bwd_workspace_bytes", "mh_ssd_h_states_bwd",
-                         "mh_ssd_ref_scan_workspace_bytes", "mh_ssd_ref_scan_fwd"):
+                         "mh_ssd_ref_scan_workspace_bytes", "mh_ssd_ref_scan_fwd",
+                         "mh_silu_gate_fwd", "mh_silu_gate_bwd"):
                 getattr(h, name).restype = ct.c_int
             ver = h.mh_abi_version()
             if ver != ABI_VERSION:

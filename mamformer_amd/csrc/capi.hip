@@ -855,6 +855,57 @@ static int hs_bwd_validate(const mh_ssd_hs_bwd_args* a) {
   return MH_OK;
 }
 
+// ---------------------------------------------------------------- output gate (training path)
+static int gate_validate(const mh_gate_args* a, bool bwd) {
+  if (!a) return fail(MH_ERR_NULL, "silu_gate: args is NULL");
+  if (a->batch < 0 || a->seqlen < 0 || a->nheads < 0 || a->headdim <= 0)
+    return fail(MH_ERR_SHAPE, "silu_gate: sizes must be non-negative (headdim positive)");
+  if (a->headdim % 8) return fail(MH_ERR_UNSUPPORTED, "silu_gate: headdim must be a multiple of 8");
+  const int es = elem_size(a->dtype);
+  if (!es) return fail(MH_ERR_DTYPE, "silu_gate: unknown dtype %d", a->dtype);
+  if (a->batch * a->seqlen * a->nheads == 0) return MH_OK;
+  if (!a->y || !a->z || !a->out || (bwd && (!a->g || !a->dz)))
+    return fail(MH_ERR_NULL, bwd ? "silu_gate_bwd: y, z, g, out (dy), dz are required"
+                                 : "silu_gate_fwd: y, z, out are required");
+  const void* ptrs[5] = {a->y, a->z, a->out, bwd ? a->g : a->y, bwd ? a->dz : a->y};
+  const int64_t strides[5][3] = {{a->y_stride_b, a->y_stride_l, a->y_stride_h},
+                                 {a->z_stride_b, a->z_stride_l, a->z_stride_h},
+                                 {a->out_stride_b, a->out_stride_l, a->out_stride_h},
+                                 {a->g_stride_b, a->g_stride_l, a->g_stride_h},
+                                 {a->dz_stride_b, a->dz_stride_l, a->dz_stride_h}};
+  for (int i = 0; i < (bwd ? 5 : 3); ++i) {
+    if (!aligned16(ptrs[i])) return fail(MH_ERR_ALIGN, "silu_gate: tensors must be 16-byte aligned");
+    for (int k = 0; k < 3; ++k)
+      if (strides[i][k] < 0 || !stride_ok(strides[i][k], es))
+        return fail(MH_ERR_ALIGN, "silu_gate: strides must be non-negative multiples of 16 bytes");
+  }
+  return MH_OK;
+}
+
+static hipError_t gate_launch(const mh_gate_args* a, bool bwd, hipStream_t st) {
+  mh::GateParams g{};
+  g.es = elem_size(a->dtype);
+  g.d0 = a->batch; g.d1 = a->seqlen; g.d2 = a->nheads; g.ncols = a->headdim;
+  g.y = a->y; g.y0 = a->y_stride_b; g.y1 = a->y_stride_l; g.y2 = a->y_stride_h;
+  g.z = a->z; g.z0 = a->z_stride_b; g.z1 = a->z_stride_l; g.z2 = a->z_stride_h;
+  g.g = a->g; g.g0 = a->g_stride_b; g.g1 = a->g_stride_l; g.g2 = a->g_stride_h;
+  g.out = a->out; g.o0 = a->out_stride_b; g.o1 = a->out_stride_l; g.o2 = a->out_stride_h;
+  g.dz = a->dz; g.dz0 = a->dz_stride_b; g.dz1 = a->dz_stride_l; g.dz2 = a->dz_stride_h;
+  return mh::launch_gate(g, bwd, st);
+}
+
+int mh_silu_gate_fwd(const mh_gate_args* a, void* stream) {
+  const int rc = gate_validate(a, false);
+  if (rc) return rc;
+  return hip_status(gate_launch(a, false, reinterpret_cast<hipStream_t>(stream)), "silu_gate_fwd");
+}
+
+int mh_silu_gate_bwd(const mh_gate_args* a, void* stream) {
+  const int rc = gate_validate(a, true);
+  if (rc) return rc;
+  return hip_status(gate_launch(a, true, reinterpret_cast<hipStream_t>(stream)), "silu_gate_bwd");
+}
+
 int mh_ssd_ref_scan_workspace_bytes(const mh_ssd_args* a, int h_states, size_t* bytes) {
   if (!bytes) return fail(MH_ERR_NULL, "ssd_ref_scan: bytes output is NULL");
   const int rc = rf_validate(a, h_states != 0);

@@ -247,5 +247,16 @@ struct RowAdd {
   const void* gate; int64_t g0, g1, g2;
 };
 hipError_t launch_row_add(const RowAdd& a, hipStream_t st);
+// The block's output gate: forward out = y silu(z); backward out = g silu(z), dz = g y silu'(z) (widen.hip).
+struct GateParams {
+  int es;
+  int64_t d0, d1, d2, ncols;
+  const void* y; int64_t y0, y1, y2;
+  const void* z; int64_t z0, z1, z2;
+  const void* g; int64_t g0, g1, g2;
+  void* out; int64_t o0, o1, o2;
+  void* dz; int64_t dz0, dz1, dz2;
+};
+hipError_t launch_gate(const GateParams& a, bool backward, hipStream_t st);
 
 }  // namespace mh

@@ -242,7 +242,7 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
         cfg = (dt_softplus, dt_limit, chunk_size)
         y4, fin = _SelectiveScanFn.apply(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg)
         if z4 is not None:
-            y4 = y4 * torch.nn.functional.silu(z4)
+            y4 = _GateFn.apply(y4, z4)
         out = [y4.reshape(x.shape) if x.dim() == 3 else y4]
         if return_h_states:
             out.append(_h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=True))
@@ -348,6 +348,45 @@ class _SelectiveScanFn(torch.autograd.Function):
         dx, ddt, dA, dB, dC, dD, dh0, dbias = _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, ctx.cfg, dy4,
                                                         dfin, need_dh0)
         return dx, ddt, dA, dB, dC, dD, dh0, dbias, None
+
+
+def _gate_args(y4, z4, out, g=None, dz=None):
+    b, L, H, P = y4.shape
+    a = _lib.GateArgs()
+    a.batch, a.seqlen, a.nheads, a.headdim = b, L, H, P
+    a.dtype = _DT[y4.dtype]
+    for name, t in (("y", y4), ("z", z4), ("out", out), ("g", g), ("dz", dz)):
+        if t is not None:
+            setattr(a, name, _ptr(t))
+            setattr(a, name + "_stride_b", t.stride(0))
+            setattr(a, name + "_stride_l", t.stride(1))
+            setattr(a, name + "_stride_h", t.stride(2))
+    return a
+
+
+class _GateFn(torch.autograd.Function):
+    """The block's output gate y * silu(z) (R/mamformer/layers/mamba2.py:337-338) on the training path, where the
+    ungated y is kept for the backward: one fused pass forward (``mh_silu_gate_fwd``) and one backward
+    (``mh_silu_gate_bwd``: dy = g silu(z), dz = g y silu'(z)) instead of torch's separate element-wise kernels."""
+
+    @staticmethod
+    def forward(ctx, y4, z4):
+        y4c = _inner_contig(y4)
+        out = torch.empty(y4.shape, device=y4.device, dtype=y4.dtype)
+        _lib.call("mh_silu_gate_fwd", ct.byref(_gate_args(y4c, z4, out)), _stream(y4.device))
+        ctx.save_for_backward(y4c, z4)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        y4, z4 = ctx.saved_tensors
+        g = _inner_contig(g.to(y4.dtype))
+        if any(s < 0 for s in g.stride()) or g.stride(2) < y4.shape[3]:
+            g = g.contiguous()
+        dy = torch.empty(y4.shape, device=y4.device, dtype=y4.dtype)
+        dz = torch.empty(y4.shape, device=y4.device, dtype=y4.dtype)
+        _lib.call("mh_silu_gate_bwd", ct.byref(_gate_args(y4, z4, dy, g, dz)), _stream(y4.device))
+        return dy, dz
 
 
 def plan_selective_scan_bwd(*args, **kw):

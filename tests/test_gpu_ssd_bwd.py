@@ -230,3 +230,33 @@ def test_bwd_full_shape_linearity_and_leading_slice():
     check("slice dA", g["dA"], r["dA"], tol)
     check("slice dD", g["dD"], r["dD"], tol)
     check("slice dh0", g["d_initial_state"], r["dh0"], tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_output_gate_kernels_vs_float64(dtype):
+    """The training path's fused gate (mh_silu_gate_fwd / mh_silu_gate_bwd) against float64 torch: out = y silu(z),
+    dy = g silu(z), dz = g y silu'(z); z a strided view (a slice of a wider projection), and a broadcast gradient
+    (the gradient of a sum) with zero strides."""
+    from mamformer_amd.ops import _GateFn
+    g0 = torch.Generator().manual_seed(12)
+    b, L, H, P = 2, 37, 3, 64
+    y = torch.randn(b, L, H, P, generator=g0).to(dtype)
+    zw = (torch.randn(b, L, H, 2 * P, generator=g0) * 3).to(dtype)
+    gr = torch.randn(b, L, H, P, generator=g0).to(dtype)
+    say(f"output gate kernels {dtype}")
+    yd = y.cuda().requires_grad_()
+    zd = zw.cuda()[..., :P].detach().requires_grad_()
+    out = _GateFn.apply(yd, zd)
+    out.backward(gr.cuda())
+    torch.cuda.synchronize()
+    y64, z64, g64 = y.double(), zw[..., :P].double(), gr.double()
+    s = torch.sigmoid(z64)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    check("out", out, (y64 * z64 * s).numpy(), tol)
+    check("dy", yd.grad, (g64 * z64 * s).numpy(), tol)
+    check("dz", zd.grad, (g64 * y64 * s * (1 + z64 * (1 - s))).numpy(), tol)
+    yd.grad = None
+    zd.grad = None
+    _GateFn.apply(yd, zd).float().sum().backward()
+    torch.cuda.synchronize()
+    check("dz (broadcast gradient)", zd.grad, (y64 * s * (1 + z64 * (1 - s))).numpy(), tol)
