@@ -165,7 +165,8 @@ def bench_ssd(cfg, steps, warmup, nsets, chunk=None):
 def bench_ssd_hstates(cfg, steps, warmup):
     """Cost of return_h_states at the headline shape: selective_scan with and without h_states through the same
     Python entry (allocation of outputs and workspace included in both), and the h_states computation alone
-    (``mh_ssd_h_states``: the local, carry and output kernels over the state's channel sums)."""
+    (``mh_ssd_h_states``: the local, carry and output kernels over the state's channel sums, reading the sums of
+    x per half head that the prefill writes alongside y, ``xsum``)."""
     import mamformer_amd as mh
     from mamformer_amd import ops
     from mamformer_amd import workloads as W
@@ -178,8 +179,10 @@ def bench_ssd_hstates(cfg, steps, warmup):
         _, plain = time_plans([lambda: mh.selective_scan(*args, return_final_state=True)], steps, warmup)
         _, both = time_plans([lambda: mh.selective_scan(*args, return_h_states=True, return_final_state=True)],
                              steps, warmup)
-        _, alone = time_plans([lambda: ops._h_states(x4, inp["dt"], inp["A"], B4, None, None, False, None, None)],
-                              steps, warmup)
+        b_, L_, H_, P_ = x4.shape
+        xsum = x4.float().view(b_, L_, H_, 2, P_ // 2).sum(-1).contiguous()
+        _, alone = time_plans([lambda: ops._h_states(x4, inp["dt"], inp["A"], B4, None, None, False, None, None,
+                                                     xsum=xsum)], steps, warmup)
     # training: forward + backward of <gy, y> (+ <ghs, h_states>) through autograd
     leaves = [t.clone().requires_grad_() for t in (inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"])]
     gy = torch.randn_like(inp["x"])

@@ -91,6 +91,10 @@ typedef struct {
   /* optional output gate (NULL: none): y <- y * silu(z), z laid out like y in the dtype of x -- the
      z-gate that Mamba2Block.forward applies right after the scan (mamformer/layers/mamba2.py:337-338) */
   const void* z;   int64_t z_stride_b, z_stride_l, z_stride_h;
+  /* optional (NULL: none), headdim 64: xsum (b, L, nheads, 2) fp32, the sums of x over each 32-channel half of a
+     head per token.  mh_ssd_chunk_scan_fwd writes it (the scan has x on chip); mh_ssd_h_states and
+     mh_ssd_h_states_bwd read it instead of x (h_states needs only these sums). */
+  float* xsum;
 } mh_ssd_args;
 
 /* Bytes of workspace mh_ssd_chunk_scan_fwd needs for these sizes. */

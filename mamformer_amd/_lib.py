@@ -45,6 +45,7 @@ class SsdArgs(ct.Structure):
         ("final_state", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
         ("z", _vp), ("z_stride_b", _i64), ("z_stride_l", _i64), ("z_stride_h", _i64),
+        ("xsum", _vp),
     ]
 
 

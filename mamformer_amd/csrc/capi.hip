@@ -110,6 +110,7 @@ int ssd_validate(const mh_ssd_args* a, int64_t* chunk_len_out) {
     if (a->z_stride_l * es * 64 >= ((int64_t)1 << 31))
       return fail(MH_ERR_STRIDE, "ssd: z token stride too large (64 tokens must span less than 2 GiB)");
   }
+  if (a->xsum && !aligned16(a->xsum)) return fail(MH_ERR_ALIGN, "ssd: xsum must be 16-byte aligned");
   if ((a->B_stride_l != 0 && a->B_stride_l < a->ngroups * a->dstate) ||
       (a->C_stride_l != 0 && a->C_stride_l < a->ngroups * a->dstate))
     return fail(MH_ERR_STRIDE, "ssd: B/C token stride smaller than ngroups*dstate ((g, n) must be contiguous; 0 broadcasts)");
@@ -274,6 +275,7 @@ void ssd_fill(const mh_ssd_args* a, int64_t cl, int64_t nchunks, mh::SsdParams& 
   p.final_state = a->final_state;
   p.z = a->z; p.z_sb = a->z_stride_b; p.z_sl = a->z_stride_l; p.z_sh = a->z_stride_h;
   p.nseg = (int)((a->seqlen + 63) / 64);
+  p.xsum = a->xsum;
 }
 
 int ssd_bwd_validate(const mh_ssd_bwd_args* a) {

@@ -54,7 +54,11 @@ struct SsdParams {
   void* entering;        // workspace (bf16 I/O): bf16 entering states, chunk_states order
   int nseg;              // ceil(seqlen / 64)
   int state_perm;        // workspace states in state_row_perm row order (two-pass prefill)
+  float* xsum;           // optional (b, L, H, 2): sums of x over each half of a head's 64 channels per token
+                         // (written by the prefill, read by h_states instead of x)
 };
+// xsum from x by a separate pass (prefill paths whose scan does not write it).
+hipError_t launch_ssd_xsum(const SsdParams& p, hipStream_t st);
 hipError_t launch_ssd(const SsdParams& p, hipStream_t st);
 // The two-pass bf16 prefill (ssd_lookback.hip): sizes it implements, and its launch.
 bool ssd_lb_supported(int dtype, int dstate);

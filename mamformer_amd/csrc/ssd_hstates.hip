@@ -66,7 +66,19 @@ __device__ void hs_prologue(const SsdParams& p, const HsParams& q, Smem& sm, int
     const int t = e / H, h = e % H;
     sm.c[t][h] = t < len ? dtb[(tok0 + t) * p.dt_sl + h] : 0.f;
   }
-  if (!FROM_WS) {
+  if (!FROM_WS && p.xsum) {
+    // xs[t][h] from the sums of x over each half of the head that the prefill wrote (x is not read)
+    const float* xsb = p.xsum + ((int64_t)b * p.seqlen + tok0) * H * 2;
+    for (int e = tid; e < HS_SEG * H; e += blockDim.x) {
+      const int t = e / H, h = e % H;
+      float xs = 0.f;
+      if (t < len) {
+        const f32x2 v = *reinterpret_cast<const f32x2*>(xsb + ((int64_t)t * H + h) * 2);
+        xs = v[0] + v[1];
+      }
+      sm.u[t][h] = xs;                 // xs for now; times dt below
+    }
+  } else if (!FROM_WS) {
     // xs[t][h] = sum_p x[t][h][p] (P = 64): one (token, head) row per thread pass, its 16 loads issued together
     const T* xb = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb;
     for (int e = tid; e < HS_SEG * H; e += blockDim.x) {

@@ -257,6 +257,7 @@ constexpr int lb_waves = HG * (2 / PH);
 // Per-wave constants of a workgroup's chunk (both passes).
 struct LbWave {
   int w, l, hw, ph0, c0, c1, last, nseg;
+  int b, h;           // batch and head of the wave
   float Ah, dtb;
   const bf16* xg;     // x of the wave's head, token 0, column 0
   const bf16* xg0;    // x of the workgroup's first head, token 0, column 0
@@ -288,6 +289,8 @@ __device__ __forceinline__ LbWave lb_wave(const SsdParams& p, int& k, int& b, in
   c.Bg = reinterpret_cast<const bf16*>(p.B) + (int64_t)b * p.B_sb + (int64_t)g * N;
   c.Cg = reinterpret_cast<const bf16*>(p.C) + (int64_t)b * p.C_sb + (int64_t)g * N;
   c.dtg = p.dt + (int64_t)b * p.dt_sb + h;
+  c.b = b;
+  c.h = h;
   return c;
 }
 
@@ -545,6 +548,17 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
   const float dtv = dec[(2 * dj + 1) * SEG + l];
   lds_barrier();                                           // tiles in LDS; the other stage is free
   if (si > 0 && si + 1 < nseg) lb_scan_fetch<N, HG, NW>(p, c, nxt, si + 1);
+  if (PH == 1 && p.xsum && pos + l < c.c1) {
+    // the sum of x over the wave's 32 channels of token pos + l (the input of h_states), from the x tile
+    float xs = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(xw + Sub64::off(l, 8 * q));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xs += (float)v[j];
+    }
+    p.xsum[(((int64_t)c.b * p.seqlen + pos + l) * p.nheads + c.h) * 2 + c.ph0] = xs;
+  }
   bf16x4 zq[PH][2][4];
   if constexpr (GATE) load_z_pieces<PH>(zg + (int64_t)pos * p.z_sl, p.z_sl, c.c1 - 1 - pos, zq);
   const bool dnext = dj == LB_DSEG - 1 && si + 1 < nseg;  // the next decay block is due

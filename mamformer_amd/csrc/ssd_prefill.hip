@@ -792,15 +792,41 @@ hipError_t launch_ssd(const SsdParams& p, hipStream_t st) {
                        p.final_state, n);
     return hipGetLastError();
   }
-  if (ssd_lb_supported(p.dtype, p.dstate)) return launch_ssd_lb(p, st);
+  if (ssd_lb_supported(p.dtype, p.dstate)) return launch_ssd_lb(p, st);    // its scan writes xsum itself
+  hipError_t e = hipErrorInvalidValue;
   if (p.dtype == DT_BF16) {
-    if (p.dstate == 128) return launch_ssd_n<bf16, bf16, 128>(p, st);
-    if (p.dstate == 64) return launch_ssd_n<bf16, bf16, 64>(p, st);
+    if (p.dstate == 128) e = launch_ssd_n<bf16, bf16, 128>(p, st);
+    if (p.dstate == 64) e = launch_ssd_n<bf16, bf16, 64>(p, st);
   } else {
-    if (p.dstate == 128) return launch_ssd_n<float, float, 128>(p, st);
-    if (p.dstate == 64) return launch_ssd_n<float, float, 64>(p, st);
+    if (p.dstate == 128) e = launch_ssd_n<float, float, 128>(p, st);
+    if (p.dstate == 64) e = launch_ssd_n<float, float, 64>(p, st);
   }
-  return hipErrorInvalidValue;
+  if (e == hipSuccess && p.xsum) e = launch_ssd_xsum(p, st);
+  return e;
+}
+
+// xsum[b][t][h][half] = sum of x[b][t][h][32 half .. 32 half + 31]: one (token, head, half) per thread.
+template <typename T>
+__global__ __launch_bounds__(256) void ssd_xsum_kernel(SsdParams p) {
+  const int64_t n = (int64_t)p.batch * p.seqlen * p.nheads * 2;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int half = (int)(i & 1), h = (int)((i >> 1) % p.nheads);
+  const int64_t bt = (i >> 1) / p.nheads, t = bt % p.seqlen, b = bt / p.seqlen;
+  const T* row = reinterpret_cast<const T*>(p.x) + b * p.x_sb + t * p.x_sl + (int64_t)h * p.x_sh + 32 * half;
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) s += to_f32(row[k]);
+  p.xsum[i] = s;
+}
+
+hipError_t launch_ssd_xsum(const SsdParams& p, hipStream_t st) {
+  const int64_t n = (int64_t)p.batch * p.seqlen * p.nheads * 2;
+  if (n == 0) return hipSuccess;
+  const unsigned nb = (unsigned)((n + 255) / 256);
+  if (p.dtype == DT_BF16) hipLaunchKernelGGL(ssd_xsum_kernel<bf16>, dim3(nb), dim3(256), 0, st, p);
+  else hipLaunchKernelGGL(ssd_xsum_kernel<float>, dim3(nb), dim3(256), 0, st, p);
+  return hipGetLastError();
 }
 
 }  // namespace mh

@@ -84,7 +84,7 @@ def _inner_contig(t: torch.Tensor, ndim_inner: int = 1) -> torch.Tensor:
 
 
 def _ssd_args(x4, dt, A, B4, C4, D, dt_bias, dt_softplus, dt_limit, initial_state, y4, final_state, chunk_size,
-              z4=None):
+              z4=None, xsum=None):
     b, L, H, P = x4.shape
     G, N = B4.shape[2], B4.shape[3]
     a = SsdArgs()
@@ -110,6 +110,7 @@ def _ssd_args(x4, dt, A, B4, C4, D, dt_bias, dt_softplus, dt_limit, initial_stat
     a.final_state = _ptr(final_state)
     if z4 is not None:
         a.z, a.z_stride_b, a.z_stride_l, a.z_stride_h = _ptr(z4), z4.stride(0), z4.stride(1), z4.stride(2)
+    a.xsum = _ptr(xsum)
     return a
 
 
@@ -237,21 +238,26 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
         else:
             z4 = z
         z4 = _inner_contig(z4)
+    # with h_states, the scan also writes the sums of x over each half of a head, which h_states then reads
+    # instead of x (headdim 64; the forward and the h_states backward take them)
+    xsum = torch.empty((b, L, H, 2), device=x.device, dtype=torch.float32) if (return_h_states and P == 64) else None
     if not _plan_only and torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (x4, dt32, A32, B4, C4, D32, bias32, h0, z4)):
-        cfg = (dt_softplus, dt_limit, chunk_size)
+        cfg = (dt_softplus, dt_limit, chunk_size, xsum)
         y4, fin = _SelectiveScanFn.apply(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg)
         if z4 is not None:
             y4 = _GateFn.apply(y4, z4)
         out = [y4.reshape(x.shape) if x.dim() == 3 else y4]
         if return_h_states:
-            out.append(_h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=True))
+            out.append(_h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=True,
+                                 xsum=xsum))
         if return_final_state:
             out.append(fin.reshape(b, H * P, N) if x.dim() == 3 else fin)
         return out[0] if len(out) == 1 else tuple(out)
     y4 = torch.empty((b, L, H, P), device=x.device, dtype=x.dtype)
     fin = torch.empty((b, H, P, N), device=x.device, dtype=torch.float32) if return_final_state else None
-    args = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, y4, fin, chunk_size, z4)
+    args = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, y4, fin, chunk_size, z4,
+                     None if _plan_only else xsum)
     nbytes = ct.c_size_t()
     _lib.call("mh_ssd_workspace_bytes", ct.byref(args), ct.byref(nbytes))
     ws = torch.empty(max(int(nbytes.value), 16), device=x.device, dtype=torch.uint8)
@@ -268,19 +274,21 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
     plan()
     out = [y]
     if return_h_states:
-        out.append(_h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size))
+        out.append(_h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, xsum=xsum))
     if return_final_state:
         out.append(fin_out)
     return out[0] if len(out) == 1 else tuple(out)
 
 
 def _scan_fwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg):
-    dt_softplus, dt_limit, chunk_size = cfg
+    dt_softplus, dt_limit, chunk_size = cfg[:3]
+    xsum = cfg[3] if len(cfg) > 3 else None
     b, L, H, P = x4.shape
     N = B4.shape[3]
     y4 = torch.empty((b, L, H, P), device=x4.device, dtype=x4.dtype)
     fin = torch.empty((b, H, P, N), device=x4.device, dtype=torch.float32)
-    args = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, y4, fin, chunk_size)
+    args = _ssd_args(x4, dt32, A32, B4, C4, D32, bias32, dt_softplus, dt_limit, h0, y4, fin, chunk_size, None,
+                     xsum)
     nbytes = ct.c_size_t()
     _lib.call("mh_ssd_workspace_bytes", ct.byref(args), ct.byref(nbytes))
     ws = torch.empty(max(int(nbytes.value), 16), device=x4.device, dtype=torch.uint8)
@@ -290,7 +298,7 @@ def _scan_fwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg):
 
 
 def _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4, dfin, need_dh0, plan_only=False):
-    dt_softplus, dt_limit, _ = cfg
+    dt_softplus, dt_limit = cfg[0], cfg[1]
     b, L, H, P = x4.shape
     G, N = B4.shape[2], B4.shape[3]
     dev = x4.device
@@ -447,17 +455,17 @@ def selective_scan_bwd(dy, x, dt, A, B, C, D=None, *, d_final_state=None, initia
     return out
 
 
-def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=False):
+def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=False, xsum=None):
     """h_states[b, t, n] = mean over (h, p) of the state h_t[h, p, n] (mamba2.py:114-116).
 
     Computed by ``mh_ssd_h_states`` (the channel sums of the state follow a recurrence with one scalar input per
     (token, head), sum_p x); with ``grad`` through an autograd node whose backward differentiates the equivalent
     swapped prefill below.  More than 128 heads take the swapped prefill in the forward as well.
     """
-    cfg = (dt_softplus, dt_limit, chunk_size)
+    cfg = (dt_softplus, dt_limit, chunk_size, xsum)
     if grad:
         return _HStatesFn.apply(x4, dt32, A32, B4, h0, bias32, cfg)
-    return _h_states_fwd(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit)
+    return _h_states_fwd(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum)
 
 
 _HS_MAXH = 128    # heads the h_states kernels hold at once (forward and backward)
@@ -490,12 +498,13 @@ def _h_block_args(x4, dt32, A32, B4, h0, bias32, h0_, h1_):
             None if bias32 is None else bias32[h0_:h1_].contiguous(), g0, g1)
 
 
-def _h_states_fwd(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
-    """h_states by ``mh_ssd_h_states``; more than 128 heads run as head blocks whose fp32 h_states are combined
-    with weights H_block / H (the mean over (h, p) is linear in the heads)."""
+def _h_states_fwd(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum=None):
+    """h_states by ``mh_ssd_h_states`` (reading the prefill's sums of x, ``xsum``, when given); more than 128 heads
+    run as head blocks whose fp32 h_states are combined with weights H_block / H (the mean over (h, p) is linear
+    in the heads)."""
     H = x4.shape[2]
     if H <= _HS_MAXH:
-        return _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit)
+        return _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum)
     x32, B32 = x4.to(torch.float32), B4.to(torch.float32)
     acc = None
     for h0_, h1_ in _head_blocks(H, B4.shape[2]):
@@ -505,11 +514,11 @@ def _h_states_fwd(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
     return acc.to(x4.dtype)
 
 
-def _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
+def _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum=None):
     b, L, H, P = x4.shape
     N = B4.shape[3]
     hs = torch.empty((b, L, N), device=x4.device, dtype=x4.dtype)
-    args = _ssd_args(x4, dt32, A32, B4, B4, None, bias32, dt_softplus, dt_limit, h0, x4, None, 64)
+    args = _ssd_args(x4, dt32, A32, B4, B4, None, bias32, dt_softplus, dt_limit, h0, x4, None, 64, None, xsum)
     nbytes = ct.c_size_t()
     _lib.call("mh_ssd_h_states_workspace_bytes", ct.byref(args), ct.byref(nbytes))
     ws = torch.empty(max(int(nbytes.value), 16), device=x4.device, dtype=torch.uint8)
@@ -518,7 +527,7 @@ def _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
     return hs
 
 
-def _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
+def _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum=None):
     """Gradients of <ghs, h_states> by ``mh_ssd_h_states_bwd``: (dx, ddt, dA, dB, d h0, d dt_bias)."""
     b, L, H, P = x4.shape
     G, N = B4.shape[2], B4.shape[3]
@@ -531,7 +540,7 @@ def _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_lim
     dh0 = None if h0 is None else torch.empty((b, H, P, N), device=dev, dtype=torch.float32)
     dbias = None if bias32 is None else torch.empty((H,), device=dev, dtype=torch.float32)
     a = _lib.SsdHsBwdArgs()
-    a.fwd = _ssd_args(x4, dt32, A32, B4, B4, None, bias32, dt_softplus, dt_limit, h0, x4, None, 64)
+    a.fwd = _ssd_args(x4, dt32, A32, B4, B4, None, bias32, dt_softplus, dt_limit, h0, x4, None, 64, None, xsum)
     a.dhs, a.dx, a.ddt, a.dA, a.dB = _ptr(ghs), _ptr(dx), _ptr(ddt), _ptr(dA), _ptr(dB)
     a.d_dt_bias, a.d_initial_state = _ptr(dbias), _ptr(dh0)
     nbytes = ct.c_size_t()
@@ -542,7 +551,7 @@ def _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_lim
     return dx, ddt, dA, dB, dh0, dbias
 
 
-def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit):
+def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum=None):
     """``mh_ssd_h_states_bwd`` for any head count and dstate: the state columns separate (column n of h_states
     depends on B[..., n] alone; dx, ddt, dA and d dt_bias are sums over columns, dB and d h0 per column), so
     dstate > 128 runs as column pieces of at most 128; the heads enter h_states as a sum, so more than 128 heads
@@ -556,7 +565,7 @@ def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_lim
             n1 = min(N, n0 + _HS_BWD_MAXN)
             outs.append(_h_states_bwd_blocks(ghs[..., n0:n1], x4, dt32, A32, B4[..., n0:n1].contiguous(),
                                              None if h0 is None else h0[..., n0:n1].contiguous(), bias32,
-                                             dt_softplus, dt_limit))
+                                             dt_softplus, dt_limit, xsum))
         dx = sum(o[0].to(torch.float32) for o in outs).to(x4.dtype)
         ddt = sum(o[1] for o in outs)
         dA = sum(o[2] for o in outs)
@@ -565,7 +574,7 @@ def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_lim
         dbias = None if bias32 is None else sum(o[5] for o in outs)
         return dx, ddt, dA, dB, dh0, dbias
     if H <= _HS_MAXH:
-        return _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit)
+        return _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum)
     dev = x4.device
     dx = torch.empty((b, L, H, P), device=dev, dtype=x4.dtype)
     ddt = torch.empty((b, L, H), device=dev, dtype=torch.float32)
@@ -597,21 +606,21 @@ class _HStatesFn(torch.autograd.Function):
     def forward(ctx, x4, dt32, A32, B4, h0, bias32, cfg):
         ctx.save_for_backward(x4, dt32, A32, B4, h0, bias32)
         ctx.cfg = cfg
-        return _h_states_fwd(x4, dt32, A32, B4, h0, bias32, cfg[0], cfg[1])
+        return _h_states_fwd(x4, dt32, A32, B4, h0, bias32, cfg[0], cfg[1], cfg[3])
 
     @staticmethod
     def backward(ctx, ghs):
         saved = ctx.saved_tensors
         x4 = saved[0]
         if x4.shape[3] == 64:
-            dx, ddt, dA, dB, dh0, dbias = _h_states_bwd_blocks(ghs, *saved, ctx.cfg[0], ctx.cfg[1])
+            dx, ddt, dA, dB, dh0, dbias = _h_states_bwd_blocks(ghs, *saved, ctx.cfg[0], ctx.cfg[1], ctx.cfg[3])
             need = ctx.needs_input_grad
             return (dx if need[0] else None, ddt if need[1] else None, dA if need[2] else None,
                     dB if need[3] else None, dh0 if need[4] else None, dbias if need[5] else None, None)
         leaves = [None if t is None else t.detach().requires_grad_(bool(need))
                   for t, need in zip(saved, ctx.needs_input_grad[:6])]
         with torch.enable_grad():
-            hs = _h_states_swap(*leaves, *ctx.cfg, grad=True)
+            hs = _h_states_swap(*leaves, *ctx.cfg[:3], grad=True)
         want = [t for t in leaves if t is not None and t.requires_grad]
         got = torch.autograd.grad(hs, want, ghs, allow_unused=True) if want else ()
         grads, k = [], 0
