@@ -760,7 +760,8 @@ int mh_ssd_h_states_workspace_bytes(const mh_ssd_args* a, size_t* bytes) {
   if (!bytes) return fail(MH_ERR_NULL, "ssd_h_states: bytes output is NULL");
   int rc = hs_validate(a);
   if (rc) return rc;
-  *bytes = mh::ssd_hs_workspace_bytes((int)a->batch, (int)a->seqlen, (int)a->nheads, (int)a->dstate, false);
+  *bytes = mh::ssd_hs_workspace_bytes((int)a->batch, (int)a->seqlen, (int)a->nheads, (int)a->dstate,
+                                      (int)a->ngroups, false);
   return MH_OK;
 }
 
@@ -769,7 +770,8 @@ int mh_ssd_h_states(const mh_ssd_args* a, void* h_states, void* stream) {
   if (rc) return rc;
   if (a->seqlen > 0 && !h_states) return fail(MH_ERR_NULL, "ssd_h_states: h_states output is NULL");
   if (!aligned16(h_states)) return fail(MH_ERR_ALIGN, "ssd_h_states: h_states must be 16-byte aligned");
-  const size_t need = mh::ssd_hs_workspace_bytes((int)a->batch, (int)a->seqlen, (int)a->nheads, (int)a->dstate, false);
+  const size_t need = mh::ssd_hs_workspace_bytes((int)a->batch, (int)a->seqlen, (int)a->nheads, (int)a->dstate,
+                                                 (int)a->ngroups, false);
   if (a->seqlen > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
     return fail(MH_ERR_WORKSPACE, "ssd_h_states: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
                 a->workspace_bytes);
@@ -937,7 +939,8 @@ int mh_ssd_h_states_bwd_workspace_bytes(const mh_ssd_hs_bwd_args* a, size_t* byt
   int rc = hs_bwd_validate(a);
   if (rc) return rc;
   const mh_ssd_args* f = &a->fwd;
-  *bytes = mh::ssd_hs_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate, true);
+  *bytes = mh::ssd_hs_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate,
+                                      (int)f->ngroups, true);
   return MH_OK;
 }
 
@@ -945,7 +948,8 @@ int mh_ssd_h_states_bwd(const mh_ssd_hs_bwd_args* a, void* stream) {
   int rc = hs_bwd_validate(a);
   if (rc) return rc;
   const mh_ssd_args* f = &a->fwd;
-  const size_t need = mh::ssd_hs_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate, true);
+  const size_t need = mh::ssd_hs_workspace_bytes((int)f->batch, (int)f->seqlen, (int)f->nheads, (int)f->dstate,
+                                                 (int)f->ngroups, true);
   if (f->seqlen > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
     return fail(MH_ERR_WORKSPACE, "ssd_h_states_bwd: workspace of %zu bytes (16-byte aligned) required, got %zu",
                 need, a->workspace_bytes);

@@ -100,7 +100,8 @@ struct HsParams {
   void* hs;                  // (b, L, N) in the I/O dtype
   float* z;                  // workspace: (b, nseg, H, N) per-segment state sums (local, then entering)
   float* dec;                // workspace: (b, nseg, H) segment decays
-  float* u;                  // workspace: (b, L, H) sum_p x
+  float* u;                  // workspace: (b, L, H) sum_p x (backward); e^{c} per (token, head) (forward)
+  float* w;                  // workspace, forward: (b, nseg, G, 32, 32) the segments' in-segment weights W_g[t][s]
   // backward
   const void* dhs;           // (b, L, N) gradient of h_states, I/O dtype
   void* dx;                  // (b, L, H, P) contiguous, I/O dtype
@@ -113,7 +114,7 @@ struct HsParams {
 };
 bool ssd_hs_supported(int nheads, int dstate);
 bool ssd_hs_bwd_supported(int nheads, int dstate);
-size_t ssd_hs_workspace_bytes(int batch, int seqlen, int nheads, int dstate, bool backward);
+size_t ssd_hs_workspace_bytes(int batch, int seqlen, int nheads, int dstate, int ngroups, bool backward);
 // Lays out q's workspace parts and sets p.nseg to this pass's segment count.
 void ssd_hs_workspace_layout(SsdParams& p, HsParams& q, void* workspace, bool backward);
 hipError_t launch_ssd_hs(const SsdParams& p, const HsParams& q, hipStream_t st);

@@ -3,19 +3,17 @@
 //     Z_t[h, n] = sum_p h_t[h, p, n] = e^{A_h dt_t,h} Z_{t-1}[h, n] + dt_t,h xs_t[h] B_t[g(h), n],
 //     xs_t[h] = sum_p x_t[h, p],        hs_t[n] = sum_h Z_t[h, n] / (H P),
 // so h_states needs one scalar input per (token, head) instead of P of them.  Three passes over 32-token
-// segments, all in fp32:
-//   ssd_hs_local_kernel  (segment, batch): dt processed as the prefill does it, c = in-segment inclusive cumsum
-//                        of A dt, xs per (token, head) into the workspace, u = dt xs, and the segment's own
-//                        contribution Zloc[h][n] = sum_s e^{c_end - c_s} u_s[h] B_s[g(h)][n] with the decay
-//                        e^{c_end} of each head.
+// segments, all in fp32, the state columns in blocks of HS_NB:
+//   ssd_hs_local_kernel  (segment, batch, column block): dt processed as the prefill does it, c = in-segment
+//                        inclusive cumsum of A dt, u = dt xs (xs from the prefill's per-head sums of x, or from x),
+//                        the segment's own contribution Zloc[h][n] = sum_s e^{c_end - c_s} u_s[h] B_s[g(h)][n] for
+//                        the block's columns (fp32 MFMAs), and its share of the segment's factors
+//                        Ei[h][t] = e^{c_t,h} and W_g[t][s] = sum_{h in g} e^{c_t,h - c_s,h} u_s[h] (s <= t).
 //   ssd_hs_carry_kernel  (batch, head, n): Zin of every segment, Zin_0 = sum_p h0[h, p, n] (or 0),
-//                        Zin_{k+1} = e^{c_end,k} Zin_k + Zloc_k (in place over Zloc).
-//   ssd_hs_out_kernel    (segment, batch): hs_t[n] = (sum_h e^{c_t,h} Zin[h][n]
-//                        + sum_g sum_{s <= t} W_g[t][s] B_s[g][n]) / (H P),  W_g[t][s] = sum_{h in g} e^{c_t,h - c_s,h} u_s[h],
-//                        W formed as a product over heads of E[t][h] = e^{c_t,h - m_h} and F[s][h] = e^{m_h - c_s,h} u_s[h]
-//                        (m_h the midpoint of the head's range in the segment); a head whose range exceeds PR
-//                        adds its terms with one exponential each instead, so no factor exceeds e^{PR / 2}.
-// The other exponents are <= 0 (A <= 0, dt >= 0): no factor can overflow whatever the decay.
+//                        Zin_{k+1} = e^{c_end,k} Zin_k + Zloc_k (in place over Zloc), a two-level scan.
+//   ssd_hs_out_kernel    (segment, batch, column block), one wave of fp32 MFMAs:
+//                        hs_t[n] = (sum_h Ei[h][t] Zin[h][n] + sum_g sum_{s <= t} W_g[t][s] B_s[g][n]) / (H P).
+// Every exponent is <= 0 (A <= 0, dt >= 0, c falls along the segment): no factor can overflow whatever the decay.
 #include "common.h"
 #include "launch.h"
 #include "ssd_shared.h"
@@ -27,10 +25,11 @@ namespace {
 constexpr int HS_SEG = 32;       // tokens per segment
 constexpr int HS_MAXH = 128;     // heads held in LDS
 constexpr int HS_MAXN = 256;
-constexpr int HS_ZH = 32;        // heads of entering sums staged in LDS at a time
+constexpr int HS_NB = 32;        // state columns per forward workgroup
 constexpr int HS_HP = HS_MAXH + 1;   // row pitch of the per-(token, head) arrays: a column (one head, 32 tokens)
                                      // then spans 32 banks
-constexpr float PR = 80.f;       // largest in-segment range of c factorised as E F
+constexpr int HS_LP = HS_MAXH + 4;   // the same in the forward local pass: 16-byte reads of 4 heads, and 16
+                                     // consecutive rows read together fall on distinct banks
 
 __device__ __forceinline__ float hs_dt(const SsdParams& p, float d, int h) {
   if (p.dt_bias) d += p.dt_bias[h];
@@ -39,49 +38,65 @@ __device__ __forceinline__ float hs_dt(const SsdParams& p, float d, int h) {
   return d;
 }
 
-struct HsSmem {
-  float c[HS_SEG][HS_HP];        // raw dt, then the in-segment inclusive cumsum of A dt (flat past the end)
-  float u[HS_SEG][HS_HP];        // dt xs (0 past the end); local pass: e^{c_end - c_s} dt xs
-  float E[HS_SEG][HS_HP];        // out pass: e^{c_t - m}
-  float F[HS_SEG][HS_HP];        // out pass: e^{m - c_s} u_s
-  float Ei[HS_SEG][HS_HP];       // out pass: e^{c_t}
-  float Bt[HS_SEG][HS_MAXN];     // B of one group
-  float Zs[HS_ZH][HS_MAXN];      // out pass: entering state sums of HS_ZH heads
-  float W[HS_SEG][HS_SEG + 4];   // W_g[t][s]
-  float cend[HS_MAXH], mid[HS_MAXH];
-  int wide[HS_MAXH];
-  int anywide;
-};
-
-// dt, c and u = dt xs of segment si into LDS, xs = sum_p x computed from x (local pass, and written to the
-// workspace) or read from it (out pass).
-template <typename T, bool FROM_WS, typename Smem>
-__device__ void hs_prologue(const SsdParams& p, const HsParams& q, Smem& sm, int b, int si, int len) {
-  const int H = p.nheads, tid = threadIdx.x;
+// dt, c and u = dt xs of segment si into LDS (sm.c, sm.u, sm.cend).  xs = sum_p x is taken from the prefill's
+// per-half sums (p.xsum) when given, else summed from x; xs_out (or null) receives xs per (token, head).  dt is
+// processed element-parallel (bias, softplus, clamp) as it arrives; only the cumsum of A dt runs per head.
+// The element loads are unconditional at clamped (valid) addresses, so that each thread's KB loads of a pass are
+// in flight together: an element past the end of the segment is zeroed by a factor 0 (its dt finite), and a thread
+// past the last element repeats the last one (the same value written twice).
+template <bool XS, typename Smem>
+__device__ void hs_prologue_elems(const SsdParams& p, Smem& sm, int b, int si, int len, float* uws) {
+  const int H = p.nheads, tid = threadIdx.x, tot = HS_SEG * H, nt = blockDim.x;
   const int64_t tok0 = (int64_t)si * HS_SEG;
-  float* uws = q.u + ((int64_t)b * p.seqlen + tok0) * H;
-  // raw dt of the segment into LDS (all loads in flight together; the per-head cumsum below reads LDS)
   const float* dtb = p.dt + (int64_t)b * p.dt_sb;
-  for (int e = tid; e < HS_SEG * H; e += blockDim.x) {
-    const int t = e / H, h = e % H;
-    sm.c[t][h] = t < len ? dtb[(tok0 + t) * p.dt_sl + h] : 0.f;
-  }
-  if (!FROM_WS && p.xsum) {
-    // xs[t][h] from the sums of x over each half of the head that the prefill wrote (x is not read)
-    const float* xsb = p.xsum + ((int64_t)b * p.seqlen + tok0) * H * 2;
-    for (int e = tid; e < HS_SEG * H; e += blockDim.x) {
-      const int t = e / H, h = e % H;
-      float xs = 0.f;
-      if (t < len) {
-        const f32x2 v = *reinterpret_cast<const f32x2*>(xsb + ((int64_t)t * H + h) * 2);
-        xs = v[0] + v[1];
-      }
-      sm.u[t][h] = xs;                 // xs for now; times dt below
+  const float* xsb = XS ? p.xsum + ((int64_t)b * p.seqlen + tok0) * H * 2 : nullptr;
+  const float* bias = p.dt_bias ? p.dt_bias : p.A;       // any valid per-head array when there is no bias
+  const float bmul = p.dt_bias ? 1.f : 0.f;
+  constexpr int KB = 8;
+  for (int base = 0; base < tot; base += KB * nt) {
+    float d[KB], av[KB], bv[KB];
+    f32x2 xv[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      const int e = min(base + tid + k * nt, tot - 1), t = e / H, h = e % H, tc = min(t, len - 1);
+      d[k] = dtb[(tok0 + tc) * p.dt_sl + h];
+      av[k] = p.A[h];
+      bv[k] = bias[h];
+      if constexpr (XS) xv[k] = *reinterpret_cast<const f32x2*>(xsb + ((int64_t)tc * H + h) * 2);
     }
-  } else if (!FROM_WS) {
+    __builtin_amdgcn_sched_barrier(0);  // every load of the pass issued before the first use
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      const int e = min(base + tid + k * nt, tot - 1), t = e / H, h = e % H;
+      float x = d[k] + bv[k] * bmul;
+      if (p.dt_softplus) x = softplus_f(x);
+      if (p.has_dt_limit) x = fminf(fmaxf(x, p.dt_min), p.dt_max);
+      const float dd = x * (t < len ? 1.f : 0.f);          // 0 past the end: c flat, u = 0
+      sm.c[t][h] = av[k] * dd;                               // the cumsum below makes it c
+      if constexpr (XS) {
+        const float xs = xv[k][0] + xv[k][1];
+        if (uws && t < len) uws[(int64_t)t * H + h] = xs;
+        sm.u[t][h] = dd * xs;
+      } else {
+        sm.u[t][h] = dd;                                     // times xs below
+      }
+    }
+  }
+}
+
+template <typename T, typename Smem>
+__device__ void hs_prologue(const SsdParams& p, Smem& sm, int b, int si, int len, float* xs_out) {
+  const int H = p.nheads, tid = threadIdx.x, tot = HS_SEG * H, nt = blockDim.x;
+  const int64_t tok0 = (int64_t)si * HS_SEG;
+  float* uws = xs_out ? xs_out + ((int64_t)b * p.seqlen + tok0) * H : nullptr;
+  const bool xsb = p.xsum != nullptr;
+  if (xsb) hs_prologue_elems<true>(p, sm, b, si, len, uws);
+  else hs_prologue_elems<false>(p, sm, b, si, len, uws);
+  if (!xsb) {
+    __syncthreads();                   // the element pass's repeated writes of the last element are done
     // xs[t][h] = sum_p x[t][h][p] (P = 64): one (token, head) row per thread pass, its 16 loads issued together
     const T* xb = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb;
-    for (int e = tid; e < HS_SEG * H; e += blockDim.x) {
+    for (int e = tid; e < tot; e += nt) {
       const int t = e / H, h = e % H;
       float xs = 0.f;
       if (t < len) {
@@ -99,246 +114,249 @@ __device__ void hs_prologue(const SsdParams& p, const HsParams& q, Smem& sm, int
         }
 #pragma unroll
         for (int k = 0; k < 16; ++k) xs += part[k];
+        if (uws) uws[(int64_t)t * H + h] = xs;
       }
-      sm.u[t][h] = xs;                 // xs for now; times dt below
-    }
-  } else {
-    for (int e = tid; e < HS_SEG * H; e += blockDim.x) {
-      const int t = e / H, h = e % H;
-      sm.u[t][h] = t < len ? uws[(int64_t)t * H + h] : 0.f;
+      sm.u[t][h] *= xs;
     }
   }
   __syncthreads();
-  // per head: processed dt, cumsum c, u = dt xs (local pass)
-  for (int h = tid; h < H; h += blockDim.x) {
-    const float A = p.A[h];
+  // per head: the inclusive cumsum of A dt over the segment
+  for (int h = tid; h < H; h += nt) {
+    float a[HS_SEG];
+#pragma unroll
+    for (int t = 0; t < HS_SEG; ++t) a[t] = sm.c[t][h];
     float c = 0.f;
+#pragma unroll
     for (int t = 0; t < HS_SEG; ++t) {
-      if (t < len) {
-        const float d = hs_dt(p, sm.c[t][h], h);
-        c += A * d;
-        const float xs = sm.u[t][h];
-        if (!FROM_WS) uws[(int64_t)t * H + h] = xs;
-        sm.u[t][h] = d * xs;
-      } else {
-        sm.u[t][h] = 0.f;
-      }
+      c += a[t];
       sm.c[t][h] = c;
     }
     sm.cend[h] = c;
-    sm.mid[h] = 0.5f * (sm.c[0][h] + c);
-    sm.wide[h] = sm.c[0][h] - c > PR;
   }
 }
 
-// B of group g for the segment's tokens (0 past the end) into LDS as fp32.
-template <typename T>
-__device__ void hs_load_b(const SsdParams& p, HsSmem& sm, int b, int si, int len, int g) {
-  const int N = p.dstate, tid = threadIdx.x;
-  const T* Bb = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)g * N;
-  const int64_t tok0 = (int64_t)si * HS_SEG;
-  for (int e = tid; e < HS_SEG * N / 4; e += blockDim.x) {
-    const int t = e / (N / 4), n = 4 * (e % (N / 4));
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (t < len) {
-      const T* src = Bb + (tok0 + t) * p.B_sl + n;
-      if constexpr (sizeof(T) == 2) {
-        const bf16x4 w = *reinterpret_cast<const bf16x4*>(src);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = (float)w[j];
-      } else {
-        v = *reinterpret_cast<const f32x4*>(src);
-      }
-    }
-    *reinterpret_cast<f32x4*>(&sm.Bt[t][n]) = v;
-  }
-}
+struct __align__(16) HsLocSmem {
+  float c[HS_SEG][HS_LP];        // raw dt, then the in-segment inclusive cumsum of A dt
+  float u[HS_SEG][HS_LP];        // dt xs
+  float cend[HS_MAXH];
+};
 
-// 8 consecutive columns of an LDS row
-__device__ __forceinline__ void ld8f(const float* p, float (&v)[8]) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[4 + j] = b[j]; }
-}
-
+// Workgroup (segment, batch, column block zb of nblk): the prologue, then
+//  - its share of the output pass's factors: W_g[t][s] for s = zb, zb + nblk, ... and all t, stored s-major (row s
+//    of WT holds W_g[.][s] over the 32 tokens, 0 for t < s), and Ei[h][t] = e^{c_t,h} for h = zb, zb + nblk, ...
+//    (0 past the end);
+//  - Zloc[h][n] = sum_s e^{c_end - c_s} u_s[h] B_s[n] for its HS_NB columns, as fp32 MFMAs (32 heads x 32 columns a
+//    tile, k over pairs of tokens, B read from global memory);
+//  - the segment's decays (zb = 0).
 template <typename T>
 __global__ __launch_bounds__(256) void ssd_hs_local_kernel(SsdParams p, HsParams q) {
-  __shared__ HsSmem sm;
-  const int si = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int H = p.nheads, N = p.dstate, hpg = H / p.ngroups, N8 = N / 8;
+  __shared__ HsLocSmem sm;
+  const int si = blockIdx.x, b = blockIdx.y, zb = blockIdx.z, nblk = gridDim.z, n0 = HS_NB * zb;
+  const int tid = threadIdx.x, H = p.nheads, N = p.dstate, G = p.ngroups, hpg = H / G;
   const int len = min(HS_SEG, p.seqlen - si * HS_SEG);
-  hs_prologue<T, false>(p, q, sm, b, si, len);
-  __syncthreads();
-  // w[s][h] = e^{c_end - c_s} u_s[h] (<= u: the exponent is <= 0), in place over u
-  for (int e = tid; e < HS_SEG * H; e += blockDim.x) {
-    const int s = e / H, h = e % H;
-    sm.u[s][h] *= __expf(sm.cend[h] - sm.c[s][h]);
-  }
-  float* zl = q.z + (((int64_t)b * p.nseg + si) * H) * N;
-  for (int g = 0; g < p.ngroups; ++g) {
-    __syncthreads();                   // w complete; the previous group's B no longer read
-    hs_load_b<T>(p, sm, b, si, len, g);
-    __syncthreads();
-    // Zloc[h][n0 .. n0 + 8) = sum_s w[s][h] B[s][n]
-    for (int e = tid; e < hpg * N8; e += blockDim.x) {
-      const int h = g * hpg + e / N8, n0 = 8 * (e % N8);
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int s = 0; s < HS_SEG; ++s) {
-        float bv[8];
-        ld8f(&sm.Bt[s][n0], bv);
-        const float w = sm.u[s][h];
+  const int64_t tok0 = (int64_t)si * HS_SEG;
+  const int l = lane_id(), i = l & 31, hf = l >> 5, tiles = (hpg + 31) / 32, nw = blockDim.x / 64;
+  const bool col = n0 + i < N;
+  // B operands of this wave's Zloc tile (k = token pairs), loaded before the prologue so that they arrive meanwhile;
+  // unmasked at clamped addresses: a token past the end meets u = 0, a lane past the last column feeds an output
+  // column that is not stored
+  T bv[HS_SEG / 2];                    // converted at their use, so that nothing waits for them before
+  auto load_b = [&](int unit) {
+    const T* Bg = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)(unit / tiles) * N + n0 +
+                  min(i, N - 1 - n0);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] += w * bv[j];
+    for (int m = 0; m < HS_SEG / 2; ++m) bv[m] = Bg[(tok0 + min(2 * m + hf, len - 1)) * p.B_sl];
+  };
+  int unit = wave_id();
+  if (unit < G * tiles) load_b(unit);
+  hs_prologue<T>(p, sm, b, si, len, nullptr);
+  __syncthreads();
+  {
+    const int nrow = (HS_SEG - zb + nblk - 1) / nblk;
+    float* wt = q.w + ((int64_t)b * p.nseg + si) * G * (HS_SEG * HS_SEG);
+    for (int e = tid; e < G * nrow * HS_SEG; e += blockDim.x) {
+      const int t = e % HS_SEG, s = zb + nblk * ((e / HS_SEG) % nrow), g = e / (HS_SEG * nrow);
+      float w = 0.f;
+      if (s <= t) {                    // every exponent c_t - c_s <= 0
+        if (hpg % 4 == 0) {
+          for (int h = g * hpg; h < (g + 1) * hpg; h += 4) {
+            const f32x4 ct = *reinterpret_cast<const f32x4*>(&sm.c[t][h]);
+            const f32x4 cs = *reinterpret_cast<const f32x4*>(&sm.c[s][h]);
+            const f32x4 us = *reinterpret_cast<const f32x4*>(&sm.u[s][h]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w += __expf(ct[j] - cs[j]) * us[j];
+          }
+        } else {
+          for (int h = g * hpg; h < (g + 1) * hpg; ++h) w += __expf(sm.c[t][h] - sm.c[s][h]) * sm.u[s][h];
+        }
       }
-      float* o = zl + (int64_t)h * N + n0;
-      *reinterpret_cast<f32x4*>(o) = f32x4{acc[0], acc[1], acc[2], acc[3]};
-      *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+      wt[((int64_t)g * HS_SEG + s) * HS_SEG + t] = w;
+    }
+    float* eit = q.u + ((int64_t)b * p.nseg + si) * H * HS_SEG;
+    const int nhr = (H - zb + nblk - 1) / nblk;
+    for (int e = tid; e < nhr * HS_SEG; e += blockDim.x) {
+      const int t = e % HS_SEG, h = zb + nblk * (e / HS_SEG);
+      eit[(int64_t)h * HS_SEG + t] = t < len ? __expf(sm.c[t][h]) : 0.f;
     }
   }
-  if (tid < H) q.dec[((int64_t)b * p.nseg + si) * H + tid] = __expf(sm.cend[tid]);
+  // Zloc: tiles of (group, 32 heads), one per wave at a time
+  for (; unit < G * tiles; unit += nw) {
+    const int g = unit / tiles, hl = (unit % tiles) * 32;
+    const int h = g * hpg + min(hl + i, hpg - 1);            // A row (clamped; rows past hpg are not stored)
+    const float ce = sm.cend[h];
+    float a[HS_SEG / 2];
+#pragma unroll
+    for (int m = 0; m < HS_SEG / 2; ++m) {
+      const int sk = 2 * m + hf;
+      a[m] = sm.u[sk][h] * __expf(ce - sm.c[sk][h]);           // u is 0 past the end
+    }
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int m = 0; m < HS_SEG / 2; ++m)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[m], to_f32(bv[m]), acc, 0, 0, 0);
+    if (unit + nw < G * tiles) load_b(unit + nw);
+    if (col) {
+      float* zl = q.z + (((int64_t)b * p.nseg + si) * H + g * hpg + hl) * N + n0 + i;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int hr = acc_row(hf, r);
+        if (hl + hr < hpg) zl[(int64_t)hr * N] = acc[r];
+      }
+    }
+  }
+  if (zb == 0 && tid < H) q.dec[((int64_t)b * p.nseg + si) * H + tid] = __expf(sm.cend[tid]);
 }
 
+// The carry over segments as a two-level scan.  The segments of a chain (b, h, n) are cut into NP parts of
+// consecutive segments; within a wave, lane j * CW + i holds part j of the wave's chain i (CW = 64 / NP chains per
+// wave, consecutive in n, so a load of one part covers CW consecutive floats).  Each lane reduces its part to
+// (decay product, sum entering from zero), forms the sum entering its part from the parts before it, read across
+// the wave, starting at sum_p h0 (summed by all parts, rows p = j, j + NP, ...), then walks its part again writing
+// every segment's entering sum in place over Zloc.  A part of at most KB segments stays in registers between the
+// two walks; a longer one is loaded KB segments at a time, twice.
+template <int NP>
 __global__ __launch_bounds__(256) void ssd_hs_carry_kernel(SsdParams p, HsParams q) {
-  const int H = p.nheads, N = p.dstate, P = p.headdim;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)p.batch * H * N) return;
-  const int n = (int)(i % N), h = (int)((i / N) % H), b = (int)(i / ((int64_t)N * H));
-  float Z = 0.f;
-  if (p.init_state) {
-    const float* s0 = p.init_state + (((int64_t)b * H + h) * P) * N + n;
-    for (int k = 0; k < P; ++k) Z += s0[(int64_t)k * N];
-  }
+  constexpr int CW = 64 / NP, KB = 16;
+  const int H = p.nheads, N = p.dstate, P = p.headdim, l = lane_id();
+  const int part = l / CW, ci = l % CW;
+  const int64_t chain = ((int64_t)blockIdx.x * 4 + wave_id()) * CW + ci;
+  const bool on = chain < (int64_t)p.batch * H * N;
+  const int64_t ch = on ? chain : 0;
+  const int n = (int)(ch % N), h = (int)((ch / N) % H), b = (int)(ch / ((int64_t)N * H));
+  const int pl = (p.nseg + NP - 1) / NP, k0 = min(p.nseg, part * pl), k1 = min(p.nseg, k0 + pl);
   float* zp = q.z + ((int64_t)b * p.nseg * H + h) * N + n;
   const float* dp = q.dec + (int64_t)b * p.nseg * H + h;
   const int64_t zs = (int64_t)H * N;
-  // 16 segments' loads issued together, the next 16's while the chain runs through these (two buffers)
-  auto ld = [&](int s0, float (&zl)[16], float (&d)[16]) {
+  float d[KB], z[KB];
+  auto load = [&](int k) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const bool in = s0 + k < p.nseg;
-      zl[k] = in ? zp[(s0 + k) * zs] : 0.f;
-      d[k] = in ? dp[(int64_t)(s0 + k) * H] : 1.f;
+    for (int j = 0; j < KB; ++j) {
+      const bool in = on && k + j < k1;
+      d[j] = in ? dp[(int64_t)(k + j) * H] : 1.f;
+      z[j] = in ? zp[(int64_t)(k + j) * zs] : 0.f;
     }
   };
-  auto step = [&](int s0, const float (&zl)[16], const float (&d)[16]) {
+  float Z0 = 0.f;
+  if (on && p.init_state) {
+    const float* s0 = p.init_state + (((int64_t)b * H + h) * P) * N + n;
+    for (int k = part; k < P; k += NP) Z0 += s0[(int64_t)k * N];
+  }
+  float Zp = 0.f, Dp = 1.f;
+  for (int k = k0; k < k1 || k == k0; k += KB) {     // at least once: the registers hold the first KB segments
+    load(k);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      if (s0 + k < p.nseg) zp[(s0 + k) * zs] = Z;    // the state sum entering segment s0 + k
-      Z = d[k] * Z + zl[k];
-    }
-  };
-  float za[16], da[16], zb[16], dbf[16];
-  if (p.nseg > 0) ld(0, za, da);
-  for (int s0 = 0; s0 < p.nseg; s0 += 32) {
-    if (s0 + 16 < p.nseg) ld(s0 + 16, zb, dbf);
-    step(s0, za, da);
-    if (s0 + 16 < p.nseg) {
-      if (s0 + 32 < p.nseg) ld(s0 + 32, za, da);
-      step(s0 + 16, zb, dbf);
+    for (int j = 0; j < KB; ++j) {
+      Zp = d[j] * Zp + z[j];
+      Dp *= d[j];
     }
   }
+  float Z = 0.f;
+#pragma unroll
+  for (int j = 0; j < NP; ++j) Z += __shfl(Z0, j * CW + ci, 64);
+#pragma unroll
+  for (int j = 0; j < NP - 1; ++j) {
+    const float dj = __shfl(Dp, j * CW + ci, 64), zj = __shfl(Zp, j * CW + ci, 64);
+    if (j < part) Z = dj * Z + zj;
+  }
+  if (on)
+    for (int k = k0; k < k1; k += KB) {
+      if (pl > KB) load(k);              // else the registers still hold the part
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+        if (k + j < k1) {
+          zp[(int64_t)(k + j) * zs] = Z;   // the state sum entering segment k + j
+          Z = d[j] * Z + z[j];
+        }
+    }
 }
 
+// One wave per (segment, batch, column block), operands straight from global memory into fp32 MFMAs
+// (32 tokens x 32 columns):
+//   hs_t[n] = (sum_h Ei[h][t] Zin[h][n] + sum_g sum_s WT_g[s][t] B_s[g][n]) / (H P),
+// k-steps over pairs of heads, then over pairs of tokens of each group (WT_g[s][t] = 0 for s > t and past the end).
+// Loads are unconditional at clamped (valid) addresses, so that a batch of them is in flight together: group 0's
+// in-segment operands and the first heads' go out first, the next heads' before the current ones' MFMAs.  No B
+// operand is masked: a lane past the last column only feeds an output column that is not stored, and a token
+// past the end meets WT_g[s][t] = 0 (u = 0 there); a head past H (odd H) has its Ei operand multiplied by 0.
 template <typename T>
-__global__ __launch_bounds__(256) void ssd_hs_out_kernel(SsdParams p, HsParams q) {
-  __shared__ HsSmem sm;
-  const int si = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int H = p.nheads, N = p.dstate, hpg = H / p.ngroups, N8 = N / 8;
+__global__ __launch_bounds__(64) void ssd_hs_out_kernel(SsdParams p, HsParams q) {
+  const int si = blockIdx.x, b = blockIdx.y, n0 = HS_NB * blockIdx.z, l = lane_id(), i = l & 31, hf = l >> 5;
+  const int H = p.nheads, N = p.dstate, G = p.ngroups;
   const int len = min(HS_SEG, p.seqlen - si * HS_SEG);
-  if (tid == 0) sm.anywide = 0;
-  hs_prologue<T, true>(p, q, sm, b, si, len);
-  __syncthreads();
-  if (tid < H && sm.wide[tid]) sm.anywide = 1;       // benign race: every writer stores 1
-  for (int e = tid; e < HS_SEG * H; e += blockDim.x) {
-    const int t = e / H, h = e % H;
-    const float c = sm.c[t][h], m = sm.mid[h];
-    const bool wide = sm.wide[h];
-    sm.E[t][h] = wide ? 0.f : __expf(c - m);
-    sm.F[t][h] = wide ? 0.f : __expf(m - c) * sm.u[t][h];
-    sm.Ei[t][h] = __expf(c);
+  const int64_t tok0 = (int64_t)si * HS_SEG;
+  const bool col = n0 + i < N;
+  const int ic = min(i, N - 1 - n0);                                             // a valid column for every lane
+  const float* eit = q.u + ((int64_t)b * p.nseg + si) * H * HS_SEG + i;        // [h][t], this lane's t
+  const float* zin = q.z + (((int64_t)b * p.nseg + si) * H) * N + n0 + ic;     // [h][n], this lane's n
+  const float* wseg = q.w + ((int64_t)b * p.nseg + si) * G * (HS_SEG * HS_SEG) + i;   // [g][s][t]
+  const T* Bb = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + n0 + ic;
+  constexpr int KU = 16, KS = HS_SEG / 2;
+  f32x16 acc = zero16();
+  auto mm = [&](const float (&a)[KU], const float (&bq)[KU]) {
+#pragma unroll
+    for (int j = 0; j < KU; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j], bq[j], acc, 0, 0, 0);
+  };
+  // in-segment operands of group g: step m = tokens (2m, 2m + 1), lane half hf takes token 2m + hf
+  auto ldw = [&](int g, float (&a)[KS], float (&bq)[KS]) {
+#pragma unroll
+    for (int m = 0; m < KS; ++m) {
+      const int sk = 2 * m + hf, skc = min(sk, len - 1);
+      a[m] = wseg[((int64_t)g * HS_SEG + sk) * HS_SEG];
+      bq[m] = to_f32(Bb[(tok0 + skc) * p.B_sl + (int64_t)g * N]);
+    }
+  };
+  // inter-segment operands: step k = heads (2k, 2k + 1), lane half hf takes head 2k + hf
+  auto ldz = [&](int k0, float (&a)[KU], float (&bq)[KU]) {
+#pragma unroll
+    for (int j = 0; j < KU; ++j) {
+      const int h = 2 * (k0 + j) + hf, hc = min(h, H - 1);
+      a[j] = eit[(int64_t)hc * HS_SEG] * (h < H ? 1.f : 0.f);     // Ei in [0, 1]
+      bq[j] = zin[(int64_t)hc * N];
+    }
+  };
+  const int nz = (H + 1) / 2;
+  float aw[KS], bw[KS], a0[KU], b0[KU], a1[KU], b1[KU];
+  ldw(0, aw, bw);
+  ldz(0, a0, b0);
+  for (int k0 = 0; k0 < nz; k0 += 2 * KU) {
+    const bool more = k0 + KU < nz, more2 = k0 + 2 * KU < nz;
+    if (more) ldz(k0 + KU, a1, b1);
+    mm(a0, b0);
+    if (more2) ldz(k0 + 2 * KU, a0, b0);
+    if (more) mm(a1, b1);
   }
-  // output blocks (row t, 8 columns n0 ..): thread tid owns blocks tid, tid + 256, ... (at most 4)
-  constexpr int MB = HS_SEG * (HS_MAXN / 8) / 256;
-  const int nblk = HS_SEG * N8;
-  float acc[MB][8];
-#pragma unroll
-  for (int k = 0; k < MB; ++k)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[k][j] = 0.f;
-  // inter-segment part: sum_h e^{c_t,h} Zin[h][n], HS_ZH heads of Zin staged in LDS at a time
-  const float* zin = q.z + (((int64_t)b * p.nseg + si) * H) * N;
-  for (int h0 = 0; h0 < H; h0 += HS_ZH) {
-    const int nh = min(HS_ZH, H - h0);
-    __syncthreads();                   // E / F / Ei formed; the previous heads' Zs no longer read
-    for (int e = tid; e < nh * N / 4; e += blockDim.x) {
-      const int hh = e / (N / 4), n = 4 * (e % (N / 4));
-      *reinterpret_cast<f32x4*>(&sm.Zs[hh][n]) = *reinterpret_cast<const f32x4*>(zin + (int64_t)(h0 + hh) * N + n);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < MB; ++k) {
-      const int e = tid + 256 * k;
-      if (e < nblk) {
-        const int t = e / N8, n0 = 8 * (e % N8);
-        for (int hh = 0; hh < nh; ++hh) {
-          float zv[8];
-          ld8f(&sm.Zs[hh][n0], zv);
-          const float ei = sm.Ei[t][h0 + hh];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[k][j] += ei * zv[j];
-        }
-      }
-    }
+  mm(aw, bw);
+  for (int g = 1; g < G; ++g) {
+    ldw(g, aw, bw);
+    mm(aw, bw);
   }
-  for (int g = 0; g < p.ngroups; ++g) {
-    __syncthreads();                   // the previous group's W and B no longer read
-    hs_load_b<T>(p, sm, b, si, len, g);
-    // W_g[t][s] = sum_{h in g} E[t][h] F[s][h] (+ the wide heads' terms directly), s <= t
-    for (int e = tid; e < HS_SEG * HS_SEG; e += blockDim.x) {
-      const int t = e / HS_SEG, s = e % HS_SEG;
-      float w = 0.f;
-      if (s <= t) {
-        float w4[4] = {0.f, 0.f, 0.f, 0.f};
-        int h = g * hpg;
-        for (; h + 4 <= (g + 1) * hpg; h += 4)
+  if (col) {
+    const float scale = 1.f / ((float)H * (float)p.headdim);
+    T* out = reinterpret_cast<T*>(q.hs) + ((int64_t)b * p.seqlen + tok0) * N + n0 + i;
 #pragma unroll
-          for (int k = 0; k < 4; ++k) w4[k] += sm.E[t][h + k] * sm.F[s][h + k];
-        for (; h < (g + 1) * hpg; ++h) w4[0] += sm.E[t][h] * sm.F[s][h];
-        w = (w4[0] + w4[1]) + (w4[2] + w4[3]);
-        if (sm.anywide)
-          for (h = g * hpg; h < (g + 1) * hpg; ++h)
-            if (sm.wide[h]) w += __expf(sm.c[t][h] - sm.c[s][h]) * sm.u[s][h];
-      }
-      sm.W[t][s] = w;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < MB; ++k) {
-      const int e = tid + 256 * k;
-      if (e < nblk) {
-        const int t = e / N8, n0 = 8 * (e % N8);
-        for (int s = 0; s <= t; ++s) {
-          float bv[8];
-          ld8f(&sm.Bt[s][n0], bv);
-          const float w = sm.W[t][s];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[k][j] += w * bv[j];
-        }
-      }
-    }
-  }
-  T* out = reinterpret_cast<T*>(q.hs) + ((int64_t)b * p.seqlen + (int64_t)si * HS_SEG) * N;
-  const float scale = 1.f / ((float)H * (float)p.headdim);
-#pragma unroll
-  for (int k = 0; k < MB; ++k) {
-    const int e = tid + 256 * k;
-    if (e < nblk) {
-      const int t = e / N8, n0 = 8 * (e % N8);
-      if (t < len) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) out[(int64_t)t * N + n0 + j] = from_f32<T>(acc[k][j] * scale);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int t = acc_row(hf, r);
+      if (t < len) out[(int64_t)t * N] = from_f32<T>(acc[r] * scale);
     }
   }
 }
@@ -391,12 +409,11 @@ __device__ void hsb_load_g(const SsdParams& p, const HsParams& q, float (*g)[W],
 }
 
 struct HsbLocSmem {
-  float c[HS_SEG][HS_HP];        // as in HsSmem
+  float c[HS_SEG][HS_HP];        // as in HsLocSmem
   float u[HS_SEG][HS_HP];
   float g[HS_SEG][HSB_MAXN];     // ghs / (H P) (0 past the end and beyond N)
   float B[HS_SEG][HSB_MAXN];     // B of one group (likewise)
-  float cend[HSB_MAXH], mid[HSB_MAXH];
-  int wide[HSB_MAXH];
+  float cend[HSB_MAXH];
 };
 
 // One head per wave at a time, lanes over pairs of state columns, the per-token weights broadcast from lane t:
@@ -409,7 +426,7 @@ __global__ __launch_bounds__(64 * HSB_WAVES_LOC) void ssd_hsb_local_kernel(SsdPa
   const int64_t tok0 = (int64_t)si * HS_SEG;
   const int len = min(HS_SEG, p.seqlen - (int)tok0);
   const int n0 = 2 * l, t = l & 31;
-  hs_prologue<T, false>(p, q, sm, b, si, len);
+  hs_prologue<T>(p, sm, b, si, len, q.u);
   hsb_load_g<T, HSB_MAXN>(p, q, sm.g, b, si, len);
   float* gl = q.lam + (((int64_t)b * p.nseg + si) * H) * N;
   float* zl = q.z + (((int64_t)b * p.nseg + si) * H) * N;
@@ -722,12 +739,13 @@ __global__ __launch_bounds__(256) void ssd_hsb_reduce_kernel(SsdParams p, HsPara
 bool ssd_hs_supported(int nheads, int dstate) { return nheads <= HS_MAXH && dstate <= HS_MAXN; }
 bool ssd_hs_bwd_supported(int nheads, int dstate) { return nheads <= HSB_MAXH && dstate <= HSB_MAXN; }
 
-size_t ssd_hs_workspace_bytes(int batch, int seqlen, int nheads, int dstate, bool backward) {
+size_t ssd_hs_workspace_bytes(int batch, int seqlen, int nheads, int dstate, int ngroups, bool backward) {
   const size_t nseg = (seqlen + HS_SEG - 1) / HS_SEG;
   const size_t st = align256((size_t)batch * nseg * nheads * dstate * sizeof(float));
   return st + align256((size_t)batch * nseg * nheads * sizeof(float)) +
-         align256((size_t)batch * seqlen * nheads * sizeof(float)) +
-         (backward ? st + align256((size_t)batch * nseg * nheads * 2 * sizeof(float)) : 0);
+         align256((size_t)batch * nseg * HS_SEG * nheads * sizeof(float)) +
+         (backward ? st + align256((size_t)batch * nseg * nheads * 2 * sizeof(float))
+                   : align256((size_t)batch * nseg * ngroups * HS_SEG * HS_SEG * sizeof(float)));
 }
 
 void ssd_hs_workspace_layout(SsdParams& p, HsParams& q, void* workspace, bool backward) {
@@ -739,8 +757,9 @@ void ssd_hs_workspace_layout(SsdParams& p, HsParams& q, void* workspace, bool ba
   q.dec = reinterpret_cast<float*>(c);
   c += align256((size_t)p.batch * p.nseg * p.nheads * sizeof(float));
   q.u = reinterpret_cast<float*>(c);
-  c += align256((size_t)p.batch * p.seqlen * p.nheads * sizeof(float));
+  c += align256((size_t)p.batch * p.nseg * HS_SEG * p.nheads * sizeof(float));
   q.lam = backward ? reinterpret_cast<float*>(c) : nullptr;
+  q.w = backward ? nullptr : reinterpret_cast<float*>(c);
   c += backward ? st : 0;
   q.part = backward ? reinterpret_cast<float*>(c) : nullptr;
 }
@@ -766,21 +785,30 @@ hipError_t launch_ssd_hs_bwd(const SsdParams& p, const HsParams& q, float* dh0, 
 
 hipError_t launch_ssd_hs(const SsdParams& p, const HsParams& q, hipStream_t st) {
   if (p.seqlen == 0) return hipSuccess;
-  const dim3 grid((unsigned)p.nseg, (unsigned)p.batch);
+  const dim3 grid((unsigned)p.nseg, (unsigned)p.batch, (unsigned)((p.dstate + HS_NB - 1) / HS_NB));
   if (p.dtype == DT_BF16)
     hipLaunchKernelGGL(ssd_hs_local_kernel<bf16>, grid, dim3(256), 0, st, p, q);
   else
     hipLaunchKernelGGL(ssd_hs_local_kernel<float>, grid, dim3(256), 0, st, p, q);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  // parts per chain: about 16 segments each, at most 8 (a part's load then covers 8 consecutive columns)
+  const int np = p.nseg >= 128 ? 8 : p.nseg >= 64 ? 4 : p.nseg >= 32 ? 2 : 1;
   const int64_t nc = (int64_t)p.batch * p.nheads * p.dstate;
-  hipLaunchKernelGGL(ssd_hs_carry_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, st, p, q);
+  const int64_t waves = (nc * np + 63) / 64;
+  const dim3 cg((unsigned)((waves + 3) / 4));
+  switch (np) {
+    case 8: hipLaunchKernelGGL(ssd_hs_carry_kernel<8>, cg, dim3(256), 0, st, p, q); break;
+    case 4: hipLaunchKernelGGL(ssd_hs_carry_kernel<4>, cg, dim3(256), 0, st, p, q); break;
+    case 2: hipLaunchKernelGGL(ssd_hs_carry_kernel<2>, cg, dim3(256), 0, st, p, q); break;
+    default: hipLaunchKernelGGL(ssd_hs_carry_kernel<1>, cg, dim3(256), 0, st, p, q); break;
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.dtype == DT_BF16)
-    hipLaunchKernelGGL(ssd_hs_out_kernel<bf16>, grid, dim3(256), 0, st, p, q);
+    hipLaunchKernelGGL(ssd_hs_out_kernel<bf16>, grid, dim3(64), 0, st, p, q);
   else
-    hipLaunchKernelGGL(ssd_hs_out_kernel<float>, grid, dim3(256), 0, st, p, q);
+    hipLaunchKernelGGL(ssd_hs_out_kernel<float>, grid, dim3(64), 0, st, p, q);
   return hipGetLastError();
 }
 

@@ -484,9 +484,12 @@ def test_h_states_workspace_and_bwd_validation():
     assert _rc("mh_ssd_h_states_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
     g = _good_hs_bwd()
     assert _rc("mh_ssd_h_states_bwd_workspace_bytes", ct.byref(g), ct.byref(nb)) == 0
-    # the backward adds the adjoint's per-segment sums (b, nseg, H, N) fp32 to the forward's workspace
-    b, L, H, N = 2, 300, 8, 128
-    assert nb.value >= n.value + b * (-(-L // 32)) * H * N * 4
+    # forward: per-segment state sums (b, nseg, H, N), decays, e^c per (token, head) and the in-segment weights
+    # (b, nseg, G, 32, 32); backward: the state sums twice (forward and adjoint), decays, xs per (token, head)
+    b, L, H, N, G = 2, 300, 8, 128, 2
+    nseg = -(-L // 32)
+    assert n.value >= 4 * (b * nseg * H * N + b * nseg * H + b * L * H + b * nseg * G * 32 * 32)
+    assert nb.value >= 4 * (2 * b * nseg * H * N + b * nseg * H + b * L * H)
     g.dA = None
     assert _rc("mh_ssd_h_states_bwd", ct.byref(g), None) == -1
     g = _good_hs_bwd()
