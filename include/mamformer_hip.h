@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MH_ABI_VERSION 9
+#define MH_ABI_VERSION 10
 
 /* element types of x / B / C / y / q / k / v / o */
 enum { MH_F32 = 0, MH_BF16 = 1 };
@@ -148,6 +148,9 @@ int mh_ssd_ref_scan_fwd(const mh_ssd_args* a, void* h_states, void* stream);
  *   raw dt, through dt_bias, softplus and the clamp); dA (H,) fp32; d_dt_bias (H,) fp32 (required when
  *   fwd.dt_bias is set, else ignored); d_initial_state (b, H, P, N) fp32 or NULL.  Every output is overwritten
  *   (C, D and the gate get no gradient from h_states; the caller adds these to the output's gradients).
+ *   dx_rows (optional): the gradient w.r.t. x is the same for every channel p of a (token, head); when dx_rows is
+ *   set it is written there once per row, (b, L, H) fp32 contiguous, and dx is not written (may be NULL): pass it
+ *   as mh_ssd_bwd_args.dx_rows of the scan's backward to have it added to the scan's dx on the way out.
  *   Supported: nheads <= 128, dstate <= 128. */
 typedef struct {
   mh_ssd_args fwd;
@@ -159,6 +162,7 @@ typedef struct {
   float* d_dt_bias;
   float* d_initial_state;
   void* workspace; size_t workspace_bytes;
+  float* dx_rows;
 } mh_ssd_hs_bwd_args;
 int mh_ssd_h_states_bwd_workspace_bytes(const mh_ssd_hs_bwd_args* a, size_t* bytes);
 int mh_ssd_h_states_bwd(const mh_ssd_hs_bwd_args* a, void* stream);
@@ -174,7 +178,9 @@ int mh_ssd_h_states_bwd(const mh_ssd_hs_bwd_args* a, void* stream);
  *   (NULL: zero / not wanted); ddt (b, L, H) fp32, the gradient w.r.t. the raw dt (through
  *   dt_bias, softplus and the clamp per fwd.flags); dA (H,) fp32; dB, dC (b, L, G, N) in the dtype
  *   of x; dD like D (NULL when D is NULL); d_dt_bias (H,) fp32 or NULL.  Every output is
- *   overwritten.  Same supported sizes (and compositions) as the forward.
+ *   overwritten.  dx_rows (optional, NULL: none): (b, L, H) fp32 contiguous, added to every channel of
+ *   dx[b, t, h, :] before it is stored (the h_states backward's dx_rows, so that the two gradients w.r.t. x
+ *   meet without a second pass over dx).  Same supported sizes (and compositions) as the forward.
  * ---------------------------------------------------------------------- */
 typedef struct {
   mh_ssd_args fwd;
@@ -189,6 +195,7 @@ typedef struct {
   float* d_dt_bias;
   float* d_initial_state;
   void* workspace; size_t workspace_bytes;
+  const float* dx_rows;
 } mh_ssd_bwd_args;
 
 /* Bytes of workspace mh_ssd_chunk_scan_bwd needs for these sizes. */

@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # bytes of the static device scratch behind mh_ssd_chunk_scan_fwd_noalloc (MH_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -61,6 +61,7 @@ class SsdBwdArgs(ct.Structure):
         ("dC", _vp), ("dC_stride_b", _i64), ("dC_stride_l", _i64),
         ("dD", _vp), ("d_dt_bias", _vp), ("d_initial_state", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
+        ("dx_rows", _vp),
     ]
 
 
@@ -70,6 +71,7 @@ class SsdHsBwdArgs(ct.Structure):
         ("dhs", _vp), ("dx", _vp), ("ddt", _vp), ("dA", _vp), ("dB", _vp),
         ("d_dt_bias", _vp), ("d_initial_state", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
+        ("dx_rows", _vp),
     ]
 
 

@@ -305,6 +305,7 @@ int ssd_bwd_validate(const mh_ssd_bwd_args* a) {
     return fail(MH_ERR_ALIGN, "ssd_bwd: strides of dy, dx, dB, dC must be multiples of 16 bytes");
   if (a->dy_stride_h < f->headdim || a->dx_stride_h < f->headdim)
     return fail(MH_ERR_STRIDE, "ssd_bwd: dy/dx head stride smaller than headdim (headdim must be contiguous)");
+  if (reinterpret_cast<uintptr_t>(a->dx_rows) % 4) return fail(MH_ERR_ALIGN, "ssd_bwd: dx_rows must be 4-byte aligned");
   if (a->dB_stride_l < f->ngroups * f->dstate || a->dC_stride_l < f->ngroups * f->dstate)
     return fail(MH_ERR_STRIDE, "ssd_bwd: dB/dC token stride smaller than ngroups*dstate");
   if (a->ddt_stride_b < 0 || a->ddt_stride_l < 0) return fail(MH_ERR_STRIDE, "ssd_bwd: negative ddt stride");
@@ -339,6 +340,7 @@ hipError_t ssd_launch_bwd_native(const mh_ssd_bwd_args* a, hipStream_t st) {
   q.dB = a->dB; q.dB_sb = a->dB_stride_b; q.dB_sl = a->dB_stride_l;
   q.dC = a->dC; q.dC_sb = a->dC_stride_b; q.dC_sl = a->dC_stride_l;
   q.heads_per_wg = ssd_bwd_heads_per_wg(f);
+  q.dx_rows = a->dx_rows;
   if (nseg > 0) mh::ssd_bwd_workspace_layout(q, a->workspace);
   return mh::launch_ssd_bwd(q, st);
 }
@@ -539,6 +541,7 @@ int ssd_bwd_wide(const mh_ssd_bwd_args* a, hipStream_t st) {
     }
     if (q > 0) {
       in.dx = at(ws, w.oX2); in.dx_stride_h = P; in.dx_stride_l = H * P; in.dx_stride_b = L * H * P;
+      in.dx_rows = nullptr;            // added once, by the first piece
       in.ddt = reinterpret_cast<float*>(at(ws, w.oT2)); in.ddt_stride_l = H; in.ddt_stride_b = L * H;
       in.dA = reinterpret_cast<float*>(at(ws, w.oH3));
       in.dD = nullptr;
@@ -852,10 +855,12 @@ static int hs_bwd_validate(const mh_ssd_hs_bwd_args* a) {
                 (long long)f->nheads, (long long)f->dstate);
   if (!a->dA) return fail(MH_ERR_NULL, "ssd_h_states_bwd: dA is NULL");
   if (f->dt_bias && !a->d_dt_bias) return fail(MH_ERR_NULL, "ssd_h_states_bwd: d_dt_bias is NULL while dt_bias is set");
-  if (f->seqlen > 0 && (!a->dhs || !a->dx || !a->ddt || !a->dB))
-    return fail(MH_ERR_NULL, "ssd_h_states_bwd: dhs, dx, ddt and dB are required");
+  if (f->seqlen > 0 && (!a->dhs || !(a->dx || a->dx_rows) || !a->ddt || !a->dB))
+    return fail(MH_ERR_NULL, "ssd_h_states_bwd: dhs, dx (or dx_rows), ddt and dB are required");
   if (!aligned16(a->dhs) || !aligned16(a->dx) || !aligned16(a->dB) || !aligned16(a->d_initial_state))
     return fail(MH_ERR_ALIGN, "ssd_h_states_bwd: dhs, dx, dB and d_initial_state must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(a->dx_rows) % 4)
+    return fail(MH_ERR_ALIGN, "ssd_h_states_bwd: dx_rows must be 4-byte aligned");
   return MH_OK;
 }
 
@@ -957,7 +962,7 @@ int mh_ssd_h_states_bwd(const mh_ssd_hs_bwd_args* a, void* stream) {
   ssd_fill(f, 64, (f->seqlen + 63) / 64, p);
   mh::HsParams q;
   memset(&q, 0, sizeof(q));
-  q.dhs = a->dhs; q.dx = a->dx; q.ddt = a->ddt; q.dA = a->dA; q.dB = a->dB;
+  q.dhs = a->dhs; q.dx = a->dx; q.ddt = a->ddt; q.dA = a->dA; q.dB = a->dB; q.dx_rows = a->dx_rows;
   q.d_dt_bias = f->dt_bias ? a->d_dt_bias : nullptr;
   if (f->seqlen > 0) mh::ssd_hs_workspace_layout(p, q, a->workspace, true);
   else p.nseg = 0;

@@ -109,6 +109,7 @@ struct HsParams {
   float* dA;                 // (H,)
   void* dB;                  // (b, L, G, N) contiguous, I/O dtype
   float* d_dt_bias;          // (H,) or null
+  float* dx_rows;            // (b, L, H) fp32 or null: dx written once per (token, head) row instead of into dx
   float* lam;                // workspace: (b, nseg, H, N) the adjoint's local parts, then the adjoint entering
   float* part;               // workspace: (b, nseg, H, 2) dA and d_dt_bias partials
 };
@@ -142,6 +143,7 @@ struct SsdBwdParams {
   float* part_s;             // workspace: (b, nseg, H, 3) per-segment dA, d_dt_bias, dD (per head) partials
   float* part_dc;            // workspace: (b, nseg, H, 2, P) per-segment, per-token-half dD partials (per channel)
   int heads_per_wg;          // heads of one group handled by a workgroup of the gradient kernel (HB)
+  const float* dx_rows;      // (b, L, H) fp32 or null: added to every channel of dx[b, t, h, :]
 };
 hipError_t launch_ssd_bwd(const SsdBwdParams& p, hipStream_t st);
 size_t ssd_bwd_workspace_bytes(int batch, int seqlen, int nheads, int dstate, int ngroups, int dtype,

@@ -893,6 +893,7 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
     auto store_dx = [&]() {
       const float dtx = from_half(dtv, sbx);
       if (s_x < len) {
+        const float xr = q.dx_rows ? q.dx_rows[((int64_t)b * q.f.seqlen + tok0 + s_x) * q.f.nheads + h] : 0.f;
         T* o = reinterpret_cast<T*>(q.dx) + (int64_t)b * q.dx_sb + (int64_t)(tok0 + s_x) * q.dx_sl +
                (int64_t)h * q.dx_sh + 32 * pb + 4 * half;
 #pragma unroll
@@ -900,12 +901,12 @@ __global__ __launch_bounds__(128 * (N / 32)) void ssd_bwd_grad_kernel(SsdBwdPara
           if constexpr (sizeof(T) == 2) {
             bf16x4 v;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = (bf16)(dtx * ax[4 * jj + k] + Dv[4 * jj + k] * dyv[4 * jj + k]);
+            for (int k = 0; k < 4; ++k) v[k] = (bf16)(dtx * ax[4 * jj + k] + Dv[4 * jj + k] * dyv[4 * jj + k] + xr);
             *reinterpret_cast<bf16x4*>(o + 8 * jj) = v;
           } else {
             f32x4 v;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = dtx * ax[4 * jj + k] + Dv[4 * jj + k] * dyv[4 * jj + k];
+            for (int k = 0; k < 4; ++k) v[k] = dtx * ax[4 * jj + k] + Dv[4 * jj + k] * dyv[4 * jj + k] + xr;
             *reinterpret_cast<f32x4*>(o + 8 * jj) = v;
           }
         }

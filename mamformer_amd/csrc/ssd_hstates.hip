@@ -680,8 +680,11 @@ __global__ __launch_bounds__(64 * HSB_WAVES) void ssd_hsb_main_kernel(SsdParams 
         part[2 * h] = dA;
         part[2 * h + 1] = db;
       }
-      // dx[t][h][p] = dt_t du_t for every p: lane t writes the first half of the row, lane t + 32 the second
-      if (tv) {
+      // dx[t][h][p] = dt_t du_t for every p: lane t writes the first half of the row, lane t + 32 the second (or
+      // lane t the row's one value into dx_rows)
+      if (tv && q.dx_rows) {
+        if (l < 32) q.dx_rows[((int64_t)b * p.seqlen + tok0 + t) * H + h] = d * du;
+      } else if (tv) {
         const float dxs = d * du;
         T* o = dxb + ((int64_t)t * H + h) * HD + (l >> 5) * (HD / 2);
         if constexpr (sizeof(T) == 2) {

@@ -244,13 +244,15 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
     if not _plan_only and torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (x4, dt32, A32, B4, C4, D32, bias32, h0, z4)):
         cfg = (dt_softplus, dt_limit, chunk_size, xsum)
-        y4, fin = _SelectiveScanFn.apply(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg)
+        if return_h_states:
+            y4, fin, hs = _SelectiveScanHsFn.apply(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg)
+        else:
+            y4, fin = _SelectiveScanFn.apply(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg)
         if z4 is not None:
             y4 = _GateFn.apply(y4, z4)
         out = [y4.reshape(x.shape) if x.dim() == 3 else y4]
         if return_h_states:
-            out.append(_h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=True,
-                                 xsum=xsum))
+            out.append(hs)
         if return_final_state:
             out.append(fin.reshape(b, H * P, N) if x.dim() == 3 else fin)
         return out[0] if len(out) == 1 else tuple(out)
@@ -297,7 +299,7 @@ def _scan_fwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg):
     return y4, fin
 
 
-def _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4, dfin, need_dh0, plan_only=False):
+def _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4, dfin, need_dh0, plan_only=False, dx_rows=None):
     dt_softplus, dt_limit = cfg[0], cfg[1]
     b, L, H, P = x4.shape
     G, N = B4.shape[2], B4.shape[3]
@@ -327,6 +329,7 @@ def _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4, dfin, need_dh0, 
     a.dB, a.dB_stride_b, a.dB_stride_l = _ptr(dB), dB.stride(0), dB.stride(1)
     a.dC, a.dC_stride_b, a.dC_stride_l = _ptr(dC), dC.stride(0), dC.stride(1)
     a.dD, a.d_dt_bias, a.d_initial_state = _ptr(dD), _ptr(dbias), _ptr(dh0)
+    a.dx_rows = _ptr(dx_rows)
     nbytes = ct.c_size_t()
     _lib.call("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(nbytes))
     ws = torch.empty(max(int(nbytes.value), 16), device=dev, dtype=torch.uint8)
@@ -356,6 +359,47 @@ class _SelectiveScanFn(torch.autograd.Function):
         dx, ddt, dA, dB, dC, dD, dh0, dbias = _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, ctx.cfg, dy4,
                                                         dfin, need_dh0)
         return dx, ddt, dA, dB, dC, dD, dh0, dbias, None
+
+
+class _SelectiveScanHsFn(torch.autograd.Function):
+    """The scan with h_states (``selective_scan(..., return_h_states=True)`` under autograd, mamba2.py:114-116):
+    forward = the prefill kernels (which also write the per-head sums of x) and ``mh_ssd_h_states``; backward =
+    the h_states gradient first, its gradient w.r.t. x as one fp32 value per (token, head) row
+    (``mh_ssd_h_states_bwd`` with ``dx_rows``), then ``mh_ssd_chunk_scan_bwd``, which adds those rows to its dx as
+    it stores it, so the two gradients w.r.t. x meet without a separate pass over dx.  The remaining gradients
+    (dt, A, B, dt_bias, the initial state) of the two outputs are added here."""
+
+    @staticmethod
+    def forward(ctx, x4, dt32, A32, B4, C4, D32, h0, bias32, cfg):
+        y4, fin = _scan_fwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg)
+        hs = _h_states_fwd(x4, dt32, A32, B4, h0, bias32, cfg[0], cfg[1], cfg[3])
+        ctx.save_for_backward(x4, dt32, A32, B4, C4, D32, h0, bias32)
+        ctx.cfg = cfg
+        ctx.set_materialize_grads(False)
+        return y4, fin, hs
+
+    @staticmethod
+    def backward(ctx, dy4, dfin, dhs):
+        x4, dt32, A32, B4, C4, D32, h0, bias32 = ctx.saved_tensors
+        cfg = ctx.cfg
+        need_dh0 = h0 is not None and ctx.needs_input_grad[6]
+        if dhs is None:
+            dx, ddt, dA, dB, dC, dD, dh0, dbias = _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4,
+                                                            dfin, need_dh0)
+            return dx, ddt, dA, dB, dC, dD, dh0, dbias, None
+        xr, ddt_h, dA_h, dB_h, dh0_h, dbias_h = _h_states_bwd_blocks(dhs, x4, dt32, A32, B4, h0, bias32, cfg[0],
+                                                                     cfg[1], cfg[3], rows=True)
+        if dy4 is None and dfin is None:            # only h_states reaches the loss
+            b, L, H, P = x4.shape
+            dx = xr[..., None].expand(b, L, H, P).to(x4.dtype)
+            dC = torch.zeros_like(C4)
+            dD = None if D32 is None else torch.zeros_like(D32)
+            return (dx, ddt_h, dA_h, dB_h, dC, dD, dh0_h if need_dh0 else None, dbias_h, None)
+        dx, ddt, dA, dB, dC, dD, dh0, dbias = _scan_bwd(x4, dt32, A32, B4, C4, D32, h0, bias32, cfg, dy4, dfin,
+                                                        need_dh0, dx_rows=xr)
+        dh0 = dh0 + dh0_h if need_dh0 else None
+        dbias = None if dbias is None else dbias + dbias_h
+        return dx, ddt + ddt_h, dA + dA_h, dB + dB_h, dC, dD, dh0, dbias, None
 
 
 def _gate_args(y4, z4, out, g=None, dz=None):
@@ -455,16 +499,12 @@ def selective_scan_bwd(dy, x, dt, A, B, C, D=None, *, d_final_state=None, initia
     return out
 
 
-def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=False, xsum=None):
-    """h_states[b, t, n] = mean over (h, p) of the state h_t[h, p, n] (mamba2.py:114-116).
+def _h_states(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, xsum=None):
+    """h_states[b, t, n] = mean over (h, p) of the state h_t[h, p, n] (mamba2.py:114-116), without autograd.
 
     Computed by ``mh_ssd_h_states`` (the channel sums of the state follow a recurrence with one scalar input per
-    (token, head), sum_p x); with ``grad`` through an autograd node whose backward differentiates the equivalent
-    swapped prefill below.  More than 128 heads take the swapped prefill in the forward as well.
+    (token, head), sum_p x); under autograd ``_SelectiveScanHsFn`` computes it together with the scan.
     """
-    cfg = (dt_softplus, dt_limit, chunk_size, xsum)
-    if grad:
-        return _HStatesFn.apply(x4, dt32, A32, B4, h0, bias32, cfg)
     return _h_states_fwd(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum)
 
 
@@ -527,13 +567,15 @@ def _h_states_kernel(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum=
     return hs
 
 
-def _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum=None):
-    """Gradients of <ghs, h_states> by ``mh_ssd_h_states_bwd``: (dx, ddt, dA, dB, d h0, d dt_bias)."""
+def _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum=None, rows=False):
+    """Gradients of <ghs, h_states> by ``mh_ssd_h_states_bwd``: (dx, ddt, dA, dB, d h0, d dt_bias); with ``rows``
+    the gradient w.r.t. x as its one value per (token, head), (b, L, H) fp32, instead of dx."""
     b, L, H, P = x4.shape
     G, N = B4.shape[2], B4.shape[3]
     dev = x4.device
     ghs = ghs.to(x4.dtype).contiguous()
-    dx = torch.empty((b, L, H, P), device=dev, dtype=x4.dtype)
+    dx = None if rows else torch.empty((b, L, H, P), device=dev, dtype=x4.dtype)
+    dxr = torch.empty((b, L, H), device=dev, dtype=torch.float32) if rows else None
     ddt = torch.empty((b, L, H), device=dev, dtype=torch.float32)
     dA = torch.empty((H,), device=dev, dtype=torch.float32)
     dB = torch.empty((b, L, G, N), device=dev, dtype=B4.dtype)
@@ -542,21 +584,22 @@ def _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_lim
     a = _lib.SsdHsBwdArgs()
     a.fwd = _ssd_args(x4, dt32, A32, B4, B4, None, bias32, dt_softplus, dt_limit, h0, x4, None, 64, None, xsum)
     a.dhs, a.dx, a.ddt, a.dA, a.dB = _ptr(ghs), _ptr(dx), _ptr(ddt), _ptr(dA), _ptr(dB)
-    a.d_dt_bias, a.d_initial_state = _ptr(dbias), _ptr(dh0)
+    a.d_dt_bias, a.d_initial_state, a.dx_rows = _ptr(dbias), _ptr(dh0), _ptr(dxr)
     nbytes = ct.c_size_t()
     _lib.call("mh_ssd_h_states_bwd_workspace_bytes", ct.byref(a), ct.byref(nbytes))
     ws = torch.empty(max(int(nbytes.value), 16), device=dev, dtype=torch.uint8)
     a.workspace, a.workspace_bytes = _ptr(ws), nbytes.value
     _lib.call("mh_ssd_h_states_bwd", ct.byref(a), _stream(dev))
-    return dx, ddt, dA, dB, dh0, dbias
+    return (dxr if rows else dx), ddt, dA, dB, dh0, dbias
 
 
-def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum=None):
+def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum=None, rows=False):
     """``mh_ssd_h_states_bwd`` for any head count and dstate: the state columns separate (column n of h_states
     depends on B[..., n] alone; dx, ddt, dA and d dt_bias are sums over columns, dB and d h0 per column), so
     dstate > 128 runs as column pieces of at most 128; the heads enter h_states as a sum, so more than 128 heads
     run as head blocks, each with the gradient scaled by H_block / H (its h_states is a mean over its own heads).
-    Every piece is the dedicated kernel; pieces combine in a fixed order (deterministic)."""
+    Every piece is the dedicated kernel; pieces combine in a fixed order (deterministic).  With ``rows`` the
+    gradient w.r.t. x comes as its one fp32 value per (token, head), (b, L, H)."""
     b, L, H, P = x4.shape
     G, N = B4.shape[2], B4.shape[3]
     if N > _HS_BWD_MAXN:
@@ -565,8 +608,9 @@ def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_lim
             n1 = min(N, n0 + _HS_BWD_MAXN)
             outs.append(_h_states_bwd_blocks(ghs[..., n0:n1], x4, dt32, A32, B4[..., n0:n1].contiguous(),
                                              None if h0 is None else h0[..., n0:n1].contiguous(), bias32,
-                                             dt_softplus, dt_limit, xsum))
-        dx = sum(o[0].to(torch.float32) for o in outs).to(x4.dtype)
+                                             dt_softplus, dt_limit, xsum, rows))
+        dx = sum(o[0].to(torch.float32) for o in outs)
+        dx = dx if rows else dx.to(x4.dtype)
         ddt = sum(o[1] for o in outs)
         dA = sum(o[2] for o in outs)
         dB = torch.cat([o[3] for o in outs], dim=-1)
@@ -574,9 +618,9 @@ def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_lim
         dbias = None if bias32 is None else sum(o[5] for o in outs)
         return dx, ddt, dA, dB, dh0, dbias
     if H <= _HS_MAXH:
-        return _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum)
+        return _h_states_bwd_kernel(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, xsum, rows)
     dev = x4.device
-    dx = torch.empty((b, L, H, P), device=dev, dtype=x4.dtype)
+    dx = torch.empty((b, L, H) if rows else (b, L, H, P), device=dev, dtype=torch.float32 if rows else x4.dtype)
     ddt = torch.empty((b, L, H), device=dev, dtype=torch.float32)
     dA = torch.empty((H,), device=dev, dtype=torch.float32)
     dB = torch.zeros((b, L, G, N), device=dev, dtype=torch.float32)
@@ -585,7 +629,8 @@ def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_lim
     g32 = ghs.to(torch.float32)
     for h0_, h1_ in _head_blocks(H, G):
         xb, db, ab, bb, h0b, biasb, g0, g1 = _h_block_args(x4, dt32, A32, B4, h0, bias32, h0_, h1_)
-        r = _h_states_bwd_kernel(g32 * ((h1_ - h0_) / H), xb, db, ab, bb, h0b, biasb, dt_softplus, dt_limit)
+        r = _h_states_bwd_kernel(g32 * ((h1_ - h0_) / H), xb, db, ab, bb, h0b, biasb, dt_softplus, dt_limit,
+                                 rows=rows)
         dx[:, :, h0_:h1_] = r[0]
         ddt[:, :, h0_:h1_] = r[1]
         dA[h0_:h1_] = r[2]
@@ -597,44 +642,9 @@ def _h_states_bwd_blocks(ghs, x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_lim
     return dx, ddt, dA, dB.to(B4.dtype), dh0, dbias
 
 
-class _HStatesFn(torch.autograd.Function):
-    """h_states with its gradient: forward = ``mh_ssd_h_states``, backward = ``mh_ssd_h_states_bwd``, each as head
-    blocks and state-column pieces of at most 128 (``_h_states_fwd``, ``_h_states_bwd_blocks``); only a headdim
-    other than 64 (which the prefill itself does not take) would differentiate the swapped prefill instead."""
-
-    @staticmethod
-    def forward(ctx, x4, dt32, A32, B4, h0, bias32, cfg):
-        ctx.save_for_backward(x4, dt32, A32, B4, h0, bias32)
-        ctx.cfg = cfg
-        return _h_states_fwd(x4, dt32, A32, B4, h0, bias32, cfg[0], cfg[1], cfg[3])
-
-    @staticmethod
-    def backward(ctx, ghs):
-        saved = ctx.saved_tensors
-        x4 = saved[0]
-        if x4.shape[3] == 64:
-            dx, ddt, dA, dB, dh0, dbias = _h_states_bwd_blocks(ghs, *saved, ctx.cfg[0], ctx.cfg[1], ctx.cfg[3])
-            need = ctx.needs_input_grad
-            return (dx if need[0] else None, ddt if need[1] else None, dA if need[2] else None,
-                    dB if need[3] else None, dh0 if need[4] else None, dbias if need[5] else None, None)
-        leaves = [None if t is None else t.detach().requires_grad_(bool(need))
-                  for t, need in zip(saved, ctx.needs_input_grad[:6])]
-        with torch.enable_grad():
-            hs = _h_states_swap(*leaves, *ctx.cfg[:3], grad=True)
-        want = [t for t in leaves if t is not None and t.requires_grad]
-        got = torch.autograd.grad(hs, want, ghs, allow_unused=True) if want else ()
-        grads, k = [], 0
-        for t in leaves:
-            if t is not None and t.requires_grad:
-                grads.append(got[k])
-                k += 1
-            else:
-                grads.append(None)
-        return (*grads, None)
-
-
 def _h_states_swap(x4, dt32, A32, B4, h0, bias32, dt_softplus, dt_limit, chunk_size, grad=False):
-    """h_states by a second run of the prefill kernels on a swapped problem (used for the gradient).
+    """h_states by a second run of the prefill kernels on a swapped problem: an independent second formulation
+    (the tests check the dedicated kernels and their gradient against it at full size).
 
     The channel sum of the state is itself an SSD output once the roles of x and B are swapped: with
     heads h' = (h, q) over the two 64-wide halves q of the state dimension n, headdim' = 64 (n' = n - 64q),

@@ -506,3 +506,31 @@ def test_h_states_workspace_and_bwd_validation():
     g = _good_hs_bwd()
     g.workspace, g.workspace_bytes = ct.c_void_p(4096), 16
     assert _rc("mh_ssd_h_states_bwd", ct.byref(g), None) == -7
+    # dx_rows in place of dx: dx may then be NULL; dx_rows needs 4-byte alignment
+    g = _good_hs_bwd()
+    g.dx, g.dx_rows = None, ct.c_void_p(4096)
+    assert _rc("mh_ssd_h_states_bwd_workspace_bytes", ct.byref(g), ct.byref(nb)) == 0
+    g.dx_rows = ct.c_void_p(4098)
+    assert _rc("mh_ssd_h_states_bwd_workspace_bytes", ct.byref(g), ct.byref(nb)) == -5
+    g.dx_rows = None
+    assert _rc("mh_ssd_h_states_bwd_workspace_bytes", ct.byref(g), ct.byref(nb)) == -1
+
+
+def test_scan_bwd_dx_rows_alignment():
+    a = _lib.SsdBwdArgs()
+    a.fwd = _good_ssd()
+    fake = ct.c_void_p(4096)
+    a.dy = a.dx = a.ddt = a.dA = a.dB = a.dC = fake
+    b, L, H, P, N, G = 2, 300, 8, 64, 128, 2
+    a.dy_stride_h = a.dx_stride_h = P
+    a.dy_stride_l = a.dx_stride_l = H * P
+    a.dy_stride_b = a.dx_stride_b = L * H * P
+    a.ddt_stride_l, a.ddt_stride_b = H, L * H
+    a.dB_stride_l = a.dC_stride_l = G * N
+    a.dB_stride_b = a.dC_stride_b = L * G * N
+    n = ct.c_size_t()
+    assert _rc("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+    a.dx_rows = ct.c_void_p(4096)
+    assert _rc("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
+    a.dx_rows = ct.c_void_p(4097)
+    assert _rc("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == -5

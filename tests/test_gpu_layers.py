@@ -16,6 +16,7 @@ import torch
 import torch.nn.functional as F
 
 import mamformer_amd as mh
+from mamformer_amd import ops
 from mamformer_amd.layers import Mamba2Layer, kda_linear_attention
 from oracle import kda as okda
 from oracle import ssd as ref
@@ -228,7 +229,6 @@ def test_h_states_gradients_alone_vs_recurrence(dtype, b, L, H, G, N, h0, limit,
 def test_h_states_bwd_matches_swapped_prefill_backward_at_size(dtype):
     """At a training size (b2 L2048 H64 N128) the dedicated h_states backward and autograd through the swapped
     prefill (the prefill backward kernels on the problem with x and B exchanged) give the same gradients."""
-    from mamformer_amd import ops
     g = torch.Generator(device="cuda").manual_seed(5)
     b, L, H, P, G, N = 2, 2048, 64, 64, 1, 128
     x = torch.randn(b, L, H, P, device="cuda", generator=g).to(dtype)
@@ -423,3 +423,35 @@ def test_kda_linear_attention_cache_semantics(K):
     check("one-token cache S", c3["S"], S3, 1e-4)
     check("one-token cache z", c3["z"], z3, 1e-4)
     assert c3["attn_type"] == "linear" and c3["S"].shape == (B, H, K, D) and c3["z"].shape == (B, H, K, 1)
+
+
+def test_h_states_bwd_rows_match_dx_and_scan_bwd_adds_rows():
+    """mh_ssd_h_states_bwd with dx_rows writes the one value per (token, head) that it otherwise broadcasts over
+    the row of dx (equal after the bf16 rounding), leaving its other outputs bit-identical; mh_ssd_chunk_scan_bwd
+    with dx_rows adds them to every channel of its dx and leaves its other outputs bit-identical."""
+    g = torch.Generator().manual_seed(5)
+    b, L, H, P, N, G = 2, 200, 8, 64, 64, 2
+    bf = torch.bfloat16
+    x = torch.randn(b, L, H, P, generator=g).to(bf).cuda()
+    dt = F.softplus(torch.randn(b, L, H, generator=g) - 1.0).cuda()
+    A = -torch.exp(torch.rand(H, generator=g) * 2.0).cuda()
+    B = torch.randn(b, L, G, N, generator=g).to(bf).cuda()
+    C = torch.randn(b, L, G, N, generator=g).to(bf).cuda()
+    D = (1 + 0.1 * torch.randn(H, generator=g)).cuda()
+    ghs = torch.randn(b, L, N, generator=g).to(bf).cuda()
+    dy = torch.randn(b, L, H, P, generator=g).to(bf).cuda()
+    say("h_states bwd rows / scan bwd dx_rows")
+    r_dx = ops._h_states_bwd_kernel(ghs, x, dt, A, B, None, None, False, None)
+    r_rows = ops._h_states_bwd_kernel(ghs, x, dt, A, B, None, None, False, None, rows=True)
+    cfg = (False, None, None, None)
+    base = ops._scan_bwd(x, dt, A, B, C, D, None, None, cfg, dy, None, False)
+    withr = ops._scan_bwd(x, dt, A, B, C, D, None, None, cfg, dy, None, False, dx_rows=r_rows[0])
+    torch.cuda.synchronize()
+    assert r_rows[0].shape == (b, L, H) and r_rows[0].dtype == torch.float32
+    assert torch.equal(r_dx[0], r_rows[0].to(bf)[..., None].expand(b, L, H, P))
+    for k in (1, 2, 3):
+        assert torch.equal(r_dx[k], r_rows[k])
+    ref = base[0].double().cpu() + r_rows[0].double().cpu()[..., None]
+    check("dx + rows", withr[0], ref.numpy(), 5e-3)
+    for k in range(1, 6):
+        assert torch.equal(base[k], withr[k])
