@@ -357,7 +357,9 @@ def bench_ref_scan(steps, warmup, batch=2, seqlen=4096, d_inner=2048, dstate=128
     mamba2.py:70-130) at the reference's 1b preset width (d_inner 2048, N 128; config.py:833-843), bf16, with and
     without h_states.  Bound by one exponential per (token, channel, state): ``exp_roofline_us`` is that count at
     the transcendental rate, ``valu_roofline_us`` adds the four fp32 operations per element (decay argument,
-    B dt x, the state update and the C read-out) at the VALU rate, sharing the same issue slots."""
+    B dt x, the state update and the C read-out) at the VALU rate, sharing the same issue slots.  ``us_train`` is a
+    forward + backward through autograd (the backward recomputes the states from checkpoints twice, so it costs
+    about three forward passes of exponentials)."""
     import mamformer_amd as mh
 
     g = torch.Generator(device="cuda").manual_seed(21)
@@ -373,16 +375,28 @@ def bench_ref_scan(steps, warmup, batch=2, seqlen=4096, d_inner=2048, dstate=128
         plans_hs.append(mh.plan_selective_scan_reference(x, dt, A_log, B, C, D, True, True))
     _, ev = time_plans(plans, steps, warmup)
     _, ev_hs = time_plans(plans_hs, steps, warmup)
+    # training: forward + backward of <gy, y> through autograd (mh_ssd_ref_scan_fwd, then mh_ssd_ref_scan_bwd:
+    # a checkpointing forward pass and two recomputing gradient kernels)
+    leaves = [x.clone().requires_grad_(), dt.clone().requires_grad_(), A_log.clone().requires_grad_(),
+              B.clone().requires_grad_(), C.clone().requires_grad_(), D.clone().requires_grad_()]
+    gy = torch.randn_like(x)
+
+    def train():
+        y = mh.selective_scan_reference(*leaves)
+        torch.autograd.grad(y, leaves, gy)
+
+    _, ev_tr = time_plans([train], max(3, steps // 10), 1)
     elems = batch * seqlen * d_inner * dstate
     t_exp = elems / PEAK_EXP
     t_valu = elems * (4 + 4) / PEAK_VALU
     nbytes = batch * seqlen * (d_inner * (2 + 4 + 2) + 2 * dstate * 2) + batch * d_inner * dstate * 4
     t = ev * 1e-3
-    res = dict(us_per_step=ev * 1e3, us_with_h_states=ev_hs * 1e3, mtok_s=batch * seqlen / t / 1e6,
+    res = dict(us_per_step=ev * 1e3, us_with_h_states=ev_hs * 1e3, us_train=ev_tr * 1e3,
+               mtok_s=batch * seqlen / t / 1e6,
                exp_roofline_us=t_exp * 1e6, valu_roofline_us=t_valu * 1e6, exp_frac=t_exp / t, valu_frac=t_valu / t,
                alg_bytes=nbytes, hbm_frac=nbytes / PEAK_HBM / t,
                shape=f"b{batch} L{seqlen} d_inner{d_inner} N{dstate} bf16")
-    del plans, plans_hs
+    del plans, plans_hs, leaves
     torch.cuda.empty_cache()
     return res
 

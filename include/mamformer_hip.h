@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MH_ABI_VERSION 10
+#define MH_ABI_VERSION 11
 
 /* element types of x / B / C / y / q / k / v / o */
 enum { MH_F32 = 0, MH_BF16 = 1 };
@@ -137,9 +137,38 @@ int mh_ssd_h_states(const mh_ssd_args* a, void* h_states, void* stream);
  *   reference starts from zero); chunk_len is ignored.  h_states (b, L, dstate) in the dtype of x, the mean over
  *   channels of the state after every token (mamba2.py:114-116), or NULL; it needs the workspace
  *   mh_ssd_ref_scan_workspace_bytes(a, 1, ..) gives (0 bytes without h_states).  Supported: dstate in {16, 32,
- *   64, 128, 256}, d_inner a multiple of 16.  No backward. */
+ *   64, 128, 256}, d_inner a multiple of 16.  Backward: mh_ssd_ref_scan_bwd below. */
 int mh_ssd_ref_scan_workspace_bytes(const mh_ssd_args* a, int h_states, size_t* bytes);
 int mh_ssd_ref_scan_fwd(const mh_ssd_args* a, void* h_states, void* stream);
+
+/* Backward of the reference-form scan: the autograd backward of selective_scan / _selective_scan_impl in the
+ *   reference's own parameterisation (mamformer/layers/mamba2.py:70-130, trained through in
+ *   tests/test_mamba2.py:56-71), i.e. the gradients of <dy, y> + <dhs, h_states> + <d_final_state, final_state> for
+ *   the call described by `fwd` (as mh_ssd_ref_scan_fwd reads it; fwd.y, final_state and workspace are ignored and
+ *   fwd.z must be NULL: the gate's backward is mh_silu_gate_bwd).  dy, dx (b, L, d_inner) and dhs, dB, dC (b, L, N)
+ *   contiguous in the dtype of x (dy, dhs NULL: zero); d_final_state, d_initial_state (b, d_inner, N) fp32 (NULL:
+ *   zero / not wanted); ddt (b, L, d_inner) fp32 w.r.t. the raw dt (through dt_bias, softplus and the clamp); dA
+ *   (N,) fp32 w.r.t. the rates A (the caller chains it to A_log through its clamp and exponential); dD like D;
+ *   d_dt_bias (d_inner,) fp32.  Every output is overwritten; the sums over channels, tokens and batch rows are
+ *   added in a fixed order (run-to-run identical).  The workspace holds the state at every 16th token (8th for
+ *   dstate 256), b * ceil(L / 16) * d_inner * N fp32, and the channel-block partials. */
+typedef struct {
+  mh_ssd_args fwd;
+  const void* dy;
+  const void* dhs;
+  const float* d_final_state;
+  void* dx;
+  float* ddt;
+  float* dA;
+  void* dB;
+  void* dC;
+  float* dD;
+  float* d_dt_bias;
+  float* d_initial_state;
+  void* workspace; size_t workspace_bytes;
+} mh_ssd_ref_bwd_args;
+int mh_ssd_ref_scan_bwd_workspace_bytes(const mh_ssd_ref_bwd_args* a, size_t* bytes);
+int mh_ssd_ref_scan_bwd(const mh_ssd_ref_bwd_args* a, void* stream);
 
 /* Backward of h_states: the autograd backward of the mean over (h, p) of the states
  *   (mamformer/layers/mamba2.py:114-116) taken through the scan, i.e. the gradients of <dhs, h_states> for the

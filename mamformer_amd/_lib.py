@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmamformer_hip.so"
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # bytes of the static device scratch behind mh_ssd_chunk_scan_fwd_noalloc (MH_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -72,6 +72,16 @@ class SsdHsBwdArgs(ct.Structure):
         ("d_dt_bias", _vp), ("d_initial_state", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
         ("dx_rows", _vp),
+    ]
+
+
+class SsdRefBwdArgs(ct.Structure):
+    _fields_ = [
+        ("fwd", SsdArgs),
+        ("dy", _vp), ("dhs", _vp), ("d_final_state", _vp),
+        ("dx", _vp), ("ddt", _vp), ("dA", _vp), ("dB", _vp), ("dC", _vp), ("dD", _vp),
+        ("d_dt_bias", _vp), ("d_initial_state", _vp),
+        ("workspace", _vp), ("workspace_bytes", _sz),
     ]
 
 
@@ -173,6 +183,7 @@ EXPORTS = (
     "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states",
     "mh_ssd_h_states_bwd_workspace_bytes", "mh_ssd_h_states_bwd",
     "mh_ssd_ref_scan_workspace_bytes", "mh_ssd_ref_scan_fwd",
+    "mh_ssd_ref_scan_bwd_workspace_bytes", "mh_ssd_ref_scan_bwd",
     "mh_silu_gate_fwd", "mh_silu_gate_bwd",
     "mh_ssd_state_update",
     "mh_kda_chunk_scan_fwd", "mh_kda_bwd_workspace_bytes", "mh_kda_chunk_scan_bwd",
@@ -220,6 +231,8 @@ def lib():
             h.mh_ssd_h_states_bwd.argtypes = [ct.POINTER(SsdHsBwdArgs), _vp]
             h.mh_ssd_ref_scan_workspace_bytes.argtypes = [ct.POINTER(SsdArgs), ct.c_int, ct.POINTER(_sz)]
             h.mh_ssd_ref_scan_fwd.argtypes = [ct.POINTER(SsdArgs), _vp, _vp]
+            h.mh_ssd_ref_scan_bwd_workspace_bytes.argtypes = [ct.POINTER(SsdRefBwdArgs), ct.POINTER(_sz)]
+            h.mh_ssd_ref_scan_bwd.argtypes = [ct.POINTER(SsdRefBwdArgs), _vp]
             h.mh_silu_gate_fwd.argtypes = [ct.POINTER(GateArgs), _vp]
             h.mh_silu_gate_bwd.argtypes = [ct.POINTER(GateArgs), _vp]
             h.mh_kda_chunk_scan_fwd.argtypes = [ct.POINTER(KdaArgs), _vp]
@@ -238,6 +251,7 @@ def lib():
                          "mh_ssd_h_states_workspace_bytes", "mh_ssd_h_states",
                          "mh_ssd_h_states_bwd_workspace_bytes", "mh_ssd_h_states_bwd",
                          "mh_ssd_ref_scan_workspace_bytes", "mh_ssd_ref_scan_fwd",
+                         "mh_ssd_ref_scan_bwd_workspace_bytes", "mh_ssd_ref_scan_bwd",
                          "mh_silu_gate_fwd", "mh_silu_gate_bwd"):
                 getattr(h, name).restype = ct.c_int
             ver = h.mh_abi_version()

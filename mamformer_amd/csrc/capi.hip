@@ -939,6 +939,63 @@ int mh_ssd_ref_scan_fwd(const mh_ssd_args* a, void* h_states, void* stream) {
   return hip_status(mh::launch_ssd_rf(p, reinterpret_cast<hipStream_t>(stream)), "ssd_ref_scan");
 }
 
+static int rf_bwd_validate(const mh_ssd_ref_bwd_args* a) {
+  if (!a) return fail(MH_ERR_NULL, "ssd_ref_scan_bwd: args is NULL");
+  // the forward's checks, with the output the backward does not write taken from x
+  mh_ssd_args g = a->fwd;
+  if (g.z) return fail(MH_ERR_UNSUPPORTED, "ssd_ref_scan_bwd: the output gate is not differentiated here (fwd.z must be NULL)");
+  g.y = const_cast<void*>(g.x); g.y_stride_b = g.x_stride_b; g.y_stride_l = g.x_stride_l; g.y_stride_h = g.x_stride_h;
+  int rc = rf_validate(&g, false);
+  if (rc) return rc;
+  const mh_ssd_args* f = &a->fwd;
+  if (f->seqlen > 0 && (!a->dx || !a->ddt || !a->dB || !a->dC))
+    return fail(MH_ERR_NULL, "ssd_ref_scan_bwd: dx, ddt, dB and dC are required");
+  if (!a->dA) return fail(MH_ERR_NULL, "ssd_ref_scan_bwd: dA is required");
+  if (f->D && !a->dD) return fail(MH_ERR_NULL, "ssd_ref_scan_bwd: dD is required when D is given");
+  if (f->dt_bias && !a->d_dt_bias) return fail(MH_ERR_NULL, "ssd_ref_scan_bwd: d_dt_bias is required with dt_bias");
+  const int es = elem_size(f->dtype);
+  const uintptr_t m = (uintptr_t)es - 1;
+  if (((uintptr_t)a->dy & m) || ((uintptr_t)a->dhs & m) || ((uintptr_t)a->dx & m) || ((uintptr_t)a->dB & m) ||
+      ((uintptr_t)a->dC & m) || ((uintptr_t)a->ddt & 3) || ((uintptr_t)a->d_final_state & 3) ||
+      ((uintptr_t)a->d_initial_state & 3))
+    return fail(MH_ERR_ALIGN, "ssd_ref_scan_bwd: gradient pointers must be aligned to their element size");
+  return MH_OK;
+}
+
+static size_t rf_bwd_need(const mh_ssd_ref_bwd_args* a) {
+  const mh_ssd_args* f = &a->fwd;
+  return mh::ssd_rf_bwd_workspace_bytes((int)f->batch, (int)f->seqlen, (int)(f->nheads * f->headdim), (int)f->dstate);
+}
+
+int mh_ssd_ref_scan_bwd_workspace_bytes(const mh_ssd_ref_bwd_args* a, size_t* bytes) {
+  if (!bytes) return fail(MH_ERR_NULL, "ssd_ref_scan_bwd: bytes output is NULL");
+  const int rc = rf_bwd_validate(a);
+  if (rc) return rc;
+  *bytes = rf_bwd_need(a);
+  return MH_OK;
+}
+
+int mh_ssd_ref_scan_bwd(const mh_ssd_ref_bwd_args* a, void* stream) {
+  const int rc = rf_bwd_validate(a);
+  if (rc) return rc;
+  const size_t need = rf_bwd_need(a);
+  if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
+    return fail(MH_ERR_WORKSPACE, "ssd_ref_scan_bwd: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
+                a->workspace_bytes);
+  mh::RfParams p;
+  rf_fill(&a->fwd, p);
+  p.y = nullptr;
+  p.z = nullptr;
+  p.final_state = nullptr;
+  p.dy = a->dy; p.dhs = a->dhs; p.d_final = a->d_final_state;
+  p.dx = a->dx; p.ddt = a->ddt; p.dA = a->dA; p.dB = a->dB; p.dC = a->dC;
+  p.dD = a->fwd.D ? a->dD : nullptr;
+  p.d_dt_bias = a->fwd.dt_bias ? a->d_dt_bias : nullptr;
+  p.dh0 = a->d_initial_state;
+  mh::ssd_rf_bwd_layout(p, a->workspace);
+  return hip_status(mh::launch_ssd_rf_bwd(p, reinterpret_cast<hipStream_t>(stream)), "ssd_ref_scan_bwd");
+}
+
 int mh_ssd_h_states_bwd_workspace_bytes(const mh_ssd_hs_bwd_args* a, size_t* bytes) {
   if (!bytes) return fail(MH_ERR_NULL, "ssd_h_states_bwd: bytes output is NULL");
   int rc = hs_bwd_validate(a);

@@ -90,10 +90,29 @@ struct RfParams {
   float* final_state;        // (b, d_inner, N) or null
   void* hs;                  // (b, L, N) h_states in the I/O dtype, or null
   float* hs_part;            // workspace: per-channel-block sums of the states, (b, blocks, L, N)
+  // backward (launch_ssd_rf_bwd): upstream gradients, outputs, and the workspace pieces
+  const void* dy;            // (b, L, d_inner) contiguous, I/O dtype, or null (zero)
+  const void* dhs;           // (b, L, N) contiguous, I/O dtype, or null
+  const float* d_final;      // (b, d_inner, N) or null
+  void* dx;                  // (b, L, d_inner) contiguous, I/O dtype
+  float* ddt;                // (b, L, d_inner) contiguous, w.r.t. the raw dt
+  float* dA;                 // (N,) w.r.t. the rates A
+  void* dB; void* dC;        // (b, L, N) contiguous, I/O dtype
+  float* dD;                 // like D, or null
+  float* d_dt_bias;          // (d_inner,) or null
+  float* dh0;                // (b, d_inner, N) or null
+  float* ckpt;               // workspace: (b, pieces, d_inner, N) the state entering every piece of the sequence
+  float* dB_part; float* dC_part;   // workspace: (b, channel blocks, L, N) sums over a block's channels
+  float* dA_part;            // workspace: (b, channel blocks, N)
+  float* dD_part; float* dbias_part;  // workspace: (b, d_inner) sums over the tokens of one batch row
 };
 bool ssd_rf_supported(int dstate);
 size_t ssd_rf_workspace_bytes(int batch, int seqlen, int d_inner, int dstate, bool h_states);
 hipError_t launch_ssd_rf(const RfParams& p, hipStream_t st);
+// Backward of the reference-form scan: checkpoints (a forward pass), the gradients, fixed-order reductions.
+size_t ssd_rf_bwd_workspace_bytes(int batch, int seqlen, int d_inner, int dstate);
+void ssd_rf_bwd_layout(RfParams& p, void* workspace);
+hipError_t launch_ssd_rf_bwd(const RfParams& p, hipStream_t st);
 
 // h_states of the prefill (ssd_hstates.hip): mean over (h, p) of the state after every token.
 struct HsParams {

@@ -36,6 +36,9 @@ template <int N> constexpr int rf_lpc() { return N >= 32 ? 32 : 16; }
 template <int N> constexpr int rf_ns() { return N / rf_lpc<N>(); }
 template <int N> constexpr int rf_cpb() { return 4 * (64 / rf_lpc<N>()); }
 template <int N> constexpr int rf_tb() { return N <= 128 ? 32 : 16; }
+// Tokens per piece of the backward (the checkpoint spacing): the per-token states and decays of a piece are held in
+// registers, RK * NS of each per lane.
+template <int N> constexpr int rf_rk() { return rf_ns<N>() <= 4 ? 16 : 8; }
 
 // Per-lane token prologue: dt <- clamp(softplus?(dt + bias), dt_min, dt_max).
 __device__ __forceinline__ float rf_dt(const RfParams& p, float raw, float bias) {
@@ -207,7 +210,9 @@ __device__ __forceinline__ void rf_tok(const RfStage<N, TB, CPB>& s, int t, int 
   }
 }
 
-template <typename T, int N, bool GATE>
+// CKPT: the checkpoint pass of the backward, which writes the state entering every piece of rf_rk<N>() tokens
+// (p.ckpt) and no y.
+template <typename T, int N, bool GATE, bool CKPT = false>
 __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
   constexpr int TB = rf_tb<N>(), LPC = rf_lpc<N>(), NS = rf_ns<N>(), CPB = rf_cpb<N>();
   __shared__ RfSmem<N, TB, CPB> sm;
@@ -246,6 +251,16 @@ __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
 #pragma unroll 2
     for (int t = 0; t < TB; ++t) {
       if (t + 1 < TB) rf_tok<N, TB, CPB, NS>(s, t + 1, cl, n0, nxt);
+      if constexpr (CKPT) {
+        constexpr int RK = rf_rk<N>();                     // divides TB: a piece starts where t % RK == 0
+        const int tt = k * TB + t;
+        if (t % RK == 0 && tt < p.seqlen) {
+          const int nsb = (p.seqlen + RK - 1) / RK;
+          float* o = p.ckpt + (((int64_t)b * nsb + tt / RK) * p.d_inner + c) * N + n0;
+#pragma unroll
+          for (int s2 = 0; s2 < NS; ++s2) o[s2] = h[s2];
+        }
+      }
       const float u = cur.dt * cur.x;
       float yp = 0.f;
 #pragma unroll
@@ -254,12 +269,14 @@ __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
         h[s2] = fmaf(a, h[s2], u * cur.b[s2]);
         yp = fmaf(cur.c[s2], h[s2], yp);
       }
-      yp = row_sum16(yp);
-      if constexpr (LPC == 32) yp += dppf<0x142, 0xa>(yp);   // row_bcast:15 -> rows 1, 3: both rows of a channel
-      if (ylane) {
-        float yv = yp + Dc * cur.x;
-        if constexpr (GATE) yv *= silu_f(s.z[t][cl]);
-        ys[t][cl] = yv;
+      if constexpr (!CKPT) {
+        yp = row_sum16(yp);
+        if constexpr (LPC == 32) yp += dppf<0x142, 0xa>(yp);   // row_bcast:15 -> rows 1, 3: both rows of a channel
+        if (ylane) {
+          float yv = yp + Dc * cur.x;
+          if constexpr (GATE) yv *= silu_f(s.z[t][cl]);
+          ys[t][cl] = yv;
+        }
       }
       cur = nxt;
     }
@@ -267,7 +284,7 @@ __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
     if (k + 2 < nblk) rf_load<T, N, TB, CPB, GATE>(p, r, b, c0, (k + 2) * TB);
     __syncthreads();
     // y rows of this block: CPB channels = CPB / 8 pieces of 8 per token
-    if (tid < TB * (CPB / 8)) {
+    if (!CKPT && tid < TB * (CPB / 8)) {
       const int t = tid / (CPB / 8), piece = tid % (CPB / 8);
       const int row = k * TB + t;
       if (row < p.seqlen) {
@@ -277,7 +294,7 @@ __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
       }
     }
   }
-  if (p.final_state) {
+  if (!CKPT && p.final_state) {
     float* fo = p.final_state + ((int64_t)b * p.d_inner + c) * N + n0;
 #pragma unroll
     for (int q = 0; q < NS; ++q) fo[q] = h[q];
@@ -418,6 +435,389 @@ hipError_t launch_rf_n(const RfParams& p, hipStream_t st) {
   }
 }
 
+// ---------------------------------------------------------------- backward
+// With lam_t[c, n] the adjoint of h_t[c, n] (lam after the last token = d_final),
+//     lam_t = dy_t[c] C_t[n] + dhs_t[n] / d_inner + a_{t+1} lam_{t+1},      a_t = exp(A_n dt_t[c]),
+//     dx_t[c]  = dt_t[c] sum_n lam_t B_t[n] + D_c dy_t[c],
+//     ddt_t[c] = (sum_n lam_t A_n a_t h_{t-1} + x_t[c] sum_n lam_t B_t[n]) * d dt / d raw,
+//     dB_t[n]  = sum_c lam_t dt_t[c] x_t[c],      dC_t[n] = sum_c dy_t[c] h_t[c, n],
+//     dA_n     = sum_{t, c} lam_t a_t dt_t[c] h_{t-1},   d h0 = a_0 lam_0,   dD_c = sum_t dy_t[c] x_t[c].
+// Every (c, n) pair follows its own recurrences given the per-token inputs.  The sums over n (dx, ddt) and over c
+// (dB, dC, dA) want opposite layouts, so two kernels walk the sequence backward in pieces of RK tokens from the
+// checkpoints (the state entering each piece, written by the CKPT scan): in each piece the states and decays are
+// recomputed forward into registers, then the adjoint runs backward through them.
+//   rf_bwd_chan_kernel: the scan's layout (a channel's states over LPC lanes, CPB channels per workgroup); the sums
+//     over n on the DPP crossbar; dx, ddt per token, and per (batch, channel) dD, d dt_bias partials and d h0.
+//   rf_bwd_state_kernel: lane = channel (256 per workgroup), 4 states per lane (a workgroup per batch, channel
+//     block and group of 4 states); the sums over c as in rf_hs_kernel; dB, dC per (channel block, token) and dA per
+//     channel block, as partials.
+//   rf_bwd_reduce_kernel / rf_bwd_param_kernel: the partials added in a fixed order (deterministic).
+
+// d dt / d raw for dt = clamp(softplus?(raw + bias), dt_min, dt_max) (the clamp passes the gradient inside its
+// closed range, as torch.clamp does).
+__device__ __forceinline__ float rf_dt_chain(const RfParams& p, float raw, float bias) {
+  const float u = raw + bias;
+  float g = 1.f, v = u;
+  if (p.dt_softplus) {
+    if (u <= 20.f) g = 1.f / (1.f + __expf(-u));
+    v = softplus_f(u);
+  }
+  if (p.has_dt_limit && !(v >= p.dt_min && v <= p.dt_max)) g = 0.f;
+  return g;
+}
+
+template <int N, int RK, int CPB>
+struct RfbChanSmem {
+  float B[RK][N], C[RK][N], G[RK][N];      // G = dhs / d_inner
+  float dt[RK][CPB], chain[RK][CPB], x[RK][CPB], dy[RK][CPB];
+  float dx[RK][CPB], ddt[RK][CPB];
+};
+
+// Piece j's rows into LDS (0 past the end of the sequence).
+template <typename T, int N, int RK, int CPB>
+__device__ void rfb_load_piece(const RfParams& p, RfbChanSmem<N, RK, CPB>& sm, int b, int c0, int t0) {
+  const int tid = threadIdx.x, L = p.seqlen, di = p.d_inner;
+  const T* Bp = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb;
+  const T* Cp = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb;
+  const T* Gp = reinterpret_cast<const T*>(p.dhs) + (int64_t)b * L * N;
+  const float inv = 1.f / (float)di;
+  for (int e = tid; e < RK * N; e += RF_NT) {
+    const int t = e / N, n = e % N, tt = t0 + t;
+    const bool in = tt < L;
+    sm.B[t][n] = in ? to_f32(Bp[(int64_t)tt * p.B_sl + n]) : 0.f;
+    sm.C[t][n] = in ? to_f32(Cp[(int64_t)tt * p.C_sl + n]) : 0.f;
+    sm.G[t][n] = (in && p.dhs) ? to_f32(Gp[(int64_t)tt * N + n]) * inv : 0.f;
+  }
+  for (int e = tid; e < RK * CPB; e += RF_NT) {
+    const int t = e / CPB, cl = e % CPB, tt = t0 + t, c = c0 + cl;
+    const bool in = tt < L;
+    const float raw = in ? p.dt[(int64_t)b * p.dt_sb + (int64_t)tt * p.dt_sl + c] : 0.f;
+    const float bias = p.dt_bias ? p.dt_bias[c] : 0.f;
+    sm.dt[t][cl] = in ? rf_dt(p, raw, bias) : 0.f;
+    sm.chain[t][cl] = in ? rf_dt_chain(p, raw, bias) : 0.f;
+    sm.x[t][cl] = in ? to_f32(reinterpret_cast<const T*>(p.x)[(int64_t)b * p.x_sb + (int64_t)tt * p.x_sl + c]) : 0.f;
+    sm.dy[t][cl] = (in && p.dy) ? to_f32(reinterpret_cast<const T*>(p.dy)[((int64_t)b * L + tt) * di + c]) : 0.f;
+  }
+}
+
+template <typename T, int N>
+__global__ __launch_bounds__(RF_NT) void rf_bwd_chan_kernel(RfParams p) {
+  constexpr int LPC = rf_lpc<N>(), NS = rf_ns<N>(), CPB = rf_cpb<N>(), RK = rf_rk<N>();
+  __shared__ RfbChanSmem<N, RK, CPB> sm;
+  const int nper = p.d_inner / CPB;
+  const int b = blockIdx.x / nper, c0 = (blockIdx.x % nper) * CPB;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int cl = (64 / LPC) * w + lane / LPC, g = lane % LPC;
+  const int c = c0 + cl, n0 = g * NS, L = p.seqlen, di = p.d_inner;
+  const bool ylane = g == LPC - 1;   // holds the channel's sums over n after the row sums (as in the scan)
+  const int nsb = (L + RK - 1) / RK;
+  float k2[NS], As[NS], lamc[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    As[s] = p.A[n0 + s];
+    k2[s] = As[s] * LOG2E;
+    lamc[s] = p.d_final ? p.d_final[((int64_t)b * di + c) * N + n0 + s] : 0.f;
+  }
+  const float Dc = p.D ? (p.D_per_channel ? p.D[c] : p.D[c / p.headdim]) : 0.f;
+  float dD_acc = 0.f, db_acc = 0.f;
+  for (int j = nsb - 1; j >= 0; --j) {
+    const int t0 = j * RK;
+    __syncthreads();                   // the previous piece's LDS no longer read
+    rfb_load_piece<T, N, RK, CPB>(p, sm, b, c0, t0);
+    float h[NS];
+    {
+      const float* ck = p.ckpt + (((int64_t)b * nsb + j) * di + c) * N + n0;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) h[s] = ck[s];
+    }
+    __syncthreads();
+    // forward through the piece: the state before every token and every decay
+    float hp[RK][NS], av[RK][NS];
+#pragma unroll
+    for (int t = 0; t < RK; ++t) {
+      const float dtv = sm.dt[t][cl], u = dtv * sm.x[t][cl];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const float a = __builtin_amdgcn_exp2f(dtv * k2[s]);
+        hp[t][s] = h[s];
+        av[t][s] = a;
+        h[s] = fmaf(a, h[s], u * sm.B[t][n0 + s]);
+      }
+    }
+    // backward through it
+#pragma unroll
+    for (int t = RK - 1; t >= 0; --t) {
+      const float dyv = sm.dy[t][cl];
+      float du = 0.f, qq = 0.f;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const float lam = lamc[s] + dyv * sm.C[t][n0 + s] + sm.G[t][n0 + s];
+        du = fmaf(lam, sm.B[t][n0 + s], du);
+        qq = fmaf(lam * As[s], av[t][s] * hp[t][s], qq);
+        lamc[s] = av[t][s] * lam;
+      }
+      du = row_sum16(du);
+      qq = row_sum16(qq);
+      if constexpr (LPC == 32) {
+        du += dppf<0x142, 0xa>(du);
+        qq += dppf<0x142, 0xa>(qq);
+      }
+      if (ylane) {
+        const float dtv = sm.dt[t][cl], xv = sm.x[t][cl];
+        const float ddr = (qq + xv * du) * sm.chain[t][cl];
+        sm.dx[t][cl] = dtv * du + Dc * dyv;
+        sm.ddt[t][cl] = ddr;
+        dD_acc = fmaf(dyv, xv, dD_acc);
+        db_acc += ddr;
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < RK * CPB; e += RF_NT) {
+      const int t = e / CPB, q = e % CPB, tt = t0 + t;
+      if (tt < L) {
+        const int64_t o = ((int64_t)b * L + tt) * di + c0 + q;
+        reinterpret_cast<T*>(p.dx)[o] = from_f32<T>(sm.dx[t][q]);
+        p.ddt[o] = sm.ddt[t][q];
+      }
+    }
+  }
+  if (p.dh0) {
+    float* o = p.dh0 + ((int64_t)b * di + c) * N + n0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) o[s] = lamc[s];
+  }
+  if (ylane) {
+    p.dD_part[(int64_t)b * di + c] = dD_acc;
+    p.dbias_part[(int64_t)b * di + c] = db_acc;
+  }
+}
+
+// lane = channel, states n0 .. n0 + 3 of group gs; the piece's B, C and dhs of those states in LDS.
+template <typename T, int N>
+__global__ __launch_bounds__(RF_NT) void rf_bwd_state_kernel(RfParams p) {
+  constexpr int RK = rf_rk<N>();
+  __shared__ float4 sB[RK], sC[RK], sG[RK];
+  __shared__ float red[4][RK][2 * HS_NS];
+  const int L = p.seqlen, di = p.d_inner;
+  const int ncb = (di + HS_CPB - 1) / HS_CPB, ngs = N / HS_NS;
+  const int i = blockIdx.x;
+  const int gs = i % ngs, cblk = (i / ngs) % ncb, b = i / (ngs * ncb);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int c = cblk * HS_CPB + tid;
+  const bool on = c < di;
+  const int cc = on ? c : di - 1;
+  const int n0 = gs * HS_NS, nsb = (L + RK - 1) / RK;
+  const bool u32 = lane & 32, u16 = lane & 16;
+  float k2[HS_NS], As[HS_NS], lamc[HS_NS], dA_acc[HS_NS];
+#pragma unroll
+  for (int s = 0; s < HS_NS; ++s) {
+    As[s] = p.A[n0 + s];
+    k2[s] = As[s] * LOG2E;
+    lamc[s] = (on && p.d_final) ? p.d_final[((int64_t)b * di + c) * N + n0 + s] : 0.f;
+    dA_acc[s] = 0.f;
+  }
+  const float bias = p.dt_bias ? p.dt_bias[cc] : 0.f;
+  const float inv = 1.f / (float)di;
+  float* dBp = p.dB_part + ((int64_t)b * ncb + cblk) * L * N + n0;
+  float* dCp = p.dC_part + ((int64_t)b * ncb + cblk) * L * N + n0;
+  for (int j = nsb - 1; j >= 0; --j) {
+    const int t0 = j * RK;
+    __syncthreads();                   // the previous piece's LDS no longer read
+    if (tid < RK) {
+      const int tt = t0 + tid;
+      float4 bv = {0.f, 0.f, 0.f, 0.f}, cv = bv, gv = bv;
+      if (tt < L) {
+        const T* bp = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)tt * p.B_sl + n0;
+        const T* cp = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb + (int64_t)tt * p.C_sl + n0;
+        bv = float4{to_f32(bp[0]), to_f32(bp[1]), to_f32(bp[2]), to_f32(bp[3])};
+        cv = float4{to_f32(cp[0]), to_f32(cp[1]), to_f32(cp[2]), to_f32(cp[3])};
+        if (p.dhs) {
+          const T* gp = reinterpret_cast<const T*>(p.dhs) + ((int64_t)b * L + tt) * N + n0;
+          gv = float4{to_f32(gp[0]) * inv, to_f32(gp[1]) * inv, to_f32(gp[2]) * inv, to_f32(gp[3]) * inv};
+        }
+      }
+      sB[tid] = bv;
+      sC[tid] = cv;
+      sG[tid] = gv;
+    }
+    float dtv[RK], xv[RK], dyv[RK];
+#pragma unroll
+    for (int t = 0; t < RK; ++t) {
+      const int tt = min(t0 + t, L - 1);
+      const bool in = on && t0 + t < L;
+      const float raw = p.dt[(int64_t)b * p.dt_sb + (int64_t)tt * p.dt_sl + cc];
+      const float xr = to_f32(reinterpret_cast<const T*>(p.x)[(int64_t)b * p.x_sb + (int64_t)tt * p.x_sl + cc]);
+      const float dr = p.dy ? to_f32(reinterpret_cast<const T*>(p.dy)[((int64_t)b * L + tt) * di + cc]) : 0.f;
+      dtv[t] = in ? rf_dt(p, raw, bias) : 0.f;
+      xv[t] = in ? xr : 0.f;
+      dyv[t] = in ? dr : 0.f;
+    }
+    float h[HS_NS];
+    {
+      const float4 hv = *reinterpret_cast<const float4*>(p.ckpt + (((int64_t)b * nsb + j) * di + cc) * N + n0);
+      h[0] = hv.x; h[1] = hv.y; h[2] = hv.z; h[3] = hv.w;
+    }
+    __syncthreads();
+    // forward through the piece: the state after every token (hs[t]) and every decay; hs[-1] = the entry state
+    float he[HS_NS], hs[RK][HS_NS], av[RK][HS_NS];
+#pragma unroll
+    for (int s = 0; s < HS_NS; ++s) he[s] = h[s];
+#pragma unroll
+    for (int t = 0; t < RK; ++t) {
+      const float4 b4 = sB[t];
+      const float bb[HS_NS] = {b4.x, b4.y, b4.z, b4.w};
+      const float u = dtv[t] * xv[t];
+#pragma unroll
+      for (int s = 0; s < HS_NS; ++s) {
+        const float a = __builtin_amdgcn_exp2f(dtv[t] * k2[s]);
+        av[t][s] = a;
+        h[s] = fmaf(a, h[s], u * bb[s]);
+        hs[t][s] = h[s];
+      }
+    }
+#pragma unroll
+    for (int t = RK - 1; t >= 0; --t) {
+      const float4 c4 = sC[t], g4 = sG[t];
+      const float cv[HS_NS] = {c4.x, c4.y, c4.z, c4.w}, gv[HS_NS] = {g4.x, g4.y, g4.z, g4.w};
+      const float dx_ = dtv[t] * xv[t];
+      float vb[HS_NS], vc[HS_NS];
+#pragma unroll
+      for (int s = 0; s < HS_NS; ++s) {
+        const float lam = lamc[s] + dyv[t] * cv[s] + gv[s];
+        const float hprev = t > 0 ? hs[t - 1][s] : he[s];
+        vb[s] = lam * dx_;
+        vc[s] = dyv[t] * hs[t][s];
+        dA_acc[s] = fmaf(lam * av[t][s], dtv[t] * hprev, dA_acc[s]);
+        lamc[s] = av[t][s] * lam;
+      }
+      // reduce-scatter of each 4-vector over the wave (as in rf_hs_kernel): row r of lanes holds state r
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const float* v = q ? vc : vb;
+        float v2[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 2]), false,
+                                                           false);
+          v2[k] = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+        }
+        const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(v2[0]), __float_as_uint(v2[1]), false, false);
+        float v1 = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+        v1 = row_sum16(v1);
+        if ((lane & 15) == 0) red[w][t][HS_NS * q + 2 * (int)u32 + (int)u16] = v1;
+      }
+    }
+    __syncthreads();
+    if (tid < RK * 2 * HS_NS) {
+      const int t = tid / (2 * HS_NS), k = tid % (2 * HS_NS), tt = t0 + t;
+      if (tt < L) {
+        const float v = red[0][t][k] + red[1][t][k] + red[2][t][k] + red[3][t][k];
+        (k < HS_NS ? dBp : dCp)[(int64_t)tt * N + (k % HS_NS)] = v;
+      }
+    }
+  }
+  // dA over the workgroup's channels: the same reduce-scatter, then the 4 waves in order
+  {
+    float v2[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(dA_acc[k]), __float_as_uint(dA_acc[k + 2]),
+                                                       false, false);
+      v2[k] = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+    }
+    const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(v2[0]), __float_as_uint(v2[1]), false, false);
+    float v1 = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+    v1 = row_sum16(v1);
+    __syncthreads();
+    if ((lane & 15) == 0) red[w][0][2 * (int)u32 + (int)u16] = v1;
+    __syncthreads();
+    if (tid < HS_NS)
+      p.dA_part[((int64_t)b * ncb + cblk) * N + n0 + tid] = red[0][0][tid] + red[1][0][tid] + red[2][0][tid] +
+                                                            red[3][0][tid];
+  }
+}
+
+// dB, dC (b, L, N) = the channel blocks' partials added in order.
+template <typename T>
+__global__ __launch_bounds__(256) void rf_bwd_reduce_kernel(RfParams p) {
+  const int ncb = (p.d_inner + HS_CPB - 1) / HS_CPB;
+  const int64_t per = (int64_t)p.seqlen * p.dstate;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)p.batch * per) return;
+  const int64_t b = i / per, r = i % per;
+  float sb = 0.f, sc = 0.f;
+  for (int k = 0; k < ncb; ++k) {
+    sb += p.dB_part[(b * ncb + k) * per + r];
+    sc += p.dC_part[(b * ncb + k) * per + r];
+  }
+  reinterpret_cast<T*>(p.dB)[i] = from_f32<T>(sb);
+  reinterpret_cast<T*>(p.dC)[i] = from_f32<T>(sc);
+}
+
+// dA (N), dD (like D) and d dt_bias (d_inner): partials added over batch rows (and channel blocks) in order.
+__global__ __launch_bounds__(256) void rf_bwd_param_kernel(RfParams p) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int di = p.d_inner, N = p.dstate, ncb = (di + HS_CPB - 1) / HS_CPB;
+  if (i < N) {
+    float s = 0.f;
+    for (int k = 0; k < p.batch * ncb; ++k) s += p.dA_part[(int64_t)k * N + i];
+    p.dA[i] = s;
+  }
+  if (i < di) {
+    float sd = 0.f, sb = 0.f;
+    for (int b = 0; b < p.batch; ++b) {
+      sd += p.dD_part[(int64_t)b * di + i];
+      sb += p.dbias_part[(int64_t)b * di + i];
+    }
+    if (p.d_dt_bias) p.d_dt_bias[i] = sb;
+    if (p.dD && p.D_per_channel) p.dD[i] = sd;
+  }
+  if (p.dD && !p.D_per_channel && i < di / p.headdim) {     // D per head: its channels' sums
+    float sd = 0.f;
+    for (int b = 0; b < p.batch; ++b)
+      for (int q = 0; q < p.headdim; ++q) sd += p.dD_part[(int64_t)b * di + i * p.headdim + q];
+    p.dD[i] = sd;
+  }
+}
+
+template <typename T, int N>
+hipError_t launch_rf_bwd_t(const RfParams& p, hipStream_t st) {
+  const int nblk = p.batch * (p.d_inner / rf_cpb<N>());
+  if (p.seqlen > 0) {
+    hipLaunchKernelGGL((rf_scan_kernel<T, N, false, true>), dim3(nblk), dim3(RF_NT), 0, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((rf_bwd_chan_kernel<T, N>), dim3(nblk), dim3(RF_NT), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int ncb = (p.d_inner + HS_CPB - 1) / HS_CPB;
+  hipLaunchKernelGGL((rf_bwd_state_kernel<T, N>), dim3(p.batch * ncb * (N / HS_NS)), dim3(RF_NT), 0, st, p);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t tot = (int64_t)p.batch * p.seqlen * N;
+  if (tot > 0) {
+    hipLaunchKernelGGL((rf_bwd_reduce_kernel<T>), dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const int np = p.d_inner > N ? p.d_inner : N;
+  hipLaunchKernelGGL(rf_bwd_param_kernel, dim3((unsigned)((np + 255) / 256)), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_rf_bwd_n(const RfParams& p, hipStream_t st) {
+  switch (p.dstate) {
+    case 16: return launch_rf_bwd_t<T, 16>(p, st);
+    case 32: return launch_rf_bwd_t<T, 32>(p, st);
+    case 64: return launch_rf_bwd_t<T, 64>(p, st);
+    case 128: return launch_rf_bwd_t<T, 128>(p, st);
+    case 256: return launch_rf_bwd_t<T, 256>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
 
 bool ssd_rf_supported(int dstate) {
@@ -433,6 +833,39 @@ size_t ssd_rf_workspace_bytes(int batch, int seqlen, int d_inner, int dstate, bo
 hipError_t launch_ssd_rf(const RfParams& p, hipStream_t st) {
   if (p.dtype == DT_BF16) return launch_rf_n<bf16>(p, st);
   return launch_rf_n<float>(p, st);
+}
+
+// Backward workspace: the checkpoints (b, pieces, d_inner, N), the dB and dC partials (b, channel blocks, L, N),
+// the dA partials (b, channel blocks, N), and the dD / d dt_bias partials (b, d_inner), all fp32.
+static size_t rf_rk_of(int dstate) { return dstate == 256 ? 8 : 16; }
+
+size_t ssd_rf_bwd_workspace_bytes(int batch, int seqlen, int d_inner, int dstate) {
+  const size_t rk = rf_rk_of(dstate), nsb = (seqlen + rk - 1) / rk;
+  const size_t ncb = (size_t)(d_inner + HS_CPB - 1) / HS_CPB;
+  return align256((size_t)batch * nsb * d_inner * dstate * 4) + 2 * align256((size_t)batch * ncb * seqlen * dstate * 4) +
+         align256((size_t)batch * ncb * dstate * 4) + 2 * align256((size_t)batch * d_inner * 4);
+}
+
+void ssd_rf_bwd_layout(RfParams& p, void* workspace) {
+  const size_t rk = rf_rk_of(p.dstate), nsb = (p.seqlen + rk - 1) / rk;
+  const size_t ncb = (size_t)(p.d_inner + HS_CPB - 1) / HS_CPB;
+  char* w = reinterpret_cast<char*>(workspace);
+  p.ckpt = reinterpret_cast<float*>(w);
+  w += align256((size_t)p.batch * nsb * p.d_inner * p.dstate * 4);
+  p.dB_part = reinterpret_cast<float*>(w);
+  w += align256((size_t)p.batch * ncb * p.seqlen * p.dstate * 4);
+  p.dC_part = reinterpret_cast<float*>(w);
+  w += align256((size_t)p.batch * ncb * p.seqlen * p.dstate * 4);
+  p.dA_part = reinterpret_cast<float*>(w);
+  w += align256((size_t)p.batch * ncb * p.dstate * 4);
+  p.dD_part = reinterpret_cast<float*>(w);
+  w += align256((size_t)p.batch * p.d_inner * 4);
+  p.dbias_part = reinterpret_cast<float*>(w);
+}
+
+hipError_t launch_ssd_rf_bwd(const RfParams& p, hipStream_t st) {
+  if (p.dtype == DT_BF16) return launch_rf_bwd_n<bf16>(p, st);
+  return launch_rf_bwd_n<float>(p, st);
 }
 
 }  // namespace mh

@@ -939,14 +939,13 @@ def selective_scan_reference(x, dt, A, B, C, D, return_h_states=False, return_fi
     log-rates A_log (N,) clamped to [-5, 5] as in :87, B, C (b, L, N), D (d_inner,) or None.  Returns y, or a tuple
     (y, h_states (b, L, N) in the dtype of x, final_state (b, d_inner, N) float32) as requested (:121-130).
     ``initial_state`` (b, d_inner, N) seeds the state (the reference starts at zero); ``z`` (b, L, d_inner) applies
-    the block's gate y * silu(z) (mamba2.py:337-338) in the kernel.  x / B / C / z bf16 or fp32 (y in that dtype),
-    state and arithmetic fp32.  Forward only (no autograd)."""
+    the block's gate y * silu(z) (mamba2.py:337-338), in the kernel without autograd.  x / B / C / z bf16 or fp32
+    (y in that dtype), state and arithmetic fp32.  Differentiable: under autograd the backward is
+    ``mh_ssd_ref_scan_bwd`` (A_log's gradient passes through the clamp and the exponential in torch) and the gate's
+    ``mh_silu_gate_bwd``."""
     _require_cuda("selective_scan_reference", x, dt, A, B, C, D, initial_state, dt_bias, z)
     if x.dim() != 3 or dt.shape != x.shape:
         raise ValueError("selective_scan_reference: x and dt must be (batch, seqlen, d_inner)")
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, dt, A, B, C, D, initial_state, z)):
-        raise NotImplementedError("selective_scan_reference: no backward in this build (the per-head selective_scan "
-                                  "is the differentiable path)")
     b, L, di = x.shape
     if B.dim() == 4:
         B, C = B.squeeze(2), C.squeeze(2)
@@ -959,6 +958,8 @@ def selective_scan_reference(x, dt, A, B, C, D, return_h_states=False, return_fi
     if P is None:
         raise ValueError("selective_scan_reference: d_inner must be a multiple of 16")
     H = di // P
+    if D is not None and D.numel() != di:
+        raise ValueError("selective_scan_reference: D must have d_inner entries")
     dt32 = _inner_contig(dt.to(torch.float32))
     if dt32.stride(1) % 4 or dt32.stride(0) % 4:
         dt32 = dt32.contiguous()
@@ -969,25 +970,19 @@ def selective_scan_reference(x, dt, A, B, C, D, return_h_states=False, return_fi
     D32 = _f32c(D)
     h0 = None if initial_state is None else initial_state.to(torch.float32).reshape(b, di, N).contiguous()
     bias32 = _f32c(dt_bias)
+    zc = None if z is None else _inner_contig(z.to(x.dtype))
+    cfg = (dt_softplus, dt_limit, H, P)
+    if not _plan_only and torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (xc, dt32, rates, Bc, Cc, D32, h0, bias32, zc)):
+        y, hs, fin = _RefScanFn.apply(xc, dt32, rates, Bc, Cc, D32, h0, bias32, cfg, return_h_states)
+        if zc is not None:
+            y = _GateFn.apply(y.view(b, L, H, P), zc.view(b, L, H, P)).view(b, L, di)
+        out = [y] + ([hs] if return_h_states else []) + ([fin] if return_final_state else [])
+        return out[0] if len(out) == 1 else tuple(out)
     y = torch.empty((b, L, di), device=x.device, dtype=x.dtype)
     fin = torch.empty((b, di, N), device=x.device, dtype=torch.float32) if return_final_state else None
     hs = torch.empty((b, L, N), device=x.device, dtype=x.dtype) if return_h_states else None
-    zc = None if z is None else _inner_contig(z.to(x.dtype))
-    a = _ssd_args(xc.view(b, L, H, P), dt32, rates, Bc.view(b, L, 1, N), Cc.view(b, L, 1, N), None, bias32,
-                  dt_softplus, dt_limit, h0, y.view(b, L, H, P), fin, None,
-                  None if zc is None else zc.view(b, L, H, P))
-    flags = a.flags | _lib.MH_A_PER_STATE | _lib.MH_DT_PER_CHANNEL
-    if D32 is not None:
-        a.D = _ptr(D32)
-        if D32.numel() == di:
-            flags |= _lib.MH_D_PER_CHANNEL
-        elif D32.numel() != H:
-            raise ValueError("selective_scan_reference: D must have d_inner entries")
-    a.flags = flags
-    # the (b, L, d_inner) rows: strides of the flattened channel axis
-    a.x_stride_h = a.y_stride_h = P
-    if zc is not None:
-        a.z_stride_h = P
+    a = _ref_args(xc, dt32, rates, Bc, Cc, D32, h0, bias32, cfg, y, fin, zc)
     n = ct.c_size_t()
     _lib.call("mh_ssd_ref_scan_workspace_bytes", ct.byref(a), int(return_h_states), ct.byref(n))
     ws = torch.empty(max(n.value, 1), device=x.device, dtype=torch.uint8) if n.value else None
@@ -1002,6 +997,80 @@ def selective_scan_reference(x, dt, A, B, C, D, return_h_states=False, return_fi
     if return_final_state:
         out.append(fin)
     return out[0] if len(out) == 1 else tuple(out)
+
+
+def _ref_args(xc, dt32, rates, Bc, Cc, D32, h0, bias32, cfg, y, fin, zc):
+    """``mh_ssd_args`` of the reference-form scan: (b, L, d_inner) rows seen as H heads of P channels."""
+    dt_softplus, dt_limit, H, P = cfg
+    b, L, di = xc.shape
+    N = rates.shape[0]
+    a = _ssd_args(xc.view(b, L, H, P), dt32, rates, Bc.view(b, L, 1, N), Cc.view(b, L, 1, N), None, bias32,
+                  dt_softplus, dt_limit, h0, (xc if y is None else y).view(b, L, H, P), fin, None,
+                  None if zc is None else zc.view(b, L, H, P))
+    flags = a.flags | _lib.MH_A_PER_STATE | _lib.MH_DT_PER_CHANNEL
+    if D32 is not None:
+        a.D = _ptr(D32)
+        if D32.numel() == di:
+            flags |= _lib.MH_D_PER_CHANNEL
+    a.flags = flags
+    # the (b, L, d_inner) rows: strides of the flattened channel axis
+    a.x_stride_h = a.y_stride_h = P
+    if zc is not None:
+        a.z_stride_h = P
+    return a
+
+
+class _RefScanFn(torch.autograd.Function):
+    """Autograd node of the reference-form scan: forward ``mh_ssd_ref_scan_fwd`` (y ungated, h_states when asked,
+    the final state), backward ``mh_ssd_ref_scan_bwd`` (every gradient, w.r.t. the rates A; torch chains A_log)."""
+
+    @staticmethod
+    def forward(ctx, xc, dt32, rates, Bc, Cc, D32, h0, bias32, cfg, want_hs):
+        b, L, di = xc.shape
+        N = rates.shape[0]
+        y = torch.empty((b, L, di), device=xc.device, dtype=xc.dtype)
+        fin = torch.empty((b, di, N), device=xc.device, dtype=torch.float32)
+        hs = torch.empty((b, L, N), device=xc.device, dtype=xc.dtype) if want_hs else None
+        a = _ref_args(xc, dt32, rates, Bc, Cc, D32, h0, bias32, cfg, y, fin, None)
+        n = ct.c_size_t()
+        _lib.call("mh_ssd_ref_scan_workspace_bytes", ct.byref(a), int(want_hs), ct.byref(n))
+        ws = torch.empty(max(n.value, 1), device=xc.device, dtype=torch.uint8) if n.value else None
+        a.workspace, a.workspace_bytes = _ptr(ws), n.value
+        _lib.call("mh_ssd_ref_scan_fwd", ct.byref(a), _ptr(hs), _stream(xc.device))
+        ctx.save_for_backward(xc, dt32, rates, Bc, Cc, D32, h0, bias32)
+        ctx.cfg = cfg
+        ctx.set_materialize_grads(False)
+        return y, hs, fin
+
+    @staticmethod
+    def backward(ctx, dy, dhs, dfin):
+        xc, dt32, rates, Bc, Cc, D32, h0, bias32 = ctx.saved_tensors
+        b, L, di = xc.shape
+        N = rates.shape[0]
+        dev = xc.device
+        g = _lib.SsdRefBwdArgs()
+        g.fwd = _ref_args(xc, dt32, rates, Bc, Cc, D32, h0, bias32, ctx.cfg, None, None, None)
+        dy = None if dy is None else dy.to(xc.dtype).contiguous()
+        dhs = None if dhs is None else dhs.to(xc.dtype).contiguous()
+        dfin = None if dfin is None else dfin.to(torch.float32).contiguous()
+        dx = torch.empty((b, L, di), device=dev, dtype=xc.dtype)
+        ddt = torch.empty((b, L, di), device=dev, dtype=torch.float32)
+        dA = torch.empty((N,), device=dev, dtype=torch.float32)
+        dB = torch.empty((b, L, N), device=dev, dtype=xc.dtype)
+        dC = torch.empty((b, L, N), device=dev, dtype=xc.dtype)
+        dD = None if D32 is None else torch.empty_like(D32)
+        dbias = None if bias32 is None else torch.empty_like(bias32)
+        need_dh0 = h0 is not None and ctx.needs_input_grad[6]
+        dh0 = torch.empty((b, di, N), device=dev, dtype=torch.float32) if need_dh0 else None
+        g.dy, g.dhs, g.d_final_state = _ptr(dy), _ptr(dhs), _ptr(dfin)
+        g.dx, g.ddt, g.dA, g.dB, g.dC = _ptr(dx), _ptr(ddt), _ptr(dA), _ptr(dB), _ptr(dC)
+        g.dD, g.d_dt_bias, g.d_initial_state = _ptr(dD), _ptr(dbias), _ptr(dh0)
+        n = ct.c_size_t()
+        _lib.call("mh_ssd_ref_scan_bwd_workspace_bytes", ct.byref(g), ct.byref(n))
+        ws = torch.empty(max(n.value, 16), device=dev, dtype=torch.uint8)
+        g.workspace, g.workspace_bytes = _ptr(ws), n.value
+        _lib.call("mh_ssd_ref_scan_bwd", ct.byref(g), _stream(dev))
+        return dx, ddt, dA, dB, dC, dD, dh0, dbias, None, None
 
 
 class _RefScanPlan(Plan):

@@ -534,3 +534,51 @@ def test_scan_bwd_dx_rows_alignment():
     assert _rc("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == 0
     a.dx_rows = ct.c_void_p(4097)
     assert _rc("mh_ssd_bwd_workspace_bytes", ct.byref(a), ct.byref(n)) == -5
+
+
+def _good_ref():
+    """Arguments of the reference-form scan: (b, L, d_inner) rows as H heads of P channels, one B / C group, dt per
+    channel, A per state."""
+    a = SsdArgs()
+    b, L, H, P, N = 2, 100, 4, 16, 32
+    di = H * P
+    a.batch, a.seqlen, a.nheads, a.headdim, a.dstate, a.ngroups = b, L, H, P, N, 1
+    a.dtype = _lib.MH_BF16
+    a.flags = _lib.MH_A_PER_STATE | _lib.MH_DT_PER_CHANNEL
+    fake = ct.c_void_p(4096)
+    a.x = a.B = a.C = a.y = a.dt = a.A = fake
+    a.x_stride_h = a.y_stride_h = P
+    a.x_stride_l = a.y_stride_l = a.dt_stride_l = di
+    a.x_stride_b = a.y_stride_b = a.dt_stride_b = L * di
+    a.B_stride_l = a.C_stride_l = N
+    a.B_stride_b = a.C_stride_b = L * N
+    return a
+
+
+def test_ref_scan_bwd_validation_and_workspace():
+    g = _lib.SsdRefBwdArgs()
+    g.fwd = _good_ref()
+    fake = ct.c_void_p(4096)
+    g.dy = g.dx = g.ddt = g.dA = g.dB = g.dC = fake
+    n = ct.c_size_t()
+    assert _rc("mh_ssd_ref_scan_bwd_workspace_bytes", ct.byref(g), ct.byref(n)) == 0
+    # the state at every 16th token (b, ceil(L / 16), d_inner, N) fp32 plus the channel-block partials
+    b, L, di, N = 2, 100, 64, 32
+    assert n.value >= 4 * (b * -(-L // 16) * di * N + 2 * b * L * N + b * N + 2 * b * di)
+    g.fwd.z = fake                                   # the gate's backward is mh_silu_gate_bwd
+    assert _rc("mh_ssd_ref_scan_bwd_workspace_bytes", ct.byref(g), ct.byref(n)) == -6
+    g.fwd.z = None
+    g.dA = None
+    assert _rc("mh_ssd_ref_scan_bwd", ct.byref(g), None) == -1
+    g.dA = fake
+    g.fwd.D = fake                                   # dD required with D
+    assert _rc("mh_ssd_ref_scan_bwd", ct.byref(g), None) == -1
+    g.fwd.D = None
+    g.dx = ct.c_void_p(4097)                         # bf16 elements: 2-byte alignment
+    assert _rc("mh_ssd_ref_scan_bwd", ct.byref(g), None) == -5
+    g.dx = fake
+    g.workspace, g.workspace_bytes = fake, 16
+    assert _rc("mh_ssd_ref_scan_bwd", ct.byref(g), None) == -7
+    g.fwd.flags = 0                                  # the head form is not the reference form
+    assert _rc("mh_ssd_ref_scan_bwd_workspace_bytes", ct.byref(g), ct.byref(n)) < 0
+    assert b"reference form" in _lib.lib().mh_last_error()

@@ -8,7 +8,7 @@ Cases: several (d_inner, N) including the 1b preset width (d_inner 2048, N 128),
 D, h_states and the final state, an initial state (through a split sequence: the second half started from the
 first half's final state equals the whole), dt's bias / softplus / clamp prologue in the kernel, the z-gate,
 an empty sequence, and the full 1b-preset shape (b 2, L 4096) through exact linearity in x and the split
-sequence.
+sequence.  The backward is in tests/test_gpu_ssd_refform_bwd.py.
 """
 
 import numpy as np
@@ -130,9 +130,9 @@ def test_ref_scan_empty_sequence_and_errors():
     with pytest.raises(MHError):                       # dstate 8: outside what the kernel tiles
         mh.selective_scan_reference(x, x, torch.zeros(8, device="cuda"), torch.zeros(1, 4, 8, device="cuda"),
                                     torch.zeros(1, 4, 8, device="cuda"), None)
-    with pytest.raises(NotImplementedError):
-        mh.selective_scan_reference(x.requires_grad_(), x, torch.zeros(16, device="cuda"),
-                                    torch.zeros(1, 4, 16, device="cuda"), torch.zeros(1, 4, 16, device="cuda"), None)
+    with pytest.raises(ValueError):                    # D per channel only (the reference's (d_inner,))
+        mh.selective_scan_reference(x, x, torch.zeros(16, device="cuda"), torch.zeros(1, 4, 16, device="cuda"),
+                                    torch.zeros(1, 4, 16, device="cuda"), torch.ones(2, device="cuda"))
 
 
 def test_ref_scan_1b_preset_full_shape_properties():
