@@ -96,6 +96,11 @@ __device__ __forceinline__ Frag<TM> acc_to_frag_scaled(const f32x16& acc, int c,
 
 // ---------------------------------------------------------------- wave helpers
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// v from the lane the DPP control CTRL selects (rows in ROWS; every lane of the selected rows active).
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dppf(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, false));
+}
 // The lane index recomputed where it is used (v_mbcnt in a volatile asm): address arithmetic built on it is not
 // hoisted out of loops, where it would hold registers for the whole loop.
 __device__ __forceinline__ int lane_id_here() {

@@ -53,12 +53,25 @@ __device__ void hs_prologue_elems(const SsdParams& p, Smem& sm, int b, int si, i
   const float* bias = p.dt_bias ? p.dt_bias : p.A;       // any valid per-head array when there is no bias
   const float bmul = p.dt_bias ? 1.f : 0.f;
   constexpr int KB = 8;
+  // element e = tid + nt i is (t, h) = (e / H, e % H), stepped by (nt / H, nt % H) without a division per element
+  const int dq = nt / H, dr = nt % H;
+  int te = tid / H, he = tid % H;
   for (int base = 0; base < tot; base += KB * nt) {
     float d[KB], av[KB], bv[KB];
     f32x2 xv[KB];
+    int tk[KB], hk[KB];
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
-      const int e = min(base + tid + k * nt, tot - 1), t = e / H, h = e % H, tc = min(t, len - 1);
+      const bool past = te >= HS_SEG;                     // e >= tot: repeat the last element
+      tk[k] = past ? HS_SEG - 1 : te;
+      hk[k] = past ? H - 1 : he;
+      he += dr;
+      te += dq;
+      if (he >= H) {
+        he -= H;
+        ++te;
+      }
+      const int t = tk[k], h = hk[k], tc = min(t, len - 1);
       d[k] = dtb[(tok0 + tc) * p.dt_sl + h];
       av[k] = p.A[h];
       bv[k] = bias[h];
@@ -67,7 +80,7 @@ __device__ void hs_prologue_elems(const SsdParams& p, Smem& sm, int b, int si, i
     __builtin_amdgcn_sched_barrier(0);  // every load of the pass issued before the first use
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
-      const int e = min(base + tid + k * nt, tot - 1), t = e / H, h = e % H;
+      const int t = tk[k], h = hk[k];
       float x = d[k] + bv[k] * bmul;
       if (p.dt_softplus) x = softplus_f(x);
       if (p.has_dt_limit) x = fminf(fmaxf(x, p.dt_min), p.dt_max);
@@ -463,59 +476,97 @@ __global__ __launch_bounds__(64 * HSB_WAVES_LOC) void ssd_hsb_local_kernel(SsdPa
   if (tid < H) q.dec[((int64_t)b * p.nseg + si) * H + tid] = __expf(sm.cend[tid]);
 }
 
-// Both carries of one (batch, head, column): forward Zin_{k+1} = dec_k Zin_k + Zloc_k from the summed initial
-// state, backward Lam_{k-1} = dec_k Lam_k + GL_k from Lam_last = 0; 16 segments of each chain loaded together.
+// Both carries of the chains (batch, head, column), as two-level scans like the forward's: the forward
+// Zin_{k+1} = dec_k Zin_k + Zloc_k from the summed initial state, written over Zloc, and the adjoint handed into
+// each segment from the right, Lam_{k-1} = dec_k Lam_k + GL_k from Lam = 0 past the last segment, written over GL;
+// finally d h0 = the adjoint left of segment 0 in every row p.  Lane j * CW + i holds part j (NP parts of
+// consecutive segments) of the wave's chain i; each part is reduced in both directions from registers, the parts
+// before it (forward) and after it (adjoint) are folded across the wave, and the part is walked again.
+template <int NP>
 __global__ __launch_bounds__(256) void ssd_hsb_carry_kernel(SsdParams p, HsParams q, float* dh0) {
-  const int H = p.nheads, N = p.dstate, P = p.headdim, ns = p.nseg;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)p.batch * H * N) return;
-  const int n = (int)(i % N), h = (int)((i / N) % H), b = (int)(i / ((int64_t)N * H));
-  float Z = 0.f;
-  if (p.init_state) {
-    const float* s0 = p.init_state + (((int64_t)b * H + h) * P) * N + n;
-    for (int k = 0; k < P; ++k) Z += s0[(int64_t)k * N];
-  }
+  constexpr int CW = 64 / NP, KB = 16;
+  const int H = p.nheads, N = p.dstate, P = p.headdim, ns = p.nseg, l = lane_id();
+  const int part = l / CW, ci = l % CW;
+  const int64_t chain = ((int64_t)blockIdx.x * 4 + wave_id()) * CW + ci;
+  const bool on = chain < (int64_t)p.batch * H * N;
+  const int64_t ch = on ? chain : 0;
+  const int n = (int)(ch % N), h = (int)((ch / N) % H), b = (int)(ch / ((int64_t)N * H));
+  const int pl = (ns + NP - 1) / NP, k0 = min(ns, part * pl), k1 = min(ns, k0 + pl);
   float* zp = q.z + ((int64_t)b * ns * H + h) * N + n;
   float* lp = q.lam + ((int64_t)b * ns * H + h) * N + n;
   const float* dp = q.dec + (int64_t)b * ns * H + h;
   const int64_t zs = (int64_t)H * N;
-  float L = 0.f;
-  // 16 segments of each chain loaded together, the next 16's while the chains run through these (two buffers;
-  // the loads read segments neither chain has written yet)
-  struct Batch { float zl[16], df[16], gl[16], db[16]; };
-  auto ld = [&](int s0, Batch& t) {
+  float d[KB], z[KB], gl[KB];
+  auto load = [&](int k) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int sf = s0 + k, sb = ns - 1 - s0 - k;
-      t.zl[k] = sf < ns ? zp[sf * zs] : 0.f;
-      t.df[k] = sf < ns ? dp[(int64_t)sf * H] : 1.f;
-      t.gl[k] = sb >= 0 ? lp[sb * zs] : 0.f;
-      t.db[k] = sb >= 0 ? dp[(int64_t)sb * H] : 1.f;
+    for (int j = 0; j < KB; ++j) {
+      const bool in = on && k + j < k1;
+      d[j] = in ? dp[(int64_t)(k + j) * H] : 1.f;
+      z[j] = in ? zp[(int64_t)(k + j) * zs] : 0.f;
+      gl[j] = in ? lp[(int64_t)(k + j) * zs] : 0.f;
     }
   };
-  auto step = [&](int s0, const Batch& t) {
+  float Z0 = 0.f;
+  if (on && p.init_state) {
+    const float* s0 = p.init_state + (((int64_t)b * H + h) * P) * N + n;
+    for (int k = part; k < P; k += NP) Z0 += s0[(int64_t)k * N];
+  }
+  // the part's reductions: forward (decay product, sum from zero, in order) and adjoint (sum from zero, right to
+  // left: the chunks of KB segments from the last back); a part of one chunk stays in registers throughout
+  float Zp = 0.f, Dp = 1.f, Lp = 0.f;
+  for (int k = k0; k < k1 || k == k0; k += KB) {
+    load(k);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int sf = s0 + k, sb = ns - 1 - s0 - k;
-      if (sf < ns) zp[sf * zs] = Z;      // the state sum entering segment sf
-      Z = t.df[k] * Z + t.zl[k];
-      if (sb >= 0) lp[sb * zs] = L;      // the adjoint handed into segment sb from the right
-      L = t.db[k] * L + t.gl[k];
-    }
-  };
-  Batch ba, bb;
-  if (ns > 0) ld(0, ba);
-  for (int s0 = 0; s0 < ns; s0 += 32) {
-    if (s0 + 16 < ns) ld(s0 + 16, bb);
-    step(s0, ba);
-    if (s0 + 16 < ns) {
-      if (s0 + 32 < ns) ld(s0 + 32, ba);
-      step(s0 + 16, bb);
+    for (int j = 0; j < KB; ++j) {
+      Zp = d[j] * Zp + z[j];
+      Dp *= d[j];
     }
   }
-  if (dh0) {
-    float* o = dh0 + (((int64_t)b * H + h) * P) * N + n;
-    for (int k = 0; k < P; ++k) o[(int64_t)k * N] = L;
+  const int nck = max(1, (k1 - k0 + KB - 1) / KB);
+  for (int c = nck - 1; c >= 0; --c) {
+    if (pl > KB) load(k0 + c * KB);
+#pragma unroll
+    for (int j = KB - 1; j >= 0; --j) Lp = d[j] * Lp + gl[j];
+  }
+  float Z = 0.f, L = 0.f, Lall = 0.f;
+#pragma unroll
+  for (int j = 0; j < NP; ++j) Z += __shfl(Z0, j * CW + ci, 64);
+#pragma unroll
+  for (int j = 0; j < NP - 1; ++j) {
+    const float dj = __shfl(Dp, j * CW + ci, 64), zj = __shfl(Zp, j * CW + ci, 64);
+    if (j < part) Z = dj * Z + zj;
+  }
+#pragma unroll
+  for (int j = NP - 1; j >= 0; --j) {
+    const float dj = __shfl(Dp, j * CW + ci, 64), lj = __shfl(Lp, j * CW + ci, 64);
+    if (j > part) L = dj * L + lj;
+    Lall = dj * Lall + lj;
+  }
+  if (on) {
+    // forward walk in order, adjoint walk right to left (from registers when the part is one chunk)
+    for (int k = k0; k < k1; k += KB) {
+      if (pl > KB) load(k);
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+        if (k + j < k1) {
+          zp[(int64_t)(k + j) * zs] = Z;   // the state sum entering segment k + j
+          Z = d[j] * Z + z[j];
+        }
+    }
+    for (int c = nck - 1; c >= 0; --c) {
+      const int k = k0 + c * KB;
+      if (pl > KB) load(k);
+#pragma unroll
+      for (int j = KB - 1; j >= 0; --j)
+        if (k + j < k1) {
+          lp[(int64_t)(k + j) * zs] = L;   // the adjoint handed into segment k + j from the right
+          L = d[j] * L + gl[j];
+        }
+    }
+    if (dh0) {
+      float* o = dh0 + (((int64_t)b * H + h) * P) * N + n;
+      for (int k = part; k < P; k += NP) o[(int64_t)k * N] = Lall;
+    }
   }
 }
 
@@ -771,15 +822,25 @@ hipError_t launch_ssd_hs_bwd(const SsdParams& p, const HsParams& q, float* dh0, 
   const dim3 grid((unsigned)p.nseg, (unsigned)p.batch);
   const int64_t nc = (int64_t)p.batch * p.nheads * p.dstate;
   const bool bf = p.dtype == DT_BF16;
+  auto carry = [&]() {
+    const int np = p.nseg >= 128 ? 8 : p.nseg >= 64 ? 4 : p.nseg >= 32 ? 2 : 1;
+    const dim3 cg((unsigned)(((nc * np + 63) / 64 + 3) / 4));
+    switch (np) {
+      case 8: hipLaunchKernelGGL(ssd_hsb_carry_kernel<8>, cg, dim3(256), 0, st, p, q, dh0); break;
+      case 4: hipLaunchKernelGGL(ssd_hsb_carry_kernel<4>, cg, dim3(256), 0, st, p, q, dh0); break;
+      case 2: hipLaunchKernelGGL(ssd_hsb_carry_kernel<2>, cg, dim3(256), 0, st, p, q, dh0); break;
+      default: hipLaunchKernelGGL(ssd_hsb_carry_kernel<1>, cg, dim3(256), 0, st, p, q, dh0); break;
+    }
+  };
   if (p.seqlen == 0) {                 // d h0 = 0 (the carry over no segments), dA = d_dt_bias = 0
-    hipLaunchKernelGGL(ssd_hsb_carry_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, st, p, q, dh0);
+    carry();
     hipLaunchKernelGGL(ssd_hsb_reduce_kernel, dim3((unsigned)((p.nheads + 3) / 4)), dim3(256), 0, st, p, q);
     return hipGetLastError();
   }
   // the segments' local sums of the state and of the adjoint, both carries, then the gradients
   if (bf) hipLaunchKernelGGL(ssd_hsb_local_kernel<bf16>, grid, dim3(64 * HSB_WAVES_LOC), 0, st, p, q);
   else hipLaunchKernelGGL(ssd_hsb_local_kernel<float>, grid, dim3(64 * HSB_WAVES_LOC), 0, st, p, q);
-  hipLaunchKernelGGL(ssd_hsb_carry_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, st, p, q, dh0);
+  carry();
   if (bf) hipLaunchKernelGGL(ssd_hsb_main_kernel<bf16>, grid, dim3(64 * HSB_WAVES), 0, st, p, q);
   else hipLaunchKernelGGL(ssd_hsb_main_kernel<float>, grid, dim3(64 * HSB_WAVES), 0, st, p, q);
   hipLaunchKernelGGL(ssd_hsb_reduce_kernel, dim3((unsigned)((p.nheads + 3) / 4)), dim3(256), 0, st, p, q);

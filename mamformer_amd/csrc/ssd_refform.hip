@@ -48,10 +48,6 @@ __device__ __forceinline__ float rf_dt(const RfParams& p, float raw, float bias)
   return d;
 }
 
-template <int CTRL, int ROWS = 0xf>
-__device__ __forceinline__ float dppf(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, false));
-}
 // Sum over each 16-lane row, in every lane of the row: quad permutes, then the half-row and row mirrors.
 __device__ __forceinline__ float row_sum16(float v) {
   v += dppf<0xB1>(v);      // quad_perm 1,0,3,2
