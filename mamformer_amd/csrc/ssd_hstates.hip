@@ -161,7 +161,10 @@ struct __align__(16) HsLocSmem {
 //  - Zloc[h][n] = sum_s e^{c_end - c_s} u_s[h] B_s[n] for its HS_NB columns, as fp32 MFMAs (32 heads x 32 columns a
 //    tile, k over pairs of tokens, B read from global memory);
 //  - the segment's decays (zb = 0).
-template <typename T>
+// BWD: the backward's local pass instead: no W or Ei, xs per (token, head) written to q.u (column block 0), and
+// besides Zloc the segment's part of the adjoint handed left, GL[h][n] = sum_t e^{c_t} g_t[n] with g = dhs / (H P),
+// into q.lam (MFMA tiles like Zloc's, A = e^{c_t} (0 past the end), B = the block's columns of dhs).
+template <typename T, bool BWD>
 __global__ __launch_bounds__(256) void ssd_hs_local_kernel(SsdParams p, HsParams q) {
   __shared__ HsLocSmem sm;
   const int si = blockIdx.x, b = blockIdx.y, zb = blockIdx.z, nblk = gridDim.z, n0 = HS_NB * zb;
@@ -170,21 +173,26 @@ __global__ __launch_bounds__(256) void ssd_hs_local_kernel(SsdParams p, HsParams
   const int64_t tok0 = (int64_t)si * HS_SEG;
   const int l = lane_id(), i = l & 31, hf = l >> 5, tiles = (hpg + 31) / 32, nw = blockDim.x / 64;
   const bool col = n0 + i < N;
-  // B operands of this wave's Zloc tile (k = token pairs), loaded before the prologue so that they arrive meanwhile;
-  // unmasked at clamped addresses: a token past the end meets u = 0, a lane past the last column feeds an output
-  // column that is not stored
+  // B operands of this wave's tile (k = token pairs), loaded before the prologue so that they arrive meanwhile;
+  // unmasked at clamped addresses: a token past the end meets a zero A operand, a lane past the last column feeds
+  // an output column that is not stored.  Units [0, G tiles): Zloc of (group, 32 heads), B of the group's columns;
+  // BWD units [G tiles, 2 G tiles): GL, the columns of dhs.
+  const int nz = G * tiles, nunit = BWD ? 2 * nz : nz;
   T bv[HS_SEG / 2];                    // converted at their use, so that nothing waits for them before
   auto load_b = [&](int unit) {
-    const T* Bg = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)(unit / tiles) * N + n0 +
-                  min(i, N - 1 - n0);
+    const T* Bg = unit < nz
+        ? reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)(unit / tiles) * N
+        : reinterpret_cast<const T*>(q.dhs) + (int64_t)b * p.seqlen * N;
+    const int64_t ld = unit < nz ? p.B_sl : N;
+    Bg += n0 + min(i, N - 1 - n0);
 #pragma unroll
-    for (int m = 0; m < HS_SEG / 2; ++m) bv[m] = Bg[(tok0 + min(2 * m + hf, len - 1)) * p.B_sl];
+    for (int m = 0; m < HS_SEG / 2; ++m) bv[m] = Bg[(tok0 + min(2 * m + hf, len - 1)) * ld];
   };
   int unit = wave_id();
-  if (unit < G * tiles) load_b(unit);
-  hs_prologue<T>(p, sm, b, si, len, nullptr);
+  if (unit < nunit) load_b(unit);
+  hs_prologue<T>(p, sm, b, si, len, (BWD && zb == 0) ? q.u : nullptr);
   __syncthreads();
-  {
+  if constexpr (!BWD) {
     const int nrow = (HS_SEG - zb + nblk - 1) / nblk;
     float* wt = q.w + ((int64_t)b * p.nseg + si) * G * (HS_SEG * HS_SEG);
     for (int e = tid; e < G * nrow * HS_SEG; e += blockDim.x) {
@@ -212,28 +220,33 @@ __global__ __launch_bounds__(256) void ssd_hs_local_kernel(SsdParams p, HsParams
       eit[(int64_t)h * HS_SEG + t] = t < len ? __expf(sm.c[t][h]) : 0.f;
     }
   }
-  // Zloc: tiles of (group, 32 heads), one per wave at a time
-  for (; unit < G * tiles; unit += nw) {
-    const int g = unit / tiles, hl = (unit % tiles) * 32;
+  // Zloc (and GL): tiles of (group, 32 heads), one per wave at a time
+  const float gscale = 1.f / ((float)H * (float)p.headdim);
+  for (; unit < nunit; unit += nw) {
+    const bool gl = BWD && unit >= nz;
+    const int uz = gl ? unit - nz : unit;
+    const int g = uz / tiles, hl = (uz % tiles) * 32;
     const int h = g * hpg + min(hl + i, hpg - 1);            // A row (clamped; rows past hpg are not stored)
     const float ce = sm.cend[h];
     float a[HS_SEG / 2];
 #pragma unroll
     for (int m = 0; m < HS_SEG / 2; ++m) {
       const int sk = 2 * m + hf;
-      a[m] = sm.u[sk][h] * __expf(ce - sm.c[sk][h]);           // u is 0 past the end
+      if (gl) a[m] = sk < len ? __expf(sm.c[sk][h]) : 0.f;
+      else a[m] = sm.u[sk][h] * __expf(ce - sm.c[sk][h]);      // u is 0 past the end
     }
     f32x16 acc = zero16();
 #pragma unroll
     for (int m = 0; m < HS_SEG / 2; ++m)
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[m], to_f32(bv[m]), acc, 0, 0, 0);
-    if (unit + nw < G * tiles) load_b(unit + nw);
+    if (unit + nw < nunit) load_b(unit + nw);
     if (col) {
-      float* zl = q.z + (((int64_t)b * p.nseg + si) * H + g * hpg + hl) * N + n0 + i;
+      float* zl = (gl ? q.lam : q.z) + (((int64_t)b * p.nseg + si) * H + g * hpg + hl) * N + n0 + i;
+      const float sc = gl ? gscale : 1.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int hr = acc_row(hf, r);
-        if (hl + hr < hpg) zl[(int64_t)hr * N] = acc[r];
+        if (hl + hr < hpg) zl[(int64_t)hr * N] = acc[r] * sc;
       }
     }
   }
@@ -381,9 +394,9 @@ __global__ __launch_bounds__(64) void ssd_hs_out_kernel(SsdParams p, HsParams q)
 //   d dt_t = A a_t q_t + xs_t du_t (through bias, softplus and clamp),   d xs_t = dt_t du_t (dx[t][h][p], every p),
 //   dA = sum_t dt_t a_t q_t,   d h0[h][p][n] = a_0 lambda_0 (the adjoint of the state sum before the first token).
 // Per 32-token segment with Zin the state sum entering it and Lam = a lambda of the next segment's first token:
-//   ssd_hsb_local_kernel (segment, batch): the forward's local pass (xs, Zloc, segment decay) and
-//                        GL[h][n] = sum_t e^{c_t} g_t[n] (c the in-segment inclusive cumsum of A dt), the
-//                        segment's part of the adjoint handed to the left.
+//   ssd_hs_local_kernel<T, true> (segment, batch, column block): the forward's local pass (xs, Zloc, segment
+//                        decay) and GL[h][n] = sum_t e^{c_t} g_t[n] (c the in-segment inclusive cumsum of A dt),
+//                        the segment's part of the adjoint handed to the left, both as fp32 MFMA tiles.
 //   ssd_hsb_carry_kernel (batch, head, n): Zin of every segment left to right (in place over Zloc) and Lam of
 //                        every segment right to left (in place over GL), then d h0.
 //   ssd_hsb_main_kernel  (segment, batch): one head per wave at a time, lanes over the state columns: the two
@@ -392,7 +405,7 @@ __global__ __launch_bounds__(64) void ssd_hs_out_kernel(SsdParams p, HsParams q)
 //                        over the waves in a fixed order, dx, ddt and per-segment dA / d_dt_bias partials.
 //   ssd_hsb_reduce_kernel: dA and d_dt_bias summed over (batch, segment) in a fixed order.
 constexpr int HSB_MAXH = 128, HSB_MAXN = 128;   // state columns: two per lane
-constexpr int HSB_WAVES = 4, HSB_WAVES_LOC = 8;
+constexpr int HSB_WAVES = 4;
 
 __device__ __forceinline__ float hsb_dt_chain(const SsdParams& p, float raw, float bias) {
   const float u = raw + bias;
@@ -419,61 +432,6 @@ __device__ void hsb_load_g(const SsdParams& p, const HsParams& q, float (*g)[W],
     const int t = e / W, n = e % W;
     g[t][n] = (t < len && n < N) ? to_f32(src[(int64_t)t * N + n]) * scale : 0.f;
   }
-}
-
-struct HsbLocSmem {
-  float c[HS_SEG][HS_HP];        // as in HsLocSmem
-  float u[HS_SEG][HS_HP];
-  float g[HS_SEG][HSB_MAXN];     // ghs / (H P) (0 past the end and beyond N)
-  float B[HS_SEG][HSB_MAXN];     // B of one group (likewise)
-  float cend[HSB_MAXH];
-};
-
-// One head per wave at a time, lanes over pairs of state columns, the per-token weights broadcast from lane t:
-// GL[h][n] = sum_t e^{c_t} g_t[n] and Zloc[h][n] = sum_s e^{c_end - c_s} u_s B_s[n].
-template <typename T>
-__global__ __launch_bounds__(64 * HSB_WAVES_LOC) void ssd_hsb_local_kernel(SsdParams p, HsParams q) {
-  __shared__ HsbLocSmem sm;
-  const int si = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = wave_id(), l = lane_id();
-  const int H = p.nheads, N = p.dstate, G = p.ngroups, hpg = H / G;
-  const int64_t tok0 = (int64_t)si * HS_SEG;
-  const int len = min(HS_SEG, p.seqlen - (int)tok0);
-  const int n0 = 2 * l, t = l & 31;
-  hs_prologue<T>(p, sm, b, si, len, q.u);
-  hsb_load_g<T, HSB_MAXN>(p, q, sm.g, b, si, len);
-  float* gl = q.lam + (((int64_t)b * p.nseg + si) * H) * N;
-  float* zl = q.z + (((int64_t)b * p.nseg + si) * H) * N;
-  for (int gi = 0; gi < G; ++gi) {
-    __syncthreads();                   // c, u, g stored; the previous group's B no longer read
-    {
-      const T* Bb = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)gi * N;
-      for (int e = tid; e < HS_SEG * HSB_MAXN; e += blockDim.x) {
-        const int s = e / HSB_MAXN, n = e % HSB_MAXN;
-        sm.B[s][n] = (s < len && n < N) ? to_f32(Bb[(tok0 + s) * p.B_sl + n]) : 0.f;
-      }
-    }
-    __syncthreads();
-    for (int h = gi * hpg + w; h < (gi + 1) * hpg; h += HSB_WAVES_LOC) {
-      const float c = sm.c[t][h];
-      const float ei = __expf(c), wt = __expf(sm.cend[h] - c) * sm.u[t][h];   // both exponents <= 0
-      float g0 = 0.f, g1 = 0.f, z0 = 0.f, z1 = 0.f;
-#pragma unroll
-      for (int s = 0; s < HS_SEG; ++s) {
-        const float es = hsb_readlane(ei, s), ws = hsb_readlane(wt, s);
-        const float2 gv = *reinterpret_cast<const float2*>(&sm.g[s][n0]);
-        const float2 bv = *reinterpret_cast<const float2*>(&sm.B[s][n0]);
-        g0 += es * gv.x;
-        g1 += es * gv.y;
-        z0 += ws * bv.x;
-        z1 += ws * bv.y;
-      }
-      if (n0 < N) {
-        *reinterpret_cast<float2*>(gl + (int64_t)h * N + n0) = float2{g0, g1};
-        *reinterpret_cast<float2*>(zl + (int64_t)h * N + n0) = float2{z0, z1};
-      }
-    }
-  }
-  if (tid < H) q.dec[((int64_t)b * p.nseg + si) * H + tid] = __expf(sm.cend[tid]);
 }
 
 // Both carries of the chains (batch, head, column), as two-level scans like the forward's: the forward
@@ -838,8 +796,9 @@ hipError_t launch_ssd_hs_bwd(const SsdParams& p, const HsParams& q, float* dh0, 
     return hipGetLastError();
   }
   // the segments' local sums of the state and of the adjoint, both carries, then the gradients
-  if (bf) hipLaunchKernelGGL(ssd_hsb_local_kernel<bf16>, grid, dim3(64 * HSB_WAVES_LOC), 0, st, p, q);
-  else hipLaunchKernelGGL(ssd_hsb_local_kernel<float>, grid, dim3(64 * HSB_WAVES_LOC), 0, st, p, q);
+  const dim3 lgrid((unsigned)p.nseg, (unsigned)p.batch, (unsigned)((p.dstate + HS_NB - 1) / HS_NB));
+  if (bf) hipLaunchKernelGGL((ssd_hs_local_kernel<bf16, true>), lgrid, dim3(256), 0, st, p, q);
+  else hipLaunchKernelGGL((ssd_hs_local_kernel<float, true>), lgrid, dim3(256), 0, st, p, q);
   carry();
   if (bf) hipLaunchKernelGGL(ssd_hsb_main_kernel<bf16>, grid, dim3(64 * HSB_WAVES), 0, st, p, q);
   else hipLaunchKernelGGL(ssd_hsb_main_kernel<float>, grid, dim3(64 * HSB_WAVES), 0, st, p, q);
@@ -851,9 +810,9 @@ hipError_t launch_ssd_hs(const SsdParams& p, const HsParams& q, hipStream_t st) 
   if (p.seqlen == 0) return hipSuccess;
   const dim3 grid((unsigned)p.nseg, (unsigned)p.batch, (unsigned)((p.dstate + HS_NB - 1) / HS_NB));
   if (p.dtype == DT_BF16)
-    hipLaunchKernelGGL(ssd_hs_local_kernel<bf16>, grid, dim3(256), 0, st, p, q);
+    hipLaunchKernelGGL((ssd_hs_local_kernel<bf16, false>), grid, dim3(256), 0, st, p, q);
   else
-    hipLaunchKernelGGL(ssd_hs_local_kernel<float>, grid, dim3(256), 0, st, p, q);
+    hipLaunchKernelGGL((ssd_hs_local_kernel<float, false>), grid, dim3(256), 0, st, p, q);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // parts per chain: about 16 segments each, at most 8 (a part's load then covers 8 consecutive columns)
