@@ -114,8 +114,8 @@ struct RfRegs {
   static constexpr int PB = (NP + RF_NT - 1) / RF_NT;      // per thread
   static constexpr int NQ = TB * CPB / 4;                  // 4-element pieces of dt (x, z) per block
   Row8<T> b[PB], c[PB];
-  float4 dt;
-  float xv[4], zv[4];
+  float4 dt;                   // raw dt; processed (bias, softplus, clamp, 0 past the end) by rf_store
+  T xv[4], zv[4];              // raw x and gate
 };
 
 // Workgroup -> (batch, channel block): runs of 4 consecutive blocks go to the same XCD (workgroups are dealt to
@@ -128,6 +128,8 @@ __device__ __forceinline__ void rf_block(int nblk, int nper, int& b, int& cb) {
   cb = j % nper;
 }
 
+// Loads only (every one unconditional at a clamped row), so that they stay in flight while the current block
+// computes: the values are converted, masked and stored to LDS by rf_store a block later.
 template <typename T, int N, int TB, int CPB, bool GATE>
 __device__ __forceinline__ void rf_load(const RfParams& p, RfRegs<T, N, TB, CPB>& r, int b, int c0, int t0) {
   using R = RfRegs<T, N, TB, CPB>;
@@ -145,24 +147,23 @@ __device__ __forceinline__ void rf_load(const RfParams& p, RfRegs<T, N, TB, CPB>
   if (tid < R::NQ) {
     const int row = t0 + tid / (CPB / 4), col = 4 * (tid % (CPB / 4));
     const int rr = min(row, last);
-    const bool in = row <= last;
-    const float4 raw = *reinterpret_cast<const float4*>(p.dt + (int64_t)b * p.dt_sb + (int64_t)rr * p.dt_sl + c0 + col);
-    const float4 bias = p.dt_bias ? *reinterpret_cast<const float4*>(p.dt_bias + c0 + col) : float4{0.f, 0.f, 0.f, 0.f};
-    r.dt = float4{in ? rf_dt(p, raw.x, bias.x) : 0.f, in ? rf_dt(p, raw.y, bias.y) : 0.f,
-                  in ? rf_dt(p, raw.z, bias.z) : 0.f, in ? rf_dt(p, raw.w, bias.w) : 0.f};
+    r.dt = *reinterpret_cast<const float4*>(p.dt + (int64_t)b * p.dt_sb + (int64_t)rr * p.dt_sl + c0 + col);
     const T* xp = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + (int64_t)rr * p.x_sl + c0 + col;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.xv[j] = in ? to_f32(xp[j]) : 0.f;
+    for (int j = 0; j < 4; ++j) r.xv[j] = xp[j];
     if constexpr (GATE) {
       const T* zp = reinterpret_cast<const T*>(p.z) + (int64_t)b * p.z_sb + (int64_t)rr * p.z_sl + c0 + col;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) r.zv[j] = to_f32(zp[j]);
+      for (int j = 0; j < 4; ++j) r.zv[j] = zp[j];
     }
   }
 }
 
+// The block at t0 into LDS: B and C as fp32; dt processed with the thread's 4 channels' bias (bias4), dt and x 0
+// past the end of the sequence.
 template <typename T, int N, int TB, int CPB, bool GATE>
-__device__ __forceinline__ void rf_store(const RfRegs<T, N, TB, CPB>& r, RfStage<N, TB, CPB>& s) {
+__device__ __forceinline__ void rf_store(const RfParams& p, const RfRegs<T, N, TB, CPB>& r, RfStage<N, TB, CPB>& s,
+                                         int t0, const float4& bias4) {
   using R = RfRegs<T, N, TB, CPB>;
   const int tid = threadIdx.x;
 #pragma unroll
@@ -174,9 +175,15 @@ __device__ __forceinline__ void rf_store(const RfRegs<T, N, TB, CPB>& r, RfStage
   }
   if (tid < R::NQ) {
     const int row = tid / (CPB / 4), col = 4 * (tid % (CPB / 4));
-    *reinterpret_cast<float4*>(&s.dt[row][col]) = r.dt;
-    *reinterpret_cast<float4*>(&s.x[row][col]) = float4{r.xv[0], r.xv[1], r.xv[2], r.xv[3]};
-    if constexpr (GATE) *reinterpret_cast<float4*>(&s.z[row][col]) = float4{r.zv[0], r.zv[1], r.zv[2], r.zv[3]};
+    const float in = t0 + row < p.seqlen ? 1.f : 0.f;
+    *reinterpret_cast<float4*>(&s.dt[row][col]) =
+        float4{rf_dt(p, r.dt.x, bias4.x) * in, rf_dt(p, r.dt.y, bias4.y) * in, rf_dt(p, r.dt.z, bias4.z) * in,
+               rf_dt(p, r.dt.w, bias4.w) * in};
+    *reinterpret_cast<float4*>(&s.x[row][col]) =
+        float4{to_f32(r.xv[0]) * in, to_f32(r.xv[1]) * in, to_f32(r.xv[2]) * in, to_f32(r.xv[3]) * in};
+    if constexpr (GATE)
+      *reinterpret_cast<float4*>(&s.z[row][col]) =
+          float4{to_f32(r.zv[0]), to_f32(r.zv[1]), to_f32(r.zv[2]), to_f32(r.zv[3])};
   }
 }
 
@@ -232,9 +239,12 @@ __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
   const float Dc = p.D ? (p.D_per_channel ? p.D[c] : p.D[c / p.headdim]) : 0.f;
   const int nblk = (p.seqlen + TB - 1) / TB;
   RfRegs<T, N, TB, CPB> r;
+  float4 bias4 = {0.f, 0.f, 0.f, 0.f};      // this thread's 4 channels of dt_bias (the same rows every block)
+  if (p.dt_bias && tid < RfRegs<T, N, TB, CPB>::NQ)
+    bias4 = *reinterpret_cast<const float4*>(p.dt_bias + c0 + 4 * (tid % (CPB / 4)));
   if (nblk > 0) {
     rf_load<T, N, TB, CPB, GATE>(p, r, b, c0, 0);
-    rf_store<T, N, TB, CPB, GATE>(r, sm.st[0]);
+    rf_store<T, N, TB, CPB, GATE>(p, r, sm.st[0], 0, bias4);
   }
   if (nblk > 1) rf_load<T, N, TB, CPB, GATE>(p, r, b, c0, TB);
   __syncthreads();
@@ -276,7 +286,7 @@ __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
       }
       cur = nxt;
     }
-    if (k + 1 < nblk) rf_store<T, N, TB, CPB, GATE>(r, sm.st[(k + 1) & 1]);
+    if (k + 1 < nblk) rf_store<T, N, TB, CPB, GATE>(p, r, sm.st[(k + 1) & 1], (k + 1) * TB, bias4);
     if (k + 2 < nblk) rf_load<T, N, TB, CPB, GATE>(p, r, b, c0, (k + 2) * TB);
     __syncthreads();
     // y rows of this block: CPB channels = CPB / 8 pieces of 8 per token
@@ -469,30 +479,62 @@ struct RfbChanSmem {
   float dx[RK][CPB], ddt[RK][CPB];
 };
 
-// Piece j's rows into LDS (0 past the end of the sequence).
+// Piece j's rows into LDS (0 past the end of the sequence).  Every load is unconditional at a clamped (valid)
+// address and masked by a factor 0 afterwards, so that all of a thread's loads are in flight together (a select
+// between a loaded value and 0 lets the compiler put each load behind its own branch and wait); a missing dy or
+// dhs reads x or B instead, times 0 (finite inputs).
 template <typename T, int N, int RK, int CPB>
 __device__ void rfb_load_piece(const RfParams& p, RfbChanSmem<N, RK, CPB>& sm, int b, int c0, int t0) {
+  constexpr int NE = RK * N / RF_NT, NC = (RK * CPB + RF_NT - 1) / RF_NT;
+  static_assert(RK * N % RF_NT == 0, "whole rows of B / C per pass");
   const int tid = threadIdx.x, L = p.seqlen, di = p.d_inner;
   const T* Bp = reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb;
   const T* Cp = reinterpret_cast<const T*>(p.C) + (int64_t)b * p.C_sb;
-  const T* Gp = reinterpret_cast<const T*>(p.dhs) + (int64_t)b * L * N;
-  const float inv = 1.f / (float)di;
-  for (int e = tid; e < RK * N; e += RF_NT) {
-    const int t = e / N, n = e % N, tt = t0 + t;
-    const bool in = tt < L;
-    sm.B[t][n] = in ? to_f32(Bp[(int64_t)tt * p.B_sl + n]) : 0.f;
-    sm.C[t][n] = in ? to_f32(Cp[(int64_t)tt * p.C_sl + n]) : 0.f;
-    sm.G[t][n] = (in && p.dhs) ? to_f32(Gp[(int64_t)tt * N + n]) * inv : 0.f;
+  const T* Gp = p.dhs ? reinterpret_cast<const T*>(p.dhs) + (int64_t)b * L * N : Bp;
+  const int64_t gsl = p.dhs ? N : p.B_sl;
+  const float gmul = p.dhs ? 1.f / (float)di : 0.f;
+  T bv[NE], cv[NE], gv[NE];
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int e = tid + RF_NT * k, t = e / N, n = e % N, tt = min(t0 + t, L - 1);
+    bv[k] = Bp[(int64_t)tt * p.B_sl + n];
+    cv[k] = Cp[(int64_t)tt * p.C_sl + n];
+    gv[k] = Gp[(int64_t)tt * gsl + n];
   }
-  for (int e = tid; e < RK * CPB; e += RF_NT) {
-    const int t = e / CPB, cl = e % CPB, tt = t0 + t, c = c0 + cl;
-    const bool in = tt < L;
-    const float raw = in ? p.dt[(int64_t)b * p.dt_sb + (int64_t)tt * p.dt_sl + c] : 0.f;
-    const float bias = p.dt_bias ? p.dt_bias[c] : 0.f;
-    sm.dt[t][cl] = in ? rf_dt(p, raw, bias) : 0.f;
-    sm.chain[t][cl] = in ? rf_dt_chain(p, raw, bias) : 0.f;
-    sm.x[t][cl] = in ? to_f32(reinterpret_cast<const T*>(p.x)[(int64_t)b * p.x_sb + (int64_t)tt * p.x_sl + c]) : 0.f;
-    sm.dy[t][cl] = (in && p.dy) ? to_f32(reinterpret_cast<const T*>(p.dy)[((int64_t)b * L + tt) * di + c]) : 0.f;
+  const T* xb = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb;
+  const T* dyb = p.dy ? reinterpret_cast<const T*>(p.dy) + (int64_t)b * L * di : xb;
+  const int64_t dysl = p.dy ? di : p.x_sl;
+  const float dymul = p.dy ? 1.f : 0.f;
+  float raw[NC];
+  T xv[NC], dv[NC];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int e = min(tid + RF_NT * k, RK * CPB - 1), t = e / CPB, cl = e % CPB, tt = min(t0 + t, L - 1);
+    raw[k] = p.dt[(int64_t)b * p.dt_sb + (int64_t)tt * p.dt_sl + c0 + cl];
+    xv[k] = xb[(int64_t)tt * p.x_sl + c0 + cl];
+    dv[k] = dyb[(int64_t)tt * dysl + c0 + cl];
+  }
+  __builtin_amdgcn_sched_barrier(0);   // every load issued before the first use
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int e = tid + RF_NT * k, t = e / N, n = e % N;
+    const float in = t0 + t < L ? 1.f : 0.f;
+    sm.B[t][n] = to_f32(bv[k]) * in;
+    sm.C[t][n] = to_f32(cv[k]) * in;
+    sm.G[t][n] = to_f32(gv[k]) * (in * gmul);
+  }
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int e = tid + RF_NT * k;
+    if (e < RK * CPB) {
+      const int t = e / CPB, cl = e % CPB;
+      const float in = t0 + t < L ? 1.f : 0.f;
+      const float bias = p.dt_bias ? p.dt_bias[c0 + cl] : 0.f;
+      sm.dt[t][cl] = rf_dt(p, raw[k], bias) * in;
+      sm.chain[t][cl] = rf_dt_chain(p, raw[k], bias) * in;
+      sm.x[t][cl] = to_f32(xv[k]) * in;
+      sm.dy[t][cl] = to_f32(dv[k]) * (in * dymul);
+    }
   }
 }
 
@@ -614,6 +656,7 @@ __global__ __launch_bounds__(RF_NT) void rf_bwd_state_kernel(RfParams p) {
   }
   const float bias = p.dt_bias ? p.dt_bias[cc] : 0.f;
   const float inv = 1.f / (float)di;
+  float h[HS_NS];
   float* dBp = p.dB_part + ((int64_t)b * ncb + cblk) * L * N + n0;
   float* dCp = p.dC_part + ((int64_t)b * ncb + cblk) * L * N + n0;
   for (int j = nsb - 1; j >= 0; --j) {
@@ -636,22 +679,33 @@ __global__ __launch_bounds__(RF_NT) void rf_bwd_state_kernel(RfParams p) {
       sC[tid] = cv;
       sG[tid] = gv;
     }
+    // this lane's channel for the piece's tokens: unconditional loads at clamped addresses, masked by factors
+    // (a missing dy reads x, times 0), so that they are all in flight together
     float dtv[RK], xv[RK], dyv[RK];
-#pragma unroll
-    for (int t = 0; t < RK; ++t) {
-      const int tt = min(t0 + t, L - 1);
-      const bool in = on && t0 + t < L;
-      const float raw = p.dt[(int64_t)b * p.dt_sb + (int64_t)tt * p.dt_sl + cc];
-      const float xr = to_f32(reinterpret_cast<const T*>(p.x)[(int64_t)b * p.x_sb + (int64_t)tt * p.x_sl + cc]);
-      const float dr = p.dy ? to_f32(reinterpret_cast<const T*>(p.dy)[((int64_t)b * L + tt) * di + cc]) : 0.f;
-      dtv[t] = in ? rf_dt(p, raw, bias) : 0.f;
-      xv[t] = in ? xr : 0.f;
-      dyv[t] = in ? dr : 0.f;
-    }
-    float h[HS_NS];
     {
+      float raw[RK];
+      T xr[RK], dr[RK];
+      const T* xb = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_sb + cc;
+      const T* dyb = p.dy ? reinterpret_cast<const T*>(p.dy) + (int64_t)b * L * di + cc : xb;
+      const int64_t dysl = p.dy ? di : p.x_sl;
+#pragma unroll
+      for (int t = 0; t < RK; ++t) {
+        const int tt = min(t0 + t, L - 1);
+        raw[t] = p.dt[(int64_t)b * p.dt_sb + (int64_t)tt * p.dt_sl + cc];
+        xr[t] = xb[(int64_t)tt * p.x_sl];
+        dr[t] = dyb[(int64_t)tt * dysl];
+      }
       const float4 hv = *reinterpret_cast<const float4*>(p.ckpt + (((int64_t)b * nsb + j) * di + cc) * N + n0);
       h[0] = hv.x; h[1] = hv.y; h[2] = hv.z; h[3] = hv.w;
+      __builtin_amdgcn_sched_barrier(0);   // every load issued before the first use
+      const float dymul = p.dy ? 1.f : 0.f;
+#pragma unroll
+      for (int t = 0; t < RK; ++t) {
+        const float in = (on && t0 + t < L) ? 1.f : 0.f;
+        dtv[t] = rf_dt(p, raw[t], bias) * in;
+        xv[t] = to_f32(xr[t]) * in;
+        dyv[t] = to_f32(dr[t]) * (in * dymul);
+      }
     }
     __syncthreads();
     // forward through the piece: the state after every token (hs[t]) and every decay; hs[-1] = the entry state
