@@ -80,6 +80,30 @@ __device__ __forceinline__ void cvt8(const Raw8<T>& r, float (&v)[CV]) {
     for (int i = 0; i < 4; ++i) { v[i] = r.a[i]; v[4 + i] = r.b[i]; }
   }
 }
+
+// The K-1 window rows before t0 (rows of x, the cached rows before the sequence, or 0), loaded together: each row's
+// source is chosen by address and the row masked by a factor afterwards, so that no load waits behind a branch.
+template <typename T, int K>
+__device__ __forceinline__ void load_halo(const Conv1dParams& p, const T* xb, const T* sb, int t0,
+                                          float (&win)[K][CV]) {
+  constexpr int NH = K > 1 ? K - 1 : 1;
+  Raw8<T> hr[NH];
+  float hm[NH];
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) {
+    const int tp = t0 - (K - 1) + j;
+    const bool inx = tp >= 0, ins = !inx && sb && tp >= -p.cs_len;
+    const T* src = inx ? xb + (int64_t)tp * p.x_sl : ins ? sb + (int64_t)(p.cs_len + tp) * p.cs_sl : xb;
+    hm[j] = (inx || ins) ? 1.f : 0.f;
+    hr[j] = ldraw<T>(src);
+  }
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) {
+    cvt8<T>(hr[j], win[j]);
+#pragma unroll
+    for (int i = 0; i < CV; ++i) win[j][i] *= hm[j];
+  }
+}
 constexpr int RG = 8;      // rows loaded together
 
 template <typename T, int K>
@@ -104,18 +128,7 @@ __global__ __launch_bounds__(256) void conv1d_kernel(Conv1dParams p) {
 
   // window rows t0-K+1 .. t0-1 (win[j] holds xin[t - (K-1) + j] for the next output t)
   float win[K][CV];
-#pragma unroll
-  for (int j = 0; j < K - 1; ++j) {
-    const int tp = t0 - (K - 1) + j;
-    if (tp >= 0) {
-      load8<T>(xb + (int64_t)tp * p.x_sl, win[j]);
-    } else if (sb && tp >= -p.cs_len) {
-      load8<T>(sb + (int64_t)(p.cs_len + tp) * p.cs_sl, win[j]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < CV; ++i) win[j][i] = 0.f;
-    }
-  }
+  load_halo<T, K>(p, xb, sb, t0, win);
   const int t1 = min(p.seqlen, t0 + TTF);
   auto emit = [&](int t) {               // win[K-1] holds row t
     float o[CV];
@@ -178,18 +191,7 @@ __global__ __launch_bounds__(256) void conv1d_bwd_kernel(Conv1dBwdParams q) {
   for (int i = 0; i < CV; ++i) bias[i] = p.bias ? p.bias[d0 + i] : 0.f;
 
   float win[K][CV];       // win[j] = xin[t - (K-1) + j] for the current t
-#pragma unroll
-  for (int j = 0; j < K - 1; ++j) {
-    const int tp = t0 - (K - 1) + j;
-    if (tp >= 0) {
-      load8<T>(xb + (int64_t)tp * p.x_sl, win[j]);
-    } else if (sb && tp >= -p.cs_len) {
-      load8<T>(sb + (int64_t)(p.cs_len + tp) * p.cs_sl, win[j]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < CV; ++i) win[j][i] = 0.f;
-    }
-  }
+  load_halo<T, K>(p, xb, sb, t0, win);
   float duw[K][CV];       // duw[K-1-j] = du[t - j]
 #pragma unroll
   for (int j = 0; j < K; ++j)

@@ -685,18 +685,35 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
   const int dt = w & 3, ktb = 2 * (w >> 2);     // dS tiles (ktb + i, dt)
   const int x4 = w & 3, st = w >> 2;            // output tiles: dv^T (d-block x4, s-block st), dphi(k)^T (k-block x4)
 
-  // the adjoint after this segment: the final-state gradient plus the later segments' sums (fixed order)
+  // the adjoint after this segment: the final-state gradient plus the later segments' sums (fixed order: the
+  // final-state gradient, then parts j from the last down); each part's 32 values of a lane are loaded together
   f32x16 dS[2];
+  {
+    int eo[2][16];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    dS[i] = zero16();
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int e = (32 * (ktb + i) + acc_row(half, r)) * BD + 32 * dt + l32;
-      float a = q.d_final ? q.d_final[(int64_t)bh * BD * BD + e] : 0.f;
-      for (int j = SEG_PARTS * nseg - 1; j >= SEG_PARTS * (seg + 1); --j)
-        a += q.segsum[((int64_t)j * nbh + bh) * (BD * BD + BD) + e];
-      dS[i][r] = a;
+      for (int r = 0; r < 16; ++r) eo[i][r] = (32 * (ktb + i) + acc_row(half, r)) * BD + 32 * dt + l32;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dS[i] = zero16();
+    if (q.d_final) {
+      const float* df = q.d_final + (int64_t)bh * BD * BD;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dS[i][r] = df[eo[i][r]];
+    }
+    for (int j = SEG_PARTS * nseg - 1; j >= SEG_PARTS * (seg + 1); --j) {
+      const float* sp = q.segsum + ((int64_t)j * nbh + bh) * (BD * BD + BD);
+      float v[2][16];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[i][r] = sp[eo[i][r]];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dS[i][r] += v[i][r];
     }
   }
   if (tid < BD) {
