@@ -175,10 +175,15 @@ __device__ __forceinline__ void scaled_x(const bf16* x, const float (&wb)[2], co
 
 // H[ph][n][p] += sum_s B^T[n][s] xs[ph][s][p] over the segment's 64 tokens, B^T read transposed from the B tile
 // with the state rows in state_row_perm order; the fragments of tile nt + 1 are requested before tile nt's
-// MFMAs.
-template <int N, int PH>
+// MFMAs, and issue(nt) (global -> LDS loads of a later segment) runs between them, so that the loads queue at
+// the memory unit while the matrix unit works.
+struct NoIssue {
+  __device__ void operator()(int) const {}
+};
+template <int N, int PH, typename Issue = NoIssue>
 __device__ __forceinline__ void lb_state_update(f32x16 (&H)[PH][N / 32], const bf16* btile,
-                                                const Frag<bf16> (&xa)[PH][4], const LaneOffs& lo) {
+                                                const Frag<bf16> (&xa)[PH][4], const LaneOffs& lo,
+                                                const Issue& issue = Issue()) {
   Frag<bf16> cur[4], nxt[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) cur[c] = tr_frag(btile, 16 * c, lo.trp);
@@ -188,6 +193,7 @@ __device__ __forceinline__ void lb_state_update(f32x16 (&H)[PH][N / 32], const b
 #pragma unroll
       for (int c = 0; c < 4; ++c) nxt[c] = tr_frag(btile + (nt + 1) * Sub64::ELEMS, 16 * c, lo.trp);
     }
+    issue(nt);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -305,15 +311,16 @@ constexpr int lb_state_nbuf = 3 * sizeof(LbStateStage<N, HG>) <= LB_LDS_BYTES ? 
 
 // Segment si of the chunk into a pass-1 stage: every wave issues exactly N / 8 / NW + 4 PH + 1 loads (its
 // share of the B tile, its halves of its head's x tile, its head's dt; rows past the end of the sequence are
-// clamped).
+// clamped).  part < 0: all of them; else part 0 the B share, part min(1, NT - 1) the x halves and part NT - 1
+// the dt (in the same order of issue).
 template <int N, int HG, int PH>
 __device__ __forceinline__ void lb_state_fetch(const SsdParams& p, const LbWave& c,
-                                               LbStateStage<N, HG>* __restrict__ s, int si) {
-  constexpr int BB = N / 8 / lb_waves<HG, PH>;
+                                               LbStateStage<N, HG>* __restrict__ s, int si, int part = -1) {
+  constexpr int BB = N / 8 / lb_waves<HG, PH>, NT = N / 32;
   const int pos = c.c0 + si * SEG;
-  fetch_sub64(&s->Bt[0][0], c.Bg, p.B_sl, pos, c.last, c.w * BB, BB);
-  fetch_sub64(&s->X[c.hw][0][0], c.xg, p.x_sl, pos, c.last, 4 * c.ph0, 4 * PH);
-  fetch_dt(s->dt[c.hw], c.dtg, p.dt_sl, pos, c.last, lane_id_here());
+  if (part < 0 || part == 0) fetch_sub64(&s->Bt[0][0], c.Bg, p.B_sl, pos, c.last, c.w * BB, BB);
+  if (part < 0 || part == (NT > 1 ? 1 : 0)) fetch_sub64(&s->X[c.hw][0][0], c.xg, p.x_sl, pos, c.last, 4 * c.ph0, 4 * PH);
+  if (part < 0 || part == NT - 1) fetch_dt(s->dt[c.hw], c.dtg, p.dt_sl, pos, c.last, lane_id_here());
 }
 
 // Segment si of pass 1's reverse walk, its tiles in stage `cur`; segment fsi (if >= 0) is fetched into
@@ -330,7 +337,6 @@ __device__ __forceinline__ void lb_state_segment(const SsdParams& p, const LbWav
   if (NBUF == 3 && more) wait_vmem_n<LOADS>();             // this segment's loads; the next one's may fly
   else wait_vmem();
   lds_barrier();                                           // the segment's tiles are in LDS for every wave
-  if (fsi >= 0) lb_state_fetch<N, HG, PH>(p, c, nxt, fsi);
   const int pos = c.c0 + si * SEG;
   float dtv;
   const float cs = seg_decay(p, cur->dt[c.hw][c.l], c.dtb, c.Ah, pos + c.l, c.c1, dtv);
@@ -340,7 +346,11 @@ __device__ __forceinline__ void lb_state_segment(const SsdParams& p, const LbWav
   halves(__expf(R + cse - cs) * dtv, wb);
   Frag<bf16> xa[PH][4];
   scaled_x<PH>(&cur->X[c.hw][c.ph0][0], wb, dm, lo, xa);
-  lb_state_update<N, PH>(S, &cur->Bt[0][0], xa, lo);
+  // segment fsi's loads, issued in parts between the state update's tiles: issued together right after the
+  // barrier, every wave's loads queued behind the whole workgroup's at the memory unit (~1K cycles a segment)
+  lb_state_update<N, PH>(S, &cur->Bt[0][0], xa, lo, [&](int nt) {
+    if (fsi >= 0) lb_state_fetch<N, HG, PH>(p, c, nxt, fsi, nt);
+  });
   R += cse;
 }
 
