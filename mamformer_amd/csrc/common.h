@@ -210,5 +210,7 @@ __device__ __forceinline__ float softplus_f(float x) {
 // silu(x) = x / (1 + e^{-x}), the quotient through the hardware reciprocal (v_rcp_f32, 1 ulp) rather than an
 // IEEE division sequence; e^{-x} overflowing to +inf gives -0 (the limit) for very negative x.
 __device__ __forceinline__ float silu_f(float x) { return x * __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+// sigmoid(x) = 1 / (1 + e^{-x}) through the same reciprocal (0 for e^{-x} = +inf).
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 }  // namespace mh
