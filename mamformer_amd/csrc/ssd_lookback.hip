@@ -559,15 +559,18 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
   lds_barrier();                                           // tiles in LDS; the other stage is free
   if (si > 0 && si + 1 < nseg) lb_scan_fetch<N, HG, NW>(p, c, nxt, si + 1);
   if (PH == 1 && p.xsum && pos + l < c.c1) {
-    // the sum of x over the wave's 32 channels of token pos + l (the input of h_states), from the x tile
+    // the sum of x over the wave's 32 channels of token pos + l (the input of h_states), from the x tile (row
+    // offsets from a lane index recomputed here: hoisted, they were spilled, and each reload waited for the
+    // next segment's tile loads)
     float xs = 0.f;
+    const int lh = lane_id_here();
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(xw + Sub64::off(l, 8 * q));
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(xw + Sub64::off(lh, 8 * q));
 #pragma unroll
       for (int j = 0; j < 8; ++j) xs += (float)v[j];
     }
-    p.xsum[(((int64_t)c.b * p.seqlen + pos + l) * p.nheads + c.h) * 2 + c.ph0] = xs;
+    p.xsum[(((int64_t)c.b * p.seqlen + pos + lh) * p.nheads + c.h) * 2 + c.ph0] = xs;
   }
   bf16x4 zq[PH][2][4];
   if constexpr (GATE) load_z_pieces<PH>(zg + (int64_t)pos * p.z_sl, p.z_sl, c.c1 - 1 - pos, zq);
