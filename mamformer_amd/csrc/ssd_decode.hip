@@ -23,8 +23,9 @@ namespace mh {
 constexpr int SSU_ROWS = 2;   // state rows per thread per pass
 
 // GEN: the general form, with the decay rate per state column (p.A_per_state) and/or the step per channel
-// (p.dt_per_channel); without it one decay factor per head.
-template <int N, typename T, bool GEN>
+// (p.dt_per_channel); without it one decay factor per head.  GATE: p.z is given (its rows are loaded with x's,
+// not under a branch of their own, which would wait for them alone).
+template <int N, typename T, bool GEN, bool GATE>
 __global__ __launch_bounds__(1024) void ssu_kernel(SsuParams p) {
   constexpr int TPR = N / 4;        // threads per state row
   const int rp = blockDim.x / TPR;  // rows per pass
@@ -41,7 +42,7 @@ __global__ __launch_bounds__(1024) void ssu_kernel(SsuParams p) {
   f32x4* sout = reinterpret_cast<f32x4*>(p.state_out + sbase);
   const T* xp = reinterpret_cast<const T*>(p.x) + (int64_t)b * p.x_stride_b + (int64_t)h * P;
   T* yp = reinterpret_cast<T*>(p.y) + (int64_t)b * p.y_stride_b + (int64_t)h * P;
-  const T* zp = p.z ? reinterpret_cast<const T*>(p.z) + (int64_t)b * p.z_stride_b + (int64_t)h * P : nullptr;
+  const T* zp = GATE ? reinterpret_cast<const T*>(p.z) + (int64_t)b * p.z_stride_b + (int64_t)h * P : nullptr;
 
   // Loads use row indices clamped into [0, P) so they are straight-line code
   // (no per-row branches, hence no early waits); only the stores are guarded.
@@ -54,14 +55,13 @@ __global__ __launch_bounds__(1024) void ssu_kernel(SsuParams p) {
 #pragma unroll
     for (int i = 0; i < SSU_ROWS; ++i) s[i] = __builtin_nontemporal_load(&sin[min(pbase + i * rp, P - 1) * TPR + ln]);
 #pragma unroll
-    for (int i = 0; i < SSU_ROWS; ++i) xv[i] = to_f32(xp[min(pbase + i * rp, P - 1)]);
+    for (int i = 0; i < SSU_ROWS; ++i) {
+      xv[i] = to_f32(xp[min(pbase + i * rp, P - 1)]);
+      if constexpr (GATE) zv[i] = to_f32(zp[min(pbase + i * rp, P - 1)]);
+    }
     if (Dc) {
 #pragma unroll
       for (int i = 0; i < SSU_ROWS; ++i) dv[i] = Dc[min(pbase + i * rp, P - 1)];
-    }
-    if (zp) {
-#pragma unroll
-      for (int i = 0; i < SSU_ROWS; ++i) zv[i] = to_f32(zp[min(pbase + i * rp, P - 1)]);
     }
     if (dtc) {
 #pragma unroll
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(1024) void ssu_kernel(SsuParams p) {
         for (int off = TPR / 2; off > 0; off >>= 1) part += __shfl_xor(part, off, TPR);
         if (ln == 0) {
           float yv = part + (Dc ? dv[i] : Dh) * xv[i];
-          if (zp) yv *= silu_f(zv[i]);                 // z-gate of mamba2.py:337-338
+          if constexpr (GATE) yv *= silu_f(zv[i]);     // z-gate of mamba2.py:337-338
           yp[pr] = from_f32<T>(yv);
         }
       }
@@ -138,14 +138,20 @@ static hipError_t launch_ssu_n(const SsuParams& p, hipStream_t st) {
   if (rows * TPR > 1024) rows = 1024 / TPR;
   const int threads = ((rows * TPR + 63) / 64) * 64;   // whole waves; extra lanes fall past P
   dim3 grid((unsigned)(p.batch * p.nheads)), block((unsigned)threads);
-  const bool gen = p.A_per_state || p.dt_per_channel;
-  if (p.dtype == DT_BF16) {
-    if (gen) hipLaunchKernelGGL((ssu_kernel<N, bf16, true>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((ssu_kernel<N, bf16, false>), grid, block, 0, st, p);
-  } else {
-    if (gen) hipLaunchKernelGGL((ssu_kernel<N, float, true>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((ssu_kernel<N, float, false>), grid, block, 0, st, p);
-  }
+  const bool gen = p.A_per_state || p.dt_per_channel, gate = p.z != nullptr;
+#define SSU_LAUNCH(T)                                                                              \
+  do {                                                                                             \
+    if (gen) {                                                                                     \
+      if (gate) hipLaunchKernelGGL((ssu_kernel<N, T, true, true>), grid, block, 0, st, p);         \
+      else hipLaunchKernelGGL((ssu_kernel<N, T, true, false>), grid, block, 0, st, p);             \
+    } else {                                                                                       \
+      if (gate) hipLaunchKernelGGL((ssu_kernel<N, T, false, true>), grid, block, 0, st, p);        \
+      else hipLaunchKernelGGL((ssu_kernel<N, T, false, false>), grid, block, 0, st, p);            \
+    }                                                                                              \
+  } while (0)
+  if (p.dtype == DT_BF16) SSU_LAUNCH(bf16);
+  else SSU_LAUNCH(float);
+#undef SSU_LAUNCH
   return hipGetLastError();
 }
 
