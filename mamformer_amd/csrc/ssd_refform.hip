@@ -57,6 +57,51 @@ __device__ __forceinline__ float row_sum16(float v) {
   return v;
 }
 
+// Lane-crossing moves within 16-lane rows (DPP): the value of lane l ^ 8, ^ 4, ^ 2, ^ 1 of the same row.
+__device__ __forceinline__ float xor8(float v) { return dppf<0x128>(v); }       // row_ror:8
+__device__ __forceinline__ float xor4(float v) {
+  // lanes 4-7 and 12-15 (banks 1, 3) read lane l - 4, lanes 0-3 and 8-11 (banks 0, 2) lane l + 4
+  const int a = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xa, false);   // row_shr:4
+  return __int_as_float(__builtin_amdgcn_update_dpp(a, __float_as_int(v), 0x104, 0xf, 0x5, false));   // row_shl:4
+}
+__device__ __forceinline__ float xor2(float v) { return dppf<0x4E>(v); }        // quad_perm 2,3,0,1
+__device__ __forceinline__ float xor1(float v) { return dppf<0xB1>(v); }        // quad_perm 1,0,3,2
+
+// One step of the reduce-scatter below: the lanes with lane bit M set keep the upper half of their first K
+// values and hand the lower half to the partner l ^ M, which keeps its lower half.
+template <int M, int K>
+__device__ __forceinline__ void rf_rs_step(float (&v)[32], int l) {
+  const bool up = (l & M) != 0;
+#pragma unroll
+  for (int k = 0; k < K / 2; ++k) {
+    const float keep = up ? v[k + K / 2] : v[k], send = up ? v[k] : v[k + K / 2];
+    float r;
+    if constexpr (M == 8) r = xor8(send);
+    else if constexpr (M == 4) r = xor4(send);
+    else if constexpr (M == 2) r = xor2(send);
+    else r = xor1(send);
+    v[k] = keep + r;
+  }
+}
+
+// Sums of v[t] (t < 32) over the 32 lanes of a channel (lanes 32 c .. 32 c + 31, two 16-lane rows), lane g of
+// the channel ending with the sum for t = g: one exchange-and-add per value pair and step, 31 for 32 tokens,
+// where a separate row sum per token took five dependent DPP additions.
+__device__ __forceinline__ float rf_reduce_scatter32(float (&v)[32], int l) {
+  // lane bit 16: v_permlane16_swap trades the odd rows of its first operand with the even rows of its second,
+  // so row 0 of the channel ends with v[k] of both rows and row 1 with v[k + 16] of both
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 16]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  rf_rs_step<8, 16>(v, l);
+  rf_rs_step<4, 8>(v, l);
+  rf_rs_step<2, 4>(v, l);
+  rf_rs_step<1, 2>(v, l);
+  return v[0];
+}
+
 // 8 consecutive elements of a row: load, convert to fp32, pack from fp32, store.
 template <typename T> struct Row8;
 template <> struct Row8<bf16> {
@@ -93,9 +138,10 @@ template <> struct Row8<float> {
 };
 
 template <int N, int TB, int CPB>
-struct RfStage {
-  float B[TB][N];
-  float C[TB][N];
+struct __align__(16) RfStage {
+  // 16-byte aligned rows, so that a lane's 4 states of B and C are one 16-byte LDS read at an immediate offset
+  __align__(16) float B[TB][N];
+  __align__(16) float C[TB][N];
   float dt[TB][CPB];        // processed dt (0 past the sequence)
   float x[TB][CPB];         // x (0 past the sequence)
   float z[TB][CPB];         // gate (GATE only)
@@ -252,6 +298,29 @@ __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
   for (int k = 0; k < nblk; ++k) {
     const RfStage<N, TB, CPB>& s = sm.st[k & 1];
     float (*ys)[CPB] = sm.y[k & 1];
+    if constexpr (!CKPT && TB == LPC && LPC == 32) {
+      // the block's 32 tokens unrolled: every token's y is left as one partial per lane, and a reduce-scatter
+      // over the channel's 32 lanes after the block hands lane g the sum for token g
+      float yacc[32];
+#pragma unroll
+      for (int t = 0; t < TB; ++t) {
+        RfTok<NS> o;
+        rf_tok<N, TB, CPB, NS>(s, t, cl, n0, o);
+        const float u = o.dt * o.x;
+        float yp = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < NS; ++s2) {
+          const float a = __builtin_amdgcn_exp2f(o.dt * k2[s2]);
+          h[s2] = fmaf(a, h[s2], u * o.b[s2]);
+          yp = fmaf(o.c[s2], h[s2], yp);
+        }
+        yacc[t] = yp;
+      }
+      float yv = rf_reduce_scatter32(yacc, lane);
+      yv += Dc * s.x[g][cl];
+      if constexpr (GATE) yv *= silu_f(s.z[g][cl]);
+      ys[g][cl] = yv;
+    } else {
     RfTok<NS> cur, nxt;
     rf_tok<N, TB, CPB, NS>(s, 0, cl, n0, cur);
 #pragma unroll 2
@@ -285,6 +354,7 @@ __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
         }
       }
       cur = nxt;
+    }
     }
     if (k + 1 < nblk) rf_store<T, N, TB, CPB, GATE>(p, r, sm.st[(k + 1) & 1], (k + 1) * TB, bias4);
     if (k + 2 < nblk) rf_load<T, N, TB, CPB, GATE>(p, r, b, c0, (k + 2) * TB);
