@@ -543,8 +543,11 @@ __device__ __forceinline__ float rf_dt_chain(const RfParams& p, float raw, float
 }
 
 template <int N, int RK, int CPB>
-struct RfbChanSmem {
-  float B[RK][N], C[RK][N], G[RK][N];      // G = dhs / d_inner
+struct __align__(16) RfbChanSmem {
+  // 16-byte aligned rows: a lane's consecutive states of B, C and G are 16-byte LDS reads
+  __align__(16) float B[RK][N];
+  __align__(16) float C[RK][N];
+  __align__(16) float G[RK][N];            // G = dhs / d_inner
   float dt[RK][CPB], chain[RK][CPB], x[RK][CPB], dy[RK][CPB];
   float dx[RK][CPB], ddt[RK][CPB];
 };
