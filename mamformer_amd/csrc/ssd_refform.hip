@@ -69,8 +69,8 @@ __device__ __forceinline__ float xor1(float v) { return dppf<0xB1>(v); }        
 
 // One step of the reduce-scatter below: the lanes with lane bit M set keep the upper half of their first K
 // values and hand the lower half to the partner l ^ M, which keeps its lower half.
-template <int M, int K>
-__device__ __forceinline__ void rf_rs_step(float (&v)[32], int l) {
+template <int M, int K, int NV>
+__device__ __forceinline__ void rf_rs_step(float (&v)[NV], int l) {
   const bool up = (l & M) != 0;
 #pragma unroll
   for (int k = 0; k < K / 2; ++k) {
@@ -90,6 +90,25 @@ __device__ __forceinline__ void rf_rs_step(float (&v)[32], int l) {
 __device__ __forceinline__ float rf_reduce_scatter32(float (&v)[32], int l) {
   // lane bit 16: v_permlane16_swap trades the odd rows of its first operand with the even rows of its second,
   // so row 0 of the channel ends with v[k] of both rows and row 1 with v[k + 16] of both
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 16]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  rf_rs_step<8, 16>(v, l);
+  rf_rs_step<4, 8>(v, l);
+  rf_rs_step<2, 4>(v, l);
+  rf_rs_step<1, 2>(v, l);
+  return v[0];
+}
+
+// The same over all 64 lanes of the wave: lane l ends with the sum of v[l] (v_permlane32_swap first).
+__device__ __forceinline__ float rf_reduce_scatter64(float (&v)[64], int l) {
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 32]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 16]), false, false);
@@ -423,39 +442,33 @@ __global__ __launch_bounds__(RF_NT) void rf_hs_kernel(RfParams p) {
     if (tid < HS_TB) sB[0][tid] = bn;
     __syncthreads();
   }
-  const bool u32 = lane & 32, u16 = lane & 16;
+  static_assert(HS_TB * HS_NS == 64, "one value of the block per lane after the reduce-scatter");
   for (int k = 0; k < nblk; ++k) {
-    float dc[HS_TB], xc[HS_TB];
+    // the block's steps first (no branch per token: dt and u are 0 for a channel past d_inner or a token past
+    // the sequence, whose raw values are finite clamped reads)
+    float dtv[HS_TB], uu[HS_TB];
 #pragma unroll
     for (int j = 0; j < HS_TB; ++j) {
-      dc[j] = dn[j];
-      xc[j] = xn[j];
+      const float in = (on && k * HS_TB + j < p.seqlen) ? 1.f : 0.f;
+      dtv[j] = rf_dt(p, dn[j], bias) * in;
+      uu[j] = dtv[j] * xn[j];
     }
     if (k + 1 < nblk) load((k + 1) * HS_TB);
-#pragma unroll 4
+    // every token's 4 states stay one value per lane (v[4 j + s]); one reduce-scatter over the wave's 64
+    // channels after the block leaves lane l the sum for token l / 4, state l % 4 (per-token sums took
+    // three swaps and a DPP row sum each)
+    float v[64];
+#pragma unroll
     for (int j = 0; j < HS_TB; ++j) {
-      const int t = k * HS_TB + j;
-      const bool valid = on && t < p.seqlen;
-      const float dtv = valid ? rf_dt(p, dc[j], bias) : 0.f;
-      const float u = dtv * (valid ? xc[j] : 0.f);
       const float4 b4 = sB[k & 1][j];
       const float bv[HS_NS] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
-      for (int s = 0; s < HS_NS; ++s) h[s] = fmaf(__builtin_amdgcn_exp2f(dtv * k2[s]), h[s], u * bv[s]);
-      // reduce-scatter over the wave: v_permlane32_swap leaves the lower half-wave states 0-1 and the upper
-      // states 2-3, each summed over its pair of lanes; v_permlane16_swap splits them again within each half;
-      // the DPP row sum then adds the 16 lanes of a row.  Row r (lanes 16 r ..) holds state r.
-      float v2[2];
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(h[q]), __float_as_uint(h[q + 2]), false, false);
-        v2[q] = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+      for (int s = 0; s < HS_NS; ++s) {
+        h[s] = fmaf(__builtin_amdgcn_exp2f(dtv[j] * k2[s]), h[s], uu[j] * bv[s]);
+        v[HS_NS * j + s] = h[s];
       }
-      const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(v2[0]), __float_as_uint(v2[1]), false, false);
-      float v1 = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
-      v1 = row_sum16(v1);
-      if ((lane & 15) == 0) red[w][j][2 * (int)u32 + (int)u16] = v1;
     }
+    red[w][lane / HS_NS][lane % HS_NS] = rf_reduce_scatter64(v, lane);
     if (k + 1 < nblk && tid < HS_TB) sB[(k + 1) & 1][tid] = bn;
     __syncthreads();
     if (tid < HS_TB * HS_NS) {
