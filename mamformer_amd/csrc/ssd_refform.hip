@@ -102,6 +102,24 @@ __device__ __forceinline__ float rf_reduce_scatter32(float (&v)[32], int l) {
   return v[0];
 }
 
+// 32 values over all 64 lanes of the wave: lanes 2 m and 2 m + 1 end with the sum of v[m].
+__device__ __forceinline__ float rf_reduce_scatter64_32(float (&v)[32], int l) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 16]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 8]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  rf_rs_step<8, 8>(v, l);
+  rf_rs_step<4, 4>(v, l);
+  rf_rs_step<2, 2>(v, l);
+  return v[0] + xor1(v[0]);
+}
+
 // The same over all 64 lanes of the wave: lane l ends with the sum of v[l] (v_permlane32_swap first).
 __device__ __forceinline__ float rf_reduce_scatter64(float (&v)[64], int l) {
 #pragma unroll
@@ -811,36 +829,30 @@ __global__ __launch_bounds__(RF_NT) void rf_bwd_state_kernel(RfParams p) {
         hs[t][s] = h[s];
       }
     }
+    // the piece's tokens backwards, in groups of 4: each token's 4-vectors of the dB and dC sums stay one value
+    // per lane (v[4 ti + s] and v[16 + 4 ti + s]) and one reduce-scatter over the wave's 64 channels after the
+    // group leaves lanes 2 m, 2 m + 1 the sum for (dB | dC by m / 16, token t + (m % 16) / 4, state m % 4)
+    static_assert(RK % 4 == 0, "whole groups of 4 tokens");
+    float v[32];
 #pragma unroll
     for (int t = RK - 1; t >= 0; --t) {
       const float4 c4 = sC[t], g4 = sG[t];
       const float cv[HS_NS] = {c4.x, c4.y, c4.z, c4.w}, gv[HS_NS] = {g4.x, g4.y, g4.z, g4.w};
       const float dx_ = dtv[t] * xv[t];
-      float vb[HS_NS], vc[HS_NS];
+      const int ti = t % 4;
 #pragma unroll
       for (int s = 0; s < HS_NS; ++s) {
         const float lam = lamc[s] + dyv[t] * cv[s] + gv[s];
         const float hprev = t > 0 ? hs[t - 1][s] : he[s];
-        vb[s] = lam * dx_;
-        vc[s] = dyv[t] * hs[t][s];
+        v[HS_NS * ti + s] = lam * dx_;
+        v[16 + HS_NS * ti + s] = dyv[t] * hs[t][s];
         dA_acc[s] = fmaf(lam * av[t][s], dtv[t] * hprev, dA_acc[s]);
         lamc[s] = av[t][s] * lam;
       }
-      // reduce-scatter of each 4-vector over the wave (as in rf_hs_kernel): row r of lanes holds state r
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const float* v = q ? vc : vb;
-        float v2[2];
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 2]), false,
-                                                           false);
-          v2[k] = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
-        }
-        const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(v2[0]), __float_as_uint(v2[1]), false, false);
-        float v1 = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
-        v1 = row_sum16(v1);
-        if ((lane & 15) == 0) red[w][t][HS_NS * q + 2 * (int)u32 + (int)u16] = v1;
+      if (ti == 0) {
+        const float r = rf_reduce_scatter64_32(v, lane);
+        const int m = lane >> 1;
+        if ((lane & 1) == 0) red[w][t + ((m & 15) >> 2)][HS_NS * (m >> 4) + (m & 3)] = r;
       }
     }
     __syncthreads();
