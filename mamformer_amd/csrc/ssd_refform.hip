@@ -102,6 +102,19 @@ __device__ __forceinline__ float rf_reduce_scatter32(float (&v)[32], int l) {
   return v[0];
 }
 
+// 16 values over the 32 lanes of a channel: lanes 2 m and 2 m + 1 of the channel end with the sum of v[m].
+__device__ __forceinline__ float rf_reduce_scatter32_16(float (&v)[16], int l) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 8]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  rf_rs_step<8, 8>(v, l);
+  rf_rs_step<4, 4>(v, l);
+  rf_rs_step<2, 2>(v, l);
+  return v[0] + xor1(v[0]);
+}
+
 // 32 values over all 64 lanes of the wave: lanes 2 m and 2 m + 1 end with the sum of v[m].
 __device__ __forceinline__ float rf_reduce_scatter64_32(float (&v)[32], int l) {
 #pragma unroll
@@ -687,6 +700,42 @@ __global__ __launch_bounds__(RF_NT) void rf_bwd_chan_kernel(RfParams p) {
       }
     }
     // backward through it
+    if constexpr (LPC == 32 && RK == 16) {
+      // every token's two sums over the states (du, qq) stay one value per lane; after each group of 8 tokens one
+      // reduce-scatter over the channel's 32 lanes leaves lanes 2 m, 2 m + 1 the sum for du (m < 8) or qq (m >= 8)
+      // of token t + m % 8
+      float vv[16];
+#pragma unroll
+      for (int t = RK - 1; t >= 0; --t) {
+        const float dyv = sm.dy[t][cl];
+        float du = 0.f, qq = 0.f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const float lam = lamc[s] + dyv * sm.C[t][n0 + s] + sm.G[t][n0 + s];
+          du = fmaf(lam, sm.B[t][n0 + s], du);
+          qq = fmaf(lam * As[s], av[t][s] * hp[t][s], qq);
+          lamc[s] = av[t][s] * lam;
+        }
+        vv[t % 8] = du;
+        vv[8 + t % 8] = qq;
+        if (t % 8 == 0) {
+          const float r = rf_reduce_scatter32_16(vv, lane);
+          // v_permlane16_swap of the value with itself: the first row's lanes hold du (first) and, from the second
+          // row, qq (second) of token t + g / 2; its even lanes finish the token
+          const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(r), __float_as_uint(r), false, false);
+          if (g < 16 && (g & 1) == 0) {
+            const int tk = t + (g >> 1);
+            const float du = __uint_as_float(pr[0]), qq = __uint_as_float(pr[1]);
+            const float dyk = sm.dy[tk][cl], dtv = sm.dt[tk][cl], xv = sm.x[tk][cl];
+            const float ddr = (qq + xv * du) * sm.chain[tk][cl];
+            sm.dx[tk][cl] = dtv * du + Dc * dyk;
+            sm.ddt[tk][cl] = ddr;
+            dD_acc = fmaf(dyk, xv, dD_acc);
+            db_acc += ddr;
+          }
+        }
+      }
+    } else {
 #pragma unroll
     for (int t = RK - 1; t >= 0; --t) {
       const float dyv = sm.dy[t][cl];
@@ -713,6 +762,7 @@ __global__ __launch_bounds__(RF_NT) void rf_bwd_chan_kernel(RfParams p) {
         db_acc += ddr;
       }
     }
+    }
     __syncthreads();
     for (int e = tid; e < RK * CPB; e += RF_NT) {
       const int t = e / CPB, q = e % CPB, tt = t0 + t;
@@ -728,7 +778,15 @@ __global__ __launch_bounds__(RF_NT) void rf_bwd_chan_kernel(RfParams p) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) o[s] = lamc[s];
   }
-  if (ylane) {
+  if constexpr (LPC == 32 && RK == 16) {
+    // the first row's lanes hold the channel's partial sums over their tokens
+    dD_acc = row_sum16(dD_acc);
+    db_acc = row_sum16(db_acc);
+    if (g == 0) {
+      p.dD_part[(int64_t)b * di + c] = dD_acc;
+      p.dbias_part[(int64_t)b * di + c] = db_acc;
+    }
+  } else if (ylane) {
     p.dD_part[(int64_t)b * di + c] = dD_acc;
     p.dbias_part[(int64_t)b * di + c] = db_acc;
   }
