@@ -348,12 +348,23 @@ __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
   for (int k = 0; k < nblk; ++k) {
     const RfStage<N, TB, CPB>& s = sm.st[k & 1];
     float (*ys)[CPB] = sm.y[k & 1];
-    if constexpr (!CKPT && TB == LPC && LPC == 32) {
+    if constexpr (TB == LPC && LPC == 32) {
       // the block's 32 tokens unrolled: every token's y is left as one partial per lane, and a reduce-scatter
-      // over the channel's 32 lanes after the block hands lane g the sum for token g
+      // over the channel's 32 lanes after the block hands lane g the sum for token g (CKPT: no y; the state
+      // entering every piece is stored)
       float yacc[32];
 #pragma unroll
       for (int t = 0; t < TB; ++t) {
+        if constexpr (CKPT) {
+          constexpr int RK = rf_rk<N>();                   // divides TB: a piece starts where t % RK == 0
+          const int tt = k * TB + t;
+          if (t % RK == 0 && tt < p.seqlen) {
+            const int nsb = (p.seqlen + RK - 1) / RK;
+            float* o = p.ckpt + (((int64_t)b * nsb + tt / RK) * p.d_inner + c) * N + n0;
+#pragma unroll
+            for (int s2 = 0; s2 < NS; ++s2) o[s2] = h[s2];
+          }
+        }
         RfTok<NS> o;
         rf_tok<N, TB, CPB, NS>(s, t, cl, n0, o);
         const float u = o.dt * o.x;
@@ -366,10 +377,12 @@ __global__ __launch_bounds__(RF_NT) void rf_scan_kernel(RfParams p) {
         }
         yacc[t] = yp;
       }
-      float yv = rf_reduce_scatter32(yacc, lane);
-      yv += Dc * s.x[g][cl];
-      if constexpr (GATE) yv *= silu_f(s.z[g][cl]);
-      ys[g][cl] = yv;
+      if constexpr (!CKPT) {
+        float yv = rf_reduce_scatter32(yacc, lane);
+        yv += Dc * s.x[g][cl];
+        if constexpr (GATE) yv *= silu_f(s.z[g][cl]);
+        ys[g][cl] = yv;
+      }
     } else {
     RfTok<NS> cur, nxt;
     rf_tok<N, TB, CPB, NS>(s, 0, cl, n0, cur);
