@@ -853,13 +853,16 @@ __global__ __launch_bounds__(NT) void kda_ref_bwd_kv_kernel(KdaBwdParams q) {
       }
     }
 
-    const int s_ = 32 * st + l32;
+    // the row and column of this lane from a lane index recomputed here: hoisted out of the chunk loop, the
+    // per-lane row pointers were spilled, and each reload waited for every outstanding load
+    const int lh = lane_id_here();
+    const int s_ = 32 * st + (lh & 31), hh = lh >> 5;
     if (s_ < len) {
       bf16* dvrow = reinterpret_cast<bf16*>(q.dv) + (rowbase + pos + s_) * BD + 32 * x4;
       bf16* dkrow = reinterpret_cast<bf16*>(q.dk) + (rowbase + pos + s_) * BD + 32 * x4;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int k0 = 8 * g + 4 * half;
+        const int k0 = 8 * g + 4 * hh;
         const bf16x4 ph = *reinterpret_cast<const bf16x4*>(&sm.PK[s_ * P128 + 32 * x4 + k0]);
         bf16x4 ov, ok;
 #pragma unroll

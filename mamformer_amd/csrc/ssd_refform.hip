@@ -171,18 +171,18 @@ template <> struct Row8<bf16> {
   }
 };
 template <> struct Row8<float> {
-  float4 a, b;
+  f32x4 a, b;                  // (vector types that stay in registers: a struct of float4 went to scratch)
   __device__ __forceinline__ void load(const float* p) {
-    a = reinterpret_cast<const float4*>(p)[0];
-    b = reinterpret_cast<const float4*>(p)[1];
+    a = reinterpret_cast<const f32x4*>(p)[0];
+    b = reinterpret_cast<const f32x4*>(p)[1];
   }
   __device__ __forceinline__ void set(const float* s) {
-    a = float4{s[0], s[1], s[2], s[3]};
-    b = float4{s[4], s[5], s[6], s[7]};
+    a = f32x4{s[0], s[1], s[2], s[3]};
+    b = f32x4{s[4], s[5], s[6], s[7]};
   }
   __device__ __forceinline__ void store(float* d) const {
-    reinterpret_cast<float4*>(d)[0] = a;
-    reinterpret_cast<float4*>(d)[1] = b;
+    reinterpret_cast<f32x4*>(d)[0] = a;
+    reinterpret_cast<f32x4*>(d)[1] = b;
   }
   __device__ __forceinline__ void store_f32(float* d) const { store(d); }
 };
