@@ -224,6 +224,16 @@ __device__ __forceinline__ void rf_block(int nblk, int nper, int& b, int& cb) {
   cb = j % nper;
 }
 
+// Workgroup index of the channel-major walks (rf_hs_kernel, rf_bwd_state_kernel: (batch, channel block, state
+// group), state group fastest), remapped so that each XCD runs a contiguous range of them: the state groups of a
+// channel block then read its rows of dt, x and dy through one L2 (workgroups are dealt to the 8 XCDs
+// round-robin; dealt as they come, each row was fetched by all eight).
+__device__ __forceinline__ int rf_xcd_block() {
+  const int i = blockIdx.x, n = gridDim.x;
+  if (n % 8 != 0) return i;
+  return (i & 7) * (n >> 3) + (i >> 3);
+}
+
 // Loads only (every one unconditional at a clamped row), so that they stay in flight while the current block
 // computes: the values are converted, masked and stored to LDS by rf_store a block later.
 template <typename T, int N, int TB, int CPB, bool GATE>
@@ -447,7 +457,7 @@ __global__ __launch_bounds__(RF_NT) void rf_hs_kernel(RfParams p) {
   __shared__ float red[4][HS_TB][HS_NS];
   __shared__ float4 sB[2][HS_TB];                          // the group's 4 states of B per token
   const int ncb = (p.d_inner + HS_CPB - 1) / HS_CPB, ngs = N / HS_NS;
-  const int i = blockIdx.x;
+  const int i = rf_xcd_block();
   const int gs = i % ngs, cblk = (i / ngs) % ncb, b = i / (ngs * ncb);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c = cblk * HS_CPB + tid;
@@ -813,7 +823,7 @@ __global__ __launch_bounds__(RF_NT) void rf_bwd_state_kernel(RfParams p) {
   __shared__ float red[4][RK][2 * HS_NS];
   const int L = p.seqlen, di = p.d_inner;
   const int ncb = (di + HS_CPB - 1) / HS_CPB, ngs = N / HS_NS;
-  const int i = blockIdx.x;
+  const int i = rf_xcd_block();
   const int gs = i % ngs, cblk = (i / ngs) % ncb, b = i / (ngs * ncb);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c = cblk * HS_CPB + tid;
