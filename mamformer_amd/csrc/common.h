@@ -156,6 +156,31 @@ __device__ __forceinline__ float sum_halves(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// A wave's 16 floats per lane parked in LDS as four planes of 16-byte pieces (plane k holds elements 4k .. 4k + 3
+// of every lane, lanes contiguous): each wave-wide 16-byte access is 1 KB contiguous, free of bank conflicts (a
+// 64-byte lane stride puts four lanes of every 16 on one bank).
+struct AccPark {
+  f32x4 p[4][64];
+};
+__device__ __forceinline__ void park_acc(AccPark& d, const float (&v)[16], int lane) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) d.p[k][lane] = f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+}
+__device__ __forceinline__ void park_acc(AccPark& d, const f32x16& v, int lane) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) d.p[k][lane] = f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+}
+__device__ __forceinline__ f32x16 unpark_acc(const AccPark& d, int lane) {
+  f32x16 v;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const f32x4 q = d.p[k][lane];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[4 * k + j] = q[j];
+  }
+  return v;
+}
+
 // Sum over each group of 4 lanes (quad permutes on the DPP crossbar), the same in the 4 lanes.
 __device__ __forceinline__ float sum_quad(float v) {
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));   // quad_perm 1,0,3,2

@@ -434,10 +434,10 @@ struct KdaRefSmem {
   alignas(16) float z[DK];               // running sum of phi(k) before this segment
   float zq[NQ][SEGK];                    // phi(q_i,t) . z
   float nrm[NQ][3][32];                  // row sums of the masked A tiles
-  f32x16 red[2][NQ][2][64];              // k-half 1 read-out partials: vt, query, t-tile, lane
+  AccPark red[2][NQ][2];                 // k-half 1 read-out partials: vt, query, t-tile
   Frag<bf16> A[3 * NQ][2][64];           // masked A^T tiles as B-operand fragments (bf16 high part)
   Frag<bf16> Alo[3 * NQ][2][64];         // ... and the bf16 rounding remainder (A = A + Alo to ~2^-17)
-  float xb[NQ == 2 ? 2 : 1][2][64][16];  // fused differential output: query 2's normalised rows (vt, tt, lane)
+  AccPark xb[NQ == 2 ? 2 : 1][2];        // fused differential output: query 2's normalised rows (vt, tt)
 };
 
 // Threads of a reference-mode workgroup: 4 waves per query stream (v-tile x k-half each).
@@ -676,7 +676,7 @@ __global__ __launch_bounds__(256 * NQ) void kda_ref_kernel(KdaParams p) {
         o[0] = mma(vf[c], sm.A[3 * qw + 0][c][l], o[0]);
         o[0] = mma(vf[c], sm.Alo[3 * qw + 0][c][l], o[0]);
       }
-      sm.red[vt][qw][1][l] = o[1];
+      park_acc(sm.red[vt][qw][1], o[1], l);
     } else {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -685,7 +685,7 @@ __global__ __launch_bounds__(256 * NQ) void kda_ref_kernel(KdaParams p) {
         o[1] = mma(vf[2 + c], sm.A[3 * qw + 2][c][l], o[1]);
         o[1] = mma(vf[2 + c], sm.Alo[3 * qw + 2][c][l], o[1]);
       }
-      sm.red[vt][qw][0][l] = o[0];
+      park_acc(sm.red[vt][qw][0], o[0], l);
     }
     // state update (no decay): S[k][v] += sum_s phi(k_s)[k] v_s[v]
 #pragma unroll
@@ -706,7 +706,7 @@ __global__ __launch_bounds__(256 * NQ) void kda_ref_kernel(KdaParams p) {
       if (valid) {
         const float nr = sm.zq[qw][tl] + (tt == 0 ? sm.nrm[qw][0][l32] : sm.nrm[qw][1][l32] + sm.nrm[qw][2][l32]);
         const float inv = 1.f / (nr + 1e-8f);
-        const f32x16 other = sm.red[vt][qw][tt][l];
+        const f32x16 other = unpark_acc(sm.red[vt][qw][tt], l);
 #pragma unroll
         for (int r = 0; r < 16; ++r) res[r] = (o[tt][r] + other[r]) * inv;
       }
@@ -722,17 +722,13 @@ __global__ __launch_bounds__(256 * NQ) void kda_ref_kernel(KdaParams p) {
       __syncthreads();
     } else {
       // the differential combination (o1 - lam o2) / (1 - lam + 1e-8): query 2's waves hand their rows over
-      if (qw == 1 && valid) {
-#pragma unroll
-        for (int r = 0; r < 16; r += 4)
-          *reinterpret_cast<f32x4*>(&sm.xb[vt][kh][l][r]) = f32x4{res[r], res[r + 1], res[r + 2], res[r + 3]};
-      }
+      if (qw == 1 && valid) park_acc(sm.xb[vt][kh], res, l);
       __syncthreads();
       if (qw == 0 && valid) {
         bf16* orow = op[0] + (rowbase + pos + tl) * 128 + v0 + 32 * vt;
 #pragma unroll
         for (int r = 0; r < 16; r += 4) {
-          const f32x4 r2 = *reinterpret_cast<const f32x4*>(&sm.xb[vt][kh][l][r]);
+          const f32x4 r2 = sm.xb[vt][kh].p[r >> 2][l];
 #pragma unroll
           for (int j = 0; j < 4; ++j) orow[acc_row(half, r + j)] = (bf16)((res[r + j] - lam * r2[j]) * inv_1ml);
         }
