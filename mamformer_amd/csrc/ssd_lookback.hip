@@ -6,7 +6,7 @@
 // -- the reference's selective_scan (mamformer/layers/mamba2.py:84-126) in the per-head SSD form, with an
 // optional initial state and the final state returned for the decode cache.
 //
-// Pass 1, ssd_lb_state_kernel, one workgroup per (chunk, batch, block of HG heads): the chunk-local state
+// Pass 1, ssd_lb_state_kernel, one workgroup per (chunk, batch, block of heads): the chunk-local state
 //     S_k[p, n] = sum_{s in k} exp(sum_{s < tau in k} A dt_tau) dt_s x_s[p] B_s[n]
 // and the chunk's total log-decay T_k.  The chunk is walked from its last 64-token segment to its first, so
 // every decay factor is taken relative to the chunk end and is at most 1: the accumulators never need
@@ -306,8 +306,13 @@ struct LbStateStage {
   bf16 Bt[N / 32][Sub64::ELEMS];  // B tile
   float dt[HG][SEG];              // per head: raw dt
 };
+// Pass 1 on chunks of at most LB_STATE_SHORT tokens runs two heads per workgroup with two stages (66.5 KB of
+// LDS at N = 128), so that two workgroups share a CU and overlap their ramp-up and drain (b2 L4096 H64 N128,
+// chunk 512: 21.6 against 22.4 us with four heads and three stages, one workgroup per CU); longer chunks are
+// long streams from HBM that prefer the third stage (b1 L131072 H128, chunk 16384: 2% slower with two heads).
+constexpr int LB_STATE_SHORT = 1024;
 template <int N, int HG>
-constexpr int lb_state_nbuf = 3 * sizeof(LbStateStage<N, HG>) <= LB_LDS_BYTES ? 3 : 2;
+constexpr int lb_state_nbuf = (HG > 2 && 3 * sizeof(LbStateStage<N, HG>) <= LB_LDS_BYTES) ? 3 : 2;
 
 // Segment si of the chunk into a pass-1 stage: every wave issues exactly N / 8 / NW + 4 PH + 1 loads (its
 // share of the B tile, its halves of its head's x tile, its head's dt; rows past the end of the sequence are
@@ -355,7 +360,7 @@ __device__ __forceinline__ void lb_state_segment(const SsdParams& p, const LbWav
 }
 
 template <int N, int HG, int PH>
-__global__ __launch_bounds__(64 * HG * (2 / PH)) void ssd_lb_state_kernel(SsdParams p) {
+__global__ __launch_bounds__(64 * HG * (2 / PH), HG <= 2 ? 2 : 1) void ssd_lb_state_kernel(SsdParams p) {
   constexpr int NT = N / 32;
   constexpr int NBUF = lb_state_nbuf<N, HG>;
   static_assert((N / 8) % lb_waves<HG, PH> == 0, "B tile split evenly over the waves");
@@ -812,7 +817,12 @@ template <int N, int HG>
 hipError_t launch_lb_t(const SsdParams& p, hipStream_t stream) {
   constexpr int NW = lb_waves<HG, LB_PH>;
   dim3 grid((unsigned)(p.nchunks * p.batch * (p.nheads / HG)));
-  hipLaunchKernelGGL((ssd_lb_state_kernel<N, HG, LB_PH>), grid, dim3(64 * NW), 0, stream, p);
+  constexpr int HS = HG < 2 ? HG : 2;                      // pass 1's heads per workgroup on short chunks
+  if (p.chunk_len <= LB_STATE_SHORT)
+    hipLaunchKernelGGL((ssd_lb_state_kernel<N, HS, LB_PH>), dim3((unsigned)(p.nchunks * p.batch * (p.nheads / HS))),
+                       dim3(64 * lb_waves<HS, LB_PH>), 0, stream, p);
+  else
+    hipLaunchKernelGGL((ssd_lb_state_kernel<N, HG, LB_PH>), grid, dim3(64 * NW), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.entering) {
