@@ -44,7 +44,7 @@ __device__ __forceinline__ float hs_dt(const SsdParams& p, float d, int h) {
 // The element loads are unconditional at clamped (valid) addresses, so that each thread's KB loads of a pass are
 // in flight together: an element past the end of the segment is zeroed by a factor 0 (its dt finite), and a thread
 // past the last element repeats the last one (the same value written twice).
-template <bool XS, typename Smem>
+template <bool XS, int KB, typename Smem>
 __device__ void hs_prologue_elems(const SsdParams& p, Smem& sm, int b, int si, int len, float* uws) {
   const int H = p.nheads, tid = threadIdx.x, tot = HS_SEG * H, nt = blockDim.x;
   const int64_t tok0 = (int64_t)si * HS_SEG;
@@ -52,7 +52,6 @@ __device__ void hs_prologue_elems(const SsdParams& p, Smem& sm, int b, int si, i
   const float* xsb = XS ? p.xsum + ((int64_t)b * p.seqlen + tok0) * H * 2 : nullptr;
   const float* bias = p.dt_bias ? p.dt_bias : p.A;       // any valid per-head array when there is no bias
   const float bmul = p.dt_bias ? 1.f : 0.f;
-  constexpr int KB = 8;
   // element e = tid + nt i is (t, h) = (e / H, e % H), stepped by (nt / H, nt % H) without a division per element
   const int dq = nt / H, dr = nt % H;
   int te = tid / H, he = tid % H;
@@ -97,14 +96,15 @@ __device__ void hs_prologue_elems(const SsdParams& p, Smem& sm, int b, int si, i
   }
 }
 
-template <typename T, typename Smem>
+// KB: elements per thread and pass (KB x the workgroup's threads = 2048 covers a segment of 64 heads in one pass).
+template <typename T, int KB, typename Smem>
 __device__ void hs_prologue(const SsdParams& p, Smem& sm, int b, int si, int len, float* xs_out) {
   const int H = p.nheads, tid = threadIdx.x, tot = HS_SEG * H, nt = blockDim.x;
   const int64_t tok0 = (int64_t)si * HS_SEG;
   float* uws = xs_out ? xs_out + ((int64_t)b * p.seqlen + tok0) * H : nullptr;
   const bool xsb = p.xsum != nullptr;
-  if (xsb) hs_prologue_elems<true>(p, sm, b, si, len, uws);
-  else hs_prologue_elems<false>(p, sm, b, si, len, uws);
+  if (xsb) hs_prologue_elems<true, KB>(p, sm, b, si, len, uws);
+  else hs_prologue_elems<false, KB>(p, sm, b, si, len, uws);
   if (!xsb) {
     __syncthreads();                   // the element pass's repeated writes of the last element are done
     // xs[t][h] = sum_p x[t][h][p] (P = 64): one (token, head) row per thread pass, its 16 loads issued together
@@ -154,77 +154,101 @@ struct __align__(16) HsLocSmem {
   float cend[HS_MAXH];
 };
 
-// Workgroup (segment, batch, column block zb of nblk): the prologue, then
-//  - its share of the output pass's factors: W_g[t][s] for s = zb, zb + nblk, ... and all t, stored s-major (row s
-//    of WT holds W_g[.][s] over the 32 tokens, 0 for t < s), and Ei[h][t] = e^{c_t,h} for h = zb, zb + nblk, ...
-//    (0 past the end);
-//  - Zloc[h][n] = sum_s e^{c_end - c_s} u_s[h] B_s[n] for its HS_NB columns, as fp32 MFMAs (32 heads x 32 columns a
-//    tile, k over pairs of tokens, B read from global memory);
-//  - the segment's decays (zb = 0).
-// BWD: the backward's local pass instead: no W or Ei, xs per (token, head) written to q.u (column block 0), and
-// besides Zloc the segment's part of the adjoint handed left, GL[h][n] = sum_t e^{c_t} g_t[n] with g = dhs / (H P),
-// into q.lam (MFMA tiles like Zloc's, A = e^{c_t} (0 past the end), B = the block's columns of dhs).
+// W_g[t][s] = sum_{h in g} e^{c_t,h - c_s,h} u_s[h] for s <= t (every exponent c_t - c_s <= 0).
+__device__ __forceinline__ float hs_weight(const HsLocSmem& sm, int g, int hpg, int t, int s) {
+  float w = 0.f;
+  if (hpg % 4 == 0) {
+    for (int h = g * hpg; h < (g + 1) * hpg; h += 4) {
+      const f32x4 ct = *reinterpret_cast<const f32x4*>(&sm.c[t][h]);
+      const f32x4 cs = *reinterpret_cast<const f32x4*>(&sm.c[s][h]);
+      const f32x4 us = *reinterpret_cast<const f32x4*>(&sm.u[s][h]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w += __expf(ct[j] - cs[j]) * us[j];
+    }
+  } else {
+    for (int h = g * hpg; h < (g + 1) * hpg; ++h) w += __expf(sm.c[t][h] - sm.c[s][h]) * sm.u[s][h];
+  }
+  return w;
+}
+
+// Forward: HS_FS workgroups of HS_LOC_FWD threads per (segment, batch), each over every block of HS_NB state
+// columns, so that the prologue runs HS_FS times per segment instead of once per column block: the prologue,
+// then its share of
+//  - the output pass's factors: W_g[t][s] for the pairs s <= t (one pair per thread; the entries s > t are never
+//    written: the output pass masks them), stored s-major (row s of WT holds W_g[.][s] over the 32 tokens), and
+//    Ei[h][t] = e^{c_t,h} (0 past the end);
+//  - Zloc[h][n] = sum_s e^{c_end - c_s} u_s[h] B_s[n], one (column block, group, 32 heads) tile of fp32 MFMAs per
+//    wave at a time (32 heads x 32 columns, k over pairs of tokens, B read from global memory);
+//  - the segment's decays.
+// BWD: the backward's local pass, one workgroup of 256 threads per (segment, batch, column block zb): no W or
+// Ei, xs per (token, head) written to q.u (column block 0), and besides Zloc the segment's part of the adjoint
+// handed left, GL[h][n] = sum_t e^{c_t} g_t[n] with g = dhs / (H P), into q.lam (MFMA tiles like Zloc's,
+// A = e^{c_t} (0 past the end), B = the block's columns of dhs).
+// Forward workgroups per segment and their threads: 2 x 256 (b2 L4096 H64 N128 on one box, the three h_states
+// passes: 29.4 us, against 30.8 us with one workgroup per (segment, column block) and 29.9 / 32.4 us with
+// 1 x 512 / 4 x 128).
+constexpr int HS_FS = 2;
+constexpr int HS_LOC_FWD = 512 / HS_FS;
 template <typename T, bool BWD>
-__global__ __launch_bounds__(256) void ssd_hs_local_kernel(SsdParams p, HsParams q) {
+__global__ __launch_bounds__(BWD ? 256 : HS_LOC_FWD) void ssd_hs_local_kernel(SsdParams p, HsParams q) {
   __shared__ HsLocSmem sm;
-  const int si = blockIdx.x, b = blockIdx.y, zb = blockIdx.z, nblk = gridDim.z, n0 = HS_NB * zb;
+  const int si = blockIdx.x, b = blockIdx.y, zb = blockIdx.z;
+  // forward: workgroup zb of the segment's HS_FS takes, of each list (W pairs, Ei entries), the items
+  // fs0 + tid + k fstep, and of the Zloc tiles the units zb nw + wave + k ustep
+  const int fs0 = BWD ? 0 : zb * blockDim.x, fstep = BWD ? blockDim.x : HS_FS * blockDim.x;
   const int tid = threadIdx.x, H = p.nheads, N = p.dstate, G = p.ngroups, hpg = H / G;
   const int len = min(HS_SEG, p.seqlen - si * HS_SEG);
   const int64_t tok0 = (int64_t)si * HS_SEG;
-  const int l = lane_id(), i = l & 31, hf = l >> 5, tiles = (hpg + 31) / 32, nw = blockDim.x / 64;
-  const bool col = n0 + i < N;
+  const int l = lane_id(), i = l & 31, hf = l >> 5, tiles = (hpg + 31) / 32;
   // B operands of this wave's tile (k = token pairs), loaded before the prologue so that they arrive meanwhile;
   // unmasked at clamped addresses: a token past the end meets a zero A operand, a lane past the last column feeds
-  // an output column that is not stored.  Units [0, G tiles): Zloc of (group, 32 heads), B of the group's columns;
-  // BWD units [G tiles, 2 G tiles): GL, the columns of dhs.
-  const int nz = G * tiles, nunit = BWD ? 2 * nz : nz;
+  // an output column that is not stored.  Units of a column block: [0, G tiles) Zloc of (group, 32 heads), B of
+  // the group's columns; BWD [G tiles, 2 G tiles): GL, the columns of dhs.  The forward's unit u is unit u % per
+  // of column block u / per.
+  const int nz = G * tiles, per = BWD ? 2 * nz : nz, nunit = BWD ? per : per * ((N + HS_NB - 1) / HS_NB);
+  auto unit_n0 = [&](int unit) { return HS_NB * (BWD ? zb : unit / per); };
+  const int nw = blockDim.x / 64, ustep = BWD ? nw : HS_FS * nw;
   T bv[HS_SEG / 2];                    // converted at their use, so that nothing waits for them before
   auto load_b = [&](int unit) {
-    const T* Bg = unit < nz
-        ? reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)(unit / tiles) * N
+    const int n0 = unit_n0(unit), uu = unit % per;
+    const T* Bg = uu < nz
+        ? reinterpret_cast<const T*>(p.B) + (int64_t)b * p.B_sb + (int64_t)(uu / tiles) * N
         : reinterpret_cast<const T*>(q.dhs) + (int64_t)b * p.seqlen * N;
-    const int64_t ld = unit < nz ? p.B_sl : N;
+    const int64_t ld = uu < nz ? p.B_sl : N;
     Bg += n0 + min(i, N - 1 - n0);
 #pragma unroll
     for (int m = 0; m < HS_SEG / 2; ++m) bv[m] = Bg[(tok0 + min(2 * m + hf, len - 1)) * ld];
   };
-  int unit = wave_id();
+  int unit = (BWD ? 0 : zb * nw) + wave_id();
   if (unit < nunit) load_b(unit);
-  hs_prologue<T>(p, sm, b, si, len, (BWD && zb == 0) ? q.u : nullptr);
+  hs_prologue<T, BWD ? 8 : HS_SEG * 64 / HS_LOC_FWD>(p, sm, b, si, len, (BWD && zb == 0) ? q.u : nullptr);
   __syncthreads();
   if constexpr (!BWD) {
-    const int nrow = (HS_SEG - zb + nblk - 1) / nblk;
+    // pair r = t (t + 1) / 2 + s of group g (s <= t), t from the inverse triangular number (float estimate,
+    // corrected by one either way)
+    constexpr int NPAIR = HS_SEG * (HS_SEG + 1) / 2;
     float* wt = q.w + ((int64_t)b * p.nseg + si) * G * (HS_SEG * HS_SEG);
-    for (int e = tid; e < G * nrow * HS_SEG; e += blockDim.x) {
-      const int t = e % HS_SEG, s = zb + nblk * ((e / HS_SEG) % nrow), g = e / (HS_SEG * nrow);
-      float w = 0.f;
-      if (s <= t) {                    // every exponent c_t - c_s <= 0
-        if (hpg % 4 == 0) {
-          for (int h = g * hpg; h < (g + 1) * hpg; h += 4) {
-            const f32x4 ct = *reinterpret_cast<const f32x4*>(&sm.c[t][h]);
-            const f32x4 cs = *reinterpret_cast<const f32x4*>(&sm.c[s][h]);
-            const f32x4 us = *reinterpret_cast<const f32x4*>(&sm.u[s][h]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) w += __expf(ct[j] - cs[j]) * us[j];
-          }
-        } else {
-          for (int h = g * hpg; h < (g + 1) * hpg; ++h) w += __expf(sm.c[t][h] - sm.c[s][h]) * sm.u[s][h];
-        }
-      }
-      wt[((int64_t)g * HS_SEG + s) * HS_SEG + t] = w;
+    for (int e = fs0 + tid; e < G * NPAIR; e += fstep) {
+      const int g = e / NPAIR, r = e - g * NPAIR;
+      int t = (int)((sqrtf(8.f * (float)r + 1.f) - 1.f) * 0.5f);
+      if ((t + 1) * (t + 2) / 2 <= r) ++t;
+      if (t * (t + 1) / 2 > r) --t;
+      const int s = r - t * (t + 1) / 2;
+      wt[((int64_t)g * HS_SEG + s) * HS_SEG + t] = hs_weight(sm, g, hpg, t, s);
     }
     float* eit = q.u + ((int64_t)b * p.nseg + si) * H * HS_SEG;
-    const int nhr = (H - zb + nblk - 1) / nblk;
-    for (int e = tid; e < nhr * HS_SEG; e += blockDim.x) {
-      const int t = e % HS_SEG, h = zb + nblk * (e / HS_SEG);
+    for (int e = fs0 + tid; e < H * HS_SEG; e += fstep) {
+      const int t = e % HS_SEG, h = e / HS_SEG;
       eit[(int64_t)h * HS_SEG + t] = t < len ? __expf(sm.c[t][h]) : 0.f;
     }
   }
   // Zloc (and GL): tiles of (group, 32 heads), one per wave at a time
   const float gscale = 1.f / ((float)H * (float)p.headdim);
-  for (; unit < nunit; unit += nw) {
-    const bool gl = BWD && unit >= nz;
-    const int uz = gl ? unit - nz : unit;
+  for (; unit < nunit; unit += ustep) {
+    const int n0 = unit_n0(unit), uu = unit % per;
+    const bool col = n0 + i < N;
+    const bool gl = BWD && uu >= nz;
+    const int uz = gl ? uu - nz : uu;
     const int g = uz / tiles, hl = (uz % tiles) * 32;
     const int h = g * hpg + min(hl + i, hpg - 1);            // A row (clamped; rows past hpg are not stored)
     const float ce = sm.cend[h];
@@ -239,7 +263,7 @@ __global__ __launch_bounds__(256) void ssd_hs_local_kernel(SsdParams p, HsParams
 #pragma unroll
     for (int m = 0; m < HS_SEG / 2; ++m)
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[m], to_f32(bv[m]), acc, 0, 0, 0);
-    if (unit + nw < nunit) load_b(unit + nw);
+    if (unit + ustep < nunit) load_b(unit + ustep);
     if (col) {
       float* zl = (gl ? q.lam : q.z) + (((int64_t)b * p.nseg + si) * H + g * hpg + hl) * N + n0 + i;
       const float sc = gl ? gscale : 1.f;
@@ -250,7 +274,8 @@ __global__ __launch_bounds__(256) void ssd_hs_local_kernel(SsdParams p, HsParams
       }
     }
   }
-  if (zb == 0 && tid < H) q.dec[((int64_t)b * p.nseg + si) * H + tid] = __expf(sm.cend[tid]);
+  if (zb == 0)
+    for (int h = tid; h < H; h += blockDim.x) q.dec[((int64_t)b * p.nseg + si) * H + h] = __expf(sm.cend[h]);
 }
 
 // The carry over segments as a two-level scan.  The segments of a chain (b, h, n) are cut into NP parts of
@@ -347,7 +372,7 @@ __global__ __launch_bounds__(64) void ssd_hs_out_kernel(SsdParams p, HsParams q)
 #pragma unroll
     for (int m = 0; m < KS; ++m) {
       const int sk = 2 * m + hf, skc = min(sk, len - 1);
-      a[m] = wseg[((int64_t)g * HS_SEG + sk) * HS_SEG];
+      a[m] = sk <= i ? wseg[((int64_t)g * HS_SEG + sk) * HS_SEG] : 0.f;   // W_g[t][s] = 0 for s > t
       bq[m] = to_f32(Bb[(tok0 + skc) * p.B_sl + (int64_t)g * N]);
     }
   };
@@ -809,10 +834,11 @@ hipError_t launch_ssd_hs_bwd(const SsdParams& p, const HsParams& q, float* dh0, 
 hipError_t launch_ssd_hs(const SsdParams& p, const HsParams& q, hipStream_t st) {
   if (p.seqlen == 0) return hipSuccess;
   const dim3 grid((unsigned)p.nseg, (unsigned)p.batch, (unsigned)((p.dstate + HS_NB - 1) / HS_NB));
+  const dim3 lgrid((unsigned)p.nseg, (unsigned)p.batch, (unsigned)HS_FS);
   if (p.dtype == DT_BF16)
-    hipLaunchKernelGGL((ssd_hs_local_kernel<bf16, false>), grid, dim3(256), 0, st, p, q);
+    hipLaunchKernelGGL((ssd_hs_local_kernel<bf16, false>), lgrid, dim3(HS_LOC_FWD), 0, st, p, q);
   else
-    hipLaunchKernelGGL((ssd_hs_local_kernel<float, false>), grid, dim3(256), 0, st, p, q);
+    hipLaunchKernelGGL((ssd_hs_local_kernel<float, false>), lgrid, dim3(HS_LOC_FWD), 0, st, p, q);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // parts per chain: about 16 segments each, at most 8 (a part's load then covers 8 consecutive columns)
