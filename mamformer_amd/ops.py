@@ -52,6 +52,58 @@ __all__ = ["selective_scan", "selective_scan_reference", "plan_selective_scan_re
 _DT = {torch.float32: _lib.MH_F32, torch.bfloat16: _lib.MH_BF16}
 
 
+class _Heads64:
+    """Head size P of the SSD prefill in the kernels' 64 channels: a head of P = 64 k channels is k heads of 64
+    sharing its dt, A, dt_bias and B / C group (the recurrence of each channel depends only on its head's decay
+    and the group's B, C), and other sizes are zero-padded to the next multiple of 64 first (a zero channel keeps
+    a zero state and a zero output, so it changes nothing else; h_states, a mean over every channel, is rescaled).
+    Every map is a view, repeat or pad that autograd differentiates."""
+
+    def __init__(self, H, P):
+        self.H, self.P, self.k = H, P, (P + 63) // 64
+        self.Pp = 64 * self.k
+
+    def chan(self, t4):             # (b, L, H, P) -> (b, L, H k, 64)
+        b, L = t4.shape[:2]
+        if self.Pp != self.P:
+            t4 = torch.nn.functional.pad(t4, (0, self.Pp - self.P))
+        return t4.reshape(b, L, self.H * self.k, 64)
+
+    def unchan(self, t4):           # (b, L, H k, 64) -> (b, L, H, P)
+        b, L = t4.shape[:2]
+        return t4.reshape(b, L, self.H, self.Pp)[..., :self.P]
+
+    def state(self, s):             # (b, H, P, N) -> (b, H k, 64, N)
+        if self.Pp != self.P:
+            s = torch.nn.functional.pad(s, (0, 0, 0, self.Pp - self.P))
+        return s.reshape(s.shape[0], self.H * self.k, 64, s.shape[-1])
+
+    def unstate(self, s):           # (b, H k, 64, N) -> (b, H, P, N)
+        return s.reshape(s.shape[0], self.H, self.Pp, s.shape[-1])[:, :, :self.P]
+
+    def head(self, v, dim=-1):      # per-head values -> per sub-head
+        return None if v is None else v.repeat_interleave(self.k, dim=dim)
+
+    def unhead(self, v):            # gradient per sub-head -> per head (last dim H k)
+        return None if v is None else v.reshape(*v.shape[:-1], self.H, self.k).sum(-1)
+
+    def d_vec(self, D):             # D (H,) or (H P,) -> per sub-head or per padded channel
+        if D is None:
+            return None
+        D = D.reshape(-1)
+        if D.numel() == self.H:
+            return self.head(D)
+        D = D.reshape(self.H, self.P)
+        if self.Pp != self.P:
+            D = torch.nn.functional.pad(D, (0, self.Pp - self.P))
+        return D.reshape(-1)
+
+    def d_grad(self, dD, D):        # gradient of d_vec(D) -> gradient of D
+        if dD.numel() == self.H * self.k and D.numel() == self.H:
+            return self.unhead(dD).reshape(D.shape)
+        return dD.reshape(self.H, self.Pp)[:, :self.P].reshape(D.shape)
+
+
 def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else ct.c_void_p(t.data_ptr())
 
@@ -165,7 +217,9 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
     """Mamba-2 SSD chunked-scan prefill.  Drop-in for ``selective_scan`` (R/mamformer/layers/mamba2.py:31-67).
 
     Args (SSD convention; see module docstring):
-        x: (b, L, H*P) like the reference, or (b, L, H, P); fp32 or bf16.
+        x: (b, L, H*P) like the reference, or (b, L, H, P); fp32 or bf16.  The kernels run heads of P = 64
+            channels; a head of 64 k channels runs as k of them, other head sizes zero-padded to the next
+            multiple of 64 (``_Heads64``).
         dt: (b, L, H) per-head step sizes (positive unless ``dt_softplus``).
         A: (H,) per-head decay rates, A <= 0.
         B, C: (b, L, N) (one group, as the reference) or (b, L, G, N); dtype of x.
@@ -215,24 +269,42 @@ def selective_scan(x, dt, A, B, C, D, return_h_states=False, return_final_state=
         raise ValueError(f"selective_scan: A must be (H,) = ({H},), got {tuple(A.shape)}")
     if D is not None and D.numel() not in (H, H * P):
         raise ValueError(f"selective_scan: D must have H or H*P entries, got {tuple(D.shape)}")
+    if dt_bias is not None and dt_bias.numel() != H:
+        raise ValueError(f"selective_scan: dt_bias must have H = {H} entries")
+    if initial_state is not None and initial_state.numel() != b * H * P * N:
+        raise ValueError(f"selective_scan: initial_state must hold b*H*P*N = {b * H * P * N} values")
+    if z is not None and (z.shape != x.shape or z.dtype != x.dtype):
+        raise ValueError(f"selective_scan: z must have the shape and dtype of x, got {tuple(z.shape)} {z.dtype}")
+    if P != 64:
+        # the kernels run heads of 64 channels: split (or pad and split) and map the outputs back
+        if _plan_only:
+            raise ValueError("plan_selective_scan: headdim must be 64 (selective_scan takes other head sizes)")
+        hm = _Heads64(H, P)
+        out = selective_scan(
+            hm.chan(x4), hm.head(dt, 2), hm.head(A), B4, C4, hm.d_vec(D), return_h_states, return_final_state,
+            chunk_size=chunk_size, dt_bias=hm.head(dt_bias), dt_softplus=dt_softplus, dt_limit=dt_limit,
+            initial_state=None if initial_state is None else hm.state(initial_state.reshape(b, H, P, N)),
+            z=None if z is None else hm.chan(z.reshape(b, L, H, P)))
+        out = list(out) if isinstance(out, tuple) else [out]
+        res = [hm.unchan(out[0]).reshape(x.shape)]
+        if return_h_states:
+            res.append(out[1] * (hm.Pp / P) if hm.Pp != P else out[1])
+        if return_final_state:
+            fin = hm.unstate(out[-1])
+            res.append(fin.reshape(b, H * P, N) if x.dim() == 3 else fin)
+        return res[0] if len(res) == 1 else tuple(res)
     x4 = _inner_contig(x4)
     B4 = _inner_contig(B4, 2)
     C4 = _inner_contig(C4, 2)
     dt32 = dt.to(torch.float32)
     if dt32.stride(-1) != 1:
         dt32 = dt32.contiguous()
-    if dt_bias is not None and dt_bias.numel() != H:
-        raise ValueError(f"selective_scan: dt_bias must have H = {H} entries")
     A32, D32, bias32 = _f32c(A), _f32c(D.reshape(-1) if D is not None else None), _f32c(dt_bias)
     h0 = None
     if initial_state is not None:
-        if initial_state.numel() != b * H * P * N:
-            raise ValueError(f"selective_scan: initial_state must hold b*H*P*N = {b * H * P * N} values")
         h0 = initial_state.reshape(b, H, P, N).to(torch.float32).contiguous()
     z4 = None
     if z is not None:
-        if z.shape != x.shape or z.dtype != x.dtype:
-            raise ValueError(f"selective_scan: z must have the shape and dtype of x, got {tuple(z.shape)} {z.dtype}")
         if z.dim() == 3:
             z4 = z.view(b, L, H, P) if z.stride(-1) == 1 else z.contiguous().view(b, L, H, P)
         else:
@@ -476,6 +548,25 @@ def selective_scan_bwd(dy, x, dt, A, B, C, D=None, *, d_final_state=None, initia
         raise ValueError(f"selective_scan_bwd: A must be (H,) = ({H},), got {tuple(A.shape)}")
     if D is not None and D.numel() not in (H, H * P):
         raise ValueError(f"selective_scan_bwd: D must have H or H*P entries, got {tuple(D.shape)}")
+    if P != 64:
+        # heads of 64 channels, as in selective_scan; the gradients of the shared per-head values are summed
+        if _plan_only:
+            raise ValueError("plan_selective_scan_bwd: headdim must be 64 (selective_scan_bwd takes other head sizes)")
+        hm = _Heads64(H, P)
+        r = selective_scan_bwd(
+            None if dy is None else hm.chan(dy.reshape(b, L, H, P)), hm.chan(x4), hm.head(dt, 2), hm.head(A), B4,
+            C4, hm.d_vec(D), dt_softplus=dt_softplus, dt_limit=dt_limit, dt_bias=hm.head(dt_bias),
+            d_final_state=None if d_final_state is None else hm.state(d_final_state.reshape(b, H, P, N)),
+            initial_state=None if initial_state is None else hm.state(initial_state.reshape(b, H, P, N)))
+        dh0 = hm.unstate(r["d_initial_state"])
+        out = {"dx": hm.unchan(r["dx"]).reshape(x.shape), "ddt": hm.unhead(r["ddt"]), "dA": hm.unhead(r["dA"]),
+               "dB": r["dB"].reshape(B.shape), "dC": r["dC"].reshape(C.shape),
+               "d_initial_state": dh0 if initial_state is None else dh0.reshape(initial_state.shape)}
+        if D is not None:
+            out["dD"] = hm.d_grad(r["dD"], D)
+        if dt_bias is not None:
+            out["d_dt_bias"] = hm.unhead(r["d_dt_bias"]).reshape(dt_bias.shape)
+        return out
     x4 = _inner_contig(x4)
     B4, C4 = _inner_contig(B4, 2), _inner_contig(C4, 2)
     dt32 = dt.to(torch.float32)
