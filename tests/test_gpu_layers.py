@@ -296,15 +296,18 @@ def _layer_ref(layer, u, cache=None):
     return out, fin.reshape(b, H * Pd, N), hs, x
 
 
-@pytest.mark.parametrize("G,N", [(1, 64), (2, 128), (1, 16), (2, 32), (1, 256)])
-def test_mamba2_layer_forward_vs_oracle(G, N):
+@pytest.mark.parametrize("G,N,P", [(1, 64, 64), (2, 128, 64), (1, 16, 64), (2, 32, 64), (1, 256, 64), (2, 128, 128),
+                                   (1, 64, 32)])
+def test_mamba2_layer_forward_vs_oracle(G, N, P):
+    """The layer's prefill (and its h_states and cache) against the float64 composition; head sizes 128 and 32 run
+    through the ops' 64-channel heads."""
     torch.manual_seed(11)
-    layer = Mamba2Layer(256, d_state=N, expand=1, headdim=64, ngroups=G, device="cuda", dtype=torch.float32)
+    layer = Mamba2Layer(256, d_state=N, expand=1, headdim=P, ngroups=G, device="cuda", dtype=torch.float32)
     with torch.no_grad():   # larger dt projections than the default init so the scan dominates the output
         for lin in layer.dt_proj:
             lin.weight.normal_(std=0.05)
     u = torch.randn(2, 97, 256, device="cuda")
-    say(f"Mamba2Layer forward G={G} N={N}")
+    say(f"Mamba2Layer forward G={G} N={N} headdim={P}")
     with torch.no_grad():
         out, cache = layer(u)
         out2, cache2, hs = layer(u, use_cache=True, return_h_states=True)
@@ -342,11 +345,12 @@ def test_mamba2_layer_A_log_clamped_in_prefill_only():
     check("step state", c2["ssm_state"], r_sfin, 1e-4)
 
 
-def test_mamba2_layer_prefill_then_step_equals_longer_prefill():
+@pytest.mark.parametrize("P", [64, 128, 32])
+def test_mamba2_layer_prefill_then_step_equals_longer_prefill(P):
     torch.manual_seed(12)
-    layer = Mamba2Layer(256, d_state=128, expand=2, headdim=64, ngroups=1, device="cuda", dtype=torch.float32)
+    layer = Mamba2Layer(256, d_state=128, expand=2, headdim=P, ngroups=1, device="cuda", dtype=torch.float32)
     u = torch.randn(2, 65, 256, device="cuda")
-    say("Mamba2Layer prefill 64 + step vs prefill 65")
+    say(f"Mamba2Layer prefill 64 + step vs prefill 65, headdim {P}")
     with torch.no_grad():
         full, cfull = layer(u, use_cache=True)
         pre, c = layer(u[:, :64], use_cache=True)
