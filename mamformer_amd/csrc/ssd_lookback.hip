@@ -25,10 +25,11 @@
 // The three masked (C B^T) tiles of a segment are formed once per workgroup and shared through LDS.  A
 // segment whose own decay range exceeds LB_FACT_RANGE takes an exact per-element path (wave-uniform branch).
 //
-// Work split (both passes): a workgroup owns HG heads of one group, one wave per head (one wave per SIMD);
-// a wave's state is its head's 64 columns p as two 32-column halves of N/32 accumulator tiles (rows n, columns
-// p), so every B / C operand fragment it reads from LDS feeds one MFMA per half, and the decay, the weights
-// and the diagonal operands are formed once for both halves.  Every segment's tiles (x, B, C, dt) are fetched
+// Work split (both passes): a workgroup owns HG heads of one group (pass 1 on chunks of at most
+// LB_STATE_SHORT tokens: two heads), 2 / PH waves per head; a wave's state is PH of its head's two 32-column
+// halves of P as N/32 accumulator tiles each (rows n, columns p).  With PH = 1 (LB_PH, two waves per head,
+// two waves per SIMD) every B / C operand fragment a wave reads from LDS feeds one MFMA; PH = 2 (one wave per
+// head, both halves from each fragment) needs ~500 registers and one wave per SIMD, and measured slower.  Every segment's tiles (x, B, C, dt) are fetched
 // straight into LDS (global_load_lds) ahead of use, in the Sub64 layout (tiles.h): every LDS access of the
 // loops is one lane offset (a few per kernel) plus an immediate, the stage being a compile-time index (the
 // segment loop is unrolled by the number of stages).
