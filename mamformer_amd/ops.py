@@ -60,6 +60,8 @@ class _Heads64:
     Every map is a view, repeat or pad that autograd differentiates."""
 
     def __init__(self, H, P):
+        if P < 1:
+            raise ValueError(f"selective_scan: head size must be positive, got {P}")
         self.H, self.P, self.k = H, P, (P + 63) // 64
         self.Pp = 64 * self.k
 

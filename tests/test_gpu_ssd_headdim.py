@@ -107,3 +107,39 @@ def test_autograd_head_size_matches_explicit_backward():
     for name, got, key in zip(("dx", "ddt", "dA", "dB", "dC", "dD", "dh0", "d_dt_bias"), grads,
                               ("dx", "ddt", "dA", "dB", "dC", "dD", "d_initial_state", "d_dt_bias")):
         check(f"autograd {name}", got, host(g[key]), 1e-5)
+
+
+@pytest.mark.parametrize("P,dtype", [(96, BF), (128, F32)])
+def test_gate_head_sizes(P, dtype):
+    """The z-gate y * silu(z) at other head sizes (z split and padded like x; a padded channel's gate is silu(0) = 0
+    on a zero output)."""
+    b, L, H, N, G = 1, 120, 2, 64, 1
+    rng = np.random.default_rng(50 + P)
+    d = make(rng, b, L, H, N, G, dtype, False, False, "head", P=P)
+    z = rng.standard_normal((b, L, H * P))
+    if dtype == BF:
+        z = torch.tensor(z, dtype=torch.float32).to(torch.bfloat16).to(torch.float64).numpy()
+    say(f"ssd gate head size P={P} {dtype}")
+    y = mh.selective_scan(dev(d["x"], dtype).reshape(b, L, H * P), dev(d["dt"]), dev(d["A"]), dev(d["B"], dtype),
+                          dev(d["C"], dtype), dev(d["D"]), dt_bias=dev(d["bias"]), dt_softplus=True, z=dev(z, dtype))
+    torch.cuda.synchronize()
+    dtp = ossd.process_dt(d["dt"], dt_bias=d["bias"], dt_softplus=True)
+    yr, _ = ossd.ssd_via_reference(d["x"], dtp, d["A"], d["B"], d["C"], d["D"])
+    zr = z.reshape(b, L, H, P)
+    check(f"gated y P={P}", host(y).reshape(b, L, H, P), yr * zr / (1 + np.exp(-zr)), TOL[dtype])
+
+
+def test_empty_sequence_head_size():
+    """L = 0 at P = 96: an empty output and the initial state back as the final state."""
+    b, H, P, N = 2, 3, 96, 64
+    x = torch.zeros(b, 0, H * P, device="cuda")
+    dt = torch.zeros(b, 0, H, device="cuda")
+    B = torch.zeros(b, 0, N, device="cuda")
+    h0 = torch.randn(b, H * P, N, device="cuda")
+    say("ssd empty sequence head size P=96")
+    y, fin = mh.selective_scan(x, dt, -torch.ones(H, device="cuda"), B, B, None, return_final_state=True,
+                               initial_state=h0)
+    torch.cuda.synchronize()
+    assert y.shape == (b, 0, H * P) and fin.shape == (b, H * P, N)
+    assert torch.equal(fin, h0)
+
