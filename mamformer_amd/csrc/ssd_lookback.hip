@@ -451,22 +451,6 @@ __device__ __forceinline__ void cb_tile(int ti, const bf16* btile, const bf16* c
   out[64 + l] = acc_to_frag<bf16>(acc, 1);
 }
 
-// Gate values z in the epilogue's lane layout: z[ph][tt][q] = the 4 values of row 32 tt + lane % 32, columns
-// 32 ph + 8 q + 4 (lane / 32) .. + 3 (src at the segment's first row and the wave's first column; rows past rmax
-// re-read row rmax).
-template <int PH>
-__device__ __forceinline__ void load_z_pieces(const bf16* src, int64_t row_stride, int rmax, bf16x4 (&z)[PH][2][4]) {
-  const int lane = lane_id_here(), half = lane >> 5, l32 = lane & 31;
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const bf16* row = src + (int64_t)min(32 * tt + l32, rmax) * row_stride + 4 * half;
-#pragma unroll
-    for (int ph = 0; ph < PH; ++ph)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) z[ph][tt][q] = *reinterpret_cast<const bf16x4*>(row + 32 * ph + 8 * q);
-  }
-}
-
 // H[ph][nt] += f S on the MFMA unit, for the wave's halves of one state S in bf16 fragment order
 // (v[ph][nt][c] = the B-operand fragment of k-step c of tile (nt, ph0 + ph)): A = f I, with f split into bf16
 // parts f_hi + f_lo (LO: else f is taken as exact in bf16), so the sum keeps about 16 bits of f.
@@ -578,8 +562,6 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
     }
     p.xsum[(((int64_t)c.b * p.seqlen + pos + lh) * p.nheads + c.h) * 2 + c.ph0] = xs;
   }
-  bf16x4 zq[PH][2][4];
-  if constexpr (GATE) load_z_pieces<PH>(zg + (int64_t)pos * p.z_sl, p.z_sl, c.c1 - 1 - pos, zq);
   const bool dnext = dj == LB_DSEG - 1 && si + 1 < nseg;  // the next decay block is due
   if (dnext) lb_dt_fetch(p, c, dec, si + 1);
   const float cse = readlane_f(cs, SEG - 1);
@@ -589,7 +571,7 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
   // e^LB_FACT_RANGE, so a segment whose decay range exceeds it takes several passes (a token's own decay,
   // however large, is applied to the state at the start of its pass)
   int a = 0;
-  bf16x4 yb[PH][2][4];                                     // without the gate: the segment's y pieces over the passes
+  bf16x4 yb[PH][2][4];                                     // the segment's y pieces over the passes
   for (int pass = 0;; ++pass) {
     // the tile reads of a pass stay inside the pass loop (hoisted, the C and B fragments would hold their
     // registers through it): the tile pointers are offset by an opaque zero
@@ -629,11 +611,9 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
       Y[ph][1] = mma(xa[ph][2], mt[256 + l], Y[ph][1]);
       Y[ph][1] = mma(xa[ph][3], mt[320 + l], Y[ph][1]);
     }
-    // ---- epilogue: y[t][p] = rs_t Y^T[p][t] + D_p x[t][p] (times silu(z[t][p]) with the gate) for the pass's
-    // tokens, in the accumulator layout (lane = token t, 8-byte pieces of 4 columns).  With the gate they are
-    // stored from there (before the first stores every load of this wave is complete, in particular the next
-    // segment's tiles); without it they are kept for the segment's row-chunk stores below.
-    if (GATE && pass == 0) wait_vmem();
+    // ---- epilogue: y[t][p] = rs_t Y^T[p][t] + D_p x[t][p] for the pass's tokens, in the accumulator layout
+    // (lane = token t, 8-byte pieces of 4 columns), kept for the segment's row-chunk stores below (rows past the
+    // end of the sequence are computed from clamped rows and not stored)
 #pragma unroll
     for (int ph = 0; ph < PH; ++ph) {
       const bf16* xt = xwp + ph * Sub64::ELEMS;
@@ -649,19 +629,16 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int t = 32 * tt + l32;
-        if (t >= a && t < bnd && (!GATE || pos + t < c.c1)) {
-          bf16* yrow = yg + (int64_t)(pos + t) * p.y_sl + 32 * ph + 4 * half;
+        if (t >= a && t < bnd) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             bf16x4 yo;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               float yv = rsb[tt] * Y[ph][tt][4 * q + i] + d4[q][i] * (float)xv[tt][q][i];
-              if constexpr (GATE) yv *= silu_f((float)zq[ph][tt][q][i]);
               yo[i] = (bf16)yv;
             }
-            if constexpr (GATE) *reinterpret_cast<bf16x4*>(yrow + 8 * q) = yo;
-            else yb[ph][tt][q] = yo;
+            yb[ph][tt][q] = yo;
           }
         }
       }
@@ -669,7 +646,7 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
     if (bnd >= SEG) break;
     a = bnd;
   }
-  if constexpr (!GATE) {
+  {
     // y through the wave's own x sub-tile (no longer read; the same swizzled layout) into 16-byte row chunks:
     // a store instruction then writes 16 rows of 64 contiguous bytes instead of 32 rows of 16, which the
     // memory system drains at about twice the rate.  Before the stores: every load of this wave is complete,
@@ -682,6 +659,18 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
 #pragma unroll
         for (int q = 0; q < 4; ++q) *reinterpret_cast<bf16x4*>(ys + 32 * tt * Sub64::W + lo.piece[q]) = yb[ph][tt][q];
     }
+    // the gate y * silu(z) on the same 16-byte row chunks: z is loaded here, so no z registers are held through
+    // the segment (the staged y is bf16: the gated value is rounded a second time, within half an ulp more)
+    uint4 zc[PH][4];
+    if constexpr (GATE) {
+#pragma unroll
+      for (int ph = 0; ph < PH; ++ph)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = min((l >> 2) + 16 * j, c.c1 - 1 - pos), ch = l & 3;
+          zc[ph][j] = *reinterpret_cast<const uint4*>(zg + (int64_t)(pos + r) * p.z_sl + 32 * ph + 8 * ch);
+        }
+    }
     wait_vmem();
 #pragma unroll
     for (int ph = 0; ph < PH; ++ph) {
@@ -689,7 +678,14 @@ __device__ __forceinline__ void lb_scan_segment(const SsdParams& p, const LbWave
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = (l >> 2) + 16 * j, ch = l & 3;
-        const uint4 v = *reinterpret_cast<const uint4*>(ys + Sub64::off(r, 8 * ch));
+        uint4 v = *reinterpret_cast<const uint4*>(ys + Sub64::off(r, 8 * ch));
+        if constexpr (GATE) {
+          bf16x8 yv = __builtin_bit_cast(bf16x8, v);
+          const bf16x8 zv = __builtin_bit_cast(bf16x8, zc[ph][j]);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) yv[i] = (bf16)((float)yv[i] * silu_f((float)zv[i]));
+          v = __builtin_bit_cast(uint4, yv);
+        }
         if (pos + r < c.c1) *reinterpret_cast<uint4*>(yg + (int64_t)(pos + r) * p.y_sl + 32 * ph + 8 * ch) = v;
       }
     }
