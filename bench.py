@@ -52,12 +52,12 @@ def log(*a):
 
 # ----------------------------------------------------------------- algorithmic counts (compulsory I/O, dense FLOPs)
 
-def ssd_alg(cfg, Q=256):
-    """Bytes: x, B, C, dt read once, y and the fp32 final state written once (+ h0 read); A, D (2H floats) omitted.
-    FLOPs: per (b, chunk of Q): 2Q^2 N G (C B^T) + H (2Q^2 P + 4 Q N P)."""
+def ssd_alg(cfg, Q=256, gated=False):
+    """Bytes: x, B, C, dt read once, y and the fp32 final state written once (+ h0 read, + z read with the gate);
+    A, D (2H floats) omitted.  FLOPs: per (b, chunk of Q): 2Q^2 N G (C B^T) + H (2Q^2 P + 4 Q N P)."""
     b, L, H, P, N, G = cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups
     es = 2 if cfg.dtype == torch.bfloat16 else 4
-    nbytes = (2 * b * L * H * P * es + 2 * b * L * G * N * es + b * L * H * 4
+    nbytes = ((3 if gated else 2) * b * L * H * P * es + 2 * b * L * G * N * es + b * L * H * 4
               + b * H * P * N * 4 * (2 if cfg.init_state else 1))
     nchunks = L // Q
     flops = b * nchunks * (2 * Q * Q * N * G + H * (2 * Q * Q * P + 4 * Q * N * P))
@@ -138,18 +138,21 @@ def time_plans(plans, steps, warmup):
     return wall, ev0.elapsed_time(ev1) / steps
 
 
-def bench_ssd(cfg, steps, warmup, nsets, chunk=None):
+def bench_ssd(cfg, steps, warmup, nsets, chunk=None, gated=False):
+    """The prefill op (plans on `nsets` rotating buffer sets); `gated`: with the output gate y * silu(z) fused into
+    the stores (the form Mamba2Block.forward runs, mamba2.py:337-338), z drawn like x."""
     import mamformer_amd as mh
     from mamformer_amd import workloads as W
 
     plans = []
     for i in range(nsets):
         inp = W.ssd_inputs(cfg.scaled(seed=cfg.seed + 1000 * i), device="cuda")
+        z = torch.randn_like(inp["x"]) if gated else None
         plans.append(mh.plan_selective_scan(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
                                             return_final_state=True, initial_state=inp["initial_state"],
-                                            chunk_size=chunk))
+                                            chunk_size=chunk, z=z))
     wall, ev = time_plans(plans, steps, warmup)
-    nbytes, flops = ssd_alg(cfg)
+    nbytes, flops = ssd_alg(cfg, gated=gated)
     t = ev * 1e-3
     chunk_len = mh.ssd_chunk_len(cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups,
                                  cfg.dtype, chunk)
@@ -631,6 +634,11 @@ def main():
             dec[f"dec3_b{b}"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
         out["decode"] = dec
     other = {}
+    if "ssd2" in legs:
+        r, _, _ = bench_ssd(cfg, args.steps, args.warmup, nsets=3, gated=True)
+        log(f"ssd2 gated (y * silu(z) fused): {r['mtok_s']:.1f} Mtok/s, {r['us_per_step']:.1f} us, "
+            f"roofline {r['roofline_frac']:.3f}")
+        other["ssd2_gated"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
     if "ssd4" in legs:
         r, _, _ = bench_ssd(W.SSD4, max(5, args.steps // 10), 3, nsets=1)
         log(f"ssd4: {r['mtok_s']:.1f} Mtok/s, {r['us_per_step']:.0f} us, roofline {r['roofline_frac']:.3f}")
